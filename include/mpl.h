@@ -1,0 +1,102 @@
+/*
+ * mpl.h -- C ABI of the MI355X (gfx950) memory-layer lookup library
+ * (libmpl.so, built from model_amd/csrc/*.hip).
+ *
+ * The reference (KumarDev7/model) has no FFI: its operator is the Flax module
+ * `MemoryPool` (memory_pool_model/memory.py:64-227) plus the trainer's sparse
+ * row update (memory_pool_model/train.py:146-172, 395-426).  Each entry point
+ * below replaces one stage of that module, cited per function.  A JAX
+ * integration registers thin XLA FFI handlers over these functions; the
+ * Python host mirror in model_amd/ calls them through ctypes.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers and sizes; `stream` is a hipStream_t (NULL = the
+ *     null stream) passed as void*;
+ *   - no entry point allocates device memory or synchronises the stream;
+ *     scratch comes from a caller-owned workspace sized by the matching
+ *     *_workspace_bytes() query;
+ *   - return 0 on success, otherwise an MPL_E* code, with a message for the
+ *     calling thread in mpl_last_error();
+ *   - tensors are dense row-major in the shapes given; M = number of query
+ *     tokens, H = heads, n = sub-keys per codebook, half = d_key / 2,
+ *     k = top_k, N = n*n slots, d = d_value.
+ */
+#ifndef MPL_H
+#define MPL_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { MPL_F32 = 0, MPL_F16 = 1 };
+enum { MPL_OK = 0, MPL_EINVAL = 1, MPL_EHIP = 2, MPL_EWORKSPACE = 3, MPL_EUNSUPPORTED = 4 };
+
+/* Library version (major*10000 + minor*100 + patch). */
+int mpl_version(void);
+
+/* Message for the last failing call on this thread ("" if none). */
+const char* mpl_last_error(void);
+
+/*
+ * memory.py:30-31 and 136-139: y = x * rsqrt(sum(x*x) + eps) over rows of
+ * length `dim`.  x, y: [rows, dim] fp32 (may alias).  If row_len != NULL it
+ * receives sqrt(sum(x*x) + eps) / sqrt(dim) per row: the q_len of
+ * memory.py:137 (used when query_scale is on).
+ */
+int mpl_l2_normalize(const float* x, int64_t rows, int dim, float eps, float* y,
+                     float* row_len, void* stream);
+
+/*
+ * memory.py:139: normalise sub_keys [H,2,n,half] (fp32) and pack them into
+ * the MFMA operand layout consumed by mpl_score_select.  keys_hat [H,2,n,half]
+ * fp32 (required) receives the normalised keys.  score_dtype selects the
+ * scoring precision: MPL_F16 (fp16 MFMA, fp32 accumulate) or MPL_F32 (fp32
+ * MFMA).  `packed` must hold mpl_packed_keys_bytes() bytes.
+ */
+size_t mpl_packed_keys_bytes(int H, int n, int half, int score_dtype);
+int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype,
+                  float* keys_hat, void* packed, void* stream);
+
+/*
+ * memory.py:149-178: cosine scores of q_hat [M,H,2,half] (fp32, unit rows)
+ * against the packed keys, times `temperature` (already clamped, memory.py:
+ * 143-146) and times q_len [M,H,2] when q_len != NULL (query_scale,
+ * memory.py:151-152); optional routing noise select = scores + noise_coef *
+ * gumbel with gumbel [M,H,2,n] fp32 (memory.py:155-159, NULL = no noise);
+ * exact stage-1 top-k per codebook (ties: lowest sub-key index), exact
+ * stage-2 top-k over the k*k candidates (ties: lowest flat index
+ * rank_a*k + rank_b, memory.py:171), softmax of the clean slot scores.
+ * Outputs (descending select order):
+ *   sub_idx    [M,H,2,k] int32   stage-1 sub-key ids   (memory.py:162)
+ *   sub_scores [M,H,2,k] fp32    clean sub scores      (memory.py:163)
+ *   flat_idx   [M,H,k]   int32   rank_a*k + rank_b     (memory.py:171)
+ *   slots      [M,H,k]   int32   idx_a*n + idx_b       (memory.py:175)
+ *   weights    [M,H,k]   fp32    softmax               (memory.py:178)
+ * Requires 1 <= k <= min(n, 32), 1 <= half <= 128, n*n < 2^31.
+ */
+size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int half, int k);
+int mpl_score_select(const float* q_hat, const float* q_len, const void* packed_keys,
+                     int64_t M, int H, int n, int half, int k, int score_dtype,
+                     float temperature, const float* gumbel, float noise_coef,
+                     void* workspace, size_t workspace_bytes,
+                     int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
+                     int32_t* slots, float* weights, void* stream);
+
+/*
+ * memory.py:179-193: out[m,:] = sum_r weights[m,r] * values[read(slots[m,r]),:]
+ * over the R = H*k rows of each token, fp32 accumulation; values [N,d] in
+ * values_dtype (MPL_F16 or MPL_F32); read(s) = s, or (s + N/2 + 1) % N when
+ * shuffle_reads != 0 (memory.py:179).  out: [M,d] fp32.
+ */
+int mpl_gather_wsum(const void* values, int values_dtype, int64_t N, int d,
+                    const int32_t* slots, const float* weights, int64_t M, int R,
+                    int shuffle_reads, float* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MPL_H */

@@ -1,0 +1,67 @@
+"""ctypes binding of libmpl.so (include/mpl.h).
+
+The product path has no fallback: if the library is missing or fails to load
+this module raises, so a GPU run can never silently use another code path.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libmpl.so")
+
+MPL_F32, MPL_F16 = 0, 1
+
+# name -> (restype, argtypes); the C ABI of include/mpl.h
+_P, _I, _I64, _F, _SZ = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
+SIGNATURES = {
+    "mpl_version": (_I, []),
+    "mpl_last_error": (C.c_char_p, []),
+    "mpl_l2_normalize": (_I, [_P, _I64, _I, _F, _P, _P, _P]),
+    "mpl_packed_keys_bytes": (_SZ, [_I, _I, _I, _I]),
+    "mpl_pack_keys": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
+    "mpl_score_select_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
+    "mpl_score_select": (_I, [_P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
+                              _P, _P, _P, _P, _P, _P]),
+    "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
+}
+
+_lib = None
+
+
+class MplError(RuntimeError):
+    pass
+
+
+def lib() -> C.CDLL:
+    """The loaded library (raises MplError if it was not built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise MplError(f"{LIB_PATH} is missing: build it with `python -m model_amd.build`")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().mpl_last_error().decode(errors="replace")
+        raise MplError(f"{what or 'libmpl'} failed (code {rc}): {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a torch tensor (None for None)."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_ptr(device) -> int:
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream

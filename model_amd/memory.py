@@ -1,0 +1,299 @@
+"""Host mirror of the reference's Flax ``MemoryPool`` (memory_pool_model/memory.py:64-227).
+
+Same attributes, parameter names and layout (``sub_keys`` [H, 2, n, d_key/2],
+``values`` [n*n, d_value], ``log_temperature`` []), same call keywords
+(``train``, ``sparse_grad``, ``noise_scale``, ``shuffle_reads``) and the same
+``aux`` keys.  Parameters are torch tensors on the GPU; every step of the
+lookup runs in libmpl.so (include/mpl.h) on torch's current HIP stream:
+
+  mpl_l2_normalize   queries, q_len             memory.py:136-138
+  mpl_pack_keys      keys (cached per version)  memory.py:139
+  mpl_score_select   scores + 2-stage top-k     memory.py:149-178
+                     + routing softmax
+  mpl_gather_wsum    value read                 memory.py:179-193
+
+The routing statistics of ``aux`` (memory.py:196-215) are derived from the
+returned ids on first access, so a decode loop that never reads them never
+pays for the N-sized ``slot_counts`` (the reference relies on XLA dead-code
+elimination for the same effect, memory.py:215).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any, Dict, Optional, Tuple
+
+import torch
+
+from . import _lib
+from ._lib import MPL_F16, MPL_F32, check, ptr
+
+NORM_EPS = 1e-6
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.float16:
+        return MPL_F16
+    if dt == torch.float32:
+        return MPL_F32
+    raise TypeError(f"unsupported dtype {dt} (float16 or float32)")
+
+
+class _KeyCache:
+    """Normalised + MFMA-packed sub-keys, rebuilt when the parameter changes
+    (tracked by storage pointer and torch's in-place version counter)."""
+
+    def __init__(self):
+        self.key = None
+        self.k_hat = None
+        self.packed = None
+
+    def get(self, sub_keys: torch.Tensor, score_code: int):
+        key = (sub_keys.data_ptr(), sub_keys._version, tuple(sub_keys.shape), score_code)
+        if key != self.key:
+            H, _, n, half = sub_keys.shape
+            L = _lib.lib()
+            nbytes = L.mpl_packed_keys_bytes(H, n, half, score_code)
+            if nbytes == 0:
+                raise _lib.MplError(f"unsupported key shape {tuple(sub_keys.shape)}")
+            src = sub_keys.detach().float().contiguous()
+            k_hat = torch.empty_like(src)
+            packed = torch.empty(nbytes, dtype=torch.uint8, device=src.device)
+            check(L.mpl_pack_keys(ptr(src), H, n, half, score_code, ptr(k_hat), ptr(packed),
+                                  _lib.stream_ptr(src.device)), "mpl_pack_keys")
+            self.key, self.k_hat, self.packed = key, k_hat, packed
+        return self.k_hat, self.packed
+
+
+class LazyAux(dict):
+    """The ``aux`` dict of memory.py:217-226.  ``queries``, ``slots``,
+    ``weights`` and ``temperature`` are stored; ``balance_loss``,
+    ``subkey_counts``, ``slot_counts`` and ``top1_weight`` are computed the
+    first time they are read."""
+
+    _LAZY = ("balance_loss", "subkey_counts", "slot_counts", "top1_weight")
+
+    def __init__(self, eager: Dict[str, Any], compute):
+        super().__init__(eager)
+        self._compute = compute
+
+    def __missing__(self, key):
+        if key in self._LAZY:
+            self.update(self._compute())
+            return dict.__getitem__(self, key)
+        raise KeyError(key)
+
+    def __contains__(self, key):
+        return key in self._LAZY or dict.__contains__(self, key)
+
+    def keys(self):
+        return list(dict.keys(self)) + [k for k in self._LAZY if not dict.__contains__(self, k)]
+
+    def materialize(self) -> "LazyAux":
+        for k in self._LAZY:
+            self[k]
+        return self
+
+
+class MemoryPool:
+    """memory.py:64-113 attributes, memory.py:119-227 call."""
+
+    def __init__(self, n_sub_keys: int, heads: int, d_key: int, d_value: int, top_k: int,
+                 routing_noise: float = 1.0, init_temperature: float = 10.0,
+                 min_temperature: float = 10.0, balance_temperature_grad: bool = False,
+                 max_temperature: float = 100.0, query_scale: bool = False, host_pool: str = "",
+                 name: str = "pool", *, values_dtype: torch.dtype = torch.float16,
+                 score_dtype: Optional[torch.dtype] = None):
+        assert d_key % 2 == 0, "d_key must be even (split into two halves)"  # memory.py:95
+        assert top_k <= n_sub_keys  # memory.py:96
+        if host_pool:
+            raise NotImplementedError("host_pool (host_pool.py) is outside this library's scope")
+        self.n_sub_keys, self.heads, self.d_key, self.d_value, self.top_k = n_sub_keys, heads, d_key, d_value, top_k
+        self.routing_noise = routing_noise
+        self.init_temperature = init_temperature
+        self.min_temperature, self.max_temperature = min_temperature, max_temperature
+        self.balance_temperature_grad = balance_temperature_grad
+        self.query_scale = query_scale
+        self.host_pool = host_pool
+        self.name = name
+        self.values_dtype = values_dtype
+        # fp16 MFMA scoring for fp16 tables, fp32 MFMA scoring for fp32 tables
+        self.score_dtype = score_dtype or (torch.float16 if values_dtype == torch.float16 else torch.float32)
+        self._keys = _KeyCache()
+        self._temp_key = None
+        self._temp_val = None
+
+    @property
+    def pool_size(self) -> int:
+        return self.n_sub_keys ** 2
+
+    # ------------------------------------------------------------ params
+    def init(self, rng: int | torch.Generator = 0, queries=None, *, device="cuda") -> Dict[str, Any]:
+        """memory.py:94-113: sub_keys on the unit sphere, values ~ N(0, d^-1/2),
+        log_temperature = log(init_temperature).  ``rng`` is a seed or a
+        torch.Generator on ``device``."""
+        g = rng if isinstance(rng, torch.Generator) else torch.Generator(device=device).manual_seed(int(rng))
+        H, n, half = self.heads, self.n_sub_keys, self.d_key // 2
+        keys = torch.randn((H, 2, n, half), generator=g, device=device, dtype=torch.float32)
+        keys = keys * torch.rsqrt((keys * keys).sum(-1, keepdim=True) + NORM_EPS)
+        values = torch.randn((self.pool_size, self.d_value), generator=g, device=device, dtype=self.values_dtype)
+        values.mul_(self.d_value ** -0.5)
+        log_t = torch.tensor(math.log(self.init_temperature), dtype=torch.float32, device=device)
+        return {"params": {"sub_keys": keys, "values": values, "log_temperature": log_t}}
+
+    def temperature(self, log_temperature: torch.Tensor) -> float:
+        """memory.py:143-146 value of the clamped temperature (host float,
+        re-read only when the parameter changes)."""
+        key = (log_temperature.data_ptr(), log_temperature._version)
+        if key != self._temp_key:
+            lt = float(log_temperature.detach().float().cpu())
+            lo = math.log(self.min_temperature)
+            hi = math.log(self.max_temperature)
+            lt32 = torch.tensor(lt, dtype=torch.float32).clamp(lo, hi)
+            self._temp_val = float(torch.exp(lt32))
+            self._temp_key = key
+        return self._temp_val
+
+    # -------------------------------------------------------------- call
+    def apply(self, variables: Dict[str, Any], queries: torch.Tensor, *, train: bool = False,
+              sparse_grad: bool = False, noise_scale: float | torch.Tensor = 1.0,
+              shuffle_reads: bool = False, rngs: Optional[Dict[str, Any]] = None
+              ) -> Tuple[torch.Tensor, LazyAux]:
+        """memory.py:119-227.  ``variables`` = {"params": {...}} as from init();
+        ``rngs["routing"]`` (seed or torch.Generator) drives the Gumbel noise."""
+        params = variables["params"] if "params" in variables else variables
+        res = self.lookup(params, queries, train=train, noise_scale=noise_scale,
+                          shuffle_reads=shuffle_reads, rngs=rngs)
+        return res["out"], res["aux"]
+
+    __call__ = apply
+
+    def lookup(self, params, queries: torch.Tensor, *, train: bool = False,
+               noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
+               rngs: Optional[Dict[str, Any]] = None, gumbel: Optional[torch.Tensor] = None) -> Dict[str, Any]:
+        """Forward lookup; returns out, aux and the tensors a backward needs.
+        ``gumbel`` [M, H, 2, n] may be given explicitly (parity tests)."""
+        H, n, k, d = self.heads, self.n_sub_keys, self.top_k, self.d_value
+        half = self.d_key // 2
+        lead = tuple(queries.shape[:-2])
+        if tuple(queries.shape[-2:]) != (H, self.d_key):
+            raise ValueError(f"queries must be [..., {H}, {self.d_key}], got {tuple(queries.shape)}")
+        dev = queries.device
+        if dev.type != "cuda":
+            raise RuntimeError("MemoryPool runs on the GPU only (libmpl.so); got a tensor on " + str(dev))
+        L = _lib.lib()
+        stream = _lib.stream_ptr(dev)
+        q = queries.detach().reshape(-1, H, 2, half).float().contiguous()
+        M = q.shape[0]
+        q_hat = torch.empty_like(q)
+        q_len = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if self.query_scale else None
+        check(L.mpl_l2_normalize(ptr(q), M * H * 2, half, NORM_EPS, ptr(q_hat), ptr(q_len), stream),
+              "mpl_l2_normalize")
+        score_code = _dtype_code(self.score_dtype)
+        k_hat, packed = self._keys.get(params["sub_keys"], score_code)
+        T = self.temperature(params["log_temperature"])
+
+        noise_coef = 0.0
+        if gumbel is None and train and self.routing_noise > 0:
+            gen = None
+            if rngs is not None and "routing" in rngs:
+                r = rngs["routing"]
+                gen = r if isinstance(r, torch.Generator) else torch.Generator(device=dev).manual_seed(int(r))
+            u = torch.rand((M, H, 2, n), generator=gen, device=dev, dtype=torch.float32)
+            tiny = torch.finfo(torch.float32).tiny
+            gumbel = -torch.log(-torch.log(u.clamp_(min=tiny)))  # jax.random.gumbel's transform
+        if gumbel is not None:
+            ns = float(noise_scale) if not isinstance(noise_scale, torch.Tensor) else float(noise_scale.detach().cpu())
+            noise_coef = float(self.routing_noise) * ns
+            gumbel = gumbel.reshape(M, H, 2, n).float().contiguous()
+
+        ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        sub_idx = torch.empty((M, H, 2, k), dtype=torch.int32, device=dev)
+        sub_scores = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
+        flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
+        slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
+        weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
+        check(L.mpl_score_select(ptr(q_hat), ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
+                                 T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
+                                 ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
+              "mpl_score_select")
+
+        values = params["values"]
+        if values.dtype not in (torch.float16, torch.float32) or not values.is_contiguous():
+            raise TypeError("values must be a contiguous float16/float32 [n*n, d_value] tensor")
+        out = torch.empty((M, d), dtype=torch.float32, device=dev)
+        check(L.mpl_gather_wsum(ptr(values), _dtype_code(values.dtype), self.pool_size, d, ptr(slots),
+                                ptr(weights), M, H * k, int(bool(shuffle_reads)), ptr(out), stream),
+              "mpl_gather_wsum")
+
+        noisy = gumbel is not None
+
+        def stats():
+            return self._routing_stats(params, q_hat, k_hat, T, q_len, sub_idx, slots, weights,
+                                       noisy, packed, score_code, M)
+
+        aux = LazyAux({
+            "queries": q_hat,
+            "slots": slots.reshape(*lead, H, k),
+            "weights": weights.reshape(*lead, H, k),
+            "temperature": torch.tensor(T, dtype=torch.float32, device=dev),
+        }, stats)
+        return {
+            "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_hat": q_hat, "q_len": q_len,
+            "k_hat": k_hat, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
+            "flat_idx": flat_idx, "slots": slots, "weights": weights, "gumbel": gumbel,
+            "noise_coef": noise_coef,
+        }
+
+    # ------------------------------------------------------------- stats
+    def _routing_stats(self, params, q_hat, k_hat, T, q_len, sub_idx, slots, weights, noisy,
+                       packed, score_code, M):
+        """memory.py:196-215 from the selected ids."""
+        H, n, k = self.heads, self.n_sub_keys, self.top_k
+        dev = q_hat.device
+        codebook = ((torch.arange(H, device=dev)[:, None, None] * 2
+                     + torch.arange(2, device=dev)[None, :, None]) * n)
+
+        def count_subkeys(ids):  # memory.py:199-201
+            flat = (ids.long() + codebook[None]).reshape(-1)
+            return torch.bincount(flat, minlength=H * 2 * n).float().reshape(H, 2, n)
+
+        sl = slots.long()
+        subkey_counts = count_subkeys(torch.stack([sl // n, sl % n], dim=2))
+        if noisy:  # memory.py:207: an extra clean selection
+            clean = self._clean_sub_idx(q_hat, q_len, packed, score_code, T, M)
+        else:
+            clean = sub_idx
+        f = count_subkeys(clean) / (M * k)
+        cos = torch.einsum("mhcd,hcnd->mhcn", q_hat, k_hat)
+        if self.balance_temperature_grad:
+            p_scores = cos * T * (q_len[..., None] if q_len is not None else 1.0)
+        else:
+            p_scores = cos * T
+        P = torch.softmax(p_scores, dim=-1).mean(0)
+        balance = n * torch.mean(torch.sum(f * P, dim=-1))
+        slot_counts = torch.bincount(sl.reshape(-1), minlength=self.pool_size).float()
+        return {
+            "balance_loss": balance,
+            "subkey_counts": subkey_counts,
+            "slot_counts": slot_counts,
+            "top1_weight": weights.max(-1).values.mean(),
+        }
+
+    def _clean_sub_idx(self, q_hat, q_len, packed, score_code, T, M):
+        H, n, k, half = self.heads, self.n_sub_keys, self.top_k, self.d_key // 2
+        dev = q_hat.device
+        L = _lib.lib()
+        ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+        sub_idx = torch.empty((M, H, 2, k), dtype=torch.int32, device=dev)
+        sub_scores = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
+        flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
+        slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
+        weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
+        check(L.mpl_score_select(ptr(q_hat), ptr(q_len), ptr(packed), M, H, n, half, k, score_code, T,
+                                 None, 0.0, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores),
+                                 ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
+              "mpl_score_select(clean)")
+        return sub_idx

@@ -1,0 +1,341 @@
+"""Pins the numpy oracle (oracle/) to the reference's behaviour without
+running the reference (jax/flax/optax are not installed).
+
+Each check is chosen so that a plausible slip in the oracle -- a dropped
+term, a wrong tie rule, a transposed operand -- fails it: brute force over all
+n^2 slots, hand-derived known answers, fp64 closed forms, and torch-CPU
+autograd of an independent torch restatement for the backward.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import backward as ob
+from oracle import lookup as ol
+from oracle import rows as orow
+
+N_SUB, HEADS, D_KEY, D_VALUE, K = 16, 2, 8, 12, 4  # tests/test_memory_pool.py:18
+
+
+def _inputs(seed=0, M=15, H=HEADS, n=N_SUB, d_key=D_KEY, d_value=D_VALUE):
+    rng = np.random.default_rng(seed)
+    q = rng.standard_normal((M, H, d_key)).astype(np.float32)
+    keys = ol.l2_normalize(rng.standard_normal((H, 2, n, d_key // 2)).astype(np.float32))
+    values = (rng.standard_normal((n * n, d_value)) * d_value ** -0.5).astype(np.float32)
+    return q, keys, values
+
+
+# ------------------------------------------------------------------ A2
+def test_l2_normalize_closed_form():
+    x = np.random.default_rng(1).standard_normal((7, 33)).astype(np.float32)
+    y = ol.l2_normalize(x)
+    x64 = x.astype(np.float64)
+    want = x64 / np.sqrt((x64 ** 2).sum(-1, keepdims=True) + 1e-6)
+    np.testing.assert_allclose(y, want, rtol=2e-7, atol=0)
+    np.testing.assert_allclose(np.linalg.norm(y, axis=-1), 1.0, rtol=1e-6)
+
+
+# ------------------------------------------------------------------ A6
+@pytest.mark.parametrize("n", [100, 5000])
+def test_top_k_matches_sorted_with_ties(n):
+    """tests:55-63: descending values, ties -> lowest index; both code paths."""
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((64, n)).astype(np.float32)
+    x[:, 10] = x[:, 3]
+    x[:, 50] = x[:, 3]
+    x[::3, 3] = 9.0  # forces a tie group at the top of every third row
+    x[::3, 10] = 9.0
+    for k in (1, 4, 16):
+        v, i = ol.top_k(x, k)
+        for r in range(0, 64, 7):
+            order = sorted(range(n), key=lambda j: (-float(x[r, j]), j))[:k]
+            assert list(i[r]) == order
+            np.testing.assert_array_equal(v[r], x[r, order])
+
+
+def test_top_k_partition_path_equals_sort_path():
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal((512, 8192)).astype(np.float32)
+    x[:, 100] = x[:, 7]
+    x[:, 4000] = x[:, 7]
+    flat_big = ol._top_k_partition(x, 16)
+    sort = np.argsort(-x, axis=1, kind="stable")[:, :16]
+    np.testing.assert_array_equal(flat_big, sort)
+
+
+# ------------------------------------------------------------------ A4-A7
+@pytest.mark.parametrize("n,H,d_key,k,M", [(16, 2, 8, 4, 15), (64, 4, 32, 16, 40), (32, 1, 64, 32, 9)])
+def test_product_keys_find_exact_top_k(n, H, d_key, k, M):
+    """tests:40-52 restated: product-key slots == brute force over n^2 sums."""
+    q, keys, _ = _inputs(3, M=M, H=H, n=n, d_key=d_key)
+    res = ol.lookup_forward(q, keys, None, np.log(10.0), top_k_=k)
+    brute = ol.brute_force_slots(q, keys, np.log(10.0), top_k_=k, dtype=np.float32)
+    np.testing.assert_array_equal(np.sort(res["slots"], -1), np.sort(brute, -1))
+
+
+def test_product_keys_exact_with_query_scale_and_noise_free_select():
+    q, keys, _ = _inputs(4, M=20, H=2, n=16, d_key=8)
+    res = ol.lookup_forward(q, keys, None, np.log(10.0), top_k_=4, query_scale=True)
+    brute = ol.brute_force_slots(q, keys, np.log(10.0), top_k_=4, dtype=np.float32, query_scale=True)
+    np.testing.assert_array_equal(np.sort(res["slots"], -1), np.sort(brute, -1))
+
+
+def tie_case():
+    """Hand-built exact ties (n=4, k=2, H=1, half=2).
+
+    Both query halves are the same unit vector, so a key shared by both
+    codebooks has the same cosine in each.  Codebook a = [u, u, z, w],
+    codebook b = [u, w, z, z] with cos(u)=x < cos(w)=y and z low:
+      stage 1: a -> [3, 0] (index 0 beats its tie 1), b -> [1, 0]
+      candidates: flat0 = y+y, flat1 = y+x, flat2 = x+y, flat3 = x+x
+      flat1 and flat2 tie exactly; memory.py:171 keeps the lower flat index.
+    Expected slots: [3*4+1, 3*4+0] = [13, 12].  (A slot-index tie rule would
+    pick slot 0*4+1 = 1 instead of 12.)
+    """
+    qv = np.array([1.0, 0.0], np.float32)
+    u = np.array([0.6, 0.8], np.float32)
+    w = np.array([0.8, 0.6], np.float32)
+    z = np.array([-1.0, 0.0], np.float32)
+    keys = np.stack([np.stack([u, u, z, w]), np.stack([u, w, z, z])])[None]  # [1, 2, 4, 2]
+    q = np.concatenate([qv, qv])[None, None, :]  # [1, 1, 4]
+    return q, keys
+
+
+def test_stage2_flat_index_tie_rule_known_answer():
+    q, keys = tie_case()
+    res = ol.lookup_forward(q, keys, None, np.log(10.0), top_k_=2)
+    assert res["sub_idx"][0, 0, 0].tolist() == [3, 0]
+    assert res["sub_idx"][0, 0, 1].tolist() == [1, 0]
+    assert res["slots"][0, 0].tolist() == [13, 12]
+    assert res["flat_idx"][0, 0].tolist() == [0, 1]
+
+
+# ------------------------------------------------------------------ A8-A11
+def test_weights_and_read_closed_forms():
+    q, keys, values = _inputs(5)
+    res = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K)
+    w = res["weights"]
+    np.testing.assert_allclose(w.sum(-1), 1.0, rtol=1e-6)
+    # softmax closed form in fp64 from the slot scores
+    s = res["slot_scores"].astype(np.float64)
+    e = np.exp(s - s.max(-1, keepdims=True))
+    np.testing.assert_allclose(w, e / e.sum(-1, keepdims=True), rtol=1e-6)
+    # weighted sum: explicit loop in fp64
+    out = np.zeros((q.shape[0], D_VALUE))
+    for m in range(q.shape[0]):
+        for h in range(HEADS):
+            for j in range(K):
+                out[m] += float(w[m, h, j]) * values[res["slots"][m, h, j]].astype(np.float64)
+    np.testing.assert_allclose(res["out"], out, rtol=1e-5, atol=1e-7)
+    # weights are descending (slots come out in descending score order)
+    assert np.all(np.diff(res["slot_scores"], axis=-1) <= 0)
+
+
+def test_shuffle_reads_closed_form():
+    """tests:577-588."""
+    q, keys, values = _inputs(6)
+    a = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K)
+    b = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K, shuffle_reads=True)
+    np.testing.assert_array_equal(a["slots"], b["slots"])
+    N = N_SUB ** 2
+    manual = np.einsum("mhk,mhkd->md", a["weights"], values[(a["slots"] + N // 2 + 1) % N])
+    np.testing.assert_allclose(b["out"], manual, rtol=1e-5, atol=1e-6)
+    assert not np.allclose(a["out"], b["out"])
+
+
+def test_temperature_clamp():
+    assert ol.clamp_temperature(np.log(2.0), 5.0, 100.0) == pytest.approx(5.0, rel=1e-6)
+    assert ol.clamp_temperature(np.log(500.0), 10.0, 100.0) == pytest.approx(100.0, rel=1e-6)
+    assert ol.clamp_temperature(np.log(20.0), 10.0, 100.0) == pytest.approx(20.0, rel=1e-6)
+
+
+def test_noise_only_changes_selection_and_never_weights_formula():
+    """tests:66-76: zero noise coefficient reproduces the clean picks; with
+    noise the weights are still the softmax of the *clean* slot scores."""
+    q, keys, values = _inputs(7)
+    g = np.random.default_rng(8).gumbel(size=(q.shape[0], HEADS, 2, N_SUB)).astype(np.float32)
+    clean = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K)
+    zero = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K, gumbel=g, noise_coef=0.0)
+    noisy = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K, gumbel=g, noise_coef=5.0)
+    np.testing.assert_array_equal(clean["slots"], zero["slots"])
+    assert not np.array_equal(clean["slots"], noisy["slots"])
+    # clean slot score of every selected slot = its two clean sub-scores
+    n = N_SUB
+    cs = noisy["scores"]
+    ia, ib = noisy["slots"] // n, noisy["slots"] % n
+    m_i, h_i = np.meshgrid(np.arange(q.shape[0]), np.arange(HEADS), indexing="ij")
+    want = cs[m_i[..., None], h_i[..., None], 0, ia] + cs[m_i[..., None], h_i[..., None], 1, ib]
+    np.testing.assert_allclose(noisy["slot_scores"], want, rtol=1e-6)
+    e = np.exp(want - want.max(-1, keepdims=True))
+    np.testing.assert_allclose(noisy["weights"], e / e.sum(-1, keepdims=True), rtol=1e-5)
+
+
+# ------------------------------------------------------------------ A12
+def test_aux_counts_and_shapes():
+    """tests:30-37."""
+    rng = np.random.default_rng(9)
+    q = rng.standard_normal((3, 5, HEADS, D_KEY)).astype(np.float32)
+    keys = ol.l2_normalize(rng.standard_normal((HEADS, 2, N_SUB, D_KEY // 2)).astype(np.float32))
+    values = rng.standard_normal((N_SUB ** 2, D_VALUE)).astype(np.float32)
+    res = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K)
+    aux = ol.aux_stats(res, n=N_SUB, noisy=False)
+    assert res["out"].shape == (3, 5, D_VALUE)
+    assert aux["slots"].shape == (3, 5, HEADS, K)
+    assert aux["slot_counts"].sum() == 3 * 5 * HEADS * K
+    np.testing.assert_allclose(aux["subkey_counts"].sum(-1), 3 * 5 * K)
+
+
+def test_balance_loss_detects_collapse():
+    """tests:153-160."""
+    q, keys, _ = _inputs(10, M=4096)
+    collapsed = np.broadcast_to(q[:1], q.shape).copy()
+    a = ol.aux_stats(ol.lookup_forward(q, keys, None, np.log(10.0), top_k_=K), n=N_SUB, noisy=False)
+    b = ol.aux_stats(ol.lookup_forward(collapsed, keys, None, np.log(10.0), top_k_=K), n=N_SUB, noisy=False)
+    assert a["balance_loss"] < 1.5
+    assert b["balance_loss"] > 2 * a["balance_loss"]
+
+
+# ------------------------------------------------------------------ A13
+def _torch_forward(q, raw_keys, values, log_t, res, *, n, query_scale, balance_temperature_grad, f):
+    """Independent torch restatement of memory.py:136-213 with the selection
+    held fixed at the oracle's (sub_idx, flat_idx)."""
+    H, _, _, half = raw_keys.shape
+    M = q.shape[0]
+    k = res["sub_idx"].shape[-1]
+    qq = q.reshape(M, H, 2, half)
+    q_len = torch.sqrt((qq * qq).sum(-1, keepdim=True) + 1e-6) / np.sqrt(half)
+    qh = qq * torch.rsqrt((qq * qq).sum(-1, keepdim=True) + 1e-6)
+    kh = raw_keys * torch.rsqrt((raw_keys * raw_keys).sum(-1, keepdim=True) + 1e-6)
+    lt = log_t + (torch.clamp(log_t, np.log(10.0), np.log(100.0)) - log_t).detach()
+    T = torch.exp(lt)
+    cos = torch.einsum("mhcd,hcnd->mhcn", qh, kh)
+    scores = cos * T
+    if query_scale:
+        scores = scores * q_len
+    sub_idx = torch.as_tensor(res["sub_idx"])
+    sub = torch.gather(scores, -1, sub_idx)
+    cand = (sub[:, :, 0, :, None] + sub[:, :, 1, None, :]).reshape(M, H, k * k)
+    slot_scores = torch.gather(cand, -1, torch.as_tensor(res["flat_idx"]))
+    w = torch.softmax(slot_scores, -1)
+    rows = values[torch.as_tensor(res["read_slots"]).reshape(-1)].reshape(M, H, k, -1)
+    out = torch.einsum("mhk,mhkd->md", w, rows)
+    p_scores = scores if balance_temperature_grad else cos * T.detach()
+    P = torch.softmax(p_scores, -1).mean(0)
+    bal = n * torch.mean(torch.sum(torch.as_tensor(f) * P, -1))
+    return out, bal
+
+
+@pytest.mark.parametrize("query_scale,btg,g_bal", [(False, False, 0.0), (True, False, 0.7), (False, True, 1.3)])
+def test_backward_matches_torch_autograd(query_scale, btg, g_bal):
+    q, keys, values = _inputs(11, M=12, n=16, d_key=8)
+    raw = keys * 1.7  # non-unit raw keys so the normalisation backward matters
+    log_t = np.log(20.0)
+    res = ol.lookup_forward(q, raw, values, log_t, top_k_=K, query_scale=query_scale, dtype=np.float64)
+    aux = ol.aux_stats(res, n=16, noisy=False, balance_temperature_grad=btg)
+    g = np.random.default_rng(12).standard_normal((12, D_VALUE))
+    got = ob.lookup_backward(res, values, g, n=16, query_scale=query_scale, g_balance=g_bal,
+                             f=aux["_f"], balance_temperature_grad=btg, dense_values=True)
+    tq = torch.tensor(q, dtype=torch.float64, requires_grad=True)
+    tk = torch.tensor(raw, dtype=torch.float64, requires_grad=True)
+    tv = torch.tensor(values, dtype=torch.float64, requires_grad=True)
+    tl = torch.tensor(log_t, dtype=torch.float64, requires_grad=True)
+    out, bal = _torch_forward(tq, tk, tv, tl, res, n=16, query_scale=query_scale,
+                              balance_temperature_grad=btg, f=aux["_f"])
+    loss = (out * torch.tensor(g)).sum() + g_bal * bal
+    loss.backward()
+    np.testing.assert_allclose(got["d_queries"], tq.grad.numpy(), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(got["d_sub_keys"], tk.grad.numpy(), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(got["d_log_temperature"], tl.grad.item(), rtol=1e-9, atol=1e-12)
+    np.testing.assert_allclose(got["d_values"], tv.grad.numpy(), rtol=1e-9, atol=1e-12)
+
+
+# ------------------------------------------------------------------ A14-A15
+def test_merge_rows_equals_dense_gradient_and_untouched_rows_are_zero():
+    """tests:321-344: scatter of the merged rows == autograd dense dV."""
+    q, keys, values = _inputs(13, M=30)
+    res = ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=K)
+    g = np.random.default_rng(14).standard_normal((30, D_VALUE)).astype(np.float32)
+    uniq, rows = orow.fetched_row_grads([res["slots"]], [res["weights"]], [g], N_SUB ** 2)
+    tv = torch.tensor(values, dtype=torch.float64, requires_grad=True)
+    rd = torch.as_tensor(res["slots"]).reshape(-1)
+    out = torch.einsum("mr,mrd->md", torch.tensor(res["weights"], dtype=torch.float64).reshape(30, -1),
+                       tv[rd].reshape(30, -1, D_VALUE))
+    (out * torch.tensor(g, dtype=torch.float64)).sum().backward()
+    dense = np.zeros_like(values, dtype=np.float64)
+    keep = uniq < N_SUB ** 2
+    dense[uniq[keep]] = rows[keep]
+    np.testing.assert_allclose(dense, tv.grad.numpy(), rtol=1e-4, atol=1e-6)
+    untouched = np.setdiff1d(np.arange(N_SUB ** 2), uniq)
+    assert np.all(tv.grad.numpy()[untouched] == 0)
+    # cap and padding semantics of jnp.unique(size=cap, fill_value=pool_size)
+    assert uniq.shape[0] == min(30 * HEADS * K, N_SUB ** 2)
+    assert np.all(np.diff(uniq[keep]) > 0) and np.all(uniq[~keep] == N_SUB ** 2)
+
+
+def test_merge_rows_cap_is_pool_size_when_fetches_exceed_it():
+    slots = np.array([5, 1, 5, 3, 1, 1, 0, 2])
+    contribs = np.arange(16, dtype=np.float32).reshape(8, 2)
+    uniq, rows = orow.merge_rows(slots, contribs, 6)
+    assert uniq.tolist() == [0, 1, 2, 3, 5, 6]
+    np.testing.assert_array_equal(rows[1], contribs[1] + contribs[4] + contribs[5])
+    np.testing.assert_array_equal(rows[5], [0, 0])
+
+
+# ------------------------------------------------------------------ A16-A18
+def test_rowwise_adagrad_known_answer():
+    """tests:505-513: grads of ones on rows [3, 7] + padding 1000."""
+    values = np.random.default_rng(0).standard_normal((1000, 64)).astype(np.float32)
+    acc = np.zeros(1000, np.float32)
+    before = values.copy()
+    orow.rowwise_adagrad(values, acc, np.array([3, 7, 1000]), np.ones((3, 64), np.float32), lr=0.1)
+    changed = np.flatnonzero(np.any(values != before, axis=1))
+    assert changed.tolist() == [3, 7] and acc[3] == 1.0
+    # acc' = 1 -> step = -0.1 / (1 + 1e-8) per element
+    np.testing.assert_allclose(values[3] - before[3], -0.1 / (1 + 1e-8), rtol=1e-6)
+
+
+def test_rowwise_adagrad_fp16_table_with_master():
+    values = np.zeros((10, 8), np.float16)
+    master = np.zeros((10, 8), np.float32)
+    acc = np.zeros(10, np.float32)
+    g = np.full((2, 8), 2.0, np.float32)
+    orow.rowwise_adagrad(values, acc, np.array([1, 4]), g, lr=0.5, master=master)
+    # acc = mean(4) = 4 -> step = -0.5 / 2 * 2 = -0.5
+    np.testing.assert_allclose(master[[1, 4]], -0.5, rtol=1e-6)
+    assert values.dtype == np.float16 and np.all(values[[1, 4]] == np.float16(-0.5))
+    np.testing.assert_allclose(acc[[1, 4]], 4.0)
+
+
+def test_lazy_adam_first_step_closed_form():
+    rng = np.random.default_rng(3)
+    values = rng.standard_normal((50, 16)).astype(np.float32)
+    m = np.zeros_like(values)
+    v = np.zeros_like(values)
+    before = values.copy()
+    g = rng.standard_normal((3, 16)).astype(np.float32)
+    orow.lazy_adam(values, m, v, np.array([2, 9, 50]), g, lr=0.01, step=0)
+    np.testing.assert_allclose(values[[2, 9]] - before[[2, 9]], -0.01 * g[:2] / (np.abs(g[:2]) + 1e-8),
+                               rtol=2e-4, atol=1e-9)
+    np.testing.assert_allclose(m[[2, 9]], 0.1 * g[:2], rtol=1e-6)
+    np.testing.assert_allclose(v[[2, 9]], 0.001 * g[:2] ** 2, rtol=5e-5)  # fp32(1 - 0.999) != 1e-3
+    others = np.setdiff1d(np.arange(50), [2, 9])
+    np.testing.assert_array_equal(values[others], before[others])
+
+
+def test_clip_scale_closed_form():
+    s, gnorm = orow.clip_scale(9.0, np.full((2, 8), 1.0), grad_clip=1.0)
+    assert gnorm == pytest.approx(5.0)
+    assert s == pytest.approx(1.0 / (5.0 + 1e-6))
+    s, _ = orow.clip_scale(0.0, np.full((1, 1), 0.1), grad_clip=1.0)
+    assert s == 1.0
+
+
+def test_warmup_cosine_closed_form():
+    lr = 3e-3
+    assert orow.warmup_cosine(0, lr, 200, 6000) == 0.0
+    assert orow.warmup_cosine(100, lr, 200, 6000) == pytest.approx(lr / 2)
+    assert orow.warmup_cosine(200, lr, 200, 6000) == pytest.approx(lr)
+    assert orow.warmup_cosine(3100, lr, 200, 6000) == pytest.approx(lr * 0.55)
+    assert orow.warmup_cosine(6000, lr, 200, 6000) == pytest.approx(0.1 * lr)
+    assert orow.warmup_cosine(9000, lr, 200, 6000) == pytest.approx(0.1 * lr)
