@@ -1,0 +1,280 @@
+"""Benchmark of the memory-layer lookup on one MI355X.
+
+Headline (``value``): lookup tokens/s on the text-study layer, 8,192 tokens,
+262,144 fp16 slots (H=4, d_key=256, k=16, d_value=256).  One step is the full
+lookup of memory.py:132-193 on inputs already resident in HBM: sub-key
+normalisation + packing, query normalisation, scoring with the two-stage
+top-k and softmax, and the fp16 gather-weighted-sum.
+
+Also reported in the same JSON line:
+  * ``roofline``: the dominant kernel's algorithmic throughput against
+    MI355X's published peak, timed with HIP events on its own stream;
+  * ``pool_67M``: the large-pool decode lookup (67,108,864 fp16 slots, 34 GB
+    in HBM) at 1, 16, 256 and 4,096 tokens, with the gather's HBM roofline;
+  * ``cpu_baseline``: the numpy oracle on the host cores over a bounded sample
+    of the same workload.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "memory-layer lookups tokens/s at 262k & 67M slots; gather HBM GB/s % peak"
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-large", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    return ap.parse_args()
+
+
+class Lookup:
+    """Preallocated buffers + direct C-ABI calls for one workload."""
+
+    def __init__(self, torch, L, *, M, H, n, d_key, d, k, seed, values=None):
+        from model_amd import _lib
+
+        self.torch, self.L, self._lib = torch, L, _lib
+        self.M, self.H, self.n, self.half, self.d, self.k = M, H, n, d_key // 2, d, k
+        dev = "cuda"
+        g = torch.Generator(device=dev).manual_seed(seed)
+        # hidden ~ N(0,1) [M, 256] through a Xavier-uniform 256 -> H*d_key query projection
+        d_model = 256
+        hidden = torch.randn((M, d_model), generator=g, device=dev)
+        lim = math.sqrt(6.0 / (d_model + H * d_key))
+        w_q = (torch.rand((d_model, H * d_key), generator=g, device=dev) * 2 - 1) * lim
+        self.q = (hidden @ w_q).reshape(M, H, 2, self.half).contiguous()
+        self.sub_keys = torch.randn((H, 2, n, self.half), generator=g, device=dev) * (self.half ** -0.5)
+        if values is None:
+            values = torch.empty((n * n, d), dtype=torch.float16, device=dev)
+            values.normal_(0.0, 0.02, generator=g)
+        self.values = values
+        self.T = 10.0
+        f32, i32, u8 = torch.float32, torch.int32, torch.uint8
+        self.q_hat = torch.empty_like(self.q)
+        self.q16 = torch.empty_like(self.q, dtype=torch.float16)
+        self.k_hat = torch.empty_like(self.sub_keys)
+        self.packed = torch.empty(L.mpl_packed_keys_bytes(H, n, self.half, _lib.MPL_F16), dtype=u8, device=dev)
+        self.ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, self.half, k)
+        self.ws = torch.empty(max(1, self.ws_bytes), dtype=u8, device=dev)
+        self.sub_idx = torch.empty((M, H, 2, k), dtype=i32, device=dev)
+        self.sub_scores = torch.empty((M, H, 2, k), dtype=f32, device=dev)
+        self.flat_idx = torch.empty((M, H, k), dtype=i32, device=dev)
+        self.slots = torch.empty((M, H, k), dtype=i32, device=dev)
+        self.weights = torch.empty((M, H, k), dtype=f32, device=dev)
+        self.out = torch.empty((M, d), dtype=f32, device=dev)
+
+    @property
+    def stream(self):
+        # queried per call: under graph capture the current stream is the capture stream
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def pack(self):
+        p = self._lib.ptr
+        self._lib.check(self.L.mpl_pack_keys(p(self.sub_keys), self.H, self.n, self.half, self._lib.MPL_F16,
+                                             p(self.k_hat), p(self.packed), self.stream), "pack")
+
+    def norm(self):
+        p = self._lib.ptr
+        self._lib.check(self.L.mpl_l2_normalize(p(self.q), self.M * self.H * 2, self.half, 1e-6, p(self.q_hat),
+                                                p(self.q16), None, self.stream), "norm")
+
+    def select(self):
+        p = self._lib.ptr
+        self._lib.check(self.L.mpl_score_select(
+            p(self.q16), None, p(self.packed), self.M, self.H, self.n, self.half, self.k, self._lib.MPL_F16,
+            self.T, None, 0.0, p(self.ws), self.ws_bytes, p(self.sub_idx), p(self.sub_scores), p(self.flat_idx),
+            p(self.slots), p(self.weights), self.stream), "select")
+
+    def gather(self):
+        p = self._lib.ptr
+        self._lib.check(self.L.mpl_gather_wsum(p(self.values), self._lib.MPL_F16, self.n * self.n, self.d,
+                                               p(self.slots), p(self.weights), self.M, self.H * self.k, 0,
+                                               p(self.out), self.stream), "gather")
+
+    def step(self):
+        self.pack()
+        self.norm()
+        self.select()
+        self.gather()
+
+
+def time_loop(torch, fn, iters, warmup):
+    """Average ms per call of fn: `iters` calls captured in one HIP graph,
+    replayed between HIP events on the current stream (the stream every entry
+    point is launched on), so host launch overhead is not measured."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(max(1, warmup)):
+            fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(iters):
+            fn()
+    graph.replay()  # warm replay
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / iters
+    del graph
+    return ms
+
+
+def kernel_breakdown(torch, lk, iters):
+    return {
+        "pack_keys_ms": time_loop(torch, lk.pack, iters, 3),
+        "normalize_ms": time_loop(torch, lk.norm, iters, 3),
+        "score_select_ms": time_loop(torch, lk.select, iters, 3),
+        "gather_wsum_ms": time_loop(torch, lk.gather, iters, 3),
+    }
+
+
+def roofline_for(lk, br):
+    """The dominant entry point of one lookup and its roofline."""
+    gather_bytes = lk.M * lk.H * lk.k * lk.d * 2          # fp16 rows read
+    score_flops = 2.0 * lk.H * 2 * lk.n * lk.half * lk.M  # 2048*n per token at d_key=256
+    g = gather_bytes / (br["gather_wsum_ms"] * 1e-3) / 1e9
+    s = score_flops / (br["score_select_ms"] * 1e-3) / 1e12
+    if br["gather_wsum_ms"] >= br["score_select_ms"]:
+        return {"kernel": "gather_wsum", "bound": "hbm", "achieved": g, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": g / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": gather_bytes}
+    return {"kernel": "score_select", "bound": "mfma", "achieved": s, "peak": MFMA_F16_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": s / MFMA_F16_PEAK_TFLOPS, "traffic": None, "algorithmic_flops": score_flops}
+
+
+def gather_roofline(lk, br):
+    gb = lk.M * lk.H * lk.k * lk.d * 2
+    a = gb / (br["gather_wsum_ms"] * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
+            "algorithmic_bytes": gb}
+
+
+def cpu_baseline(seconds: float):
+    """The numpy oracle (oracle/lookup.py) on the host cores: the same layer
+    shape (262,144 fp16 slots, H=4, d_key=256, k=16) on batches of 1,024
+    tokens, repeated for about `seconds` seconds."""
+    from oracle import lookup as ol
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # pragma: no cover
+        blas_threads = 1
+    rng = np.random.default_rng(0)
+    H, n, half, k, d, M = 4, 512, 128, 16, 256, 1024
+    keys = (rng.standard_normal((H, 2, n, half)) * half ** -0.5).astype(np.float32)
+    values = (rng.standard_normal((n * n, d)) * 0.02).astype(np.float16)
+    w_q = ((rng.random((256, H * 2 * half)) * 2 - 1) * math.sqrt(6.0 / (256 + H * 2 * half))).astype(np.float32)
+    tokens, t0, runs = 0, time.perf_counter(), 0
+    while True:
+        q = (rng.standard_normal((M, 256)).astype(np.float32) @ w_q).reshape(M, H, 2 * half)
+        ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=k, with_dense=False)
+        tokens += M
+        runs += 1
+        el = time.perf_counter() - t0
+        if el >= seconds or runs >= 64:
+            break
+    return {"value": tokens / el, "unit": "tokens/s", "cores": int(blas_threads), "kind": "port",
+            "sample": f"{runs} batches x {M} tokens of the 262,144-slot fp16 layer (numpy oracle, "
+                      f"BLAS scoring on {blas_threads} threads, sort-based top-k single-threaded), {el:.1f} s"}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(see DESIGN.md for how the lookup would shard).", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    from model_amd import _lib
+
+    L = _lib.lib()
+    torch.cuda.set_device(0)
+
+    # ---- headline: 262,144 slots, 8,192 tokens
+    lk = Lookup(torch, L, M=8192, H=4, n=512, d_key=256, d=256, k=16, seed=0)
+    ms = time_loop(torch, lk.step, args.steps, args.warmup)
+    value = lk.M / (ms * 1e-3)
+    br = kernel_breakdown(torch, lk, max(20, args.steps // 2))
+    roof = roofline_for(lk, br)
+
+    # ---- large pool: 67,108,864 fp16 slots (34 GB) held in HBM
+    large = None
+    if not args.no_large:
+        n3 = 8192
+        vals = torch.empty((n3 * n3, 256), dtype=torch.float16, device="cuda")
+        vals.normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(3))
+        sweep = {}
+        for M in (1, 16, 256, 4096):
+            lk3 = Lookup(torch, L, M=M, H=4, n=n3, d_key=256, d=256, k=16, seed=10 + M, values=vals)
+            it = max(10, args.steps // (4 if M == 4096 else 2))
+            ms3 = time_loop(torch, lk3.step, it, max(3, args.warmup // 4))
+            entry = {"ms_per_step": ms3, "tokens_per_s": M / (ms3 * 1e-3)}
+            if M == 4096:
+                br3 = kernel_breakdown(torch, lk3, it)
+                entry["kernels"] = br3
+                entry["gather_roofline"] = gather_roofline(lk3, br3)
+            sweep[str(M)] = entry
+            del lk3
+        del vals
+        torch.cuda.empty_cache()
+        large = {"workload": "decode lookup, 67,108,864 fp16 slots (34 GB), H=4, d_key=256, k=16, d_value=256",
+                 "by_tokens": sweep}
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": "text-study memory-layer lookup: 8,192 tokens, 262,144 fp16 slots, H=4, "
+                               "d_key=256, n_sub_keys=512, top_k=16, d_value=256",
+                   "tokens": 8192, "slots": 262144, "values_dtype": "f16", "score_dtype": "f16 MFMA, f32 accumulate",
+                   "parallelism": "single GPU"},
+        "roofline": roof,
+        "kernels": br,
+        "pool_67M": large,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -42,12 +42,13 @@ const char* mpl_last_error(void);
 
 /*
  * memory.py:30-31 and 136-139: y = x * rsqrt(sum(x*x) + eps) over rows of
- * length `dim`.  x, y: [rows, dim] fp32 (may alias).  If row_len != NULL it
- * receives sqrt(sum(x*x) + eps) / sqrt(dim) per row: the q_len of
- * memory.py:137 (used when query_scale is on).
+ * length `dim`.  x, y: [rows, dim] fp32 (may alias).  If y16 != NULL it also
+ * receives y rounded to fp16 (the query operand of fp16 scoring).  If
+ * row_len != NULL it receives sqrt(sum(x*x) + eps) / sqrt(dim) per row: the
+ * q_len of memory.py:137 (used when query_scale is on).
  */
 int mpl_l2_normalize(const float* x, int64_t rows, int dim, float eps, float* y,
-                     float* row_len, void* stream);
+                     void* y16, float* row_len, void* stream);
 
 /*
  * memory.py:139: normalise sub_keys [H,2,n,half] (fp32) and pack them into
@@ -61,8 +62,8 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
                   float* keys_hat, void* packed, void* stream);
 
 /*
- * memory.py:149-178: cosine scores of q_hat [M,H,2,half] (fp32, unit rows)
- * against the packed keys, times `temperature` (already clamped, memory.py:
+ * memory.py:149-178: cosine scores of q_hat [M,H,2,half] (unit rows, in
+ * score_dtype: fp16 for MPL_F16, fp32 for MPL_F32) against the packed keys, times `temperature` (already clamped, memory.py:
  * 143-146) and times q_len [M,H,2] when q_len != NULL (query_scale,
  * memory.py:151-152); optional routing noise select = scores + noise_coef *
  * gumbel with gumbel [M,H,2,n] fp32 (memory.py:155-159, NULL = no noise);
@@ -78,7 +79,7 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
  * Requires 1 <= k <= min(n, 32), 1 <= half <= 128, n*n < 2^31.
  */
 size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int half, int k);
-int mpl_score_select(const float* q_hat, const float* q_len, const void* packed_keys,
+int mpl_score_select(const void* q_hat, const float* q_len, const void* packed_keys,
                      int64_t M, int H, int n, int half, int k, int score_dtype,
                      float temperature, const float* gumbel, float noise_coef,
                      void* workspace, size_t workspace_bytes,

@@ -19,7 +19,7 @@ _P, _I, _I64, _F, _SZ = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
 SIGNATURES = {
     "mpl_version": (_I, []),
     "mpl_last_error": (C.c_char_p, []),
-    "mpl_l2_normalize": (_I, [_P, _I64, _I, _F, _P, _P, _P]),
+    "mpl_l2_normalize": (_I, [_P, _I64, _I, _F, _P, _P, _P, _P]),
     "mpl_packed_keys_bytes": (_SZ, [_I, _I, _I, _I]),
     "mpl_pack_keys": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "mpl_score_select_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),

@@ -47,6 +47,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_wsum_kernel(
   constexpr int RPI = kWave / LPR;
   constexpr int VPL = VR <= kWave ? 1 : VR / kWave;
   constexpr int VE = Vec16<V>::kElems;
+  constexpr int NB = VPL >= 4 ? 4 : 16 / VPL;  // row groups in flight per lane
   const int64_t m = (int64_t)blockIdx.x * (kGatherThreads / kWave) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (m >= M) return;
@@ -61,27 +62,38 @@ __global__ __launch_bounds__(kGatherThreads) void gather_wsum_kernel(
   const uint4* base = (const uint4*)values;
   for (int r0 = 0; r0 < R; r0 += kWave) {
     const int rr = r0 + lane;
-    int sl = 0;
-    float ww = 0.f;
-    if (rr < R) {
-      sl = slots[m * R + rr];
-      ww = weights[m * R + rr];
-      if (shuffle) sl = (int)(((int64_t)sl + N / 2 + 1) % N);
-      sl = (int)min(max((int64_t)sl, (int64_t)0), N - 1);  // out-of-range ids read the nearest row
-    }
+    const bool in = rr < R;
+    int sl = slots[m * R + (in ? rr : 0)];  // unconditional (clamped) loads
+    float ww = weights[m * R + (in ? rr : 0)];
+    if (shuffle) sl = (int)(((int64_t)sl + N / 2 + 1) % N);
+    sl = in ? (int)min(max((int64_t)sl, (int64_t)0), N - 1) : 0;  // out-of-range ids read the nearest row
+    ww = in ? ww : 0.f;
     const int nr = min(kWave, R - r0);
-#pragma unroll 16
-    for (int g = 0; g < nr; g += RPI) {
-      const int row = g + sub;  // rows past nr carry weight 0 and slot 0
-      const int s = __shfl(sl, row);
-      const float wr = __shfl(ww, row);
-      const uint4* src = base + (int64_t)s * VR + col;
+    const int groups = (nr + RPI - 1) / RPI;  // row groups of this chunk
+    // Batches of NB row groups: all NB loads are issued before any is used.
+    for (int g0 = 0; g0 < groups; g0 += NB) {
+      uint4 buf[NB][VPL];
+      float wv[NB];
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        float f[VE];
-        Vec16<V>::unpack(src[v * kWave], f);
+      for (int b = 0; b < NB; ++b) {
+        const bool ok = g0 + b < groups;
+        const int row = ok ? (g0 + b) * RPI + sub : 0;  // rows past nr carry weight 0 and slot 0
+        const int s = __shfl(sl, row);
+        const float w = __shfl(ww, row);
+        wv[b] = ok ? w : 0.f;
+        const uint4* src = base + (int64_t)s * VR + col;
 #pragma unroll
-        for (int e = 0; e < VE; ++e) acc[v][e] = fmaf(wr, f[e], acc[v][e]);
+        for (int v = 0; v < VPL; ++v) buf[b][v] = src[v * kWave];
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          float f[VE];
+          Vec16<V>::unpack(buf[b][v], f);
+#pragma unroll
+          for (int e = 0; e < VE; ++e) acc[v][e] = fmaf(wv[b], f[e], acc[v][e]);
+        }
       }
     }
   }

@@ -8,6 +8,7 @@ namespace mpl {
 // 16 lanes per row, 16 rows per 256-thread block.
 __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x, int64_t rows,
                                                      int dim, float eps, float* y,
+                                                     _Float16* __restrict__ y16,
                                                      float* __restrict__ row_len) {
   const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
   const int l = threadIdx.x & 15;
@@ -26,7 +27,12 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x
     const float r = 1.0f / sqrtf(tot);
     const float* xr = x + row * dim;
     float* yr = y + row * dim;
-    for (int j = l; j < dim; j += 16) yr[j] = xr[j] * r;
+    _Float16* hr = y16 != nullptr ? y16 + row * dim : nullptr;
+    for (int j = l; j < dim; j += 16) {
+      const float v = xr[j] * r;
+      yr[j] = v;
+      if (hr != nullptr) hr[j] = (_Float16)v;
+    }
     if (row_len != nullptr && l == 0) row_len[row] = sqrtf(tot) / sqrtf((float)dim);
   }
 }
@@ -74,12 +80,13 @@ static int pack_impl(const float* khat, int HC, int n, int half, void* packed, h
 using namespace mpl;
 
 extern "C" int mpl_l2_normalize(const float* x, int64_t rows, int dim, float eps, float* y,
-                                float* row_len, void* stream) {
+                                void* y16, float* row_len, void* stream) {
   clear_error();
   MPL_REQUIRE(rows >= 0 && dim > 0, MPL_EINVAL, "mpl_l2_normalize: bad sizes");
   if (rows == 0) return MPL_OK;
   MPL_REQUIRE(x && y, MPL_EINVAL, "mpl_l2_normalize: null buffer");
-  l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, (hipStream_t)stream>>>(x, rows, dim, eps, y, row_len);
+  l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, (hipStream_t)stream>>>(x, rows, dim, eps, y,
+                                                                             (_Float16*)y16, row_len);
   return check_launch("mpl_l2_normalize");
 }
 
@@ -105,7 +112,7 @@ extern "C" int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int 
   const int64_t rows = (int64_t)2 * H * n;
   float* khat = keys_hat;
   MPL_REQUIRE(khat != nullptr, MPL_EINVAL, "mpl_pack_keys: keys_hat buffer is required");
-  l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, s>>>(sub_keys, rows, half, 1e-6f, khat, nullptr);
+  l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, s>>>(sub_keys, rows, half, 1e-6f, khat, nullptr, nullptr);
   int rc = check_launch("mpl_pack_keys(normalise)");
   if (rc) return rc;
   return score_dtype == MPL_F16 ? pack_impl<_Float16>(khat, 2 * H, n, half, packed, s)

@@ -7,47 +7,52 @@
 // blocks of 32 stream through LDS (double buffered); each wave computes a
 // 32-key x 64-query score tile with two 32x32 MFMA chains, then swaps register
 // halves across lanes (v_permlane32_swap) so that lane l owns query l with
-// all 32 scores of the block.  Each lane keeps its query's running top-k as a
-// sorted register list and a threshold (its k-th best).  Scores above the
-// threshold are appended to a per-lane LDS candidate buffer; when any lane's
-// buffer is nearly full the wave merges buffers into the lists (sorted
-// insertion, strict '>' so an equal later key never displaces an earlier
-// one).  Keys are visited in increasing index order, which makes the order
-// (score desc, index asc) of lax.top_k fall out of the insertion rule.  The
-// scores never leave registers/LDS.
+// all 32 scores of the block.  Each lane keeps its query's best k as sorted
+// 64-bit keys (topk.h) in registers and a threshold (the k-th best score).
+// Scores above the threshold go to a per-lane LDS candidate buffer; when any
+// lane's buffer is nearly full the wave sorts the buffered candidates in
+// chunks of 8 and bitonic-merges them into the lists.  Keys of equal score
+// order by index, so the result is exactly lax.top_k's.  The scores never
+// leave registers/LDS.
 //
 // Without routing noise the selection runs on the raw cosine: scores are
 // cos*T(*q_len) with positive per-query factors, so the order is the same up
 // to ties created by the rounding of that product (near-ties).
 //
-// Stage 2 (stage2_kernel).  One thread per (token, head): merges the split
-// lists of each codebook, then walks the k*k candidate grid in frontier order
-// (row pointers; at step s only rows <= s can hold the next best), selecting
-// by (select sum desc, flat index rank_a*k+rank_b asc) as memory.py:171, and
-// finishes with the softmax of the clean slot scores (memory.py:178).
+// Split plans.  Few tokens cannot fill the GPU with one workgroup per 128
+// queries, so the key range of each codebook is split across workgroups and
+// the per-split lists are merged (merge_*_kernel): per thread from registers
+// for up to 4 splits, per wave for more (decode-sized batches).
+//
+// Stage 2 (stage2_kernel).  One thread per (token, head) walks the k*k
+// candidate grid in frontier order (row pointers; at step s only rows <= s
+// can hold the next best), selecting by (select sum desc, flat index
+// rank_a*k + rank_b asc) as memory.py:171, and finishes with the softmax of
+// the clean slot scores (memory.py:178).
 #include <limits.h>
 #include <math.h>
 
 #include "common.h"
 #include "layout.h"
+#include "topk.h"
 
 namespace mpl {
 
-constexpr int kCand = 24;         // per-lane candidate buffer (entries)
+constexpr int kCand = 24;           // per-lane candidate buffer (entries)
 constexpr int kScoreThreads = 128;  // two waves per workgroup
-constexpr int kMaxSplits = 16;
+constexpr int kMaxSplits = 64;
 
 struct ScoreParams {
-  const float* q_hat;   // [M, HC, half]
+  const void* q_hat;    // [M, HC, half] in the scoring type
   const float* q_len;   // [M, HC] or null
   const uint4* packed;  // packed keys
   const float* gumbel;  // [M, HC, n] or null
   float T, noise_coef;
   int64_t M;
   int HC, n, half, k, nblk, splits, blk_per_split;
-  float* out_sel;    // [splits, M, HC, k] (may be null when no noise and splits == 1)
-  float* out_clean;  // [splits, M, HC, k]
-  int* out_idx;      // [splits, M, HC, k]
+  float* out_sel;    // [splits, HC, k, M] (null without noise: equals clean)
+  float* out_clean;  // [splits, HC, k, M]
+  int* out_idx;      // [splits, HC, k, M]
 };
 
 template <typename T>
@@ -59,12 +64,21 @@ struct Mfma<_Float16> {
   __device__ static f32x16 mma(Op a, Op b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
-  // B operand for chunk c: dims 16c + 8*(lane/32) + [0,8) of query row q.
-  __device__ static Op load_q(const float* q, bool valid, int half, int c, int lane) {
+  // B operand for chunk c: dims 16c + 8*(lane/32) + [0,8) of fp16 query row
+  // q: one 16-byte load (rows of a multiple of 8 dims) or clamped element
+  // loads.  Loads are unconditional and zeroed after: a guarded load compiles
+  // to a branch with its own wait, serialising every element.
+  __device__ static Op load_q(const _Float16* q, bool valid, int half, int c, int lane) {
     Op o;
     const int d0 = 16 * c + 8 * (lane >> 5);
+    if ((half & 7) == 0) {
+      o = *(const half8*)(q + (d0 < half ? d0 : 0));
+    } else {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (valid && d0 + i < half) ? (_Float16)q[d0 + i] : (_Float16)0.f;
+      for (int i = 0; i < 8; ++i) o[i] = q[min(d0 + i, half - 1)];
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (valid && d0 + i < half) ? o[i] : (_Float16)0.f;
     return o;
   }
   __device__ static Op from_vec(uint4 u, int) { return __builtin_bit_cast(half8, u); }
@@ -78,7 +92,8 @@ struct Mfma<float> {
   }
   __device__ static Op load_q(const float* q, bool valid, int half, int c, int lane) {
     const int d = 2 * c + (lane >> 5);
-    return (valid && d < half) ? q[d] : 0.f;
+    const float f = q[min(d, half - 1)];
+    return (valid && d < half) ? f : 0.f;
   }
   __device__ static Op from_vec(uint4 u, int e) {
     const unsigned w = e == 0 ? u.x : e == 1 ? u.y : e == 2 ? u.z : u.w;
@@ -86,57 +101,87 @@ struct Mfma<float> {
   }
 };
 
-// Sorted (descending) register list; insertion keeps earlier entries ahead
-// of equal later ones.
+// Per-lane selection state of the stage-1 kernel.
 template <int KMAX, bool NOISE>
-struct TopList {
-  float v[KMAX];
-  int id[KMAX];
-  float cl[NOISE ? KMAX : 1];
-
-  __device__ void init() {
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) {
-      v[j] = -INFINITY;
-      id[j] = INT_MAX;
-      if (NOISE) cl[j] = -INFINITY;
-    }
-  }
-  __device__ void insert(float x, int xi, float xc) {
-    bool c[KMAX];
-#pragma unroll
-    for (int j = 0; j < KMAX; ++j) c[j] = x > v[j];
-#pragma unroll
-    for (int j = KMAX - 1; j >= 1; --j) {
-      v[j] = c[j - 1] ? v[j - 1] : (c[j] ? x : v[j]);
-      id[j] = c[j - 1] ? id[j - 1] : (c[j] ? xi : id[j]);
-      if (NOISE) cl[j] = c[j - 1] ? cl[j - 1] : (c[j] ? xc : cl[j]);
-    }
-    v[0] = c[0] ? x : v[0];
-    id[0] = c[0] ? xi : id[0];
-    if (NOISE) cl[0] = c[0] ? xc : cl[0];
-  }
-  __device__ float kth(int k) const {
-    float t = v[0];
-#pragma unroll
-    for (int j = 1; j < KMAX; ++j) t = (j == k - 1) ? v[j] : t;
-    return t;
-  }
+struct LaneSel {
+  TopList<KMAX, NOISE> top;
+  float thr;
+  int cnt;
 };
+
+// Merges the lane's buffered candidates (cbuf/cpay column `lane`) into its
+// list and refreshes the threshold.  Wave-uniform control flow.
+template <int KMAX, bool NOISE>
+__device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const u64 (*cbuf)[kWave],
+                                           const float (*cpay)[kWave], int lane, bool valid, int k,
+                                           float base_thr) {
+  // Rolled on purpose: this body is inlined at five sites of the block loop
+  // and unrolled copies overflow the instruction cache.
+#pragma unroll 1
+  for (int c0 = 0; c0 < kCand; c0 += 8) {
+    if (__ballot(c0 < st.cnt) == 0) break;
+    u64 ch[8];
+    float cp[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool in = c0 + i < st.cnt;
+      ch[i] = in ? cbuf[c0 + i][lane] : 0ull;
+      cp[i] = (NOISE && in) ? cpay[NOISE ? c0 + i : 0][lane] : 0.f;
+    }
+    sort8<NOISE>(ch, cp);
+    st.top.template merge<8>(ch, cp);
+  }
+  st.cnt = 0;
+  if (valid) {
+    const u64 kk = st.top.at(k - 1);
+    st.thr = kk ? key_score(kk) : base_thr;
+  }
+}
+
+// k-th largest (k <= 32) of the 32 floats a[0..15], b[0..15]: bitonic sort
+// of the orderable bit patterns (max/min only), then a masked pick.
+__device__ __forceinline__ float kth_of_32(const float* a, const float* b, int k) {
+  uint32_t v[32];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    v[i] = orderable(a[i]);
+    v[16 + i] = orderable(b[i]);
+  }
+#pragma unroll
+  for (int size = 2; size <= 32; size <<= 1) {
+#pragma unroll
+    for (int stride = size / 2; stride >= 1; stride >>= 1) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        const int j = i ^ stride;
+        if (j > i) {
+          const bool desc = (i & size) == 0;  // sort descending overall
+          const uint32_t x = v[i], y = v[j];
+          v[i] = desc ? max(x, y) : min(x, y);
+          v[j] = desc ? min(x, y) : max(x, y);
+        }
+      }
+    }
+  }
+  uint32_t t = 0;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) t |= v[i] & (0u - (uint32_t)(i == k - 1));
+  return from_orderable(t);
+}
 
 template <typename T, int HP, bool NOISE, int KMAX>
 __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {
-  constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);   // 16-B vectors per lane per block
+  constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);  // 16-B vectors per lane per block
   constexpr int OPV = KeyPack<T>::kOpsPerVec;
-  constexpr int NCH = VPL * OPV;                          // MFMA chunks per block
-  constexpr int TILE = VPL * kWave;                       // uint4 per key block
+  constexpr int NCH = VPL * OPV;                         // MFMA chunks per block
+  constexpr int TILE = VPL * kWave;                      // uint4 per key block
   constexpr int PRE = (TILE + kScoreThreads - 1) / kScoreThreads;
+  constexpr int TILE_ALLOC = PRE * kScoreThreads;  // >= TILE: every thread stores unguarded
   typedef typename Mfma<T>::Op Op;
 
-  __shared__ uint4 tiles[2][TILE];
-  __shared__ float cs_[2][kCand][kWave];
-  __shared__ int ci_[2][kCand][kWave];
-  __shared__ float cc_[NOISE ? 2 : 1][NOISE ? kCand : 1][kWave];
+  __shared__ uint4 tiles[2][TILE_ALLOC];
+  __shared__ u64 cbuf[2][kCand][kWave];
+  __shared__ float cpay[NOISE ? 2 : 1][NOISE ? kCand : 1][kWave];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -154,273 +199,304 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   for (int s = 0; s < 2; ++s) {
     const int64_t qi = q0 + 32 * s + (lane & 31);
     const bool ok = qi < p.M;
-    const float* qrow = p.q_hat + (ok ? (qi * p.HC + hc) * (int64_t)p.half : 0);
+    const T* qrow = (const T*)p.q_hat + (ok ? (qi * p.HC + hc) * (int64_t)p.half : 0);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) qop[s][c] = Mfma<T>::load_q(qrow, ok, p.half, c, lane);
   }
 
-  // Lane state: after the half swap lane l owns query q0 + l.
+  // After the half swap lane l owns query q0 + l.
   const int64_t my_q = q0 + lane;
   const bool valid = my_q < p.M;
-  const float ql = (p.q_len != nullptr && valid) ? p.q_len[my_q * p.HC + hc] : 1.f;
-  const float* grow = NOISE && valid ? p.gumbel + (my_q * p.HC + hc) * (int64_t)p.n : nullptr;
-  TopList<KMAX, NOISE> top;
-  top.init();
-  float thr = valid ? -INFINITY : INFINITY;
-  int cnt = 0;
+  const float ql = p.q_len != nullptr ? p.q_len[(valid ? my_q : 0) * p.HC + hc] : 1.f;
+  const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
+  const u64(*mybuf)[kWave] = cbuf[wave];
+  const float(*mypay)[kWave] = cpay[NOISE ? wave : 0];
 
-  auto flush = [&]() {
-    for (int e = 0; e < kCand; ++e) {
-      if (__ballot(e < cnt) == 0) break;
-      const float x = e < cnt ? cs_[wave][e][lane] : -INFINITY;
-      const int xi = ci_[wave][e][lane];
-      const float xc = NOISE ? cc_[NOISE ? wave : 0][NOISE ? e : 0][lane] : 0.f;
-      top.insert(x, xi, xc);
-    }
-    cnt = 0;
-    if (valid) thr = top.kth(p.k);
-  };
-
+  // Key blocks are software-pipelined one block ahead: `pre` holds block b+1
+  // during block b's compute, is stored to the free LDS buffer after it, and
+  // is immediately refilled with block b+2.  The loads are loop-carried, so
+  // the compiler cannot sink them next to their stores.  No load or store is
+  // guarded (clamped sources, padded tiles): a guard would serialise them.
+  // (A vector type, not an array: a loop-carried array is not promoted to
+  // registers.)
+  typedef unsigned PreVec __attribute__((ext_vector_type(4 * PRE)));
   const uint4* kbase_ptr = p.packed + (int64_t)hc * p.nblk * TILE;
-  if (b_begin < b_end) {
+  auto fetch = [&](int blk) __attribute__((always_inline)) {
+    PreVec v;
+    const uint4* src = kbase_ptr + (int64_t)blk * TILE;
 #pragma unroll
     for (int i = 0; i < PRE; ++i) {
-      const int t = tid + i * kScoreThreads;
-      if (t < TILE) tiles[0][t] = kbase_ptr[(int64_t)b_begin * TILE + t];
+      const uint4 u = src[min(tid + i * kScoreThreads, TILE - 1)];
+      v[4 * i] = u.x;
+      v[4 * i + 1] = u.y;
+      v[4 * i + 2] = u.z;
+      v[4 * i + 3] = u.w;
     }
-  }
-  __syncthreads();
+    return v;
+  };
+  auto stage = [&](int buf, const PreVec& v) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < PRE; ++i)
+      tiles[buf][tid + i * kScoreThreads] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  };
 
-  for (int b = b_begin; b < b_end; ++b) {
-    const int cur = (b - b_begin) & 1;
-    const bool has_next = b + 1 < b_end;
-    uint4 pre[PRE];
-    if (has_next) {
+  // One sweep over this split's key blocks.  body(kb, sa, sb, ca, cb) gets
+  // the 32 selection values of the lane's query (sa[r]: key kb + 8*(r/4) +
+  // r%4, sb[r]: key kb + 8*(r/4) + 4 + r%4; padded keys are -inf) and, with
+  // noise, the clean scores ca/cb.
+  auto sweep = [&](auto&& body) __attribute__((always_inline)) {
+    PreVec pre = fetch(b_begin < b_end ? b_begin : 0);
+    stage(0, pre);
+    pre = fetch(b_begin < b_end ? min(b_begin + 1, b_end - 1) : 0);
+    __syncthreads();
+    for (int b = b_begin; b < b_end; ++b) {
+      const int cur = (b - b_begin) & 1;
+      float gblk[NOISE ? 32 : 1];  // this block's routing noise, fetched before the MFMAs
+      if (NOISE) {
 #pragma unroll
-      for (int i = 0; i < PRE; ++i) {
-        const int t = tid + i * kScoreThreads;
-        if (t < TILE) pre[i] = kbase_ptr[(int64_t)(b + 1) * TILE + t];
+        for (int i = 0; i < 32; ++i) gblk[NOISE ? i : 0] = grow[min(b * 32 + i, p.n - 1)];
       }
-    }
-    f32x16 acc0 = {}, acc1 = {};
+      f32x16 acc0 = {}, acc1 = {};
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const uint4 u = tiles[cur][v * kWave + lane];
+      for (int v = 0; v < VPL; ++v) {
+        const uint4 u = tiles[cur][v * kWave + lane];
 #pragma unroll
-      for (int e = 0; e < OPV; ++e) {
-        const Op a = Mfma<T>::from_vec(u, e);
-        acc0 = Mfma<T>::mma(a, qop[0][v * OPV + e], acc0);
-        acc1 = Mfma<T>::mma(a, qop[1][v * OPV + e], acc1);
+        for (int e = 0; e < OPV; ++e) {
+          const Op a = Mfma<T>::from_vec(u, e);
+          acc0 = Mfma<T>::mma(a, qop[0][v * OPV + e], acc0);
+          acc1 = Mfma<T>::mma(a, qop[1][v * OPV + e], acc1);
+        }
       }
-    }
-    if (has_next) {
+      // acc0[r]: query q0 + lane%32, key 8*(r/4) + 4*(lane/32) + r%4 (acc1: query + 32).
+      float sa[16], sb[16], ca[NOISE ? 16 : 1], cb[NOISE ? 16 : 1];
 #pragma unroll
-      for (int i = 0; i < PRE; ++i) {
-        const int t = tid + i * kScoreThreads;
-        if (t < TILE) tiles[cur ^ 1][t] = pre[i];
+      for (int r = 0; r < 16; ++r) {
+        sa[r] = acc0[r];
+        sb[r] = acc1[r];
+        half_swap(sa[r], sb[r]);
       }
+      const int kb = b * 32;
+      if (NOISE) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int o = 8 * (r >> 2) + (r & 3);
+          float c0 = sa[r] * p.T, c1 = sb[r] * p.T;
+          if (p.q_len != nullptr) {
+            c0 *= ql;
+            c1 *= ql;
+          }
+          ca[NOISE ? r : 0] = c0;
+          cb[NOISE ? r : 0] = c1;
+          sa[r] = c0 + p.noise_coef * gblk[NOISE ? o : 0];
+          sb[r] = c1 + p.noise_coef * gblk[NOISE ? o + 4 : 0];
+        }
+      }
+      if (kb + 32 > p.n) {  // wave-uniform: only the last block can hold padded keys
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int o = kb + 8 * (r >> 2) + (r & 3);
+          if (o >= p.n) sa[r] = -INFINITY;
+          if (o + 4 >= p.n) sb[r] = -INFINITY;
+        }
+      }
+      body(kb, sa, sb, ca, cb);
+      // Buffer cur^1 was last read before the previous barrier; past the last
+      // block the copies are clamped duplicates that are never read.
+      stage(cur ^ 1, pre);
+      pre = fetch(min(b + 2, b_end - 1));
+      __syncthreads();
     }
-    // acc0[r]: query q0 + lane%32, key 8*(r/4) + 4*(lane/32) + r%4 (acc1: query + 32).
-    float sa[16], sb[16];
+  };
+
+  // Pass 1: running maximum per key position (32 per lane, one v_max per
+  // score).  Each maximum is a distinct key's score, so the k-th largest of
+  // them is a lower bound on the lane's k-th best score (typically ~22 keys
+  // of any split clear it).
+  float ma[16], mb[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ma[r] = mb[r] = -INFINITY;
+  sweep([&](int, const float* sa, const float* sb, const float*, const float*) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      sa[r] = acc0[r];
-      sb[r] = acc1[r];
-      half_swap(sa[r], sb[r]);
+      ma[r] = fmaxf(ma[r], sa[r]);
+      mb[r] = fmaxf(mb[r], sb[r]);
     }
-    // Now, for lane-query q0 + lane: sa[r] -> key 8*(r/4) + r%4, sb[r] -> key 8*(r/4) + 4 + r%4.
-    const int kb = b * 32;
-    const bool tail = kb + 32 > p.n;
+  });
+  // Scores >= bound pass: strict '>' against the next float below it.
+  const float bound = kth_of_32(ma, mb, p.k);
+  const float base_thr = bound == -INFINITY ? -INFINITY : from_orderable(orderable(bound) - 1u);
+
+  // Pass 2: the same scores again; only candidates above the threshold are
+  // buffered and merged into the sorted register list.
+  LaneSel<KMAX, NOISE> st;
+  st.top.init();
+  st.thr = valid ? base_thr : INFINITY;
+  st.cnt = 0;
+  sweep([&](int kb, const float* sa, const float* sb, const float* ca, const float* cb)
+            __attribute__((always_inline)) {
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
-      if (__ballot(cnt > kCand - 8) != 0) flush();
+      if (__ballot(st.cnt > kCand - 8) != 0)
+        flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float cosv = e < 4 ? sa[4 * g + e] : sb[4 * g + e - 4];
-        const int key = kb + 8 * g + e;
-        float x = cosv, xc = 0.f;
-        if (NOISE) {
-          float clean = cosv * p.T;
-          if (p.q_len != nullptr) clean *= ql;
-          xc = clean;
-          const float gv = (valid && key < p.n) ? grow[key] : 0.f;
-          x = clean + p.noise_coef * gv;
-        }
-        bool hit = x > thr;
-        if (tail) hit = hit && key < p.n;
-        if (hit) {
-          cs_[wave][cnt][lane] = x;
-          ci_[wave][cnt][lane] = key;
-          if (NOISE) cc_[NOISE ? wave : 0][NOISE ? cnt : 0][lane] = xc;
-          ++cnt;
+        const int r = 4 * g + (e & 3);
+        const float x = e < 4 ? sa[r] : sb[r];
+        if (x > st.thr) {
+          cbuf[wave][st.cnt][lane] = make_key(x, kb + 8 * g + e);
+          if (NOISE) cpay[NOISE ? wave : 0][NOISE ? st.cnt : 0][lane] = e < 4 ? ca[NOISE ? r : 0] : cb[NOISE ? r : 0];
+          ++st.cnt;
         }
       }
     }
-    __syncthreads();
-  }
-  flush();
+  });
+  flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 
   if (valid) {
-    const int64_t o = ((int64_t)split * p.M + my_q) * p.HC + hc;
+    // Lists [split][M][hc][k]: each lane writes its query's k entries.
+    const int64_t o = (((int64_t)split * p.M + my_q) * p.HC + hc) * p.k;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
       if (r < p.k) {
+        const u64 kk = st.top.key[r];
         float clean, sel;
         if (NOISE) {
-          clean = top.cl[NOISE ? r : 0];
-          sel = top.v[r];
+          clean = st.top.pay[NOISE ? r : 0];
+          sel = key_score(kk);
         } else {
-          clean = top.v[r] * p.T;
+          clean = key_score(kk) * p.T;
           if (p.q_len != nullptr) clean *= ql;
           sel = clean;
         }
-        if (p.out_sel != nullptr) p.out_sel[o * p.k + r] = sel;
-        p.out_clean[o * p.k + r] = clean;
-        p.out_idx[o * p.k + r] = top.id[r];
+        if (kk == 0) clean = sel = -INFINITY;
+        if (NOISE) p.out_sel[o + r] = sel;
+        p.out_clean[o + r] = clean;
+        p.out_idx[o + r] = kk ? key_index(kk) : -1;
       }
     }
   }
 }
 
-struct Stage2Params {
-  const float* part_sel;    // [S, M, HC, k] (null: same as part_clean)
-  const float* part_clean;  // [S, M, HC, k]
-  const int* part_idx;      // [S, M, HC, k]
+// ----------------------------------------------------------------- stage 2
+// Stage-1 results arrive as "lists": sel / clean / idx arrays in the layout
+// [split][M][hc][k] (sel absent without noise, where it equals clean).
+struct PairParams {
+  const float* sel;
+  const float* clean;
+  const int* idx;
   int64_t M;
   int H, n, k, S;
-  int32_t* sub_idx;    // [M, HC, k]
-  float* sub_scores;   // [M, HC, k]
+  int32_t* sub_idx;    // [M, HC, k] (written when S > 1)
+  float* sub_scores;   // [M, HC, k] (written when S > 1)
   int32_t* flat_idx;   // [M, H, k]
   int32_t* slots;      // [M, H, k]
   float* weights;      // [M, H, k]
 };
 
-constexpr int kStage2Threads = 64;
-
-// Per-thread LDS columns: [field][entry][thread] keeps the 64 threads of a
-// wave on distinct banks for every dynamic access.
-template <int KMAX>
-__global__ __launch_bounds__(kStage2Threads) void stage2_kernel(Stage2Params p) {
-  __shared__ float sel_[2][KMAX][kStage2Threads];
-  __shared__ float cl_[2][KMAX][kStage2Threads];
-  __shared__ int id_[2][KMAX][kStage2Threads];
-  const int t = threadIdx.x;
-  const int64_t mh = (int64_t)blockIdx.x * kStage2Threads + t;
-  if (mh >= p.M * p.H) return;  // no barriers below
-  const int64_t m = mh / p.H;
-  const int h = (int)(mh % p.H);
+// A group of G lanes per (token, head).  Per codebook, the S split lists are
+// combined with cross-lane bitonic merges (lane r ends with the rank-r
+// entry).  The k*k candidates of memory.py:167-171 are then merged row by
+// row as lists keyed (select sum, flat index rank_a*k + rank_b): row i holds
+// k/(i+1) candidates that can still reach the top k, and the rows with a
+// single such candidate (i >= k/2) form one more sorted list.  The softmax
+// of memory.py:178 runs across the group.
+template <int G>
+__global__ __launch_bounds__(256) void pair_kernel(PairParams p) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane % G;
+  const int base = lane - r;
+  const int64_t mh = ((int64_t)blockIdx.x * 256 + threadIdx.x) / G;
+  const bool live = mh < p.M * p.H;  // dead groups still join the shuffles
+  const int64_t m = live ? mh / p.H : 0;
+  const int h = live ? (int)(mh % p.H) : 0;
   const int k = p.k;
   const int HC = 2 * p.H;
-  const float* psel = p.part_sel != nullptr ? p.part_sel : p.part_clean;
+  const float* lsel = p.sel != nullptr ? p.sel : p.clean;
 
-  // Stage-1 result per codebook: merge the split lists (each sorted by
-  // select desc, index asc; splits hold disjoint, increasing key ranges).
+  u64 lk[2];
+  float lc[2];
+#pragma unroll
   for (int c = 0; c < 2; ++c) {
     const int hc = 2 * h + c;
-    if (p.S == 1) {
-      const int64_t base = (m * HC + hc) * k;
-      for (int r = 0; r < k; ++r) {
-        sel_[c][r][t] = psel[base + r];
-        cl_[c][r][t] = p.part_clean[base + r];
-        id_[c][r][t] = p.part_idx[base + r];
-      }
-    } else {
-      int ptr[kMaxSplits];
-#pragma unroll
-      for (int s = 0; s < kMaxSplits; ++s) ptr[s] = 0;
-      for (int r = 0; r < k; ++r) {
-        float best = -INFINITY;
-        int bid = INT_MAX, bs = 0;
-#pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) {
-          if (s < p.S && ptr[s] < k) {
-            const int64_t o = ((s * p.M + m) * HC + hc) * k + ptr[s];
-            const float x = psel[o];
-            const int xi = p.part_idx[o];
-            if (x > best || (x == best && xi < bid)) {
-              best = x;
-              bid = xi;
-              bs = s;
-            }
-          }
-        }
-        int pb = 0;
-#pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) pb = (s == bs) ? ptr[s] : pb;
-        const int64_t o = ((bs * p.M + m) * HC + hc) * k + pb;
-        sel_[c][r][t] = best;
-        cl_[c][r][t] = p.part_clean[o];
-        id_[c][r][t] = bid;
-#pragma unroll
-        for (int s = 0; s < kMaxSplits; ++s) ptr[s] += (s == bs) ? 1 : 0;
-      }
-      const int64_t base = (m * HC + hc) * k;
-      for (int r = 0; r < k; ++r) {
-        p.sub_idx[base + r] = id_[c][r][t];
-        p.sub_scores[base + r] = cl_[c][r][t];
+    u64 acc = 0;
+    float pay = 0.f;
+    for (int s = 0; s < p.S; ++s) {
+      const bool ok = live && r < k;
+      const int64_t o = (((int64_t)s * p.M + m) * HC + hc) * k + (ok ? r : 0);  // clamped, unconditional
+      const int id0 = p.idx[o];
+      const float sl0 = lsel[o], cc0 = p.clean[o];
+      const int id = ok ? id0 : -1;
+      const u64 kk = id >= 0 ? make_key(sl0, id) : 0ull;
+      const float cc = ok ? cc0 : 0.f;
+      if (s == 0) {
+        acc = kk;
+        pay = cc;
+      } else {
+        group_merge<G>(acc, pay, kk, cc, r, base);
       }
     }
+    lk[c] = acc;
+    lc[c] = pay;
+    if (p.S > 1 && live && r < k) {
+      const int64_t so = (m * HC + hc) * k + r;
+      p.sub_idx[so] = acc ? key_index(acc) : -1;
+      p.sub_scores[so] = acc ? pay : -INFINITY;
+    }
+  }
+  const bool a_ok = lk[0] != 0ull, b_ok = lk[1] != 0ull;
+  const float a_sel = a_ok ? key_score(lk[0]) : -INFINITY;
+  const float b_sel = b_ok ? key_score(lk[1]) : -INFINITY;
+  const int a_id = a_ok ? key_index(lk[0]) : 0;
+  const int b_id = b_ok ? key_index(lk[1]) : 0;
+  const float a_cl = lc[0], b_cl = lc[1];
+
+  // row 0: (0, j) at lane j
+  const float a0 = __shfl(a_sel, base);
+  const float a0c = __shfl(a_cl, base);
+  const bool a0_ok = __shfl((int)a_ok, base) != 0;
+  u64 acc = (r < k && a0_ok && b_ok) ? make_key(a0 + b_sel, r) : 0ull;
+  float pay = a0c + b_cl;
+  // rows 1 .. k/2-1: (i, j) for j < k/(i+1)
+  for (int i = 1; i < k / 2; ++i) {
+    const float ai = __shfl(a_sel, base + i);
+    const float aic = __shfl(a_cl, base + i);
+    const bool ai_ok = __shfl((int)a_ok, base + i) != 0;
+    const u64 cand = (r < k / (i + 1) && ai_ok && b_ok) ? make_key(ai + b_sel, i * k + r) : 0ull;
+    group_merge<G>(acc, pay, cand, aic + b_cl, r, base);
+  }
+  // rows max(1, k/2) .. k-1: only (i, 0) can reach the top k
+  const int i0 = k / 2 > 1 ? k / 2 : 1;
+  if (i0 < k) {
+    const float b0 = __shfl(b_sel, base);
+    const float b0c = __shfl(b_cl, base);
+    const bool b0_ok = __shfl((int)b_ok, base) != 0;
+    const int src = base + min(i0 + r, G - 1);
+    const float ar = __shfl(a_sel, src);
+    const float arc = __shfl(a_cl, src);
+    const bool ar_ok = __shfl((int)a_ok, src) != 0;
+    const u64 cand = (r < k - i0 && ar_ok && b0_ok) ? make_key(ar + b0, (i0 + r) * k) : 0ull;
+    group_merge<G>(acc, pay, cand, arc + b0c, r, base);
   }
 
-  // Stage 2: frontier walk over rows i (rank in codebook a), ptr[i] = next
-  // rank in codebook b.
-  int ptr[KMAX];
-  float cv[KMAX];
-#pragma unroll
-  for (int i = 0; i < KMAX; ++i) {
-    ptr[i] = 0;
-    cv[i] = i < k ? sel_[0][i][t] + sel_[1][0][t] : -INFINITY;
+  // lane r < k holds the rank-r slot
+  const int flat = acc ? key_index(acc) : 0;
+  const int ra = min(flat / k, G - 1), rb = flat % k;
+  int ia = __shfl(a_id, base + ra);
+  int ib = __shfl(b_id, base + rb);
+  // ids come from keys < n; the clamp only guards non-finite inputs
+  ia = (ia >= 0 && ia < p.n) ? ia : 0;
+  ib = (ib >= 0 && ib < p.n) ? ib : 0;
+  const bool mine = r < k;
+  const float sc = mine ? pay : -INFINITY;
+  const float mx = group_max<G>(sc);
+  const float e = mine ? expf(sc - mx) : 0.f;
+  const float sum = group_sum<G>(e);
+  if (live && mine) {
+    const int64_t ob = mh * k + r;
+    p.slots[ob] = ia * p.n + ib;
+    p.flat_idx[ob] = flat;
+    p.weights[ob] = e / sum;
   }
-  float clean[KMAX];
-  const int64_t ob = mh * k;
-#pragma unroll
-  for (int s = 0; s < KMAX; ++s) {
-    if (s < k) {
-      float best = cv[0];
-      int bi = 0, bflat = ptr[0];
-#pragma unroll
-      for (int i = 1; i < KMAX; ++i) {
-        if (i <= s) {
-          const int flat = i * k + ptr[i];
-          const bool better = cv[i] > best || (cv[i] == best && flat < bflat);
-          best = better ? cv[i] : best;
-          bi = better ? i : bi;
-          bflat = better ? flat : bflat;
-        }
-      }
-      const int rb = min(bflat - bi * k, k - 1);
-      clean[s] = cl_[0][bi][t] + cl_[1][rb][t];
-      // ids come from keys < n; the clamp only guards non-finite inputs
-      // (NaN scores are never inserted) against out-of-range reads later.
-      int ia = id_[0][bi][t], ib = id_[1][rb][t];
-      ia = (ia >= 0 && ia < p.n) ? ia : 0;
-      ib = (ib >= 0 && ib < p.n) ? ib : 0;
-      p.slots[ob + s] = ia * p.n + ib;
-      p.flat_idx[ob + s] = bflat;
-      const float nv = rb + 1 < k ? sel_[0][bi][t] + sel_[1][rb + 1][t] : -INFINITY;
-#pragma unroll
-      for (int i = 0; i < KMAX; ++i) {
-        ptr[i] += (i == bi) ? 1 : 0;
-        cv[i] = (i == bi) ? nv : cv[i];
-      }
-    }
-  }
-  // Routing softmax over the clean slot scores (memory.py:178).
-  float mx = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < KMAX; ++s)
-    if (s < k) mx = fmaxf(mx, clean[s]);
-  float sum = 0.f;
-#pragma unroll
-  for (int s = 0; s < KMAX; ++s) {
-    if (s < k) {
-      clean[s] = expf(clean[s] - mx);
-      sum += clean[s];
-    }
-  }
-#pragma unroll
-  for (int s = 0; s < KMAX; ++s)
-    if (s < k) p.weights[ob + s] = clean[s] / sum;
 }
 
 // ---------------------------------------------------------------- host side
@@ -442,6 +518,13 @@ static Plan make_plan(int64_t M, int H, int n, int k) {
   pl.splits = (int)cdiv(pl.nblk, pl.blk_per_split);
   pl.kmax = k <= 16 ? 16 : 32;
   return pl;
+}
+
+// Workspace: the select scores with noise; per-split lists when split.
+static size_t ws_bytes(const Plan& pl, int64_t M, int H, int k, bool noise) {
+  const size_t per = (size_t)M * 2 * H * k;
+  if (pl.splits == 1) return noise ? per * 4 : 0;
+  return per * pl.splits * (noise ? 3 : 2) * 4;
 }
 
 template <typename T, int HP, bool NOISE, int KMAX>
@@ -484,12 +567,6 @@ static int dispatch_stage1(const ScoreParams& sp, int64_t blocks, int score_dtyp
   return MPL_OK;
 }
 
-static size_t ws_bytes(const Plan& pl, int64_t M, int H, int k, bool noise) {
-  const size_t per = (size_t)M * 2 * H * k;
-  if (pl.splits == 1) return noise ? per * sizeof(float) : 0;
-  return per * pl.splits * (2 * sizeof(float) + sizeof(int));
-}
-
 }  // namespace mpl
 
 using namespace mpl;
@@ -501,7 +578,7 @@ extern "C" size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int 
   return ws_bytes(pl, M, H, k, true);
 }
 
-extern "C" int mpl_score_select(const float* q_hat, const float* q_len, const void* packed_keys,
+extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const void* packed_keys,
                                 int64_t M, int H, int n, int half, int k, int score_dtype,
                                 float temperature, const float* gumbel, float noise_coef,
                                 void* workspace, size_t workspace_bytes, int32_t* sub_idx,
@@ -543,15 +620,16 @@ extern "C" int mpl_score_select(const float* q_hat, const float* q_len, const vo
   sp.nblk = pl.nblk;
   sp.splits = pl.splits;
   sp.blk_per_split = pl.blk_per_split;
+  float* w = (float*)workspace;
+  const size_t part = per * pl.splits;
   if (pl.splits == 1) {
-    sp.out_sel = noise ? (float*)workspace : nullptr;
     sp.out_clean = sub_scores;
     sp.out_idx = sub_idx;
+    sp.out_sel = noise ? w : nullptr;
   } else {
-    float* w = (float*)workspace;
-    sp.out_sel = w;
-    sp.out_clean = w + per * pl.splits;
-    sp.out_idx = (int*)(w + 2 * per * pl.splits);
+    sp.out_clean = w;
+    sp.out_idx = (int*)(w + part);
+    sp.out_sel = noise ? w + 2 * part : nullptr;
   }
   const int HP = score_dtype == MPL_F16 ? KeyPack<_Float16>::padded_half(half) : KeyPack<float>::padded_half(half);
   const int64_t blocks = pl.qblocks * pl.splits * HC;
@@ -563,22 +641,23 @@ extern "C" int mpl_score_select(const float* q_hat, const float* q_len, const vo
   rc = check_launch("mpl_score_select(stage 1)");
   if (rc) return rc;
 
-  Stage2Params p2;
-  p2.part_sel = sp.out_sel;
-  p2.part_clean = sp.out_clean;
-  p2.part_idx = sp.out_idx;
-  p2.M = M;
-  p2.H = H;
-  p2.n = n;
-  p2.k = k;
-  p2.S = pl.splits;
-  p2.sub_idx = sub_idx;
-  p2.sub_scores = sub_scores;
-  p2.flat_idx = flat_idx;
-  p2.slots = slots;
-  p2.weights = weights;
-  const unsigned g2 = (unsigned)cdiv(M * H, kStage2Threads);
-  if (pl.kmax == 16) stage2_kernel<16><<<g2, kStage2Threads, 0, s>>>(p2);
-  else stage2_kernel<32><<<g2, kStage2Threads, 0, s>>>(p2);
+  PairParams pp;
+  pp.sel = sp.out_sel;
+  pp.clean = sp.out_clean;
+  pp.idx = sp.out_idx;
+  pp.M = M;
+  pp.H = H;
+  pp.n = n;
+  pp.k = k;
+  pp.S = pl.splits;
+  pp.sub_idx = sub_idx;
+  pp.sub_scores = sub_scores;
+  pp.flat_idx = flat_idx;
+  pp.slots = slots;
+  pp.weights = weights;
+  const int G = k <= 16 ? 16 : 32;
+  const unsigned g2 = (unsigned)cdiv(M * H * G, 256);
+  if (G == 16) pair_kernel<16><<<g2, 256, 0, s>>>(pp);
+  else pair_kernel<32><<<g2, 256, 0, s>>>(pp);
   return check_launch("mpl_score_select(stage 2)");
 }

@@ -1,0 +1,170 @@
+// Exact top-k building blocks on 64-bit keys.
+//
+// A candidate (score, index) is packed as
+//     key = (orderable(score) << 32) | (0xFFFFFFFF - index)
+// so that unsigned key order is (score descending, index ascending): the
+// order of lax.top_k, ties going to the lowest index.  Key 0 is below every
+// real candidate and marks an empty slot.
+//
+// TopList<KMAX> keeps the best KMAX keys sorted descending in registers.
+// Candidates are merged in chunks of 8: an optimal 19-comparator network
+// sorts the chunk, the bitonic split R[i] = max(A[i], B[KMAX-1-i]) keeps the
+// KMAX best of both, and a bitonic merger re-sorts them (4 or 5 stages).
+// An optional float payload travels with each key.
+#pragma once
+
+#include "common.h"
+
+namespace mpl {
+
+typedef unsigned long long u64;
+
+__device__ __forceinline__ uint32_t orderable(float f) {
+  const uint32_t b = __float_as_uint(f + 0.0f);  // -0 -> +0
+  return b ^ ((b & 0x80000000u) ? 0xFFFFFFFFu : 0x80000000u);
+}
+
+__device__ __forceinline__ float from_orderable(uint32_t u) {
+  const uint32_t b = (u & 0x80000000u) ? (u ^ 0x80000000u) : ~u;
+  return __uint_as_float(b);
+}
+
+__device__ __forceinline__ u64 make_key(float s, int idx) {
+  return ((u64)orderable(s) << 32) | (u64)(0xFFFFFFFFu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ float key_score(u64 k) { return from_orderable((uint32_t)(k >> 32)); }
+__device__ __forceinline__ int key_index(u64 k) { return (int)(0xFFFFFFFFu - (uint32_t)k); }
+
+// Compare-exchange, larger key to `a`.
+template <bool PAY>
+__device__ __forceinline__ void cex(u64& a, u64& b, float& pa, float& pb) {
+  const bool sw = a < b;
+  const u64 t = sw ? b : a;
+  b = sw ? a : b;
+  a = t;
+  if (PAY) {
+    const float q = sw ? pb : pa;
+    pb = sw ? pa : pb;
+    pa = q;
+  }
+}
+
+// Sorts 8 keys descending (optimal 19-comparator network).
+template <bool PAY>
+__device__ __forceinline__ void sort8(u64* c, float* p) {
+#define MPL_CE(i, j) cex<PAY>(c[i], c[j], p[PAY ? i : 0], p[PAY ? j : 0])
+  MPL_CE(0, 2); MPL_CE(1, 3); MPL_CE(4, 6); MPL_CE(5, 7);
+  MPL_CE(0, 4); MPL_CE(1, 5); MPL_CE(2, 6); MPL_CE(3, 7);
+  MPL_CE(0, 1); MPL_CE(2, 3); MPL_CE(4, 5); MPL_CE(6, 7);
+  MPL_CE(2, 4); MPL_CE(3, 5);
+  MPL_CE(1, 4); MPL_CE(3, 6);
+  MPL_CE(1, 2); MPL_CE(3, 4); MPL_CE(5, 6);
+#undef MPL_CE
+}
+
+template <int KMAX, bool PAY>
+struct TopList {
+  u64 key[KMAX];
+  float pay[PAY ? KMAX : 1];
+
+  __device__ __forceinline__ void init() {
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) key[j] = 0;
+#pragma unroll
+    for (int j = 0; j < (PAY ? KMAX : 1); ++j) pay[j] = 0.f;
+  }
+
+  // Merge a sorted (descending) run of CN <= KMAX keys.
+  template <int CN>
+  __device__ __forceinline__ void merge(const u64* c, const float* cp) {
+#pragma unroll
+    for (int i = KMAX - CN; i < KMAX; ++i) {
+      const u64 b = c[KMAX - 1 - i];
+      const bool take = b > key[i];
+      key[i] = take ? b : key[i];
+      if (PAY) pay[PAY ? i : 0] = take ? cp[PAY ? KMAX - 1 - i : 0] : pay[PAY ? i : 0];
+    }
+    // Affine stage counter: every index below is a compile-time constant,
+    // so the list stays in registers.
+    constexpr int kStages = KMAX == 32 ? 5 : 4;
+#pragma unroll
+    for (int st = 0; st < kStages; ++st) {
+      const int s = (KMAX / 2) >> st;
+#pragma unroll
+      for (int i = 0; i < KMAX; ++i) {
+        if ((i & s) == 0) cex<PAY>(key[i], key[i + s], pay[PAY ? i : 0], pay[PAY ? i + s : 0]);
+      }
+    }
+  }
+
+  // Key at runtime position r (< KMAX).  Written as and/or of masked
+  // entries: a select chain on r would be folded into a dynamically indexed
+  // load, which forces the whole list out of registers into scratch.
+  __device__ __forceinline__ u64 at(int r) const {
+    u64 t = 0;
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) t |= key[j] & (0ull - (u64)(j == r));
+    return t;
+  }
+};
+
+}  // namespace mpl
+
+namespace mpl {
+
+// ------------------------------------------------------- cross-lane lists
+// A group of G lanes (16 or 32, aligned within the wave) holds one sorted
+// list: the lane of rank r (= lane % G) holds the r-th best key.
+
+__device__ __forceinline__ u64 shfl_u64(u64 v, int src) {
+  const uint32_t lo = __shfl((uint32_t)v, src);
+  const uint32_t hi = __shfl((uint32_t)(v >> 32), src);
+  return ((u64)hi << 32) | lo;
+}
+
+template <int G>
+__device__ __forceinline__ u64 shfl_xor_u64(u64 v, int mask) {
+  const uint32_t lo = __shfl_xor((uint32_t)v, mask, G);
+  const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), mask, G);
+  return ((u64)hi << 32) | lo;
+}
+
+// acc <- best G of (acc, b), both sorted descending across the group; the
+// float payload follows its key.  Bitonic split + G-wide bitonic merger.
+template <int G>
+__device__ __forceinline__ void group_merge(u64& acc, float& pay, u64 b, float bp, int r, int base) {
+  const int src = base + (G - 1 - r);
+  const u64 br = shfl_u64(b, src);
+  const float bpr = __shfl(bp, src);
+  const bool take = br > acc;
+  acc = take ? br : acc;
+  pay = take ? bpr : pay;
+  constexpr int kStages = G == 32 ? 5 : 4;
+#pragma unroll
+  for (int st = 0; st < kStages; ++st) {
+    const int s = (G / 2) >> st;
+    const u64 o = shfl_xor_u64<G>(acc, s);
+    const float op = __shfl_xor(pay, s, G);
+    const bool lower = (r & s) == 0;
+    const bool other = lower ? (o > acc) : (o < acc);
+    acc = other ? o : acc;
+    pay = other ? op : pay;
+  }
+}
+
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int s = G / 2; s >= 1; s >>= 1) v = fmaxf(v, __shfl_xor(v, s, G));
+  return v;
+}
+
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int s = G / 2; s >= 1; s >>= 1) v += __shfl_xor(v, s, G);
+  return v;
+}
+
+}  // namespace mpl

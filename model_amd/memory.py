@@ -122,6 +122,7 @@ class MemoryPool:
         self._keys = _KeyCache()
         self._temp_key = None
         self._temp_val = None
+        self._temp_tensor = None
 
     @property
     def pool_size(self) -> int:
@@ -151,6 +152,7 @@ class MemoryPool:
             hi = math.log(self.max_temperature)
             lt32 = torch.tensor(lt, dtype=torch.float32).clamp(lo, hi)
             self._temp_val = float(torch.exp(lt32))
+            self._temp_tensor = torch.tensor(self._temp_val, dtype=torch.float32, device=log_temperature.device)
             self._temp_key = key
         return self._temp_val
 
@@ -185,11 +187,14 @@ class MemoryPool:
         stream = _lib.stream_ptr(dev)
         q = queries.detach().reshape(-1, H, 2, half).float().contiguous()
         M = q.shape[0]
-        q_hat = torch.empty_like(q)
-        q_len = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if self.query_scale else None
-        check(L.mpl_l2_normalize(ptr(q), M * H * 2, half, NORM_EPS, ptr(q_hat), ptr(q_len), stream),
-              "mpl_l2_normalize")
         score_code = _dtype_code(self.score_dtype)
+        q_hat = torch.empty_like(q)
+        # the scoring operand: q_hat itself for fp32 scoring, its fp16 rounding otherwise
+        q_score = torch.empty_like(q, dtype=torch.float16) if score_code == _lib.MPL_F16 else q_hat
+        q_len = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if self.query_scale else None
+        check(L.mpl_l2_normalize(ptr(q), M * H * 2, half, NORM_EPS, ptr(q_hat),
+                                 ptr(q_score) if q_score is not q_hat else None, ptr(q_len), stream),
+              "mpl_l2_normalize")
         k_hat, packed = self._keys.get(params["sub_keys"], score_code)
         T = self.temperature(params["log_temperature"])
 
@@ -214,7 +219,7 @@ class MemoryPool:
         flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_select(ptr(q_hat), ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
+        check(L.mpl_score_select(ptr(q_score), ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
                                  T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
                                  ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
               "mpl_score_select")
@@ -230,14 +235,14 @@ class MemoryPool:
         noisy = gumbel is not None
 
         def stats():
-            return self._routing_stats(params, q_hat, k_hat, T, q_len, sub_idx, slots, weights,
+            return self._routing_stats(params, q_hat, q_score, k_hat, T, q_len, sub_idx, slots, weights,
                                        noisy, packed, score_code, M)
 
         aux = LazyAux({
             "queries": q_hat,
             "slots": slots.reshape(*lead, H, k),
             "weights": weights.reshape(*lead, H, k),
-            "temperature": torch.tensor(T, dtype=torch.float32, device=dev),
+            "temperature": self._temp_tensor,
         }, stats)
         return {
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_hat": q_hat, "q_len": q_len,
@@ -247,7 +252,7 @@ class MemoryPool:
         }
 
     # ------------------------------------------------------------- stats
-    def _routing_stats(self, params, q_hat, k_hat, T, q_len, sub_idx, slots, weights, noisy,
+    def _routing_stats(self, params, q_hat, q_score, k_hat, T, q_len, sub_idx, slots, weights, noisy,
                        packed, score_code, M):
         """memory.py:196-215 from the selected ids."""
         H, n, k = self.heads, self.n_sub_keys, self.top_k
@@ -262,7 +267,7 @@ class MemoryPool:
         sl = slots.long()
         subkey_counts = count_subkeys(torch.stack([sl // n, sl % n], dim=2))
         if noisy:  # memory.py:207: an extra clean selection
-            clean = self._clean_sub_idx(q_hat, q_len, packed, score_code, T, M)
+            clean = self._clean_sub_idx(q_score, q_len, packed, score_code, T, M)
         else:
             clean = sub_idx
         f = count_subkeys(clean) / (M * k)
@@ -281,9 +286,9 @@ class MemoryPool:
             "top1_weight": weights.max(-1).values.mean(),
         }
 
-    def _clean_sub_idx(self, q_hat, q_len, packed, score_code, T, M):
+    def _clean_sub_idx(self, q_score, q_len, packed, score_code, T, M):
         H, n, k, half = self.heads, self.n_sub_keys, self.top_k, self.d_key // 2
-        dev = q_hat.device
+        dev = q_score.device
         L = _lib.lib()
         ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -292,7 +297,7 @@ class MemoryPool:
         flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_select(ptr(q_hat), ptr(q_len), ptr(packed), M, H, n, half, k, score_code, T,
+        check(L.mpl_score_select(ptr(q_score), ptr(q_len), ptr(packed), M, H, n, half, k, score_code, T,
                                  None, 0.0, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores),
                                  ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
               "mpl_score_select(clean)")
