@@ -45,7 +45,37 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-large", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
+                         "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
     return ap.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_text_study_8192.json")
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` on the 8,192-token workload, from the
+    rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (already
+    scaled by the copy-kernel calibration); None when not recorded."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    k = rec.get("kernels", {}).get(kernel)
+    return None if k is None else k.get("hbm_bytes_per_launch")
+
+
+def copy_calibration(torch):
+    n = 512 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for _ in range(10):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 10}))
 
 
 class Lookup:
@@ -164,9 +194,11 @@ def roofline_for(lk, br):
     s = score_flops / (br["score_select_ms"] * 1e-3) / 1e12
     if br["gather_wsum_ms"] >= br["score_select_ms"]:
         return {"kernel": "gather_wsum", "bound": "hbm", "achieved": g, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": g / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes": gather_bytes}
+                "frac": g / HBM_PEAK_GBS, "traffic": measured_traffic("gather_wsum"),
+                "algorithmic_bytes": gather_bytes}
     return {"kernel": "score_select", "bound": "mfma", "achieved": s, "peak": MFMA_F16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": s / MFMA_F16_PEAK_TFLOPS, "traffic": None, "algorithmic_flops": score_flops}
+            "unit": "TFLOP/s", "frac": s / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("score_select"),
+            "algorithmic_flops": score_flops}
 
 
 def gather_roofline(lk, br):
@@ -219,6 +251,9 @@ def main():
 
     L = _lib.lib()
     torch.cuda.set_device(0)
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
 
     # ---- headline: 262,144 slots, 8,192 tokens
     lk = Lookup(torch, L, M=8192, H=4, n=512, d_key=256, d=256, k=16, seed=0)

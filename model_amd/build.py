@@ -21,10 +21,14 @@ OBJ = os.path.join(ROOT, "_build", "obj")
 LIB = os.path.join(HERE, "libmpl.so")
 ARCH = "gfx950"
 
-# Packed fp32 VALU ops are disabled for every device compile.
+# Packed fp32 VALU ops are disabled for every device compile.  MFMA results
+# go to ordinary VGPRs (gfx950's unified register file): the selection code
+# reads every score with VALU ops, and accumulators in AGPRs would need a copy
+# per element that the scheduler hoists next to the MFMAs, stalling on them.
 FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-function", "-Wno-unused-variable",
 ]
 

@@ -5,15 +5,21 @@
 // Stage 1 (score_topk_kernel).  A workgroup owns 128 queries (two waves of
 // 64) of one codebook hc = h*2 + c and one split of the n sub-keys.  Key
 // blocks of 32 stream through LDS (double buffered); each wave computes a
-// 32-key x 64-query score tile with two 32x32 MFMA chains, then swaps register
-// halves across lanes (v_permlane32_swap) so that lane l owns query l with
-// all 32 scores of the block.  Each lane keeps its query's best k as sorted
-// 64-bit keys (topk.h) in registers and a threshold (the k-th best score).
-// Scores above the threshold go to a per-lane LDS candidate buffer; when any
-// lane's buffer is nearly full the wave sorts the buffered candidates in
-// chunks of 8 and bitonic-merges them into the lists.  Keys of equal score
-// order by index, so the result is exactly lax.top_k's.  The scores never
-// leave registers/LDS.
+// 32-key x 64-query score tile with two 32x32 MFMA chains.  Two passes:
+//   1. a bound pass over the first blocks of the split keeps, per register
+//      position, the running maximum; the k-th largest of a query's 32
+//      maxima is a score that at least k distinct keys reach, so it bounds
+//      the k-th best from below;
+//   2. a select pass over the whole split swaps register halves across lanes
+//      (v_permlane32_swap) so that lane l owns query l with all 32 scores of
+//      the block, appends scores above the lane's threshold to its column of
+//      an LDS buffer, and, when any lane's buffer fills, sorts the buffered
+//      candidates in chunks of 8 and bitonic-merges them into the lane's
+//      register list of the best k (topk.h), raising the threshold to the
+//      k-th best so far.
+// Keys of equal score order by index, so the result is exactly lax.top_k's.
+// The MFMAs of block j+1 are issued before the selection work of block j, so
+// the matrix cores and the VALU overlap.  Scores never leave registers/LDS.
 //
 // Without routing noise the selection runs on the raw cosine: scores are
 // cos*T(*q_len) with positive per-query factors, so the order is the same up
@@ -21,15 +27,16 @@
 //
 // Split plans.  Few tokens cannot fill the GPU with one workgroup per 128
 // queries, so the key range of each codebook is split across workgroups and
-// the per-split lists are merged (merge_*_kernel): per thread from registers
-// for up to 4 splits, per wave for more (decode-sized batches).
+// the per-split lists are merged in stage 2.
 //
-// Stage 2 (stage2_kernel).  One thread per (token, head) walks the k*k
-// candidate grid in frontier order (row pointers; at step s only rows <= s
-// can hold the next best), selecting by (select sum desc, flat index
-// rank_a*k + rank_b asc) as memory.py:171, and finishes with the softmax of
-// the clean slot scores (memory.py:178).
+// Stage 2 (pair_kernel).  A group of 16 (k <= 16) or 32 lanes per (token,
+// head) merges the split lists of both codebooks with cross-lane bitonic
+// merges, walks the k*k candidate grid as sorted row lists keyed by (select
+// sum desc, flat index rank_a*k + rank_b asc) as memory.py:171, and finishes
+// with the softmax of the clean slot scores (memory.py:178).
 #include <limits.h>
+
+#include <algorithm>
 #include <math.h>
 
 #include "common.h"
@@ -39,7 +46,7 @@
 namespace mpl {
 
 constexpr int kCand = 24;           // per-lane candidate buffer (entries)
-constexpr int kScoreThreads = 128;  // two waves per workgroup
+constexpr int kScoreThreads = 128;  // two waves per workgroup, 64 queries each
 constexpr int kMaxSplits = 64;
 
 struct ScoreParams {
@@ -50,6 +57,7 @@ struct ScoreParams {
   float T, noise_coef;
   int64_t M;
   int HC, n, half, k, nblk, splits, blk_per_split;
+  int pass1_blocks;  // blocks of each split scanned by the bound pass
   float* out_sel;    // [splits, HC, k, M] (null without noise: equals clean)
   float* out_clean;  // [splits, HC, k, M]
   int* out_idx;      // [splits, HC, k, M]
@@ -65,20 +73,14 @@ struct Mfma<_Float16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
   // B operand for chunk c: dims 16c + 8*(lane/32) + [0,8) of fp16 query row
-  // q: one 16-byte load (rows of a multiple of 8 dims) or clamped element
-  // loads.  Loads are unconditional and zeroed after: a guarded load compiles
-  // to a branch with its own wait, serialising every element.
+  // q (fp16 scoring requires half % 8 == 0, so this is one aligned 16-byte
+  // load).  Unconditional and zeroed after: a guarded load compiles to a
+  // branch with its own wait, serialising every chunk.
   __device__ static Op load_q(const _Float16* q, bool valid, int half, int c, int lane) {
-    Op o;
     const int d0 = 16 * c + 8 * (lane >> 5);
-    if ((half & 7) == 0) {
-      o = *(const half8*)(q + (d0 < half ? d0 : 0));
-    } else {
+    Op o = *(const half8*)(q + (d0 < half ? d0 : 0));
 #pragma unroll
-      for (int i = 0; i < 8; ++i) o[i] = q[min(d0 + i, half - 1)];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (valid && d0 + i < half) ? o[i] : (_Float16)0.f;
+    for (int i = 0; i < 8; ++i) o[i] = (valid && d0 < half) ? o[i] : (_Float16)0.f;
     return o;
   }
   __device__ static Op from_vec(uint4 u, int) { return __builtin_bit_cast(half8, u); }
@@ -101,37 +103,43 @@ struct Mfma<float> {
   }
 };
 
-// Per-lane selection state of the stage-1 kernel.
+// Per-lane selection state of the stage-1 kernel.  Candidates are appended
+// to the lane's column of an LDS buffer as (score bits, index) pairs; `wp`
+// points at the next free entry (entries of one lane are kWave apart).
 template <int KMAX, bool NOISE>
 struct LaneSel {
   TopList<KMAX, NOISE> top;
   float thr;
-  int cnt;
+  uint2* wp;
 };
 
-// Merges the lane's buffered candidates (cbuf/cpay column `lane`) into its
-// list and refreshes the threshold.  Wave-uniform control flow.
+// Merges the lane's buffered candidates (column `lane` of buf/pay) into its
+// list, empties the buffer and refreshes the threshold.  Wave-uniform
+// control flow.
 template <int KMAX, bool NOISE>
-__device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const u64 (*cbuf)[kWave],
-                                           const float (*cpay)[kWave], int lane, bool valid, int k,
+__device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, uint2 (*buf)[kWave],
+                                           const float (*pay)[kWave], int lane, bool valid, int k,
                                            float base_thr) {
+  uint2* const start = &buf[0][lane];
+  const int cnt = (int)(st.wp - start) / kWave;
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
 #pragma unroll 1
   for (int c0 = 0; c0 < kCand; c0 += 8) {
-    if (__ballot(c0 < st.cnt) == 0) break;
+    if (__ballot(c0 < cnt) == 0) break;
     u64 ch[8];
     float cp[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const bool in = c0 + i < st.cnt;
-      ch[i] = in ? cbuf[c0 + i][lane] : 0ull;
-      cp[i] = (NOISE && in) ? cpay[NOISE ? c0 + i : 0][lane] : 0.f;
+      const bool in = c0 + i < cnt;
+      const uint2 e = buf[c0 + i][lane];
+      ch[i] = in ? make_key(__uint_as_float(e.x), (int)e.y) : 0ull;
+      cp[i] = (NOISE && in) ? pay[NOISE ? c0 + i : 0][lane] : 0.f;
     }
     sort8<NOISE>(ch, cp);
     st.top.template merge<8>(ch, cp);
   }
-  st.cnt = 0;
+  st.wp = start;
   if (valid) {
     const u64 kk = st.top.at(k - 1);
     st.thr = kk ? key_score(kk) : base_thr;
@@ -180,7 +188,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   typedef typename Mfma<T>::Op Op;
 
   __shared__ uint4 tiles[2][TILE_ALLOC];
-  __shared__ u64 cbuf[2][kCand][kWave];
+  __shared__ uint2 cbuf[2][kCand][kWave];
   __shared__ float cpay[NOISE ? 2 : 1][NOISE ? kCand : 1][kWave];
 
   const int tid = threadIdx.x;
@@ -209,17 +217,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   const bool valid = my_q < p.M;
   const float ql = p.q_len != nullptr ? p.q_len[(valid ? my_q : 0) * p.HC + hc] : 1.f;
   const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
-  const u64(*mybuf)[kWave] = cbuf[wave];
+  uint2(*mybuf)[kWave] = cbuf[wave];
   const float(*mypay)[kWave] = cpay[NOISE ? wave : 0];
 
-  // Key blocks are software-pipelined one block ahead: `pre` holds block b+1
-  // during block b's compute, is stored to the free LDS buffer after it, and
-  // is immediately refilled with block b+2.  The loads are loop-carried, so
-  // the compiler cannot sink them next to their stores.  No load or store is
-  // guarded (clamped sources, padded tiles): a guard would serialise them.
-  // (A vector type, not an array: a loop-carried array is not promoted to
-  // registers.)
+  // Key blocks stream through two LDS buffers; `pre` holds the block after
+  // next in registers between its global load and its LDS store.  The loads
+  // are loop-carried, so the compiler cannot sink them next to their stores,
+  // and none is guarded (clamped sources, padded tiles): a guard would
+  // serialise them.  (A vector type, not an array: a loop-carried array is
+  // not promoted to registers.)
   typedef unsigned PreVec __attribute__((ext_vector_type(4 * PRE)));
+  typedef float GVec __attribute__((ext_vector_type(NOISE ? 32 : 1)));
   const uint4* kbase_ptr = p.packed + (int64_t)hc * p.nblk * TILE;
   auto fetch = [&](int blk) __attribute__((always_inline)) {
     PreVec v;
@@ -239,113 +247,172 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     for (int i = 0; i < PRE; ++i)
       tiles[buf][tid + i * kScoreThreads] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   };
-
-  // One sweep over this split's key blocks.  body(kb, sa, sb, ca, cb) gets
-  // the 32 selection values of the lane's query (sa[r]: key kb + 8*(r/4) +
-  // r%4, sb[r]: key kb + 8*(r/4) + 4 + r%4; padded keys are -inf) and, with
-  // noise, the clean scores ca/cb.
-  auto sweep = [&](auto&& body) __attribute__((always_inline)) {
-    PreVec pre = fetch(b_begin < b_end ? b_begin : 0);
+  auto fetch_noise = [&](int blk) __attribute__((always_inline)) {
+    GVec g;
+    if (NOISE) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) g[NOISE ? i : 0] = grow[min(blk * 32 + i, p.n - 1)];
+    }
+    return g;
+  };
+  // Both 32x32 score tiles of one key block: c0[r] = query q0 + lane%32,
+  // c1[r] = query q0 + 32 + lane%32, both against key 8*(r/4) + 4*(lane/32)
+  // + r%4 of the block.
+  auto mma_block = [&](int buf, f32x16& c0, f32x16& c1) __attribute__((always_inline)) {
+    c0 = f32x16{};
+    c1 = f32x16{};
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const uint4 u = tiles[buf][v * kWave + lane];
+#pragma unroll
+      for (int e = 0; e < OPV; ++e) {
+        const Op a = Mfma<T>::from_vec(u, e);
+        c0 = Mfma<T>::mma(a, qop[0][v * OPV + e], c0);
+        c1 = Mfma<T>::mma(a, qop[1][v * OPV + e], c1);
+      }
+    }
+  };
+  // One sweep over key blocks [bb, be), software-pipelined: while the VALU
+  // runs body() on block j, the MFMAs of block j+1 are already in flight.
+  // body(kb, c0, c1, g) gets the raw cosine tiles of the block starting at key
+  // kb and, with noise, the lane's noise for those 32 keys.
+  // LDS order per iteration j: reads of block j+1, then the store of block j+2
+  // into block j's buffer, then one barrier.  Block j was read in iteration
+  // j-1, before that iteration's barrier; block j+2 is read in iteration j+1,
+  // after this one's.
+  auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
+    const int nb = be - bb;
+    if (nb <= 0) return;
+    PreVec pre = fetch(bb);
     stage(0, pre);
-    pre = fetch(b_begin < b_end ? min(b_begin + 1, b_end - 1) : 0);
+    pre = fetch(min(bb + 1, be - 1));
+    stage(1, pre);
+    pre = fetch(min(bb + 2, be - 1));
+    GVec gcur = fetch_noise(bb);
     __syncthreads();
-    for (int b = b_begin; b < b_end; ++b) {
-      const int cur = (b - b_begin) & 1;
-      float gblk[NOISE ? 32 : 1];  // this block's routing noise, fetched before the MFMAs
-      if (NOISE) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) gblk[NOISE ? i : 0] = grow[min(b * 32 + i, p.n - 1)];
-      }
-      f32x16 acc0 = {}, acc1 = {};
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const uint4 u = tiles[cur][v * kWave + lane];
-#pragma unroll
-        for (int e = 0; e < OPV; ++e) {
-          const Op a = Mfma<T>::from_vec(u, e);
-          acc0 = Mfma<T>::mma(a, qop[0][v * OPV + e], acc0);
-          acc1 = Mfma<T>::mma(a, qop[1][v * OPV + e], acc1);
-        }
-      }
-      // acc0[r]: query q0 + lane%32, key 8*(r/4) + 4*(lane/32) + r%4 (acc1: query + 32).
-      float sa[16], sb[16], ca[NOISE ? 16 : 1], cb[NOISE ? 16 : 1];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sa[r] = acc0[r];
-        sb[r] = acc1[r];
-        half_swap(sa[r], sb[r]);
-      }
-      const int kb = b * 32;
-      if (NOISE) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int o = 8 * (r >> 2) + (r & 3);
-          float c0 = sa[r] * p.T, c1 = sb[r] * p.T;
-          if (p.q_len != nullptr) {
-            c0 *= ql;
-            c1 *= ql;
-          }
-          ca[NOISE ? r : 0] = c0;
-          cb[NOISE ? r : 0] = c1;
-          sa[r] = c0 + p.noise_coef * gblk[NOISE ? o : 0];
-          sb[r] = c1 + p.noise_coef * gblk[NOISE ? o + 4 : 0];
-        }
-      }
-      if (kb + 32 > p.n) {  // wave-uniform: only the last block can hold padded keys
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int o = kb + 8 * (r >> 2) + (r & 3);
-          if (o >= p.n) sa[r] = -INFINITY;
-          if (o + 4 >= p.n) sb[r] = -INFINITY;
-        }
-      }
-      body(kb, sa, sb, ca, cb);
-      // Buffer cur^1 was last read before the previous barrier; past the last
-      // block the copies are clamped duplicates that are never read.
-      stage(cur ^ 1, pre);
-      pre = fetch(min(b + 2, b_end - 1));
+    f32x16 x0, x1, y0, y1;
+    mma_block(0, x0, x1);
+    // The MFMAs of the next block are issued unconditionally (past the end
+    // they score a clamped duplicate that nobody reads): a branch around them
+    // would make the accumulators a phi, which the compiler resolves by
+    // copying them right after the MFMAs, stalling on their results.
+    auto step = [&](int j, f32x16& c0, f32x16& c1, f32x16& d0, f32x16& d1) __attribute__((always_inline)) {
+      mma_block((j + 1) & 1, d0, d1);
+      const GVec gnext = fetch_noise(min(bb + j + 1, be - 1));
+      if (j < nb) body((bb + j) * 32, c0, c1, gcur);
+      gcur = gnext;
+      stage(j & 1, pre);  // past the end: clamped duplicates, never read
+      pre = fetch(min(bb + j + 3, be - 1));
       __syncthreads();
+    };
+    for (int j = 0; j < nb; j += 2) {
+      step(j, x0, x1, y0, y1);
+      step(j + 1, y0, y1, x0, x1);
     }
   };
 
-  // Pass 1: running maximum per key position (32 per lane, one v_max per
-  // score).  Each maximum is a distinct key's score, so the k-th largest of
-  // them is a lower bound on the lane's k-th best score (typically ~22 keys
-  // of any split clear it).
+  // Lane-owned selection values of a block: after the half swap sa[r] is key
+  // kb + 8*(r/4) + r%4 and sb[r] key kb + 8*(r/4) + 4 + r%4 of query q0 + lane
+  // (padded keys -inf); with noise, ca/cb are the clean scores.
+  auto lane_scores = [&](int kb, const f32x16& c0, const f32x16& c1, const GVec& g, float* sa, float* sb,
+                         float* ca, float* cb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      sa[r] = c0[r];
+      sb[r] = c1[r];
+      half_swap(sa[r], sb[r]);
+    }
+    if (NOISE) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = 8 * (r >> 2) + (r & 3);
+        float v0 = sa[r] * p.T, v1 = sb[r] * p.T;
+        if (p.q_len != nullptr) {
+          v0 *= ql;
+          v1 *= ql;
+        }
+        ca[NOISE ? r : 0] = v0;
+        cb[NOISE ? r : 0] = v1;
+        sa[r] = __builtin_fmaf(p.noise_coef, g[NOISE ? o : 0], v0);
+        sb[r] = __builtin_fmaf(p.noise_coef, g[NOISE ? o + 4 : 0], v1);
+      }
+    }
+    if (kb + 32 > p.n) {  // wave-uniform: only the last block can hold padded keys
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int o = kb + 8 * (r >> 2) + (r & 3);
+        if (o >= p.n) sa[r] = -INFINITY;
+        if (o + 4 >= p.n) sb[r] = -INFINITY;
+      }
+    }
+  };
+
+  // Pass 1 over the first pass1_blocks blocks of the split: running maximum
+  // per (lane, register) position.  Each maximum is a distinct key's score,
+  // so the k-th largest of a lane's 32 maxima (after the half swap) is a
+  // lower bound on its query's k-th best score.  Without noise the maxima are
+  // taken on the raw tiles and swapped once at the end.
   float ma[16], mb[16];
 #pragma unroll
   for (int r = 0; r < 16; ++r) ma[r] = mb[r] = -INFINITY;
-  sweep([&](int, const float* sa, const float* sb, const float*, const float*) __attribute__((always_inline)) {
+  const int p1_end = min(b_end, b_begin + p.pass1_blocks);
+  sweep(b_begin, p1_end, [&](int kb, const f32x16& c0, const f32x16& c1, const GVec& g)
+                             __attribute__((always_inline)) {
+    if (NOISE || kb + 32 > p.n) {
+      float sa[16], sb[16], ca[NOISE ? 16 : 1], cb[NOISE ? 16 : 1];
+      lane_scores(kb, c0, c1, g, sa, sb, ca, cb);
+      if (!NOISE) {  // back to the raw layout (the swap is an involution)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      ma[r] = fmaxf(ma[r], sa[r]);
-      mb[r] = fmaxf(mb[r], sb[r]);
+        for (int r = 0; r < 16; ++r) half_swap(sa[r], sb[r]);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        ma[r] = fmaxf(ma[r], sa[r]);
+        mb[r] = fmaxf(mb[r], sb[r]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        ma[r] = fmaxf(ma[r], c0[r]);
+        mb[r] = fmaxf(mb[r], c1[r]);
+      }
     }
   });
+  if (!NOISE) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) half_swap(ma[r], mb[r]);
+  }
   // Scores >= bound pass: strict '>' against the next float below it.
   const float bound = kth_of_32(ma, mb, p.k);
   const float base_thr = bound == -INFINITY ? -INFINITY : from_orderable(orderable(bound) - 1u);
 
-  // Pass 2: the same scores again; only candidates above the threshold are
-  // buffered and merged into the sorted register list.
+  // Pass 2 over the whole split: only candidates above the threshold are
+  // buffered (a wave-uniform branch skips an element no lane keeps) and
+  // merged into the sorted register list.
   LaneSel<KMAX, NOISE> st;
   st.top.init();
   st.thr = valid ? base_thr : INFINITY;
-  st.cnt = 0;
-  sweep([&](int kb, const float* sa, const float* sb, const float* ca, const float* cb)
-            __attribute__((always_inline)) {
+  st.wp = &mybuf[0][lane];
+  uint2* const flush_at = &mybuf[kCand - 8][lane];
+  sweep(b_begin, b_end, [&](int kb, const f32x16& c0, const f32x16& c1, const GVec& g)
+                            __attribute__((always_inline)) {
+    float sa[16], sb[16], ca[NOISE ? 16 : 1], cb[NOISE ? 16 : 1];
+    lane_scores(kb, c0, c1, g, sa, sb, ca, cb);
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      if (__ballot(st.cnt > kCand - 8) != 0)
+    for (int q = 0; q < 4; ++q) {
+      if (__ballot(st.wp > flush_at) != 0)
         flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int r = 4 * g + (e & 3);
+        const int r = 4 * q + (e & 3);
         const float x = e < 4 ? sa[r] : sb[r];
         if (x > st.thr) {
-          cbuf[wave][st.cnt][lane] = make_key(x, kb + 8 * g + e);
-          if (NOISE) cpay[NOISE ? wave : 0][NOISE ? st.cnt : 0][lane] = e < 4 ? ca[NOISE ? r : 0] : cb[NOISE ? r : 0];
-          ++st.cnt;
+          *st.wp = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * q + e));
+          if (NOISE) {
+            const int slot = (int)(st.wp - &mybuf[0][0]);
+            (&cpay[NOISE ? wave : 0][0][0])[NOISE ? slot : 0] = e < 4 ? ca[NOISE ? r : 0] : cb[NOISE ? r : 0];
+          }
+          st.wp += kWave;
         }
       }
     }
@@ -501,22 +568,38 @@ __global__ __launch_bounds__(256) void pair_kernel(PairParams p) {
 
 // ---------------------------------------------------------------- host side
 struct Plan {
-  int splits, blk_per_split, nblk, kmax;
+  int splits, blk_per_split, nblk, kmax, pass1_blocks;
   int64_t qblocks;
 };
+
+// Workgroups a launch should reach before the key range is split (two waves
+// each: two waves per SIMD of the 256 CUs, so that one wave's selection work
+// overlaps the other's MFMAs).
+#ifndef MPL_SCORE_TARGET_WGS
+#define MPL_SCORE_TARGET_WGS 1024
+#endif
+// The bound pass scans min(blocks, max(MIN, blocks / DIV)) blocks of a split.
+#ifndef MPL_PASS1_MIN
+#define MPL_PASS1_MIN 16
+#endif
+#ifndef MPL_PASS1_DIV
+#define MPL_PASS1_DIV 8
+#endif
 
 static Plan make_plan(int64_t M, int H, int n, int k) {
   Plan pl;
   pl.nblk = (int)cdiv(n, 32);
   pl.qblocks = cdiv(M, kScoreThreads);
   const int64_t base = pl.qblocks * 2 * H;
-  int64_t s = cdiv(1024, base);
+  int64_t s = cdiv(MPL_SCORE_TARGET_WGS, base);
   s = s < 1 ? 1 : s;
   s = s > kMaxSplits ? kMaxSplits : s;
   s = s > pl.nblk ? pl.nblk : s;
   pl.blk_per_split = (int)cdiv(pl.nblk, s);
   pl.splits = (int)cdiv(pl.nblk, pl.blk_per_split);
   pl.kmax = k <= 16 ? 16 : 32;
+  const int p1 = pl.blk_per_split / MPL_PASS1_DIV;
+  pl.pass1_blocks = std::min(pl.blk_per_split, std::max(MPL_PASS1_MIN, p1));
   return pl;
 }
 
@@ -590,6 +673,8 @@ extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const voi
   MPL_REQUIRE(k <= n && k <= 32, MPL_EUNSUPPORTED, "mpl_score_select: need k <= min(n, 32), got k=%d n=%d",
               k, n);
   MPL_REQUIRE(half <= 128, MPL_EUNSUPPORTED, "mpl_score_select: half=%d > 128", half);
+  MPL_REQUIRE(score_dtype != MPL_F16 || half % 8 == 0, MPL_EUNSUPPORTED,
+              "mpl_score_select: fp16 scoring needs half %% 8 == 0 (got %d); use MPL_F32", half);
   MPL_REQUIRE((int64_t)n * n < ((int64_t)1 << 31), MPL_EUNSUPPORTED, "mpl_score_select: n*n must be < 2^31");
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
               "mpl_score_select: score_dtype must be MPL_F16 or MPL_F32");
@@ -620,6 +705,7 @@ extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const voi
   sp.nblk = pl.nblk;
   sp.splits = pl.splits;
   sp.blk_per_split = pl.blk_per_split;
+  sp.pass1_blocks = pl.pass1_blocks;
   float* w = (float*)workspace;
   const size_t part = per * pl.splits;
   if (pl.splits == 1) {

@@ -117,8 +117,14 @@ class MemoryPool:
         self.host_pool = host_pool
         self.name = name
         self.values_dtype = values_dtype
-        # fp16 MFMA scoring for fp16 tables, fp32 MFMA scoring for fp32 tables
-        self.score_dtype = score_dtype or (torch.float16 if values_dtype == torch.float16 else torch.float32)
+        # fp16 MFMA scoring for fp16 tables, fp32 MFMA scoring for fp32 tables; fp16 scoring
+        # reads 8-dim query vectors, so key halves of other widths score in fp32
+        if score_dtype is None:
+            fp16_ok = values_dtype == torch.float16 and (d_key // 2) % 8 == 0
+            score_dtype = torch.float16 if fp16_ok else torch.float32
+        elif score_dtype == torch.float16 and (d_key // 2) % 8 != 0:
+            raise ValueError(f"fp16 scoring needs d_key/2 to be a multiple of 8, got d_key={d_key}")
+        self.score_dtype = score_dtype
         self._keys = _KeyCache()
         self._temp_key = None
         self._temp_val = None
