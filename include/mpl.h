@@ -96,6 +96,60 @@ int mpl_gather_wsum(const void* values, int values_dtype, int64_t N, int d,
                     const int32_t* slots, const float* weights, int64_t M, int R,
                     int shuffle_reads, float* out, void* stream);
 
+/*
+ * train.py:146-172 (fetched_row_grads + _merge_rows): gradient rows of the
+ * fetched pool rows.  Fetch p in [0, P) of token p / fetches_per_token reads
+ * slot slots[p] with weight weights[p] (weights == NULL: 1).  With
+ * cap = min(P, pool_size) it writes
+ *   uniq       [cap]    int32  distinct slots ascending, then pool_size padding
+ *   rows       [cap,d]  fp32   sum over the fetches of uniq[u] of
+ *                              weights[p] * g[p / fetches_per_token, :]; 0 for padding
+ *   row_sq     [cap]    fp32   squared L2 norm of each row (for the global clip)
+ *   num_unique [1]      int32  number of distinct slots (device memory)
+ * g: [P / fetches_per_token, d] fp32.  Several memory layers are merged by
+ * stacking their tokens (slots/weights concatenated in the same order).
+ * Passing the materialised contributions as g with fetches_per_token = 1 and
+ * weights = NULL is _merge_rows itself.  Deterministic: a stable radix sort
+ * by slot and fixed-order segment sums, no float atomics.  Needs d <= 1024,
+ * P and pool_size < 2^31, slots in [0, pool_size).
+ */
+size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_size);
+int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
+                   const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
+                   int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, void* stream);
+
+/*
+ * train.py:395-397: gnorm = sqrt(rest_sq + sum(row_sq)) and
+ * scale = min(1, grad_clip / (gnorm + 1e-6)); scale_gnorm[0] = scale,
+ * scale_gnorm[1] = gnorm (device memory).  rest_sq (device, may be NULL = 0)
+ * is the squared global norm of the dense gradients.
+ */
+int mpl_clip_scale(const float* row_sq, int64_t cap, const float* rest_sq, float grad_clip,
+                   float* scale_gnorm, void* stream);
+
+/*
+ * train.py:412-416 (row-wise Adagrad, in place): for each u < cap with
+ * 0 <= uniq[u] < pool_size (padding is dropped), g = rows[u] * grad_scale,
+ * acc' = acc[s] + mean(g^2), values[s] += -lr / (sqrt(acc') + 1e-8) * g,
+ * acc[s] = acc'.  values [pool_size, d] in values_dtype; with master != NULL
+ * (fp32 [pool_size, d]) the master takes the update and values receives its
+ * cast (host_pool.py:152 semantics for fp16 tables otherwise).  grad_scale:
+ * device scalar or NULL (= 1), e.g. scale_gnorm from mpl_clip_scale.
+ */
+int mpl_row_adagrad(void* values, int values_dtype, float* master, float* acc,
+                    const int32_t* uniq, const float* rows, int64_t cap, int d,
+                    int64_t pool_size, float lr, const float* grad_scale, void* stream);
+
+/*
+ * train.py:417-426 (lazy Adam on the fetched rows, in place): m, v
+ * [pool_size, d] fp32; b1 = 0.9, b2 = 0.999, eps = 1e-8; bias corrections
+ * with n = step + 1 (step = the 0-based TrainState.step).  values, master,
+ * grad_scale and padding as for mpl_row_adagrad.
+ */
+int mpl_row_adam(void* values, int values_dtype, float* master, float* m, float* v,
+                 const int32_t* uniq, const float* rows, int64_t cap, int d,
+                 int64_t pool_size, float lr, int step, const float* grad_scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,678 @@
+// Sparse value gradients and row-wise optimizers of the memory pool
+// (train.py:146-172, 395-399, 409-426).
+//
+// merge_rows: the gradient of a fetched row is the sum, over the fetches of
+// that slot, of weight * dL/dout of the fetching token.  The reference
+// materialises one contribution row per fetch and runs jnp.unique +
+// segment_sum; here the (slot, fetch) pairs are sorted by slot with a stable
+// LSD radix sort (8-bit digits), runs of equal slots become segments, and
+// each segment's rows are summed in a fixed order straight from dL/dout, so
+// the contribution rows never exist and no float atomics are used: the
+// result is bitwise reproducible.
+//
+// Radix pass (three kernels): per-tile digit histograms laid out
+// digit-major, one exclusive scan over them, and a stable scatter in which
+// each wave ranks its 64 keys by digit with ballots (lanes of equal digit
+// and lower lane id), waves of a tile are ordered through LDS counters, and
+// tiles through the scanned histogram.
+//
+// Segmented sum: wave r owns sorted entries [r*128, r*128 + 128) and walks
+// them in order, eight rows in flight.  A segment that lies inside the range
+// is written as a finished row; the range's first and last segment, when
+// they cross the range boundary, leave partial sums that a fix-up kernel
+// adds in range order.  Hot rows (Zipf-skewed routing) therefore spread over
+// many waves without changing the summation order from run to run.
+#include <math.h>
+
+#include "common.h"
+
+namespace mpl {
+
+constexpr int kSortThreads = 256;
+constexpr int kSortRounds = 8;
+constexpr int kSortTile = kSortThreads * kSortRounds;  // keys per tile
+constexpr int kRangeLen = 128;                         // sorted entries per reduce wave
+constexpr int kRowThreads = 256;                       // four rows (waves) per block
+
+__device__ __forceinline__ uint64_t lanes_below(int lane) { return (1ull << lane) - 1ull; }
+
+// Mask of the valid lanes whose 8-bit digit equals this lane's.
+__device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid) {
+  uint64_t peers = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 8; ++b) {
+    const bool bit = (digit >> b) & 1u;
+    const uint64_t m = __ballot(bit);
+    peers &= bit ? m : ~m;
+  }
+  return peers;
+}
+
+// ------------------------------------------------------------ radix sort
+__global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n,
+                                                                   int shift, uint32_t* __restrict__ hist,
+                                                                   int64_t ntiles) {
+  __shared__ uint32_t h[256];
+  const int tid = threadIdx.x;
+  h[tid] = 0;
+  __syncthreads();
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+#pragma unroll
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = base + r * kSortThreads + tid;
+    if (i < n) atomicAdd(&h[(keys[i] >> shift) & 255u], 1u);  // integer LDS counts: order-free
+  }
+  __syncthreads();
+  hist[(int64_t)tid * ntiles + blockIdx.x] = h[tid];
+}
+
+// In-place exclusive scan of a[0, len) by one workgroup; *total (if not
+// null) receives the sum.
+__global__ __launch_bounds__(1024) void scan_exclusive_kernel(uint32_t* __restrict__ a, int64_t len,
+                                                              uint32_t* __restrict__ total) {
+  __shared__ uint32_t part[1024];
+  const int tid = threadIdx.x;
+  const int64_t chunk = cdiv(len, 1024);
+  const int64_t b = tid * chunk;
+  const int64_t e = b + chunk < len ? b + chunk : len;
+  uint32_t s = 0;
+  for (int64_t i = b; i < e; ++i) s += a[i];
+  part[tid] = s;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const uint32_t v = tid >= off ? part[tid - off] : 0u;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  uint32_t run = tid ? part[tid - 1] : 0u;
+  for (int64_t i = b; i < e; ++i) {
+    const uint32_t v = a[i];
+    a[i] = run;
+    run += v;
+  }
+  if (tid == 1023 && total != nullptr) *total = part[1023];
+}
+
+// Stable scatter of one radix pass.  vals_in == null means the identity
+// (values = input positions).
+__global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
+    uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist_scan, int64_t ntiles) {
+  __shared__ uint32_t tile_off[256];
+  __shared__ uint32_t seen[256];  // keys of each digit in earlier rounds of this tile
+  __shared__ uint32_t wave_cnt[kSortThreads / kWave][256];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  tile_off[tid] = hist_scan[(int64_t)tid * ntiles + blockIdx.x];
+  seen[tid] = 0;
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = base + r * kSortThreads + tid;
+    const bool valid = i < n;
+    const uint32_t key = keys_in[valid ? i : 0];
+    const uint32_t val = vals_in != nullptr ? vals_in[valid ? i : 0] : (uint32_t)i;
+    const uint32_t digit = (key >> shift) & 255u;
+    const uint64_t peers = digit_peers(digit, valid);
+    const uint32_t rank = (uint32_t)__popcll(peers & lanes_below(lane));
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wave_cnt[wave][lane * 4 + j] = 0;
+    if (valid && rank == 0) wave_cnt[wave][digit] = (uint32_t)__popcll(peers);
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_cnt[w][digit];
+    if (valid) {
+      const uint32_t pos = tile_off[digit] + seen[digit] + before + rank;
+      keys_out[pos] = key;
+      vals_out[pos] = val;
+    }
+    __syncthreads();
+    uint32_t add = 0;
+#pragma unroll
+    for (int w = 0; w < kSortThreads / kWave; ++w) add += wave_cnt[w][tid];
+    seen[tid] += add;
+    __syncthreads();
+  }
+}
+
+// --------------------------------------------------------------- segments
+__device__ __forceinline__ bool seg_head(const uint32_t* s, int64_t i) { return i == 0 || s[i] != s[i - 1]; }
+
+__global__ __launch_bounds__(kSortThreads) void seg_count_kernel(const uint32_t* __restrict__ s, int64_t n,
+                                                                  uint32_t* __restrict__ tile_cnt) {
+  __shared__ uint32_t c[kSortThreads / kWave];
+  const int tid = threadIdx.x;
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  uint32_t cnt = 0;
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = base + r * kSortThreads + tid;
+    cnt += (i < n && seg_head(s, i)) ? 1u : 0u;
+  }
+  for (int off = 32; off >= 1; off >>= 1) cnt += __shfl_xor(cnt, off);
+  if ((tid & 63) == 0) c[tid >> 6] = cnt;
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t t = 0;
+    for (int w = 0; w < kSortThreads / kWave; ++w) t += c[w];
+    tile_cnt[blockIdx.x] = t;
+  }
+}
+
+// Segment u starts at sorted position seg_start[u] and has slot uniq[u];
+// seg_of[i] is the segment of position i.
+__global__ __launch_bounds__(kSortThreads) void seg_write_kernel(const uint32_t* __restrict__ s, int64_t n,
+                                                                  const uint32_t* __restrict__ tile_base,
+                                                                  int32_t* __restrict__ uniq,
+                                                                  int32_t* __restrict__ seg_start,
+                                                                  int32_t* __restrict__ seg_of) {
+  __shared__ uint32_t wave_cnt[kSortThreads / kWave];
+  __shared__ uint32_t seen;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  if (tid == 0) seen = 0;
+  const int64_t base = (int64_t)blockIdx.x * kSortTile;
+  const uint32_t tb = tile_base[blockIdx.x];
+  for (int r = 0; r < kSortRounds; ++r) {
+    const int64_t i = base + r * kSortThreads + tid;
+    const bool valid = i < n;
+    const bool head = valid && seg_head(s, i);
+    const uint64_t heads = __ballot(head);
+    if (lane == 0) wave_cnt[wave] = (uint32_t)__popcll(heads);
+    __syncthreads();
+    uint32_t before = seen;
+    for (int w = 0; w < wave; ++w) before += wave_cnt[w];
+    // inclusive count of heads up to this lane, minus one
+    const uint32_t incl = before + (uint32_t)__popcll(heads & (lanes_below(lane) | (1ull << lane)));
+    if (valid) {
+      const uint32_t u = tb + incl - 1u;
+      seg_of[i] = (int32_t)u;
+      if (head) {
+        uniq[u] = (int32_t)s[i];
+        seg_start[u] = (int32_t)i;
+      }
+    }
+    __syncthreads();
+    if (tid == 0) {
+      uint32_t t = 0;
+      for (int w = 0; w < kSortThreads / kWave; ++w) t += wave_cnt[w];
+      seen += t;
+    }
+    __syncthreads();
+  }
+}
+
+// --------------------------------------------------------- segmented sum
+// A row of d floats is nv vectors of W floats (W = 4 when d % 4 == 0, else
+// 1); lane l owns vectors l, l+64, ...  Loads are clamped and zeroed after,
+// so lanes past the row end hold zeros.
+template <int W>
+struct RowVec {
+  float x[W];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int i = 0; i < W; ++i) x[i] = 0.f;
+  }
+  __device__ __forceinline__ void load(const float* p, int64_t vec, bool in) {
+    const int64_t o = (in ? vec : 0) * W;
+    if (W == 4) {
+      const float4 f = *(const float4*)(p + o);
+      x[0] = f.x;
+      x[W > 1 ? 1 : 0] = f.y;
+      x[W > 2 ? 2 : 0] = f.z;
+      x[W > 3 ? 3 : 0] = f.w;
+    } else {
+      x[0] = p[o];
+    }
+    if (!in) zero();
+  }
+  __device__ __forceinline__ void store(float* p, int64_t vec) const {
+    if (W == 4) {
+      *(float4*)(p + vec * W) = make_float4(x[0], x[W > 1 ? 1 : 0], x[W > 2 ? 2 : 0], x[W > 3 ? 3 : 0]);
+    } else {
+      p[vec] = x[0];
+    }
+  }
+  __device__ __forceinline__ void fma_add(float w, const RowVec& r) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) x[i] += w * r.x[i];
+  }
+  __device__ __forceinline__ void add(const RowVec& r) {
+#pragma unroll
+    for (int i = 0; i < W; ++i) x[i] += r.x[i];
+  }
+  __device__ __forceinline__ float sq() const {
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < W; ++i) s += x[i] * x[i];
+    return s;
+  }
+};
+
+template <int W, int VPL>
+__device__ __forceinline__ float wave_sq(const RowVec<W> (&a)[VPL]) {
+  float s = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) s += a[v].sq();
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off);
+  return s;
+}
+
+template <int W, int VPL>
+__global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
+    const uint32_t* __restrict__ sorted_p, const int32_t* __restrict__ seg_of, const int32_t* __restrict__ seg_start,
+    const float* __restrict__ weights, const float* __restrict__ g, int fpt, int nv, int64_t n,
+    float* __restrict__ rows, float* __restrict__ row_sq, float* __restrict__ partial) {
+  const int64_t r = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = r * kRangeLen;
+  if (r0 >= n) return;
+  const int64_t r1 = r0 + kRangeLen < n ? r0 + kRangeLen : n;
+
+  RowVec<W> acc[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) acc[v].zero();
+  int cur = seg_of[r0];
+  bool first = true;
+  auto emit = [&](int seg) {
+    const int64_t s0 = seg_start[seg], s1 = seg_start[seg + 1];
+    if (s0 >= r0 && s1 <= r1) {
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        if (c < nv) acc[v].store(rows, (int64_t)seg * nv + c);
+      }
+      const float sq = wave_sq<W, VPL>(acc);
+      if (lane == 0) row_sq[seg] = sq;
+    } else {
+      const int slot = first ? 0 : 1;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        if (c < nv) acc[v].store(partial, (r * 2 + slot) * nv + c);
+      }
+    }
+  };
+  for (int64_t i = r0; i < r1; i += 8) {
+    uint32_t pp[8];
+    int sg[8];
+    float ww[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t idx = i + j < r1 ? i + j : r1 - 1;
+      pp[j] = sorted_p[idx];
+      sg[j] = seg_of[idx];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ww[j] = weights != nullptr ? weights[pp[j]] : 1.f;
+    RowVec<W> row[8][VPL];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int64_t t = pp[j] / (uint32_t)fpt;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        row[j][v].load(g, t * nv + c, c < nv);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (i + j < r1) {
+        if (sg[j] != cur) {
+          emit(cur);
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) acc[v].zero();
+          cur = sg[j];
+          first = false;
+        }
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) acc[v].fma_add(ww[j], row[j][v]);
+      }
+    }
+  }
+  emit(cur);
+}
+
+// Adds the partial sums of segments that cross range boundaries (in range
+// order) and pads rows [U, cap) with slot pool_size and zeros.
+template <int W, int VPL>
+__global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* __restrict__ seg_start,
+                                                                 const uint32_t* __restrict__ num_seg, int64_t cap,
+                                                                 int nv, int64_t pool_size,
+                                                                 const float* __restrict__ partial,
+                                                                 int32_t* __restrict__ uniq, float* __restrict__ rows,
+                                                                 float* __restrict__ row_sq) {
+  const int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (u >= cap) return;
+  const int64_t U = *num_seg;
+  RowVec<W> acc[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) acc[v].zero();
+  if (u < U) {
+    const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
+    const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
+    if (ra == rb) return;  // finished by seg_reduce_kernel
+    const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
+    for (int64_t r = ra; r <= rb; ++r) {
+      const int slot = r == ra ? slot_a : 0;
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        RowVec<W> p;
+        p.load(partial, (r * 2 + slot) * nv + c, c < nv);
+        acc[v].add(p);
+      }
+    }
+  } else if (lane == 0) {
+    uniq[u] = (int32_t)pool_size;
+  }
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = lane + kWave * v;
+    if (c < nv) acc[v].store(rows, u * nv + c);
+  }
+  const float sq = wave_sq<W, VPL>(acc);
+  if (lane == 0) row_sq[u] = sq;
+}
+
+__global__ void seg_finish_kernel(const uint32_t* __restrict__ num_seg, int64_t n, int32_t* __restrict__ seg_start,
+                                  int32_t* __restrict__ num_unique) {
+  const uint32_t U = *num_seg;
+  seg_start[U] = (int32_t)n;
+  *num_unique = (int32_t)U;
+}
+
+__global__ void store_zero_kernel(int32_t* p) { *p = 0; }
+
+// ---------------------------------------------------------- global norm
+// train.py:395-396 over the rows: sum of row_sq in a fixed order (fp64), then
+// gnorm = sqrt(rest + sum) and scale = min(1, clip / (gnorm + 1e-6)).
+__global__ __launch_bounds__(1024) void clip_scale_kernel(const float* __restrict__ row_sq, int64_t cap,
+                                                          const float* __restrict__ rest_sq, float clip,
+                                                          float* __restrict__ out) {
+  __shared__ double part[1024];
+  const int tid = threadIdx.x;
+  double s = 0.0;
+  for (int64_t i = tid; i < cap; i += 1024) s += (double)row_sq[i];
+  part[tid] = s;
+  __syncthreads();
+  for (int off = 512; off >= 1; off >>= 1) {
+    if (tid < off) part[tid] += part[tid + off];
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const double total = part[0] + (rest_sq != nullptr ? (double)*rest_sq : 0.0);
+    const float gnorm = (float)sqrt(total);
+    out[0] = fminf(1.f, clip / (gnorm + 1e-6f));
+    out[1] = gnorm;
+  }
+}
+
+// ---------------------------------------------------------- optimizers
+template <typename V>
+__device__ __forceinline__ float load_val(const V* p) { return (float)*p; }
+template <typename V>
+__device__ __forceinline__ void store_val(V* p, float x) { *p = (V)x; }
+
+// train.py:412-416.  One wave per row; padding (slot outside [0, N)) dropped.
+template <typename V>
+__global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict__ values, float* __restrict__ master,
+                                                                   float* __restrict__ acc,
+                                                                   const int32_t* __restrict__ uniq,
+                                                                   const float* __restrict__ rows, int64_t cap, int d,
+                                                                   int64_t N, float lr,
+                                                                   const float* __restrict__ grad_scale) {
+  const int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (u >= cap) return;
+  const int64_t s = uniq[u];
+  if (s < 0 || s >= N) return;
+  const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
+  float sq = 0.f;
+  for (int c = lane; c < d; c += kWave) {
+    const float g = rows[u * d + c] * sc;
+    sq += g * g;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+  const float a = acc[s] + sq / (float)d;
+  const float step = lr / (sqrtf(a) + 1e-8f);
+  for (int c = lane; c < d; c += kWave) {
+    const float upd = -step * (rows[u * d + c] * sc);
+    const int64_t o = s * d + c;
+    if (master != nullptr) {
+      const float m = master[o] + upd;
+      master[o] = m;
+      store_val(values + o, m);
+    } else {
+      store_val(values + o, load_val(values + o) + upd);
+    }
+  }
+  if (lane == 0) acc[s] = a;
+}
+
+// train.py:417-426 (c1 = 1 - b1^n, c2 = 1 - b2^n with n = step + 1).
+template <typename V>
+__global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ values, float* __restrict__ master,
+                                                                float* __restrict__ m1, float* __restrict__ m2,
+                                                                const int32_t* __restrict__ uniq,
+                                                                const float* __restrict__ rows, int64_t cap, int d,
+                                                                int64_t N, float lr, float c1, float c2,
+                                                                const float* __restrict__ grad_scale) {
+  const int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (u >= cap) return;
+  const int64_t s = uniq[u];
+  if (s < 0 || s >= N) return;
+  const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
+  const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+  for (int c = lane; c < d; c += kWave) {
+    const int64_t o = s * d + c;
+    const float g = rows[u * d + c] * sc;
+    const float m = b1 * m1[o] + (1.f - b1) * g;
+    const float v = b2 * m2[o] + (1.f - b2) * g * g;
+    const float upd = -lr * (m / c1) / (sqrtf(v / c2) + eps);
+    m1[o] = m;
+    m2[o] = v;
+    if (master != nullptr) {
+      const float x = master[o] + upd;
+      master[o] = x;
+      store_val(values + o, x);
+    } else {
+      store_val(values + o, load_val(values + o) + upd);
+    }
+  }
+}
+
+// ------------------------------------------------------------ host side
+struct MergeLayout {
+  int64_t ntiles, nranges, cap;
+  int passes;
+  size_t keys[2], vals[2], hist, tile_cnt, counters, seg_start, seg_of, partial, total;
+};
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+static MergeLayout merge_layout(int64_t P, int d, int64_t pool_size) {
+  MergeLayout L;
+  L.ntiles = cdiv(P, kSortTile);
+  L.nranges = cdiv(P, kRangeLen);
+  L.cap = P < pool_size ? P : pool_size;
+  int bits = 0;
+  while (bits < 62 && ((int64_t)1 << bits) < pool_size) ++bits;
+  L.passes = bits <= 8 ? 1 : (bits + 7) / 8;
+  const int64_t nfl = d;  // partial rows: d floats
+  size_t o = 0;
+  for (int b = 0; b < 2; ++b) {
+    L.keys[b] = o;
+    o += align256((size_t)P * 4);
+    L.vals[b] = o;
+    o += align256((size_t)P * 4);
+  }
+  L.hist = o;
+  o += align256((size_t)256 * L.ntiles * 4);
+  L.tile_cnt = o;
+  o += align256((size_t)L.ntiles * 4);
+  L.counters = o;  // [0]: segment count
+  o += 256;
+  L.seg_start = o;
+  o += align256((size_t)(L.cap + 1) * 4);
+  L.seg_of = o;
+  o += align256((size_t)P * 4);
+  L.partial = o;
+  o += align256((size_t)L.nranges * 2 * nfl * 4);
+  L.total = o;
+  return L;
+}
+
+template <int W, int VPL>
+static void launch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32_t* seg_start, const float* weights,
+                          const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
+                          const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
+                          hipStream_t s) {
+  const unsigned b1 = (unsigned)cdiv(L.nranges, kRowThreads / kWave);
+  seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq,
+                                                       partial);
+  const unsigned b2 = (unsigned)cdiv(L.cap, kRowThreads / kWave);
+  seg_fixup_kernel<W, VPL><<<b2, kRowThreads, 0, s>>>(seg_start, nseg, L.cap, nv, pool_size, partial, uniq, rows,
+                                                      row_sq);
+}
+
+template <int W>
+static void dispatch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32_t* seg_start, const float* weights,
+                            const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
+                            const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
+                            hipStream_t s) {
+  const int vpl = (int)cdiv(nv, kWave);
+#define MPL_REDUCE(V)                                                                                              \
+  launch_reduce<W, V>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq, partial, L, nseg, pool_size, \
+                      uniq, s)
+  if (vpl <= 1) MPL_REDUCE(1);
+  else if (vpl <= 2) MPL_REDUCE(2);
+  else if (vpl <= 4) MPL_REDUCE(4);
+  else if (vpl <= 8) MPL_REDUCE(8);
+  else MPL_REDUCE(16);
+#undef MPL_REDUCE
+}
+
+}  // namespace mpl
+
+using namespace mpl;
+
+extern "C" size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_size) {
+  if (P <= 0 || d <= 0 || pool_size <= 0) return 0;
+  return merge_layout(P, d, pool_size).total;
+}
+
+extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
+                              const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
+                              int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, void* stream) {
+  clear_error();
+  MPL_REQUIRE(P >= 0 && fetches_per_token > 0 && d > 0 && pool_size > 0, MPL_EINVAL,
+              "mpl_merge_rows: bad sizes P=%lld fetches_per_token=%d d=%d pool_size=%lld", (long long)P,
+              fetches_per_token, d, (long long)pool_size);
+  MPL_REQUIRE(P < ((int64_t)1 << 31) && pool_size < ((int64_t)1 << 31), MPL_EUNSUPPORTED,
+              "mpl_merge_rows: P and pool_size must be < 2^31");
+  MPL_REQUIRE(d <= 16 * kWave, MPL_EUNSUPPORTED, "mpl_merge_rows: d must be <= 1024, got %d", d);
+  hipStream_t s = (hipStream_t)stream;
+  if (P == 0) {
+    MPL_REQUIRE(num_unique != nullptr, MPL_EINVAL, "mpl_merge_rows: null num_unique");
+    store_zero_kernel<<<1, 1, 0, s>>>(num_unique);  // a kernel, not a memset: safe under graph capture
+    return check_launch("mpl_merge_rows");
+  }
+  MPL_REQUIRE(slots && g && uniq && rows && row_sq && num_unique, MPL_EINVAL, "mpl_merge_rows: null buffer");
+  const MergeLayout L = merge_layout(P, d, pool_size);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
+              "mpl_merge_rows: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+  char* ws = (char*)workspace;
+  uint32_t* keys[2] = {(uint32_t*)(ws + L.keys[0]), (uint32_t*)(ws + L.keys[1])};
+  uint32_t* vals[2] = {(uint32_t*)(ws + L.vals[0]), (uint32_t*)(ws + L.vals[1])};
+  uint32_t* hist = (uint32_t*)(ws + L.hist);
+  uint32_t* tile_cnt = (uint32_t*)(ws + L.tile_cnt);
+  uint32_t* nseg = (uint32_t*)(ws + L.counters);
+  int32_t* seg_start = (int32_t*)(ws + L.seg_start);
+  int32_t* seg_of = (int32_t*)(ws + L.seg_of);
+  float* partial = (float*)(ws + L.partial);
+
+  const unsigned nt = (unsigned)L.ntiles;
+  const uint32_t* kin = (const uint32_t*)slots;
+  const uint32_t* vin = nullptr;
+  int cur = 0;
+  for (int pass = 0; pass < L.passes; ++pass) {
+    const int shift = 8 * pass;
+    radix_hist_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);
+    scan_exclusive_kernel<<<1, 1024, 0, s>>>(hist, 256 * L.ntiles, nullptr);
+    radix_scatter_kernel<<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles);
+    kin = keys[cur];
+    vin = vals[cur];
+    cur ^= 1;
+  }
+  int rc = check_launch("mpl_merge_rows(sort)");
+  if (rc) return rc;
+  seg_count_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt);
+  scan_exclusive_kernel<<<1, 1024, 0, s>>>(tile_cnt, L.ntiles, nseg);
+  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of);
+  seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique);
+  if (d % 4 == 0)
+    dispatch_reduce<4>(vin, seg_of, seg_start, weights, g, fetches_per_token, d / 4, P, rows, row_sq, partial, L,
+                       nseg, pool_size, uniq, s);
+  else
+    dispatch_reduce<1>(vin, seg_of, seg_start, weights, g, fetches_per_token, d, P, rows, row_sq, partial, L, nseg,
+                       pool_size, uniq, s);
+  return check_launch("mpl_merge_rows(reduce)");
+}
+
+extern "C" int mpl_clip_scale(const float* row_sq, int64_t cap, const float* rest_sq, float grad_clip,
+                              float* scale_gnorm, void* stream) {
+  clear_error();
+  MPL_REQUIRE(cap >= 0 && scale_gnorm != nullptr && (cap == 0 || row_sq != nullptr), MPL_EINVAL,
+              "mpl_clip_scale: bad arguments");
+  clip_scale_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(row_sq, cap, rest_sq, grad_clip, scale_gnorm);
+  return check_launch("mpl_clip_scale");
+}
+
+extern "C" int mpl_row_adagrad(void* values, int values_dtype, float* master, float* acc, const int32_t* uniq,
+                               const float* rows, int64_t cap, int d, int64_t pool_size, float lr,
+                               const float* grad_scale, void* stream) {
+  clear_error();
+  MPL_REQUIRE(cap >= 0 && d > 0 && pool_size > 0, MPL_EINVAL, "mpl_row_adagrad: bad sizes");
+  MPL_REQUIRE(values_dtype == MPL_F16 || values_dtype == MPL_F32, MPL_EINVAL,
+              "mpl_row_adagrad: values_dtype must be MPL_F16 or MPL_F32");
+  if (cap == 0) return MPL_OK;
+  MPL_REQUIRE(values && acc && uniq && rows, MPL_EINVAL, "mpl_row_adagrad: null buffer");
+  const unsigned b = (unsigned)cdiv(cap, kRowThreads / kWave);
+  hipStream_t s = (hipStream_t)stream;
+  if (values_dtype == MPL_F16)
+    row_adagrad_kernel<_Float16><<<b, kRowThreads, 0, s>>>((_Float16*)values, master, acc, uniq, rows, cap, d,
+                                                           pool_size, lr, grad_scale);
+  else
+    row_adagrad_kernel<float><<<b, kRowThreads, 0, s>>>((float*)values, master, acc, uniq, rows, cap, d, pool_size,
+                                                        lr, grad_scale);
+  return check_launch("mpl_row_adagrad");
+}
+
+extern "C" int mpl_row_adam(void* values, int values_dtype, float* master, float* m, float* v, const int32_t* uniq,
+                            const float* rows, int64_t cap, int d, int64_t pool_size, float lr, int step,
+                            const float* grad_scale, void* stream) {
+  clear_error();
+  MPL_REQUIRE(cap >= 0 && d > 0 && pool_size > 0 && step >= 0, MPL_EINVAL, "mpl_row_adam: bad sizes");
+  MPL_REQUIRE(values_dtype == MPL_F16 || values_dtype == MPL_F32, MPL_EINVAL,
+              "mpl_row_adam: values_dtype must be MPL_F16 or MPL_F32");
+  if (cap == 0) return MPL_OK;
+  MPL_REQUIRE(values && m && v && uniq && rows, MPL_EINVAL, "mpl_row_adam: null buffer");
+  const float n = (float)(step + 1);
+  const float c1 = 1.f - powf(0.9f, n);
+  const float c2 = 1.f - powf(0.999f, n);
+  const unsigned b = (unsigned)cdiv(cap, kRowThreads / kWave);
+  hipStream_t s = (hipStream_t)stream;
+  if (values_dtype == MPL_F16)
+    row_adam_kernel<_Float16><<<b, kRowThreads, 0, s>>>((_Float16*)values, master, m, v, uniq, rows, cap, d,
+                                                        pool_size, lr, c1, c2, grad_scale);
+  else
+    row_adam_kernel<float><<<b, kRowThreads, 0, s>>>((float*)values, master, m, v, uniq, rows, cap, d, pool_size, lr,
+                                                     c1, c2, grad_scale);
+  return check_launch("mpl_row_adam");
+}

@@ -1,0 +1,203 @@
+"""Sparse pool-row gradients and row-wise optimizers on the GPU (libmpl.so).
+
+Host mirror of the sparse half of the reference training step
+(memory_pool_model/train.py):
+
+  * ``fetched_row_grads(aux, probe_grads, layers, pool_size)``  train.py:146-163
+  * ``merge_rows(slots, contribs, pool_size)``                 train.py:166-172
+  * ``clip_scale(row_sq, rest_sq, grad_clip)``                 train.py:395-399
+  * ``rowwise_adagrad(...)``                                   train.py:412-416
+  * ``lazy_adam(...)``                                         train.py:417-426
+  * ``warmup_cosine(step, lr, warmup_steps, steps)``           train.py:100-103
+  * ``SparseRowUpdate``: the whole sparse step of train.py:378-429 on one GPU
+
+Every tensor stays on the device: the number of distinct rows and the clip
+scale are device scalars, so a step never synchronises with the host.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Dict, Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import check, ptr
+
+MPL_F16, MPL_F32 = _lib.MPL_F16, _lib.MPL_F32
+
+
+def _vcode(t: torch.Tensor) -> int:
+    if t.dtype == torch.float16:
+        return MPL_F16
+    if t.dtype == torch.float32:
+        return MPL_F32
+    raise TypeError(f"pool values must be float16 or float32, got {t.dtype}")
+
+
+@dataclass
+class MergedRows:
+    """Result of a row merge: ``uniq`` [cap] int32 (ascending, padded with
+    pool_size), ``rows`` [cap, d] fp32, ``row_sq`` [cap] fp32 squared row
+    norms and ``num_unique`` [1] int32, all on the device."""
+
+    uniq: torch.Tensor
+    rows: torch.Tensor
+    row_sq: torch.Tensor
+    num_unique: torch.Tensor
+
+
+def merge_fetches(slots: torch.Tensor, weights: Optional[torch.Tensor], g: torch.Tensor,
+                  pool_size: int) -> MergedRows:
+    """Sum weights[p] * g[p // fpt] per distinct slot, fpt = P / g.shape[0]
+    (the fetches of one token are consecutive)."""
+    dev = g.device
+    slots = slots.reshape(-1).to(torch.int32).contiguous()
+    P = slots.shape[0]
+    g = g.reshape(-1, g.shape[-1]).float().contiguous()
+    tokens, d = g.shape
+    if tokens == 0 or P % tokens:
+        if P == 0 and tokens == 0:
+            fpt = 1
+        else:
+            raise ValueError(f"{P} fetches do not divide evenly over {tokens} gradient rows")
+    else:
+        fpt = P // tokens
+    if weights is not None:
+        weights = weights.reshape(-1).float().contiguous()
+        if weights.shape[0] != P:
+            raise ValueError("weights must have one entry per fetch")
+    cap = min(P, pool_size)
+    L = _lib.lib()
+    uniq = torch.empty(cap, dtype=torch.int32, device=dev)
+    rows = torch.empty((cap, d), dtype=torch.float32, device=dev)
+    row_sq = torch.empty(cap, dtype=torch.float32, device=dev)
+    num_unique = torch.empty(1, dtype=torch.int32, device=dev)
+    wsb = L.mpl_merge_rows_workspace_bytes(P, d, pool_size)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    check(L.mpl_merge_rows(ptr(slots), ptr(weights), P, fpt, ptr(g), d, pool_size, ptr(ws), wsb, ptr(uniq),
+                           ptr(rows), ptr(row_sq), ptr(num_unique), _lib.stream_ptr(dev)), "mpl_merge_rows")
+    return MergedRows(uniq, rows, row_sq, num_unique)
+
+
+def merge_rows(slots: torch.Tensor, contribs: torch.Tensor, pool_size: int):
+    """train.py:166-172: (uniq [cap], rows [cap, d]) for materialised
+    per-fetch contribution rows."""
+    m = merge_fetches(slots, None, contribs.reshape(-1, contribs.shape[-1]), pool_size)
+    return m.uniq, m.rows
+
+
+def fetched_row_grads_full(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int) -> MergedRows:
+    """train.py:146-163 with the extra outputs (row norms, distinct count)."""
+    slots, weights, grads = [], [], []
+    for layer, sl, w in zip(layers, aux["slots"], aux["weights"]):
+        g = probe_grads[layer]
+        d = g.shape[-1]
+        hk = sl.shape[-2] * sl.shape[-1]
+        slots.append(sl.reshape(-1, hk).reshape(-1))
+        weights.append(w.detach().reshape(-1))
+        grads.append(g.reshape(-1, d))
+    return merge_fetches(torch.cat(slots), torch.cat(weights), torch.cat(grads), pool_size)
+
+
+def fetched_row_grads(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int):
+    """train.py:146-163: (unique_slots [cap], row_grads [cap, d])."""
+    m = fetched_row_grads_full(aux, probe_grads, layers, pool_size)
+    return m.uniq, m.rows
+
+
+def clip_scale(row_sq: torch.Tensor, rest_sq: Optional[torch.Tensor], grad_clip: float) -> torch.Tensor:
+    """train.py:395-397: device tensor [scale, gnorm]."""
+    dev = row_sq.device
+    out = torch.empty(2, dtype=torch.float32, device=dev)
+    if rest_sq is not None:
+        rest_sq = rest_sq.reshape(1).float().contiguous()
+    check(_lib.lib().mpl_clip_scale(ptr(row_sq.contiguous()), row_sq.shape[0], ptr(rest_sq), float(grad_clip),
+                                    ptr(out), _lib.stream_ptr(dev)), "mpl_clip_scale")
+    return out
+
+
+def rowwise_adagrad(values: torch.Tensor, acc: torch.Tensor, uniq: torch.Tensor, rows: torch.Tensor, lr: float,
+                    master: Optional[torch.Tensor] = None, grad_scale: Optional[torch.Tensor] = None) -> None:
+    """train.py:412-416, in place on values / master / acc."""
+    _check_table(values, master)
+    cap, d = rows.shape
+    check(_lib.lib().mpl_row_adagrad(ptr(values), _vcode(values), ptr(master), ptr(acc), ptr(uniq.contiguous()),
+                                     ptr(rows.contiguous()), cap, d, values.shape[0], float(lr), ptr(grad_scale),
+                                     _lib.stream_ptr(values.device)), "mpl_row_adagrad")
+
+
+def lazy_adam(values: torch.Tensor, m: torch.Tensor, v: torch.Tensor, uniq: torch.Tensor, rows: torch.Tensor,
+              lr: float, step: int, master: Optional[torch.Tensor] = None,
+              grad_scale: Optional[torch.Tensor] = None) -> None:
+    """train.py:417-426, in place; ``step`` is the 0-based TrainState.step."""
+    _check_table(values, master)
+    cap, d = rows.shape
+    check(_lib.lib().mpl_row_adam(ptr(values), _vcode(values), ptr(master), ptr(m), ptr(v), ptr(uniq.contiguous()),
+                                  ptr(rows.contiguous()), cap, d, values.shape[0], float(lr), int(step),
+                                  ptr(grad_scale), _lib.stream_ptr(values.device)), "mpl_row_adam")
+
+
+def _check_table(values, master):
+    if not values.is_contiguous() or values.dim() != 2:
+        raise ValueError("pool values must be a contiguous [N, d] tensor")
+    if master is not None and (master.shape != values.shape or master.dtype != torch.float32
+                               or not master.is_contiguous()):
+        raise ValueError("master must be a contiguous fp32 tensor shaped like values")
+
+
+def warmup_cosine(step: int, lr: float, warmup_steps: int, steps: int) -> float:
+    """train.py:100-103: optax.warmup_cosine_decay_schedule(0, lr, warmup,
+    max(steps, warmup + 1), 0.1 * lr) evaluated at ``step``."""
+    decay_steps = max(steps, warmup_steps + 1)
+    if step < warmup_steps:
+        return lr * step / warmup_steps
+    d = decay_steps - warmup_steps
+    t = min(step - warmup_steps, d)
+    return lr * (0.9 * 0.5 * (1.0 + math.cos(math.pi * t / d)) + 0.1)
+
+
+class SparseRowUpdate:
+    """The sparse pool update of train.py:378-429 on one GPU.
+
+    Holds the pool optimizer state: ``acc`` [N] (row-wise Adagrad, the
+    default ``pool_optimizer``) or ``m``, ``v`` [N, d] (lazy Adam), and an
+    optional fp32 ``master`` copy of an fp16 table."""
+
+    def __init__(self, values: torch.Tensor, *, optimizer: str = "rowwise_adagrad", lr: float = 3e-4,
+                 pool_lr_mult: float = 3.0, warmup_steps: int = 0, steps: int = 1, grad_clip: float = 1.0,
+                 master: bool = True):
+        if optimizer not in ("rowwise_adagrad", "adam"):
+            raise ValueError(f"unknown pool optimizer {optimizer!r}")
+        self.values = values
+        self.optimizer = optimizer
+        self.lr, self.pool_lr_mult = lr, pool_lr_mult
+        self.warmup_steps, self.steps, self.grad_clip = warmup_steps, steps, grad_clip
+        N, d = values.shape
+        dev = values.device
+        self.master = values.float().clone() if (master and values.dtype != torch.float32) else None
+        if optimizer == "rowwise_adagrad":
+            self.acc = torch.zeros(N, dtype=torch.float32, device=dev)
+            self.m = self.v = None
+        else:
+            self.acc = None
+            self.m = torch.zeros((N, d), dtype=torch.float32, device=dev)
+            self.v = torch.zeros((N, d), dtype=torch.float32, device=dev)
+        self.step = 0
+
+    def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
+                 rest_sq: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
+        N = self.values.shape[0]
+        merged = fetched_row_grads_full(aux, probe_grads, layers, N)
+        sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip)
+        lr = warmup_cosine(self.step, self.lr, self.warmup_steps, self.steps) * self.pool_lr_mult
+        scale = sg[0:1]
+        if self.optimizer == "rowwise_adagrad":
+            rowwise_adagrad(self.values, self.acc, merged.uniq, merged.rows, lr, self.master, scale)
+        else:
+            lazy_adam(self.values, self.m, self.v, merged.uniq, merged.rows, lr, self.step, self.master, scale)
+        self.step += 1
+        return {"grad_scale": sg[0], "grad_norm": sg[1], "rows_updated": merged.num_unique[0],
+                "uniq": merged.uniq, "row_grads": merged.rows}

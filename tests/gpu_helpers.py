@@ -75,3 +75,31 @@ def oracle_check(pool: MemoryPool, params, queries: torch.Tensor, res, *, gumbel
     out_g64 = np.einsum("mr,mrd->md", gw.reshape(M, -1), rows_g.reshape(M, H * k, d))
     np.testing.assert_allclose(out_got, out_g64, rtol=2e-5, atol=2e-6 * (np.abs(out_g64).max() + 1e-30))
     return mask
+
+
+def zipf_slots(M: int, H: int, k: int, N: int, *, s: float = 1.1, seed: int = 5) -> np.ndarray:
+    """[M, H, k] int32 slots drawn by rank with p(r) ~ r^-s over 1..N, mapped
+    through a fixed random permutation, distinct within each (token, head)."""
+    rng = np.random.default_rng(seed)
+    w = np.arange(1, N + 1, dtype=np.float64) ** -s
+    cdf = np.cumsum(w)
+    cdf /= cdf[-1]
+    perm = rng.permutation(N)
+    G = M * H
+    out = np.empty((G, k), dtype=np.int64)
+    draws = np.minimum(np.searchsorted(cdf, rng.random((G, 8 * k))), N - 1)
+    order = np.argsort(draws, axis=1, kind="stable")
+    sd = np.take_along_axis(draws, order, 1)
+    dup_sorted = np.zeros_like(sd, dtype=bool)
+    dup_sorted[:, 1:] = sd[:, 1:] == sd[:, :-1]
+    dup = np.empty_like(dup_sorted)
+    np.put_along_axis(dup, order, dup_sorted, 1)
+    nd = ~dup
+    c = np.cumsum(nd, axis=1)
+    full = c[:, -1] >= k
+    out[full] = draws[full][(nd & (c <= k))[full]].reshape(-1, k)
+    for g in np.flatnonzero(~full):  # extremely rare: top up with unused ranks
+        first = draws[g][nd[g]]
+        extra = np.setdiff1d(np.arange(N), first)[: k - first.shape[0]]
+        out[g] = np.concatenate([first, extra])
+    return perm[out].reshape(M, H, k).astype(np.int32)
