@@ -150,6 +150,54 @@ int mpl_row_adam(void* values, int values_dtype, float* master, float* m, float*
                  const int32_t* uniq, const float* rows, int64_t cap, int d,
                  int64_t pool_size, float lr, int step, const float* grad_scale, void* stream);
 
+/*
+ * Backward of the lookup (XLA's derivative of memory.py:136-193, written
+ * out).  Route part: dw[m,r] = <g_out[m], values[read(slots[m,r])]>
+ * (memory.py:192), the softmax backward ds = w (dw - sum w dw) per head
+ * (:178) and its scatter to the stage-1 ranks, d_sub[m,h,0,flat/k] and
+ * d_sub[m,h,1,flat%k] (:167-175), in j order.  g_out [M,d] fp32; slots,
+ * weights, flat_idx [M,H,k] and sub_scores [M,H,2,k] from mpl_score_select;
+ * read() as in mpl_gather_wsum.  Writes d_sub [M,H,2,k], d_weights [M,H,k]
+ * (dw, optional) and dlogt_part [M] = sum over the token of
+ * d_sub * sub_scores (the token's share of d log_temperature: T is the
+ * straight-through clamp of memory.py:143-146).  Needs H*k <= 128.
+ */
+int mpl_lookup_bwd_route(const float* g_out, const void* values, int values_dtype, int64_t N, int d,
+                         const int32_t* slots, const float* weights, const int32_t* flat_idx,
+                         const float* sub_scores, int64_t M, int H, int k, int shuffle_reads,
+                         float* d_weights, float* d_sub, float* dlogt_part, void* stream);
+
+/*
+ * d_queries [M,H,2,half] (the raw queries' gradient): dq_hat = sum_i
+ * d_sub_i * T * q_len * k_hat[hc, sub_idx_i] + dq_hat_extra (optional dense
+ * part [M,H,2,half], e.g. the balance loss), then the backward of
+ * x * rsqrt(sum x^2 + 1e-6) (memory.py:30-31) and, with q_len != NULL
+ * (query_scale), of q_len = sqrt(sum q^2 + 1e-6) / sqrt(half) (memory.py:137)
+ * with d q_len = sum_i d_sub_i * sub_scores_i / q_len + dlen_extra (optional
+ * [M,H,2]).  q: raw queries [M,H,2,half] fp32; k_hat [H,2,n,half] fp32
+ * (mpl_pack_keys).  half <= 128.
+ */
+int mpl_lookup_bwd_queries(const float* q, const float* q_len, const float* k_hat,
+                           const int32_t* sub_idx, const float* d_sub, const float* sub_scores,
+                           const float* dq_hat_extra, const float* dlen_extra, int64_t M, int H,
+                           int n, int half, int k, float temperature, float* d_queries, void* stream);
+
+/*
+ * d_sub_keys [H,2,n,half] (the raw sub_keys' gradient): dk_hat[hc,key] =
+ * sum over the (m, i) that selected key of d_sub * T * q_len * q_hat[m,hc]
+ * (a deterministic sort-by-key segmented sum, mpl_merge_rows) +
+ * dk_hat_extra (optional dense part), then the l2-normalisation backward
+ * against the raw sub_keys [H,2,n,half].  q_hat [M,H,2,half] fp32.
+ */
+size_t mpl_lookup_bwd_keys_workspace_bytes(int64_t M, int H, int n, int half, int k);
+int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, const float* q_len,
+                        const int32_t* sub_idx, const float* d_sub, const float* dk_hat_extra,
+                        int64_t M, int H, int n, int half, int k, float temperature,
+                        void* workspace, size_t workspace_bytes, float* d_sub_keys, void* stream);
+
+/* *out = sum(x[0, n)) (+ *add if add != NULL), fixed order, fp64 accumulation. */
+int mpl_sum(const float* x, int64_t n, const float* add, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

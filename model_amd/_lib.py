@@ -31,6 +31,11 @@ SIGNATURES = {
     "mpl_clip_scale": (_I, [_P, _I64, _P, _F, _P, _P]),
     "mpl_row_adagrad": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I, _I64, _F, _P, _P]),
     "mpl_row_adam": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I, _I64, _F, _I, _P, _P]),
+    "mpl_lookup_bwd_route": (_I, [_P, _P, _I, _I64, _I, _P, _P, _P, _P, _I64, _I, _I, _I, _P, _P, _P, _P]),
+    "mpl_lookup_bwd_queries": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _F, _P, _P]),
+    "mpl_lookup_bwd_keys_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
+    "mpl_lookup_bwd_keys": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _F, _P, _SZ, _P, _P]),
+    "mpl_sum": (_I, [_P, _I64, _P, _P, _P]),
 }
 
 _lib = None

@@ -72,6 +72,7 @@ class LazyAux(dict):
     first time they are read."""
 
     _LAZY = ("balance_loss", "subkey_counts", "slot_counts", "top1_weight")
+    _INTERNAL = ("_f", "_p", "_cos")
 
     def __init__(self, eager: Dict[str, Any], compute):
         super().__init__(eager)
@@ -79,7 +80,9 @@ class LazyAux(dict):
 
     def __missing__(self, key):
         if key in self._LAZY:
-            self.update(self._compute())
+            stats = self._compute()
+            self.internal = {k: stats.pop(k) for k in self._INTERNAL if k in stats}
+            self.update(stats)
             return dict.__getitem__(self, key)
         raise KeyError(key)
 
@@ -170,6 +173,9 @@ class MemoryPool:
         """memory.py:119-227.  ``variables`` = {"params": {...}} as from init();
         ``rngs["routing"]`` (seed or torch.Generator) drives the Gumbel noise."""
         params = variables["params"] if "params" in variables else variables
+        if _needs_grad(params, queries, sparse_grad):
+            return _lookup_with_grad(self, params, queries, train=train, sparse_grad=sparse_grad,
+                                     noise_scale=noise_scale, shuffle_reads=shuffle_reads, rngs=rngs)
         res = self.lookup(params, queries, train=train, noise_scale=noise_scale,
                           shuffle_reads=shuffle_reads, rngs=rngs)
         return res["out"], res["aux"]
@@ -282,7 +288,8 @@ class MemoryPool:
             p_scores = cos * T * (q_len[..., None] if q_len is not None else 1.0)
         else:
             p_scores = cos * T
-        P = torch.softmax(p_scores, dim=-1).mean(0)
+        p = torch.softmax(p_scores, dim=-1)
+        P = p.mean(0)
         balance = n * torch.mean(torch.sum(f * P, dim=-1))
         slot_counts = torch.bincount(sl.reshape(-1), minlength=self.pool_size).float()
         return {
@@ -290,6 +297,7 @@ class MemoryPool:
             "subkey_counts": subkey_counts,
             "slot_counts": slot_counts,
             "top1_weight": weights.max(-1).values.mean(),
+            "_f": f, "_p": p, "_cos": cos,
         }
 
     def _clean_sub_idx(self, q_score, q_len, packed, score_code, T, M):
@@ -308,3 +316,126 @@ class MemoryPool:
                                  ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
               "mpl_score_select(clean)")
         return sub_idx
+
+
+# ------------------------------------------------------------------ autograd
+def _needs_grad(params, queries, sparse_grad) -> bool:
+    if not torch.is_grad_enabled():
+        return False
+    ts = [queries, params["sub_keys"], params["log_temperature"]]
+    if not sparse_grad:
+        ts.append(params["values"])
+    return any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts)
+
+
+class _LookupFunction(torch.autograd.Function):
+    """(queries, sub_keys, log_temperature, values) -> (out, balance_loss) with
+    the backward of memory.py:136-213 on the GPU (include/mpl.h
+    mpl_lookup_bwd_*): the selection is piecewise constant, so gradients flow
+    through the selected clean scores, the routing softmax, the value read and
+    (dense over n) the balance loss."""
+
+    @staticmethod
+    def forward(ctx, queries, sub_keys, log_temperature, values, pool, opts):
+        params = {"sub_keys": sub_keys, "values": values, "log_temperature": log_temperature}
+        res = pool.lookup(params, queries.detach(), train=opts["train"], noise_scale=opts["noise_scale"],
+                          shuffle_reads=opts["shuffle_reads"], rngs=opts["rngs"])
+        aux = res["aux"]
+        balance = aux["balance_loss"]  # also computes f and p (memory.py:196-213)
+        ctx.pool, ctx.opts, ctx.res = pool, opts, res
+        ctx.internal = aux.internal
+        opts["_aux"] = aux  # handed back to the caller with the differentiable balance loss
+        ctx.shapes = (tuple(queries.shape), queries.dtype, sub_keys.dtype, log_temperature.dtype)
+        ctx.save_for_backward(sub_keys, values)
+        return res["out"], balance.detach()
+
+    @staticmethod
+    def backward(ctx, g_out, g_balance):
+        pool, res, opts = ctx.pool, ctx.res, ctx.opts
+        sub_keys, values = ctx.saved_tensors
+        q_shape, q_dtype, k_dtype, t_dtype = ctx.shapes
+        H, n, k, d = pool.heads, pool.n_sub_keys, pool.top_k, pool.d_value
+        half = pool.d_key // 2
+        q = res["q"]
+        M = q.shape[0]
+        dev = q.device
+        L = _lib.lib()
+        stream = _lib.stream_ptr(dev)
+        T = res["temperature"]
+        q_hat, q_len, k_hat = res["q_hat"], res["q_len"], res["k_hat"]
+        if g_out is None:
+            g_out = torch.zeros((M, d), dtype=torch.float32, device=dev)
+        g_out = g_out.reshape(M, d).float().contiguous()
+
+        # route: dw, softmax backward, scatter to the stage-1 ranks
+        d_sub = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
+        dlogt_part = torch.empty(max(M, 1), dtype=torch.float32, device=dev)
+        vals = values.detach()
+        check(L.mpl_lookup_bwd_route(ptr(g_out), ptr(vals), _dtype_code(vals.dtype), pool.pool_size, d,
+                                     ptr(res["slots"]), ptr(res["weights"]), ptr(res["flat_idx"]),
+                                     ptr(res["sub_scores"]), M, H, k, int(bool(opts["shuffle_reads"])), None,
+                                     ptr(d_sub), ptr(dlogt_part), stream), "mpl_lookup_bwd_route")
+
+        # balance loss, dense over n (memory.py:208-213)
+        dq_extra = dk_extra = dlen_extra = dlogt_extra = None
+        if g_balance is not None and M > 0:
+            f, p = ctx.internal["_f"], ctx.internal["_p"]
+            a = g_balance.reshape(()).float() * (n / (2.0 * H * M))
+            dp = a * f[None]
+            dps = p * (dp - (p * dp).sum(-1, keepdim=True))
+            btg = pool.balance_temperature_grad
+            scale = T * (q_len[..., None] if (btg and q_len is not None) else 1.0)
+            dcos = (dps * scale).contiguous()
+            hc_first = dcos.permute(1, 2, 0, 3).reshape(2 * H, M, n)
+            kh = k_hat.reshape(2 * H, n, half)
+            qh = q_hat.permute(1, 2, 0, 3).reshape(2 * H, M, half).contiguous()
+            dq_extra = torch.bmm(hc_first, kh).reshape(H, 2, M, half).permute(2, 0, 1, 3).contiguous()
+            dk_extra = torch.bmm(hc_first.transpose(1, 2).contiguous(), qh).reshape(H, 2, n, half).contiguous()
+            if btg:
+                cos = ctx.internal["_cos"]
+                scores = cos * T * (q_len[..., None] if q_len is not None else 1.0)
+                dlogt_extra = (dps * scores).sum().reshape(1).float()
+                if q_len is not None:
+                    dlen_extra = (dps * cos * T).sum(-1).contiguous()
+
+        # queries
+        dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
+        check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
+                                       ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
+                                       float(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
+        # sub-keys
+        dk = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+        raw_keys = sub_keys.detach().float().contiguous()
+        wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
+                                    ptr(dk_extra), M, H, n, half, k, float(T), ptr(ws), wsb, ptr(dk), stream),
+              "mpl_lookup_bwd_keys")
+        # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
+        dlt = torch.empty(1, dtype=torch.float32, device=dev)
+        check(L.mpl_sum(ptr(dlogt_part), M, ptr(dlogt_extra), ptr(dlt), stream), "mpl_sum")
+
+        # values: dense gradient only when the table is differentiated (sparse_grad=False)
+        dv = None
+        if ctx.needs_input_grad[3] and not opts["sparse_grad"]:
+            N = pool.pool_size
+            sl = res["slots"].long()
+            if opts["shuffle_reads"]:
+                sl = (sl + N // 2 + 1) % N
+            from .rows import merge_fetches
+            m = merge_fetches(sl.to(torch.int32), res["weights"], g_out, N)
+            dv_ext = torch.zeros((N + 1, d), dtype=torch.float32, device=dev)
+            dv_ext.index_copy_(0, m.uniq.long(), m.rows)  # padding rows (all zero) land on row N
+            dv = dv_ext[:N].to(values.dtype)
+
+        return (dq.reshape(q_shape).to(q_dtype), dk.to(k_dtype), dlt.reshape(()).to(t_dtype), dv, None, None)
+
+
+def _lookup_with_grad(pool, params, queries, *, train, sparse_grad, noise_scale, shuffle_reads, rngs):
+    opts = {"train": train, "sparse_grad": sparse_grad, "noise_scale": noise_scale,
+            "shuffle_reads": shuffle_reads, "rngs": rngs}
+    out, balance = _LookupFunction.apply(queries, params["sub_keys"], params["log_temperature"],
+                                         params["values"], pool, opts)
+    aux = opts.pop("_aux")
+    dict.__setitem__(aux, "balance_loss", balance)  # the autograd-tracked copy
+    return out.reshape(*tuple(queries.shape[:-2]), pool.d_value), aux
