@@ -14,7 +14,11 @@ Also reported in the same JSON line:
   * ``cpu_baseline``: the numpy oracle on the host cores over a bounded sample
     of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large]
+  * ``training_262k``: the training step of the same layer (forward +
+    backward + sparse row-wise Adagrad) and the sparse row update alone on
+    Zipf(1.1)-skewed routing;
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large] [--no-train]
 """
 
 from __future__ import annotations
@@ -45,6 +49,7 @@ def parse():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-large", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -208,6 +213,118 @@ def gather_roofline(lk, br):
             "algorithmic_bytes": gb}
 
 
+def zipf_slots(M, H, k, N, s=1.1, seed=5):
+    """[M, H, k] slots drawn by rank with p(r) ~ r^-s over 1..N through a fixed
+    random permutation, distinct within each (token, head)."""
+    rng = np.random.default_rng(seed)
+    cdf = np.cumsum(np.arange(1, N + 1, dtype=np.float64) ** -s)
+    cdf /= cdf[-1]
+    perm = rng.permutation(N)
+    G = M * H
+    draws = np.minimum(np.searchsorted(cdf, rng.random((G, 8 * k))), N - 1)
+    order = np.argsort(draws, axis=1, kind="stable")
+    sd = np.take_along_axis(draws, order, 1)
+    dup_s = np.zeros_like(sd, dtype=bool)
+    dup_s[:, 1:] = sd[:, 1:] == sd[:, :-1]
+    dup = np.empty_like(dup_s)
+    np.put_along_axis(dup, order, dup_s, 1)
+    nd = ~dup
+    c = np.cumsum(nd, axis=1)
+    out = np.empty((G, k), dtype=np.int64)
+    full = c[:, -1] >= k
+    out[full] = draws[full][(nd & (c <= k))[full]].reshape(-1, k)
+    for g in np.flatnonzero(~full):
+        first = draws[g][nd[g]]
+        out[g] = np.concatenate([first, np.setdiff1d(np.arange(N), first)[: k - first.shape[0]]])
+    return perm[out].reshape(M, H, k).astype(np.int32)
+
+
+def sparse_update_bench(torch, iters):
+    """The sparse value update of the training config on Zipf(1.1) routing:
+    merge of 524,288 fetches (8,192 tokens x 4 heads x 16) into rows of a
+    262,144-slot table, global-norm clip, row-wise Adagrad on an fp32 master
+    with the fp16 table refreshed."""
+    from model_amd import rows as R
+
+    M, H, k, N, d = 8192, 4, 16, 262144, 256
+    dev = "cuda"
+    slots = torch.as_tensor(zipf_slots(M, H, k, N), device=dev)
+    g = torch.Generator(device=dev).manual_seed(4)
+    w = torch.rand((M, H, k), generator=g, device=dev)
+    w = w / w.sum(-1, keepdim=True)
+    g_out = torch.randn((M, d), generator=g, device=dev) * 1e-3
+    values = torch.empty((N, d), dtype=torch.float16, device=dev).normal_(0.0, 0.02, generator=g)
+    master = values.float()
+    acc = torch.zeros(N, device=dev)
+    rest = torch.tensor([1e-4], device=dev)
+
+    def step():
+        m = R.merge_fetches(slots, w, g_out, N)
+        sg = R.clip_scale(m.row_sq, rest, 1.0)
+        R.rowwise_adagrad(values, acc, m.uniq, m.rows, 3e-3, master=master, grad_scale=sg[0:1])
+        return m
+
+    m = step()
+    torch.cuda.synchronize()
+    U = int(m.num_unique.cpu()[0])
+    ms = time_loop(torch, step, iters, 3)
+    P = M * H * k
+    alg = P * 8 + M * d * 4 + U * (2 * d * 4 + d * 2 + 8)
+    return {"workload": "sparse row update: 524,288 Zipf(1.1) fetches (8,192 tokens x 4 heads x 16), "
+                        "262,144-slot fp16 table + fp32 master, d=256, row-wise Adagrad",
+            "unique_rows": U, "ms": ms, "fetches_per_s": P / (ms * 1e-3),
+            "hbm": {"algorithmic_bytes": alg, "achieved_GBs": alg / (ms * 1e-3) / 1e9,
+                    "frac": alg / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS}}
+
+
+def train_step_bench(torch, iters):
+    """Forward + backward of the text-study layer in training (8,192 tokens,
+    262,144 fp16 slots, H=4, d_key=256, k=16, balance coefficient 0.01,
+    sparse value gradient through a probe) followed by the sparse row update
+    (merge, clip, row-wise Adagrad on the fp32 master)."""
+    from model_amd import rows as R
+    from model_amd.memory import MemoryPool
+
+    M, H, n, d_key, d, k = 8192, 4, 512, 256, 256, 16
+    dev = "cuda"
+    pool = MemoryPool(n, H, d_key, d, k, values_dtype=torch.float16)
+    g = torch.Generator(device=dev).manual_seed(0)
+    keys = (torch.randn((H, 2, n, d_key // 2), generator=g, device=dev) * (d_key // 2) ** -0.5).requires_grad_(True)
+    values = torch.empty((n * n, d), dtype=torch.float16, device=dev).normal_(0.0, 0.02, generator=g)
+    log_t = torch.tensor(math.log(10.0), device=dev, requires_grad=True)
+    params = {"sub_keys": keys, "values": values, "log_temperature": log_t}
+    hidden = torch.randn((M, 256), generator=g, device=dev)
+    lim = math.sqrt(6.0 / (256 + H * d_key))
+    w_q = ((torch.rand((256, H * d_key), generator=g, device=dev) * 2 - 1) * lim).requires_grad_(True)
+    g_out = torch.randn((M, d), generator=g, device=dev) * 1e-3
+    upd = R.SparseRowUpdate(values, lr=1e-3, pool_lr_mult=3.0, warmup_steps=0, steps=1000, grad_clip=1.0)
+
+    def step():
+        q = (hidden @ w_q).reshape(M, H, d_key)
+        probe = torch.zeros((M, d), device=dev, requires_grad=True)
+        out, aux = pool.apply({"params": params}, q, train=False, sparse_grad=True)
+        loss = ((out + probe) * g_out).sum() + 0.01 * aux["balance_loss"]
+        gw, gk, gt, gp = torch.autograd.grad(loss, [w_q, keys, log_t, probe])
+        rest = (gw.square().sum() + gk.square().sum() + gt.square()).reshape(1)
+        upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: gp}, [0], rest_sq=rest)
+
+    for _ in range(3):
+        step()
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(iters):
+        step()
+    b.record()
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / iters
+    return {"workload": "training step of the text-study layer: 8,192 tokens, 262,144 fp16 slots + fp32 master, "
+                        "forward + backward (queries through a 256->1024 projection, sub-keys, log-temperature, "
+                        "balance loss 0.01, probe gradient) + sparse row-wise Adagrad",
+            "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events"}
+
+
 def cpu_baseline(seconds: float):
     """The numpy oracle (oracle/lookup.py) on the host cores: the same layer
     shape (262,144 fp16 slots, H=4, d_key=256, k=16) on batches of 1,024
@@ -285,6 +402,11 @@ def main():
         large = {"workload": "decode lookup, 67,108,864 fp16 slots (34 GB), H=4, d_key=256, k=16, d_value=256",
                  "by_tokens": sweep}
 
+    train = None
+    if not args.no_train:
+        train = {"train_step": train_step_bench(torch, max(5, args.steps // 20)),
+                 "sparse_update_zipf": sparse_update_bench(torch, max(10, args.steps // 10))}
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -306,6 +428,7 @@ def main():
         "roofline": roof,
         "kernels": br,
         "pool_67M": large,
+        "training_262k": train,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

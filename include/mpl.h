@@ -122,10 +122,13 @@ int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fe
  * train.py:395-397: gnorm = sqrt(rest_sq + sum(row_sq)) and
  * scale = min(1, grad_clip / (gnorm + 1e-6)); scale_gnorm[0] = scale,
  * scale_gnorm[1] = gnorm (device memory).  rest_sq (device, may be NULL = 0)
- * is the squared global norm of the dense gradients.
+ * is the squared global norm of the dense gradients.  The sum is taken in a
+ * fixed order in fp64 (two stages, workspace of
+ * mpl_clip_scale_workspace_bytes()).
  */
+size_t mpl_clip_scale_workspace_bytes(void);
 int mpl_clip_scale(const float* row_sq, int64_t cap, const float* rest_sq, float grad_clip,
-                   float* scale_gnorm, void* stream);
+                   float* scale_gnorm, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * train.py:412-416 (row-wise Adagrad, in place): for each u < cap with

@@ -187,17 +187,38 @@ __global__ __launch_bounds__(kBwdThreads) void queries_bwd_kernel(
   const float scale = T * ql;
   float dy[2] = {0.f, 0.f};
   float dlen = 0.f;
-  for (int i = 0; i < k; ++i) {
-    const float g = d_sub[row * k + i];
-    const int key = sub_idx[row * k + i];
-    const float* kr = k_hat + ((int64_t)hc * n + (key >= 0 && key < n ? key : 0)) * half;
-    const float gs = (key >= 0 && key < n) ? g * scale : 0.f;
+  // lane i < k holds entry i of the row; entries are broadcast in batches of
+  // eight so that sixteen key-row loads per lane are in flight
+  const int li = lane < k ? lane : 0;
+  const int key_l = sub_idx[row * k + li];
+  const float g_l = d_sub[row * k + li];
+  const float s_l = q_len != nullptr ? sub_scores[row * k + li] : 0.f;
+  if (q_len != nullptr) {
+    float t = lane < k ? g_l * (s_l / ql) : 0.f;  // cos * T
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int c = lane + kWave * t;
-      if (c < half) dy[t] = fmaf(gs, kr[c], dy[t]);
+    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+    dlen = t;
+  }
+  for (int i0 = 0; i0 < k; i0 += 8) {
+    float kv[8][2], gs[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int i = i0 + b < k ? i0 + b : 0;
+      const int key = __shfl(key_l, i);
+      const float g = __shfl(g_l, i);
+      const bool ok = i0 + b < k && key >= 0 && key < n;
+      gs[b] = ok ? g * scale : 0.f;
+      const float* kr = k_hat + ((int64_t)hc * n + (ok ? key : 0)) * half;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int c = lane + kWave * t;
+        kv[b][t] = kr[c < half ? c : 0];
+      }
     }
-    if (q_len != nullptr) dlen = fmaf(g, sub_scores[row * k + i] / ql, dlen);  // cos * T
+#pragma unroll
+    for (int b = 0; b < 8; ++b)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) dy[t] = fmaf(gs[b], kv[b][t], dy[t]);
   }
   if (q_len != nullptr && dlen_extra != nullptr) dlen += dlen_extra[row];
   float x[2], xdy = 0.f, ss = 0.f;

@@ -24,6 +24,8 @@
 // many waves without changing the summation order from run to run.
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace mpl {
@@ -94,19 +96,66 @@ __global__ __launch_bounds__(1024) void scan_exclusive_kernel(uint32_t* __restri
   if (tid == 1023 && total != nullptr) *total = part[1023];
 }
 
+// Exclusive scan of each digit's row hist[digit][0, ntiles) (one workgroup
+// per digit, chunks of 1024 tiles); the digit's total goes to totals[digit].
+__global__ __launch_bounds__(1024) void digit_scan_kernel(uint32_t* __restrict__ hist, int64_t ntiles,
+                                                          uint32_t* __restrict__ totals) {
+  __shared__ uint32_t wsum[1024 / kWave];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  uint32_t* row = hist + (int64_t)blockIdx.x * ntiles;
+  uint32_t carry = 0;
+  for (int64_t c0 = 0; c0 < ntiles; c0 += 1024) {
+    const int64_t i = c0 + tid;
+    const uint32_t v = i < ntiles ? row[i] : 0u;
+    uint32_t x = v;  // inclusive scan within the wave
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t y = __shfl_up(x, off);
+      if (lane >= off) x += y;
+    }
+    if (lane == kWave - 1) wsum[wave] = x;
+    __syncthreads();
+    uint32_t before = carry;
+    for (int w = 0; w < wave; ++w) before += wsum[w];
+    uint32_t chunk = 0;
+    for (int w = 0; w < 1024 / kWave; ++w) chunk += wsum[w];
+    if (i < ntiles) row[i] = before + x - v;
+    carry += chunk;
+    __syncthreads();
+  }
+  if (tid == 0) totals[blockIdx.x] = carry;
+}
+
 // Stable scatter of one radix pass.  vals_in == null means the identity
-// (values = input positions).
+// (values = input positions).  hist_scan holds each digit's scan over tiles;
+// the digits' starting offsets are the scan of `totals`, done here in LDS.
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
-    uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist_scan, int64_t ntiles) {
+    uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist_scan, int64_t ntiles,
+    const uint32_t* __restrict__ totals) {
   __shared__ uint32_t tile_off[256];
   __shared__ uint32_t seen[256];  // keys of each digit in earlier rounds of this tile
   __shared__ uint32_t wave_cnt[kSortThreads / kWave][256];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  tile_off[tid] = hist_scan[(int64_t)tid * ntiles + blockIdx.x];
-  seen[tid] = 0;
+  {  // digit base = exclusive scan of the digit totals
+    const uint32_t t = totals[tid];
+    uint32_t x = t;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+      const uint32_t y = __shfl_up(x, off);
+      if (lane >= off) x += y;
+    }
+    if (lane == kWave - 1) wave_cnt[0][wave] = x;
+    __syncthreads();
+    uint32_t before = 0;
+    for (int w = 0; w < wave; ++w) before += wave_cnt[0][w];
+    tile_off[tid] = before + x - t + hist_scan[(int64_t)tid * ntiles + blockIdx.x];
+    seen[tid] = 0;
+    __syncthreads();
+  }
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = base + r * kSortThreads + tid;
@@ -356,15 +405,25 @@ __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* _
     const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
     if (ra == rb) return;  // finished by seg_reduce_kernel
     const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
-    for (int64_t r = ra; r <= rb; ++r) {
-      const int slot = r == ra ? slot_a : 0;
+    // hot rows span hundreds of ranges: eight partial rows in flight, added
+    // in range order
+    for (int64_t r0 = ra; r0 <= rb; r0 += 8) {
+      RowVec<W> p[8][VPL];
 #pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const int c = lane + kWave * v;
-        RowVec<W> p;
-        p.load(partial, (r * 2 + slot) * nv + c, c < nv);
-        acc[v].add(p);
+      for (int b = 0; b < 8; ++b) {
+        const int64_t r = r0 + b <= rb ? r0 + b : rb;
+        const int slot = r == ra ? slot_a : 0;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          const int c = lane + kWave * v;
+          p[b][v].load(partial, (r * 2 + slot) * nv + c, c < nv);
+        }
       }
+#pragma unroll
+      for (int b = 0; b < 8; ++b)
+        if (r0 + b <= rb)
+#pragma unroll
+          for (int v = 0; v < VPL; ++v) acc[v].add(p[b][v]);
     }
   } else if (lane == 0) {
     uniq[u] = (int32_t)pool_size;
@@ -390,21 +449,39 @@ __global__ void store_zero_kernel(int32_t* p) { *p = 0; }
 // ---------------------------------------------------------- global norm
 // train.py:395-396 over the rows: sum of row_sq in a fixed order (fp64), then
 // gnorm = sqrt(rest + sum) and scale = min(1, clip / (gnorm + 1e-6)).
-__global__ __launch_bounds__(1024) void clip_scale_kernel(const float* __restrict__ row_sq, int64_t cap,
-                                                          const float* __restrict__ rest_sq, float clip,
-                                                          float* __restrict__ out) {
-  __shared__ double part[1024];
+// Stage 1: block b sums the contiguous chunk b; stage 2 sums the chunks.
+constexpr int kSumBlocks = 256;
+
+__device__ __forceinline__ double block_sum_f64(double s, double* part) {
   const int tid = threadIdx.x;
-  double s = 0.0;
-  for (int64_t i = tid; i < cap; i += 1024) s += (double)row_sq[i];
   part[tid] = s;
   __syncthreads();
-  for (int off = 512; off >= 1; off >>= 1) {
+  for (int off = blockDim.x / 2; off >= 1; off >>= 1) {
     if (tid < off) part[tid] += part[tid + off];
     __syncthreads();
   }
-  if (tid == 0) {
-    const double total = part[0] + (rest_sq != nullptr ? (double)*rest_sq : 0.0);
+  return part[0];
+}
+
+__global__ __launch_bounds__(256) void sum_chunks_kernel(const float* __restrict__ x, int64_t n,
+                                                         double* __restrict__ chunk_sums) {
+  __shared__ double part[256];
+  const int64_t per = cdiv(n, kSumBlocks);
+  const int64_t b0 = (int64_t)blockIdx.x * per;
+  const int64_t b1 = b0 + per < n ? b0 + per : n;
+  double s = 0.0;
+  for (int64_t i = b0 + threadIdx.x; i < b1; i += 256) s += (double)x[i];
+  const double t = block_sum_f64(s, part);
+  if (threadIdx.x == 0) chunk_sums[blockIdx.x] = t;
+}
+
+__global__ __launch_bounds__(256) void clip_finish_kernel(const double* __restrict__ chunk_sums,
+                                                          const float* __restrict__ rest_sq, float clip,
+                                                          float* __restrict__ out) {
+  __shared__ double part[256];
+  const double t = block_sum_f64(chunk_sums[threadIdx.x], part);
+  if (threadIdx.x == 0) {
+    const double total = t + (rest_sq != nullptr ? (double)*rest_sq : 0.0);
     const float gnorm = (float)sqrt(total);
     out[0] = fminf(1.f, clip / (gnorm + 1e-6f));
     out[1] = gnorm;
@@ -412,77 +489,128 @@ __global__ __launch_bounds__(1024) void clip_scale_kernel(const float* __restric
 }
 
 // ---------------------------------------------------------- optimizers
-template <typename V>
-__device__ __forceinline__ float load_val(const V* p) { return (float)*p; }
-template <typename V>
-__device__ __forceinline__ void store_val(V* p, float x) { *p = (V)x; }
+// One wave per row, grid-stride over the cap rows (a fixed grid: most of the
+// cap rows are padding when routing is skewed).  A row of d elements is nv
+// vectors of W (4 when d % 4 == 0, else 1); lane l owns vectors l, l+64, ...
+constexpr int kOptBlocks = 1024;
 
-// train.py:412-416.  One wave per row; padding (slot outside [0, N)) dropped.
+template <typename V, int W>
+struct TableVec;
+template <>
+struct TableVec<float, 4> {
+  __device__ static void load(const float* p, float* x) {
+    const float4 f = *(const float4*)p;
+    x[0] = f.x; x[1] = f.y; x[2] = f.z; x[3] = f.w;
+  }
+  __device__ static void store(float* p, const float* x) { *(float4*)p = make_float4(x[0], x[1], x[2], x[3]); }
+};
+template <>
+struct TableVec<_Float16, 4> {
+  typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+  __device__ static void load(const _Float16* p, float* x) {
+    const h4 h = *(const h4*)p;
+    x[0] = (float)h[0]; x[1] = (float)h[1]; x[2] = (float)h[2]; x[3] = (float)h[3];
+  }
+  __device__ static void store(_Float16* p, const float* x) {
+    h4 h;
+    h[0] = (_Float16)x[0]; h[1] = (_Float16)x[1]; h[2] = (_Float16)x[2]; h[3] = (_Float16)x[3];
+    *(h4*)p = h;
+  }
+};
 template <typename V>
+struct TableVec<V, 1> {
+  __device__ static void load(const V* p, float* x) { x[0] = (float)*p; }
+  __device__ static void store(V* p, const float* x) { *p = (V)x[0]; }
+};
+
+template <typename V, int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict__ values, float* __restrict__ master,
                                                                    float* __restrict__ acc,
                                                                    const int32_t* __restrict__ uniq,
                                                                    const float* __restrict__ rows, int64_t cap, int d,
                                                                    int64_t N, float lr,
                                                                    const float* __restrict__ grad_scale) {
-  const int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
-  if (u >= cap) return;
-  const int64_t s = uniq[u];
-  if (s < 0 || s >= N) return;
+  const int64_t nw = (int64_t)gridDim.x * (kRowThreads / kWave);
+  const int nv = d / W;
   const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
-  float sq = 0.f;
-  for (int c = lane; c < d; c += kWave) {
-    const float g = rows[u * d + c] * sc;
-    sq += g * g;
-  }
+  for (int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6; u < cap; u += nw) {
+    const int64_t s = uniq[u];
+    if (s < 0 || s >= N) continue;  // padding (mode="drop")
+    float g[VPL][W];
+    float sq = 0.f;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
-  const float a = acc[s] + sq / (float)d;
-  const float step = lr / (sqrtf(a) + 1e-8f);
-  for (int c = lane; c < d; c += kWave) {
-    const float upd = -step * (rows[u * d + c] * sc);
-    const int64_t o = s * d + c;
-    if (master != nullptr) {
-      const float m = master[o] + upd;
-      master[o] = m;
-      store_val(values + o, m);
-    } else {
-      store_val(values + o, load_val(values + o) + upd);
+    for (int v = 0; v < VPL; ++v) {
+      const int c = lane + kWave * v;
+      if (c < nv) {
+        TableVec<float, W>::load(rows + u * d + (int64_t)c * W, g[v]);
+#pragma unroll
+        for (int i = 0; i < W; ++i) {
+          g[v][i] *= sc;
+          sq += g[v][i] * g[v][i];
+        }
+      }
     }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+    const float a = acc[s] + sq / (float)d;
+    const float step = lr / (sqrtf(a) + 1e-8f);
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int c = lane + kWave * v;
+      if (c < nv) {
+        const int64_t o = s * d + (int64_t)c * W;
+        float x[W];
+        if (master != nullptr) TableVec<float, W>::load(master + o, x);
+        else TableVec<V, W>::load(values + o, x);
+#pragma unroll
+        for (int i = 0; i < W; ++i) x[i] += -step * g[v][i];
+        if (master != nullptr) TableVec<float, W>::store(master + o, x);
+        TableVec<V, W>::store(values + o, x);
+      }
+    }
+    if (lane == 0) acc[s] = a;
   }
-  if (lane == 0) acc[s] = a;
 }
 
 // train.py:417-426 (c1 = 1 - b1^n, c2 = 1 - b2^n with n = step + 1).
-template <typename V>
+template <typename V, int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ values, float* __restrict__ master,
                                                                 float* __restrict__ m1, float* __restrict__ m2,
                                                                 const int32_t* __restrict__ uniq,
                                                                 const float* __restrict__ rows, int64_t cap, int d,
                                                                 int64_t N, float lr, float c1, float c2,
                                                                 const float* __restrict__ grad_scale) {
-  const int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
-  if (u >= cap) return;
-  const int64_t s = uniq[u];
-  if (s < 0 || s >= N) return;
+  const int64_t nw = (int64_t)gridDim.x * (kRowThreads / kWave);
+  const int nv = d / W;
   const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
   const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
-  for (int c = lane; c < d; c += kWave) {
-    const int64_t o = s * d + c;
-    const float g = rows[u * d + c] * sc;
-    const float m = b1 * m1[o] + (1.f - b1) * g;
-    const float v = b2 * m2[o] + (1.f - b2) * g * g;
-    const float upd = -lr * (m / c1) / (sqrtf(v / c2) + eps);
-    m1[o] = m;
-    m2[o] = v;
-    if (master != nullptr) {
-      const float x = master[o] + upd;
-      master[o] = x;
-      store_val(values + o, x);
-    } else {
-      store_val(values + o, load_val(values + o) + upd);
+  for (int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6; u < cap; u += nw) {
+    const int64_t s = uniq[u];
+    if (s < 0 || s >= N) continue;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int c = lane + kWave * v;
+      if (c >= nv) continue;
+      const int64_t o = s * d + (int64_t)c * W;
+      float g[W], m[W], q[W], x[W];
+      TableVec<float, W>::load(rows + u * d + (int64_t)c * W, g);
+      TableVec<float, W>::load(m1 + o, m);
+      TableVec<float, W>::load(m2 + o, q);
+      if (master != nullptr) TableVec<float, W>::load(master + o, x);
+      else TableVec<V, W>::load(values + o, x);
+#pragma unroll
+      for (int i = 0; i < W; ++i) {
+        const float gi = g[i] * sc;
+        m[i] = b1 * m[i] + (1.f - b1) * gi;
+        q[i] = b2 * q[i] + (1.f - b2) * gi * gi;
+        x[i] += -lr * (m[i] / c1) / (sqrtf(q[i] / c2) + eps);
+      }
+      TableVec<float, W>::store(m1 + o, m);
+      TableVec<float, W>::store(m2 + o, q);
+      if (master != nullptr) TableVec<float, W>::store(master + o, x);
+      TableVec<V, W>::store(values + o, x);
     }
   }
 }
@@ -491,7 +619,7 @@ __global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ v
 struct MergeLayout {
   int64_t ntiles, nranges, cap;
   int passes;
-  size_t keys[2], vals[2], hist, tile_cnt, counters, seg_start, seg_of, partial, total;
+  size_t keys[2], vals[2], hist, tile_cnt, counters, totals, seg_start, seg_of, partial, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -518,6 +646,8 @@ static MergeLayout merge_layout(int64_t P, int d, int64_t pool_size) {
   o += align256((size_t)L.ntiles * 4);
   L.counters = o;  // [0]: segment count
   o += 256;
+  L.totals = o;  // digit totals of a radix pass
+  o += 1024;
   L.seg_start = o;
   o += align256((size_t)(L.cap + 1) * 4);
   L.seg_of = o;
@@ -593,6 +723,7 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   uint32_t* hist = (uint32_t*)(ws + L.hist);
   uint32_t* tile_cnt = (uint32_t*)(ws + L.tile_cnt);
   uint32_t* nseg = (uint32_t*)(ws + L.counters);
+  uint32_t* totals = (uint32_t*)(ws + L.totals);
   int32_t* seg_start = (int32_t*)(ws + L.seg_start);
   int32_t* seg_of = (int32_t*)(ws + L.seg_of);
   float* partial = (float*)(ws + L.partial);
@@ -604,8 +735,9 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   for (int pass = 0; pass < L.passes; ++pass) {
     const int shift = 8 * pass;
     radix_hist_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);
-    scan_exclusive_kernel<<<1, 1024, 0, s>>>(hist, 256 * L.ntiles, nullptr);
-    radix_scatter_kernel<<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles);
+    digit_scan_kernel<<<256, 1024, 0, s>>>(hist, L.ntiles, totals);
+    radix_scatter_kernel<<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles,
+                                                     totals);
     kin = keys[cur];
     vin = vals[cur];
     cur ^= 1;
@@ -625,12 +757,18 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   return check_launch("mpl_merge_rows(reduce)");
 }
 
+extern "C" size_t mpl_clip_scale_workspace_bytes() { return kSumBlocks * sizeof(double); }
+
 extern "C" int mpl_clip_scale(const float* row_sq, int64_t cap, const float* rest_sq, float grad_clip,
-                              float* scale_gnorm, void* stream) {
+                              float* scale_gnorm, void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   MPL_REQUIRE(cap >= 0 && scale_gnorm != nullptr && (cap == 0 || row_sq != nullptr), MPL_EINVAL,
               "mpl_clip_scale: bad arguments");
-  clip_scale_kernel<<<1, 1024, 0, (hipStream_t)stream>>>(row_sq, cap, rest_sq, grad_clip, scale_gnorm);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= kSumBlocks * sizeof(double), MPL_EWORKSPACE,
+              "mpl_clip_scale: workspace of %zu bytes needed", (size_t)kSumBlocks * sizeof(double));
+  hipStream_t s = (hipStream_t)stream;
+  sum_chunks_kernel<<<kSumBlocks, 256, 0, s>>>(row_sq, cap, (double*)workspace);
+  clip_finish_kernel<<<1, 256, 0, s>>>((const double*)workspace, rest_sq, grad_clip, scale_gnorm);
   return check_launch("mpl_clip_scale");
 }
 
@@ -643,14 +781,26 @@ extern "C" int mpl_row_adagrad(void* values, int values_dtype, float* master, fl
               "mpl_row_adagrad: values_dtype must be MPL_F16 or MPL_F32");
   if (cap == 0) return MPL_OK;
   MPL_REQUIRE(values && acc && uniq && rows, MPL_EINVAL, "mpl_row_adagrad: null buffer");
-  const unsigned b = (unsigned)cdiv(cap, kRowThreads / kWave);
+  const unsigned b = (unsigned)std::min<int64_t>(kOptBlocks, cdiv(cap, kRowThreads / kWave));
   hipStream_t s = (hipStream_t)stream;
-  if (values_dtype == MPL_F16)
-    row_adagrad_kernel<_Float16><<<b, kRowThreads, 0, s>>>((_Float16*)values, master, acc, uniq, rows, cap, d,
-                                                           pool_size, lr, grad_scale);
-  else
-    row_adagrad_kernel<float><<<b, kRowThreads, 0, s>>>((float*)values, master, acc, uniq, rows, cap, d, pool_size,
-                                                        lr, grad_scale);
+  const bool vec = d % 4 == 0;
+  const int nv = vec ? d / 4 : d;
+  const int vpl = (int)cdiv(nv, kWave);
+  MPL_REQUIRE(vpl <= 16, MPL_EUNSUPPORTED, "mpl_row_adagrad: d must be <= 1024");
+#define MPL_AG(V, W, P)                                                                                         \
+  row_adagrad_kernel<V, W, P><<<b, kRowThreads, 0, s>>>((V*)values, master, acc, uniq, rows, cap, d, pool_size, \
+                                                        lr, grad_scale)
+#define MPL_AG_V(V, W)                     \
+  if (vpl <= 1) MPL_AG(V, W, 1);           \
+  else if (vpl <= 4) MPL_AG(V, W, 4);      \
+  else MPL_AG(V, W, 16);
+  if (values_dtype == MPL_F16) {
+    if (vec) { MPL_AG_V(_Float16, 4) } else { MPL_AG_V(_Float16, 1) }
+  } else {
+    if (vec) { MPL_AG_V(float, 4) } else { MPL_AG_V(float, 1) }
+  }
+#undef MPL_AG_V
+#undef MPL_AG
   return check_launch("mpl_row_adagrad");
 }
 
@@ -666,13 +816,25 @@ extern "C" int mpl_row_adam(void* values, int values_dtype, float* master, float
   const float n = (float)(step + 1);
   const float c1 = 1.f - powf(0.9f, n);
   const float c2 = 1.f - powf(0.999f, n);
-  const unsigned b = (unsigned)cdiv(cap, kRowThreads / kWave);
+  const unsigned b = (unsigned)std::min<int64_t>(kOptBlocks, cdiv(cap, kRowThreads / kWave));
   hipStream_t s = (hipStream_t)stream;
-  if (values_dtype == MPL_F16)
-    row_adam_kernel<_Float16><<<b, kRowThreads, 0, s>>>((_Float16*)values, master, m, v, uniq, rows, cap, d,
-                                                        pool_size, lr, c1, c2, grad_scale);
-  else
-    row_adam_kernel<float><<<b, kRowThreads, 0, s>>>((float*)values, master, m, v, uniq, rows, cap, d, pool_size, lr,
-                                                     c1, c2, grad_scale);
+  const bool vec = d % 4 == 0;
+  const int nv = vec ? d / 4 : d;
+  const int vpl = (int)cdiv(nv, kWave);
+  MPL_REQUIRE(vpl <= 16, MPL_EUNSUPPORTED, "mpl_row_adam: d must be <= 1024");
+#define MPL_AD(V, W, P)                                                                                           \
+  row_adam_kernel<V, W, P><<<b, kRowThreads, 0, s>>>((V*)values, master, m, v, uniq, rows, cap, d, pool_size, lr, \
+                                                     c1, c2, grad_scale)
+#define MPL_AD_V(V, W)                     \
+  if (vpl <= 1) MPL_AD(V, W, 1);           \
+  else if (vpl <= 4) MPL_AD(V, W, 4);      \
+  else MPL_AD(V, W, 16);
+  if (values_dtype == MPL_F16) {
+    if (vec) { MPL_AD_V(_Float16, 4) } else { MPL_AD_V(_Float16, 1) }
+  } else {
+    if (vec) { MPL_AD_V(float, 4) } else { MPL_AD_V(float, 1) }
+  }
+#undef MPL_AD_V
+#undef MPL_AD
   return check_launch("mpl_row_adam");
 }

@@ -114,8 +114,11 @@ def clip_scale(row_sq: torch.Tensor, rest_sq: Optional[torch.Tensor], grad_clip:
     out = torch.empty(2, dtype=torch.float32, device=dev)
     if rest_sq is not None:
         rest_sq = rest_sq.reshape(1).float().contiguous()
-    check(_lib.lib().mpl_clip_scale(ptr(row_sq.contiguous()), row_sq.shape[0], ptr(rest_sq), float(grad_clip),
-                                    ptr(out), _lib.stream_ptr(dev)), "mpl_clip_scale")
+    L = _lib.lib()
+    wsb = L.mpl_clip_scale_workspace_bytes()
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    check(L.mpl_clip_scale(ptr(row_sq.contiguous()), row_sq.shape[0], ptr(rest_sq), float(grad_clip), ptr(out),
+                           ptr(ws), wsb, _lib.stream_ptr(dev)), "mpl_clip_scale")
     return out
 
 

@@ -69,5 +69,6 @@ def test_row_entry_points_validate_before_launch():
     assert rc == 1 and b"values_dtype" in L.mpl_last_error()
     rc = L.mpl_row_adam(None, _lib.MPL_F16, None, None, None, None, None, 10, 8, N, 0.1, -1, None, None)
     assert rc == 1
-    rc = L.mpl_clip_scale(None, 10, None, 1.0, None, None)
+    assert L.mpl_clip_scale_workspace_bytes() >= 8
+    rc = L.mpl_clip_scale(None, 10, None, 1.0, None, None, 0, None)
     assert rc == 1
