@@ -360,7 +360,7 @@ def main():
     args = parse()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(see DESIGN.md for how the lookup would shard).", file=sys.stderr)
+              "(the lookup shards over tokens; one GPU is what is built and measured).", file=sys.stderr)
         sys.exit(2)
     import torch
 

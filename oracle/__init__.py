@@ -5,7 +5,7 @@ memory-layer lookup (KumarDev7/model ``memory_pool_model/memory.py``) and of
 its sparse backward / row optimizer (``memory_pool_model/train.py``).  Every
 function cites the reference file:line it follows.
 
-It is the *checker*, never the product: only ``tests/``,
+It is a test oracle, never the product: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 it.  The product path (``model_amd``) never imports it and fails loudly when
 its HIP library is missing.

@@ -9,7 +9,7 @@ Follows KumarDev7/model ``memory_pool_model/memory.py``:
   * ``aux_stats``      memory.py:196-226
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
-this module, and only as the checker.
+this module, and only to check results.
 """
 
 from __future__ import annotations

@@ -14,7 +14,7 @@ def pytest_configure(config):
 
 @pytest.fixture(scope="session")
 def gpu_lib():
-    """The built C-ABI library, loaded on a GPU box.  Fails (does not skip)
+    """The built C-ABI library, loaded on a machine with a GPU.  Fails (does not skip)
     when the library is missing: the product path has no fallback."""
     import torch
 

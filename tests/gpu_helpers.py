@@ -10,7 +10,7 @@ import torch
 from model_amd.memory import MemoryPool
 from oracle import lookup as ol
 
-TOL = {torch.float16: 1e-2, torch.float32: 1e-5}  # north_star: fp16 / fp32 relative
+TOL = {torch.float16: 1e-2, torch.float32: 1e-5}  # parity tolerance: fp16 / fp32 paths, relative
 
 
 def make_params(pool: MemoryPool, seed: int, *, key_std=None, value_std=None, device="cuda"):

@@ -4,7 +4,7 @@ itself pinned by torch autograd in tests/test_oracle.py.
 
 loss = <g_out, out> + g_bal * balance_loss; gradients w.r.t. the raw
 queries, raw sub_keys, log_temperature and (sparse_grad=False) the values.
-Tolerance (north_star): 1e-5 relative for fp32 paths, 1e-2 for fp16 paths,
+Tolerance: 1e-5 relative for fp32 paths, 1e-2 for fp16 paths,
 relative to the largest magnitude of each gradient."""
 
 import numpy as np

@@ -1,5 +1,5 @@
 """GPU parity of the forward lookup (libmpl.so through the C ABI) against the
-oracle: tiny reference shapes, the BASELINE workloads' shapes, ties, noise,
+oracle: tiny reference shapes, the benchmark workloads' shapes, ties, noise,
 query_scale, shuffle_reads, ragged token counts and split-key plans."""
 
 import numpy as np
