@@ -45,8 +45,16 @@
 
 namespace mpl {
 
-constexpr int kCand = 24;           // per-lane candidate buffer (entries)
-constexpr int kScoreThreads = 128;  // two waves per workgroup, 64 queries each
+#ifndef MPL_CAND
+#define MPL_CAND 24
+#endif
+constexpr int kCand = MPL_CAND;  // per-lane candidate buffer (entries)
+#ifndef MPL_SCORE_THREADS
+#define MPL_SCORE_THREADS 128
+#endif
+constexpr int kScoreThreads = MPL_SCORE_THREADS;  // waves per workgroup x 64
+constexpr int kQueriesPerWave = 32;
+constexpr int kQueriesPerGroup = kQueriesPerWave * (kScoreThreads / 64);
 constexpr int kMaxSplits = 64;
 
 struct ScoreParams {
@@ -185,36 +193,34 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   constexpr int TILE = VPL * kWave;                      // uint4 per key block
   constexpr int PRE = (TILE + kScoreThreads - 1) / kScoreThreads;
   constexpr int TILE_ALLOC = PRE * kScoreThreads;  // >= TILE: every thread stores unguarded
+  constexpr int WAVES = kScoreThreads / kWave;
   typedef typename Mfma<T>::Op Op;
 
   __shared__ uint4 tiles[2][TILE_ALLOC];
-  __shared__ uint2 cbuf[2][kCand][kWave];
-  __shared__ float cpay[NOISE ? 2 : 1][NOISE ? kCand : 1][kWave];
+  __shared__ uint2 cbuf[WAVES][kCand][kWave];
+  __shared__ float cpay[NOISE ? WAVES : 1][NOISE ? kCand : 1][kWave];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
+  const int par = lane >> 5;  // key parity class of this lane
   const int hc = blockIdx.x % p.HC;
   const int split = (blockIdx.x / p.HC) % p.splits;
   const int64_t qb = blockIdx.x / (p.HC * p.splits);
-  const int64_t q0 = qb * kScoreThreads + wave * kWave;
+  const int64_t q0 = qb * kQueriesPerGroup + wave * kQueriesPerWave;
   const int b_begin = split * p.blk_per_split;
   const int b_end = min(p.nblk, b_begin + p.blk_per_split);
 
-  // B operands: set s holds queries q0 + 32*s + (lane % 32).
-  Op qop[2][NCH];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    const int64_t qi = q0 + 32 * s + (lane & 31);
-    const bool ok = qi < p.M;
-    const T* qrow = (const T*)p.q_hat + (ok ? (qi * p.HC + hc) * (int64_t)p.half : 0);
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) qop[s][c] = Mfma<T>::load_q(qrow, ok, p.half, c, lane);
-  }
-
-  // After the half swap lane l owns query q0 + l.
-  const int64_t my_q = q0 + lane;
+  // Lanes l and l+32 own query q0 + l%32: the B operand holds that query, and
+  // of each key block lane l scores keys 8*(r/4) + 4*par + r%4 (r < 16).
+  const int64_t my_q = q0 + (lane & 31);
   const bool valid = my_q < p.M;
+  Op qop[NCH];
+  {
+    const T* qrow = (const T*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::load_q(qrow, valid, p.half, c, lane);
+  }
   const float ql = p.q_len != nullptr ? p.q_len[(valid ? my_q : 0) * p.HC + hc] : 1.f;
   const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
   uint2(*mybuf)[kWave] = cbuf[wave];
@@ -227,7 +233,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   // serialise them.  (A vector type, not an array: a loop-carried array is
   // not promoted to registers.)
   typedef unsigned PreVec __attribute__((ext_vector_type(4 * PRE)));
-  typedef float GVec __attribute__((ext_vector_type(NOISE ? 32 : 1)));
+  typedef float GVec __attribute__((ext_vector_type(NOISE ? 16 : 1)));
   const uint4* kbase_ptr = p.packed + (int64_t)hc * p.nblk * TILE;
   auto fetch = [&](int blk) __attribute__((always_inline)) {
     PreVec v;
@@ -247,35 +253,29 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     for (int i = 0; i < PRE; ++i)
       tiles[buf][tid + i * kScoreThreads] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   };
+  // The lane's 16 noise values of block blk (keys 8*(r/4) + 4*par + r%4).
   auto fetch_noise = [&](int blk) __attribute__((always_inline)) {
     GVec g;
     if (NOISE) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) g[NOISE ? i : 0] = grow[min(blk * 32 + i, p.n - 1)];
+      for (int r = 0; r < 16; ++r)
+        g[NOISE ? r : 0] = grow[min(blk * 32 + 8 * (r >> 2) + 4 * par + (r & 3), p.n - 1)];
     }
     return g;
   };
-  // Both 32x32 score tiles of one key block: c0[r] = query q0 + lane%32,
-  // c1[r] = query q0 + 32 + lane%32, both against key 8*(r/4) + 4*(lane/32)
-  // + r%4 of the block.
-  auto mma_block = [&](int buf, f32x16& c0, f32x16& c1) __attribute__((always_inline)) {
-    c0 = f32x16{};
-    c1 = f32x16{};
+  // The 32-key x 32-query score tile of one key block: c[r] = query
+  // q0 + lane%32 against key 8*(r/4) + 4*par + r%4.
+  auto mma_block = [&](int buf, f32x16& c) __attribute__((always_inline)) {
+    c = f32x16{};
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
       const uint4 u = tiles[buf][v * kWave + lane];
 #pragma unroll
-      for (int e = 0; e < OPV; ++e) {
-        const Op a = Mfma<T>::from_vec(u, e);
-        c0 = Mfma<T>::mma(a, qop[0][v * OPV + e], c0);
-        c1 = Mfma<T>::mma(a, qop[1][v * OPV + e], c1);
-      }
+      for (int e = 0; e < OPV; ++e) c = Mfma<T>::mma(Mfma<T>::from_vec(u, e), qop[v * OPV + e], c);
     }
   };
   // One sweep over key blocks [bb, be), software-pipelined: while the VALU
   // runs body() on block j, the MFMAs of block j+1 are already in flight.
-  // body(kb, c0, c1, g) gets the raw cosine tiles of the block starting at key
-  // kb and, with noise, the lane's noise for those 32 keys.
   // LDS order per iteration j: reads of block j+1, then the store of block j+2
   // into block j's buffer, then one barrier.  Block j was read in iteration
   // j-1, before that iteration's barrier; block j+2 is read in iteration j+1,
@@ -290,127 +290,102 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     pre = fetch(min(bb + 2, be - 1));
     GVec gcur = fetch_noise(bb);
     __syncthreads();
-    f32x16 x0, x1, y0, y1;
-    mma_block(0, x0, x1);
+    f32x16 x, y;
+    mma_block(0, x);
     // The MFMAs of the next block are issued unconditionally (past the end
     // they score a clamped duplicate that nobody reads): a branch around them
-    // would make the accumulators a phi, which the compiler resolves by
-    // copying them right after the MFMAs, stalling on their results.
-    auto step = [&](int j, f32x16& c0, f32x16& c1, f32x16& d0, f32x16& d1) __attribute__((always_inline)) {
-      mma_block((j + 1) & 1, d0, d1);
+    // would make the accumulator a phi, which the compiler resolves by
+    // copying it right after the MFMAs, stalling on their results.
+    auto step = [&](int j, f32x16& c, f32x16& d) __attribute__((always_inline)) {
+      mma_block((j + 1) & 1, d);
       const GVec gnext = fetch_noise(min(bb + j + 1, be - 1));
-      if (j < nb) body((bb + j) * 32, c0, c1, gcur);
+      if (j < nb) body((bb + j) * 32, c, gcur);
       gcur = gnext;
       stage(j & 1, pre);  // past the end: clamped duplicates, never read
       pre = fetch(min(bb + j + 3, be - 1));
       __syncthreads();
     };
     for (int j = 0; j < nb; j += 2) {
-      step(j, x0, x1, y0, y1);
-      step(j + 1, y0, y1, x0, x1);
+      step(j, x, y);
+      step(j + 1, y, x);
     }
   };
 
-  // Lane-owned selection values of a block: after the half swap sa[r] is key
-  // kb + 8*(r/4) + r%4 and sb[r] key kb + 8*(r/4) + 4 + r%4 of query q0 + lane
-  // (padded keys -inf); with noise, ca/cb are the clean scores.
-  auto lane_scores = [&](int kb, const f32x16& c0, const f32x16& c1, const GVec& g, float* sa, float* sb,
-                         float* ca, float* cb) __attribute__((always_inline)) {
+  // Selection values of the lane's 16 keys of a block (padded keys -inf);
+  // with noise, cl holds the clean scores.
+  auto lane_scores = [&](int kb, const f32x16& c, const GVec& g, float* sv, float* cl)
+                         __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      sa[r] = c0[r];
-      sb[r] = c1[r];
-      half_swap(sa[r], sb[r]);
-    }
-    if (NOISE) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int o = 8 * (r >> 2) + (r & 3);
-        float v0 = sa[r] * p.T, v1 = sb[r] * p.T;
-        if (p.q_len != nullptr) {
-          v0 *= ql;
-          v1 *= ql;
-        }
-        ca[NOISE ? r : 0] = v0;
-        cb[NOISE ? r : 0] = v1;
-        sa[r] = __builtin_fmaf(p.noise_coef, g[NOISE ? o : 0], v0);
-        sb[r] = __builtin_fmaf(p.noise_coef, g[NOISE ? o + 4 : 0], v1);
+      float v = c[r];
+      if (NOISE) {
+        v = v * p.T;
+        if (p.q_len != nullptr) v *= ql;
+        cl[NOISE ? r : 0] = v;
+        v = __builtin_fmaf(p.noise_coef, g[NOISE ? r : 0], v);
       }
+      sv[r] = v;
     }
     if (kb + 32 > p.n) {  // wave-uniform: only the last block can hold padded keys
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int o = kb + 8 * (r >> 2) + (r & 3);
-        if (o >= p.n) sa[r] = -INFINITY;
-        if (o + 4 >= p.n) sb[r] = -INFINITY;
-      }
+      for (int r = 0; r < 16; ++r)
+        if (kb + 8 * (r >> 2) + 4 * par + (r & 3) >= p.n) sv[r] = -INFINITY;
     }
   };
 
   // Pass 1 over the first pass1_blocks blocks of the split: running maximum
-  // per (lane, register) position.  Each maximum is a distinct key's score,
-  // so the k-th largest of a lane's 32 maxima (after the half swap) is a
-  // lower bound on its query's k-th best score.  Without noise the maxima are
-  // taken on the raw tiles and swapped once at the end.
-  float ma[16], mb[16];
+  // per register position.  Each maximum is a distinct key's score, so the
+  // k-th largest of the 32 maxima of a lane pair (one query) is a lower bound
+  // on that query's k-th best score.
+  float ma[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) ma[r] = mb[r] = -INFINITY;
+  for (int r = 0; r < 16; ++r) ma[r] = -INFINITY;
   const int p1_end = min(b_end, b_begin + p.pass1_blocks);
-  sweep(b_begin, p1_end, [&](int kb, const f32x16& c0, const f32x16& c1, const GVec& g)
-                             __attribute__((always_inline)) {
+  sweep(b_begin, p1_end, [&](int kb, const f32x16& c, const GVec& g) __attribute__((always_inline)) {
     if (NOISE || kb + 32 > p.n) {
-      float sa[16], sb[16], ca[NOISE ? 16 : 1], cb[NOISE ? 16 : 1];
-      lane_scores(kb, c0, c1, g, sa, sb, ca, cb);
-      if (!NOISE) {  // back to the raw layout (the swap is an involution)
+      float sv[16], cl[NOISE ? 16 : 1];
+      lane_scores(kb, c, g, sv, cl);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) half_swap(sa[r], sb[r]);
-      }
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        ma[r] = fmaxf(ma[r], sa[r]);
-        mb[r] = fmaxf(mb[r], sb[r]);
-      }
+      for (int r = 0; r < 16; ++r) ma[r] = fmaxf(ma[r], sv[r]);
     } else {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        ma[r] = fmaxf(ma[r], c0[r]);
-        mb[r] = fmaxf(mb[r], c1[r]);
-      }
+      for (int r = 0; r < 16; ++r) ma[r] = fmaxf(ma[r], c[r]);
     }
   });
-  if (!NOISE) {
+  float mb[16];  // the partner lane's maxima
 #pragma unroll
-    for (int r = 0; r < 16; ++r) half_swap(ma[r], mb[r]);
+  for (int r = 0; r < 16; ++r) {
+    float a = ma[r], b = ma[r];
+    half_swap(a, b);  // lane < 32: (own, partner); lane >= 32: (partner, own)
+    mb[r] = par ? a : b;
   }
   // Scores >= bound pass: strict '>' against the next float below it.
   const float bound = kth_of_32(ma, mb, p.k);
   const float base_thr = bound == -INFINITY ? -INFINITY : from_orderable(orderable(bound) - 1u);
 
   // Pass 2 over the whole split: only candidates above the threshold are
-  // buffered (a wave-uniform branch skips an element no lane keeps) and
-  // merged into the sorted register list.
+  // buffered and merged into the lane's sorted register list.
   LaneSel<KMAX, NOISE> st;
   st.top.init();
   st.thr = valid ? base_thr : INFINITY;
   st.wp = &mybuf[0][lane];
   uint2* const flush_at = &mybuf[kCand - 8][lane];
-  sweep(b_begin, b_end, [&](int kb, const f32x16& c0, const f32x16& c1, const GVec& g)
-                            __attribute__((always_inline)) {
-    float sa[16], sb[16], ca[NOISE ? 16 : 1], cb[NOISE ? 16 : 1];
-    lane_scores(kb, c0, c1, g, sa, sb, ca, cb);
+  sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g) __attribute__((always_inline)) {
+    float sv[16], cl[NOISE ? 16 : 1];
+    lane_scores(kb, c, g, sv, cl);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < 2; ++q) {
       if (__ballot(st.wp > flush_at) != 0)
         flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int r = 4 * q + (e & 3);
-        const float x = e < 4 ? sa[r] : sb[r];
+        const int r = 8 * q + e;
+        const float x = sv[r];
         if (x > st.thr) {
-          *st.wp = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * q + e));
+          *st.wp = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3)));
           if (NOISE) {
             const int slot = (int)(st.wp - &mybuf[0][0]);
-            (&cpay[NOISE ? wave : 0][0][0])[NOISE ? slot : 0] = e < 4 ? ca[NOISE ? r : 0] : cb[NOISE ? r : 0];
+            (&cpay[NOISE ? wave : 0][0][0])[NOISE ? slot : 0] = cl[NOISE ? r : 0];
           }
           st.wp += kWave;
         }
@@ -419,8 +394,31 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   });
   flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 
-  if (valid) {
-    // Lists [split][M][hc][k]: each lane writes its query's k entries.
+  // Merge the two lanes' lists of the query: the partner's sorted list
+  // arrives through v_permlane32_swap and is bitonic-merged (keys of the two
+  // lanes are distinct: different key parities).
+  {
+    u64 other[KMAX];
+    float opay[NOISE ? KMAX : 1];
+#pragma unroll
+    for (int j = 0; j < KMAX; ++j) {
+      float lo = __uint_as_float((uint32_t)st.top.key[j]), lo2 = lo;
+      float hi = __uint_as_float((uint32_t)(st.top.key[j] >> 32)), hi2 = hi;
+      half_swap(lo, lo2);
+      half_swap(hi, hi2);
+      const float plo = par ? lo : lo2, phi = par ? hi : hi2;
+      other[j] = ((u64)__float_as_uint(phi) << 32) | __float_as_uint(plo);
+      if (NOISE) {
+        float a = st.top.pay[NOISE ? j : 0], b = a;
+        half_swap(a, b);
+        opay[NOISE ? j : 0] = par ? a : b;
+      }
+    }
+    st.top.template merge<KMAX>(other, opay);
+  }
+
+  if (valid && par == 0) {
+    // Lists [split][M][hc][k]: lane l < 32 writes its query's k entries.
     const int64_t o = (((int64_t)split * p.M + my_q) * p.HC + hc) * p.k;
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
@@ -589,7 +587,7 @@ struct Plan {
 static Plan make_plan(int64_t M, int H, int n, int k) {
   Plan pl;
   pl.nblk = (int)cdiv(n, 32);
-  pl.qblocks = cdiv(M, kScoreThreads);
+  pl.qblocks = cdiv(M, kQueriesPerGroup);
   const int64_t base = pl.qblocks * 2 * H;
   int64_t s = cdiv(MPL_SCORE_TARGET_WGS, base);
   s = s < 1 ? 1 : s;
