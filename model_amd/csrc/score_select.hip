@@ -564,6 +564,117 @@ __global__ __launch_bounds__(256) void pair_kernel(PairParams p) {
   }
 }
 
+// pair_kernel for k == 16: the same algorithm on 16-lane rows with DPP /
+// swizzle exchanges (no LDS traffic) and compile-time row broadcasts; split
+// lists are loaded four at a time so their loads overlap.
+__global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
+  constexpr int K = 16;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int64_t mh = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const bool live = mh < p.M * p.H;  // dead rows still join the exchanges
+  const int64_t m = live ? mh / p.H : 0;
+  const int h = live ? (int)(mh % p.H) : 0;
+  const int HC = 2 * p.H;
+  const float* lsel = p.sel != nullptr ? p.sel : p.clean;
+
+  u64 lk[2];
+  float lc[2];
+#pragma unroll
+  for (int c = 0; c < 2; ++c) {
+    const int hc = 2 * h + c;
+    const int64_t o0 = ((int64_t)m * HC + hc) * K + r;
+    const int64_t sstride = p.M * HC * K;
+    u64 acc = 0;
+    float pay = 0.f;
+    for (int s0 = 0; s0 < p.S; s0 += 4) {
+      int id[4];
+      float sl[4], cc[4];
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int64_t o = (int64_t)min(s0 + t, p.S - 1) * sstride + o0;  // clamped, unconditional
+        id[t] = p.idx[o];
+        sl[t] = lsel[o];
+        cc[t] = p.clean[o];
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (s0 + t < p.S) {  // uniform
+          const int i = live ? id[t] : -1;
+          const u64 kk = i >= 0 ? make_key(sl[t], i) : 0ull;
+          const float pc = live ? cc[t] : 0.f;
+          if (s0 + t == 0) {
+            acc = kk;
+            pay = pc;
+          } else {
+            g16::merge(acc, pay, kk, pc, r);
+          }
+        }
+      }
+    }
+    lk[c] = acc;
+    lc[c] = pay;
+    if (p.S > 1 && live) {
+      p.sub_idx[o0] = acc ? key_index(acc) : -1;
+      p.sub_scores[o0] = acc ? pay : -INFINITY;
+    }
+  }
+  const bool a_ok = lk[0] != 0ull, b_ok = lk[1] != 0ull;
+  const float a_sel = a_ok ? key_score(lk[0]) : -INFINITY;
+  const float b_sel = b_ok ? key_score(lk[1]) : -INFINITY;
+  const int a_id = a_ok ? key_index(lk[0]) : 0;
+  const int b_id = b_ok ? key_index(lk[1]) : 0;
+  const float a_cl = lc[0], b_cl = lc[1];
+  const float aok = a_ok ? 1.f : 0.f;
+
+  // row 0: (0, j) at lane j
+  u64 acc;
+  float pay;
+  {
+    const float a0 = g16::bcastf<0>(a_sel), a0c = g16::bcastf<0>(a_cl), a0k = g16::bcastf<0>(aok);
+    acc = (a0k != 0.f && b_ok) ? make_key(a0 + b_sel, r) : 0ull;
+    pay = a0c + b_cl;
+  }
+  // rows 1..7: (i, j) for j < 16/(i+1)
+#define MPL_PAIR_ROW(I)                                                                               \
+  {                                                                                                   \
+    const float ai = g16::bcastf<I>(a_sel), aic = g16::bcastf<I>(a_cl), aik = g16::bcastf<I>(aok);  \
+    const u64 cand = (r < K / (I + 1) && aik != 0.f && b_ok) ? make_key(ai + b_sel, I * K + r) : 0ull; \
+    g16::merge(acc, pay, cand, aic + b_cl, r);                                                        \
+  }
+  MPL_PAIR_ROW(1) MPL_PAIR_ROW(2) MPL_PAIR_ROW(3) MPL_PAIR_ROW(4) MPL_PAIR_ROW(5) MPL_PAIR_ROW(6)
+  MPL_PAIR_ROW(7)
+#undef MPL_PAIR_ROW
+  // rows 8..15: only (i, 0) can reach the top 16; lane r takes row 8 + r
+  {
+    const float b0 = g16::bcastf<0>(b_sel), b0c = g16::bcastf<0>(b_cl);
+    const bool b0_ok = b0 != -INFINITY;
+    const float ar = __uint_as_float(g16::shl8(__float_as_uint(a_sel)));
+    const float arc = __uint_as_float(g16::shl8(__float_as_uint(a_cl)));
+    const float ark = __uint_as_float(g16::shl8(__float_as_uint(aok)));
+    const u64 cand = (r < 8 && ark != 0.f && b0_ok) ? make_key(ar + b0, (8 + r) * K) : 0ull;
+    g16::merge(acc, pay, cand, arc + b0c, r);
+  }
+
+  // lane r holds the rank-r slot
+  const int flat = acc ? key_index(acc) : 0;
+  const int base = lane - r;
+  int ia = __shfl(a_id, base + flat / K);
+  int ib = __shfl(b_id, base + flat % K);
+  ia = (ia >= 0 && ia < p.n) ? ia : 0;  // ids come from keys < n; guards non-finite inputs
+  ib = (ib >= 0 && ib < p.n) ? ib : 0;
+  const float sc = acc ? pay : -INFINITY;
+  const float mx = g16::rmax(sc);
+  const float e = acc ? expf(sc - mx) : 0.f;
+  const float sum = g16::rsum(e);
+  if (live) {
+    const int64_t ob = mh * K + r;
+    p.slots[ob] = ia * p.n + ib;
+    p.flat_idx[ob] = flat;
+    p.weights[ob] = e / sum;
+  }
+}
+
 // ---------------------------------------------------------------- host side
 struct Plan {
   int splits, blk_per_split, nblk, kmax, pass1_blocks;
@@ -741,7 +852,8 @@ extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const voi
   pp.weights = weights;
   const int G = k <= 16 ? 16 : 32;
   const unsigned g2 = (unsigned)cdiv(M * H * G, 256);
-  if (G == 16) pair_kernel<16><<<g2, 256, 0, s>>>(pp);
+  if (k == 16) pair_kernel_k16<<<g2, 256, 0, s>>>(pp);
+  else if (G == 16) pair_kernel<16><<<g2, 256, 0, s>>>(pp);
   else pair_kernel<32><<<g2, 256, 0, s>>>(pp);
   return check_launch("mpl_score_select(stage 2)");
 }

@@ -168,3 +168,87 @@ __device__ __forceinline__ float group_sum(float v) {
 }
 
 }  // namespace mpl
+
+namespace mpl {
+
+// ------------------------------------------- 16-lane groups without LDS
+// Lane exchanges inside aligned 16-lane rows on the VALU (DPP) or the
+// swizzle network: xor 1 / 2 are quad permutes, xor 8 is a rotate by 8 of
+// the row, xor 4 and the broadcasts are ds_swizzle bit patterns
+// (lane' = ((lane & and) | or) ^ xor within 32 lanes).
+namespace g16 {
+
+template <int S>
+__device__ __forceinline__ uint32_t xr(uint32_t v) {
+  if constexpr (S == 1) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);
+  else if constexpr (S == 2) return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);
+  else if constexpr (S == 4) return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (4 << 10) | 0x1F);
+  else return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+}
+// lane i of the row <- lane 15 - i
+__device__ __forceinline__ uint32_t mirror(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x140, 0xF, 0xF, false);
+}
+// every lane of the row <- lane I of the row
+template <int I>
+__device__ __forceinline__ uint32_t bcast(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, (I << 5) | 0x10);
+}
+// lane i <- lane i + 8 (lanes 8..15 receive 0)
+__device__ __forceinline__ uint32_t shl8(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x108, 0xF, 0xF, true);
+}
+
+template <int S>
+__device__ __forceinline__ u64 xr64(u64 v) {
+  return ((u64)xr<S>((uint32_t)(v >> 32)) << 32) | xr<S>((uint32_t)v);
+}
+template <int S>
+__device__ __forceinline__ float xrf(float v) {
+  return __uint_as_float(xr<S>(__float_as_uint(v)));
+}
+template <int I>
+__device__ __forceinline__ float bcastf(float v) {
+  return __uint_as_float(bcast<I>(__float_as_uint(v)));
+}
+
+// acc <- best 16 of (acc, b), both sorted descending across the row (lane r
+// holds rank r); payloads follow their keys.  Bitonic split against the
+// mirrored b, then a 4-stage bitonic merger.
+__device__ __forceinline__ void merge(u64& acc, float& pay, u64 b, float bp, int r) {
+  const u64 br = ((u64)mirror((uint32_t)(b >> 32)) << 32) | mirror((uint32_t)b);
+  const float bpr = __uint_as_float(mirror(__float_as_uint(bp)));
+  const bool take = br > acc;
+  acc = take ? br : acc;
+  pay = take ? bpr : pay;
+#define MPL_G16_STAGE(S)                                  \
+  {                                                       \
+    const u64 o = xr64<S>(acc);                           \
+    const float op = xrf<S>(pay);                         \
+    const bool lower = (r & S) == 0;                      \
+    const bool other = lower ? (o > acc) : (o < acc);     \
+    acc = other ? o : acc;                                \
+    pay = other ? op : pay;                               \
+  }
+  MPL_G16_STAGE(8)
+  MPL_G16_STAGE(4)
+  MPL_G16_STAGE(2)
+  MPL_G16_STAGE(1)
+#undef MPL_G16_STAGE
+}
+
+__device__ __forceinline__ float rmax(float v) {
+  v = fmaxf(v, xrf<8>(v));
+  v = fmaxf(v, xrf<4>(v));
+  v = fmaxf(v, xrf<2>(v));
+  return fmaxf(v, xrf<1>(v));
+}
+__device__ __forceinline__ float rsum(float v) {
+  v += xrf<8>(v);
+  v += xrf<4>(v);
+  v += xrf<2>(v);
+  return v + xrf<1>(v);
+}
+
+}  // namespace g16
+}  // namespace mpl
