@@ -3,8 +3,8 @@
 Headline (``value``): lookup tokens/s on the text-study layer, 8,192 tokens,
 262,144 fp16 slots (H=4, d_key=256, k=16, d_value=256).  One step is the full
 lookup of memory.py:132-193 on inputs already resident in HBM: sub-key
-normalisation + packing, query normalisation, scoring with the two-stage
-top-k and softmax, and the fp16 gather-weighted-sum.
+normalisation + packing, scoring (with the query normalisation fused in)
+with the two-stage top-k and softmax, and the fp16 gather-weighted-sum.
 
 Also reported in the same JSON line:
   * ``roofline``: the dominant kernel's algorithmic throughput against
@@ -106,8 +106,6 @@ class Lookup:
         self.values = values
         self.T = 10.0
         f32, i32, u8 = torch.float32, torch.int32, torch.uint8
-        self.q_hat = torch.empty_like(self.q)
-        self.q16 = torch.empty_like(self.q, dtype=torch.float16)
         self.k_hat = torch.empty_like(self.sub_keys)
         self.packed = torch.empty(L.mpl_packed_keys_bytes(H, n, self.half, _lib.MPL_F16), dtype=u8, device=dev)
         self.ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, self.half, k)
@@ -129,15 +127,12 @@ class Lookup:
         self._lib.check(self.L.mpl_pack_keys(p(self.sub_keys), self.H, self.n, self.half, self._lib.MPL_F16,
                                              p(self.k_hat), p(self.packed), self.stream), "pack")
 
-    def norm(self):
-        p = self._lib.ptr
-        self._lib.check(self.L.mpl_l2_normalize(p(self.q), self.M * self.H * 2, self.half, 1e-6, p(self.q_hat),
-                                                p(self.q16), None, self.stream), "norm")
-
     def select(self):
+        # raw queries: the scoring kernel l2-normalises them (memory.py:136)
         p = self._lib.ptr
         self._lib.check(self.L.mpl_score_select(
-            p(self.q16), None, p(self.packed), self.M, self.H, self.n, self.half, self.k, self._lib.MPL_F16,
+            p(self.q), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
+            self._lib.MPL_F16,
             self.T, None, 0.0, p(self.ws), self.ws_bytes, p(self.sub_idx), p(self.sub_scores), p(self.flat_idx),
             p(self.slots), p(self.weights), self.stream), "select")
 
@@ -149,7 +144,6 @@ class Lookup:
 
     def step(self):
         self.pack()
-        self.norm()
         self.select()
         self.gather()
 
@@ -185,7 +179,6 @@ def time_loop(torch, fn, iters, warmup):
 def kernel_breakdown(torch, lk, iters):
     return {
         "pack_keys_ms": time_loop(torch, lk.pack, iters, 3),
-        "normalize_ms": time_loop(torch, lk.norm, iters, 3),
         "score_select_ms": time_loop(torch, lk.select, iters, 3),
         "gather_wsum_ms": time_loop(torch, lk.gather, iters, 3),
     }

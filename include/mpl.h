@@ -34,6 +34,9 @@ extern "C" {
 enum { MPL_F32 = 0, MPL_F16 = 1 };
 enum { MPL_OK = 0, MPL_EINVAL = 1, MPL_EHIP = 2, MPL_EWORKSPACE = 3, MPL_EUNSUPPORTED = 4 };
 
+/* query_mode of mpl_score_select */
+enum { MPL_Q_NORMALIZED = 0, MPL_Q_RAW = 1, MPL_Q_RAW_SCALED = 2 };
+
 /* Library version (major*10000 + minor*100 + patch). */
 int mpl_version(void);
 
@@ -62,10 +65,17 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
                   float* keys_hat, void* packed, void* stream);
 
 /*
- * memory.py:149-178: cosine scores of q_hat [M,H,2,half] (unit rows, in
- * score_dtype: fp16 for MPL_F16, fp32 for MPL_F32) against the packed keys, times `temperature` (already clamped, memory.py:
- * 143-146) and times q_len [M,H,2] when q_len != NULL (query_scale,
- * memory.py:151-152); optional routing noise select = scores + noise_coef *
+ * memory.py:136-178: cosine scores of the queries [M,H,2,half] against the
+ * packed keys, times `temperature` (already clamped, memory.py:143-146) and,
+ * with query_scale, times q_len (memory.py:151-152).  `queries` is either
+ *   query_mode MPL_Q_NORMALIZED: unit rows in score_dtype (fp16 for MPL_F16,
+ *     fp32 for MPL_F32, e.g. from mpl_l2_normalize); q_len [M,H,2] is an
+ *     input (NULL = no query_scale);
+ *   MPL_Q_RAW / MPL_Q_RAW_SCALED (fp16 scoring only): the raw fp32 queries,
+ *     l2-normalised inside the kernel (memory.py:30-31, 136); with
+ *     MPL_Q_RAW_SCALED the scores are also scaled by
+ *     q_len = sqrt(sum q^2 + 1e-6) / sqrt(half), written to q_len if not NULL.
+ * Optional routing noise select = scores + noise_coef *
  * gumbel with gumbel [M,H,2,n] fp32 (memory.py:155-159, NULL = no noise);
  * exact stage-1 top-k per codebook (ties: lowest sub-key index), exact
  * stage-2 top-k over the k*k candidates (ties: lowest flat index
@@ -79,7 +89,7 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
  * Requires 1 <= k <= min(n, 32), 1 <= half <= 128, n*n < 2^31.
  */
 size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int half, int k);
-int mpl_score_select(const void* q_hat, const float* q_len, const void* packed_keys,
+int mpl_score_select(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                      int64_t M, int H, int n, int half, int k, int score_dtype,
                      float temperature, const float* gumbel, float noise_coef,
                      void* workspace, size_t workspace_bytes,

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmpl.so")
 
 MPL_F32, MPL_F16 = 0, 1
+MPL_Q_NORMALIZED, MPL_Q_RAW, MPL_Q_RAW_SCALED = 0, 1, 2
 
 # name -> (restype, argtypes); the C ABI of include/mpl.h
 _P, _I, _I64, _F, _SZ = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
@@ -23,7 +24,7 @@ SIGNATURES = {
     "mpl_packed_keys_bytes": (_SZ, [_I, _I, _I, _I]),
     "mpl_pack_keys": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "mpl_score_select_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
-    "mpl_score_select": (_I, [_P, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
+    "mpl_score_select": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
                               _P, _P, _P, _P, _P, _P]),
     "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
     "mpl_merge_rows_workspace_bytes": (_SZ, [_I64, _I, _I64]),

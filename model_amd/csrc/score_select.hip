@@ -58,8 +58,10 @@ constexpr int kQueriesPerGroup = kQueriesPerWave * (kScoreThreads / 64);
 constexpr int kMaxSplits = 64;
 
 struct ScoreParams {
-  const void* q_hat;    // [M, HC, half] in the scoring type
-  const float* q_len;   // [M, HC] or null
+  const void* q_hat;    // [M, HC, half]: normalised in the scoring type (mode 0) or raw fp32
+  const float* q_len;   // [M, HC] or null (mode 0 input)
+  float* out_qlen;      // [M, HC] or null (mode 2 output)
+  int query_mode;       // MPL_Q_NORMALIZED / MPL_Q_RAW / MPL_Q_RAW_SCALED
   const uint4* packed;  // packed keys
   const float* gumbel;  // [M, HC, n] or null
   float T, noise_coef;
@@ -92,6 +94,28 @@ struct Mfma<_Float16> {
     return o;
   }
   __device__ static Op from_vec(uint4 u, int) { return __builtin_bit_cast(half8, u); }
+  // Raw fp32 query dims 16c + 8*(lane/32) + [0,8): two aligned 16-byte loads,
+  // zeroed after when out of range; adds their squares to ss.
+  static constexpr int kQElems = 8;
+  __device__ static void load_q_raw(const float* q, bool valid, int half, int c, int lane, float* x, float& ss) {
+    const int d0 = 16 * c + 8 * (lane >> 5);
+    const bool ok = valid && d0 < half;
+    const float4* src = (const float4*)(q + (d0 < half ? d0 : 0));
+    const float4 u = src[0], v = src[1];
+    x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
+    x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[i] = ok ? x[i] : 0.f;
+      ss = fmaf(x[i], x[i], ss);
+    }
+  }
+  __device__ static Op scale_q(const float* x, float r) {
+    Op o;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = (_Float16)(x[i] * r);
+    return o;
+  }
 };
 
 template <>
@@ -109,6 +133,14 @@ struct Mfma<float> {
     const unsigned w = e == 0 ? u.x : e == 1 ? u.y : e == 2 ? u.z : u.w;
     return __uint_as_float(w);
   }
+  static constexpr int kQElems = 1;
+  __device__ static void load_q_raw(const float* q, bool valid, int half, int c, int lane, float* x, float& ss) {
+    const int d = 2 * c + (lane >> 5);
+    const float f = q[min(d, half - 1)];
+    x[0] = (valid && d < half) ? f : 0.f;
+    ss = fmaf(x[0], x[0], ss);
+  }
+  __device__ static Op scale_q(const float* x, float r) { return x[0] * r; }
 };
 
 // Per-lane selection state of the stage-1 kernel.  Candidates are appended
@@ -216,12 +248,32 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   const int64_t my_q = q0 + (lane & 31);
   const bool valid = my_q < p.M;
   Op qop[NCH];
-  {
+  float ql = 1.f;
+  if (p.query_mode == MPL_Q_NORMALIZED) {
     const T* qrow = (const T*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
 #pragma unroll
     for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::load_q(qrow, valid, p.half, c, lane);
+    if (p.q_len != nullptr) ql = p.q_len[(valid ? my_q : 0) * p.HC + hc];
+  } else {
+    // Raw fp32 queries, normalised here (memory.py:30-31, 136-137): the
+    // lane pair holds the row's 2*NCH*8 dims, so one half-swap completes
+    // the sum of squares.
+    const float* qrow = (const float*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
+    float x[NCH][Mfma<T>::kQElems];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) Mfma<T>::load_q_raw(qrow, valid, p.half, c, lane, x[c], ss);
+    float a = ss, b = ss;
+    half_swap(a, b);
+    const float tot = ss + (par ? a : b) + 1e-6f;
+    const float rn = 1.0f / sqrtf(tot);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::scale_q(x[c], rn);
+    if (p.query_mode == MPL_Q_RAW_SCALED) {
+      ql = sqrtf(tot) / sqrtf((float)p.half);
+      if (p.out_qlen != nullptr && valid && split == 0 && par == 0) p.out_qlen[my_q * p.HC + hc] = ql;
+    }
   }
-  const float ql = p.q_len != nullptr ? p.q_len[(valid ? my_q : 0) * p.HC + hc] : 1.f;
   const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
   uint2(*mybuf)[kWave] = cbuf[wave];
   const float(*mypay)[kWave] = cpay[NOISE ? wave : 0];
@@ -320,7 +372,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       float v = c[r];
       if (NOISE) {
         v = v * p.T;
-        if (p.q_len != nullptr) v *= ql;
+        v *= ql;  // ql == 1 without query_scale
         cl[NOISE ? r : 0] = v;
         v = __builtin_fmaf(p.noise_coef, g[NOISE ? r : 0], v);
       }
@@ -430,7 +482,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
           sel = key_score(kk);
         } else {
           clean = key_score(kk) * p.T;
-          if (p.q_len != nullptr) clean *= ql;
+          clean *= ql;  // ql == 1 without query_scale
           sel = clean;
         }
         if (kk == 0) clean = sel = -INFINITY;
@@ -770,7 +822,7 @@ extern "C" size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int 
   return ws_bytes(pl, M, H, k, true);
 }
 
-extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const void* packed_keys,
+extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                                 int64_t M, int H, int n, int half, int k, int score_dtype,
                                 float temperature, const float* gumbel, float noise_coef,
                                 void* workspace, size_t workspace_bytes, int32_t* sub_idx,
@@ -788,8 +840,10 @@ extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const voi
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
               "mpl_score_select: score_dtype must be MPL_F16 or MPL_F32");
   if (M == 0) return MPL_OK;
-  MPL_REQUIRE(q_hat && packed_keys && sub_idx && sub_scores && flat_idx && slots && weights, MPL_EINVAL,
+  MPL_REQUIRE(queries && packed_keys && sub_idx && sub_scores && flat_idx && slots && weights, MPL_EINVAL,
               "mpl_score_select: null buffer");
+  MPL_REQUIRE(query_mode == MPL_Q_NORMALIZED || query_mode == MPL_Q_RAW || query_mode == MPL_Q_RAW_SCALED,
+              MPL_EINVAL, "mpl_score_select: bad query_mode %d", query_mode);
   const bool noise = gumbel != nullptr;
   const Plan pl = make_plan(M, H, n, k);
   const size_t need = ws_bytes(pl, M, H, k, noise);
@@ -800,8 +854,10 @@ extern "C" int mpl_score_select(const void* q_hat, const float* q_len, const voi
   const size_t per = (size_t)M * HC * k;
 
   ScoreParams sp;
-  sp.q_hat = q_hat;
-  sp.q_len = q_len;
+  sp.q_hat = queries;
+  sp.q_len = query_mode == MPL_Q_NORMALIZED ? q_len : nullptr;
+  sp.out_qlen = query_mode == MPL_Q_RAW_SCALED ? q_len : nullptr;
+  sp.query_mode = query_mode;
   sp.packed = (const uint4*)packed_keys;
   sp.gumbel = gumbel;
   sp.T = temperature;

@@ -74,11 +74,16 @@ class LazyAux(dict):
     _LAZY = ("balance_loss", "subkey_counts", "slot_counts", "top1_weight")
     _INTERNAL = ("_f", "_p", "_cos")
 
-    def __init__(self, eager: Dict[str, Any], compute):
+    def __init__(self, eager: Dict[str, Any], compute, **lazy):
         super().__init__(eager)
         self._compute = compute
+        self._lazy = lazy  # further keys computed on first access (e.g. queries)
 
     def __missing__(self, key):
+        if key in self._lazy:
+            v = self._lazy[key]()
+            self[key] = v
+            return v
         if key in self._LAZY:
             stats = self._compute()
             self.internal = {k: stats.pop(k) for k in self._INTERNAL if k in stats}
@@ -87,15 +92,32 @@ class LazyAux(dict):
         raise KeyError(key)
 
     def __contains__(self, key):
-        return key in self._LAZY or dict.__contains__(self, key)
+        return key in self._LAZY or key in self._lazy or dict.__contains__(self, key)
 
     def keys(self):
-        return list(dict.keys(self)) + [k for k in self._LAZY if not dict.__contains__(self, k)]
+        pending = [k for k in (*self._lazy, *self._LAZY) if not dict.__contains__(self, k)]
+        return list(dict.keys(self)) + pending
 
     def materialize(self) -> "LazyAux":
-        for k in self._LAZY:
+        for k in (*self._lazy, *self._LAZY):
             self[k]
         return self
+
+
+class _Result(dict):
+    """The lookup's result; "q_hat" (fp32 normalised queries, which the
+    scoring kernel does not need) is computed on first access."""
+
+    def __missing__(self, key):
+        if key != "q_hat":
+            raise KeyError(key)
+        q = self["q"]
+        M, H, _, half = q.shape
+        q_hat = torch.empty_like(q)
+        check(_lib.lib().mpl_l2_normalize(ptr(q), M * H * 2, half, NORM_EPS, ptr(q_hat), None, None,
+                                          _lib.stream_ptr(q.device)), "mpl_l2_normalize")
+        self["q_hat"] = q_hat
+        return q_hat
 
 
 class MemoryPool:
@@ -200,13 +222,10 @@ class MemoryPool:
         q = queries.detach().reshape(-1, H, 2, half).float().contiguous()
         M = q.shape[0]
         score_code = _dtype_code(self.score_dtype)
-        q_hat = torch.empty_like(q)
-        # the scoring operand: q_hat itself for fp32 scoring, its fp16 rounding otherwise
-        q_score = torch.empty_like(q, dtype=torch.float16) if score_code == _lib.MPL_F16 else q_hat
+        # the scoring kernel normalises the raw queries itself (and computes
+        # q_len with query_scale); the fp32 q_hat is produced only on demand
+        q_mode = _lib.MPL_Q_RAW_SCALED if self.query_scale else _lib.MPL_Q_RAW
         q_len = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if self.query_scale else None
-        check(L.mpl_l2_normalize(ptr(q), M * H * 2, half, NORM_EPS, ptr(q_hat),
-                                 ptr(q_score) if q_score is not q_hat else None, ptr(q_len), stream),
-              "mpl_l2_normalize")
         k_hat, packed = self._keys.get(params["sub_keys"], score_code)
         T = self.temperature(params["log_temperature"])
 
@@ -231,7 +250,7 @@ class MemoryPool:
         flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_select(ptr(q_score), ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
+        check(L.mpl_score_select(ptr(q), q_mode, ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
                                  T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
                                  ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
               "mpl_score_select")
@@ -245,30 +264,32 @@ class MemoryPool:
               "mpl_gather_wsum")
 
         noisy = gumbel is not None
+        res = _Result()
 
         def stats():
-            return self._routing_stats(params, q_hat, q_score, k_hat, T, q_len, sub_idx, slots, weights,
+            return self._routing_stats(params, res, k_hat, T, q_len, sub_idx, slots, weights,
                                        noisy, packed, score_code, M)
 
         aux = LazyAux({
-            "queries": q_hat,
             "slots": slots.reshape(*lead, H, k),
             "weights": weights.reshape(*lead, H, k),
             "temperature": self._temp_tensor,
-        }, stats)
-        return {
-            "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_hat": q_hat, "q_len": q_len,
+        }, stats, queries=lambda: res["q_hat"])
+        res.update({
+            "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
             "k_hat": k_hat, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
             "flat_idx": flat_idx, "slots": slots, "weights": weights, "gumbel": gumbel,
             "noise_coef": noise_coef,
-        }
+        })
+        return res
 
     # ------------------------------------------------------------- stats
-    def _routing_stats(self, params, q_hat, q_score, k_hat, T, q_len, sub_idx, slots, weights, noisy,
+    def _routing_stats(self, params, res, k_hat, T, q_len, sub_idx, slots, weights, noisy,
                        packed, score_code, M):
         """memory.py:196-215 from the selected ids."""
         H, n, k = self.heads, self.n_sub_keys, self.top_k
-        dev = q_hat.device
+        dev = sub_idx.device
+        q_hat = res["q_hat"]
         codebook = ((torch.arange(H, device=dev)[:, None, None] * 2
                      + torch.arange(2, device=dev)[None, :, None]) * n)
 
@@ -279,7 +300,7 @@ class MemoryPool:
         sl = slots.long()
         subkey_counts = count_subkeys(torch.stack([sl // n, sl % n], dim=2))
         if noisy:  # memory.py:207: an extra clean selection
-            clean = self._clean_sub_idx(q_score, q_len, packed, score_code, T, M)
+            clean = self._clean_sub_idx(res["q"], packed, score_code, T, M)
         else:
             clean = sub_idx
         f = count_subkeys(clean) / (M * k)
@@ -300,9 +321,10 @@ class MemoryPool:
             "_f": f, "_p": p, "_cos": cos,
         }
 
-    def _clean_sub_idx(self, q_score, q_len, packed, score_code, T, M):
+    def _clean_sub_idx(self, q, packed, score_code, T, M):
         H, n, k, half = self.heads, self.n_sub_keys, self.top_k, self.d_key // 2
-        dev = q_score.device
+        dev = q.device
+        q_mode = _lib.MPL_Q_RAW_SCALED if self.query_scale else _lib.MPL_Q_RAW
         L = _lib.lib()
         ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
@@ -311,7 +333,7 @@ class MemoryPool:
         flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_select(ptr(q_score), ptr(q_len), ptr(packed), M, H, n, half, k, score_code, T,
+        check(L.mpl_score_select(ptr(q), q_mode, None, ptr(packed), M, H, n, half, k, score_code, T,
                                  None, 0.0, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores),
                                  ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
               "mpl_score_select(clean)")

@@ -120,6 +120,11 @@ def test_query_scale(gpu_lib):
     b = pool.lookup(params, q * 10.0)
     assert torch.equal(a["slots"], b["slots"])
     assert float(b["aux"]["top1_weight"]) > float(a["aux"]["top1_weight"])
+    # q_len from the scoring kernel and the lazily normalised aux queries (memory.py:136-137, :220)
+    qn = q.detach().double().cpu().numpy().reshape(120, 2, 2, 16)
+    nrm = np.sqrt((qn * qn).sum(-1) + 1e-6)
+    np.testing.assert_allclose(a["q_len"].cpu().numpy(), nrm / np.sqrt(16), rtol=1e-6)
+    np.testing.assert_allclose(a["aux"]["queries"].cpu().numpy(), qn / nrm[..., None], rtol=1e-5, atol=1e-7)
 
 
 @pytest.mark.parametrize("dt", ["fp32", "fp16"])
