@@ -727,6 +727,65 @@ __global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
   }
 }
 
+// Split lists are reduced eight at a time before stage 2 (k == 16 only).
+constexpr int kMergeChunk = 8;
+
+// Split-list reduction for k == 16: 16-lane row (s2, m, hc) merges lists
+// s2*8 .. s2*8+7 of (m, hc) (loaded four at a time) into list s2.
+struct MergeParams {
+  const float* sel;  // null without noise (equals clean)
+  const float* clean;
+  const int* idx;
+  int64_t rows;  // M * HC
+  int S, S2;
+  float* out_sel;
+  float* out_clean;
+  int* out_idx;
+};
+
+__global__ __launch_bounds__(256) void merge_splits_k16(MergeParams p) {
+  constexpr int K = 16;
+  const int r = threadIdx.x & 15;
+  const int64_t g = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const bool live = g < p.rows * p.S2;  // dead rows still join the exchanges
+  const int64_t row = live ? g % p.rows : 0;
+  const int s2 = live ? (int)(g / p.rows) : 0;
+  const float* lsel = p.sel != nullptr ? p.sel : p.clean;
+  const int64_t sstride = p.rows * K;
+  u64 acc = 0;
+  float pay = 0.f;
+#pragma unroll
+  for (int t0 = 0; t0 < kMergeChunk; t0 += 4) {
+    int id[4];
+    float sl[4], cc[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const int s = min(s2 * kMergeChunk + t0 + t, p.S - 1);  // clamped, unconditional
+      const int64_t o = (int64_t)s * sstride + row * K + r;
+      id[t] = p.idx[o];
+      sl[t] = lsel[o];
+      cc[t] = p.clean[o];
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      const bool in = s2 * kMergeChunk + t0 + t < p.S;  // uniform per row
+      const u64 kk = (in && id[t] >= 0) ? make_key(sl[t], id[t]) : 0ull;
+      if (t0 + t == 0) {
+        acc = kk;
+        pay = cc[t];
+      } else {
+        g16::merge(acc, pay, kk, in ? cc[t] : 0.f, r);
+      }
+    }
+  }
+  if (live) {
+    const int64_t o = ((int64_t)s2 * p.rows + row) * K + r;
+    p.out_idx[o] = acc ? key_index(acc) : -1;
+    p.out_clean[o] = acc ? pay : -INFINITY;
+    if (p.out_sel != nullptr) p.out_sel[o] = acc ? key_score(acc) : -INFINITY;
+  }
+}
+
 // ---------------------------------------------------------------- host side
 struct Plan {
   int splits, blk_per_split, nblk, kmax, pass1_blocks;
@@ -765,10 +824,14 @@ static Plan make_plan(int64_t M, int H, int n, int k) {
 }
 
 // Workspace: the select scores with noise; per-split lists when split.
+static int reduced_splits(const Plan& pl, int k) {
+  return (k == 16 && pl.splits > kMergeChunk) ? (int)cdiv(pl.splits, kMergeChunk) : 0;
+}
+
 static size_t ws_bytes(const Plan& pl, int64_t M, int H, int k, bool noise) {
   const size_t per = (size_t)M * 2 * H * k;
   if (pl.splits == 1) return noise ? per * 4 : 0;
-  return per * pl.splits * (noise ? 3 : 2) * 4;
+  return per * (pl.splits + reduced_splits(pl, k)) * (noise ? 3 : 2) * 4;
 }
 
 template <typename T, int HP, bool NOISE, int KMAX>
@@ -906,6 +969,30 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
   pp.flat_idx = flat_idx;
   pp.slots = slots;
   pp.weights = weights;
+  const int S2 = reduced_splits(pl, k);
+  if (S2 > 0) {
+    // many splits (decode-sized batches): reduce the lists in parallel first,
+    // so stage 2 merges S2 <= 8 lists instead of a long sequential chain
+    float* r = w + (noise ? 3 : 2) * part;
+    const size_t part2 = per * S2;
+    MergeParams mp;
+    mp.sel = sp.out_sel;
+    mp.clean = sp.out_clean;
+    mp.idx = sp.out_idx;
+    mp.rows = M * HC;
+    mp.S = pl.splits;
+    mp.S2 = S2;
+    mp.out_clean = r;
+    mp.out_idx = (int*)(r + part2);
+    mp.out_sel = noise ? r + 2 * part2 : nullptr;
+    merge_splits_k16<<<(unsigned)cdiv(mp.rows * S2 * 16, 256), 256, 0, s>>>(mp);
+    rc = check_launch("mpl_score_select(split merge)");
+    if (rc) return rc;
+    pp.sel = mp.out_sel;
+    pp.clean = mp.out_clean;
+    pp.idx = mp.out_idx;
+    pp.S = S2;
+  }
   const int G = k <= 16 ? 16 : 32;
   const unsigned g2 = (unsigned)cdiv(M * H * G, 256);
   if (k == 16) pair_kernel_k16<<<g2, 256, 0, s>>>(pp);
