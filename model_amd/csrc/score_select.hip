@@ -217,18 +217,26 @@ __device__ __forceinline__ float kth_of_32(const float* a, const float* b, int k
   return from_orderable(t);
 }
 
+// s_waitcnt that waits until at most N vector-memory loads of this wave are
+// outstanding (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt_le() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+
 template <typename T, int HP, bool NOISE, int KMAX>
 __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {
   constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);  // 16-B vectors per lane per block
   constexpr int OPV = KeyPack<T>::kOpsPerVec;
   constexpr int NCH = VPL * OPV;                         // MFMA chunks per block
   constexpr int TILE = VPL * kWave;                      // uint4 per key block
-  constexpr int PRE = (TILE + kScoreThreads - 1) / kScoreThreads;
-  constexpr int TILE_ALLOC = PRE * kScoreThreads;  // >= TILE: every thread stores unguarded
   constexpr int WAVES = kScoreThreads / kWave;
   typedef typename Mfma<T>::Op Op;
 
-  __shared__ uint4 tiles[2][TILE_ALLOC];
+  __shared__ uint4 tile0[TILE], tile1[TILE];
   __shared__ uint2 cbuf[WAVES][kCand][kWave];
   __shared__ float cpay[NOISE ? WAVES : 1][NOISE ? kCand : 1][kWave];
 
@@ -278,32 +286,24 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   uint2(*mybuf)[kWave] = cbuf[wave];
   const float(*mypay)[kWave] = cpay[NOISE ? wave : 0];
 
-  // Key blocks stream through two LDS buffers; `pre` holds the block after
-  // next in registers between its global load and its LDS store.  The loads
-  // are loop-carried, so the compiler cannot sink them next to their stores,
-  // and none is guarded (clamped sources, padded tiles): a guard would
-  // serialise them.  (A vector type, not an array: a loop-carried array is
-  // not promoted to registers.)
-  typedef unsigned PreVec __attribute__((ext_vector_type(4 * PRE)));
+  // Key blocks stream into two LDS buffers by LDS DMA (global_load_lds: no
+  // registers, no LDS store instructions).  Wave w copies the tile's 16-byte
+  // vectors w, w+WAVES, ... (with fewer vectors than waves, several waves
+  // copy the same bytes).  The buffers are separate arrays used in a
+  // compile-time alternation, so the compiler sees which buffer each LDS read
+  // touches and does not drain the in-flight DMA of the other one before it.
   typedef float GVec __attribute__((ext_vector_type(NOISE ? 16 : 1)));
+  constexpr int LPW = VPL >= WAVES ? VPL / WAVES : 1;
+  static_assert(VPL < WAVES || VPL % WAVES == 0, "tile vectors must split over the waves");
   const uint4* kbase_ptr = p.packed + (int64_t)hc * p.nblk * TILE;
-  auto fetch = [&](int blk) __attribute__((always_inline)) {
-    PreVec v;
+  auto dma = [&](uint4* dst, int blk) __attribute__((always_inline)) {
     const uint4* src = kbase_ptr + (int64_t)blk * TILE;
 #pragma unroll
-    for (int i = 0; i < PRE; ++i) {
-      const uint4 u = src[min(tid + i * kScoreThreads, TILE - 1)];
-      v[4 * i] = u.x;
-      v[4 * i + 1] = u.y;
-      v[4 * i + 2] = u.z;
-      v[4 * i + 3] = u.w;
+    for (int i = 0; i < LPW; ++i) {
+      const int v = VPL >= WAVES ? wave + WAVES * i : wave % VPL;
+      __builtin_amdgcn_global_load_lds((const void*)(src + v * kWave + lane), (lds_void*)(dst + v * kWave), 16, 0,
+                                       0);
     }
-    return v;
-  };
-  auto stage = [&](int buf, const PreVec& v) __attribute__((always_inline)) {
-#pragma unroll
-    for (int i = 0; i < PRE; ++i)
-      tiles[buf][tid + i * kScoreThreads] = make_uint4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   };
   // The lane's 16 noise values of block blk (keys 8*(r/4) + 4*par + r%4).
   auto fetch_noise = [&](int blk) __attribute__((always_inline)) {
@@ -315,51 +315,55 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     }
     return g;
   };
-  // The 32-key x 32-query score tile of one key block: c[r] = query
-  // q0 + lane%32 against key 8*(r/4) + 4*par + r%4.
-  auto mma_block = [&](int buf, f32x16& c) __attribute__((always_inline)) {
-    c = f32x16{};
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const uint4 u = tiles[buf][v * kWave + lane];
-#pragma unroll
-      for (int e = 0; e < OPV; ++e) c = Mfma<T>::mma(Mfma<T>::from_vec(u, e), qop[v * OPV + e], c);
-    }
-  };
   // One sweep over key blocks [bb, be), software-pipelined: while the VALU
   // runs body() on block j, the MFMAs of block j+1 are already in flight.
-  // LDS order per iteration j: reads of block j+1, then the store of block j+2
-  // into block j's buffer, then one barrier.  Block j was read in iteration
-  // j-1, before that iteration's barrier; block j+2 is read in iteration j+1,
-  // after this one's.
+  // Block j lives in buffer j % 2.  Iteration j: wait for this wave's DMA of
+  // block j+1 (issued in iteration j-1; only the noise loads issued after it
+  // may still be in flight: loads complete in order), join the barrier (so
+  // every wave's DMA has landed and every wave has finished reading block j,
+  // whose MFMAs were issued in iteration j-1), DMA block j+2 into block j's
+  // buffer, then read block j+1 and run body() on block j with the next
+  // block's MFMAs interleaved.  Past the end, DMAs copy clamped duplicates
+  // and the one extra MFMA group scores one; nobody reads either.
   auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
     const int nb = be - bb;
     if (nb <= 0) return;
-    PreVec pre = fetch(bb);
-    stage(0, pre);
-    pre = fetch(min(bb + 1, be - 1));
-    stage(1, pre);
-    pre = fetch(min(bb + 2, be - 1));
+    dma(tile0, bb);
+    dma(tile1, min(bb + 1, be - 1));
     GVec gcur = fetch_noise(bb);
-    __syncthreads();
-    f32x16 x, y;
-    mma_block(0, x);
-    // The MFMAs of the next block are issued unconditionally (past the end
-    // they score a clamped duplicate that nobody reads): a branch around them
-    // would make the accumulator a phi, which the compiler resolves by
-    // copying it right after the MFMAs, stalling on their results.
-    auto step = [&](int j, f32x16& c, f32x16& d) __attribute__((always_inline)) {
-      mma_block((j + 1) & 1, d);
+    wait_vmcnt_le<LPW + (NOISE ? 16 : 0)>();
+    asm volatile("s_barrier" ::: "memory");
+    f32x16 x = f32x16{}, y;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const uint4 u = tile0[v * kWave + lane];
+#pragma unroll
+      for (int e = 0; e < OPV; ++e) x = Mfma<T>::mma(Mfma<T>::from_vec(u, e), qop[v * OPV + e], x);
+    }
+    // The MFMAs of the next block are issued unconditionally: a branch around
+    // them would make the accumulator a phi, which the compiler resolves by
+    // copying it right after the MFMAs, stalling on their results.  They are
+    // handed to body() as issue(i), i < NCH, which body calls between its
+    // element steps: a chain of dependent MFMAs issued back to back would
+    // hold the wave's issue slot until each finishes.
+    auto step = [&](int j, f32x16& c, f32x16& d, const uint4* rd, uint4* wr) __attribute__((always_inline)) {
+      wait_vmcnt_le<NOISE ? 16 : 0>();
+      asm volatile("s_barrier" ::: "memory");
+      dma(wr, min(bb + j + 2, be - 1));
+      uint4 u[VPL];
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) u[v] = rd[v * kWave + lane];
+      d = f32x16{};
+      auto issue = [&](int i) __attribute__((always_inline)) {
+        d = Mfma<T>::mma(Mfma<T>::from_vec(u[i / OPV], i % OPV), qop[i], d);
+      };
       const GVec gnext = fetch_noise(min(bb + j + 1, be - 1));
-      if (j < nb) body((bb + j) * 32, c, gcur);
+      body((bb + j) * 32, c, gcur, j < nb, issue);
       gcur = gnext;
-      stage(j & 1, pre);  // past the end: clamped duplicates, never read
-      pre = fetch(min(bb + j + 3, be - 1));
-      __syncthreads();
     };
     for (int j = 0; j < nb; j += 2) {
-      step(j, x, y);
-      step(j + 1, y, x);
+      step(j, x, y, tile1, tile0);
+      step(j + 1, y, x, tile0, tile1);
     }
   };
 
@@ -393,15 +397,21 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
 #pragma unroll
   for (int r = 0; r < 16; ++r) ma[r] = -INFINITY;
   const int p1_end = min(b_end, b_begin + p.pass1_blocks);
-  sweep(b_begin, p1_end, [&](int kb, const f32x16& c, const GVec& g) __attribute__((always_inline)) {
-    if (NOISE || kb + 32 > p.n) {
-      float sv[16], cl[NOISE ? 16 : 1];
-      lane_scores(kb, c, g, sv, cl);
+  // element r of 16 issues the next block's MFMA chunks [r*NCH/16, (r+1)*NCH/16)
+  auto issue_for = [&](int r, auto&& issue) __attribute__((always_inline)) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ma[r] = fmaxf(ma[r], sv[r]);
-    } else {
+    for (int i = r * NCH / 16; i < (r + 1) * NCH / 16; ++i) issue(i);
+  };
+  sweep(b_begin, p1_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
+                             __attribute__((always_inline)) {
+    float sv[16], cl[NOISE ? 16 : 1];
+    const bool raw = !NOISE && kb + 32 <= p.n;  // wave-uniform
+    if (!raw) lane_scores(kb, c, g, sv, cl);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) ma[r] = fmaxf(ma[r], c[r]);
+    for (int r = 0; r < 16; ++r) {
+      issue_for(r, issue);
+      const float v = raw ? c[r] : sv[r];
+      ma[r] = active ? fmaxf(ma[r], v) : ma[r];
     }
   });
   float mb[16];  // the partner lane's maxima
@@ -422,18 +432,20 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   st.thr = valid ? base_thr : INFINITY;
   st.wp = &mybuf[0][lane];
   uint2* const flush_at = &mybuf[kCand - 8][lane];
-  sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g) __attribute__((always_inline)) {
+  sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
+                            __attribute__((always_inline)) {
     float sv[16], cl[NOISE ? 16 : 1];
     lane_scores(kb, c, g, sv, cl);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      if (__ballot(st.wp > flush_at) != 0)
+      if (active && __ballot(st.wp > flush_at) != 0)
         flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int r = 8 * q + e;
+        issue_for(r, issue);
         const float x = sv[r];
-        if (x > st.thr) {
+        if (active && x > st.thr) {
           *st.wp = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3)));
           if (NOISE) {
             const int slot = (int)(st.wp - &mybuf[0][0]);
