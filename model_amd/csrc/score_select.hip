@@ -46,7 +46,7 @@
 namespace mpl {
 
 #ifndef MPL_CAND
-#define MPL_CAND 24
+#define MPL_CAND 22
 #endif
 constexpr int kCand = MPL_CAND;  // per-lane candidate buffer (entries)
 #ifndef MPL_SCORE_THREADS
