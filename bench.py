@@ -106,7 +106,6 @@ class Lookup:
         self.values = values
         self.T = 10.0
         f32, i32, u8 = torch.float32, torch.int32, torch.uint8
-        self.k_hat = torch.empty_like(self.sub_keys)
         self.packed = torch.empty(L.mpl_packed_keys_bytes(H, n, self.half, _lib.MPL_F16), dtype=u8, device=dev)
         self.ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, self.half, k)
         self.ws = torch.empty(max(1, self.ws_bytes), dtype=u8, device=dev)
@@ -124,8 +123,9 @@ class Lookup:
 
     def pack(self):
         p = self._lib.ptr
+        # inference needs only the packed operand, not the fp32 normalised keys
         self._lib.check(self.L.mpl_pack_keys(p(self.sub_keys), self.H, self.n, self.half, self._lib.MPL_F16,
-                                             p(self.k_hat), p(self.packed), self.stream), "pack")
+                                             None, p(self.packed), self.stream), "pack")
 
     def select(self):
         # raw queries: the scoring kernel l2-normalises them (memory.py:136)

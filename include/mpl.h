@@ -55,8 +55,9 @@ int mpl_l2_normalize(const float* x, int64_t rows, int dim, float eps, float* y,
 
 /*
  * memory.py:139: normalise sub_keys [H,2,n,half] (fp32) and pack them into
- * the MFMA operand layout consumed by mpl_score_select.  keys_hat [H,2,n,half]
- * fp32 (required) receives the normalised keys.  score_dtype selects the
+ * the MFMA operand layout consumed by mpl_score_select, in one pass.
+ * keys_hat [H,2,n,half] fp32 (optional, NULL = not written) receives the
+ * normalised keys (the backward needs them).  score_dtype selects the
  * scoring precision: MPL_F16 (fp16 MFMA, fp32 accumulate) or MPL_F32 (fp32
  * MFMA).  `packed` must hold mpl_packed_keys_bytes() bytes.
  */

@@ -29,6 +29,7 @@ template <>
 struct KeyPack<_Float16> {
   static constexpr int kChunk = 16;  // dims per MFMA
   static constexpr int kOpsPerVec = 1;
+  static constexpr bool kContiguous = true;  // a lane's dims of a vector are consecutive
   __host__ __device__ static int padded_half(int half) {
     return half <= 16 ? 16 : half <= 32 ? 32 : half <= 64 ? 64 : 128;
   }
@@ -47,6 +48,7 @@ template <>
 struct KeyPack<float> {
   static constexpr int kChunk = 2;
   static constexpr int kOpsPerVec = 4;
+  static constexpr bool kContiguous = false;
   __host__ __device__ static int padded_half(int half) {
     return half <= 8 ? 8 : half <= 16 ? 16 : half <= 32 ? 32 : half <= 64 ? 64 : 128;
   }

@@ -37,43 +37,79 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x
   }
 }
 
-// One thread per 16-byte operand vector of the packed layout (layout.h).
-template <typename T>
-__global__ __launch_bounds__(256) void pack_keys_kernel(const float* __restrict__ khat, int HC, int n,
-                                                        int half, int HP, int nblk,
+// Normalise and pack in one pass: one wave per (codebook, block of 32 keys).
+// Lane l owns exactly the dims of key l % 32 that the packed layout gives it
+// (the other half sits in lane l ^ 32), so one half-swap completes the row's
+// sum of squares and every lane writes its own operand vectors.
+// With few key blocks (small n) the VPL vectors of a block are spread over
+// `parts` waves (each recomputes the row norms and writes VPL / parts
+// vectors) so that the launch still fills the GPU.
+template <typename T, int VPL>
+__global__ __launch_bounds__(256) void norm_pack_kernel(const float* __restrict__ keys, int HC, int n, int half,
+                                                        int nblk, int parts, float* __restrict__ khat,
                                                         uint4* __restrict__ packed) {
-  const int vpl = KeyPack<T>::vectors_per_lane(HP);
-  const int64_t total = (int64_t)HC * nblk * vpl * kWave;
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (t >= total) return;
-  const int lane = (int)(t % kWave);
-  const int v = (int)((t / kWave) % vpl);
-  const int blk = (int)((t / ((int64_t)kWave * vpl)) % nblk);
-  const int hc = (int)(t / ((int64_t)kWave * vpl * nblk));
+  constexpr int PER = KeyPack<T>::elems_per_vector();
+  const int64_t w = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (w >= (int64_t)HC * nblk * parts) return;  // wave-uniform
+  const int part = (int)(w % parts);
+  const int hc = (int)(w / parts / nblk), blk = (int)(w / parts % nblk);
+  const int v0 = part * (VPL / parts), v1 = v0 + VPL / parts;
   const int key = blk * 32 + (lane & 31);
-  float e[8];
+  const bool kin = key < n;
+  const float* row = keys + ((int64_t)hc * n + (kin ? key : 0)) * half;
+  float e[VPL][PER];
+  float ss = 0.f;
+  if (KeyPack<T>::kContiguous && (half & 7) == 0) {
+    // fp16 packing: the lane's dims of vector v are 8 consecutive floats
 #pragma unroll
-  for (int i = 0; i < 8; ++i) e[i] = 0.f;
-  const int per = KeyPack<T>::elems_per_vector();
+    for (int v = 0; v < VPL; ++v) {
+      const int d0 = KeyPack<T>::dim_of(v, 0, lane);
+      const float4* src = (const float4*)(row + (d0 < half ? d0 : 0));  // clamped load, zeroed after
+      const float4 a = src[0], b = src[1];
+      const float x[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    if (i < per) {
-      const int dim = KeyPack<T>::dim_of(v, i, lane);
-      if (key < n && dim < half) e[i] = khat[((int64_t)hc * n + key) * half + dim];
+      for (int i = 0; i < PER; ++i) {
+        e[v][i] = (kin && d0 < half) ? x[i < 8 ? i : 0] : 0.f;
+        ss = fmaf(e[v][i], e[v][i], ss);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int dim = KeyPack<T>::dim_of(v, i, lane);
+        const float x = row[dim < half ? dim : 0];  // clamped load, zeroed after
+        e[v][i] = (kin && dim < half) ? x : 0.f;
+        ss = fmaf(e[v][i], e[v][i], ss);
+      }
+  }
+  float a = ss, b = ss;
+  half_swap(a, b);
+  const float r = 1.0f / sqrtf(ss + ((lane >> 5) ? a : b) + 1e-6f);
+  uint4* dst = packed + ((int64_t)hc * nblk + blk) * VPL * kWave;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    if (v < v0 || v >= v1) continue;
+#pragma unroll
+    for (int i = 0; i < PER; ++i) e[v][i] *= r;
+    dst[v * kWave + lane] = KeyPack<T>::pack(e[v]);
+  }
+  if (khat != nullptr && kin) {
+    float* kr = khat + ((int64_t)hc * n + key) * half;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      if (v < v0 || v >= v1) continue;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int dim = KeyPack<T>::dim_of(v, i, lane);
+        if (dim < half) kr[dim] = e[v][i];
+      }
     }
   }
-  packed[t] = KeyPack<T>::pack(e);
 }
 
-template <typename T>
-static int pack_impl(const float* khat, int HC, int n, int half, void* packed, hipStream_t s) {
-  const int HP = KeyPack<T>::padded_half(half);
-  const int nblk = (int)cdiv(n, 32);
-  const int64_t total = (int64_t)HC * nblk * KeyPack<T>::vectors_per_lane(HP) * kWave;
-  pack_keys_kernel<T><<<(unsigned)cdiv(total, 256), 256, 0, s>>>(khat, HC, n, half, HP, nblk,
-                                                                (uint4*)packed);
-  return check_launch("mpl_pack_keys");
-}
 
 }  // namespace mpl
 
@@ -109,12 +145,22 @@ extern "C" int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int 
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
               "mpl_pack_keys: score_dtype must be MPL_F16 or MPL_F32");
   hipStream_t s = (hipStream_t)stream;
-  const int64_t rows = (int64_t)2 * H * n;
-  float* khat = keys_hat;
-  MPL_REQUIRE(khat != nullptr, MPL_EINVAL, "mpl_pack_keys: keys_hat buffer is required");
-  l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, s>>>(sub_keys, rows, half, 1e-6f, khat, nullptr, nullptr);
-  int rc = check_launch("mpl_pack_keys(normalise)");
-  if (rc) return rc;
-  return score_dtype == MPL_F16 ? pack_impl<_Float16>(khat, 2 * H, n, half, packed, s)
-                                : pack_impl<float>(khat, 2 * H, n, half, packed, s);
+  const int HC = 2 * H;
+  const int nblk = (int)cdiv(n, 32);
+  const int vpl = score_dtype == MPL_F16 ? KeyPack<_Float16>::vectors_per_lane(KeyPack<_Float16>::padded_half(half))
+                                        : KeyPack<float>::vectors_per_lane(KeyPack<float>::padded_half(half));
+  int parts = 1;  // aim for >= 1024 waves
+  while (parts < vpl && (int64_t)HC * nblk * parts < 1024) parts *= 2;
+  const unsigned blocks = (unsigned)cdiv((int64_t)HC * nblk * parts, 256 / kWave);
+#define MPL_NP(T, V)                                                                                  \
+  norm_pack_kernel<T, V><<<blocks, 256, 0, s>>>(sub_keys, HC, n, half, nblk, parts, keys_hat, (uint4*)packed)
+  switch (vpl) {
+    case 1: if (score_dtype == MPL_F16) MPL_NP(_Float16, 1); else MPL_NP(float, 1); break;
+    case 2: if (score_dtype == MPL_F16) MPL_NP(_Float16, 2); else MPL_NP(float, 2); break;
+    case 4: if (score_dtype == MPL_F16) MPL_NP(_Float16, 4); else MPL_NP(float, 4); break;
+    case 8: if (score_dtype == MPL_F16) MPL_NP(_Float16, 8); else MPL_NP(float, 8); break;
+    default: MPL_NP(float, 16); break;  // fp32 packing of half = 128
+  }
+#undef MPL_NP
+  return check_launch("mpl_pack_keys");
 }
