@@ -295,7 +295,7 @@ class MemoryPool:
 
         def count_subkeys(ids):  # memory.py:199-201
             flat = (ids.long() + codebook[None]).reshape(-1)
-            return torch.bincount(flat, minlength=H * 2 * n).float().reshape(H, 2, n)
+            return _count(flat, H * 2 * n).reshape(H, 2, n)
 
         sl = slots.long()
         subkey_counts = count_subkeys(torch.stack([sl // n, sl % n], dim=2))
@@ -312,7 +312,7 @@ class MemoryPool:
         p = torch.softmax(p_scores, dim=-1)
         P = p.mean(0)
         balance = n * torch.mean(torch.sum(f * P, dim=-1))
-        slot_counts = torch.bincount(sl.reshape(-1), minlength=self.pool_size).float()
+        slot_counts = _count(sl.reshape(-1), self.pool_size)
         return {
             "balance_loss": balance,
             "subkey_counts": subkey_counts,
@@ -338,6 +338,15 @@ class MemoryPool:
                                  ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
               "mpl_score_select(clean)")
         return sub_idx
+
+
+def _count(ids: torch.Tensor, size: int) -> torch.Tensor:
+    """Occurrences of each id in [0, size) as float32, without a host sync
+    (torch.bincount reads the id range back to the host). Integer adds, so the
+    result does not depend on their order."""
+    c = torch.zeros(size, dtype=torch.int32, device=ids.device)
+    c.index_add_(0, ids, torch.ones(1, dtype=torch.int32, device=ids.device).expand(ids.shape[0]))
+    return c.float()
 
 
 # ------------------------------------------------------------------ autograd
