@@ -212,6 +212,58 @@ int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, const float* 
 /* *out = sum(x[0, n)) (+ *add if add != NULL), fixed order, fp64 accumulation. */
 int mpl_sum(const float* x, int64_t n, const float* add, float* out, void* stream);
 
+/*
+ * memory.py:199-204, 206-208, 215: routing counts from the selected ids.
+ *   subkey_counts [H,2,n] (or NULL): per codebook, how often each sub-key is
+ *     an index of a final slot (slots [M,H,k] int32: slot = a*n + b counts
+ *     a in codebook 0 and b in codebook 1 of its head);
+ *   clean_counts [H,2,n] (or NULL): occurrences of each sub-key in
+ *     clean_sub_idx [M,H,2,k] (the clean stage-1 ids; f = counts / (M k));
+ *   slot_counts [n*n] (or NULL): occurrences of each slot in `slots`.
+ * Outputs are overwritten.  Counts are fp32 whole numbers, exact (and so
+ * independent of the order of the additions) while below 2^24.  Ids outside
+ * their range are not counted.
+ */
+int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_idx, int64_t M, int H, int n, int k,
+                     float* subkey_counts, float* clean_counts, float* slot_counts, void* stream);
+
+/*
+ * memory.py:209-213 (fp16 scoring: half % 8 == 0, half <= 128): the
+ * load-balance loss
+ *   balance = n * mean_{h,c} sum_n f[h,c,n] * mean_m softmax_n(z[m,h,c,:])
+ * with z = cos(q, k_n) * T * (q_len if scaled), f = clean_counts / (M k), the
+ * cosine on fp16 MFMA tiles and each softmax taken over all n sub-keys in
+ * one online pass.  `scaled` = balance_temperature_grad && query_scale (the
+ * balance logits are then the query-scaled scores).  queries: raw fp32
+ * [M,H,2,half] (normalised inside).  packed_keys: from mpl_pack_keys with
+ * MPL_F16.  `state` (mpl_balance_state_bytes) receives per (token, codebook)
+ * the softmax statistics that mpl_balance_bwd needs; loss [1].
+ */
+size_t mpl_balance_state_bytes(int64_t M, int H);
+int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
+                    int64_t M, int H, int n, int half, int k, float temperature, void* state, float* loss,
+                    void* stream);
+
+/*
+ * Derivative of the balance loss (memory.py:209-213 under XLA autodiff, f
+ * held constant) for the upstream gradient g_balance (device scalar):
+ *   dq_hat [M,H,2,half]: d/d(normalised queries), written;
+ *   dk_hat [H,2,n,half]: d/d(normalised sub-keys), written;
+ * with balance_temperature_grad additionally
+ *   dlen [M,H,2] (query_scale only): d/d q_len, written;
+ *   dlogt [1]: the balance's share of d log_temperature.
+ * These are the *_extra inputs of mpl_lookup_bwd_queries / _keys and the
+ * `add` of mpl_sum.  q_hat from mpl_l2_normalize, k_hat from mpl_pack_keys,
+ * `state` from mpl_balance_fwd of the same inputs.  Two MFMA passes recompute
+ * the score tiles (no [M, n] tensor is formed).
+ */
+size_t mpl_balance_bwd_workspace_bytes(int64_t M, int H, int n, int half);
+int mpl_balance_bwd(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
+                    const float* clean_counts, const void* state, const float* g_balance,
+                    int balance_temperature_grad, int query_scale, int64_t M, int H, int n, int half, int k,
+                    float temperature, void* workspace, size_t workspace_bytes, float* dq_hat, float* dk_hat,
+                    float* dlen, float* dlogt, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,757 @@
+// Training-side routing statistics and the load-balance loss of
+// memory.py:196-215 on the GPU (fp16 MFMA scoring).
+//
+//   route_counts_kernel  subkey_counts from the final slots (memory.py:199-204),
+//                        the clean stage-1 counts behind f (:206-208) and
+//                        slot_counts (:215): integer histograms in LDS,
+//                        flushed with float atomics of whole numbers
+//   balance_fwd_kernel   per (token m, codebook hc), over all n sub-keys, the
+//                        log-sum-exp of the balance logits z_n = T_eff cos_n
+//                        and r_m = sum_n f_n softmax(z)_n, online in one sweep
+//                        of MFMA score tiles; balance = n/(2H M) sum r
+//                        (memory.py:210-213)
+//   balance_grad_kernel  the gradient of balance (dense over n) with respect
+//                        to the normalised queries and sub-keys, as two MFMA
+//                        passes that recompute the score tiles
+//
+// With f fixed (stop_gradient, memory.py:208) the loss is
+// n/(2H M) sum_{m,hc} r_m, so the gradient with respect to the logits is
+//   dz_mn = c p_mn (f_n - r_m),   c = g n / (2H M),
+// and with T_eff = T rho_m (rho_m = q_len_m when the balance logits are the
+// query-scaled scores, memory.py:210 with balance_temperature_grad, else 1)
+//   d q_hat_m = T rho_m sum_n dz_mn k_hat_n
+//   d k_hat_n = T sum_m dz_mn rho_m q_hat_m.
+// The MFMA operand p (f - r) is scaled per codebook by
+// sigma = 2^floor(log2(n/4)) / max_n f_n: |p (f - r)| <= max f, so the scaled
+// operand stays below n/4 while its typical size (about 1/n^2 unscaled) no
+// longer underflows fp16.
+#include <math.h>
+
+#include "common.h"
+#include "layout.h"
+#include "mfma.h"
+
+namespace mpl {
+namespace {
+
+constexpr int kBalThreads = 256;  // four waves
+constexpr int kBalWaves = kBalThreads / kWave;
+constexpr int kRowsPerGroup = 32 * kBalWaves;  // fixed-side rows per workgroup
+constexpr float kLog2e = 1.4426950408889634f;
+
+typedef Mfma<_Float16> MF;
+
+// ------------------------------------------------------------- counting
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ x, int64_t n) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0.f;
+}
+
+// Workgroup b covers head h = b % H and tokens [t0, t0 + tpg).  With use_lds
+// the two sub-key histograms and the two clean histograms of head h ([4][n]
+// ints) are built in LDS and added to the outputs once per workgroup.  Ids
+// outside their range are not counted.
+__global__ __launch_bounds__(256) void route_counts_kernel(const int32_t* __restrict__ slots,
+                                                           const int32_t* __restrict__ clean, int64_t M, int H,
+                                                           int n, int k, int64_t tpg, int use_lds,
+                                                           float* __restrict__ sub_counts,
+                                                           float* __restrict__ clean_counts,
+                                                           float* __restrict__ slot_counts) {
+  extern __shared__ int hist[];
+  const int tid = threadIdx.x;
+  const int h = blockIdx.x % H;
+  const int64_t t0 = (int64_t)(blockIdx.x / H) * tpg;
+  const int64_t t1 = t0 + tpg < M ? t0 + tpg : M;
+  const int64_t N = (int64_t)n * n;
+  const bool do_sub = sub_counts != nullptr;
+  const bool do_clean = clean_counts != nullptr && clean != nullptr;
+  if (use_lds) {
+    for (int i = tid; i < 4 * n; i += 256) hist[i] = 0;
+    __syncthreads();
+  }
+  if (t1 > t0) {
+    const int64_t ne = (t1 - t0) * k;
+    for (int64_t e = tid; e < ne; e += 256) {
+      const int64_t m = t0 + e / k;
+      const int j = (int)(e % k);
+      const int s = slots[(m * H + h) * k + j];
+      if (s < 0 || s >= N) continue;
+      if (slot_counts != nullptr) unsafeAtomicAdd(&slot_counts[s], 1.0f);
+      if (do_sub) {
+        const int a = s / n, b = s - a * n;
+        if (use_lds) {
+          atomicAdd(&hist[a], 1);
+          atomicAdd(&hist[n + b], 1);
+        } else {
+          unsafeAtomicAdd(&sub_counts[(2 * h) * n + a], 1.0f);
+          unsafeAtomicAdd(&sub_counts[(2 * h + 1) * n + b], 1.0f);
+        }
+      }
+    }
+    if (do_clean) {
+      const int64_t nc = (t1 - t0) * 2 * k;
+      for (int64_t e = tid; e < nc; e += 256) {
+        const int64_t m = t0 + e / (2 * k);
+        const int r = (int)(e % (2 * k));  // c * k + j
+        const int c = r / k;
+        const int i = clean[(m * H + h) * 2 * k + r];
+        if (i < 0 || i >= n) continue;
+        if (use_lds)
+          atomicAdd(&hist[(2 + c) * n + i], 1);
+        else
+          unsafeAtomicAdd(&clean_counts[(2 * h + c) * n + i], 1.0f);
+      }
+    }
+  }
+  if (use_lds) {
+    __syncthreads();
+    for (int i = tid; i < 4 * n; i += 256) {
+      const int v = hist[i];
+      const int which = i / n, key = i - which * n;
+      float* dst = which < 2 ? sub_counts : (do_clean ? clean_counts : nullptr);
+      if (v == 0 || dst == nullptr) continue;
+      unsafeAtomicAdd(&dst[(2 * h + (which & 1)) * n + key], (float)v);
+    }
+  }
+}
+
+// ------------------------------------------------------------- forward
+struct BalFwdParams {
+  const float* q;         // raw queries [M, HC, half]
+  const uint4* packed;    // packed sub-keys (fp16 layout)
+  const float* counts;    // clean counts [HC, n]
+  float inv_mk;           // 1 / (M k)
+  float T;
+  int scaled;             // T_eff = T * q_len
+  int64_t M;
+  int HC, n, half, nblk;
+  float4* state;          // [HC, M]: (log2-sum-exp2 of z log2e, r, T_eff log2e, 0)
+};
+
+// One block of 32 keys staged in LDS by the whole workgroup, plain loads
+// through registers, double buffered: iteration j computes on buffer j%2
+// while block j+1 waits in registers.
+template <int TILE>
+struct Stage {
+  static constexpr int kPer = (TILE + kBalThreads - 1) / kBalThreads;
+  uint4 r[kPer];
+  __device__ __forceinline__ void load(const uint4* src, int tid) {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = tid + i * kBalThreads;
+      r[i] = idx < TILE ? src[idx] : uint4{0, 0, 0, 0};
+    }
+  }
+  __device__ __forceinline__ void store(uint4* dst, int tid) const {
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int idx = tid + i * kBalThreads;
+      if (idx < TILE) dst[idx] = r[i];
+    }
+  }
+};
+
+// Lanes l and l+32 hold the same query; returns the partner lane's value.
+__device__ __forceinline__ float partner(float v, int par) {
+  float a = v, b = v;
+  half_swap(a, b);
+  return par ? a : b;
+}
+
+template <int HP>
+__global__ __launch_bounds__(kBalThreads) void balance_fwd_kernel(BalFwdParams p) {
+  constexpr int NCH = HP / 16;
+  constexpr int TILE = NCH * kWave;
+  __shared__ uint4 tiles[2][TILE];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, par = lane >> 5;
+  const int hc = blockIdx.x % p.HC;
+  const int64_t my_q = (int64_t)(blockIdx.x / p.HC) * kRowsPerGroup + wave * 32 + (lane & 31);
+  const bool valid = my_q < p.M;
+
+  // the raw query, normalised (memory.py:30-31, 136-137)
+  const float* qrow = p.q + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
+  float x[NCH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) MF::load_q_raw(qrow, valid, p.half, c, lane, x[c], ss);
+  const float tot = ss + partner(ss, par) + 1e-6f;
+  const float rn = 1.0f / sqrtf(tot);
+  half8 qop[NCH];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) qop[c] = MF::scale_q(x[c], rn);
+  const float rho = p.scaled ? sqrtf(tot) / sqrtf((float)p.half) : 1.f;
+  const float t2 = p.T * rho * kLog2e;
+
+  const float* cnt = p.counts + (int64_t)hc * p.n;
+  const uint4* kb = p.packed + (int64_t)hc * p.nblk * TILE;
+  Stage<TILE> st;
+  st.load(kb, tid);
+  st.store(tiles[0], tid);
+  __syncthreads();
+  // online base-2 log-sum-exp over this lane's keys: z2 <= mx, S = sum 2^(z2-mx), F = sum cnt 2^(z2-mx)
+  float mx = -INFINITY, S = 0.f, F = 0.f;
+  for (int blk = 0; blk < p.nblk; ++blk) {
+    const int cur = blk & 1;
+    if (blk + 1 < p.nblk) st.load(kb + (int64_t)(blk + 1) * TILE, tid);
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc = MF::mma(MF::from_vec(tiles[cur][c * kWave + lane], 0), qop[c], acc);
+    float z[16], fv[16];
+    float bm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = blk * 32 + 8 * (r >> 2) + 4 * par + (r & 3);
+      fv[r] = cnt[key < p.n ? key : p.n - 1];
+      z[r] = key < p.n ? acc[r] * t2 : -INFINITY;
+      bm = fmaxf(bm, z[r]);
+    }
+    if (bm > mx) {
+      const float sc = exp2f(mx - bm);  // 0 while mx is -inf
+      S *= sc;
+      F *= sc;
+      mx = bm;
+    }
+    const float mu = mx == -INFINITY ? 0.f : mx;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float e = exp2f(z[r] - mu);
+      S += e;
+      F = fmaf(fv[r], e, F);
+    }
+    if (blk + 1 < p.nblk) st.store(tiles[cur ^ 1], tid);
+    __syncthreads();
+  }
+  const float mo = partner(mx, par), So = partner(S, par), Fo = partner(F, par);
+  const float mm = fmaxf(mx, mo);
+  const float s1 = mx == -INFINITY ? 0.f : exp2f(mx - mm);
+  const float s2 = mo == -INFINITY ? 0.f : exp2f(mo - mm);
+  const float St = S * s1 + So * s2, Ft = F * s1 + Fo * s2;
+  if (valid && par == 0) p.state[(int64_t)hc * p.M + my_q] = make_float4(mm + log2f(St), Ft / St * p.inv_mk, t2, 0.f);
+}
+
+// balance = coef * sum of the r column of the state, fixed order.
+__global__ __launch_bounds__(1024) void balance_loss_kernel(const float4* __restrict__ state, int64_t count,
+                                                            float coef, float* __restrict__ loss) {
+  __shared__ double part[1024];
+  const int tid = threadIdx.x;
+  double s = 0.0;
+  for (int64_t i = tid; i < count; i += 1024) s += (double)state[i].y;
+  part[tid] = s;
+  __syncthreads();
+  for (int off = 512; off >= 1; off >>= 1) {
+    if (tid < off) part[tid] += part[tid + off];
+    __syncthreads();
+  }
+  if (tid == 0) *loss = (float)(part[0] * (double)coef);
+}
+
+// ------------------------------------------------------------- backward
+// Operand packs of fp32 rows X(hc, row, d) = X[hc*s_hc + row*s_row + d]
+// (rows >= nrows and dims >= half are zero), optionally times scale(hc, row):
+//   normal      out[hc][blk][v][lane]: lane l holds row 32 blk + l%32, dims
+//               16v + 8(l/32) + [0,8) (the scoring operand, as the sub-key
+//               pack of layout.h);
+//   transposed  out[hc][blk][db][c][lane]: lane l holds dim 32 db + l%32 of
+//               rows 32 blk + 16c + 8(j/4) + 4(l/32) + j%4, j < 8: the A
+//               operand that meets a score tile's registers 8c..8c+7 as the
+//               B operand (see the tile layout in mfma.h).
+template <bool TRANS, int HP>
+__global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict__ X, int64_t s_hc, int64_t s_row,
+                                                        int64_t nrows, int HC, int half,
+                                                        const float* __restrict__ scale, int64_t sc_hc,
+                                                        int64_t sc_row, int64_t nblk, uint4* __restrict__ out) {
+  constexpr int NCH = HP / 16;
+  constexpr int ND = (HP + 31) / 32;
+  constexpr int PER_BLK = TRANS ? ND * 2 : NCH;  // 16-byte vectors per lane per block
+  const int64_t total = (int64_t)HC * nblk * PER_BLK * kWave;
+  for (int64_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
+    const int lane = (int)(t % kWave);
+    const int64_t u = t / kWave;
+    const int w = (int)(u % PER_BLK);
+    const int64_t blk = (u / PER_BLK) % nblk;
+    const int hc = (int)(u / PER_BLK / nblk);
+    const float* base = X + (int64_t)hc * s_hc;
+    float e[8];
+    if (!TRANS) {
+      const int64_t row = blk * 32 + (lane & 31);
+      const int d0 = 16 * w + 8 * (lane >> 5);
+      const bool ok = row < nrows && d0 < half;
+      const float sc = (ok && scale != nullptr) ? scale[hc * sc_hc + row * sc_row] : 1.f;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) e[i] = ok ? base[row * s_row + d0 + i] * sc : 0.f;
+    } else {
+      const int c = w & 1, db = w >> 1;
+      const int d = 32 * db + (lane & 31);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int64_t row = blk * 32 + 16 * c + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+        const bool ok = row < nrows && d < half;
+        const float sc = (ok && scale != nullptr) ? scale[hc * sc_hc + row * sc_row] : 1.f;
+        e[j] = ok ? base[row * s_row + d] * sc : 0.f;
+      }
+    }
+    out[t] = KeyPack<_Float16>::pack(e);
+  }
+}
+
+// sigma[hc] = 2^floor(log2(n/4)) / max(f), with f = counts / (M k).
+__global__ __launch_bounds__(256) void balance_sigma_kernel(const float* __restrict__ counts, int n, float inv_mk,
+                                                            float* __restrict__ sigma) {
+  __shared__ float part[256];
+  const int hc = blockIdx.x;
+  float m = 0.f;
+  for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, counts[(int64_t)hc * n + i]);
+  part[threadIdx.x] = m;
+  __syncthreads();
+  for (int off = 128; off >= 1; off >>= 1) {
+    if (threadIdx.x < off) part[threadIdx.x] = fmaxf(part[threadIdx.x], part[threadIdx.x + off]);
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const float p2 = exp2f(floorf(log2f(fmaxf((float)n * 0.25f, 1.f))));
+    const float fmax = part[0] * inv_mk;
+    sigma[hc] = fmax > 0.f ? p2 / fmax : 1.f;
+  }
+}
+
+struct BalGradParams {
+  const uint4* fix;     // fixed side, normal pack [HC][fblk][NCH][64]
+  const uint4* str;     // streamed side, normal pack [HC][sblk][NCH][64]
+  const uint4* strT;    // streamed side, transposed pack [HC][sblk][ND][2][64]
+  const float4* state;  // [HC, M] from the forward
+  const float* counts;  // clean counts [HC, n]
+  const float* sigma;   // [HC]
+  const float* g;       // d loss / d balance (device scalar)
+  float inv_mk, coef;   // 1 / (M k), n / (HC M)
+  float T;
+  int64_t M;
+  int HC, n, half;
+  int64_t fblk, sblk;  // blocks of 32 rows on the fixed / streamed side
+  int splits;
+  int64_t sblk_per_split;
+  const float* rho;  // [M, HC] (DK: folded into the streamed pack already; DQ: output scale) or null
+  float* out;        // DQ: d q_hat [M, HC, half]; DK: partial d k_hat [splits, HC, n, half]
+  float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null
+};
+
+// DK = false: the fixed side is 32 queries per wave (B operand), sub-key
+// blocks stream; DK = true: the fixed side is 32 sub-keys per wave, blocks of
+// 32 queries stream (the query range is split over `splits` workgroups).
+// Each streamed block: score tile C (rows = streamed, columns = fixed), the
+// scaled operand g = sigma p (f - r) in fp16, and for every 32-dim block db
+// of the output  acc[db] += strT[db] . g  (two MFMAs, K = 16 rows each).
+template <bool DK, int HP>
+__global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams p) {
+  constexpr int NCH = HP / 16;
+  constexpr int ND = (HP + 31) / 32;
+  constexpr int TN = NCH * kWave, TT = ND * 2 * kWave, TILE = TN + TT;
+  __shared__ uint4 tiles[2][TILE];
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, par = lane >> 5;
+  const int hc = blockIdx.x % p.HC;
+  const int64_t rest = blockIdx.x / p.HC;
+  const int split = (int)(rest % p.splits);
+  const int64_t fg = rest / p.splits;
+  const int64_t fb = fg * kBalWaves + wave;  // this wave's fixed block
+  const int64_t nfix = DK ? p.n : p.M;
+  const int64_t nstr = DK ? p.M : p.n;
+  const int64_t my_f = fb * 32 + (lane & 31);
+  const bool valid = my_f < nfix;
+  const int64_t fbc = fb < p.fblk ? fb : p.fblk - 1;
+
+  half8 fop[NCH];
+  {
+    const uint4* src = p.fix + ((int64_t)hc * p.fblk + fbc) * TN;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) fop[c] = MF::from_vec(src[c * kWave + lane], 0);
+  }
+  const float sig = p.sigma[hc];
+  const float fs = p.inv_mk * sig;  // scaled f per count
+  const float* cnt = p.counts + (int64_t)hc * p.n;
+  const float4* sth = p.state + (int64_t)hc * p.M;
+  // per-lane constants of the fixed row
+  float4 fst = make_float4(0.f, 0.f, 0.f, 0.f);
+  float ffix = 0.f;
+  if (DK)
+    ffix = cnt[valid ? my_f : 0] * fs;
+  else
+    fst = sth[valid ? my_f : 0];
+  const float rs_fix = fst.y * sig;
+
+  const int64_t sb0 = (int64_t)split * p.sblk_per_split;
+  const int64_t sb1 = sb0 + p.sblk_per_split < p.sblk ? sb0 + p.sblk_per_split : p.sblk;
+  f32x16 gacc[ND];
+#pragma unroll
+  for (int db = 0; db < ND; ++db) gacc[db] = f32x16{};
+  float usum = 0.f;
+
+  const uint4* sN = p.str + (int64_t)hc * p.sblk * TN;
+  const uint4* sT = p.strT + (int64_t)hc * p.sblk * TT;
+  Stage<TN> stn;
+  Stage<TT> stt;
+  if (sb0 < sb1) {
+    stn.load(sN + sb0 * TN, tid);
+    stt.load(sT + sb0 * TT, tid);
+    stn.store(tiles[0], tid);
+    stt.store(tiles[0] + TN, tid);
+  }
+  __syncthreads();
+  for (int64_t sb = sb0; sb < sb1; ++sb) {
+    const int cur = (int)((sb - sb0) & 1);
+    const bool more = sb + 1 < sb1;
+    if (more) {
+      stn.load(sN + (sb + 1) * TN, tid);
+      stt.load(sT + (sb + 1) * TT, tid);
+    }
+    f32x16 acc = f32x16{};
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) acc = MF::mma(MF::from_vec(tiles[cur][c * kWave + lane], 0), fop[c], acc);
+    float gv[16];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = sb * 32 + 8 * (r >> 2) + 4 * par + (r & 3);
+      const bool rv = row < nstr;
+      const int64_t rc = rv ? row : 0;
+      float pe, diff;
+      if (DK) {
+        const float4 s = sth[rc];  // the streamed query's state
+        pe = exp2f(acc[r] * s.z - s.x);
+        diff = ffix - s.y * sig;
+      } else {
+        pe = exp2f(acc[r] * fst.z - fst.x);
+        diff = cnt[rc] * fs - rs_fix;
+      }
+      gv[r] = (rv && valid) ? pe * diff : 0.f;
+      if (!DK) usum = fmaf(gv[r], acc[r], usum);
+    }
+    half8 b0, b1;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      b0[j] = (_Float16)gv[j];
+      b1[j] = (_Float16)gv[8 + j];
+    }
+    const uint4* tt = tiles[cur] + TN;
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      gacc[db] = MF::mma(MF::from_vec(tt[(db * 2) * kWave + lane], 0), b0, gacc[db]);
+      gacc[db] = MF::mma(MF::from_vec(tt[(db * 2 + 1) * kWave + lane], 0), b1, gacc[db]);
+    }
+    if (more) {
+      stn.store(tiles[cur ^ 1], tid);
+      stt.store(tiles[cur ^ 1] + TN, tid);
+    }
+    __syncthreads();
+  }
+
+  // d = c T (rho) / sigma * acc; rows of the output are the fixed rows
+  const float cc = *p.g * p.coef;
+  float scale = cc * p.T / sig;
+  if (!DK && p.rho != nullptr) scale *= p.rho[(valid ? my_f : 0) * p.HC + hc];
+  if (!DK && p.u != nullptr) {
+    const float ut = usum + partner(usum, par);
+    if (valid && par == 0) p.u[(int64_t)hc * p.M + my_f] = ut * cc / sig;
+  }
+  if (!valid) return;
+  float* orow = DK ? p.out + (((int64_t)split * p.HC + hc) * p.n + my_f) * p.half
+                   : p.out + (my_f * p.HC + hc) * (int64_t)p.half;
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int g4 = 0; g4 < 4; ++g4) {
+      const int d = 32 * db + 8 * g4 + 4 * par;
+      if (d < p.half)
+        *(float4*)(orow + d) = make_float4(gacc[db][4 * g4] * scale, gacc[db][4 * g4 + 1] * scale,
+                                           gacc[db][4 * g4 + 2] * scale, gacc[db][4 * g4 + 3] * scale);
+    }
+}
+
+// out[i] = sum over s of part[s][i], in split order (count % 4 == 0).
+__global__ __launch_bounds__(256) void split_sum_kernel(const float4* __restrict__ part, int splits, int64_t count4,
+                                                        float4* __restrict__ out) {
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < count4; i += (int64_t)gridDim.x * 256) {
+    float4 s = part[i];
+    for (int k = 1; k < splits; ++k) {
+      const float4 v = part[(int64_t)k * count4 + i];
+      s.x += v.x;
+      s.y += v.y;
+      s.z += v.z;
+      s.w += v.w;
+    }
+    out[i] = s;
+  }
+}
+
+// dlen[m, hc] = T u (query_scale); part[m, hc] = T rho u (d log_t terms).
+__global__ __launch_bounds__(256) void balance_temp_kernel(const float* __restrict__ u, const float* __restrict__ rho,
+                                                           int64_t M, int HC, float T, float* __restrict__ dlen,
+                                                           float* __restrict__ part) {
+  const int64_t total = M * HC;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
+    const int64_t m = i / HC;
+    const int hc = (int)(i % HC);
+    const float v = u[(int64_t)hc * M + m];
+    if (dlen != nullptr) dlen[i] = T * v;
+    part[i] = T * (rho != nullptr ? rho[i] : 1.f) * v;
+  }
+}
+
+__global__ __launch_bounds__(1024) void sum_plain_kernel(const float* __restrict__ x, int64_t n, float* __restrict__ out) {
+  __shared__ double part[1024];
+  const int tid = threadIdx.x;
+  double s = 0.0;
+  for (int64_t i = tid; i < n; i += 1024) s += (double)x[i];
+  part[tid] = s;
+  __syncthreads();
+  for (int off = 512; off >= 1; off >>= 1) {
+    if (tid < off) part[tid] += part[tid + off];
+    __syncthreads();
+  }
+  if (tid == 0) *out = (float)part[0];
+}
+
+size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+bool balance_shape_ok(int half) { return half >= 8 && half <= 128 && half % 8 == 0; }
+
+unsigned grid_for(int64_t items, int64_t per_block, unsigned cap = 4096) {
+  int64_t g = cdiv(items, per_block);
+  if (g < 1) g = 1;
+  return (unsigned)(g < cap ? g : cap);
+}
+
+struct BwdLayout {
+  size_t qn, qt, kt, sigma, part, u, tpart, total;
+  int HP, NCH, ND, splits;
+  int64_t mblk, nblk, sbps;
+};
+
+BwdLayout bwd_layout(int64_t M, int H, int n, int half) {
+  BwdLayout L;
+  const int HC = 2 * H;
+  L.HP = KeyPack<_Float16>::padded_half(half);
+  L.NCH = L.HP / 16;
+  L.ND = (L.HP + 31) / 32;
+  L.mblk = cdiv(M, 32);
+  L.nblk = cdiv(n, 32);
+  // the sub-key-side pass: HC * ceil(n / 128) workgroups, the query range
+  // split so that about 512 run
+  const int64_t kgroups = (int64_t)HC * cdiv(n, kRowsPerGroup);
+  int64_t sp = cdiv(512, kgroups);
+  if (sp > L.mblk) sp = L.mblk;
+  if (sp < 1) sp = 1;
+  L.sbps = cdiv(L.mblk, sp);
+  L.splits = (int)cdiv(L.mblk, L.sbps);
+  size_t o = 0;
+  L.qn = o;
+  o += al256((size_t)HC * L.mblk * L.NCH * kWave * 16);
+  L.qt = o;
+  o += al256((size_t)HC * L.mblk * L.ND * 2 * kWave * 16);
+  L.kt = o;
+  o += al256((size_t)HC * L.nblk * L.ND * 2 * kWave * 16);
+  L.sigma = o;
+  o += al256((size_t)HC * 4);
+  L.part = o;
+  o += al256((size_t)L.splits * HC * n * half * 4);
+  L.u = o;
+  o += al256((size_t)HC * M * 4);
+  L.tpart = o;
+  o += al256((size_t)HC * M * 4);
+  L.total = o;
+  return L;
+}
+
+template <bool TRANS>
+void launch_pack(int HP, const float* X, int64_t s_hc, int64_t s_row, int64_t nrows, int HC, int half,
+                 const float* scale, int64_t sc_hc, int64_t sc_row, int64_t nblk, uint4* out, hipStream_t s) {
+  const int ND = (HP + 31) / 32;
+  const int64_t total = (int64_t)HC * nblk * (TRANS ? ND * 2 : HP / 16) * kWave;
+  const unsigned g = grid_for(total, 256, 8192);
+#define MPL_PACK(HPV) \
+  pack_rows_kernel<TRANS, HPV><<<g, 256, 0, s>>>(X, s_hc, s_row, nrows, HC, half, scale, sc_hc, sc_row, nblk, out)
+  switch (HP) {
+    case 16: MPL_PACK(16); break;
+    case 32: MPL_PACK(32); break;
+    case 64: MPL_PACK(64); break;
+    default: MPL_PACK(128); break;
+  }
+#undef MPL_PACK
+}
+
+}  // namespace
+}  // namespace mpl
+
+using namespace mpl;
+
+extern "C" int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_idx, int64_t M, int H, int n, int k,
+                                float* subkey_counts, float* clean_counts, float* slot_counts, void* stream) {
+  clear_error();
+  MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_route_counts: bad shape");
+  MPL_REQUIRE(M == 0 || slots != nullptr || (subkey_counts == nullptr && slot_counts == nullptr), MPL_EINVAL,
+              "mpl_route_counts: slots is null");
+  MPL_REQUIRE(clean_counts == nullptr || M == 0 || clean_sub_idx != nullptr, MPL_EINVAL,
+              "mpl_route_counts: clean_counts needs clean_sub_idx");
+  hipStream_t s = (hipStream_t)stream;
+  const int64_t hn = (int64_t)H * 2 * n;
+  if (subkey_counts) fill_zero_kernel<<<grid_for(hn, 256), 256, 0, s>>>(subkey_counts, hn);
+  if (clean_counts) fill_zero_kernel<<<grid_for(hn, 256), 256, 0, s>>>(clean_counts, hn);
+  if (slot_counts) fill_zero_kernel<<<grid_for((int64_t)n * n, 256), 256, 0, s>>>(slot_counts, (int64_t)n * n);
+  if (M > 0 && (subkey_counts || clean_counts || slot_counts)) {
+    const int use_lds = n <= 4096 ? 1 : 0;
+    int64_t tpg = use_lds ? cdiv(16 * (int64_t)n, 3 * (int64_t)k) : 32;
+    if (tpg < 64) tpg = 64;
+    const int64_t min_tpg = cdiv(M * H, 2048);
+    if (tpg < min_tpg) tpg = min_tpg;
+    const int64_t groups = (int64_t)H * cdiv(M, tpg);
+    route_counts_kernel<<<(unsigned)groups, 256, use_lds ? 16 * n : 0, s>>>(
+        slots, clean_sub_idx, M, H, n, k, tpg, use_lds, subkey_counts, clean_counts, slot_counts);
+  }
+  return check_launch("mpl_route_counts");
+}
+
+extern "C" size_t mpl_balance_state_bytes(int64_t M, int H) { return (size_t)(M > 0 ? M : 0) * 2 * H * 16; }
+
+extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
+                               int64_t M, int H, int n, int half, int k, float temperature, void* state,
+                               float* loss, void* stream) {
+  clear_error();
+  MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_balance_fwd: bad shape");
+  MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
+              "mpl_balance_fwd: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  MPL_REQUIRE(loss != nullptr && (M == 0 || (queries && packed_keys && clean_counts && state)), MPL_EINVAL,
+              "mpl_balance_fwd: null buffer");
+  hipStream_t s = (hipStream_t)stream;
+  const int HC = 2 * H;
+  if (M == 0) {
+    fill_zero_kernel<<<1, 256, 0, s>>>(loss, 1);
+    return check_launch("mpl_balance_fwd");
+  }
+  BalFwdParams p;
+  p.q = queries;
+  p.packed = (const uint4*)packed_keys;
+  p.counts = clean_counts;
+  p.inv_mk = (float)(1.0 / ((double)M * k));
+  p.T = temperature;
+  p.scaled = scaled ? 1 : 0;
+  p.M = M;
+  p.HC = HC;
+  p.n = n;
+  p.half = half;
+  p.nblk = (int)cdiv(n, 32);
+  p.state = (float4*)state;
+  const unsigned grid = (unsigned)(HC * cdiv(M, kRowsPerGroup));
+  switch (KeyPack<_Float16>::padded_half(half)) {
+    case 16: balance_fwd_kernel<16><<<grid, kBalThreads, 0, s>>>(p); break;
+    case 32: balance_fwd_kernel<32><<<grid, kBalThreads, 0, s>>>(p); break;
+    case 64: balance_fwd_kernel<64><<<grid, kBalThreads, 0, s>>>(p); break;
+    default: balance_fwd_kernel<128><<<grid, kBalThreads, 0, s>>>(p); break;
+  }
+  balance_loss_kernel<<<1, 1024, 0, s>>>((const float4*)state, M * HC, (float)((double)n / ((double)HC * M)), loss);
+  return check_launch("mpl_balance_fwd");
+}
+
+extern "C" size_t mpl_balance_bwd_workspace_bytes(int64_t M, int H, int n, int half) {
+  if (M < 0 || H < 1 || n < 1 || !balance_shape_ok(half)) return 0;
+  return bwd_layout(M, H, n, half).total;
+}
+
+extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
+                               const float* clean_counts, const void* state, const float* g_balance,
+                               int balance_temperature_grad, int query_scale, int64_t M, int H, int n, int half,
+                               int k, float temperature, void* workspace, size_t workspace_bytes, float* dq_hat,
+                               float* dk_hat, float* dlen, float* dlogt, void* stream) {
+  clear_error();
+  MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_balance_bwd: bad shape");
+  MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
+              "mpl_balance_bwd: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  const bool btg = balance_temperature_grad != 0;
+  const bool scaled = btg && query_scale != 0;
+  MPL_REQUIRE(dk_hat != nullptr && (!btg || dlogt != nullptr), MPL_EINVAL, "mpl_balance_bwd: null output");
+  MPL_REQUIRE(!scaled || M == 0 || q_len != nullptr, MPL_EINVAL, "mpl_balance_bwd: q_len needed with query_scale");
+  hipStream_t s = (hipStream_t)stream;
+  const int HC = 2 * H;
+  if (M == 0) {
+    fill_zero_kernel<<<grid_for((int64_t)HC * n * half, 256), 256, 0, s>>>(dk_hat, (int64_t)HC * n * half);
+    if (btg) fill_zero_kernel<<<1, 256, 0, s>>>(dlogt, 1);
+    return check_launch("mpl_balance_bwd");
+  }
+  MPL_REQUIRE(q_hat && k_hat && packed_keys && clean_counts && state && g_balance && dq_hat, MPL_EINVAL,
+              "mpl_balance_bwd: null buffer");
+  const BwdLayout L = bwd_layout(M, H, n, half);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
+              "mpl_balance_bwd: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+  char* ws = (char*)workspace;
+  uint4* qn = (uint4*)(ws + L.qn);
+  uint4* qt = (uint4*)(ws + L.qt);
+  uint4* kt = (uint4*)(ws + L.kt);
+  float* sigma = (float*)(ws + L.sigma);
+  float* part = (float*)(ws + L.part);
+  float* u = (float*)(ws + L.u);
+  float* tpart = (float*)(ws + L.tpart);
+  const float* rho = scaled ? q_len : nullptr;
+
+  launch_pack<false>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
+  launch_pack<true>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, rho, 1, HC, L.mblk, qt, s);
+  launch_pack<true>(L.HP, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
+  const float inv_mk = (float)(1.0 / ((double)M * k));
+  balance_sigma_kernel<<<HC, 256, 0, s>>>(clean_counts, n, inv_mk, sigma);
+
+  BalGradParams p;
+  p.state = (const float4*)state;
+  p.counts = clean_counts;
+  p.sigma = sigma;
+  p.g = g_balance;
+  p.inv_mk = inv_mk;
+  p.coef = (float)((double)n / ((double)HC * M));
+  p.T = temperature;
+  p.M = M;
+  p.HC = HC;
+  p.n = n;
+  p.half = half;
+  p.rho = rho;
+
+  // d q_hat: fixed = queries, streamed = sub-keys
+  BalGradParams pq = p;
+  pq.fix = qn;
+  pq.str = (const uint4*)packed_keys;
+  pq.strT = kt;
+  pq.fblk = L.mblk;
+  pq.sblk = L.nblk;
+  pq.splits = 1;
+  pq.sblk_per_split = L.nblk;
+  pq.out = dq_hat;
+  pq.u = btg ? u : nullptr;
+  const unsigned gq = (unsigned)(HC * cdiv(M, kRowsPerGroup));
+  // d k_hat: fixed = sub-keys, streamed = queries
+  BalGradParams pk = p;
+  pk.fix = (const uint4*)packed_keys;
+  pk.str = qn;
+  pk.strT = qt;
+  pk.fblk = L.nblk;
+  pk.sblk = L.mblk;
+  pk.splits = L.splits;
+  pk.sblk_per_split = L.sbps;
+  pk.out = L.splits == 1 ? dk_hat : part;
+  pk.u = nullptr;
+  pk.rho = nullptr;
+  const unsigned gk = (unsigned)(HC * cdiv(n, kRowsPerGroup) * L.splits);
+#define MPL_GRAD(HPV)                                                  \
+  balance_grad_kernel<false, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
+  balance_grad_kernel<true, HPV><<<gk, kBalThreads, 0, s>>>(pk)
+  switch (L.HP) {
+    case 16: MPL_GRAD(16); break;
+    case 32: MPL_GRAD(32); break;
+    case 64: MPL_GRAD(64); break;
+    default: MPL_GRAD(128); break;
+  }
+#undef MPL_GRAD
+  if (L.splits > 1) {
+    const int64_t c4 = (int64_t)HC * n * half / 4;
+    split_sum_kernel<<<grid_for(c4, 256), 256, 0, s>>>((const float4*)part, L.splits, c4, (float4*)dk_hat);
+  }
+  if (btg) {
+    balance_temp_kernel<<<grid_for(M * HC, 256), 256, 0, s>>>(u, rho, M, HC, temperature, query_scale ? dlen : nullptr,
+                                                             tpart);
+    sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, M * HC, dlogt);
+  }
+  return check_launch("mpl_balance_bwd");
+}

@@ -2,38 +2,43 @@
 // top-k (memory.py:149-164), then stage-2 top-k over the k*k candidates and
 // the routing softmax (memory.py:167-178).
 //
-// Stage 1 (score_topk_kernel).  A workgroup owns 128 queries (two waves of
-// 64) of one codebook hc = h*2 + c and one split of the n sub-keys.  Key
-// blocks of 32 stream through LDS (double buffered); each wave computes a
-// 32-key x 64-query score tile with two 32x32 MFMA chains.  Two passes:
+// Stage 1 (score_topk_kernel).  A workgroup of two waves handles one
+// codebook hc = h*2 + c and one split of its n sub-keys; each wave owns 32
+// queries.  The queries are normalised in registers (or read normalised) and
+// held as the MFMA B operand; key blocks of 32 stream through two LDS buffers
+// by LDS DMA, and each block is one chain of 32x32 MFMAs (keys = A operand).
+// Lanes l and l+32 share query l%32 and see alternate groups of 4 keys.  Two
+// passes:
 //   1. a bound pass over the first blocks of the split keeps, per register
 //      position, the running maximum; the k-th largest of a query's 32
-//      maxima is a score that at least k distinct keys reach, so it bounds
-//      the k-th best from below;
-//   2. a select pass over the whole split swaps register halves across lanes
-//      (v_permlane32_swap) so that lane l owns query l with all 32 scores of
-//      the block, appends scores above the lane's threshold to its column of
-//      an LDS buffer, and, when any lane's buffer fills, sorts the buffered
-//      candidates in chunks of 8 and bitonic-merges them into the lane's
-//      register list of the best k (topk.h), raising the threshold to the
-//      k-th best so far.
+//      maxima (the lane pair exchanges them with v_permlane32_swap) is a
+//      score that at least k distinct keys reach, so it bounds the k-th best
+//      from below;
+//   2. a select pass over the whole split appends scores at or above the
+//      lane's threshold to its column of an LDS buffer and, when any column
+//      may overflow, sorts the buffered candidates in chunks of 8 and
+//      bitonic-merges them into the lane's register list of the best k
+//      (topk.h), raising the threshold to the k-th best so far.  At the end
+//      the two lanes of a query merge their lists.
 // Keys of equal score order by index, so the result is exactly lax.top_k's.
-// The MFMAs of block j+1 are issued before the selection work of block j, so
+// The MFMAs of block j+1 are issued between the element steps of block j, so
 // the matrix cores and the VALU overlap.  Scores never leave registers/LDS.
 //
 // Without routing noise the selection runs on the raw cosine: scores are
 // cos*T(*q_len) with positive per-query factors, so the order is the same up
 // to ties created by the rounding of that product (near-ties).
 //
-// Split plans.  Few tokens cannot fill the GPU with one workgroup per 128
+// Split plans.  Few tokens cannot fill the GPU with one workgroup per 64
 // queries, so the key range of each codebook is split across workgroups and
-// the per-split lists are merged in stage 2.
+// the per-split lists are merged (merge_splits_k16 reduces eight lists per
+// 16-lane row at a time) before stage 2.
 //
-// Stage 2 (pair_kernel).  A group of 16 (k <= 16) or 32 lanes per (token,
-// head) merges the split lists of both codebooks with cross-lane bitonic
-// merges, walks the k*k candidate grid as sorted row lists keyed by (select
-// sum desc, flat index rank_a*k + rank_b asc) as memory.py:171, and finishes
-// with the softmax of the clean slot scores (memory.py:178).
+// Stage 2 (pair_kernel_k16 for k = 16, pair_kernel<G> otherwise).  A row of
+// 16 lanes (k <= 16) or a group of 32 per (token, head) merges the lists of
+// both codebooks, walks the k*k candidate grid as sorted row lists keyed by
+// (select sum desc, flat index rank_a*k + rank_b asc) as memory.py:171, and
+// finishes with the softmax of the clean slot scores (memory.py:178).  The
+// k = 16 kernel exchanges values with DPP and ds_swizzle only.
 #include <limits.h>
 
 #include <algorithm>
@@ -41,6 +46,7 @@
 
 #include "common.h"
 #include "layout.h"
+#include "mfma.h"
 #include "topk.h"
 
 namespace mpl {
@@ -71,76 +77,6 @@ struct ScoreParams {
   float* out_sel;    // [splits, HC, k, M] (null without noise: equals clean)
   float* out_clean;  // [splits, HC, k, M]
   int* out_idx;      // [splits, HC, k, M]
-};
-
-template <typename T>
-struct Mfma;
-
-template <>
-struct Mfma<_Float16> {
-  typedef half8 Op;
-  __device__ static f32x16 mma(Op a, Op b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-  // B operand for chunk c: dims 16c + 8*(lane/32) + [0,8) of fp16 query row
-  // q (fp16 scoring requires half % 8 == 0, so this is one aligned 16-byte
-  // load).  Unconditional and zeroed after: a guarded load compiles to a
-  // branch with its own wait, serialising every chunk.
-  __device__ static Op load_q(const _Float16* q, bool valid, int half, int c, int lane) {
-    const int d0 = 16 * c + 8 * (lane >> 5);
-    Op o = *(const half8*)(q + (d0 < half ? d0 : 0));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (valid && d0 < half) ? o[i] : (_Float16)0.f;
-    return o;
-  }
-  __device__ static Op from_vec(uint4 u, int) { return __builtin_bit_cast(half8, u); }
-  // Raw fp32 query dims 16c + 8*(lane/32) + [0,8): two aligned 16-byte loads,
-  // zeroed after when out of range; adds their squares to ss.
-  static constexpr int kQElems = 8;
-  __device__ static void load_q_raw(const float* q, bool valid, int half, int c, int lane, float* x, float& ss) {
-    const int d0 = 16 * c + 8 * (lane >> 5);
-    const bool ok = valid && d0 < half;
-    const float4* src = (const float4*)(q + (d0 < half ? d0 : 0));
-    const float4 u = src[0], v = src[1];
-    x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
-    x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      x[i] = ok ? x[i] : 0.f;
-      ss = fmaf(x[i], x[i], ss);
-    }
-  }
-  __device__ static Op scale_q(const float* x, float r) {
-    Op o;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (_Float16)(x[i] * r);
-    return o;
-  }
-};
-
-template <>
-struct Mfma<float> {
-  typedef float Op;
-  __device__ static f32x16 mma(Op a, Op b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-  }
-  __device__ static Op load_q(const float* q, bool valid, int half, int c, int lane) {
-    const int d = 2 * c + (lane >> 5);
-    const float f = q[min(d, half - 1)];
-    return (valid && d < half) ? f : 0.f;
-  }
-  __device__ static Op from_vec(uint4 u, int e) {
-    const unsigned w = e == 0 ? u.x : e == 1 ? u.y : e == 2 ? u.z : u.w;
-    return __uint_as_float(w);
-  }
-  static constexpr int kQElems = 1;
-  __device__ static void load_q_raw(const float* q, bool valid, int half, int c, int lane, float* x, float& ss) {
-    const int d = 2 * c + (lane >> 5);
-    const float f = q[min(d, half - 1)];
-    x[0] = (valid && d < half) ? f : 0.f;
-    ss = fmaf(x[0], x[0], ss);
-  }
-  __device__ static Op scale_q(const float* x, float r) { return x[0] * r; }
 };
 
 // Per-lane selection state of the stage-1 kernel.  Candidates are appended
@@ -216,16 +152,6 @@ __device__ __forceinline__ float kth_of_32(const float* a, const float* b, int k
   for (int i = 0; i < 32; ++i) t |= v[i] & (0u - (uint32_t)(i == k - 1));
   return from_orderable(t);
 }
-
-// s_waitcnt that waits until at most N vector-memory loads of this wave are
-// outstanding (gfx9 encoding; expcnt and lgkmcnt left at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt_le() {
-  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-typedef __attribute__((address_space(3))) void lds_void;
 
 template <typename T, int HP, bool NOISE, int KMAX>
 __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {

@@ -72,7 +72,7 @@ class LazyAux(dict):
     first time they are read."""
 
     _LAZY = ("balance_loss", "subkey_counts", "slot_counts", "top1_weight")
-    _INTERNAL = ("_f", "_p", "_cos")
+    _INTERNAL = ("_f", "_p", "_cos", "_counts", "_state")
 
     def __init__(self, eager: Dict[str, Any], compute, **lazy):
         super().__init__(eager)
@@ -277,7 +277,7 @@ class MemoryPool:
         }, stats, queries=lambda: res["q_hat"])
         res.update({
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
-            "k_hat": k_hat, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
+            "k_hat": k_hat, "packed": packed, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
             "flat_idx": flat_idx, "slots": slots, "weights": weights, "gumbel": gumbel,
             "noise_coef": noise_coef,
         })
@@ -286,24 +286,38 @@ class MemoryPool:
     # ------------------------------------------------------------- stats
     def _routing_stats(self, params, res, k_hat, T, q_len, sub_idx, slots, weights, noisy,
                        packed, score_code, M):
-        """memory.py:196-215 from the selected ids."""
+        """memory.py:196-215 from the selected ids: the counts on the GPU
+        (mpl_route_counts); the balance loss fused over the MFMA score tiles
+        (mpl_balance_fwd) with fp16 scoring, else from the dense cosine."""
         H, n, k = self.heads, self.n_sub_keys, self.top_k
+        half = self.d_key // 2
         dev = sub_idx.device
-        q_hat = res["q_hat"]
-        codebook = ((torch.arange(H, device=dev)[:, None, None] * 2
-                     + torch.arange(2, device=dev)[None, :, None]) * n)
-
-        def count_subkeys(ids):  # memory.py:199-201
-            flat = (ids.long() + codebook[None]).reshape(-1)
-            return _count(flat, H * 2 * n).reshape(H, 2, n)
-
-        sl = slots.long()
-        subkey_counts = count_subkeys(torch.stack([sl // n, sl % n], dim=2))
+        L = _lib.lib()
+        stream = _lib.stream_ptr(dev)
         if noisy:  # memory.py:207: an extra clean selection
             clean = self._clean_sub_idx(res["q"], packed, score_code, T, M)
         else:
             clean = sub_idx
-        f = count_subkeys(clean) / (M * k)
+        subkey_counts = torch.empty((H, 2, n), dtype=torch.float32, device=dev)
+        clean_counts = torch.empty((H, 2, n), dtype=torch.float32, device=dev)
+        slot_counts = torch.empty(self.pool_size, dtype=torch.float32, device=dev)
+        check(L.mpl_route_counts(ptr(slots), ptr(clean), M, H, n, k, ptr(subkey_counts), ptr(clean_counts),
+                                 ptr(slot_counts), stream), "mpl_route_counts")
+        stats = {
+            "subkey_counts": subkey_counts,
+            "slot_counts": slot_counts,
+            "top1_weight": weights.max(-1).values.mean(),
+        }
+        if score_code == MPL_F16 and M > 0:
+            scaled = int(bool(self.balance_temperature_grad and self.query_scale))
+            state = torch.empty(max(L.mpl_balance_state_bytes(M, H), 16), dtype=torch.uint8, device=dev)
+            loss = torch.empty(1, dtype=torch.float32, device=dev)
+            check(L.mpl_balance_fwd(ptr(res["q"]), scaled, ptr(packed), ptr(clean_counts), M, H, n, half, k,
+                                    float(T), ptr(state), ptr(loss), stream), "mpl_balance_fwd")
+            stats.update(balance_loss=loss.reshape(()), _counts=clean_counts, _state=state)
+            return stats
+        f = clean_counts / (M * k)
+        q_hat = res["q_hat"]
         cos = torch.einsum("mhcd,hcnd->mhcn", q_hat, k_hat)
         if self.balance_temperature_grad:
             p_scores = cos * T * (q_len[..., None] if q_len is not None else 1.0)
@@ -311,15 +325,8 @@ class MemoryPool:
             p_scores = cos * T
         p = torch.softmax(p_scores, dim=-1)
         P = p.mean(0)
-        balance = n * torch.mean(torch.sum(f * P, dim=-1))
-        slot_counts = _count(sl.reshape(-1), self.pool_size)
-        return {
-            "balance_loss": balance,
-            "subkey_counts": subkey_counts,
-            "slot_counts": slot_counts,
-            "top1_weight": weights.max(-1).values.mean(),
-            "_f": f, "_p": p, "_cos": cos,
-        }
+        stats.update(balance_loss=n * torch.mean(torch.sum(f * P, dim=-1)), _f=f, _p=p, _cos=cos)
+        return stats
 
     def _clean_sub_idx(self, q, packed, score_code, T, M):
         H, n, k, half = self.heads, self.n_sub_keys, self.top_k, self.d_key // 2
@@ -338,15 +345,6 @@ class MemoryPool:
                                  ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
               "mpl_score_select(clean)")
         return sub_idx
-
-
-def _count(ids: torch.Tensor, size: int) -> torch.Tensor:
-    """Occurrences of each id in [0, size) as float32, without a host sync
-    (torch.bincount reads the id range back to the host). Integer adds, so the
-    result does not depend on their order."""
-    c = torch.zeros(size, dtype=torch.int32, device=ids.device)
-    c.index_add_(0, ids, torch.ones(1, dtype=torch.int32, device=ids.device).expand(ids.shape[0]))
-    return c.float()
 
 
 # ------------------------------------------------------------------ autograd
@@ -409,12 +407,25 @@ class _LookupFunction(torch.autograd.Function):
 
         # balance loss, dense over n (memory.py:208-213)
         dq_extra = dk_extra = dlen_extra = dlogt_extra = None
-        if g_balance is not None and M > 0:
+        btg = pool.balance_temperature_grad
+        if g_balance is not None and M > 0 and "_state" in ctx.internal:
+            dq_extra = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
+            dk_extra = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+            dlen_extra = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if (btg and q_len is not None) else None
+            dlogt_extra = torch.empty(1, dtype=torch.float32, device=dev) if btg else None
+            gb = g_balance.reshape(1).float().contiguous()
+            wsb = L.mpl_balance_bwd_workspace_bytes(M, H, n, half)
+            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+            check(L.mpl_balance_bwd(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]),
+                                    ptr(ctx.internal["_counts"]), ptr(ctx.internal["_state"]), ptr(gb), int(btg),
+                                    int(bool(pool.query_scale)), M, H, n, half, k, float(T), ptr(ws), wsb,
+                                    ptr(dq_extra), ptr(dk_extra), ptr(dlen_extra), ptr(dlogt_extra), stream),
+                  "mpl_balance_bwd")
+        elif g_balance is not None and M > 0:
             f, p = ctx.internal["_f"], ctx.internal["_p"]
             a = g_balance.reshape(()).float() * (n / (2.0 * H * M))
             dp = a * f[None]
             dps = p * (dp - (p * dp).sum(-1, keepdim=True))
-            btg = pool.balance_temperature_grad
             scale = T * (q_len[..., None] if (btg and q_len is not None) else 1.0)
             dcos = (dps * scale).contiguous()
             hc_first = dcos.permute(1, 2, 0, 3).reshape(2 * H, M, n)
