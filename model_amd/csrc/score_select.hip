@@ -80,13 +80,16 @@ struct ScoreParams {
 };
 
 // Per-lane selection state of the stage-1 kernel.  Candidates are appended
-// to the lane's column of an LDS buffer as (score bits, index) pairs; `wp`
-// points at the next free entry (entries of one lane are kWave apart).
+// to the lane's column of an LDS buffer as (score bits, index) pairs; `cnt`
+// is the number of buffered entries.  The buffer is addressed by index from
+// its __shared__ array (not through a loop-carried pointer), so the compiler
+// can tell these accesses from the LDS-DMA writes of the key tiles and does
+// not wait for the in-flight DMA before each append.
 template <int KMAX, bool NOISE>
 struct LaneSel {
   TopList<KMAX, NOISE> top;
   float thr;
-  uint2* wp;
+  int cnt;
 };
 
 // Merges the lane's buffered candidates (column `lane` of buf/pay) into its
@@ -96,8 +99,7 @@ template <int KMAX, bool NOISE>
 __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, uint2 (*buf)[kWave],
                                            const float (*pay)[kWave], int lane, bool valid, int k,
                                            float base_thr) {
-  uint2* const start = &buf[0][lane];
-  const int cnt = (int)(st.wp - start) / kWave;
+  const int cnt = st.cnt;
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
 #pragma unroll 1
@@ -115,7 +117,7 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, uint2 (*buf
     sort8<NOISE>(ch, cp);
     st.top.template merge<8>(ch, cp);
   }
-  st.wp = start;
+  st.cnt = 0;
   if (valid) {
     const u64 kk = st.top.at(k - 1);
     st.thr = kk ? key_score(kk) : base_thr;
@@ -356,15 +358,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   LaneSel<KMAX, NOISE> st;
   st.top.init();
   st.thr = valid ? base_thr : INFINITY;
-  st.wp = &mybuf[0][lane];
-  uint2* const flush_at = &mybuf[kCand - 8][lane];
+  st.cnt = 0;
   sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
                             __attribute__((always_inline)) {
     float sv[16], cl[NOISE ? 16 : 1];
     lane_scores(kb, c, g, sv, cl);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      if (active && __ballot(st.wp > flush_at) != 0)
+      if (active && __ballot(st.cnt > kCand - 8) != 0)
         flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -372,12 +373,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
         issue_for(r, issue);
         const float x = sv[r];
         if (active && x > st.thr) {
-          *st.wp = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3)));
-          if (NOISE) {
-            const int slot = (int)(st.wp - &mybuf[0][0]);
-            (&cpay[NOISE ? wave : 0][0][0])[NOISE ? slot : 0] = cl[NOISE ? r : 0];
-          }
-          st.wp += kWave;
+          cbuf[wave][st.cnt][lane] = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3)));
+          if (NOISE) cpay[NOISE ? wave : 0][NOISE ? st.cnt : 0][lane] = cl[NOISE ? r : 0];
+          ++st.cnt;
         }
       }
     }
