@@ -209,6 +209,43 @@ int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, const float* 
                         int64_t M, int H, int n, int half, int k, float temperature,
                         void* workspace, size_t workspace_bytes, float* d_sub_keys, void* stream);
 
+/*
+ * Backward of mpl_l2_normalize's y = x * rsqrt(sum(x*x) + eps) over rows of
+ * length dim: dx = (dy - y (y . dy)) / sqrt(sum(x*x) + eps), multiplied by
+ * *scale (a device scalar) when scale != NULL.  x, dy, dx: [rows, dim] fp32.
+ * The derivative of memory.py:30-31 (XLA autodiff in the reference).
+ */
+int mpl_l2_normalize_bwd(const float* x, const float* dy, int64_t rows, int dim, float eps,
+                         const float* scale, float* dx, void* stream);
+
+/*
+ * key_diversity_loss (memory.py:230-240): with G[h,c] = K_hat K_hat^T the
+ * cosine Gram matrix of each codebook, loss [1] = sum of the squared
+ * off-diagonal entries / (H * 2 * n * (n - 1)), the Gram tiles on fp16 MFMA
+ * (half % 8 == 0, half <= 128).  If d_k_hat [H,2,n,half] != NULL it receives
+ * d loss / d k_hat = 4 / (H * 2 * n * (n - 1)) * (G - diag G) K_hat (the
+ * raw sub-keys' gradient follows with mpl_l2_normalize_bwd).  k_hat and
+ * packed_keys from mpl_pack_keys (MPL_F16).
+ */
+size_t mpl_key_diversity_workspace_bytes(int H, int n, int half);
+int mpl_key_diversity(const float* k_hat, const void* packed_keys, int H, int n, int half, void* workspace,
+                      size_t workspace_bytes, float* loss, float* d_k_hat, void* stream);
+
+/*
+ * revive_dead_keys (memory.py:243-281), in place: in every codebook the
+ * sub-keys with usage < threshold / n (sub_keys [H,2,n,half], subkey_usage
+ * [H,2,n], both fp32) become l2-normalise(queries[pick, h, c] + noise *
+ * normal) with usage 1/n, and each codebook's usage is divided by its new
+ * sum.  queries [M,H,2,half] (unit-norm query halves); the random draws of
+ * memory.py:269-274 are inputs: pick [H,2,n] int32 in [0, M), normal
+ * [H,2,n,half] fp32 standard normal.  dead [H,2,n] (uint8, optional)
+ * receives the mask.  The trainer's reset of the optimizer moments of
+ * revived keys (train.py:497-509) stays with the caller.
+ */
+int mpl_revive_keys(float* sub_keys, float* subkey_usage, const float* queries, int64_t M, const int32_t* pick,
+                    const float* normal, int H, int n, int half, float threshold, float noise, uint8_t* dead,
+                    void* stream);
+
 /* *out = sum(x[0, n)) (+ *add if add != NULL), fixed order, fp64 accumulation. */
 int mpl_sum(const float* x, int64_t n, const float* add, float* out, void* stream);
 

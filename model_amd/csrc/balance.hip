@@ -10,9 +10,12 @@
 //                        and r_m = sum_n f_n softmax(z)_n, online in one sweep
 //                        of MFMA score tiles; balance = n/(2H M) sum r
 //                        (memory.py:210-213)
+//   revive_kernel        revive_dead_keys (memory.py:243-281) in place
 //   balance_grad_kernel  the gradient of balance (dense over n) with respect
 //                        to the normalised queries and sub-keys, as two MFMA
-//                        passes that recompute the score tiles
+//                        passes that recompute the score tiles; the same
+//                        kernel computes key_diversity_loss (memory.py:230-240)
+//                        and its gradient from the Gram tiles of the sub-keys
 //
 // With f fixed (stop_gradient, memory.py:208) the loss is
 // n/(2H M) sum_{m,hc} r_m, so the gradient with respect to the logits is
@@ -331,17 +334,24 @@ struct BalGradParams {
   int64_t sblk_per_split;
   const float* rho;  // [M, HC] (DK: folded into the streamed pack already; DQ: output scale) or null
   float* out;        // DQ: d q_hat [M, HC, half]; DK: partial d k_hat [splits, HC, n, half]
-  float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null
+  float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null; Div: per-thread sums of squares
 };
 
-// DK = false: the fixed side is 32 queries per wave (B operand), sub-key
-// blocks stream; DK = true: the fixed side is 32 sub-keys per wave, blocks of
-// 32 queries stream (the query range is split over `splits` workgroups).
+enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2 };
+
+// kModeDQ: the fixed side is 32 queries per wave (B operand), sub-key blocks
+// stream.  kModeDK: the fixed side is 32 sub-keys per wave, blocks of 32
+// queries stream (the query range is split over `splits` workgroups).
+// kModeDiv: both sides are the sub-keys of one codebook (the Gram matrix of
+// key_diversity_loss); the operand is the off-diagonal cosine itself and each
+// lane also sums its squares into u[workgroup * 256 + thread].
 // Each streamed block: score tile C (rows = streamed, columns = fixed), the
-// scaled operand g = sigma p (f - r) in fp16, and for every 32-dim block db
-// of the output  acc[db] += strT[db] . g  (two MFMAs, K = 16 rows each).
-template <bool DK, int HP>
+// operand g in fp16, and for every 32-dim block db of the output
+// acc[db] += strT[db] . g  (two MFMAs, K = 16 rows each).
+template <int MODE, int HP>
 __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams p) {
+  constexpr bool DK = MODE != kModeDQ;  // the fixed side is sub-keys
+  constexpr bool DIV = MODE == kModeDiv;
   constexpr int NCH = HP / 16;
   constexpr int ND = (HP + 31) / 32;
   constexpr int TN = NCH * kWave, TT = ND * 2 * kWave, TILE = TN + TT;
@@ -354,7 +364,8 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   const int64_t fg = rest / p.splits;
   const int64_t fb = fg * kBalWaves + wave;  // this wave's fixed block
   const int64_t nfix = DK ? p.n : p.M;
-  const int64_t nstr = DK ? p.M : p.n;
+  const int64_t nstr = (DK && !DIV) ? p.M : p.n;
+  const bool grad = p.out != nullptr;  // kModeDiv may ask for the loss only
   const int64_t my_f = fb * 32 + (lane & 31);
   const bool valid = my_f < nfix;
   const int64_t fbc = fb < p.fblk ? fb : p.fblk - 1;
@@ -365,16 +376,16 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
 #pragma unroll
     for (int c = 0; c < NCH; ++c) fop[c] = MF::from_vec(src[c * kWave + lane], 0);
   }
-  const float sig = p.sigma[hc];
+  const float sig = DIV ? 1.f : p.sigma[hc];
   const float fs = p.inv_mk * sig;  // scaled f per count
-  const float* cnt = p.counts + (int64_t)hc * p.n;
-  const float4* sth = p.state + (int64_t)hc * p.M;
+  const float* cnt = DIV ? nullptr : p.counts + (int64_t)hc * p.n;
+  const float4* sth = DIV ? nullptr : p.state + (int64_t)hc * p.M;
   // per-lane constants of the fixed row
   float4 fst = make_float4(0.f, 0.f, 0.f, 0.f);
   float ffix = 0.f;
-  if (DK)
+  if (MODE == kModeDK)
     ffix = cnt[valid ? my_f : 0] * fs;
-  else
+  else if (MODE == kModeDQ)
     fst = sth[valid ? my_f : 0];
   const float rs_fix = fst.y * sig;
 
@@ -412,6 +423,11 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       const int64_t row = sb * 32 + 8 * (r >> 2) + 4 * par + (r & 3);
       const bool rv = row < nstr;
       const int64_t rc = rv ? row : 0;
+      if (DIV) {
+        gv[r] = (rv && valid && row != my_f) ? acc[r] : 0.f;
+        usum = fmaf(gv[r], gv[r], usum);
+        continue;
+      }
       float pe, diff;
       if (DK) {
         const float4 s = sth[rc];  // the streamed query's state
@@ -431,10 +447,12 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       b1[j] = (_Float16)gv[8 + j];
     }
     const uint4* tt = tiles[cur] + TN;
+    if (!DIV || grad) {
 #pragma unroll
-    for (int db = 0; db < ND; ++db) {
-      gacc[db] = MF::mma(MF::from_vec(tt[(db * 2) * kWave + lane], 0), b0, gacc[db]);
-      gacc[db] = MF::mma(MF::from_vec(tt[(db * 2 + 1) * kWave + lane], 0), b1, gacc[db]);
+      for (int db = 0; db < ND; ++db) {
+        gacc[db] = MF::mma(MF::from_vec(tt[(db * 2) * kWave + lane], 0), b0, gacc[db]);
+        gacc[db] = MF::mma(MF::from_vec(tt[(db * 2 + 1) * kWave + lane], 0), b1, gacc[db]);
+      }
     }
     if (more) {
       stn.store(tiles[cur ^ 1], tid);
@@ -443,9 +461,14 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     __syncthreads();
   }
 
-  // d = c T (rho) / sigma * acc; rows of the output are the fixed rows
-  const float cc = *p.g * p.coef;
-  float scale = cc * p.T / sig;
+  if (DIV) {
+    p.u[(int64_t)blockIdx.x * kBalThreads + tid] = usum;
+    if (!grad) return;
+  }
+  // d = c T (rho) / sigma * acc (kModeDiv: coef * acc); rows of the output
+  // are the fixed rows
+  const float cc = DIV ? 1.f : *p.g * p.coef;
+  float scale = DIV ? p.coef : cc * p.T / sig;
   if (!DK && p.rho != nullptr) scale *= p.rho[(valid ? my_f : 0) * p.HC + hc];
   if (!DK && p.u != nullptr) {
     const float ut = usum + partner(usum, par);
@@ -495,7 +518,8 @@ __global__ __launch_bounds__(256) void balance_temp_kernel(const float* __restri
   }
 }
 
-__global__ __launch_bounds__(1024) void sum_plain_kernel(const float* __restrict__ x, int64_t n, float* __restrict__ out) {
+__global__ __launch_bounds__(1024) void sum_plain_kernel(const float* __restrict__ x, int64_t n, double scale,
+                                                         float* __restrict__ out) {
   __shared__ double part[1024];
   const int tid = threadIdx.x;
   double s = 0.0;
@@ -506,7 +530,7 @@ __global__ __launch_bounds__(1024) void sum_plain_kernel(const float* __restrict
     if (tid < off) part[tid] += part[tid + off];
     __syncthreads();
   }
-  if (tid == 0) *out = (float)part[0];
+  if (tid == 0) *out = (float)(part[0] * scale);
 }
 
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -734,9 +758,9 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
   pk.u = nullptr;
   pk.rho = nullptr;
   const unsigned gk = (unsigned)(HC * cdiv(n, kRowsPerGroup) * L.splits);
-#define MPL_GRAD(HPV)                                                  \
-  balance_grad_kernel<false, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
-  balance_grad_kernel<true, HPV><<<gk, kBalThreads, 0, s>>>(pk)
+#define MPL_GRAD(HPV)                                                        \
+  balance_grad_kernel<kModeDQ, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
+  balance_grad_kernel<kModeDK, HPV><<<gk, kBalThreads, 0, s>>>(pk)
   switch (L.HP) {
     case 16: MPL_GRAD(16); break;
     case 32: MPL_GRAD(32); break;
@@ -751,7 +775,172 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
   if (btg) {
     balance_temp_kernel<<<grid_for(M * HC, 256), 256, 0, s>>>(u, rho, M, HC, temperature, query_scale ? dlen : nullptr,
                                                              tpart);
-    sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, M * HC, dlogt);
+    sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, M * HC, 1.0, dlogt);
   }
   return check_launch("mpl_balance_bwd");
+}
+
+namespace mpl {
+namespace {
+
+struct DivLayout {
+  size_t kt, part, lpart, total;
+  int HP, splits;
+  int64_t nblk, sbps, groups;
+};
+
+DivLayout div_layout(int H, int n, int half) {
+  DivLayout L;
+  const int HC = 2 * H;
+  L.HP = KeyPack<_Float16>::padded_half(half);
+  const int ND = (L.HP + 31) / 32;
+  L.nblk = cdiv(n, 32);
+  const int64_t kgroups = (int64_t)HC * cdiv(n, kRowsPerGroup);
+  int64_t sp = cdiv(512, kgroups);
+  if (sp > L.nblk) sp = L.nblk;
+  if (sp < 1) sp = 1;
+  L.sbps = cdiv(L.nblk, sp);
+  L.splits = (int)cdiv(L.nblk, L.sbps);
+  L.groups = kgroups * L.splits;
+  size_t o = 0;
+  L.kt = o;
+  o += al256((size_t)HC * L.nblk * ND * 2 * kWave * 16);
+  L.part = o;
+  o += al256((size_t)L.splits * HC * n * half * 4);
+  L.lpart = o;
+  o += al256((size_t)L.groups * kBalThreads * 4);
+  L.total = o;
+  return L;
+}
+
+}  // namespace
+}  // namespace mpl
+
+extern "C" size_t mpl_key_diversity_workspace_bytes(int H, int n, int half) {
+  if (H < 1 || n < 1 || !balance_shape_ok(half)) return 0;
+  return div_layout(H, n, half).total;
+}
+
+extern "C" int mpl_key_diversity(const float* k_hat, const void* packed_keys, int H, int n, int half,
+                                 void* workspace, size_t workspace_bytes, float* loss, float* d_k_hat,
+                                 void* stream) {
+  clear_error();
+  MPL_REQUIRE(H >= 1 && n >= 1, MPL_EINVAL, "mpl_key_diversity: bad shape");
+  MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
+              "mpl_key_diversity: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  MPL_REQUIRE(k_hat && packed_keys && loss, MPL_EINVAL, "mpl_key_diversity: null buffer");
+  const DivLayout L = div_layout(H, n, half);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
+              "mpl_key_diversity: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  const int HC = 2 * H;
+  char* ws = (char*)workspace;
+  uint4* kt = (uint4*)(ws + L.kt);
+  float* part = (float*)(ws + L.part);
+  float* lpart = (float*)(ws + L.lpart);
+  launch_pack<true>(L.HP, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
+  // D = H * 2 * n * (n - 1) (memory.py:240); n = 1 gives 0/0 as the reference
+  const double D = (double)HC * n * (double)(n - 1);
+  BalGradParams p = {};
+  p.fix = (const uint4*)packed_keys;
+  p.str = (const uint4*)packed_keys;
+  p.strT = kt;
+  p.coef = (float)(4.0 / D);
+  p.M = 0;
+  p.HC = HC;
+  p.n = n;
+  p.half = half;
+  p.fblk = L.nblk;
+  p.sblk = L.nblk;
+  p.splits = L.splits;
+  p.sblk_per_split = L.sbps;
+  p.out = d_k_hat == nullptr ? nullptr : (L.splits == 1 ? d_k_hat : part);
+  p.u = lpart;
+  const unsigned g = (unsigned)L.groups;
+  switch (L.HP) {
+    case 16: balance_grad_kernel<kModeDiv, 16><<<g, kBalThreads, 0, s>>>(p); break;
+    case 32: balance_grad_kernel<kModeDiv, 32><<<g, kBalThreads, 0, s>>>(p); break;
+    case 64: balance_grad_kernel<kModeDiv, 64><<<g, kBalThreads, 0, s>>>(p); break;
+    default: balance_grad_kernel<kModeDiv, 128><<<g, kBalThreads, 0, s>>>(p); break;
+  }
+  if (d_k_hat != nullptr && L.splits > 1) {
+    const int64_t c4 = (int64_t)HC * n * half / 4;
+    split_sum_kernel<<<grid_for(c4, 256), 256, 0, s>>>((const float4*)part, L.splits, c4, (float4*)d_k_hat);
+  }
+  sum_plain_kernel<<<1, 1024, 0, s>>>(lpart, L.groups * kBalThreads, 1.0 / D, loss);
+  return check_launch("mpl_key_diversity");
+}
+
+namespace mpl {
+namespace {
+
+// revive_dead_keys (memory.py:243-281), one workgroup per codebook, in place:
+// keys whose usage is below threshold / n become the normalised picked query
+// plus noise * normal, their usage 1/n, and the codebook's usage is divided
+// by its new sum (fp64, fixed order).
+__global__ __launch_bounds__(256) void revive_kernel(float* __restrict__ keys, float* __restrict__ usage,
+                                                     const float* __restrict__ queries, int64_t M,
+                                                     const int32_t* __restrict__ pick,
+                                                     const float* __restrict__ normal, int HC, int n, int half,
+                                                     float threshold, float noise, uint8_t* __restrict__ dead) {
+  __shared__ double part[256];
+  const int tid = threadIdx.x;
+  const int hc = blockIdx.x;
+  float* u = usage + (int64_t)hc * n;
+  const float lim = threshold / (float)n;
+  const float inv_n = 1.0f / (float)n;
+  double s = 0.0;
+  for (int i = tid; i < n; i += 256) {
+    const float v = u[i];
+    s += (double)(v < lim ? inv_n : v);
+  }
+  part[tid] = s;
+  __syncthreads();
+  for (int off = 128; off >= 1; off >>= 1) {
+    if (tid < off) part[tid] += part[tid + off];
+    __syncthreads();
+  }
+  const float total = (float)part[0];
+  // keys: 16 lanes per row
+  const int l = tid & 15;
+  for (int i0 = 0; i0 < n; i0 += 16) {
+    const int i = i0 + (tid >> 4);
+    const bool is_dead = i < n && u[i < n ? i : 0] < lim;  // wave-divergent, no barrier inside
+    if (!is_dead) continue;
+    int pk = pick[(int64_t)hc * n + i];
+    pk = pk < 0 ? 0 : (pk >= M ? (int)(M - 1) : pk);
+    const float* qr = queries + ((int64_t)pk * HC + hc) * half;
+    const float* zr = normal + ((int64_t)hc * n + i) * half;
+    float* kr = keys + ((int64_t)hc * n + i) * half;
+    float ss = 0.f;
+    for (int d = l; d < half; d += 16) {
+      const float x = fmaf(noise, zr[d], qr[d]);
+      ss = fmaf(x, x, ss);
+    }
+    // the 16 lanes of this row are contiguous and all take this branch
+    for (int o = 8; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 16);
+    const float r = 1.0f / sqrtf(ss + 1e-6f);
+    for (int d = l; d < half; d += 16) kr[d] = fmaf(noise, zr[d], qr[d]) * r;
+  }
+  __syncthreads();  // every row read the old usage
+  for (int i = tid; i < n; i += 256) {
+    const float v = u[i];
+    const bool dd = v < lim;
+    u[i] = (dd ? inv_n : v) / total;
+    if (dead != nullptr) dead[(int64_t)hc * n + i] = dd ? 1 : 0;
+  }
+}
+
+}  // namespace
+}  // namespace mpl
+
+extern "C" int mpl_revive_keys(float* sub_keys, float* subkey_usage, const float* queries, int64_t M,
+                               const int32_t* pick, const float* normal, int H, int n, int half, float threshold,
+                               float noise, uint8_t* dead, void* stream) {
+  clear_error();
+  MPL_REQUIRE(H >= 1 && n >= 1 && half >= 1 && M >= 1, MPL_EINVAL, "mpl_revive_keys: bad shape");
+  MPL_REQUIRE(sub_keys && subkey_usage && queries && pick && normal, MPL_EINVAL, "mpl_revive_keys: null buffer");
+  revive_kernel<<<2 * H, 256, 0, (hipStream_t)stream>>>(sub_keys, subkey_usage, queries, M, pick, normal, 2 * H, n,
+                                                        half, threshold, noise, dead);
+  return check_launch("mpl_revive_keys");
 }

@@ -37,6 +37,35 @@ __global__ __launch_bounds__(256) void l2norm_kernel(const float* __restrict__ x
   }
 }
 
+// Backward of l2norm_kernel: dx = (dy - y (y . dy)) / sqrt(sum x^2 + eps),
+// y = x / sqrt(sum x^2 + eps), times *scale when given.  16 lanes per row.
+__global__ __launch_bounds__(256) void l2norm_bwd_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                                         int64_t rows, int dim, float eps,
+                                                         const float* __restrict__ scale, float* __restrict__ dx) {
+  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
+  const int l = threadIdx.x & 15;
+  const int64_t rc = row < rows ? row : 0;
+  const float* xr = x + rc * dim;
+  const float* gr = dy + rc * dim;
+  float ss = 0.f, xg = 0.f;
+  for (int j = l; j < dim; j += 16) {
+    const float v = xr[j], g = gr[j];
+    ss = fmaf(v, v, ss);
+    xg = fmaf(v, g, xg);
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o, 16);
+    xg += __shfl_xor(xg, o, 16);
+  }
+  if (row >= rows) return;
+  const float r = 1.0f / sqrtf(ss + eps);
+  const float yg = xg * r;  // y . dy
+  const float sc = scale != nullptr ? *scale : 1.f;
+  float* dr = dx + row * dim;
+  for (int j = l; j < dim; j += 16) dr[j] = sc * r * (gr[j] - xr[j] * r * yg);
+}
+
 // Normalise and pack in one pass: one wave per (codebook, block of 32 keys).
 // Lane l owns exactly the dims of key l % 32 that the packed layout gives it
 // (the other half sits in lane l ^ 32), so one half-swap completes the row's
@@ -124,6 +153,16 @@ extern "C" int mpl_l2_normalize(const float* x, int64_t rows, int dim, float eps
   l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, (hipStream_t)stream>>>(x, rows, dim, eps, y,
                                                                              (_Float16*)y16, row_len);
   return check_launch("mpl_l2_normalize");
+}
+
+extern "C" int mpl_l2_normalize_bwd(const float* x, const float* dy, int64_t rows, int dim, float eps,
+                                    const float* scale, float* dx, void* stream) {
+  clear_error();
+  MPL_REQUIRE(rows >= 0 && dim > 0, MPL_EINVAL, "mpl_l2_normalize_bwd: bad sizes");
+  if (rows == 0) return MPL_OK;
+  MPL_REQUIRE(x && dy && dx, MPL_EINVAL, "mpl_l2_normalize_bwd: null buffer");
+  l2norm_bwd_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, (hipStream_t)stream>>>(x, dy, rows, dim, eps, scale, dx);
+  return check_launch("mpl_l2_normalize_bwd");
 }
 
 extern "C" size_t mpl_packed_keys_bytes(int H, int n, int half, int score_dtype) {

@@ -6,11 +6,15 @@ Same attributes, parameter names and layout (``sub_keys`` [H, 2, n, d_key/2],
 ``aux`` keys.  Parameters are torch tensors on the GPU; every step of the
 lookup runs in libmpl.so (include/mpl.h) on torch's current HIP stream:
 
-  mpl_l2_normalize   queries, q_len             memory.py:136-138
   mpl_pack_keys      keys (cached per version)  memory.py:139
-  mpl_score_select   scores + 2-stage top-k     memory.py:149-178
+  mpl_score_select   query normalisation,       memory.py:136-138,
+                     scores + 2-stage top-k     memory.py:149-178
                      + routing softmax
   mpl_gather_wsum    value read                 memory.py:179-193
+  mpl_route_counts,  routing statistics, and    memory.py:196-215
+  mpl_balance_fwd    the balance loss
+  mpl_key_diversity  key_diversity_loss         memory.py:230-240
+  mpl_revive_keys    revive_dead_keys           memory.py:243-281
 
 The routing statistics of ``aux`` (memory.py:196-215) are derived from the
 returned ids on first access, so a decode loop that never reads them never
@@ -345,6 +349,92 @@ class MemoryPool:
                                  ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
               "mpl_score_select(clean)")
         return sub_idx
+
+
+# ------------------------------------------------------------ regularisers
+def _fp16_gram_ok(half: int) -> bool:
+    return half % 8 == 0 and half <= 128
+
+
+class _KeyDiversity(torch.autograd.Function):
+    """memory.py:230-240 on fp16 MFMA Gram tiles (mpl_key_diversity); the
+    gradient with respect to the normalised keys is formed in the forward
+    (one pass over the Gram tiles) and taken through the l2-normalisation
+    backward (mpl_l2_normalize_bwd) with the upstream gradient."""
+
+    @staticmethod
+    def forward(ctx, sub_keys):
+        H, C, n, half = sub_keys.shape
+        dev = sub_keys.device
+        L = _lib.lib()
+        stream = _lib.stream_ptr(dev)
+        src = sub_keys.detach().float().contiguous()
+        k_hat = torch.empty_like(src)
+        packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, MPL_F16), dtype=torch.uint8, device=dev)
+        check(L.mpl_pack_keys(ptr(src), H, n, half, MPL_F16, ptr(k_hat), ptr(packed), stream), "mpl_pack_keys")
+        wsb = L.mpl_key_diversity_workspace_bytes(H, n, half)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+        loss = torch.empty(1, dtype=torch.float32, device=dev)
+        dk = torch.empty_like(src) if ctx.needs_input_grad[0] else None
+        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, ptr(ws), wsb, ptr(loss), ptr(dk), stream),
+              "mpl_key_diversity")
+        ctx.save_for_backward(src, dk)
+        ctx.dtype = sub_keys.dtype
+        return loss.reshape(())
+
+    @staticmethod
+    def backward(ctx, g):
+        src, dk = ctx.saved_tensors
+        H, C, n, half = src.shape
+        dx = torch.empty_like(src)
+        gs = g.reshape(1).float().contiguous()
+        check(_lib.lib().mpl_l2_normalize_bwd(ptr(src), ptr(dk), H * C * n, half, NORM_EPS, ptr(gs), ptr(dx),
+                                              _lib.stream_ptr(src.device)), "mpl_l2_normalize_bwd")
+        return dx.to(ctx.dtype)
+
+
+def key_diversity_loss(sub_keys: torch.Tensor) -> torch.Tensor:
+    """memory.py:230-240: mean squared off-diagonal cosine inside each
+    sub-key codebook, differentiable with respect to ``sub_keys``.  Sub-key
+    widths the fp16 Gram kernel does not take (d_key/2 not a multiple of 8 or
+    above 128) use the dense cosine through library GEMMs."""
+    if sub_keys.device.type != "cuda":
+        raise RuntimeError("key_diversity_loss runs on the GPU only (libmpl.so)")
+    H, C, n, half = sub_keys.shape
+    if _fp16_gram_ok(half):
+        return _KeyDiversity.apply(sub_keys)
+    keys = sub_keys.float() * torch.rsqrt((sub_keys.float() ** 2).sum(-1, keepdim=True) + NORM_EPS)
+    gram = torch.matmul(keys, keys.transpose(-1, -2).contiguous())
+    off = gram * (1.0 - torch.eye(n, device=sub_keys.device))
+    return off.pow(2).sum() / (H * C * n * (n - 1))
+
+
+def revive_dead_keys(sub_keys: torch.Tensor, subkey_usage: torch.Tensor, queries: torch.Tensor, rng,
+                     threshold: float, noise: float = 0.05, *, pick: Optional[torch.Tensor] = None,
+                     normal: Optional[torch.Tensor] = None):
+    """memory.py:243-281 (mpl_revive_keys): returns (new_sub_keys,
+    new_subkey_usage, dead_mask).  ``rng`` (seed or torch.Generator) draws
+    the picked query per key and the normal noise; ``pick`` [H,2,n] and
+    ``normal`` [H,2,n,d] may be given instead."""
+    H, C, n, d = sub_keys.shape
+    dev = sub_keys.device
+    q = queries.detach().reshape(-1, H, C, d).float().contiguous()
+    M = q.shape[0]
+    if M < 1:
+        raise ValueError("revive_dead_keys needs at least one query")
+    if pick is None or normal is None:
+        gen = rng if isinstance(rng, torch.Generator) else torch.Generator(device=dev).manual_seed(int(rng))
+        pick = torch.randint(0, M, (H, C, n), generator=gen, device=dev)
+        normal = torch.randn((H, C, n, d), generator=gen, device=dev)
+    pick = pick.to(device=dev, dtype=torch.int32).contiguous()
+    normal = normal.to(device=dev, dtype=torch.float32).contiguous()
+    new_keys = sub_keys.detach().float().clone()
+    new_usage = subkey_usage.detach().float().clone()
+    dead = torch.empty((H, C, n), dtype=torch.uint8, device=dev)
+    check(_lib.lib().mpl_revive_keys(ptr(new_keys), ptr(new_usage), ptr(q), M, ptr(pick), ptr(normal), H, n, d,
+                                     float(threshold), float(noise), ptr(dead), _lib.stream_ptr(dev)),
+          "mpl_revive_keys")
+    return new_keys.to(sub_keys.dtype), new_usage, dead.bool()
 
 
 # ------------------------------------------------------------------ autograd

@@ -106,3 +106,17 @@ def lookup_backward(res: dict, values, g_out, *, n: int, query_scale: bool = Fal
         np.add.at(dv, read.reshape(-1), (w[..., None] * g[:, None, None, :]).reshape(-1, g.shape[1]))
         out["d_values"] = dv
     return out
+
+
+def key_diversity_backward(sub_keys, dtype=np.float64) -> np.ndarray:
+    """d key_diversity_loss / d sub_keys (memory.py:230-240 under autodiff):
+    d k_hat = 4 / (H * 2 * n * (n - 1)) * (G - diag G) k_hat, then the
+    l2-normalisation backward."""
+    raw = np.asarray(sub_keys, dtype=dtype)
+    s = np.sum(raw * raw, axis=-1, keepdims=True) + 1e-6
+    k_hat = raw / np.sqrt(s)
+    H, C, n, _ = raw.shape
+    gram = np.einsum("hcnd,hcmd->hcnm", k_hat, k_hat)
+    off = gram * (1.0 - np.eye(n, dtype=dtype))
+    dk_hat = 4.0 / (H * C * n * (n - 1)) * np.einsum("hcnm,hcmd->hcnd", off, k_hat)
+    return _l2_normalize_bwd(raw, dk_hat)

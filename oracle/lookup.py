@@ -7,6 +7,8 @@ Follows KumarDev7/model ``memory_pool_model/memory.py``:
                        memory.py:34-45 documents and tests:55-63 pins)
   * ``lookup_forward`` memory.py:132-193
   * ``aux_stats``      memory.py:196-226
+  * ``key_diversity_loss`` memory.py:230-240
+  * ``revive_dead_keys``   memory.py:243-281 (the random draws are inputs)
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
 this module, and only to check results.
@@ -244,3 +246,33 @@ def brute_force_slots(queries, sub_keys, log_temperature, *, top_k_: int, dtype=
         s = s * (np.sqrt(np.sum(q * q, -1, keepdims=True) + NORM_EPS) / np.sqrt(half))
     full = (s[:, :, 0, :, None] + s[:, :, 1, None, :]).reshape(q.shape[0], H, n * n)
     return top_k(full, top_k_)[1]
+
+
+def key_diversity_loss(sub_keys, dtype=np.float64) -> float:
+    """memory.py:230-240: mean squared off-diagonal cosine inside each
+    codebook, sum(offdiag(G)^2) / (H * 2 * n * (n - 1))."""
+    keys = l2_normalize(np.asarray(sub_keys, dtype=dtype))
+    H, C, n, _ = keys.shape
+    gram = np.einsum("hcnd,hcmd->hcnm", keys, keys)
+    off = gram * (1.0 - np.eye(n, dtype=dtype))
+    return float(np.sum(off ** 2) / (H * C * n * (n - 1)))
+
+
+def revive_dead_keys(sub_keys, subkey_usage, queries, pick, normal, threshold: float, noise: float = 0.05,
+                     dtype=np.float64):
+    """memory.py:243-281 with the two random draws given: ``pick`` [H,2,n]
+    int (the jax.random.randint of :270) and ``normal`` [H,2,n,d] (the
+    jax.random.normal of :274).  Returns (new_keys, new_usage, dead)."""
+    keys = np.asarray(sub_keys, dtype=dtype)
+    usage = np.asarray(subkey_usage, dtype=dtype)
+    q = np.asarray(queries, dtype=dtype)
+    H, C, n, d = keys.shape
+    dead = usage < threshold / n                                     # :268
+    h_idx = np.arange(H)[:, None, None]
+    c_idx = np.arange(C)[None, :, None]
+    replacement = q[np.asarray(pick), h_idx, c_idx]                  # :271-273
+    replacement = l2_normalize(replacement + noise * np.asarray(normal, dtype=dtype))  # :274-275
+    new_keys = np.where(dead[..., None], replacement, keys)          # :276
+    new_usage = np.where(dead, 1.0 / n, usage)                       # :278
+    new_usage = new_usage / new_usage.sum(axis=-1, keepdims=True)    # :280
+    return new_keys, new_usage, dead

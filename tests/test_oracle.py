@@ -339,3 +339,59 @@ def test_warmup_cosine_closed_form():
     assert orow.warmup_cosine(3100, lr, 200, 6000) == pytest.approx(lr * 0.55)
     assert orow.warmup_cosine(6000, lr, 200, 6000) == pytest.approx(0.1 * lr)
     assert orow.warmup_cosine(9000, lr, 200, 6000) == pytest.approx(0.1 * lr)
+
+
+# ------------------------------------------------------------------ regularisers (memory.py:230-281)
+def test_key_diversity_closed_forms():
+    """Orthonormal codebooks give 0; a codebook of one repeated direction gives
+    1 (every off-diagonal cosine is 1); a mixture matches the direct sum."""
+    eye = np.broadcast_to(np.eye(8, 16), (2, 2, 8, 16)).copy()
+    assert ol.key_diversity_loss(3.0 * eye) == pytest.approx(0.0, abs=1e-15)
+    same = np.broadcast_to(np.arange(1.0, 17.0), (1, 2, 5, 16)).copy()
+    assert ol.key_diversity_loss(same) == pytest.approx(1.0, rel=1e-8)  # eps of memory.py:30
+    rng = np.random.default_rng(3)
+    k = rng.standard_normal((1, 2, 4, 3))
+    kh = k / np.sqrt((k * k).sum(-1, keepdims=True) + 1e-6)
+    tot = sum((kh[0, c, i] @ kh[0, c, j]) ** 2 for c in range(2) for i in range(4) for j in range(4) if i != j)
+    assert ol.key_diversity_loss(k) == pytest.approx(tot / (2 * 4 * 3), rel=1e-12)
+
+
+def test_key_diversity_backward_matches_torch_autograd_and_finite_differences():
+    rng = np.random.default_rng(5)
+    raw = rng.standard_normal((2, 2, 6, 5)) * 1.3
+    got = ob.key_diversity_backward(raw)
+    tk = torch.tensor(raw, dtype=torch.float64, requires_grad=True)
+    kh = tk * torch.rsqrt((tk * tk).sum(-1, keepdim=True) + 1e-6)
+    gram = torch.einsum("hcnd,hcmd->hcnm", kh, kh)
+    off = gram * (1.0 - torch.eye(6, dtype=torch.float64))
+    (off.pow(2).sum() / (2 * 2 * 6 * 5)).backward()
+    np.testing.assert_allclose(got, tk.grad.numpy(), rtol=1e-10, atol=1e-14)
+    eps = 1e-6
+    for idx in [(0, 0, 0, 0), (1, 1, 5, 4), (0, 1, 3, 2)]:
+        a, b = raw.copy(), raw.copy()
+        a[idx] += eps
+        b[idx] -= eps
+        fd = (ol.key_diversity_loss(a) - ol.key_diversity_loss(b)) / (2 * eps)
+        assert got[idx] == pytest.approx(fd, rel=1e-5, abs=1e-10)
+
+
+def test_revive_dead_keys_known_answer():
+    """memory.py:243-281: keys below threshold/n move to the picked query plus
+    noise (normalised), their usage becomes 1/n, and each codebook's usage is
+    renormalised to sum to 1; live keys are untouched."""
+    rng = np.random.default_rng(7)
+    H, n, d, M = 1, 4, 3, 5
+    keys = rng.standard_normal((H, 2, n, d))
+    usage = np.array([[[0.5, 0.01, 0.3, 0.19], [0.25, 0.25, 0.25, 0.25]]])
+    q = rng.standard_normal((M, H, 2, d))
+    pick = np.array([[[4, 1, 2, 3], [0, 0, 0, 0]]])
+    normal = rng.standard_normal((H, 2, n, d))
+    nk, nu, dead = ol.revive_dead_keys(keys, usage, q, pick, normal, threshold=0.1, noise=0.05)
+    assert dead.tolist() == [[[False, True, False, False], [False, False, False, False]]]
+    r = q[1, 0, 0] + 0.05 * normal[0, 0, 1]
+    np.testing.assert_allclose(nk[0, 0, 1], r / np.sqrt(r @ r + 1e-6), rtol=1e-12)
+    np.testing.assert_array_equal(nk[0, 0, [0, 2, 3]], keys[0, 0, [0, 2, 3]])
+    np.testing.assert_array_equal(nk[0, 1], keys[0, 1])
+    u = np.array([0.5, 0.25, 0.3, 0.19])
+    np.testing.assert_allclose(nu[0, 0], u / u.sum(), rtol=1e-12)
+    np.testing.assert_allclose(nu[0, 1], usage[0, 1], rtol=1e-12)
