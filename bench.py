@@ -17,6 +17,8 @@ Also reported in the same JSON line:
   * ``training_262k``: the training step of the same layer (forward +
     backward + sparse row-wise Adagrad) and the sparse row update alone on
     Zipf(1.1)-skewed routing;
+  * ``key_diversity_67M``: key_diversity_loss and its gradient on the
+    67M-slot layer's codebooks (H=4, n=8,192): the n x n Gram tiles on MFMA.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large] [--no-train]
 """
@@ -276,7 +278,7 @@ def train_step_bench(torch, iters):
     sparse value gradient through a probe) followed by the sparse row update
     (merge, clip, row-wise Adagrad on the fp32 master)."""
     from model_amd import rows as R
-    from model_amd.memory import MemoryPool
+    from model_amd.memory import MemoryPool, key_diversity_loss
 
     M, H, n, d_key, d, k = 8192, 4, 512, 256, 256, 16
     dev = "cuda"
@@ -296,7 +298,7 @@ def train_step_bench(torch, iters):
         q = (hidden @ w_q).reshape(M, H, d_key)
         probe = torch.zeros((M, d), device=dev, requires_grad=True)
         out, aux = pool.apply({"params": params}, q, train=False, sparse_grad=True)
-        loss = ((out + probe) * g_out).sum() + 0.01 * aux["balance_loss"]
+        loss = ((out + probe) * g_out).sum() + 0.01 * aux["balance_loss"] + 0.01 * key_diversity_loss(keys)
         gw, gk, gt, gp = torch.autograd.grad(loss, [w_q, keys, log_t, probe])
         rest = (gw.square().sum() + gk.square().sum() + gt.square()).reshape(1)
         upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: gp}, [0], rest_sq=rest)
@@ -314,8 +316,40 @@ def train_step_bench(torch, iters):
     ms = a.elapsed_time(b) / iters
     return {"workload": "training step of the text-study layer: 8,192 tokens, 262,144 fp16 slots + fp32 master, "
                         "forward + backward (queries through a 256->1024 projection, sub-keys, log-temperature, "
-                        "balance loss 0.01, probe gradient) + sparse row-wise Adagrad",
+                        "balance loss 0.01, key diversity loss 0.01, probe gradient) + sparse row-wise Adagrad",
             "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events"}
+
+
+def key_diversity_bench(torch, iters):
+    """key_diversity_loss and its gradient with respect to the normalised
+    sub-keys (memory.py:230-240) for the 67M-slot layer's codebooks (H=4,
+    n=8,192, d_key=256): per codebook the Gram tiles K K^T and the product
+    (G - diag G) K, each 2 n^2 (d_key/2) FLOP, on fp16 MFMA."""
+    from model_amd import _lib
+    from model_amd._lib import check, ptr
+
+    L = _lib.lib()
+    H, n, half = 4, 8192, 128
+    g = torch.Generator(device="cuda").manual_seed(5)
+    keys = torch.randn((H, 2, n, half), generator=g, device="cuda")
+    k_hat = torch.empty_like(keys)
+    packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, _lib.MPL_F16), dtype=torch.uint8, device="cuda")
+    check(L.mpl_pack_keys(ptr(keys), H, n, half, _lib.MPL_F16, ptr(k_hat), ptr(packed),
+                          _lib.stream_ptr(keys.device)), "mpl_pack_keys")
+    wsb = L.mpl_key_diversity_workspace_bytes(H, n, half)
+    ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
+    loss = torch.empty(1, dtype=torch.float32, device="cuda")
+    dk = torch.empty_like(keys)
+
+    def fn():
+        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, ptr(ws), wsb, ptr(loss), ptr(dk),
+                                  _lib.stream_ptr(keys.device)), "mpl_key_diversity")
+
+    ms = time_loop(torch, fn, iters, 3)
+    flops = 2 * (2.0 * 2 * H * n * n * half)
+    tf = flops / (ms * 1e-3) / 1e12
+    return {"workload": "key_diversity_loss + d/d k_hat, H=4, n=8,192, d_key=256 (2 x 137.4 GFLOP)",
+            "ms": ms, "achieved_tflops": tf, "peak_tflops": MFMA_F16_PEAK_TFLOPS, "frac": tf / MFMA_F16_PEAK_TFLOPS}
 
 
 def cpu_baseline(seconds: float):
@@ -395,10 +429,11 @@ def main():
         large = {"workload": "decode lookup, 67,108,864 fp16 slots (34 GB), H=4, d_key=256, k=16, d_value=256",
                  "by_tokens": sweep}
 
-    train = None
+    train = div = None
     if not args.no_train:
         train = {"train_step": train_step_bench(torch, max(5, args.steps // 20)),
                  "sparse_update_zipf": sparse_update_bench(torch, max(10, args.steps // 10))}
+        div = key_diversity_bench(torch, max(5, args.steps // 20))
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
@@ -422,6 +457,7 @@ def main():
         "kernels": br,
         "pool_67M": large,
         "training_262k": train,
+        "key_diversity_67M": div,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
