@@ -1,0 +1,108 @@
+"""Token-by-token generation with a KV cache (memory_pool_model/generate.py:23-65).
+
+Like the reference, every position, prompt included, is one decode step of
+the backbone with its memory reads (MemoryPool: libmpl.so).  The decode step
+has static shapes (token batch [B], position as a device tensor), so it is
+captured once in a HIP graph and replayed; the next input token (the prompt's
+or the argmax of the step's logits) is chosen on the device, so a whole
+generation is queued without a host round trip per token.
+"""
+
+from __future__ import annotations
+
+import time
+from typing import Dict, Optional
+
+import numpy as np
+import torch
+
+from .model import MemoryPoolLM, ModelConfig
+
+
+class Generator:
+    """generate.py:23-65.  ``graph=False`` runs the decode step eagerly."""
+
+    def __init__(self, mcfg: ModelConfig, params, batch_size: int = 1, graph: bool = True, device="cuda"):
+        self.mcfg, self.batch_size, self.device = mcfg, batch_size, torch.device(device)
+        self.params = params["params"] if "params" in params else params
+        self.model = MemoryPoolLM(mcfg, decode=True)
+        self.cache = self.model.init_cache(batch_size, self.device)
+        self.tok = torch.zeros(batch_size, dtype=torch.int64, device=self.device)
+        self.pos = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.logits = None
+        self.graph = None
+        self.use_graph = graph
+
+    def _step(self):
+        logits, _ = self.model.apply({"params": self.params}, self.tok[:, None], positions=self.pos,
+                                     cache=self.cache)
+        return logits[:, 0]
+
+    def _reset_cache(self):
+        for c in self.cache:
+            c["k"].zero_()
+            c["v"].zero_()
+
+    def _ensure_graph(self):
+        if not self.use_graph or self.graph is not None:
+            return
+        # warm up on a side stream (key packing, temperature read, workspaces)
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                self._step()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.logits = self._step()
+
+    def generate(self, prompt, n_new: int, temperature: float = 0.0, seed: int = 0,
+                 keep_logits: bool = True, sync_each_step: bool = False) -> Dict[str, object]:
+        """prompt [B, P] int tokens; greedy when temperature == 0.  Returns
+        tokens [B, n_new], the logits of every step [B, P+n_new-1, vocab] (if
+        keep_logits) and per-step wall times (measured only with
+        sync_each_step, as the reference does)."""
+        prompt = torch.as_tensor(np.asarray(prompt), dtype=torch.int64, device=self.device)
+        B, P = prompt.shape
+        if B != self.batch_size:
+            raise ValueError(f"batch of {B} prompts for a generator built for {self.batch_size}")
+        if P + n_new > self.mcfg.max_len:
+            raise ValueError("prompt + n_new exceeds max_len")
+        with torch.no_grad():
+            return self._generate(prompt, n_new, temperature, seed, keep_logits, sync_each_step)
+
+    def _generate(self, prompt, n_new, temperature, seed, keep_logits, sync_each_step):
+        B, P = prompt.shape
+        self._ensure_graph()
+        self._reset_cache()
+        gen = torch.Generator(device=self.device).manual_seed(int(seed)) if temperature > 0 else None
+        out, logits_all, times = [], [], []
+        self.tok.copy_(prompt[:, 0])
+        for pos in range(P + n_new - 1):
+            t0 = time.perf_counter()
+            self.pos.fill_(pos)
+            if self.graph is not None:
+                self.graph.replay()
+                logits = self.logits
+            else:
+                logits = self._step()
+            if pos + 1 < P:
+                nxt = prompt[:, pos + 1]
+            elif temperature > 0:
+                nxt = torch.multinomial(torch.softmax(logits / temperature, -1), 1, generator=gen)[:, 0]
+            else:
+                nxt = torch.argmax(logits, -1)
+            if keep_logits:
+                logits_all.append(logits.clone())
+            if pos + 1 >= P:
+                out.append(nxt.clone())
+            self.tok.copy_(nxt)
+            if sync_each_step:
+                torch.cuda.synchronize(self.device)
+                times.append(time.perf_counter() - t0)
+        toks = torch.stack(out, 1) if out else torch.zeros((B, 0), dtype=torch.int64, device=self.device)
+        return {"tokens": toks,
+                "logits": torch.stack(logits_all, 1) if keep_logits else None,
+                "step_seconds": np.array(times)}

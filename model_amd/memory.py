@@ -164,16 +164,21 @@ class MemoryPool:
         return self.n_sub_keys ** 2
 
     # ------------------------------------------------------------ params
-    def init(self, rng: int | torch.Generator = 0, queries=None, *, device="cuda") -> Dict[str, Any]:
+    def init(self, rng: int | torch.Generator = 0, queries=None, *, device="cuda",
+             values: Optional[torch.Tensor] = None) -> Dict[str, Any]:
         """memory.py:94-113: sub_keys on the unit sphere, values ~ N(0, d^-1/2),
         log_temperature = log(init_temperature).  ``rng`` is a seed or a
-        torch.Generator on ``device``."""
+        torch.Generator on ``device``.  ``values`` [n*n, d_value] may be given
+        (e.g. a table filled in place) instead of a fresh draw."""
         g = rng if isinstance(rng, torch.Generator) else torch.Generator(device=device).manual_seed(int(rng))
         H, n, half = self.heads, self.n_sub_keys, self.d_key // 2
         keys = torch.randn((H, 2, n, half), generator=g, device=device, dtype=torch.float32)
         keys = keys * torch.rsqrt((keys * keys).sum(-1, keepdim=True) + NORM_EPS)
-        values = torch.randn((self.pool_size, self.d_value), generator=g, device=device, dtype=self.values_dtype)
-        values.mul_(self.d_value ** -0.5)
+        if values is None:
+            values = torch.randn((self.pool_size, self.d_value), generator=g, device=device, dtype=self.values_dtype)
+            values.mul_(self.d_value ** -0.5)
+        elif tuple(values.shape) != (self.pool_size, self.d_value):
+            raise ValueError(f"values must be [{self.pool_size}, {self.d_value}], got {tuple(values.shape)}")
         log_t = torch.tensor(math.log(self.init_temperature), dtype=torch.float32, device=device)
         return {"params": {"sub_keys": keys, "values": values, "log_temperature": log_t}}
 

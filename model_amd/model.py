@@ -1,0 +1,248 @@
+"""Host mirror of the reference backbone (memory_pool_model/model.py:15-145,
+config.py:9-61) around this library's MemoryPool.
+
+The backbone (embedding, attention, layer norms, feed-forward blocks, router
+and gated memory write-back) is small dense work and runs as plain torch ops
+in fp32; every memory read is MemoryPool (libmpl.so).  Parameter names and
+shapes follow the Flax modules, so a checkpoint of the reference
+(model_amd/checkpoint.py) loads into it:
+
+  embed/embedding [vocab, d]            nn.Embed (logits use embed.attend)
+  pos_embed [max_len, d]
+  ln_attn_i, ln_ffn_i, ln_final         nn.LayerNorm {scale, bias}, eps 1e-6
+  attn_i/{query,key,value}              DenseGeneral {kernel [d, heads, hd], bias [heads, hd]}
+  attn_i/out                            DenseGeneral {kernel [heads, hd, d], bias [d]}
+  ffn_in_i, ffn_out_i, router_i,        nn.Dense {kernel [in, out], bias [out]}
+  mem_gate_i, mem_out_i
+  pool/{sub_keys, values, log_temperature}
+
+With ``decode=True`` the attention keeps a key/value cache of max_len
+positions per layer (Flax's decode mode): one token per call at a position
+given as a device tensor, so a decode step has static shapes and can be
+captured in a HIP graph (model_amd/generate.py).
+"""
+
+from __future__ import annotations
+
+import dataclasses
+import math
+from typing import Any, Dict, List, Optional, Tuple
+
+import torch
+import torch.nn.functional as F
+
+from .memory import MemoryPool
+
+LN_EPS = 1e-6  # flax.linen.LayerNorm default
+
+
+@dataclasses.dataclass(frozen=True)
+class ModelConfig:
+    """config.py:9-61 (the fields the forward pass reads)."""
+
+    vocab_size: int = 256
+    max_len: int = 128
+    d_model: int = 128
+    n_layers: int = 2
+    n_heads: int = 4
+    ffn_mult: int = 1
+    dropout: float = 0.0
+    use_memory: bool = True
+    memory_layers: Tuple[int, ...] = (1,)
+    memory_ffn: bool = False
+    n_sub_keys: int = 64
+    pool_heads: int = 4
+    d_key: int = 64
+    d_value: int = 128
+    top_k: int = 16
+    routing_noise: float = 1.0
+    init_temperature: float = 10.0
+    min_temperature: float = 10.0
+    balance_temperature_grad: bool = False
+    max_temperature: float = 100.0
+    router_query_scale: bool = False
+    values_dtype: torch.dtype = torch.float16  # the pool table in HBM (fp32 in the reference)
+
+    @property
+    def pool_size(self) -> int:
+        return self.n_sub_keys ** 2
+
+
+def _dense(x, p):
+    return torch.matmul(x, p["kernel"]) + p["bias"]
+
+
+def _ln(x, p):
+    return F.layer_norm(x, (x.shape[-1],), p["scale"], p["bias"], LN_EPS)
+
+
+def merge_layer_aux(layer_aux: List[Dict[str, Any]]) -> Dict[str, Any]:
+    """model.py:130-145."""
+    if not layer_aux:
+        return {}
+    return {
+        "balance_loss": torch.stack([a["balance_loss"] for a in layer_aux]).mean(),
+        "subkey_counts": sum(a["subkey_counts"] for a in layer_aux),
+        "slot_counts": sum(a["slot_counts"] for a in layer_aux),
+        "queries": [a["queries"] for a in layer_aux],
+        "slots": [a["slots"] for a in layer_aux],
+        "weights": [a["weights"] for a in layer_aux],
+        "temperature": layer_aux[0]["temperature"],
+        "top1_weight": torch.stack([a["top1_weight"] for a in layer_aux]).mean(),
+    }
+
+
+class _LazyMerged(dict):
+    """merge_layer_aux computed on first access (decode never reads it)."""
+
+    def __init__(self, layer_aux):
+        super().__init__()
+        self._layer_aux = layer_aux
+
+    def _fill(self):
+        if self._layer_aux is not None:
+            self.update(merge_layer_aux(self._layer_aux))
+            self._layer_aux = None
+
+    def __getitem__(self, key):
+        self._fill()
+        return dict.__getitem__(self, key)
+
+    def __contains__(self, key):
+        self._fill()
+        return dict.__contains__(self, key)
+
+    def keys(self):
+        self._fill()
+        return dict.keys(self)
+
+
+class MemoryPoolLM:
+    """model.py:15-127."""
+
+    def __init__(self, cfg: ModelConfig, decode: bool = False):
+        self.cfg, self.decode = cfg, decode
+        self.pool = None
+        if cfg.use_memory:
+            self.pool = MemoryPool(cfg.n_sub_keys, cfg.pool_heads, cfg.d_key, cfg.d_value, cfg.top_k,
+                                   routing_noise=cfg.routing_noise, init_temperature=cfg.init_temperature,
+                                   min_temperature=cfg.min_temperature,
+                                   balance_temperature_grad=cfg.balance_temperature_grad,
+                                   max_temperature=cfg.max_temperature, query_scale=cfg.router_query_scale,
+                                   values_dtype=cfg.values_dtype)
+
+    # ------------------------------------------------------------ params
+    def init(self, seed: int = 0, device="cuda", pool_values: Optional[torch.Tensor] = None) -> Dict[str, Any]:
+        """Random parameters with Flax's default initialisers in spirit
+        (lecun-normal kernels, zero biases, unit layer-norm scales);
+        ``pool_values`` supplies the value table instead of a fresh draw."""
+        cfg = self.cfg
+        g = torch.Generator(device=device).manual_seed(int(seed))
+        d, hd = cfg.d_model, cfg.d_model // cfg.n_heads
+
+        def normal(shape, std):
+            return torch.randn(shape, generator=g, device=device) * std
+
+        def dense(i, o):
+            return {"kernel": normal((i, o), i ** -0.5), "bias": torch.zeros(o, device=device)}
+
+        def ln():
+            return {"scale": torch.ones(d, device=device), "bias": torch.zeros(d, device=device)}
+
+        p: Dict[str, Any] = {"embed": {"embedding": normal((cfg.vocab_size, d), d ** -0.5)},
+                             "pos_embed": normal((cfg.max_len, d), 0.02)}
+        for i in range(cfg.n_layers):
+            p[f"ln_attn_{i}"] = ln()
+            att = {nm: {"kernel": normal((d, cfg.n_heads, hd), d ** -0.5),
+                        "bias": torch.zeros((cfg.n_heads, hd), device=device)} for nm in ("query", "key", "value")}
+            att["out"] = {"kernel": normal((cfg.n_heads, hd, d), d ** -0.5), "bias": torch.zeros(d, device=device)}
+            p[f"attn_{i}"] = att
+            p[f"ln_ffn_{i}"] = ln()
+            mem = self.pool is not None and i in cfg.memory_layers
+            if not mem or cfg.memory_ffn:
+                p[f"ffn_in_{i}"] = dense(d, d * cfg.ffn_mult)
+                p[f"ffn_out_{i}"] = dense(d * cfg.ffn_mult, d)
+            if mem:
+                p[f"router_{i}"] = dense(d, cfg.pool_heads * cfg.d_key)
+                p[f"mem_gate_{i}"] = dense(d, cfg.d_value)
+                p[f"mem_out_{i}"] = dense(cfg.d_value, d)
+        p["ln_final"] = ln()
+        if self.pool is not None:
+            p["pool"] = self.pool.init(int(seed) + 1, device=device, values=pool_values)["params"]
+        return {"params": p}
+
+    def init_cache(self, batch_size: int, device="cuda") -> List[Dict[str, torch.Tensor]]:
+        cfg = self.cfg
+        hd = cfg.d_model // cfg.n_heads
+        shape = (batch_size, cfg.n_heads, cfg.max_len, hd)
+        return [{"k": torch.zeros(shape, device=device), "v": torch.zeros(shape, device=device)}
+                for _ in range(cfg.n_layers)]
+
+    # ----------------------------------------------------------- forward
+    def _attention(self, p, h, layer_cache, positions):
+        cfg = self.cfg
+        B, T, d = h.shape
+        hd = d // cfg.n_heads
+
+        def proj(nm):  # DenseGeneral to (heads, hd) -> [B, heads, T, hd]
+            w = p[nm]["kernel"].reshape(d, cfg.n_heads * hd)
+            return (torch.matmul(h, w).reshape(B, T, cfg.n_heads, hd) + p[nm]["bias"]).permute(0, 2, 1, 3)
+
+        q, k, v = proj("query") * (hd ** -0.5), proj("key"), proj("value")
+        if layer_cache is not None:  # decode: write position `positions`, attend to <= it
+            layer_cache["k"].index_copy_(2, positions, k)
+            layer_cache["v"].index_copy_(2, positions, v)
+            k, v = layer_cache["k"], layer_cache["v"]
+            mask = (torch.arange(cfg.max_len, device=h.device) <= positions[:, None])[None, None]
+        else:
+            mask = torch.ones((T, T), dtype=torch.bool, device=h.device).tril()[None, None]
+        s = torch.matmul(q, k.transpose(-1, -2).contiguous())
+        s = s.masked_fill(~mask, torch.finfo(s.dtype).min)
+        a = torch.matmul(torch.softmax(s, dim=-1), v)  # [B, heads, T, hd]
+        a = a.permute(0, 2, 1, 3).reshape(B, T, cfg.n_heads * hd)
+        return torch.matmul(a, p["out"]["kernel"].reshape(cfg.n_heads * hd, d)) + p["out"]["bias"]
+
+    def apply(self, variables: Dict[str, Any], tokens: torch.Tensor, *, train: bool = False, pool_off: bool = False,
+              route_through_pool: bool = False, sparse_grad: bool = False,
+              probes: Optional[Dict[int, torch.Tensor]] = None, positions: Optional[torch.Tensor] = None,
+              noise_scale: float = 1.0, shuffle_pool: bool = False, cache=None, rngs=None):
+        """model.py:27-127: (logits [B, T, vocab], aux).  In decode mode pass
+        ``cache`` (init_cache) and ``positions`` (int64 device tensor [1])."""
+        cfg = self.cfg
+        p = variables["params"] if "params" in variables else variables
+        B, T = tokens.shape
+        emb = p["embed"]["embedding"]
+        if positions is None:
+            x = emb[tokens] + p["pos_embed"][None, :T]
+        else:
+            x = emb[tokens] + p["pos_embed"][positions][None]
+        if self.decode and (cache is None or positions is None):
+            raise ValueError("decode mode needs cache and positions")
+        layer_aux = []
+        for i in range(cfg.n_layers):
+            h = _ln(x, p[f"ln_attn_{i}"])
+            x = x + self._attention(p[f"attn_{i}"], h, cache[i] if self.decode else None, positions)
+            h = _ln(x, p[f"ln_ffn_{i}"])
+            mem_layer = self.pool is not None and i in cfg.memory_layers
+            y = torch.zeros_like(x)
+            if not mem_layer or cfg.memory_ffn:
+                y = _dense(F.gelu(_dense(h, p[f"ffn_in_{i}"]), approximate="tanh"), p[f"ffn_out_{i}"])
+            if mem_layer:
+                if route_through_pool:
+                    x, y = x.detach(), y.detach()
+                if not pool_off:
+                    q = _dense(h, p[f"router_{i}"]).reshape(B, T, cfg.pool_heads, cfg.d_key)
+                    mem, aux = self.pool.apply({"params": p["pool"]}, q, train=train, sparse_grad=sparse_grad,
+                                               noise_scale=noise_scale, shuffle_reads=shuffle_pool, rngs=rngs)
+                    if probes is not None:
+                        mem = mem + probes[i]
+                    h_gate = h.detach() if route_through_pool else h
+                    gate = F.silu(_dense(h_gate, p[f"mem_gate_{i}"]))
+                    y = y + _dense(mem * gate, p[f"mem_out_{i}"])
+                    layer_aux.append(aux)
+            x = x + y
+        x = _ln(x, p["ln_final"])
+        logits = torch.matmul(x, emb.t().contiguous())
+        return logits, _LazyMerged(layer_aux)
+
+    __call__ = apply
