@@ -18,9 +18,14 @@ Also reported in the same JSON line:
     backward + sparse row-wise Adagrad) and the sparse row update alone on
     Zipf(1.1)-skewed routing;
   * ``key_diversity_67M``: key_diversity_loss and its gradient on the
-    67M-slot layer's codebooks (H=4, n=8,192): the n x n Gram tiles on MFMA.
+    67M-slot layer's codebooks (H=4, n=8,192): the n x n Gram tiles on MFMA;
+  * ``generation_268M``: end-to-end batched greedy generation, 4-layer
+    backbone (d_model 256, 4 heads, FFN x4, vocab 16,384) with memory layers
+    1 and 3 reading one 268,435,456-slot fp16 pool (137 GB in HBM), 64
+    streams, 128-token prompts, 256 new tokens, every position one
+    HIP-graph decode step.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large] [--no-train]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large] [--no-train] [--no-generate]
 """
 
 from __future__ import annotations
@@ -52,6 +57,7 @@ def parse():
     ap.add_argument("--no-large", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-train", action="store_true")
+    ap.add_argument("--no-generate", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -352,6 +358,40 @@ def key_diversity_bench(torch, iters):
             "ms": ms, "achieved_tflops": tf, "peak_tflops": MFMA_F16_PEAK_TFLOPS, "frac": tf / MFMA_F16_PEAK_TFLOPS}
 
 
+def generation_bench(torch):
+    """Batched greedy generation through the backbone mirror
+    (model_amd/model.py, generate.py) with two memory layers on a
+    268,435,456-slot fp16 pool filled in place with N(0, 0.02)."""
+    from model_amd.generate import Generator
+    from model_amd.model import MemoryPoolLM, ModelConfig
+
+    n, d, B, P, new = 16384, 256, 64, 128, 256
+    cfg = ModelConfig(vocab_size=16384, max_len=P + new, d_model=256, n_layers=4, n_heads=4, ffn_mult=4,
+                      memory_layers=(1, 3), n_sub_keys=n, pool_heads=4, d_key=256, d_value=d, top_k=16,
+                      values_dtype=torch.float16)
+    g = torch.Generator(device="cuda").manual_seed(7)
+    values = torch.empty((n * n, d), dtype=torch.float16, device="cuda")
+    values.normal_(0.0, 0.02, generator=g)
+    params = MemoryPoolLM(cfg).init(0, pool_values=values)
+    gen = Generator(cfg, params, batch_size=B)
+    prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=g, device="cuda")
+    gen.generate(prompt[:, :8], n_new=4, keep_logits=False)  # capture + warm-up
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    res = gen.generate(prompt, n_new=new, keep_logits=False)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    steps = P + new - 1
+    out = {"workload": "greedy generation: 4-layer backbone (d_model 256, 4 heads, FFN x4, vocab 16,384), "
+                       "memory layers 1 and 3, 268,435,456-slot fp16 pool (137 GB), H=4, k=16, 64 streams, "
+                       "128-token prompts, 256 new tokens (383 decode steps, one HIP graph per step)",
+           "seconds": sec, "ms_per_step": 1e3 * sec / steps, "generated_tokens_per_s": B * new / sec,
+           "processed_tokens_per_s": B * steps / sec, "tokens_shape": list(res["tokens"].shape)}
+    del gen, params, values
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds: float):
     """The numpy oracle (oracle/lookup.py) on the host cores: the same layer
     shape (262,144 fp16 slots, H=4, d_key=256, k=16) on batches of 1,024
@@ -435,6 +475,8 @@ def main():
                  "sparse_update_zipf": sparse_update_bench(torch, max(10, args.steps // 10))}
         div = key_diversity_bench(torch, max(5, args.steps // 20))
 
+    generation = None if args.no_generate else generation_bench(torch)
+
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -458,6 +500,7 @@ def main():
         "pool_67M": large,
         "training_262k": train,
         "key_diversity_67M": div,
+        "generation_268M": generation,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

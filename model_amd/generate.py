@@ -64,7 +64,9 @@ class Generator:
         tokens [B, n_new], the logits of every step [B, P+n_new-1, vocab] (if
         keep_logits) and per-step wall times (measured only with
         sync_each_step, as the reference does)."""
-        prompt = torch.as_tensor(np.asarray(prompt), dtype=torch.int64, device=self.device)
+        if not isinstance(prompt, torch.Tensor):
+            prompt = torch.as_tensor(np.asarray(prompt))
+        prompt = prompt.to(device=self.device, dtype=torch.int64)
         B, P = prompt.shape
         if B != self.batch_size:
             raise ValueError(f"batch of {B} prompts for a generator built for {self.batch_size}")
