@@ -339,7 +339,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     for (int r = 0; r < 16; ++r) {
       issue_for(r, issue);
       const float v = raw ? c[r] : sv[r];
-      ma[r] = active ? fmaxf(ma[r], v) : ma[r];
+      // compare-select, not fmaxf: IEEE maxNum makes the compiler quiet
+      // both inputs first (three v_max per element); scores are never NaN
+      ma[r] = (active && v > ma[r]) ? v : ma[r];
     }
   });
   float mb[16];  // the partner lane's maxima
