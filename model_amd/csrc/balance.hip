@@ -128,6 +128,7 @@ struct BalFwdParams {
   int64_t M;
   int HC, n, half, nblk;
   float4* state;          // [HC, M]: (log2-sum-exp2 of z log2e, r, T_eff log2e, 0)
+  float* parts;           // [grid]: sum of r over the workgroup's queries
 };
 
 // One block of 32 keys staged in LDS by the whole workgroup, plain loads
@@ -152,6 +153,20 @@ struct Stage {
     }
   }
 };
+
+// Sum over the 256 threads of a workgroup in a fixed order (every thread
+// must call it; the result is returned to all).
+__device__ __forceinline__ float block_sum256(float v, float* sh) {
+  sh[threadIdx.x] = v;
+  __syncthreads();
+  for (int off = 128; off >= 1; off >>= 1) {
+    if ((int)threadIdx.x < off) sh[threadIdx.x] += sh[threadIdx.x + off];
+    __syncthreads();
+  }
+  const float r = sh[0];
+  __syncthreads();
+  return r;
+}
 
 // Lanes l and l+32 hold the same query; returns the partner lane's value.
 __device__ __forceinline__ float partner(float v, int par) {
@@ -229,16 +244,20 @@ __global__ __launch_bounds__(kBalThreads) void balance_fwd_kernel(BalFwdParams p
   const float s1 = mx == -INFINITY ? 0.f : exp2f(mx - mm);
   const float s2 = mo == -INFINITY ? 0.f : exp2f(mo - mm);
   const float St = S * s1 + So * s2, Ft = F * s1 + Fo * s2;
-  if (valid && par == 0) p.state[(int64_t)hc * p.M + my_q] = make_float4(mm + log2f(St), Ft / St * p.inv_mk, t2, 0.f);
+  const float r = Ft / St * p.inv_mk;
+  if (valid && par == 0) p.state[(int64_t)hc * p.M + my_q] = make_float4(mm + log2f(St), r, t2, 0.f);
+  __shared__ float red[kBalThreads];
+  const float wsum = block_sum256((valid && par == 0) ? r : 0.f, red);
+  if (tid == 0) p.parts[blockIdx.x] = wsum;
 }
 
-// balance = coef * sum of the r column of the state, fixed order.
-__global__ __launch_bounds__(1024) void balance_loss_kernel(const float4* __restrict__ state, int64_t count,
+// balance = coef * sum of the workgroups' sums of r, fixed order.
+__global__ __launch_bounds__(1024) void balance_loss_kernel(const float* __restrict__ parts, int64_t count,
                                                             float coef, float* __restrict__ loss) {
   __shared__ double part[1024];
   const int tid = threadIdx.x;
   double s = 0.0;
-  for (int64_t i = tid; i < count; i += 1024) s += (double)state[i].y;
+  for (int64_t i = tid; i < count; i += 1024) s += (double)parts[i];
   part[tid] = s;
   __syncthreads();
   for (int off = 512; off >= 1; off >>= 1) {
@@ -334,7 +353,7 @@ struct BalGradParams {
   int64_t sblk_per_split;
   const float* rho;  // [M, HC] (DK: folded into the streamed pack already; DQ: output scale) or null
   float* out;        // DQ: d q_hat [M, HC, half]; DK: partial d k_hat [splits, HC, n, half]
-  float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null; Div: per-thread sums of squares
+  float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null; Div: per-workgroup sums of squares
 };
 
 enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2 };
@@ -462,7 +481,9 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   }
 
   if (DIV) {
-    p.u[(int64_t)blockIdx.x * kBalThreads + tid] = usum;
+    __shared__ float red[kBalThreads];
+    const float wsum = block_sum256(usum, red);
+    if (tid == 0) p.u[blockIdx.x] = wsum;
     if (!grad) return;
   }
   // d = c T (rho) / sigma * acc (kModeDiv: coef * acc); rows of the output
@@ -508,14 +529,18 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float4* __restrict
 __global__ __launch_bounds__(256) void balance_temp_kernel(const float* __restrict__ u, const float* __restrict__ rho,
                                                            int64_t M, int HC, float T, float* __restrict__ dlen,
                                                            float* __restrict__ part) {
+  __shared__ float red[256];
   const int64_t total = M * HC;
+  float acc = 0.f;
   for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
     const int64_t m = i / HC;
     const int hc = (int)(i % HC);
     const float v = u[(int64_t)hc * M + m];
     if (dlen != nullptr) dlen[i] = T * v;
-    part[i] = T * (rho != nullptr ? rho[i] : 1.f) * v;
+    acc += T * (rho != nullptr ? rho[i] : 1.f) * v;
   }
+  const float wsum = block_sum256(acc, red);
+  if (threadIdx.x == 0) part[blockIdx.x] = wsum;
 }
 
 __global__ __launch_bounds__(1024) void sum_plain_kernel(const float* __restrict__ x, int64_t n, double scale,
@@ -632,7 +657,12 @@ extern "C" int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_i
   return check_launch("mpl_route_counts");
 }
 
-extern "C" size_t mpl_balance_state_bytes(int64_t M, int H) { return (size_t)(M > 0 ? M : 0) * 2 * H * 16; }
+static int64_t fwd_groups(int64_t M, int H) { return (int64_t)2 * H * cdiv(M, kRowsPerGroup); }
+
+extern "C" size_t mpl_balance_state_bytes(int64_t M, int H) {
+  if (M <= 0 || H <= 0) return 0;
+  return (size_t)M * 2 * H * 16 + (size_t)fwd_groups(M, H) * 4;
+}
 
 extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
                                int64_t M, int H, int n, int half, int k, float temperature, void* state,
@@ -662,14 +692,15 @@ extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* pac
   p.half = half;
   p.nblk = (int)cdiv(n, 32);
   p.state = (float4*)state;
-  const unsigned grid = (unsigned)(HC * cdiv(M, kRowsPerGroup));
+  p.parts = (float*)((float4*)state + M * HC);
+  const unsigned grid = (unsigned)fwd_groups(M, H);
   switch (KeyPack<_Float16>::padded_half(half)) {
     case 16: balance_fwd_kernel<16><<<grid, kBalThreads, 0, s>>>(p); break;
     case 32: balance_fwd_kernel<32><<<grid, kBalThreads, 0, s>>>(p); break;
     case 64: balance_fwd_kernel<64><<<grid, kBalThreads, 0, s>>>(p); break;
     default: balance_fwd_kernel<128><<<grid, kBalThreads, 0, s>>>(p); break;
   }
-  balance_loss_kernel<<<1, 1024, 0, s>>>((const float4*)state, M * HC, (float)((double)n / ((double)HC * M)), loss);
+  balance_loss_kernel<<<1, 1024, 0, s>>>(p.parts, grid, (float)((double)n / ((double)HC * M)), loss);
   return check_launch("mpl_balance_fwd");
 }
 
@@ -773,9 +804,9 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
     split_sum_kernel<<<grid_for(c4, 256), 256, 0, s>>>((const float4*)part, L.splits, c4, (float4*)dk_hat);
   }
   if (btg) {
-    balance_temp_kernel<<<grid_for(M * HC, 256), 256, 0, s>>>(u, rho, M, HC, temperature, query_scale ? dlen : nullptr,
-                                                             tpart);
-    sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, M * HC, 1.0, dlogt);
+    const unsigned gt = grid_for(M * HC, 256);
+    balance_temp_kernel<<<gt, 256, 0, s>>>(u, rho, M, HC, temperature, query_scale ? dlen : nullptr, tpart);
+    sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, gt, 1.0, dlogt);
   }
   return check_launch("mpl_balance_bwd");
 }
@@ -808,7 +839,7 @@ DivLayout div_layout(int H, int n, int half) {
   L.part = o;
   o += al256((size_t)L.splits * HC * n * half * 4);
   L.lpart = o;
-  o += al256((size_t)L.groups * kBalThreads * 4);
+  o += al256((size_t)L.groups * 4);
   L.total = o;
   return L;
 }
@@ -867,7 +898,7 @@ extern "C" int mpl_key_diversity(const float* k_hat, const void* packed_keys, in
     const int64_t c4 = (int64_t)HC * n * half / 4;
     split_sum_kernel<<<grid_for(c4, 256), 256, 0, s>>>((const float4*)part, L.splits, c4, (float4*)d_k_hat);
   }
-  sum_plain_kernel<<<1, 1024, 0, s>>>(lpart, L.groups * kBalThreads, 1.0 / D, loss);
+  sum_plain_kernel<<<1, 1024, 0, s>>>(lpart, L.groups, 1.0 / D, loss);
   return check_launch("mpl_key_diversity");
 }
 

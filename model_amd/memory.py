@@ -70,12 +70,12 @@ class _KeyCache:
 
 
 class LazyAux(dict):
-    """The ``aux`` dict of memory.py:217-226.  ``queries``, ``slots``,
-    ``weights`` and ``temperature`` are stored; ``balance_loss``,
-    ``subkey_counts``, ``slot_counts`` and ``top1_weight`` are computed the
-    first time they are read."""
+    """The ``aux`` dict of memory.py:217-226.  ``slots``, ``weights`` and
+    ``temperature`` are stored; ``balance_loss``, ``subkey_counts`` and
+    ``slot_counts`` are computed together, and ``queries`` and
+    ``top1_weight`` each on their own, the first time they are read."""
 
-    _LAZY = ("balance_loss", "subkey_counts", "slot_counts", "top1_weight")
+    _LAZY = ("balance_loss", "subkey_counts", "slot_counts")
     _INTERNAL = ("_f", "_p", "_cos", "_counts", "_state")
 
     def __init__(self, eager: Dict[str, Any], compute, **lazy):
@@ -283,7 +283,7 @@ class MemoryPool:
             "slots": slots.reshape(*lead, H, k),
             "weights": weights.reshape(*lead, H, k),
             "temperature": self._temp_tensor,
-        }, stats, queries=lambda: res["q_hat"])
+        }, stats, queries=lambda: res["q_hat"], top1_weight=lambda: weights.max(-1).values.mean())
         res.update({
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
             "k_hat": k_hat, "packed": packed, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
@@ -312,11 +312,7 @@ class MemoryPool:
         slot_counts = torch.empty(self.pool_size, dtype=torch.float32, device=dev)
         check(L.mpl_route_counts(ptr(slots), ptr(clean), M, H, n, k, ptr(subkey_counts), ptr(clean_counts),
                                  ptr(slot_counts), stream), "mpl_route_counts")
-        stats = {
-            "subkey_counts": subkey_counts,
-            "slot_counts": slot_counts,
-            "top1_weight": weights.max(-1).values.mean(),
-        }
+        stats = {"subkey_counts": subkey_counts, "slot_counts": slot_counts}
         if score_code == MPL_F16 and M > 0:
             scaled = int(bool(self.balance_temperature_grad and self.query_scale))
             state = torch.empty(max(L.mpl_balance_state_bytes(M, H), 16), dtype=torch.uint8, device=dev)
