@@ -274,7 +274,7 @@ int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_idx, int64_t
  * balance logits are then the query-scaled scores).  queries: raw fp32
  * [M,H,2,half] (normalised inside).  packed_keys: from mpl_pack_keys with
  * MPL_F16.  `state` (mpl_balance_state_bytes) receives per (token, codebook)
- * the softmax statistics that mpl_balance_bwd needs; loss [1].
+ * the softmax statistics that mpl_lookup_bwd_dense needs; loss [1].
  */
 size_t mpl_balance_state_bytes(int64_t M, int H);
 int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
@@ -282,24 +282,32 @@ int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, c
                     void* stream);
 
 /*
- * Derivative of the balance loss (memory.py:209-213 under XLA autodiff, f
- * held constant) for the upstream gradient g_balance (device scalar):
- *   dq_hat [M,H,2,half]: d/d(normalised queries), written;
- *   dk_hat [H,2,n,half]: d/d(normalised sub-keys), written;
- * with balance_temperature_grad additionally
- *   dlen [M,H,2] (query_scale only): d/d q_len, written;
- *   dlogt [1]: the balance's share of d log_temperature.
- * These are the *_extra inputs of mpl_lookup_bwd_queries / _keys and the
- * `add` of mpl_sum.  q_hat from mpl_l2_normalize, k_hat from mpl_pack_keys,
- * `state` from mpl_balance_fwd of the same inputs.  Two MFMA passes recompute
- * the score tiles (no [M, n] tensor is formed).
+ * The dense-over-n part of the lookup backward (fp16 scoring) on MFMA tiles
+ * that recompute the scores:
+ *   dk_hat [H,2,n,half], written: d/d(normalised sub-keys) of
+ *     - the routed term (sub_idx, d_sub [M,H,2,k] non-NULL): the selected
+ *       scores' gradient d_sub * T (* q_len with query_scale) against the
+ *       normalised queries (memory.py:149-163 under XLA autodiff);
+ *     - the balance term (g_balance non-NULL, a device scalar): the
+ *       derivative of memory.py:209-213 with f held constant;
+ *   dq_hat [M,H,2,half], written when g_balance != NULL: the balance term's
+ *     d/d(normalised queries) (the routed d q_hat stays with
+ *     mpl_lookup_bwd_queries, whose dq_hat_extra this is);
+ *   with balance_temperature_grad and g_balance: dlen [M,H,2]
+ *     (query_scale only) and dlogt [1], the balance's d q_len and d log_t
+ *     shares.
+ * q_hat from mpl_l2_normalize; k_hat and packed_keys from mpl_pack_keys
+ * (MPL_F16); clean_counts and state from mpl_route_counts / mpl_balance_fwd
+ * of the same inputs; q_len [M,H,2] with query_scale.  The raw sub-keys'
+ * gradient follows with mpl_l2_normalize_bwd.  Nothing of size [M, n] is
+ * formed; no atomics.
  */
-size_t mpl_balance_bwd_workspace_bytes(int64_t M, int H, int n, int half);
-int mpl_balance_bwd(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
-                    const float* clean_counts, const void* state, const float* g_balance,
-                    int balance_temperature_grad, int query_scale, int64_t M, int H, int n, int half, int k,
-                    float temperature, void* workspace, size_t workspace_bytes, float* dq_hat, float* dk_hat,
-                    float* dlen, float* dlogt, void* stream);
+size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half);
+int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
+                         const int32_t* sub_idx, const float* d_sub, const float* clean_counts, const void* state,
+                         const float* g_balance, int balance_temperature_grad, int query_scale, int64_t M, int H,
+                         int n, int half, int k, float temperature, void* workspace, size_t workspace_bytes,
+                         float* dq_hat, float* dk_hat, float* dlen, float* dlogt, void* stream);
 
 #ifdef __cplusplus
 }

@@ -13,9 +13,12 @@
 //   revive_kernel        revive_dead_keys (memory.py:243-281) in place
 //   balance_grad_kernel  the gradient of balance (dense over n) with respect
 //                        to the normalised queries and sub-keys, as two MFMA
-//                        passes that recompute the score tiles; the same
-//                        kernel computes key_diversity_loss (memory.py:230-240)
-//                        and its gradient from the Gram tiles of the sub-keys
+//                        passes that recompute the score tiles; the sub-key
+//                        pass also takes the routed term (d sub_scores of the
+//                        selected keys), so the whole d k_hat is one dense
+//                        pass; the same kernel computes key_diversity_loss
+//                        (memory.py:230-240) and its gradient from the Gram
+//                        tiles of the sub-keys
 //
 // With f fixed (stop_gradient, memory.py:208) the loss is
 // n/(2H M) sum_{m,hc} r_m, so the gradient with respect to the logits is
@@ -41,6 +44,8 @@ constexpr int kBalThreads = 256;  // four waves
 constexpr int kBalWaves = kBalThreads / kWave;
 constexpr int kRowsPerGroup = 32 * kBalWaves;  // fixed-side rows per workgroup
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kRtPitch = 36;  // floats per key row of the routed-term tile (32 queries + bank padding)
 
 typedef Mfma<_Float16> MF;
 
@@ -316,23 +321,82 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict_
   }
 }
 
-// sigma[hc] = 2^floor(log2(n/4)) / max(f), with f = counts / (M k).
-__global__ __launch_bounds__(256) void balance_sigma_kernel(const float* __restrict__ counts, int n, float inv_mk,
-                                                            float* __restrict__ sigma) {
-  __shared__ float part[256];
-  const int hc = blockIdx.x;
-  float m = 0.f;
-  for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, counts[(int64_t)hc * n + i]);
-  part[threadIdx.x] = m;
-  __syncthreads();
-  for (int off = 128; off >= 1; off >>= 1) {
-    if (threadIdx.x < off) part[threadIdx.x] = fmaxf(part[threadIdx.x], part[threadIdx.x + off]);
+// Per codebook maxima of |d_sub| and q_len over a range of tokens: workgroup
+// b covers tokens [b * tpg, (b + 1) * tpg) and writes part[b][hc] =
+// (max |d_sub|, max q_len).  Maxima do not depend on the order of the
+// comparisons, so the result is deterministic.
+__global__ __launch_bounds__(256) void bwd_max_kernel(const float* __restrict__ d_sub,
+                                                      const float* __restrict__ q_len, int64_t M, int HC, int k,
+                                                      int64_t tpg, float2* __restrict__ part) {
+  __shared__ float red[2][256];
+  const int tid = threadIdx.x;
+  const int64_t t0 = (int64_t)blockIdx.x * tpg;
+  const int64_t t1 = t0 + tpg < M ? t0 + tpg : M;
+  for (int hc = 0; hc < HC; ++hc) {
+    float dm = 0.f, qm = 0.f;
+    if (d_sub != nullptr)
+      for (int64_t e = t0 * k + tid; e < t1 * k; e += 256) {
+        const int64_t m = e / k;
+        dm = fmaxf(dm, fabsf(d_sub[(m * HC + hc) * k + (e - m * k)]));
+      }
+    if (q_len != nullptr)
+      for (int64_t m = t0 + tid; m < t1; m += 256) qm = fmaxf(qm, q_len[m * HC + hc]);
+    red[0][tid] = dm;
+    red[1][tid] = qm;
+    __syncthreads();
+    for (int off = 128; off >= 1; off >>= 1) {
+      if (tid < off) {
+        red[0][tid] = fmaxf(red[0][tid], red[0][tid + off]);
+        red[1][tid] = fmaxf(red[1][tid], red[1][tid + off]);
+      }
+      __syncthreads();
+    }
+    if (tid == 0) part[(int64_t)blockIdx.x * HC + hc] = make_float2(red[0][0], red[1][0]);
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    const float p2 = exp2f(floorf(log2f(fmaxf((float)n * 0.25f, 1.f))));
-    const float fmax = part[0] * inv_mk;
-    sigma[hc] = fmax > 0.f ? p2 / fmax : 1.f;
+}
+
+// Per codebook: sigma = 2^floor(log2(n/4)) / max f (the d q_hat operand
+// scale, f = counts / (M k)) and S = (bound on |d cos| of the sub-key pass) /
+// 2^14, the bound being T (max q_len if query_scale) max |d_sub| plus the
+// balance term's T (max q_len if its logits carry it) |c| max f.  One
+// workgroup per codebook over the partial maxima.
+__global__ __launch_bounds__(256) void bwd_scale_kernel(const float* __restrict__ counts,
+                                                        const float2* __restrict__ part, int nparts, int n,
+                                                        int HC, float inv_mk, const float* __restrict__ g, float coef,
+                                                        float T, int btg, int qs, float* __restrict__ sigma,
+                                                        float* __restrict__ S) {
+  __shared__ float red[3][256];
+  const int hc = blockIdx.x, tid = threadIdx.x;
+  float fm = 0.f, dm = 0.f, qm = 0.f;
+  if (counts != nullptr)
+    for (int i = tid; i < n; i += 256) fm = fmaxf(fm, counts[(int64_t)hc * n + i]);
+  for (int b = tid; b < nparts; b += 256) {
+    const float2 v = part[(int64_t)b * HC + hc];
+    dm = fmaxf(dm, v.x);
+    qm = fmaxf(qm, v.y);
+  }
+  red[0][tid] = fm;
+  red[1][tid] = dm;
+  red[2][tid] = qm;
+  __syncthreads();
+  for (int off = 128; off >= 1; off >>= 1) {
+    if (tid < off)
+      for (int j = 0; j < 3; ++j) red[j][tid] = fmaxf(red[j][tid], red[j][tid + off]);
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const float fmax = red[0][0] * inv_mk;
+    if (sigma != nullptr) {
+      const float p2 = exp2f(floorf(log2f(fmaxf((float)n * 0.25f, 1.f))));
+      sigma[hc] = fmax > 0.f ? p2 / fmax : 1.f;
+    }
+    const float rho_r = qs ? red[2][0] : 1.f;
+    const float rho_b = (btg && qs) ? red[2][0] : 1.f;
+    float bound = T * rho_r * red[1][0];
+    if (g != nullptr) bound += T * rho_b * fabsf(*g * coef) * fmax;
+    const float sc = bound * (1.0f / 16384.f);
+    S[hc] = (sc > 0.f && sc < INFINITY) ? sc : 1.f;
   }
 }
 
@@ -351,16 +415,29 @@ struct BalGradParams {
   int64_t fblk, sblk;  // blocks of 32 rows on the fixed / streamed side
   int splits;
   int64_t sblk_per_split;
-  const float* rho;  // [M, HC] (DK: folded into the streamed pack already; DQ: output scale) or null
+  const float* rho;  // DQ: [M, HC] output scale (q_len in the balance logits) or null
   float* out;        // DQ: d q_hat [M, HC, half]; DK: partial d k_hat [splits, HC, n, half]
   float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null; Div: per-workgroup sums of squares
+  // kModeDK only
+  int bal;                // balance terms on (g, state, counts valid)
+  const int32_t* sub_idx; // routed term: stage-1 ids [M, HC, k], or null
+  const float* d_sub;     // routed term: d sub_scores [M, HC, k]
+  const float* qlen_rt;   // routed term: q_len [M, HC] with query_scale, or null
+  int k;
+  const float* dk_scale;  // [HC] operand scale S: the operand is dcos / S, d k_hat = S * acc
 };
 
 enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2 };
 
 // kModeDQ: the fixed side is 32 queries per wave (B operand), sub-key blocks
 // stream.  kModeDK: the fixed side is 32 sub-keys per wave, blocks of 32
-// queries stream (the query range is split over `splits` workgroups).
+// queries stream (the query range is split over `splits` workgroups); the
+// operand is the whole d cos of the sub-keys (balance term and, with
+// sub_idx, the routed term d_sub * T (* q_len) of memory.py:150-163) over S.
+// The routed entries of each query block whose ids fall in the workgroup's
+// 128 sub-keys are scattered into an LDS tile [key][query] one block ahead;
+// every lane reads its 16 entries and zeroes them, so the tile is clean when
+// its buffer comes round again.
 // kModeDiv: both sides are the sub-keys of one codebook (the Gram matrix of
 // key_diversity_loss); the operand is the off-diagonal cosine itself and each
 // lane also sums its squares into u[workgroup * 256 + thread].
@@ -375,12 +452,16 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   constexpr int ND = (HP + 31) / 32;
   constexpr int TN = NCH * kWave, TT = ND * 2 * kWave, TILE = TN + TT;
   __shared__ uint4 tiles[2][TILE];
+  __shared__ __attribute__((aligned(16)))
+  float rtile[MODE == kModeDK ? 2 : 1][MODE == kModeDK ? kRowsPerGroup : 1][MODE == kModeDK ? kRtPitch : 1];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, par = lane >> 5;
   const int hc = blockIdx.x % p.HC;
   const int64_t rest = blockIdx.x / p.HC;
   const int split = (int)(rest % p.splits);
   const int64_t fg = rest / p.splits;
+  const bool route = MODE == kModeDK && p.sub_idx != nullptr;
+  const bool bal = MODE != kModeDK || p.bal != 0;
   const int64_t fb = fg * kBalWaves + wave;  // this wave's fixed block
   const int64_t nfix = DK ? p.n : p.M;
   const int64_t nstr = (DK && !DIV) ? p.M : p.n;
@@ -395,18 +476,53 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
 #pragma unroll
     for (int c = 0; c < NCH; ++c) fop[c] = MF::from_vec(src[c * kWave + lane], 0);
   }
-  const float sig = DIV ? 1.f : p.sigma[hc];
+  const float sig = (MODE == kModeDQ) ? p.sigma[hc] : 1.f;
   const float fs = p.inv_mk * sig;  // scaled f per count
-  const float* cnt = DIV ? nullptr : p.counts + (int64_t)hc * p.n;
-  const float4* sth = DIV ? nullptr : p.state + (int64_t)hc * p.M;
+  const float* cnt = bal && !DIV ? p.counts + (int64_t)hc * p.n : nullptr;
+  const float4* sth = bal && !DIV ? p.state + (int64_t)hc * p.M : nullptr;
+  const float cc = (bal && !DIV) ? *p.g * p.coef : 1.f;
+  const float invS = MODE == kModeDK ? 1.f / p.dk_scale[hc] : 1.f;
   // per-lane constants of the fixed row
   float4 fst = make_float4(0.f, 0.f, 0.f, 0.f);
   float ffix = 0.f;
-  if (MODE == kModeDK)
-    ffix = cnt[valid ? my_f : 0] * fs;
+  if (MODE == kModeDK && bal)
+    ffix = cnt[valid ? my_f : 0] * p.inv_mk;
   else if (MODE == kModeDQ)
     fst = sth[valid ? my_f : 0];
   const float rs_fix = fst.y * sig;
+  const int64_t k0 = fg * kRowsPerGroup;  // kModeDK: the workgroup's first sub-key
+  const int f_loc = wave * 32 + (lane & 31);
+  // kModeDK: routed entries of query block b whose ids are in [k0, k0 + 128)
+  // go to rtile[x][id - k0][query - 32 b] (ids of one query are distinct).
+  // rload fetches this thread's (at most 4: k <= 32) entries of block b into
+  // registers, rstore writes them; the loads of block b+1 are issued with the
+  // tile loads and written after the block's MFMAs.
+  constexpr int kRtPer = (32 * 32 + kBalThreads - 1) / kBalThreads;
+  int rrel[kRtPer], rq[kRtPer];
+  float rval[kRtPer];
+  auto rload = [&](int64_t b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kRtPer; ++i) {
+      const int e = tid + i * kBalThreads;
+      rrel[i] = -1;
+      if (MODE != kModeDK || e >= 32 * p.k) continue;
+      const int qlo = e / p.k, j = e - qlo * p.k;
+      const int64_t m = b * 32 + qlo;
+      if (m >= p.M) continue;
+      const int64_t o = (m * p.HC + hc) * p.k + j;
+      const int64_t rel = (int64_t)p.sub_idx[o] - k0;
+      if (rel < 0 || rel >= kRowsPerGroup) continue;
+      const float sc = p.qlen_rt != nullptr ? p.qlen_rt[m * p.HC + hc] : 1.f;
+      rrel[i] = (int)rel;
+      rq[i] = qlo;
+      rval[i] = p.d_sub[o] * sc * p.T;
+    }
+  };
+  auto rstore = [&](int x) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kRtPer; ++i)
+      if (MODE == kModeDK && rrel[i] >= 0) rtile[MODE == kModeDK ? x : 0][MODE == kModeDK ? rrel[i] : 0][MODE == kModeDK ? rq[i] : 0] = rval[i];
+  };
 
   const int64_t sb0 = (int64_t)split * p.sblk_per_split;
   const int64_t sb1 = sb0 + p.sblk_per_split < p.sblk ? sb0 + p.sblk_per_split : p.sblk;
@@ -419,6 +535,15 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   const uint4* sT = p.strT + (int64_t)hc * p.sblk * TT;
   Stage<TN> stn;
   Stage<TT> stt;
+  if (route) {
+    float* rt = &rtile[0][0][0];
+    for (int i = tid; i < 2 * kRowsPerGroup * kRtPitch; i += kBalThreads) rt[MODE == kModeDK ? i : 0] = 0.f;
+    __syncthreads();
+    if (sb0 < sb1) {
+      rload(sb0);
+      rstore(0);
+    }
+  }
   if (sb0 < sb1) {
     stn.load(sN + sb0 * TN, tid);
     stt.load(sT + sb0 * TT, tid);
@@ -432,11 +557,25 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     if (more) {
       stn.load(sN + (sb + 1) * TN, tid);
       stt.load(sT + (sb + 1) * TT, tid);
+      if (route) rload(sb + 1);
     }
     f32x16 acc = f32x16{};
 #pragma unroll
     for (int c = 0; c < NCH; ++c) acc = MF::mma(MF::from_vec(tiles[cur][c * kWave + lane], 0), fop[c], acc);
-    float gv[16];
+    float gv[16], rtv[16];
+    if (route) {
+      // this lane's routed entries: key f_loc, queries 8 g4 + 4 par + [0, 4)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        float4* src = (float4*)&rtile[MODE == kModeDK ? cur : 0][MODE == kModeDK ? f_loc : 0][MODE == kModeDK ? 8 * g4 + 4 * par : 0];
+        const float4 v = *src;
+        *src = make_float4(0.f, 0.f, 0.f, 0.f);
+        rtv[4 * g4] = v.x;
+        rtv[4 * g4 + 1] = v.y;
+        rtv[4 * g4 + 2] = v.z;
+        rtv[4 * g4 + 3] = v.w;
+      }
+    }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t row = sb * 32 + 8 * (r >> 2) + 4 * par + (r & 3);
@@ -449,9 +588,14 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       }
       float pe, diff;
       if (DK) {
-        const float4 s = sth[rc];  // the streamed query's state
-        pe = exp2f(acc[r] * s.z - s.x);
-        diff = ffix - s.y * sig;
+        // d cos / S: balance c p (f - r) T_eff plus the routed d_sub T (q_len)
+        float g = route ? rtv[r] : 0.f;
+        if (bal) {
+          const float4 s = sth[rc];  // the streamed query's state
+          g += exp2f(acc[r] * s.z - s.x) * (ffix - s.y) * (s.z * kLn2) * cc;
+        }
+        gv[r] = (rv && valid) ? g * invS : 0.f;
+        continue;
       } else {
         pe = exp2f(acc[r] * fst.z - fst.x);
         diff = cnt[rc] * fs - rs_fix;
@@ -476,6 +620,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     if (more) {
       stn.store(tiles[cur ^ 1], tid);
       stt.store(tiles[cur ^ 1] + TN, tid);
+      if (route) rstore(cur ^ 1);
     }
     __syncthreads();
   }
@@ -486,10 +631,9 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     if (tid == 0) p.u[blockIdx.x] = wsum;
     if (!grad) return;
   }
-  // d = c T (rho) / sigma * acc (kModeDiv: coef * acc); rows of the output
-  // are the fixed rows
-  const float cc = DIV ? 1.f : *p.g * p.coef;
-  float scale = DIV ? p.coef : cc * p.T / sig;
+  // DQ: c T (rho) / sigma * acc; DK: S * acc; Div: coef * acc.  Rows of
+  // the output are the fixed rows
+  float scale = DIV ? p.coef : (MODE == kModeDK ? p.dk_scale[hc] : cc * p.T / sig);
   if (!DK && p.rho != nullptr) scale *= p.rho[(valid ? my_f : 0) * p.HC + hc];
   if (!DK && p.u != nullptr) {
     const float ut = usum + partner(usum, par);
@@ -569,9 +713,9 @@ unsigned grid_for(int64_t items, int64_t per_block, unsigned cap = 4096) {
 }
 
 struct BwdLayout {
-  size_t qn, qt, kt, sigma, part, u, tpart, total;
-  int HP, NCH, ND, splits;
-  int64_t mblk, nblk, sbps;
+  size_t qn, qt, kt, sigma, dks, mx, part, u, tpart, total;
+  int HP, NCH, ND, splits, mx_groups;
+  int64_t mblk, nblk, sbps, mx_tpg;
 };
 
 BwdLayout bwd_layout(int64_t M, int H, int n, int half) {
@@ -599,6 +743,12 @@ BwdLayout bwd_layout(int64_t M, int H, int n, int half) {
   o += al256((size_t)HC * L.nblk * L.ND * 2 * kWave * 16);
   L.sigma = o;
   o += al256((size_t)HC * 4);
+  L.dks = o;
+  o += al256((size_t)HC * 4);
+  L.mx_tpg = cdiv(M > 0 ? M : 1, 256) < 64 ? 64 : cdiv(M, 256);  // about 256 workgroups of partial maxima
+  L.mx_groups = (int)cdiv(M > 0 ? M : 1, L.mx_tpg);
+  L.mx = o;
+  o += al256((size_t)L.mx_groups * HC * 8);
   L.part = o;
   o += al256((size_t)L.splits * HC * n * half * 4);
   L.u = o;
@@ -704,59 +854,75 @@ extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* pac
   return check_launch("mpl_balance_fwd");
 }
 
-extern "C" size_t mpl_balance_bwd_workspace_bytes(int64_t M, int H, int n, int half) {
+extern "C" size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half) {
   if (M < 0 || H < 1 || n < 1 || !balance_shape_ok(half)) return 0;
   return bwd_layout(M, H, n, half).total;
 }
 
-extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
-                               const float* clean_counts, const void* state, const float* g_balance,
-                               int balance_temperature_grad, int query_scale, int64_t M, int H, int n, int half,
-                               int k, float temperature, void* workspace, size_t workspace_bytes, float* dq_hat,
-                               float* dk_hat, float* dlen, float* dlogt, void* stream) {
+extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat,
+                                    const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
+                                    const float* clean_counts, const void* state, const float* g_balance,
+                                    int balance_temperature_grad, int query_scale, int64_t M, int H, int n,
+                                    int half, int k, float temperature, void* workspace, size_t workspace_bytes,
+                                    float* dq_hat, float* dk_hat, float* dlen, float* dlogt, void* stream) {
   clear_error();
-  MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_balance_bwd: bad shape");
+  MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_lookup_bwd_dense: bad shape");
   MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
-              "mpl_balance_bwd: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
-  const bool btg = balance_temperature_grad != 0;
+              "mpl_lookup_bwd_dense: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  const bool bal = g_balance != nullptr;
+  const bool routed = sub_idx != nullptr || d_sub != nullptr;
+  const bool btg = bal && balance_temperature_grad != 0;
   const bool scaled = btg && query_scale != 0;
-  MPL_REQUIRE(dk_hat != nullptr && (!btg || dlogt != nullptr), MPL_EINVAL, "mpl_balance_bwd: null output");
-  MPL_REQUIRE(!scaled || M == 0 || q_len != nullptr, MPL_EINVAL, "mpl_balance_bwd: q_len needed with query_scale");
+  MPL_REQUIRE(dk_hat != nullptr && (!btg || dlogt != nullptr), MPL_EINVAL, "mpl_lookup_bwd_dense: null output");
+  MPL_REQUIRE(!routed || (sub_idx != nullptr && d_sub != nullptr), MPL_EINVAL,
+              "mpl_lookup_bwd_dense: sub_idx and d_sub go together");
+  MPL_REQUIRE(M == 0 || q_len != nullptr || !(query_scale != 0 && (routed || scaled)), MPL_EINVAL,
+              "mpl_lookup_bwd_dense: q_len needed with query_scale");
   hipStream_t s = (hipStream_t)stream;
   const int HC = 2 * H;
-  if (M == 0) {
+  if (M == 0 || (!bal && !routed)) {
     fill_zero_kernel<<<grid_for((int64_t)HC * n * half, 256), 256, 0, s>>>(dk_hat, (int64_t)HC * n * half);
     if (btg) fill_zero_kernel<<<1, 256, 0, s>>>(dlogt, 1);
-    return check_launch("mpl_balance_bwd");
+    if (bal && dq_hat != nullptr && M > 0)
+      fill_zero_kernel<<<grid_for(M * HC * half, 256), 256, 0, s>>>(dq_hat, M * HC * half);
+    return check_launch("mpl_lookup_bwd_dense");
   }
-  MPL_REQUIRE(q_hat && k_hat && packed_keys && clean_counts && state && g_balance && dq_hat, MPL_EINVAL,
-              "mpl_balance_bwd: null buffer");
+  MPL_REQUIRE(q_hat && k_hat && packed_keys, MPL_EINVAL, "mpl_lookup_bwd_dense: null buffer");
+  MPL_REQUIRE(!bal || (clean_counts && state && dq_hat), MPL_EINVAL,
+              "mpl_lookup_bwd_dense: the balance term needs clean_counts, state and dq_hat");
   const BwdLayout L = bwd_layout(M, H, n, half);
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
-              "mpl_balance_bwd: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+              "mpl_lookup_bwd_dense: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
   char* ws = (char*)workspace;
   uint4* qn = (uint4*)(ws + L.qn);
   uint4* qt = (uint4*)(ws + L.qt);
   uint4* kt = (uint4*)(ws + L.kt);
   float* sigma = (float*)(ws + L.sigma);
+  float* dks = (float*)(ws + L.dks);
+  float2* mx = (float2*)(ws + L.mx);
   float* part = (float*)(ws + L.part);
   float* u = (float*)(ws + L.u);
   float* tpart = (float*)(ws + L.tpart);
   const float* rho = scaled ? q_len : nullptr;
 
   launch_pack<false>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
-  launch_pack<true>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, rho, 1, HC, L.mblk, qt, s);
-  launch_pack<true>(L.HP, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
+  launch_pack<true>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);
+  if (bal) launch_pack<true>(L.HP, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
   const float inv_mk = (float)(1.0 / ((double)M * k));
-  balance_sigma_kernel<<<HC, 256, 0, s>>>(clean_counts, n, inv_mk, sigma);
+  const float coef = (float)((double)n / ((double)HC * M));
+  bwd_max_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC, k,
+                                             L.mx_tpg, mx);
+  bwd_scale_kernel<<<HC, 256, 0, s>>>(bal ? clean_counts : nullptr, mx, L.mx_groups, n, HC, inv_mk,
+                                      bal ? g_balance : nullptr, coef, temperature, btg ? 1 : 0, query_scale ? 1 : 0,
+                                      bal ? sigma : nullptr, dks);
 
-  BalGradParams p;
+  BalGradParams p = {};
   p.state = (const float4*)state;
   p.counts = clean_counts;
   p.sigma = sigma;
   p.g = g_balance;
   p.inv_mk = inv_mk;
-  p.coef = (float)((double)n / ((double)HC * M));
+  p.coef = coef;
   p.T = temperature;
   p.M = M;
   p.HC = HC;
@@ -764,7 +930,7 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
   p.half = half;
   p.rho = rho;
 
-  // d q_hat: fixed = queries, streamed = sub-keys
+  // d q_hat (balance term): fixed = queries, streamed = sub-keys
   BalGradParams pq = p;
   pq.fix = qn;
   pq.str = (const uint4*)packed_keys;
@@ -776,7 +942,7 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
   pq.out = dq_hat;
   pq.u = btg ? u : nullptr;
   const unsigned gq = (unsigned)(HC * cdiv(M, kRowsPerGroup));
-  // d k_hat: fixed = sub-keys, streamed = queries
+  // d k_hat (balance and routed terms): fixed = sub-keys, streamed = queries
   BalGradParams pk = p;
   pk.fix = (const uint4*)packed_keys;
   pk.str = qn;
@@ -788,9 +954,15 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
   pk.out = L.splits == 1 ? dk_hat : part;
   pk.u = nullptr;
   pk.rho = nullptr;
+  pk.bal = bal ? 1 : 0;
+  pk.sub_idx = routed ? sub_idx : nullptr;
+  pk.d_sub = d_sub;
+  pk.qlen_rt = query_scale ? q_len : nullptr;
+  pk.k = k;
+  pk.dk_scale = dks;
   const unsigned gk = (unsigned)(HC * cdiv(n, kRowsPerGroup) * L.splits);
-#define MPL_GRAD(HPV)                                                        \
-  balance_grad_kernel<kModeDQ, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
+#define MPL_GRAD(HPV)                                                                     \
+  if (bal) balance_grad_kernel<kModeDQ, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
   balance_grad_kernel<kModeDK, HPV><<<gk, kBalThreads, 0, s>>>(pk)
   switch (L.HP) {
     case 16: MPL_GRAD(16); break;
@@ -808,7 +980,7 @@ extern "C" int mpl_balance_bwd(const float* q_hat, const float* q_len, const flo
     balance_temp_kernel<<<gt, 256, 0, s>>>(u, rho, M, HC, temperature, query_scale ? dlen : nullptr, tpart);
     sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, gt, 1.0, dlogt);
   }
-  return check_launch("mpl_balance_bwd");
+  return check_launch("mpl_lookup_bwd_dense");
 }
 
 namespace mpl {

@@ -286,7 +286,7 @@ class MemoryPool:
         }, stats, queries=lambda: res["q_hat"], top1_weight=lambda: weights.max(-1).values.mean())
         res.update({
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
-            "k_hat": k_hat, "packed": packed, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
+            "k_hat": k_hat, "packed": packed, "score_code": score_code, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
             "flat_idx": flat_idx, "slots": slots, "weights": weights, "gumbel": gumbel,
             "noise_coef": noise_coef,
         })
@@ -496,22 +496,32 @@ class _LookupFunction(torch.autograd.Function):
                                      ptr(res["sub_scores"]), M, H, k, int(bool(opts["shuffle_reads"])), None,
                                      ptr(d_sub), ptr(dlogt_part), stream), "mpl_lookup_bwd_route")
 
-        # balance loss, dense over n (memory.py:208-213)
+        # dense over n: the balance loss (memory.py:208-213) and, with fp16
+        # scoring, the whole sub-key gradient on MFMA tiles
         dq_extra = dk_extra = dlen_extra = dlogt_extra = None
         btg = pool.balance_temperature_grad
-        if g_balance is not None and M > 0 and "_state" in ctx.internal:
-            dq_extra = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
-            dk_extra = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
-            dlen_extra = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if (btg and q_len is not None) else None
-            dlogt_extra = torch.empty(1, dtype=torch.float32, device=dev) if btg else None
-            gb = g_balance.reshape(1).float().contiguous()
-            wsb = L.mpl_balance_bwd_workspace_bytes(M, H, n, half)
+        raw_keys = sub_keys.detach().float().contiguous()
+        dk = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+        dense = M > 0 and res["score_code"] == MPL_F16 and _fp16_gram_ok(half)
+        if dense:
+            bal = g_balance is not None and "_state" in ctx.internal
+            dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+            gb = None
+            if bal:
+                dq_extra = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
+                dlen_extra = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if (btg and q_len is not None) else None
+                dlogt_extra = torch.empty(1, dtype=torch.float32, device=dev) if btg else None
+                gb = g_balance.reshape(1).float().contiguous()
+            wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half)
             ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
-            check(L.mpl_balance_bwd(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]),
-                                    ptr(ctx.internal["_counts"]), ptr(ctx.internal["_state"]), ptr(gb), int(btg),
-                                    int(bool(pool.query_scale)), M, H, n, half, k, float(T), ptr(ws), wsb,
-                                    ptr(dq_extra), ptr(dk_extra), ptr(dlen_extra), ptr(dlogt_extra), stream),
-                  "mpl_balance_bwd")
+            check(L.mpl_lookup_bwd_dense(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
+                                         ptr(d_sub), ptr(ctx.internal["_counts"]) if bal else None,
+                                         ptr(ctx.internal["_state"]) if bal else None, ptr(gb), int(btg),
+                                         int(bool(pool.query_scale)), M, H, n, half, k, float(T), ptr(ws), wsb,
+                                         ptr(dq_extra), ptr(dk_hat), ptr(dlen_extra), ptr(dlogt_extra), stream),
+                  "mpl_lookup_bwd_dense")
+            check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
+                                         stream), "mpl_l2_normalize_bwd")
         elif g_balance is not None and M > 0:
             f, p = ctx.internal["_f"], ctx.internal["_p"]
             a = g_balance.reshape(()).float() * (n / (2.0 * H * M))
@@ -536,14 +546,13 @@ class _LookupFunction(torch.autograd.Function):
         check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
                                        ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
                                        float(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
-        # sub-keys
-        dk = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
-        raw_keys = sub_keys.detach().float().contiguous()
-        wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
-        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-        check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
-                                    ptr(dk_extra), M, H, n, half, k, float(T), ptr(ws), wsb, ptr(dk), stream),
-              "mpl_lookup_bwd_keys")
+        # sub-keys (fp32 scoring or no tokens): sort-by-key segmented sum
+        if not dense:
+            wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
+            ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+            check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
+                                        ptr(dk_extra), M, H, n, half, k, float(T), ptr(ws), wsb, ptr(dk), stream),
+                  "mpl_lookup_bwd_keys")
         # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
         dlt = torch.empty(1, dtype=torch.float32, device=dev)
         check(L.mpl_sum(ptr(dlogt_part), M, ptr(dlogt_extra), ptr(dlt), stream), "mpl_sum")

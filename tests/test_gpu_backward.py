@@ -151,3 +151,32 @@ def test_sparse_grad_leaves_values_and_matches_dense_rows(gpu_lib):
     np.testing.assert_allclose(gv.cpu().numpy()[u[keep]], rows.cpu().numpy()[keep], rtol=1e-6, atol=1e-7)
     untouched = np.setdiff1d(np.arange(n * n), u[keep])
     assert np.all(gv.cpu().numpy()[untouched] == 0)
+
+
+@pytest.mark.parametrize("n,H,d_key,k,M,qs,btg,g_bal,seed", [
+    (100, 2, 64, 8, 77, False, False, 0.0, 61),    # routed term only; n not a multiple of 32 or 128
+    (300, 1, 32, 16, 130, True, False, 0.0, 62),   # query_scale; 3 key groups, partial last
+    (64, 2, 16, 32, 45, True, True, 0.4, 63),      # k = 32 (1024 routed entries per query block), half = 8
+    (512, 4, 256, 16, 200, False, False, 0.01, 64),  # the text-study widths with the balance term
+])
+def test_dense_sub_key_gradient_fp16_scoring(gpu_lib, n, H, d_key, k, M, qs, btg, g_bal, seed):
+    """With fp16 scoring the whole sub-key gradient (routed d sub_scores plus
+    the balance term) is one dense MFMA pass (mpl_lookup_bwd_dense) followed
+    by the l2-normalisation backward; compared for the GPU's selection."""
+    pool, params, tq, q, keys, vals, g, log_t = _setup(
+        seed, n=n, H=H, d_key=d_key, d=32, k=k, M=M, values_dtype=torch.float16, score_dtype=torch.float16,
+        query_scale=qs, btg=btg)
+    res_gpu = pool.lookup(params, tq.detach())
+    out, aux = pool.apply({"params": params}, tq, sparse_grad=True)
+    loss = (out * torch.tensor(g, device="cuda")).sum()
+    if g_bal:
+        loss = loss + g_bal * aux["balance_loss"]
+    gq, gk, gt = torch.autograd.grad(loss, [tq, params["sub_keys"], params["log_temperature"]])
+    res = ol.lookup_forward(q, keys, vals, float(log_t), top_k_=k, query_scale=qs, dtype=np.float64)
+    sel = _with_selection(res, res_gpu["sub_idx"].cpu().numpy(), res_gpu["flat_idx"].cpu().numpy(),
+                          res_gpu["slots"].cpu().numpy())
+    f = ol.aux_stats(sel, n=n, noisy=False, balance_temperature_grad=btg)["_f"]
+    ref = ob.lookup_backward(sel, vals, g, n=n, query_scale=qs, g_balance=g_bal, f=f, balance_temperature_grad=btg)
+    _check(gk.cpu().numpy(), ref["d_sub_keys"], 1e-2, "d_sub_keys")
+    _check(gq.cpu().numpy(), ref["d_queries"], 1e-2, "d_queries")
+    _check(float(gt), ref["d_log_temperature"], 1e-2, "d_log_temperature", float(np.abs(ref["d_cos"] * sel["cos"]).sum()))
