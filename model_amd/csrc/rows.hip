@@ -523,6 +523,10 @@ struct TableVec<V, 1> {
   __device__ static void store(V* p, const float* x) { *p = (V)x[0]; }
 };
 
+// One wave per touched row, two rows in flight: the lanes first fetch the
+// ids of the wave's next 64 rows (one load instead of one per row), then each
+// iteration issues both rows' gradient, master and accumulator loads before
+// any arithmetic, so the loads of a row do not wait for the previous row.
 template <typename V, int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict__ values, float* __restrict__ master,
                                                                    float* __restrict__ acc,
@@ -530,46 +534,73 @@ __global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict_
                                                                    const float* __restrict__ rows, int64_t cap, int d,
                                                                    int64_t N, float lr,
                                                                    const float* __restrict__ grad_scale) {
+  constexpr int R = VPL >= 16 ? 1 : 2;  // rows in flight per wave (one for very wide rows)
   const int lane = threadIdx.x & 63;
   const int64_t nw = (int64_t)gridDim.x * (kRowThreads / kWave);
+  const int64_t wid = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
   const int nv = d / W;
   const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
-  for (int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6; u < cap; u += nw) {
-    const int64_t s = uniq[u];
-    if (s < 0 || s >= N) continue;  // padding (mode="drop")
-    float g[VPL][W];
-    float sq = 0.f;
+  for (int64_t base = wid; base < cap; base += kWave * nw) {
+    const int64_t uj = base + lane * nw;
+    const int sj = uj < cap ? uniq[uj] : -1;
+    for (int it = 0; it < kWave; it += R) {
+      if (base + it * nw >= cap) break;  // wave-uniform
+      int64_t us[R], ss[R];
+      bool ok[R];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const int c = lane + kWave * v;
-      if (c < nv) {
-        TableVec<float, W>::load(rows + u * d + (int64_t)c * W, g[v]);
+      for (int r = 0; r < R; ++r) {
+        us[r] = base + (it + r) * nw;
+        ss[r] = __shfl(sj, it + r);
+        ok[r] = us[r] < cap && ss[r] >= 0 && ss[r] < N;  // padding (mode="drop")
+      }
+      float g[R][VPL][W], x[R][VPL][W], a0[R];
 #pragma unroll
-        for (int i = 0; i < W; ++i) {
-          g[v][i] *= sc;
-          sq += g[v][i] * g[v][i];
+      for (int r = 0; r < R; ++r) {
+        a0[r] = ok[r] ? acc[ss[r]] : 0.f;
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          const int c = lane + kWave * v;
+          if (ok[r] && c < nv) {
+            TableVec<float, W>::load(rows + us[r] * d + (int64_t)c * W, g[r][v]);
+            const int64_t o = ss[r] * d + (int64_t)c * W;
+            if (master != nullptr) TableVec<float, W>::load(master + o, x[r][v]);
+            else TableVec<V, W>::load(values + o, x[r][v]);
+          }
         }
       }
-    }
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
-    const float a = acc[s] + sq / (float)d;
-    const float step = lr / (sqrtf(a) + 1e-8f);
+      for (int r = 0; r < R; ++r) {
+        if (!ok[r]) continue;  // wave-uniform
+        float sq = 0.f;
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const int c = lane + kWave * v;
-      if (c < nv) {
-        const int64_t o = s * d + (int64_t)c * W;
-        float x[W];
-        if (master != nullptr) TableVec<float, W>::load(master + o, x);
-        else TableVec<V, W>::load(values + o, x);
+        for (int v = 0; v < VPL; ++v) {
+          const int c = lane + kWave * v;
+          if (c < nv) {
 #pragma unroll
-        for (int i = 0; i < W; ++i) x[i] += -step * g[v][i];
-        if (master != nullptr) TableVec<float, W>::store(master + o, x);
-        TableVec<V, W>::store(values + o, x);
+            for (int i = 0; i < W; ++i) {
+              g[r][v][i] *= sc;
+              sq += g[r][v][i] * g[r][v][i];
+            }
+          }
+        }
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off);
+        const float a = a0[r] + sq / (float)d;
+        const float step = lr / (sqrtf(a) + 1e-8f);
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) {
+          const int c = lane + kWave * v;
+          if (c < nv) {
+            const int64_t o = ss[r] * d + (int64_t)c * W;
+#pragma unroll
+            for (int i = 0; i < W; ++i) x[r][v][i] += -step * g[r][v][i];
+            if (master != nullptr) TableVec<float, W>::store(master + o, x[r][v]);
+            TableVec<V, W>::store(values + o, x[r][v]);
+          }
+        }
+        if (lane == 0) acc[ss[r]] = a;
       }
     }
-    if (lane == 0) acc[s] = a;
   }
 }
 
