@@ -562,9 +562,11 @@ __global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict_
           const int c = lane + kWave * v;
           if (ok[r] && c < nv) {
             TableVec<float, W>::load(rows + us[r] * d + (int64_t)c * W, g[r][v]);
-            const int64_t o = ss[r] * d + (int64_t)c * W;
-            if (master != nullptr) TableVec<float, W>::load(master + o, x[r][v]);
-            else TableVec<V, W>::load(values + o, x[r][v]);
+            if (VPL == 1) {  // wider rows load the table after the reduction (registers)
+              const int64_t o = ss[r] * d + (int64_t)c * W;
+              if (master != nullptr) TableVec<float, W>::load(master + o, x[r][v]);
+              else TableVec<V, W>::load(values + o, x[r][v]);
+            }
           }
         }
       }
@@ -592,6 +594,10 @@ __global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict_
           const int c = lane + kWave * v;
           if (c < nv) {
             const int64_t o = ss[r] * d + (int64_t)c * W;
+            if (VPL != 1) {
+              if (master != nullptr) TableVec<float, W>::load(master + o, x[r][v]);
+              else TableVec<V, W>::load(values + o, x[r][v]);
+            }
 #pragma unroll
             for (int i = 0; i < W; ++i) x[r][v][i] += -step * g[r][v][i];
             if (master != nullptr) TableVec<float, W>::store(master + o, x[r][v]);
@@ -617,31 +623,53 @@ __global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ v
   const int nv = d / W;
   const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
   const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
-  for (int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6; u < cap; u += nw) {
-    const int64_t s = uniq[u];
-    if (s < 0 || s >= N) continue;
+  constexpr int R = VPL >= 16 ? 1 : 2;  // rows in flight per wave, as in row_adagrad_kernel
+  const int64_t wid = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+  for (int64_t base = wid; base < cap; base += kWave * nw) {
+    const int64_t uj = base + lane * nw;
+    const int sj = uj < cap ? uniq[uj] : -1;
+    for (int it = 0; it < kWave; it += R) {
+      if (base + it * nw >= cap) break;  // wave-uniform
+      int64_t us[R], ss[R];
+      bool ok[R];
 #pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const int c = lane + kWave * v;
-      if (c >= nv) continue;
-      const int64_t o = s * d + (int64_t)c * W;
-      float g[W], m[W], q[W], x[W];
-      TableVec<float, W>::load(rows + u * d + (int64_t)c * W, g);
-      TableVec<float, W>::load(m1 + o, m);
-      TableVec<float, W>::load(m2 + o, q);
-      if (master != nullptr) TableVec<float, W>::load(master + o, x);
-      else TableVec<V, W>::load(values + o, x);
-#pragma unroll
-      for (int i = 0; i < W; ++i) {
-        const float gi = g[i] * sc;
-        m[i] = b1 * m[i] + (1.f - b1) * gi;
-        q[i] = b2 * q[i] + (1.f - b2) * gi * gi;
-        x[i] += -lr * (m[i] / c1) / (sqrtf(q[i] / c2) + eps);
+      for (int r = 0; r < R; ++r) {
+        us[r] = base + (it + r) * nw;
+        ss[r] = __shfl(sj, it + r);
+        ok[r] = us[r] < cap && ss[r] >= 0 && ss[r] < N;
       }
-      TableVec<float, W>::store(m1 + o, m);
-      TableVec<float, W>::store(m2 + o, q);
-      if (master != nullptr) TableVec<float, W>::store(master + o, x);
-      TableVec<V, W>::store(values + o, x);
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        if (c >= nv) continue;
+        float g[R][W], m[R][W], q[R][W], x[R][W];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (!ok[r]) continue;
+          const int64_t o = ss[r] * d + (int64_t)c * W;
+          TableVec<float, W>::load(rows + us[r] * d + (int64_t)c * W, g[r]);
+          TableVec<float, W>::load(m1 + o, m[r]);
+          TableVec<float, W>::load(m2 + o, q[r]);
+          if (master != nullptr) TableVec<float, W>::load(master + o, x[r]);
+          else TableVec<V, W>::load(values + o, x[r]);
+        }
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          if (!ok[r]) continue;
+          const int64_t o = ss[r] * d + (int64_t)c * W;
+#pragma unroll
+          for (int i = 0; i < W; ++i) {
+            const float gi = g[r][i] * sc;
+            m[r][i] = b1 * m[r][i] + (1.f - b1) * gi;
+            q[r][i] = b2 * q[r][i] + (1.f - b2) * gi * gi;
+            x[r][i] += -lr * (m[r][i] / c1) / (sqrtf(q[r][i] / c2) + eps);
+          }
+          TableVec<float, W>::store(m1 + o, m[r]);
+          TableVec<float, W>::store(m2 + o, q[r]);
+          if (master != nullptr) TableVec<float, W>::store(master + o, x[r]);
+          TableVec<V, W>::store(values + o, x[r]);
+        }
+      }
     }
   }
 }
