@@ -16,12 +16,15 @@
 // and lower lane id), waves of a tile are ordered through LDS counters, and
 // tiles through the scanned histogram.
 //
-// Segmented sum: wave r owns sorted entries [r*128, r*128 + 128) and walks
-// them in order, eight rows in flight.  A segment that lies inside the range
-// is written as a finished row; the range's first and last segment, when
-// they cross the range boundary, leave partial sums that a fix-up kernel
-// adds in range order.  Hot rows (Zipf-skewed routing) therefore spread over
-// many waves without changing the summation order from run to run.
+// Segmented sum: wave r owns sorted entries [r*128, r*128 + 128), loads
+// their (fetch, segment, weight) once (two per lane) and walks them in order,
+// the dL/dout rows of the next batch loading while the current batch is
+// added.  A segment that lies inside the range is written as a finished row;
+// the range's first and last segment, when they cross the range boundary,
+// leave partial sums that a fix-up kernel (one wave per range: the segment
+// that starts there) adds in range order.  Hot rows (Zipf-skewed routing)
+// therefore spread over many waves without changing the summation order from
+// run to run.
 #include <math.h>
 
 #include <algorithm>
@@ -344,31 +347,45 @@ __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
       }
     }
   };
-  for (int64_t i = r0; i < r1; i += 8) {
-    uint32_t pp[8];
-    int sg[8];
-    float ww[8];
+  // The range's (fetch, segment, weight) entries are loaded once, two per
+  // lane (coalesced), and broadcast with shuffles; the g rows of the next
+  // batch of B entries load while the current batch is accumulated (B rows
+  // of VPL vectors per buffer, so the registers do not grow with the width).
+  static_assert(kRangeLen == 2 * kWave, "two entries per lane");
+  constexpr int B = VPL >= 8 ? 1 : 8 / VPL;
+  uint32_t pe[2];
+  int se[2];
+  float we[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t idx = i + j < r1 ? i + j : r1 - 1;
-      pp[j] = sorted_p[idx];
-      sg[j] = seg_of[idx];
-    }
+  for (int h = 0; h < 2; ++h) {
+    const int64_t e = r0 + h * kWave + lane;
+    const int64_t ec = e < r1 ? e : r1 - 1;
+    pe[h] = sorted_p[ec];
+    se[h] = seg_of[ec];
+    we[h] = weights != nullptr ? weights[pe[h]] : 1.f;
+  }
+  const int len = (int)(r1 - r0);
+  auto fetch = [&](int i, RowVec<W> (&row)[B][VPL], int* sg, float* ww) __attribute__((always_inline)) {
+    const int h = i >= kWave;  // wave-uniform: a batch never straddles the halves (B divides 64)
 #pragma unroll
-    for (int j = 0; j < 8; ++j) ww[j] = weights != nullptr ? weights[pp[j]] : 1.f;
-    RowVec<W> row[8][VPL];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int64_t t = pp[j] / (uint32_t)fpt;
+    for (int j = 0; j < B; ++j) {
+      const int src = (i + j) & (kWave - 1);
+      const uint32_t pp = (uint32_t)__shfl((int)(h ? pe[1] : pe[0]), src);
+      sg[j] = __shfl(h ? se[1] : se[0], src);
+      ww[j] = __shfl(h ? we[1] : we[0], src);
+      const int64_t t = pp / (uint32_t)fpt;
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         const int c = lane + kWave * v;
         row[j][v].load(g, t * nv + c, c < nv);
       }
     }
+  };
+  auto consume = [&](int i, const RowVec<W> (&row)[B][VPL], const int* sg, const float* ww)
+                     __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (i + j < r1) {
+    for (int j = 0; j < B; ++j) {
+      if (i + j < len) {
         if (sg[j] != cur) {
           emit(cur);
 #pragma unroll
@@ -380,58 +397,101 @@ __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
         for (int v = 0; v < VPL; ++v) acc[v].fma_add(ww[j], row[j][v]);
       }
     }
+  };
+  RowVec<W> ra[B][VPL], rb[B][VPL];
+  int sa[B], sb[B];
+  float wa[B], wb[B];
+  fetch(0, ra, sa, wa);
+  for (int i = 0; i < len; i += 2 * B) {
+    if (i + B < len) fetch(i + B, rb, sb, wb);
+    consume(i, ra, sa, wa);
+    if (i + B >= len) break;
+    if (i + 2 * B < len) fetch(i + 2 * B, ra, sa, wa);
+    consume(i + B, rb, sb, wb);
   }
   emit(cur);
 }
 
-// Adds the partial sums of segments that cross range boundaries (in range
-// order) and pads rows [U, cap) with slot pool_size and zeros.
+// Rows [U, cap): slot pool_size, zero row, zero norm (jnp.unique's
+// fill_value and segment_sum's empty segments, train.py:166-172), by the
+// workgroups [fix_blocks, gridDim) of the fix-up launch.
+__device__ __forceinline__ void pad_rows(const uint32_t* __restrict__ num_seg, int64_t cap, int d, int64_t pool_size,
+                                         int32_t* __restrict__ uniq, float* __restrict__ rows,
+                                         float* __restrict__ row_sq, int64_t t0, int64_t stride) {
+  const int64_t U = *num_seg;
+  for (int64_t u = U + t0; u < cap; u += stride) {
+    uniq[u] = (int32_t)pool_size;
+    row_sq[u] = 0.f;
+  }
+  if ((d & 3) == 0) {
+    float4* r4 = (float4*)(rows + U * d);
+    const int64_t n4 = (cap - U) * (d / 4);
+    for (int64_t i = t0; i < n4; i += stride) r4[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  } else {
+    float* r = rows + U * d;
+    const int64_t n1 = (cap - U) * d;
+    for (int64_t i = t0; i < n1; i += stride) r[i] = 0.f;
+  }
+}
+
+// Segments that cross range boundaries: one wave per range, which finishes
+// the segment that starts in it and continues past its end (the last segment
+// of the range), adding that segment's partial rows in range order.  Rows of
+// segments inside one range were written by seg_reduce_kernel.  The same
+// launch pads rows [U, cap) with its last workgroups, so the bandwidth-bound
+// padding runs beside the latency-bound chains of hot segments.
 template <int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* __restrict__ seg_start,
+                                                                 const int32_t* __restrict__ seg_of, int64_t n,
+                                                                 int nv, const float* __restrict__ partial,
+                                                                 float* __restrict__ rows,
+                                                                 float* __restrict__ row_sq, int64_t fix_blocks,
                                                                  const uint32_t* __restrict__ num_seg, int64_t cap,
-                                                                 int nv, int64_t pool_size,
-                                                                 const float* __restrict__ partial,
-                                                                 int32_t* __restrict__ uniq, float* __restrict__ rows,
-                                                                 float* __restrict__ row_sq) {
-  const int64_t u = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+                                                                 int64_t pool_size, int32_t* __restrict__ uniq) {
+  if ((int64_t)blockIdx.x >= fix_blocks) {
+    pad_rows(num_seg, cap, nv * W, pool_size, uniq, rows, row_sq,
+             ((int64_t)blockIdx.x - fix_blocks) * kRowThreads + threadIdx.x,
+             ((int64_t)gridDim.x - fix_blocks) * kRowThreads);
+    return;
+  }
+  const int64_t r = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
-  if (u >= cap) return;
-  const int64_t U = *num_seg;
+  const int64_t r0 = r * kRangeLen;
+  if (r0 >= n) return;
+  const int64_t r1 = r0 + kRangeLen < n ? r0 + kRangeLen : n;
+  const int u = seg_of[r1 - 1];
+  const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
+  const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
+  if (ra == rb || ra != r) return;  // inside one range, or another wave's segment
+  const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
   RowVec<W> acc[VPL];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) acc[v].zero();
-  if (u < U) {
-    const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
-    const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
-    if (ra == rb) return;  // finished by seg_reduce_kernel
-    const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
-    // hot rows span hundreds of ranges: eight partial rows in flight, added
-    // in range order
-    for (int64_t r0 = ra; r0 <= rb; r0 += 8) {
-      RowVec<W> p[8][VPL];
+  // hot rows span hundreds of ranges: PB partial rows in flight (32 row
+  // vectors per lane)
+  constexpr int PB = VPL >= 8 ? 4 : 32 / VPL;
+  for (int64_t q0 = ra; q0 <= rb; q0 += PB) {
+    RowVec<W> p[PB][VPL];
 #pragma unroll
-      for (int b = 0; b < 8; ++b) {
-        const int64_t r = r0 + b <= rb ? r0 + b : rb;
-        const int slot = r == ra ? slot_a : 0;
+    for (int b = 0; b < PB; ++b) {
+      const int64_t q = q0 + b <= rb ? q0 + b : rb;
+      const int slot = q == ra ? slot_a : 0;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) {
-          const int c = lane + kWave * v;
-          p[b][v].load(partial, (r * 2 + slot) * nv + c, c < nv);
-        }
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        p[b][v].load(partial, (q * 2 + slot) * nv + c, c < nv);
       }
-#pragma unroll
-      for (int b = 0; b < 8; ++b)
-        if (r0 + b <= rb)
-#pragma unroll
-          for (int v = 0; v < VPL; ++v) acc[v].add(p[b][v]);
     }
-  } else if (lane == 0) {
-    uniq[u] = (int32_t)pool_size;
+#pragma unroll
+    for (int b = 0; b < PB; ++b)
+      if (q0 + b <= rb)
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) acc[v].add(p[b][v]);
   }
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = lane + kWave * v;
-    if (c < nv) acc[v].store(rows, u * nv + c);
+    if (c < nv) acc[v].store(rows, (int64_t)u * nv + c);
   }
   const float sq = wave_sq<W, VPL>(acc);
   if (lane == 0) row_sq[u] = sq;
@@ -725,9 +785,8 @@ static void launch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32
   const unsigned b1 = (unsigned)cdiv(L.nranges, kRowThreads / kWave);
   seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq,
                                                        partial);
-  const unsigned b2 = (unsigned)cdiv(L.cap, kRowThreads / kWave);
-  seg_fixup_kernel<W, VPL><<<b2, kRowThreads, 0, s>>>(seg_start, nseg, L.cap, nv, pool_size, partial, uniq, rows,
-                                                      row_sq);
+  seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, rows, row_sq, b1,
+                                                             nseg, L.cap, pool_size, uniq);
 }
 
 template <int W>
