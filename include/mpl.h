@@ -122,12 +122,15 @@ int mpl_gather_wsum(const void* values, int values_dtype, int64_t N, int d,
  * Passing the materialised contributions as g with fetches_per_token = 1 and
  * weights = NULL is _merge_rows itself.  Deterministic: a stable radix sort
  * by slot and fixed-order segment sums, no float atomics.  Needs d <= 1024,
- * P and pool_size < 2^31, slots in [0, pool_size).
+ * P and pool_size < 2^31, slots in [0, pool_size).  zero_padding = 0 leaves
+ * rows [num_unique, cap) unwritten (uniq and row_sq are still padded), for
+ * callers that skip padding slots, such as mpl_row_adagrad / mpl_row_adam.
  */
 size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_size);
 int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
                    const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
-                   int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, void* stream);
+                   int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, int zero_padding,
+                   void* stream);
 
 /*
  * train.py:395-397: gnorm = sqrt(rest_sq + sum(row_sq)) and

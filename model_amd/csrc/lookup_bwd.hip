@@ -17,11 +17,6 @@
 
 #include "common.h"
 
-// rows.hip
-extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
-                              const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
-                              int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, void* stream);
-extern "C" size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_size);
 
 namespace mpl {
 
@@ -448,7 +443,7 @@ extern "C" int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, co
   int rc = check_launch("mpl_lookup_bwd_keys(prep)");
   if (rc) return rc;
   rc = mpl_merge_rows(kid, kw, L.P, k, q_hat, half, nrows, ws + L.merge, L.merge_bytes, uniq, mrows, row_sq, nuniq,
-                      stream);
+                      0, stream);  // keys_bwd_kernel reads only the rows of keys it finds
   if (rc) return rc;
   keys_bwd_kernel<<<kb, kBwdThreads, 0, s>>>(sub_keys, uniq, nuniq, mrows, dk_hat_extra, nrows, half, 1e-6f,
                                              d_sub_keys);

@@ -423,6 +423,7 @@ __device__ __forceinline__ void pad_rows(const uint32_t* __restrict__ num_seg, i
     uniq[u] = (int32_t)pool_size;
     row_sq[u] = 0.f;
   }
+  if (rows == nullptr) return;  // padding rows left unwritten
   if ((d & 3) == 0) {
     float4* r4 = (float4*)(rows + U * d);
     const int64_t n4 = (cap - U) * (d / 4);
@@ -447,9 +448,10 @@ __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* _
                                                                  float* __restrict__ rows,
                                                                  float* __restrict__ row_sq, int64_t fix_blocks,
                                                                  const uint32_t* __restrict__ num_seg, int64_t cap,
-                                                                 int64_t pool_size, int32_t* __restrict__ uniq) {
+                                                                 int64_t pool_size, int32_t* __restrict__ uniq,
+                                                                 int zero_padding) {
   if ((int64_t)blockIdx.x >= fix_blocks) {
-    pad_rows(num_seg, cap, nv * W, pool_size, uniq, rows, row_sq,
+    pad_rows(num_seg, cap, nv * W, pool_size, uniq, zero_padding ? rows : nullptr, row_sq,
              ((int64_t)blockIdx.x - fix_blocks) * kRowThreads + threadIdx.x,
              ((int64_t)gridDim.x - fix_blocks) * kRowThreads);
     return;
@@ -781,23 +783,23 @@ template <int W, int VPL>
 static void launch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32_t* seg_start, const float* weights,
                           const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
                           const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
-                          hipStream_t s) {
+                          int zero_padding, hipStream_t s) {
   const unsigned b1 = (unsigned)cdiv(L.nranges, kRowThreads / kWave);
   seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq,
                                                        partial);
   seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, rows, row_sq, b1,
-                                                             nseg, L.cap, pool_size, uniq);
+                                                             nseg, L.cap, pool_size, uniq, zero_padding);
 }
 
 template <int W>
 static void dispatch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32_t* seg_start, const float* weights,
                             const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
                             const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
-                            hipStream_t s) {
+                            int zero_padding, hipStream_t s) {
   const int vpl = (int)cdiv(nv, kWave);
 #define MPL_REDUCE(V)                                                                                              \
   launch_reduce<W, V>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq, partial, L, nseg, pool_size, \
-                      uniq, s)
+                      uniq, zero_padding, s)
   if (vpl <= 1) MPL_REDUCE(1);
   else if (vpl <= 2) MPL_REDUCE(2);
   else if (vpl <= 4) MPL_REDUCE(4);
@@ -817,7 +819,8 @@ extern "C" size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_
 
 extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
                               const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
-                              int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, void* stream) {
+                              int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, int zero_padding,
+                              void* stream) {
   clear_error();
   MPL_REQUIRE(P >= 0 && fetches_per_token > 0 && d > 0 && pool_size > 0, MPL_EINVAL,
               "mpl_merge_rows: bad sizes P=%lld fetches_per_token=%d d=%d pool_size=%lld", (long long)P,
@@ -868,10 +871,10 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique);
   if (d % 4 == 0)
     dispatch_reduce<4>(vin, seg_of, seg_start, weights, g, fetches_per_token, d / 4, P, rows, row_sq, partial, L,
-                       nseg, pool_size, uniq, s);
+                       nseg, pool_size, uniq, zero_padding, s);
   else
     dispatch_reduce<1>(vin, seg_of, seg_start, weights, g, fetches_per_token, d, P, rows, row_sq, partial, L, nseg,
-                       pool_size, uniq, s);
+                       pool_size, uniq, zero_padding, s);
   return check_launch("mpl_merge_rows(reduce)");
 }
 

@@ -50,9 +50,11 @@ class MergedRows:
 
 
 def merge_fetches(slots: torch.Tensor, weights: Optional[torch.Tensor], g: torch.Tensor,
-                  pool_size: int) -> MergedRows:
+                  pool_size: int, zero_padding: bool = True) -> MergedRows:
     """Sum weights[p] * g[p // fpt] per distinct slot, fpt = P / g.shape[0]
-    (the fetches of one token are consecutive)."""
+    (the fetches of one token are consecutive).  zero_padding=False leaves
+    the padding rows [num_unique, cap) unwritten (the row optimizers skip
+    them)."""
     dev = g.device
     slots = slots.reshape(-1).to(torch.int32).contiguous()
     P = slots.shape[0]
@@ -78,7 +80,8 @@ def merge_fetches(slots: torch.Tensor, weights: Optional[torch.Tensor], g: torch
     wsb = L.mpl_merge_rows_workspace_bytes(P, d, pool_size)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
     check(L.mpl_merge_rows(ptr(slots), ptr(weights), P, fpt, ptr(g), d, pool_size, ptr(ws), wsb, ptr(uniq),
-                           ptr(rows), ptr(row_sq), ptr(num_unique), _lib.stream_ptr(dev)), "mpl_merge_rows")
+                           ptr(rows), ptr(row_sq), ptr(num_unique), int(bool(zero_padding)), _lib.stream_ptr(dev)),
+          "mpl_merge_rows")
     return MergedRows(uniq, rows, row_sq, num_unique)
 
 
@@ -89,7 +92,8 @@ def merge_rows(slots: torch.Tensor, contribs: torch.Tensor, pool_size: int):
     return m.uniq, m.rows
 
 
-def fetched_row_grads_full(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int) -> MergedRows:
+def fetched_row_grads_full(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int,
+                           zero_padding: bool = True) -> MergedRows:
     """train.py:146-163 with the extra outputs (row norms, distinct count)."""
     slots, weights, grads = [], [], []
     for layer, sl, w in zip(layers, aux["slots"], aux["weights"]):
@@ -99,7 +103,7 @@ def fetched_row_grads_full(aux: Dict, probe_grads, layers: Sequence[int], pool_s
         slots.append(sl.reshape(-1, hk).reshape(-1))
         weights.append(w.detach().reshape(-1))
         grads.append(g.reshape(-1, d))
-    return merge_fetches(torch.cat(slots), torch.cat(weights), torch.cat(grads), pool_size)
+    return merge_fetches(torch.cat(slots), torch.cat(weights), torch.cat(grads), pool_size, zero_padding)
 
 
 def fetched_row_grads(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int):
@@ -193,7 +197,7 @@ class SparseRowUpdate:
     def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
                  rest_sq: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
         N = self.values.shape[0]
-        merged = fetched_row_grads_full(aux, probe_grads, layers, N)
+        merged = fetched_row_grads_full(aux, probe_grads, layers, N, zero_padding=False)  # optimizers skip padding
         sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip)
         lr = warmup_cosine(self.step, self.lr, self.warmup_steps, self.steps) * self.pool_lr_mult
         scale = sg[0:1]

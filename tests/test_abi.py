@@ -59,11 +59,11 @@ def test_row_entry_points_validate_before_launch():
     # keys/values ping-pong (4 x P x 4 B) + segment ids (P x 4 B) + partial rows
     assert ws >= 5 * P * 4 + (P // 128) * 2 * d * 4
     assert L.mpl_merge_rows_workspace_bytes(0, d, N) == 0
-    rc = L.mpl_merge_rows(None, None, 64, 16, None, 2000, N, None, 0, None, None, None, None, None)
+    rc = L.mpl_merge_rows(None, None, 64, 16, None, 2000, N, None, 0, None, None, None, None, 1, None)
     assert rc == 4 and b"<= 1024" in L.mpl_last_error()
-    rc = L.mpl_merge_rows(None, None, -1, 16, None, 8, N, None, 0, None, None, None, None, None)
+    rc = L.mpl_merge_rows(None, None, -1, 16, None, 8, N, None, 0, None, None, None, None, 1, None)
     assert rc == 1
-    rc = L.mpl_merge_rows(None, None, 64, 16, None, 8, N, None, 0, None, None, None, None, None)
+    rc = L.mpl_merge_rows(None, None, 64, 16, None, 8, N, None, 0, None, None, None, None, 1, None)
     assert rc == 1 and b"null buffer" in L.mpl_last_error()
     rc = L.mpl_row_adagrad(None, 5, None, None, None, None, 10, 8, N, 0.1, None, None)
     assert rc == 1 and b"values_dtype" in L.mpl_last_error()

@@ -240,3 +240,25 @@ def test_sparse_row_update_step_matches_oracle(gpu_lib):
     np.testing.assert_allclose(upd.acc.cpu().numpy(), acc, rtol=1e-5, atol=1e-12)
     np.testing.assert_allclose(upd.master.cpu().numpy(), master, rtol=1e-5, atol=1e-7)
     np.testing.assert_allclose(tv.float().cpu().numpy(), ov.astype(np.float32), rtol=1e-3, atol=2e-5)
+
+
+@pytest.mark.parametrize("zipf", [True, False])
+def test_merge_without_zero_padding(gpu_lib, zipf):
+    """zero_padding=False (the optimizers' merge) writes the same ids, rows
+    and norms for the distinct slots and still pads uniq / row_sq; only the
+    padding rows' content is left unwritten."""
+    M, H, k, N, d = 2048, 4, 16, 1 << 16, 64
+    if zipf:
+        slots = torch.tensor(zipf_slots(M, H, k, N, seed=9), device="cuda", dtype=torch.int32)
+    else:
+        slots = torch.randint(0, N, (M * H * k,), device="cuda", dtype=torch.int32)
+    g = torch.randn((M, d), device="cuda")
+    w = torch.rand(M * H * k, device="cuda")
+    a = R.merge_fetches(slots.reshape(-1), w, g, N)
+    b = R.merge_fetches(slots.reshape(-1), w, g, N, zero_padding=False)
+    U = int(a.num_unique[0])
+    assert int(b.num_unique[0]) == U < a.uniq.shape[0]
+    assert torch.equal(a.uniq, b.uniq)
+    assert torch.equal(a.rows[:U], b.rows[:U])
+    assert torch.equal(a.row_sq, b.row_sq)
+    assert bool((a.rows[U:] == 0).all())
