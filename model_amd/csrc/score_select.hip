@@ -61,7 +61,10 @@ constexpr int kCand = MPL_CAND;  // per-lane candidate buffer (entries)
 constexpr int kScoreThreads = MPL_SCORE_THREADS;  // waves per workgroup x 64
 constexpr int kQueriesPerWave = 32;
 constexpr int kQueriesPerGroup = kQueriesPerWave * (kScoreThreads / 64);
-constexpr int kMaxSplits = 64;
+#ifndef MPL_MAX_SPLITS
+#define MPL_MAX_SPLITS 64
+#endif
+constexpr int kMaxSplits = MPL_MAX_SPLITS;
 
 struct ScoreParams {
   const void* q_hat;    // [M, HC, half]: normalised in the scoring type (mode 0) or raw fp32
@@ -761,15 +764,19 @@ static Plan make_plan(int64_t M, int H, int n, int k) {
   return pl;
 }
 
-// Workspace: the select scores with noise; per-split lists when split.
-static int reduced_splits(const Plan& pl, int k) {
-  return (k == 16 && pl.splits > kMergeChunk) ? (int)cdiv(pl.splits, kMergeChunk) : 0;
+// Workspace: the select scores with noise; per-split lists when split, and
+// for k == 16 the lists of each reduction level (8 lists into one) until at
+// most 8 remain for stage 2.
+static int reduced_total(const Plan& pl, int k) {
+  int tot = 0;
+  for (int S = pl.splits; k == 16 && S > kMergeChunk; S = (int)cdiv(S, kMergeChunk)) tot += (int)cdiv(S, kMergeChunk);
+  return tot;
 }
 
 static size_t ws_bytes(const Plan& pl, int64_t M, int H, int k, bool noise) {
   const size_t per = (size_t)M * 2 * H * k;
   if (pl.splits == 1) return noise ? per * 4 : 0;
-  return per * (pl.splits + reduced_splits(pl, k)) * (noise ? 3 : 2) * 4;
+  return per * (pl.splits + reduced_total(pl, k)) * (noise ? 3 : 2) * 4;
 }
 
 template <typename T, int HP, bool NOISE, int KMAX>
@@ -907,18 +914,19 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
   pp.flat_idx = flat_idx;
   pp.slots = slots;
   pp.weights = weights;
-  const int S2 = reduced_splits(pl, k);
-  if (S2 > 0) {
-    // many splits (decode-sized batches): reduce the lists in parallel first,
-    // so stage 2 merges S2 <= 8 lists instead of a long sequential chain
-    float* r = w + (noise ? 3 : 2) * part;
+  // many splits (decode-sized batches): reduce the lists in parallel, eight
+  // into one per level, so stage 2 merges at most 8 lists instead of a long
+  // sequential chain
+  float* r = w + (noise ? 3 : 2) * part;
+  while (k == 16 && pp.S > kMergeChunk) {
+    const int S2 = (int)cdiv(pp.S, kMergeChunk);
     const size_t part2 = per * S2;
     MergeParams mp;
-    mp.sel = sp.out_sel;
-    mp.clean = sp.out_clean;
-    mp.idx = sp.out_idx;
+    mp.sel = pp.sel;
+    mp.clean = pp.clean;
+    mp.idx = pp.idx;
     mp.rows = M * HC;
-    mp.S = pl.splits;
+    mp.S = pp.S;
     mp.S2 = S2;
     mp.out_clean = r;
     mp.out_idx = (int*)(r + part2);
@@ -930,6 +938,7 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
     pp.clean = mp.out_clean;
     pp.idx = mp.out_idx;
     pp.S = S2;
+    r += (noise ? 3 : 2) * part2;
   }
   const int G = k <= 16 ? 16 : 32;
   const unsigned g2 = (unsigned)cdiv(M * H * G, 256);
