@@ -5,15 +5,19 @@
 // Stage 1 (score_topk_kernel).  A workgroup of two waves handles one
 // codebook hc = h*2 + c and one split of its n sub-keys; each wave owns 32
 // queries.  The queries are normalised in registers (or read normalised) and
-// held as the MFMA B operand; key blocks of 32 stream through two LDS buffers
-// by LDS DMA, and each block is one chain of 32x32 MFMAs (keys = A operand).
+// held as the MFMA B operand; each block of 32 keys is one chain of 32x32
+// MFMAs (keys = A operand).  Key blocks reach the waves one of two ways,
+// chosen per instantiation by register budget: each wave loads its own A
+// operand two blocks ahead into registers (no LDS, no barriers; the faster
+// path wherever the extra 32-64 VGPRs keep the occupancy), or the workgroup
+// streams them through two LDS buffers by LDS DMA and shares them.
 // Lanes l and l+32 share query l%32 and see alternate groups of 4 keys.  Two
 // passes:
 //   1. a bound pass over the first blocks of the split keeps, per register
-//      position, the running maximum; the k-th largest of a query's 32
-//      maxima (the lane pair exchanges them with v_permlane32_swap) is a
-//      score that at least k distinct keys reach, so it bounds the k-th best
-//      from below;
+//      position, the running maximum of the positive scores (-inf if none);
+//      the k-th largest of a query's 32 maxima (the lane pair exchanges them
+//      with v_permlane32_swap) is a score that at least k distinct keys
+//      reach, so it bounds the k-th best from below;
 //   2. a select pass over the whole split appends scores at or above the
 //      lane's threshold to its column of an LDS buffer and, when any column
 //      may overflow, sorts the buffered candidates in chunks of 8 and
@@ -83,26 +87,35 @@ struct ScoreParams {
 };
 
 // Per-lane selection state of the stage-1 kernel.  Candidates are appended
-// to the lane's column of an LDS buffer as (score bits, index) pairs; `cnt`
-// is the number of buffered entries.  The buffer is addressed by index from
-// its __shared__ array (not through a loop-carried pointer), so the compiler
-// can tell these accesses from the LDS-DMA writes of the key tiles and does
-// not wait for the in-flight DMA before each append.
+// to the lane's column of three LDS arrays of [waves][kCand][64] words
+// (score, key index, clean score with noise); `off` is the byte offset of the
+// lane's next free entry, the same in all three.  Entries of a column are
+// 4*64 bytes apart.  The stores address the __shared__ arrays directly (array
+// + byte offset, not a loop-carried pointer), so the compiler can tell them
+// from the LDS-DMA writes of the key tiles (it does not wait for the
+// in-flight DMA before an append) and folds each array's LDS address into
+// the instruction's offset field: an append is one add and two or three
+// ds_write_b32 from one address register.
 template <int KMAX, bool NOISE>
 struct LaneSel {
   TopList<KMAX, NOISE> top;
   float thr;
-  int cnt;
+  uint32_t off;
 };
+constexpr uint32_t kEntryBytes = 4 * kWave;
 
-// Merges the lane's buffered candidates (column `lane` of buf/pay) into its
-// list, empties the buffer and refreshes the threshold.  Wave-uniform
-// control flow.
+template <typename W>
+__device__ __forceinline__ W& lds_at(W* arr, uint32_t byte_off) {
+  return *(W*)((char*)arr + byte_off);
+}
+
+// Merges the lane's buffered candidates (entries lane0, lane0 + kEntryBytes,
+// ... below st.off) into its list, empties the buffer and refreshes the
+// threshold.  Wave-uniform control flow.
 template <int KMAX, bool NOISE>
-__device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, uint2 (*buf)[kWave],
-                                           const float (*pay)[kWave], int lane, bool valid, int k,
-                                           float base_thr) {
-  const int cnt = st.cnt;
+__device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
+                                           const float* pay, uint32_t lane0, bool valid, int k, float base_thr) {
+  const int cnt = (int)((st.off - lane0) / kEntryBytes);
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
 #pragma unroll 1
@@ -113,14 +126,14 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, uint2 (*buf
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const bool in = c0 + i < cnt;
-      const uint2 e = buf[c0 + i][lane];
-      ch[i] = in ? make_key(__uint_as_float(e.x), (int)e.y) : 0ull;
-      cp[i] = (NOISE && in) ? pay[NOISE ? c0 + i : 0][lane] : 0.f;
+      const uint32_t o = lane0 + (uint32_t)(c0 + i) * kEntryBytes;
+      ch[i] = in ? make_key(lds_at(cs, o), (int)lds_at(ci, o)) : 0ull;
+      cp[i] = (NOISE && in) ? lds_at(pay, o) : 0.f;
     }
     sort8<NOISE>(ch, cp);
     st.top.template merge<8>(ch, cp);
   }
-  st.cnt = 0;
+  st.off = lane0;
   if (valid) {
     const u64 kk = st.top.at(k - 1);
     st.thr = kk ? key_score(kk) : base_thr;
@@ -158,7 +171,7 @@ __device__ __forceinline__ float kth_of_32(const float* a, const float* b, int k
   return from_orderable(t);
 }
 
-template <typename T, int HP, bool NOISE, int KMAX>
+template <typename T, int HP, bool NOISE, int KMAX, bool DIRECT>
 __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {
   constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);  // 16-B vectors per lane per block
   constexpr int OPV = KeyPack<T>::kOpsPerVec;
@@ -168,8 +181,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   typedef typename Mfma<T>::Op Op;
 
   __shared__ uint4 tile0[TILE], tile1[TILE];
-  __shared__ uint2 cbuf[WAVES][kCand][kWave];
-  __shared__ float cpay[NOISE ? WAVES : 1][NOISE ? kCand : 1][kWave];
+  __shared__ float cscore[WAVES * kCand * kWave];
+  __shared__ uint32_t cindex[WAVES * kCand * kWave];
+  __shared__ float cpay[NOISE ? WAVES * kCand * kWave : 1];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -214,8 +228,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     }
   }
   const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
-  uint2(*mybuf)[kWave] = cbuf[wave];
-  const float(*mypay)[kWave] = cpay[NOISE ? wave : 0];
+  const uint32_t lane0 = 4u * (uint32_t)(wave * kCand * kWave + lane);  // the lane's first buffer entry
+  const uint32_t flush_at = lane0 + (uint32_t)(kCand - 8) * kEntryBytes;
 
   // Key blocks stream into two LDS buffers by LDS DMA (global_load_lds: no
   // registers, no LDS store instructions).  Wave w copies the tile's 16-byte
@@ -246,6 +260,47 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     }
     return g;
   };
+  // Register path (DIRECT): each wave loads its own A operand of block blk
+  // into registers, VPL coalesced 1-KB loads, while the MFMAs of the block
+  // before it run; no LDS tiles and no barriers.  Iteration j issues the
+  // loads of block j+2 into the registers of block j (whose MFMAs were issued
+  // in iteration j-1), then waits for block j+1, issued one iteration
+  // earlier (loads complete in order).
+  auto gload = [&](uint4* dst, int blk) __attribute__((always_inline)) {
+    const uint4* src = kbase_ptr + (int64_t)blk * TILE + lane;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) dst[v] = src[v * kWave];
+  };
+  auto sweep_direct = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
+    const int nb = be - bb;
+    if (nb <= 0) return;
+    uint4 ua[VPL], ub[VPL];
+    gload(ua, bb);
+    gload(ub, min(bb + 1, be - 1));
+    GVec gcur = fetch_noise(bb);
+    wait_vmcnt_le<VPL + (NOISE ? 16 : 0)>();
+    f32x16 x = f32x16{}, y;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+#pragma unroll
+      for (int e = 0; e < OPV; ++e) x = Mfma<T>::mma(Mfma<T>::from_vec(ua[v], e), qop[v * OPV + e], x);
+    }
+    auto step = [&](int j, f32x16& c, f32x16& d, const uint4* ucur, uint4* unext) __attribute__((always_inline)) {
+      gload(unext, min(bb + j + 2, be - 1));
+      wait_vmcnt_le<VPL + (NOISE ? 16 : 0)>();
+      d = f32x16{};
+      auto issue = [&](int i) __attribute__((always_inline)) {
+        d = Mfma<T>::mma(Mfma<T>::from_vec(ucur[i / OPV], i % OPV), qop[i], d);
+      };
+      const GVec gnext = fetch_noise(min(bb + j + 1, be - 1));
+      body((bb + j) * 32, c, gcur, j < nb, issue);
+      gcur = gnext;
+    };
+    for (int j = 0; j < nb; j += 2) {
+      step(j, x, y, ub, ua);
+      step(j + 1, y, x, ua, ub);
+    }
+  };
   // One sweep over key blocks [bb, be), software-pipelined: while the VALU
   // runs body() on block j, the MFMAs of block j+1 are already in flight.
   // Block j lives in buffer j % 2.  Iteration j: wait for this wave's DMA of
@@ -256,7 +311,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   // buffer, then read block j+1 and run body() on block j with the next
   // block's MFMAs interleaved.  Past the end, DMAs copy clamped duplicates
   // and the one extra MFMA group scores one; nobody reads either.
-  auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
+  auto sweep_lds = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
     const int nb = be - bb;
     if (nb <= 0) return;
     dma(tile0, bb);
@@ -298,6 +353,11 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     }
   };
 
+  auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
+    if constexpr (DIRECT) sweep_direct(bb, be, body);
+    else sweep_lds(bb, be, body);
+  };
+
   // Selection values of the lane's 16 keys of a block (padded keys -inf);
   // with noise, cl holds the clean scores.
   auto lane_scores = [&](int kb, const f32x16& c, const GVec& g, float* sv, float* cl)
@@ -321,12 +381,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   };
 
   // Pass 1 over the first pass1_blocks blocks of the split: running maximum
-  // per register position.  Each maximum is a distinct key's score, so the
-  // k-th largest of the 32 maxima of a lane pair (one query) is a lower bound
-  // on that query's k-th best score.
-  float ma[16];
+  // per register position, taken as a signed-integer max of the float bit
+  // patterns starting from -inf (one v_max_i32, no compare-select).  In that
+  // order every positive score exceeds -inf and every negative one falls
+  // below it, so each position ends with its largest positive score, or -inf
+  // if it saw none.  Either way the 32 values of a lane pair (one query) are
+  // scores of distinct keys or -inf, so their k-th largest is a lower bound
+  // on that query's k-th best score; negative scores only loosen it.
+  int ma[16];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) ma[r] = -INFINITY;
+  for (int r = 0; r < 16; ++r) ma[r] = (int)0xff800000u;  // -inf
   const int p1_end = min(b_end, b_begin + p.pass1_blocks);
   // element r of 16 issues the next block's MFMA chunks [r*NCH/16, (r+1)*NCH/16)
   auto issue_for = [&](int r, auto&& issue) __attribute__((always_inline)) {
@@ -342,20 +406,22 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     for (int r = 0; r < 16; ++r) {
       issue_for(r, issue);
       const float v = raw ? c[r] : sv[r];
-      // compare-select, not fmaxf: IEEE maxNum makes the compiler quiet
-      // both inputs first (three v_max per element); scores are never NaN
-      ma[r] = (active && v > ma[r]) ? v : ma[r];
+      // Past the end (!active) c holds the split's last block again, whose
+      // scores are already in the maxima, so no test of `active` is needed.
+      ma[r] = max(ma[r], __float_as_int(v));
     }
+    (void)active;
   });
-  float mb[16];  // the partner lane's maxima
+  float fa[16], mb[16];  // own and the partner lane's maxima
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float a = ma[r], b = ma[r];
+    fa[r] = __int_as_float(ma[r]);
+    float a = fa[r], b = fa[r];
     half_swap(a, b);  // lane < 32: (own, partner); lane >= 32: (partner, own)
     mb[r] = par ? a : b;
   }
   // Scores >= bound pass: strict '>' against the next float below it.
-  const float bound = kth_of_32(ma, mb, p.k);
+  const float bound = kth_of_32(fa, mb, p.k);
   const float base_thr = bound == -INFINITY ? -INFINITY : from_orderable(orderable(bound) - 1u);
 
   // Pass 2 over the whole split: only candidates above the threshold are
@@ -363,29 +429,30 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   LaneSel<KMAX, NOISE> st;
   st.top.init();
   st.thr = valid ? base_thr : INFINITY;
-  st.cnt = 0;
+  st.off = lane0;
   sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
                             __attribute__((always_inline)) {
     float sv[16], cl[NOISE ? 16 : 1];
     lane_scores(kb, c, g, sv, cl);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      if (active && __ballot(st.cnt > kCand - 8) != 0)
-        flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
+      if (active && __ballot(st.off > flush_at) != 0)
+        flush_lane<KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int r = 8 * q + e;
         issue_for(r, issue);
         const float x = sv[r];
         if (active && x > st.thr) {
-          cbuf[wave][st.cnt][lane] = make_uint2(__float_as_uint(x), (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3)));
-          if (NOISE) cpay[NOISE ? wave : 0][NOISE ? st.cnt : 0][lane] = cl[NOISE ? r : 0];
-          ++st.cnt;
+          lds_at(cscore, st.off) = x;
+          lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
+          if (NOISE) lds_at(cpay, st.off) = cl[NOISE ? r : 0];
+          st.off += kEntryBytes;
         }
       }
     }
   });
-  flush_lane<KMAX, NOISE>(st, mybuf, mypay, lane, valid, p.k, base_thr);
+  flush_lane<KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr);
 
   // Merge the two lanes' lists of the query: the partner's sorted list
   // arrives through v_permlane32_swap and is bitonic-merged (keys of the two
@@ -779,9 +846,20 @@ static size_t ws_bytes(const Plan& pl, int64_t M, int H, int k, bool noise) {
   return per * (pl.splits + reduced_total(pl, k)) * (noise ? 3 : 2) * 4;
 }
 
+// Register-loaded keys cost up to 32 more VGPRs than LDS tiles; they are used
+// where the kernel stays at the same occupancy without AGPRs (measured with
+// -Rpass-analysis=kernel-resource-usage on gfx950).
+template <typename T, int HP, bool NOISE, int KMAX>
+constexpr bool direct_keys() {
+  constexpr int vpl = KeyPack<T>::vectors_per_lane(HP);
+  const bool occ1 = KMAX == 32 || (NOISE && vpl >= 8) || (!NOISE && vpl > 8);
+  const bool occ3 = !NOISE && vpl == 2;
+  return !occ1 && !occ3;
+}
 template <typename T, int HP, bool NOISE, int KMAX>
 static void launch_stage1(const ScoreParams& sp, int64_t blocks, hipStream_t s) {
-  score_topk_kernel<T, HP, NOISE, KMAX><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+  score_topk_kernel<T, HP, NOISE, KMAX, direct_keys<T, HP, NOISE, KMAX>()>
+      <<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
 }
 
 template <typename T, int HP>
