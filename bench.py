@@ -280,9 +280,10 @@ def sparse_update_bench(torch, iters):
 
 def train_step_bench(torch, iters):
     """Forward + backward of the text-study layer in training (8,192 tokens,
-    262,144 fp16 slots, H=4, d_key=256, k=16, balance coefficient 0.01,
-    sparse value gradient through a probe) followed by the sparse row update
-    (merge, clip, row-wise Adagrad on the fp32 master)."""
+    262,144 fp16 slots, H=4, d_key=256, k=16, routing noise on as in the
+    reference's training step (train=True, routing_noise 1.0), balance
+    coefficient 0.01, sparse value gradient through a probe) followed by the
+    sparse row update (merge, clip, row-wise Adagrad on the fp32 master)."""
     from model_amd import rows as R
     from model_amd.memory import MemoryPool, key_diversity_loss
 
@@ -303,7 +304,7 @@ def train_step_bench(torch, iters):
     def step():
         q = (hidden @ w_q).reshape(M, H, d_key)
         probe = torch.zeros((M, d), device=dev, requires_grad=True)
-        out, aux = pool.apply({"params": params}, q, train=False, sparse_grad=True)
+        out, aux = pool.apply({"params": params}, q, train=True, sparse_grad=True)
         loss = ((out + probe) * g_out).sum() + 0.01 * aux["balance_loss"] + 0.01 * key_diversity_loss(keys)
         gw, gk, gt, gp = torch.autograd.grad(loss, [w_q, keys, log_t, probe])
         rest = (gw.square().sum() + gk.square().sum() + gt.square()).reshape(1)
@@ -321,7 +322,8 @@ def train_step_bench(torch, iters):
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / iters
     return {"workload": "training step of the text-study layer: 8,192 tokens, 262,144 fp16 slots + fp32 master, "
-                        "forward + backward (queries through a 256->1024 projection, sub-keys, log-temperature, "
+                        "forward with Gumbel routing noise + backward (queries through a 256->1024 projection, "
+                        "sub-keys, log-temperature, "
                         "balance loss 0.01, key diversity loss 0.01, probe gradient) + sparse row-wise Adagrad",
             "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events"}
 

@@ -98,6 +98,17 @@ int mpl_score_select(const void* queries, int query_mode, float* q_len, const vo
                      int32_t* slots, float* weights, void* stream);
 
 /*
+ * memory.py:156 (jax.random.gumbel(rng, scores.shape)): fills out [rows, n]
+ * fp32 (rows = M*H*2 for the gumbel input of mpl_score_select) with
+ * Gumbel(0,1) samples g = -log(-log(u)), u on JAX's grid {k * 2^-23} of
+ * [FLT_MIN, 1), from a counter-based hash of (seed, row, column): each
+ * element depends only on those three, so the fill is one write pass and
+ * reproducible from the seed.  The stream differs from JAX's PRNG (the
+ * distribution and support are the same).
+ */
+int mpl_gumbel_noise(uint64_t seed, int64_t rows, int n, float* out, void* stream);
+
+/*
  * memory.py:179-193: out[m,:] = sum_r weights[m,r] * values[read(slots[m,r]),:]
  * over the R = H*k rows of each token, fp32 accumulation; values [N,d] in
  * values_dtype (MPL_F16 or MPL_F32); read(s) = s, or (s + N/2 + 1) % N when

@@ -17,6 +17,7 @@ MPL_Q_NORMALIZED, MPL_Q_RAW, MPL_Q_RAW_SCALED = 0, 1, 2
 
 # name -> (restype, argtypes); the C ABI of include/mpl.h
 _P, _I, _I64, _F, _SZ = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
+_U64 = C.c_uint64
 SIGNATURES = {
     "mpl_version": (_I, []),
     "mpl_last_error": (C.c_char_p, []),
@@ -27,6 +28,7 @@ SIGNATURES = {
     "mpl_score_select": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
                               _P, _P, _P, _P, _P, _P]),
     "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
+    "mpl_gumbel_noise": (_I, [_U64, _I64, _I, _P, _P]),
     "mpl_merge_rows_workspace_bytes": (_SZ, [_I64, _I, _I64]),
     "mpl_merge_rows": (_I, [_P, _P, _I64, _I, _P, _I, _I64, _P, _SZ, _P, _P, _P, _P, _I, _P]),
     "mpl_clip_scale_workspace_bytes": (_SZ, []),

@@ -78,6 +78,7 @@ struct ScoreParams {
   const uint4* packed;  // packed keys
   const float* gumbel;  // [M, HC, n] or null
   float T, noise_coef;
+  int noise_vec;  // gumbel rows 16-byte aligned (base aligned, n % 4 == 0)
   int64_t M;
   int HC, n, half, k, nblk, splits, blk_per_split;
   int pass1_blocks;  // blocks of each split scanned by the bound pass
@@ -250,13 +251,29 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
                                        0);
     }
   };
-  // The lane's 16 noise values of block blk (keys 8*(r/4) + 4*par + r%4).
+  // The lane's 16 noise values of block blk (keys 8*(r/4) + 4*par + r%4):
+  // four 16-byte loads when the block is whole and the rows are 16-byte
+  // aligned (noise_vec), else 16 clamped scalar loads.  The waits below count
+  // kNoiseLoads outstanding noise loads; the scalar form only waits longer.
+  constexpr int kNoiseLoads = NOISE ? 4 : 0;
   auto fetch_noise = [&](int blk) __attribute__((always_inline)) {
     GVec g;
     if (NOISE) {
+      const int kb = blk * 32;
+      if (p.noise_vec && kb + 32 <= p.n) {  // wave-uniform
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        g[NOISE ? r : 0] = grow[min(blk * 32 + 8 * (r >> 2) + 4 * par + (r & 3), p.n - 1)];
+        for (int grp = 0; grp < 4; ++grp) {
+          const float4 v = *(const float4*)(grow + kb + 8 * grp + 4 * par);
+          g[NOISE ? 4 * grp + 0 : 0] = v.x;
+          g[NOISE ? 4 * grp + 1 : 0] = v.y;
+          g[NOISE ? 4 * grp + 2 : 0] = v.z;
+          g[NOISE ? 4 * grp + 3 : 0] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          g[NOISE ? r : 0] = grow[min(kb + 8 * (r >> 2) + 4 * par + (r & 3), p.n - 1)];
+      }
     }
     return g;
   };
@@ -278,7 +295,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     gload(ua, bb);
     gload(ub, min(bb + 1, be - 1));
     GVec gcur = fetch_noise(bb);
-    wait_vmcnt_le<VPL + (NOISE ? 16 : 0)>();
+    wait_vmcnt_le<VPL + kNoiseLoads>();
     f32x16 x = f32x16{}, y;
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
@@ -287,7 +304,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     }
     auto step = [&](int j, f32x16& c, f32x16& d, const uint4* ucur, uint4* unext) __attribute__((always_inline)) {
       gload(unext, min(bb + j + 2, be - 1));
-      wait_vmcnt_le<VPL + (NOISE ? 16 : 0)>();
+      wait_vmcnt_le<VPL + kNoiseLoads>();
       d = f32x16{};
       auto issue = [&](int i) __attribute__((always_inline)) {
         d = Mfma<T>::mma(Mfma<T>::from_vec(ucur[i / OPV], i % OPV), qop[i], d);
@@ -317,7 +334,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     dma(tile0, bb);
     dma(tile1, min(bb + 1, be - 1));
     GVec gcur = fetch_noise(bb);
-    wait_vmcnt_le<LPW + (NOISE ? 16 : 0)>();
+    wait_vmcnt_le<LPW + kNoiseLoads>();
     asm volatile("s_barrier" ::: "memory");
     f32x16 x = f32x16{}, y;
 #pragma unroll
@@ -333,7 +350,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     // element steps: a chain of dependent MFMAs issued back to back would
     // hold the wave's issue slot until each finishes.
     auto step = [&](int j, f32x16& c, f32x16& d, const uint4* rd, uint4* wr) __attribute__((always_inline)) {
-      wait_vmcnt_le<NOISE ? 16 : 0>();
+      wait_vmcnt_le<kNoiseLoads>();
       asm volatile("s_barrier" ::: "memory");
       dma(wr, min(bb + j + 2, be - 1));
       uint4 u[VPL];
@@ -360,19 +377,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
 
   // Selection values of the lane's 16 keys of a block (padded keys -inf);
   // with noise, cl holds the clean scores.
-  auto lane_scores = [&](int kb, const f32x16& c, const GVec& g, float* sv, float* cl)
-                         __attribute__((always_inline)) {
+  // With noise, clean_at(c, r) is the clean score of element r; it is
+  // recomputed where needed rather than kept in 16 more registers.
+  auto clean_at = [&](const f32x16& c, int r) __attribute__((always_inline)) {
+    float v = c[r] * p.T;
+    return v * ql;  // ql == 1 without query_scale
+  };
+  auto lane_scores = [&](int kb, const f32x16& c, const GVec& g, float* sv) __attribute__((always_inline)) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float v = c[r];
-      if (NOISE) {
-        v = v * p.T;
-        v *= ql;  // ql == 1 without query_scale
-        cl[NOISE ? r : 0] = v;
-        v = __builtin_fmaf(p.noise_coef, g[NOISE ? r : 0], v);
-      }
-      sv[r] = v;
-    }
+    for (int r = 0; r < 16; ++r)
+      sv[r] = NOISE ? __builtin_fmaf(p.noise_coef, g[NOISE ? r : 0], clean_at(c, r)) : c[r];
     if (kb + 32 > p.n) {  // wave-uniform: only the last block can hold padded keys
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -399,9 +413,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   };
   sweep(b_begin, p1_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
                              __attribute__((always_inline)) {
-    float sv[16], cl[NOISE ? 16 : 1];
+    float sv[16];
     const bool raw = !NOISE && kb + 32 <= p.n;  // wave-uniform
-    if (!raw) lane_scores(kb, c, g, sv, cl);
+    if (!raw) lane_scores(kb, c, g, sv);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       issue_for(r, issue);
@@ -432,8 +446,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   st.off = lane0;
   sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
                             __attribute__((always_inline)) {
-    float sv[16], cl[NOISE ? 16 : 1];
-    lane_scores(kb, c, g, sv, cl);
+    float sv[16];
+    lane_scores(kb, c, g, sv);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       if (active && __ballot(st.off > flush_at) != 0)
@@ -446,7 +460,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
         if (active && x > st.thr) {
           lds_at(cscore, st.off) = x;
           lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
-          if (NOISE) lds_at(cpay, st.off) = cl[NOISE ? r : 0];
+          if (NOISE) lds_at(cpay, st.off) = clean_at(c, r);
           st.off += kEntryBytes;
         }
       }
@@ -948,6 +962,7 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
   sp.gumbel = gumbel;
   sp.T = temperature;
   sp.noise_coef = noise_coef;
+  sp.noise_vec = noise && ((uintptr_t)gumbel & 15) == 0 && n % 4 == 0;
   sp.M = M;
   sp.HC = HC;
   sp.n = n;

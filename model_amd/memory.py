@@ -124,6 +124,21 @@ class _Result(dict):
         return q_hat
 
 
+def routing_seed(rngs: Optional[Dict[str, Any]]) -> int:
+    """64-bit seed of the routing noise (the reference's make_rng("routing")):
+    ``rngs["routing"]`` as an int seed (the same noise on every call, like a
+    fixed JAX key), one draw from a torch.Generator given there, or one draw
+    from torch's default CPU generator (so torch.manual_seed reproduces runs).
+    A CPU draw needs no device synchronisation; a CUDA generator's does."""
+    r = None if rngs is None else rngs.get("routing")
+    top = (1 << 63) - 1
+    if r is None:
+        return int(torch.randint(0, top, (1,)).item())
+    if isinstance(r, torch.Generator):
+        return int(torch.randint(0, top, (1,), generator=r, device=r.device).item())
+    return int(r) & ((1 << 64) - 1)
+
+
 class MemoryPool:
     """memory.py:64-113 attributes, memory.py:119-227 call."""
 
@@ -240,13 +255,9 @@ class MemoryPool:
 
         noise_coef = 0.0
         if gumbel is None and train and self.routing_noise > 0:
-            gen = None
-            if rngs is not None and "routing" in rngs:
-                r = rngs["routing"]
-                gen = r if isinstance(r, torch.Generator) else torch.Generator(device=dev).manual_seed(int(r))
-            u = torch.rand((M, H, 2, n), generator=gen, device=dev, dtype=torch.float32)
-            tiny = torch.finfo(torch.float32).tiny
-            gumbel = -torch.log(-torch.log(u.clamp_(min=tiny)))  # jax.random.gumbel's transform
+            # memory.py:156: Gumbel(0,1) over the score shape, one fill pass
+            gumbel = torch.empty((M, H, 2, n), dtype=torch.float32, device=dev)
+            check(L.mpl_gumbel_noise(routing_seed(rngs), M * H * 2, n, ptr(gumbel), stream), "mpl_gumbel_noise")
         if gumbel is not None:
             ns = float(noise_scale) if not isinstance(noise_scale, torch.Tensor) else float(noise_scale.detach().cpu())
             noise_coef = float(self.routing_noise) * ns

@@ -395,3 +395,58 @@ def test_revive_dead_keys_known_answer():
     u = np.array([0.5, 0.25, 0.3, 0.19])
     np.testing.assert_allclose(nu[0, 0], u / u.sum(), rtol=1e-12)
     np.testing.assert_allclose(nu[0, 1], usage[0, 1], rtol=1e-12)
+
+
+# ----------------------------------------------------------- routing noise
+# MurmurHash3_x86_32 known answers (the hash's commonly published test
+# vectors) and SMHasher's verification value for it; murmur3_32 ends in
+# fmix32, so a wrong constant or shift in the oracle's fmix32 fails these.
+_MURMUR3_VECTORS = [
+    (b"", 0, 0x00000000),
+    (b"", 1, 0x514E28B7),
+    (b"", 0xFFFFFFFF, 0x81F16F39),
+    (b"\0\0\0\0", 0, 0x2362F9DE),
+    (b"aaaa", 0x9747B28C, 0x5A97808A),
+    (b"Hello, world!", 0x9747B28C, 0x24884CBA),
+    (b"The quick brown fox jumps over the lazy dog", 0x9747B28C, 0x2FA826CD),
+]
+
+
+def test_fmix32_pinned_by_murmur3_known_answers():
+    from oracle import noise as on
+
+    for data, seed, want in _MURMUR3_VECTORS:
+        assert on.murmur3_32(data, seed) == want, (data, seed)
+    # SMHasher VerificationTest: hash keys 0..i-1 with seed 256-i, then hash the hashes
+    key = bytes(range(256))
+    hashes = b"".join(on.murmur3_32(key[:i], 256 - i).to_bytes(4, "little") for i in range(256))
+    assert on.murmur3_32(hashes, 0) == 0xB0F57EE3
+    # fmix32 is a bijection: no collisions over a block of consecutive inputs
+    assert len(np.unique(on.fmix32(np.arange(1 << 16)))) == 1 << 16
+
+
+def test_gumbel_noise_support_and_moments():
+    """u on JAX's grid {k * 2^-23} clamped at FLT_MIN; g = -log(-log(u)) has
+    Gumbel(0,1) moments (mean = Euler-Mascheroni, variance = pi^2/6)."""
+    from oracle import noise as on
+
+    k = on.uniform_bits(12345, 256, 4096)
+    assert k.min() >= 0 and k.max() < 2 ** 23
+    g = on.gumbel_noise(12345, 256, 4096)
+    assert np.all(np.isfinite(g))
+    lo = -np.log(-np.log(np.float64(on.FLT_MIN)))
+    hi = -np.log(-np.log(1.0 - 2.0 ** -23))
+    assert g.min() >= lo - 1e-12 and g.max() <= hi + 1e-12
+    assert abs(g.mean() - np.euler_gamma) < 0.01
+    assert abs(g.var() - np.pi ** 2 / 6) < 0.02
+    # uniform bits: each of 16 bins within 2% of 1/16
+    frac = np.bincount(k.reshape(-1) >> 19, minlength=16) / k.size
+    assert np.all(np.abs(frac - 1 / 16) < 0.02 / 16)
+    # columns of a row, rows of a seed and seeds are decorrelated
+    a = on.gumbel_noise(1, 512, 512)
+    b = on.gumbel_noise(2, 512, 512)
+    assert abs(np.corrcoef(a.reshape(-1), b.reshape(-1))[0, 1]) < 0.01
+    assert abs(np.corrcoef(a[:-1].reshape(-1), a[1:].reshape(-1))[0, 1]) < 0.01
+    assert abs(np.corrcoef(a[:, :-1].reshape(-1), a[:, 1:].reshape(-1))[0, 1]) < 0.01
+    # rows are independent of where the block starts
+    np.testing.assert_array_equal(on.gumbel_noise(9, 4, 33, row0=5), on.gumbel_noise(9, 9, 33)[5:])
