@@ -98,6 +98,21 @@ int mpl_score_select(const void* queries, int query_mode, float* q_len, const vo
                      int32_t* slots, float* weights, void* stream);
 
 /*
+ * memory.py:161-163 and 207 (_top_k of the select scores, or of the clean
+ * scores for the balance loss's f): stage 1 of mpl_score_select alone, same
+ * arguments and semantics, writing only sub_idx [M,H,2,k] and sub_scores
+ * [M,H,2,k] (clean scores, descending select order).  With several key
+ * splits the split lists are reduced to one; the workspace query includes
+ * that scratch.
+ */
+size_t mpl_score_topk_workspace_bytes(int64_t M, int H, int n, int half, int k);
+int mpl_score_topk(const void* queries, int query_mode, float* q_len, const void* packed_keys,
+                   int64_t M, int H, int n, int half, int k, int score_dtype,
+                   float temperature, const float* gumbel, float noise_coef,
+                   void* workspace, size_t workspace_bytes,
+                   int32_t* sub_idx, float* sub_scores, void* stream);
+
+/*
  * memory.py:156 (jax.random.gumbel(rng, scores.shape)): fills out [rows, n]
  * fp32 (rows = M*H*2 for the gumbel input of mpl_score_select) with
  * Gumbel(0,1) samples g = -log(-log(u)), u on JAX's grid {k * 2^-23} of

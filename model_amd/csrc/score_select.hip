@@ -915,6 +915,13 @@ static int dispatch_stage1(const ScoreParams& sp, int64_t blocks, int score_dtyp
 
 using namespace mpl;
 
+// Scratch of the stage-1-only call beyond the selection's: with several
+// splits and k != 16 the lists are combined by the pair kernel, whose slot
+// outputs (flat_idx, slots, weights) then go to scratch.
+static size_t topk_extra_bytes(const Plan& pl, int64_t M, int H, int k) {
+  return (pl.splits > 1 && k != 16) ? (size_t)M * H * k * 3 * 4 : 0;
+}
+
 extern "C" size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int half, int k) {
   (void)half;
   if (M <= 0 || H <= 0 || n <= 0 || k <= 0) return 0;
@@ -922,33 +929,44 @@ extern "C" size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int 
   return ws_bytes(pl, M, H, k, true);
 }
 
-extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_len, const void* packed_keys,
-                                int64_t M, int H, int n, int half, int k, int score_dtype,
-                                float temperature, const float* gumbel, float noise_coef,
-                                void* workspace, size_t workspace_bytes, int32_t* sub_idx,
-                                float* sub_scores, int32_t* flat_idx, int32_t* slots,
-                                float* weights, void* stream) {
+extern "C" size_t mpl_score_topk_workspace_bytes(int64_t M, int H, int n, int half, int k) {
+  (void)half;
+  if (M <= 0 || H <= 0 || n <= 0 || k <= 0) return 0;
+  const Plan pl = make_plan(M, H, n, k);
+  const size_t extra = topk_extra_bytes(pl, M, H, k);
+  return (ws_bytes(pl, M, H, k, true) + 255) / 256 * 256 + extra;
+}
+
+// Both entry points: stage 1 (+ the split-list reduction); with `pair`, stage
+// 2 and the softmax as well.  Without `pair`, flat_idx/slots/weights are null.
+static int select_impl(const char* who, bool pair, const void* queries, int query_mode, float* q_len,
+                       const void* packed_keys, int64_t M, int H, int n, int half, int k, int score_dtype,
+                       float temperature, const float* gumbel, float noise_coef, void* workspace,
+                       size_t workspace_bytes, int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
+                       int32_t* slots, float* weights, void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H > 0 && n > 0 && half > 0 && k > 0, MPL_EINVAL,
-              "mpl_score_select: bad sizes M=%lld H=%d n=%d half=%d k=%d", (long long)M, H, n, half, k);
-  MPL_REQUIRE(k <= n && k <= 32, MPL_EUNSUPPORTED, "mpl_score_select: need k <= min(n, 32), got k=%d n=%d",
-              k, n);
-  MPL_REQUIRE(half <= 128, MPL_EUNSUPPORTED, "mpl_score_select: half=%d > 128", half);
+              "%s: bad sizes M=%lld H=%d n=%d half=%d k=%d", who, (long long)M, H, n, half, k);
+  MPL_REQUIRE(k <= n && k <= 32, MPL_EUNSUPPORTED, "%s: need k <= min(n, 32), got k=%d n=%d", who, k, n);
+  MPL_REQUIRE(half <= 128, MPL_EUNSUPPORTED, "%s: half=%d > 128", who, half);
   MPL_REQUIRE(score_dtype != MPL_F16 || half % 8 == 0, MPL_EUNSUPPORTED,
-              "mpl_score_select: fp16 scoring needs half %% 8 == 0 (got %d); use MPL_F32", half);
-  MPL_REQUIRE((int64_t)n * n < ((int64_t)1 << 31), MPL_EUNSUPPORTED, "mpl_score_select: n*n must be < 2^31");
+              "%s: fp16 scoring needs half %% 8 == 0 (got %d); use MPL_F32", who, half);
+  MPL_REQUIRE((int64_t)n * n < ((int64_t)1 << 31), MPL_EUNSUPPORTED, "%s: n*n must be < 2^31", who);
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
-              "mpl_score_select: score_dtype must be MPL_F16 or MPL_F32");
+              "%s: score_dtype must be MPL_F16 or MPL_F32", who);
   if (M == 0) return MPL_OK;
-  MPL_REQUIRE(queries && packed_keys && sub_idx && sub_scores && flat_idx && slots && weights, MPL_EINVAL,
-              "mpl_score_select: null buffer");
+  MPL_REQUIRE(queries && packed_keys && sub_idx && sub_scores && (!pair || (flat_idx && slots && weights)),
+              MPL_EINVAL, "%s: null buffer", who);
   MPL_REQUIRE(query_mode == MPL_Q_NORMALIZED || query_mode == MPL_Q_RAW || query_mode == MPL_Q_RAW_SCALED,
-              MPL_EINVAL, "mpl_score_select: bad query_mode %d", query_mode);
+              MPL_EINVAL, "%s: bad query_mode %d", who, query_mode);
   const bool noise = gumbel != nullptr;
   const Plan pl = make_plan(M, H, n, k);
-  const size_t need = ws_bytes(pl, M, H, k, noise);
+  const size_t sel_need = ws_bytes(pl, M, H, k, noise);
+  const size_t extra = pair ? 0 : topk_extra_bytes(pl, M, H, k);
+  const size_t extra_at = (sel_need + 255) / 256 * 256;
+  const size_t need = extra ? extra_at + extra : sel_need;
   MPL_REQUIRE(workspace_bytes >= need && (need == 0 || workspace != nullptr), MPL_EWORKSPACE,
-              "mpl_score_select: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+              "%s: workspace of %zu bytes needed, %zu given", who, need, workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
   const int HC = 2 * H;
   const size_t per = (size_t)M * HC * k;
@@ -987,10 +1005,10 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
   const int64_t blocks = pl.qblocks * pl.splits * HC;
   int rc = dispatch_stage1(sp, blocks, score_dtype, HP, noise, pl.kmax, s);
   if (rc) {
-    set_error("mpl_score_select: unsupported padded half %d", HP);
+    set_error("%s: unsupported padded half %d", who, HP);
     return rc;
   }
-  rc = check_launch("mpl_score_select(stage 1)");
+  rc = check_launch(pair ? "mpl_score_select(stage 1)" : "mpl_score_topk(stage 1)");
   if (rc) return rc;
 
   PairParams pp;
@@ -1033,10 +1051,53 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
     pp.S = S2;
     r += (noise ? 3 : 2) * part2;
   }
+  if (!pair && pp.S == 1) return MPL_OK;  // stage 1 wrote sub_idx / sub_scores
+  if (!pair && k == 16) {
+    // the last reduction level writes the single list straight to the outputs
+    MergeParams mp;
+    mp.sel = pp.sel;
+    mp.clean = pp.clean;
+    mp.idx = pp.idx;
+    mp.rows = M * HC;
+    mp.S = pp.S;
+    mp.S2 = 1;
+    mp.out_clean = sub_scores;
+    mp.out_idx = sub_idx;
+    mp.out_sel = nullptr;
+    merge_splits_k16<<<(unsigned)cdiv(mp.rows * 16, 256), 256, 0, s>>>(mp);
+    return check_launch("mpl_score_topk(split merge)");
+  }
+  if (!pair) {  // k != 16 with splits: the pair kernel combines them; its slot outputs go to scratch
+    char* x = (char*)workspace + extra_at;
+    const size_t mhk = (size_t)M * H * k;
+    pp.flat_idx = (int32_t*)x;
+    pp.slots = (int32_t*)(x + mhk * 4);
+    pp.weights = (float*)(x + mhk * 8);
+  }
   const int G = k <= 16 ? 16 : 32;
   const unsigned g2 = (unsigned)cdiv(M * H * G, 256);
   if (k == 16) pair_kernel_k16<<<g2, 256, 0, s>>>(pp);
   else if (G == 16) pair_kernel<16><<<g2, 256, 0, s>>>(pp);
   else pair_kernel<32><<<g2, 256, 0, s>>>(pp);
-  return check_launch("mpl_score_select(stage 2)");
+  return check_launch(pair ? "mpl_score_select(stage 2)" : "mpl_score_topk(split lists)");
+}
+
+extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_len, const void* packed_keys,
+                                int64_t M, int H, int n, int half, int k, int score_dtype,
+                                float temperature, const float* gumbel, float noise_coef,
+                                void* workspace, size_t workspace_bytes, int32_t* sub_idx,
+                                float* sub_scores, int32_t* flat_idx, int32_t* slots,
+                                float* weights, void* stream) {
+  return select_impl("mpl_score_select", true, queries, query_mode, q_len, packed_keys, M, H, n, half, k,
+                     score_dtype, temperature, gumbel, noise_coef, workspace, workspace_bytes, sub_idx,
+                     sub_scores, flat_idx, slots, weights, stream);
+}
+
+extern "C" int mpl_score_topk(const void* queries, int query_mode, float* q_len, const void* packed_keys,
+                              int64_t M, int H, int n, int half, int k, int score_dtype, float temperature,
+                              const float* gumbel, float noise_coef, void* workspace, size_t workspace_bytes,
+                              int32_t* sub_idx, float* sub_scores, void* stream) {
+  return select_impl("mpl_score_topk", false, queries, query_mode, q_len, packed_keys, M, H, n, half, k,
+                     score_dtype, temperature, gumbel, noise_coef, workspace, workspace_bytes, sub_idx,
+                     sub_scores, nullptr, nullptr, nullptr, stream);
 }

@@ -345,21 +345,18 @@ class MemoryPool:
         return stats
 
     def _clean_sub_idx(self, q, packed, score_code, T, M):
+        """memory.py:207: the stage-1 top-k of the clean scores (no stage 2)."""
         H, n, k, half = self.heads, self.n_sub_keys, self.top_k, self.d_key // 2
         dev = q.device
         q_mode = _lib.MPL_Q_RAW_SCALED if self.query_scale else _lib.MPL_Q_RAW
         L = _lib.lib()
-        ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
+        ws_bytes = L.mpl_score_topk_workspace_bytes(M, H, n, half, k)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         sub_idx = torch.empty((M, H, 2, k), dtype=torch.int32, device=dev)
         sub_scores = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
-        flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
-        slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
-        weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_select(ptr(q), q_mode, None, ptr(packed), M, H, n, half, k, score_code, T,
-                                 None, 0.0, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores),
-                                 ptr(flat_idx), ptr(slots), ptr(weights), _lib.stream_ptr(dev)),
-              "mpl_score_select(clean)")
+        check(L.mpl_score_topk(ptr(q), q_mode, None, ptr(packed), M, H, n, half, k, score_code, T,
+                               None, 0.0, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores), _lib.stream_ptr(dev)),
+              "mpl_score_topk(clean)")
         return sub_idx
 
 

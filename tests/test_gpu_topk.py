@@ -1,0 +1,94 @@
+"""mpl_score_topk (stage 1 alone: memory.py:161-163, and the clean _top_k of
+memory.py:207) against mpl_score_select's stage-1 outputs, which the lookup
+tests check against the oracle, and against the oracle's top_k directly.
+
+Ids bit-exact; scores bit-exact to mpl_score_select's (the same kernels and
+the same exact list merges), and within fp16-scoring rounding of the
+oracle's fp64 scores on near-tie-free rows.  Shapes cover one split, split
+lists reduced by merge levels (k = 16) and by the pair kernel (k != 16),
+routing noise, and fp32 scoring."""
+
+import numpy as np
+import pytest
+import torch
+
+from model_amd import _lib
+from oracle import lookup as ol
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(M, H, n, d_key, k, score, noise, seed):
+    L = _lib.lib()
+    half = d_key // 2
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn((M, H, 2, half), generator=g).cuda()
+    keys = torch.randn((H, 2, n, half), generator=g).cuda()
+    gum = None
+    if noise:
+        gum = -torch.log(-torch.log(torch.rand((M, H, 2, n), generator=g).clamp_(1e-20, 1 - 1e-7))).cuda()
+    packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, score), dtype=torch.uint8, device="cuda")
+    khat = torch.empty_like(keys)
+    st = _lib.stream_ptr(q.device)
+    _lib.check(L.mpl_pack_keys(_lib.ptr(keys), H, n, half, score, _lib.ptr(khat), _lib.ptr(packed), st), "pack")
+    mode = _lib.MPL_Q_RAW
+    if score == _lib.MPL_F32:  # raw queries are fp16-scoring only: normalise first
+        qn = torch.empty_like(q)
+        _lib.check(L.mpl_l2_normalize(_lib.ptr(q), M * H * 2, half, 1e-6, _lib.ptr(qn), None, None, st), "norm")
+        q, mode = qn, _lib.MPL_Q_NORMALIZED
+    T, coef = 10.0, (0.7 if noise else 0.0)
+    i32, f32 = torch.int32, torch.float32
+    outs = {}
+    for name in ("select", "topk"):
+        sub_idx = torch.full((M, H, 2, k), -7, dtype=i32, device="cuda")
+        sub_sc = torch.full((M, H, 2, k), 7.0, dtype=f32, device="cuda")
+        if name == "select":
+            wsb = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
+            ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+            fi = torch.empty((M, H, k), dtype=i32, device="cuda")
+            sl = torch.empty((M, H, k), dtype=i32, device="cuda")
+            w = torch.empty((M, H, k), dtype=f32, device="cuda")
+            _lib.check(L.mpl_score_select(_lib.ptr(q), mode, None, _lib.ptr(packed), M, H, n, half, k, score, T,
+                                          _lib.ptr(gum), coef, _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
+                                          _lib.ptr(fi), _lib.ptr(sl), _lib.ptr(w), st), "select")
+        else:
+            wsb = L.mpl_score_topk_workspace_bytes(M, H, n, half, k)
+            ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+            _lib.check(L.mpl_score_topk(_lib.ptr(q), mode, None, _lib.ptr(packed), M, H, n, half, k, score, T,
+                                        _lib.ptr(gum), coef, _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
+                                        st), "topk")
+        torch.cuda.synchronize()
+        outs[name] = (sub_idx.cpu().numpy(), sub_sc.cpu().numpy())
+    return q, khat, gum, T, coef, outs
+
+
+@pytest.mark.parametrize("M,H,n,d_key,k,score,noise", [
+    (300, 4, 512, 256, 16, _lib.MPL_F16, False),   # text-study keys, one split
+    (512, 4, 512, 256, 16, _lib.MPL_F16, False),   # 16 splits: merge levels
+    (3, 4, 1024, 256, 16, _lib.MPL_F16, False),    # decode: 32 splits, two levels
+    (37, 2, 64, 16, 4, _lib.MPL_F16, False),       # k != 16 with splits: pair kernel
+    (5, 2, 640, 32, 16, _lib.MPL_F16, True),       # noise with splits
+    (40, 2, 96, 12, 8, _lib.MPL_F32, True),        # fp32 scoring, noise, ragged n
+])
+def test_topk_equals_select_stage1(gpu_lib, M, H, n, d_key, k, score, noise):
+    q, khat, gum, T, coef, outs = _run(M, H, n, d_key, k, score, noise, seed=M + n + k)
+    np.testing.assert_array_equal(outs["topk"][0], outs["select"][0])
+    np.testing.assert_array_equal(outs["topk"][1], outs["select"][1])
+    # against the oracle's top_k of the fp64 select scores, on rows whose k-th
+    # and (k+1)-th scores are apart by more than twice the fp16-scoring error:
+    # unit rows rounded to fp16 move a cosine by at most 2 * 2^-12, so a score
+    # by at most 2^-11 * T
+    qn = ol.l2_normalize(q.cpu().numpy().astype(np.float64))
+    kn = khat.cpu().numpy().astype(np.float64)
+    cos = np.einsum("mhcd,hcnd->mhcn", qn, kn)
+    sel = cos * T + (coef * gum.cpu().numpy().astype(np.float64) if gum is not None else 0.0)
+    want = ol.top_k(sel, k)[1]
+    srt = -np.sort(-sel, axis=-1)
+    gap = srt[..., k - 1] - (srt[..., k] if n > k else -np.inf)
+    free = gap > 2.5 * 2.0 ** -11 * T
+    assert free.mean() > 0.5
+    # the set is fixed there; the order inside it may swap near-tied entries
+    got_ids = outs["topk"][0][free]
+    np.testing.assert_array_equal(np.sort(got_ids, -1), np.sort(want[free], -1))
+    clean = np.take_along_axis((cos * T)[free], got_ids.astype(np.int64), -1)
+    np.testing.assert_allclose(outs["topk"][1][free], clean, rtol=0, atol=2.0 ** -11 * T)
