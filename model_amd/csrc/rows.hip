@@ -684,7 +684,10 @@ __global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ v
   const int64_t nw = (int64_t)gridDim.x * (kRowThreads / kWave);
   const int nv = d / W;
   const float sc = grad_scale != nullptr ? *grad_scale : 1.f;
-  const float b1 = 0.9f, b2 = 0.999f, eps = 1e-8f;
+  // train.py:421-422 writes (1 - ADAM_B1) and (1 - ADAM_B2) with Python
+  // floats: computed in double and rounded once to fp32 (0.1f, 0.001f), not
+  // 1.f - 0.9f (0.100000024f) and 1.f - 0.999f (0.00100004673f, 5e-5 off)
+  const float b1 = 0.9f, b2 = 0.999f, ob1 = (float)(1.0 - 0.9), ob2 = (float)(1.0 - 0.999), eps = 1e-8f;
   constexpr int R = VPL >= 16 ? 1 : 2;  // rows in flight per wave, as in row_adagrad_kernel
   const int64_t wid = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
   for (int64_t base = wid; base < cap; base += kWave * nw) {
@@ -722,8 +725,8 @@ __global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ v
 #pragma unroll
           for (int i = 0; i < W; ++i) {
             const float gi = g[r][i] * sc;
-            m[r][i] = b1 * m[r][i] + (1.f - b1) * gi;
-            q[r][i] = b2 * q[r][i] + (1.f - b2) * gi * gi;
+            m[r][i] = b1 * m[r][i] + ob1 * gi;
+            q[r][i] = b2 * q[r][i] + ob2 * gi * gi;
             x[r][i] += -lr * (m[r][i] / c1) / (sqrtf(q[r][i] / c2) + eps);
           }
           TableVec<float, W>::store(m1 + o, m[r]);
@@ -812,6 +815,90 @@ static void dispatch_reduce(const uint32_t* sp, const int32_t* seg_of, const int
 
 using namespace mpl;
 
+// LSD radix sort of the slots (positions as payload), then the segments of
+// equal slots: uniq[u], seg_start[u] (seg_start[U] = P), seg_of[i] of sorted
+// position i, num_unique = U.  The workspace is laid out by merge_layout().
+struct Segments {
+  const uint32_t* pos;  // original fetch position of each sorted entry
+  int32_t* seg_start;
+  int32_t* seg_of;
+  uint32_t* nseg;
+};
+
+static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayout& L, char* ws, int32_t* uniq,
+                              int32_t* num_unique, hipStream_t s) {
+  uint32_t* keys[2] = {(uint32_t*)(ws + L.keys[0]), (uint32_t*)(ws + L.keys[1])};
+  uint32_t* vals[2] = {(uint32_t*)(ws + L.vals[0]), (uint32_t*)(ws + L.vals[1])};
+  uint32_t* hist = (uint32_t*)(ws + L.hist);
+  uint32_t* tile_cnt = (uint32_t*)(ws + L.tile_cnt);
+  uint32_t* nseg = (uint32_t*)(ws + L.counters);
+  uint32_t* totals = (uint32_t*)(ws + L.totals);
+  int32_t* seg_start = (int32_t*)(ws + L.seg_start);
+  int32_t* seg_of = (int32_t*)(ws + L.seg_of);
+  const unsigned nt = (unsigned)L.ntiles;
+  const uint32_t* kin = slots;
+  const uint32_t* vin = nullptr;
+  int cur = 0;
+  for (int pass = 0; pass < L.passes; ++pass) {
+    const int shift = 8 * pass;
+    radix_hist_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);
+    digit_scan_kernel<<<256, 1024, 0, s>>>(hist, L.ntiles, totals);
+    radix_scatter_kernel<<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles,
+                                                     totals);
+    kin = keys[cur];
+    vin = vals[cur];
+    cur ^= 1;
+  }
+  seg_count_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt);
+  scan_exclusive_kernel<<<1, 1024, 0, s>>>(tile_cnt, L.ntiles, nseg);
+  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of);
+  seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique);
+  return Segments{vin, seg_start, seg_of, nseg};
+}
+
+// inverse[pos[i]] = seg_of[i]; uniq[u] = pool_size for num_unique <= u < len.
+__global__ __launch_bounds__(256) void unique_finish_kernel(const uint32_t* __restrict__ pos,
+                                                            const int32_t* __restrict__ seg_of, int64_t P,
+                                                            const int32_t* __restrict__ num_unique,
+                                                            int64_t pool_size, int32_t* __restrict__ uniq,
+                                                            int32_t* __restrict__ inverse) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= P) return;
+  inverse[pos[i]] = seg_of[i];
+  if (i >= *num_unique) uniq[i] = (int32_t)pool_size;
+}
+
+extern "C" size_t mpl_unique_slots_workspace_bytes(int64_t P, int64_t pool_size) {
+  if (P <= 0 || pool_size <= 0) return 0;
+  return merge_layout(P, 4, pool_size > P ? pool_size : P).total;
+}
+
+extern "C" int mpl_unique_slots(const int32_t* slots, int64_t P, int64_t pool_size, void* workspace,
+                                size_t workspace_bytes, int32_t* uniq, int32_t* inverse, int32_t* num_unique,
+                                void* stream) {
+  clear_error();
+  MPL_REQUIRE(P >= 0 && pool_size > 0, MPL_EINVAL, "mpl_unique_slots: bad sizes P=%lld pool_size=%lld",
+              (long long)P, (long long)pool_size);
+  MPL_REQUIRE(P < ((int64_t)1 << 31) && pool_size < ((int64_t)1 << 31), MPL_EUNSUPPORTED,
+              "mpl_unique_slots: P and pool_size must be < 2^31");
+  MPL_REQUIRE(num_unique != nullptr, MPL_EINVAL, "mpl_unique_slots: null num_unique");
+  hipStream_t s = (hipStream_t)stream;
+  if (P == 0) {
+    store_zero_kernel<<<1, 1, 0, s>>>(num_unique);
+    return check_launch("mpl_unique_slots");
+  }
+  MPL_REQUIRE(slots && uniq && inverse, MPL_EINVAL, "mpl_unique_slots: null buffer");
+  // segments are counted against P, not min(P, pool_size): any input, even
+  // ids outside [0, pool_size), stays inside the [P] buffers
+  const MergeLayout L = merge_layout(P, 4, pool_size > P ? pool_size : P);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
+              "mpl_unique_slots: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
+  const Segments sg = sort_segments((const uint32_t*)slots, P, L, (char*)workspace, uniq, num_unique, s);
+  unique_finish_kernel<<<(unsigned)cdiv(P, 256), 256, 0, s>>>(sg.pos, sg.seg_of, P, num_unique, pool_size, uniq,
+                                                              inverse);
+  return check_launch("mpl_unique_slots");
+}
+
 extern "C" size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_size) {
   if (P <= 0 || d <= 0 || pool_size <= 0) return 0;
   return merge_layout(P, d, pool_size).total;
@@ -839,36 +926,14 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_merge_rows: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
   char* ws = (char*)workspace;
-  uint32_t* keys[2] = {(uint32_t*)(ws + L.keys[0]), (uint32_t*)(ws + L.keys[1])};
-  uint32_t* vals[2] = {(uint32_t*)(ws + L.vals[0]), (uint32_t*)(ws + L.vals[1])};
-  uint32_t* hist = (uint32_t*)(ws + L.hist);
-  uint32_t* tile_cnt = (uint32_t*)(ws + L.tile_cnt);
-  uint32_t* nseg = (uint32_t*)(ws + L.counters);
-  uint32_t* totals = (uint32_t*)(ws + L.totals);
-  int32_t* seg_start = (int32_t*)(ws + L.seg_start);
-  int32_t* seg_of = (int32_t*)(ws + L.seg_of);
-  float* partial = (float*)(ws + L.partial);
-
-  const unsigned nt = (unsigned)L.ntiles;
-  const uint32_t* kin = (const uint32_t*)slots;
-  const uint32_t* vin = nullptr;
-  int cur = 0;
-  for (int pass = 0; pass < L.passes; ++pass) {
-    const int shift = 8 * pass;
-    radix_hist_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);
-    digit_scan_kernel<<<256, 1024, 0, s>>>(hist, L.ntiles, totals);
-    radix_scatter_kernel<<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles,
-                                                     totals);
-    kin = keys[cur];
-    vin = vals[cur];
-    cur ^= 1;
-  }
+  const Segments sg = sort_segments((const uint32_t*)slots, P, L, ws, uniq, num_unique, s);
   int rc = check_launch("mpl_merge_rows(sort)");
   if (rc) return rc;
-  seg_count_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt);
-  scan_exclusive_kernel<<<1, 1024, 0, s>>>(tile_cnt, L.ntiles, nseg);
-  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of);
-  seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique);
+  const uint32_t* vin = sg.pos;
+  int32_t* seg_start = sg.seg_start;
+  int32_t* seg_of = sg.seg_of;
+  uint32_t* nseg = sg.nseg;
+  float* partial = (float*)(ws + L.partial);
   if (d % 4 == 0)
     dispatch_reduce<4>(vin, seg_of, seg_start, weights, g, fetches_per_token, d / 4, P, rows, row_sq, partial, L,
                        nseg, pool_size, uniq, zero_padding, s);

@@ -87,8 +87,10 @@ def lazy_adam(values, m, v, uniq, g_rows, lr: float, step: int, master=None):
     gk = g[keep]
     n = np.float32(step + 1)
     b1, b2 = np.float32(ADAM_B1), np.float32(ADAM_B2)
-    m_rows = b1 * m[r] + (np.float32(1) - b1) * gk
-    v_rows = b2 * v[r] + (np.float32(1) - b2) * gk * gk
+    # (1 - ADAM_B*) are Python-float expressions in train.py:421-422, rounded
+    # once to fp32 by JAX's weak typing (not 1 - float32(b), which cancels)
+    m_rows = b1 * m[r] + np.float32(1 - ADAM_B1) * gk
+    v_rows = b2 * v[r] + np.float32(1 - ADAM_B2) * gk * gk
     c1 = np.float32(1) - b1 ** n
     c2 = np.float32(1) - b2 ** n
     upd = -np.float32(lr) * (m_rows / c1) / (np.sqrt(v_rows / c2) + np.float32(ADAM_EPS))
