@@ -134,6 +134,41 @@ int mpl_gather_wsum(const void* values, int values_dtype, int64_t N, int d,
                     int shuffle_reads, float* out, void* stream);
 
 /*
+ * host_pool.py:206-220 (fetch: jnp.unique(flat, size=P, return_inverse=True)
+ * on the device before the host read): uniq [P] int32 receives the distinct
+ * slots ascending, then pool_size for u >= U; inverse [P] int32 the position
+ * of slots[p] in uniq (uniq[inverse[p]] == slots[p]); num_unique [1] (device)
+ * U.  Slots are expected in [0, pool_size); other values are tolerated
+ * (never out of bounds) but not sorted meaningfully.  Workspace of
+ * mpl_unique_slots_workspace_bytes() bytes.
+ */
+size_t mpl_unique_slots_workspace_bytes(int64_t P, int64_t pool_size);
+int mpl_unique_slots(const int32_t* slots, int64_t P, int64_t pool_size, void* workspace,
+                     size_t workspace_bytes, int32_t* uniq, int32_t* inverse, int32_t* num_unique,
+                     void* stream);
+
+/*
+ * host_pool.py:117-127 (HostPool.gather: rows of the table for the given
+ * ids) as one device kernel: out[i, :] = table[clamp(idx[i]), :] for
+ * i < min(count, *count_dev) (count_dev, device memory, may be NULL), rows
+ * of d elements of dtype (MPL_F16 / MPL_F32) copied unchanged; ids are
+ * clamped to [0, N).  The table may be device memory or pinned host memory
+ * mapped for the device (its device address from mpl_host_device_pointer):
+ * the kernel then reads the rows across the host link.
+ */
+int mpl_gather_rows(const void* table, int dtype, int64_t N, int d, const int32_t* idx,
+                    int64_t count, const int32_t* count_dev, void* out, void* stream);
+
+/*
+ * No counterpart in the reference (which reads host rows on host threads):
+ * the device address of pinned host memory (hipHostGetDevicePointer), for
+ * passing a pinned table to mpl_gather_rows, mpl_row_adagrad or
+ * mpl_row_adam.  Fails, without launching anything, for memory that is not
+ * pinned and mapped.
+ */
+int mpl_host_device_pointer(void* host_ptr, void** dev_ptr);
+
+/*
  * train.py:146-172 (fetched_row_grads + _merge_rows): gradient rows of the
  * fetched pool rows.  Fetch p in [0, P) of token p / fetches_per_token reads
  * slot slots[p] with weight weights[p] (weights == NULL: 1).  With

@@ -29,6 +29,10 @@ SIGNATURES = {
                               _P, _P, _P, _P, _P, _P]),
     "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
     "mpl_gumbel_noise": (_I, [_U64, _I64, _I, _P, _P]),
+    "mpl_unique_slots_workspace_bytes": (_SZ, [_I64, _I64]),
+    "mpl_unique_slots": (_I, [_P, _I64, _I64, _P, _SZ, _P, _P, _P, _P]),
+    "mpl_gather_rows": (_I, [_P, _I, _I64, _I, _P, _I64, _P, _P, _P]),
+    "mpl_host_device_pointer": (_I, [_P, C.POINTER(C.c_void_p)]),
     "mpl_score_topk_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
     "mpl_score_topk": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ, _P, _P, _P]),
     "mpl_merge_rows_workspace_bytes": (_SZ, [_I64, _I, _I64]),

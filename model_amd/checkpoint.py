@@ -151,7 +151,10 @@ def pool_params(tree: Dict[str, Any]) -> Dict[str, torch.Tensor]:
     loaded model tree (the module is named "pool", model.py:70-84)."""
     p = tree["params"] if "params" in tree and "pool" not in tree else tree
     pool = p["pool"]
-    return {"sub_keys": pool["sub_keys"], "values": pool["values"], "log_temperature": pool["log_temperature"]}
+    out = {"sub_keys": pool["sub_keys"], "log_temperature": pool["log_temperature"]}
+    if "values" in pool:  # absent with a host pool (memory.py:103-109)
+        out["values"] = pool["values"]
+    return out
 
 
 def _ndarray_bytes(arr: np.ndarray) -> bytes:

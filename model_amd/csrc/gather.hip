@@ -155,9 +155,86 @@ static int gather_impl(const V* values, int64_t N, int d, const int32_t* slots, 
   return check_launch("mpl_gather_wsum(generic)");
 }
 
+// Row copy for the host tier: out[i] = table[clamp(idx[i])] for i < rows,
+// rows = min(count, *count_dev) (count_dev may be null).  The table may be
+// device memory or pinned host memory mapped for the device, in which case
+// every 16-byte vector crosses the bus once; kUnroll vectors per thread are
+// loaded before any is stored, so several reads are in flight per lane.
+constexpr int kRowCopyUnroll = 4;
+
+template <int W>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const uint32_t* __restrict__ table, int64_t N, int wpr,
+                                                          const int32_t* __restrict__ idx, int64_t count,
+                                                          const int32_t* __restrict__ count_dev,
+                                                          uint32_t* __restrict__ out) {
+  // W 32-bit words per access (4: 16-byte vectors); wpr accesses per row
+  typedef uint32_t Acc __attribute__((ext_vector_type(W)));
+  const int64_t rows = count_dev != nullptr ? min(count, (int64_t)*count_dev) : count;
+  const int64_t total = rows * wpr;
+  const int64_t stride = (int64_t)gridDim.x * 256 * kRowCopyUnroll;
+  for (int64_t t0 = (int64_t)blockIdx.x * 256 * kRowCopyUnroll + threadIdx.x; t0 < total; t0 += stride) {
+    Acc v[kRowCopyUnroll];
+    int64_t dst[kRowCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kRowCopyUnroll; ++u) {
+      const int64_t t = t0 + (int64_t)u * 256;
+      const bool ok = t < total;
+      const int64_t r = ok ? t / wpr : 0;
+      const int c = ok ? (int)(t - r * wpr) : 0;
+      int64_t sl = idx[r];
+      sl = sl < 0 ? 0 : (sl >= N ? N - 1 : sl);
+      v[u] = ((const Acc*)table)[sl * wpr + c];
+      dst[u] = ok ? t : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowCopyUnroll; ++u)
+      if (dst[u] >= 0) ((Acc*)out)[dst[u]] = v[u];
+  }
+}
+
 }  // namespace mpl
 
 using namespace mpl;
+
+extern "C" int mpl_gather_rows(const void* table, int dtype, int64_t N, int d, const int32_t* idx, int64_t count,
+                               const int32_t* count_dev, void* out, void* stream) {
+  clear_error();
+  MPL_REQUIRE(N > 0 && d > 0 && count >= 0, MPL_EINVAL, "mpl_gather_rows: bad sizes N=%lld d=%d count=%lld",
+              (long long)N, d, (long long)count);
+  MPL_REQUIRE(dtype == MPL_F16 || dtype == MPL_F32, MPL_EINVAL, "mpl_gather_rows: dtype must be MPL_F16 or MPL_F32");
+  if (count == 0) return MPL_OK;
+  MPL_REQUIRE(table && idx && out, MPL_EINVAL, "mpl_gather_rows: null buffer");
+  const int64_t row_bytes = (int64_t)d * (dtype == MPL_F16 ? 2 : 4);
+  MPL_REQUIRE(row_bytes % 4 == 0, MPL_EUNSUPPORTED, "mpl_gather_rows: rows of %lld bytes (need a multiple of 4)",
+              (long long)row_bytes);
+  hipStream_t s = (hipStream_t)stream;
+  const bool vec = row_bytes % 16 == 0 && ((uintptr_t)table % 16) == 0 && ((uintptr_t)out % 16) == 0;
+  const int wpr = (int)(vec ? row_bytes / 16 : row_bytes / 4);
+  const int64_t work = cdiv(count * wpr, 256 * kRowCopyUnroll);
+  const unsigned blocks = (unsigned)(work < 4096 ? (work > 0 ? work : 1) : 4096);
+  if (vec)
+    gather_rows_kernel<4><<<blocks, 256, 0, s>>>((const uint32_t*)table, N, wpr, idx, count, count_dev,
+                                                 (uint32_t*)out);
+  else
+    gather_rows_kernel<1><<<blocks, 256, 0, s>>>((const uint32_t*)table, N, wpr, idx, count, count_dev,
+                                                 (uint32_t*)out);
+  return check_launch("mpl_gather_rows");
+}
+
+extern "C" int mpl_host_device_pointer(void* host_ptr, void** dev_ptr) {
+  clear_error();
+  MPL_REQUIRE(host_ptr && dev_ptr, MPL_EINVAL, "mpl_host_device_pointer: null argument");
+  void* p = nullptr;
+  const hipError_t e = hipHostGetDevicePointer(&p, host_ptr, 0);
+  // the failed query is reported here; clear HIP's sticky per-thread error,
+  // or the caller's next launch check would report it again
+  if (e != hipSuccess) (void)hipGetLastError();
+  MPL_REQUIRE(e == hipSuccess && p != nullptr, MPL_EINVAL,
+              "mpl_host_device_pointer: %p is not pinned host memory mapped for the device (%s)", host_ptr,
+              hipGetErrorString(e));
+  *dev_ptr = p;
+  return MPL_OK;
+}
 
 extern "C" int mpl_gather_wsum(const void* values, int values_dtype, int64_t N, int d, const int32_t* slots,
                                const float* weights, int64_t M, int R, int shuffle_reads, float* out,

@@ -150,8 +150,6 @@ class MemoryPool:
                  score_dtype: Optional[torch.dtype] = None):
         assert d_key % 2 == 0, "d_key must be even (split into two halves)"  # memory.py:95
         assert top_k <= n_sub_keys  # memory.py:96
-        if host_pool:
-            raise NotImplementedError("host_pool (host_pool.py) is outside this library's scope")
         self.n_sub_keys, self.heads, self.d_key, self.d_value, self.top_k = n_sub_keys, heads, d_key, d_value, top_k
         self.routing_noise = routing_noise
         self.init_temperature = init_temperature
@@ -184,17 +182,21 @@ class MemoryPool:
         """memory.py:94-113: sub_keys on the unit sphere, values ~ N(0, d^-1/2),
         log_temperature = log(init_temperature).  ``rng`` is a seed or a
         torch.Generator on ``device``.  ``values`` [n*n, d_value] may be given
-        (e.g. a table filled in place) instead of a fresh draw."""
+        (e.g. a table filled in place) instead of a fresh draw.  With a host
+        pool there is no values parameter (memory.py:103-109): the table is
+        the named HostPool (model_amd/host_pool.py)."""
         g = rng if isinstance(rng, torch.Generator) else torch.Generator(device=device).manual_seed(int(rng))
         H, n, half = self.heads, self.n_sub_keys, self.d_key // 2
         keys = torch.randn((H, 2, n, half), generator=g, device=device, dtype=torch.float32)
         keys = keys * torch.rsqrt((keys * keys).sum(-1, keepdim=True) + NORM_EPS)
+        log_t = torch.tensor(math.log(self.init_temperature), dtype=torch.float32, device=device)
+        if self.host_pool:
+            return {"params": {"sub_keys": keys, "log_temperature": log_t}}
         if values is None:
             values = torch.randn((self.pool_size, self.d_value), generator=g, device=device, dtype=self.values_dtype)
             values.mul_(self.d_value ** -0.5)
         elif tuple(values.shape) != (self.pool_size, self.d_value):
             raise ValueError(f"values must be [{self.pool_size}, {self.d_value}], got {tuple(values.shape)}")
-        log_t = torch.tensor(math.log(self.init_temperature), dtype=torch.float32, device=device)
         return {"params": {"sub_keys": keys, "values": values, "log_temperature": log_t}}
 
     def temperature(self, log_temperature: torch.Tensor) -> float:
@@ -275,13 +277,27 @@ class MemoryPool:
                                  ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
               "mpl_score_select")
 
-        values = params["values"]
-        if values.dtype not in (torch.float16, torch.float32) or not values.is_contiguous():
-            raise TypeError("values must be a contiguous float16/float32 [n*n, d_value] tensor")
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
-        check(L.mpl_gather_wsum(ptr(values), _dtype_code(values.dtype), self.pool_size, d, ptr(slots),
-                                ptr(weights), M, H * k, int(bool(shuffle_reads)), ptr(out), stream),
-              "mpl_gather_wsum")
+        staged = None
+        if self.host_pool:
+            # memory.py:182-183 (hp.fetch): the unique rows cross the host
+            # link once into device memory; the weighted sum reads them there
+            from . import host_pool as hp
+            read = slots
+            if shuffle_reads:  # memory.py:179
+                N = self.pool_size
+                read = ((slots.long() + N // 2 + 1) % N).to(torch.int32)
+            rows, inverse, _ = hp.get(self.host_pool).stage(read)
+            staged = (rows, inverse.reshape(M, H, k))
+            check(L.mpl_gather_wsum(ptr(rows), _dtype_code(rows.dtype), max(rows.shape[0], 1), d, ptr(staged[1]),
+                                    ptr(weights), M, H * k, 0, ptr(out), stream), "mpl_gather_wsum")
+        else:
+            values = params["values"]
+            if values.dtype not in (torch.float16, torch.float32) or not values.is_contiguous():
+                raise TypeError("values must be a contiguous float16/float32 [n*n, d_value] tensor")
+            check(L.mpl_gather_wsum(ptr(values), _dtype_code(values.dtype), self.pool_size, d, ptr(slots),
+                                    ptr(weights), M, H * k, int(bool(shuffle_reads)), ptr(out), stream),
+                  "mpl_gather_wsum")
 
         noisy = gumbel is not None
         res = _Result()
@@ -298,7 +314,7 @@ class MemoryPool:
         res.update({
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
             "k_hat": k_hat, "packed": packed, "score_code": score_code, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
-            "flat_idx": flat_idx, "slots": slots, "weights": weights, "gumbel": gumbel,
+            "flat_idx": flat_idx, "slots": slots, "weights": weights, "gumbel": gumbel, "staged": staged,
             "noise_coef": noise_coef,
         })
         return res
@@ -451,7 +467,7 @@ def _needs_grad(params, queries, sparse_grad) -> bool:
     if not torch.is_grad_enabled():
         return False
     ts = [queries, params["sub_keys"], params["log_temperature"]]
-    if not sparse_grad:
+    if not sparse_grad and "values" in params:
         ts.append(params["values"])
     return any(isinstance(t, torch.Tensor) and t.requires_grad for t in ts)
 
@@ -498,10 +514,15 @@ class _LookupFunction(torch.autograd.Function):
         # route: dw, softmax backward, scatter to the stage-1 ranks
         d_sub = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
         dlogt_part = torch.empty(max(M, 1), dtype=torch.float32, device=dev)
-        vals = values.detach()
-        check(L.mpl_lookup_bwd_route(ptr(g_out), ptr(vals), _dtype_code(vals.dtype), pool.pool_size, d,
-                                     ptr(res["slots"]), ptr(res["weights"]), ptr(res["flat_idx"]),
-                                     ptr(res["sub_scores"]), M, H, k, int(bool(opts["shuffle_reads"])), None,
+        if res["staged"] is not None:  # host pool: the staged unique rows, indexed by inverse
+            vals, vslots = res["staged"]
+            vN, vshuffle = max(vals.shape[0], 1), 0
+        else:
+            vals, vslots = values.detach(), res["slots"]
+            vN, vshuffle = pool.pool_size, int(bool(opts["shuffle_reads"]))
+        check(L.mpl_lookup_bwd_route(ptr(g_out), ptr(vals), _dtype_code(vals.dtype), vN, d,
+                                     ptr(vslots), ptr(res["weights"]), ptr(res["flat_idx"]),
+                                     ptr(res["sub_scores"]), M, H, k, vshuffle, None,
                                      ptr(d_sub), ptr(dlogt_part), stream), "mpl_lookup_bwd_route")
 
         # dense over n: the balance loss (memory.py:208-213) and, with fp16
@@ -584,8 +605,11 @@ class _LookupFunction(torch.autograd.Function):
 def _lookup_with_grad(pool, params, queries, *, train, sparse_grad, noise_scale, shuffle_reads, rngs):
     opts = {"train": train, "sparse_grad": sparse_grad, "noise_scale": noise_scale,
             "shuffle_reads": shuffle_reads, "rngs": rngs}
+    if pool.host_pool and not sparse_grad:
+        raise ValueError("a host pool is updated sparsely: call with sparse_grad=True (train.py:214-215)")
+    values = params["values"] if "values" in params else params["sub_keys"].new_empty(0)
     out, balance = _LookupFunction.apply(queries, params["sub_keys"], params["log_temperature"],
-                                         params["values"], pool, opts)
+                                         values, pool, opts)
     aux = opts.pop("_aux")
     dict.__setitem__(aux, "balance_loss", balance)  # the autograd-tracked copy
     return out.reshape(*tuple(queries.shape[:-2]), pool.d_value), aux

@@ -61,6 +61,7 @@ class ModelConfig:
     balance_temperature_grad: bool = False
     max_temperature: float = 100.0
     router_query_scale: bool = False
+    host_pool: str = ""  # config.py:33: name of a HostPool (model_amd/host_pool.py) holding the table
     values_dtype: torch.dtype = torch.float16  # the pool table in HBM (fp32 in the reference)
 
     @property
@@ -129,7 +130,7 @@ class MemoryPoolLM:
                                    min_temperature=cfg.min_temperature,
                                    balance_temperature_grad=cfg.balance_temperature_grad,
                                    max_temperature=cfg.max_temperature, query_scale=cfg.router_query_scale,
-                                   values_dtype=cfg.values_dtype)
+                                   host_pool=cfg.host_pool, values_dtype=cfg.values_dtype)
 
     # ------------------------------------------------------------ params
     def init(self, seed: int = 0, device="cuda", pool_values: Optional[torch.Tensor] = None) -> Dict[str, Any]:

@@ -171,17 +171,28 @@ class SparseRowUpdate:
 
     Holds the pool optimizer state: ``acc`` [N] (row-wise Adagrad, the
     default ``pool_optimizer``) or ``m``, ``v`` [N, d] (lazy Adam), and an
-    optional fp32 ``master`` copy of an fp16 table."""
+    optional fp32 ``master`` copy of an fp16 table.  ``values`` may instead
+    be a HostPool (model_amd/host_pool.py; train.py:210-221, 250-258): the
+    pool then keeps its own optimizer state and receives the merged, clipped
+    rows with the 1-based step."""
 
-    def __init__(self, values: torch.Tensor, *, optimizer: str = "rowwise_adagrad", lr: float = 3e-4,
+    def __init__(self, values, *, optimizer: str = "rowwise_adagrad", lr: float = 3e-4,
                  pool_lr_mult: float = 3.0, warmup_steps: int = 0, steps: int = 1, grad_clip: float = 1.0,
                  master: bool = True):
         if optimizer not in ("rowwise_adagrad", "adam"):
             raise ValueError(f"unknown pool optimizer {optimizer!r}")
-        self.values = values
         self.optimizer = optimizer
         self.lr, self.pool_lr_mult = lr, pool_lr_mult
         self.warmup_steps, self.steps, self.grad_clip = warmup_steps, steps, grad_clip
+        self.step = 0
+        self.host = None
+        if not isinstance(values, torch.Tensor):  # a HostPool
+            if values.optimizer != optimizer:
+                raise ValueError(f"host pool optimizer {values.optimizer!r} != {optimizer!r}")
+            self.host, self.values = values, None
+            self.master = self.acc = self.m = self.v = None
+            return
+        self.values = values
         N, d = values.shape
         dev = values.device
         self.master = values.float().clone() if (master and values.dtype != torch.float32) else None
@@ -196,12 +207,14 @@ class SparseRowUpdate:
 
     def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
                  rest_sq: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
-        N = self.values.shape[0]
+        N = self.host.n_slots if self.host is not None else self.values.shape[0]
         merged = fetched_row_grads_full(aux, probe_grads, layers, N, zero_padding=False)  # optimizers skip padding
         sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip)
         lr = warmup_cosine(self.step, self.lr, self.warmup_steps, self.steps) * self.pool_lr_mult
         scale = sg[0:1]
-        if self.optimizer == "rowwise_adagrad":
+        if self.host is not None:
+            self.host.update(merged.uniq, merged.rows, self.step + 1, lr, grad_scale=scale)
+        elif self.optimizer == "rowwise_adagrad":
             rowwise_adagrad(self.values, self.acc, merged.uniq, merged.rows, lr, self.master, scale)
         else:
             lazy_adam(self.values, self.m, self.v, merged.uniq, merged.rows, lr, self.step, self.master, scale)
