@@ -25,7 +25,12 @@ Also reported in the same JSON line:
     streams, 128-token prompts, 256 new tokens, every position one
     HIP-graph decode step.
 
+  * ``host_pool_1M``: the host tier (host_pool.py): the text-study lookup
+    (8,192 tokens) on a 1,048,576-slot fp16 table in pinned host memory,
+    the unique rows copied across the host link by the GPU each step.
+
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-large] [--no-train] [--no-generate]
+                       [--no-host]
 """
 
 from __future__ import annotations
@@ -58,6 +63,7 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-generate", action="store_true")
+    ap.add_argument("--no-host", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -374,6 +380,51 @@ def key_diversity_bench(torch, iters):
             "ms": ms, "achieved_tflops": tf, "peak_tflops": MFMA_F16_PEAK_TFLOPS, "frac": tf / MFMA_F16_PEAK_TFLOPS}
 
 
+def host_pool_bench(torch, iters):
+    """The lookup with the value table in pinned host memory (host_pool.py,
+    RAM mode): select on the GPU, then the unique rows cross the host link
+    once (mpl_unique_slots + mpl_gather_rows reading the pinned table) and
+    the weighted sum runs on the staged rows."""
+    from model_amd import _lib
+    from model_amd import host_pool as hp
+
+    L = _lib.lib()
+    M, H, n, d_key, d, k = 8192, 4, 1024, 256, 256, 16
+    N = n * n
+    pool = hp.HostPool(N, d, dtype=np.float16, seed=0, trainable=False)
+    lk = Lookup(torch, L, M=M, H=H, n=n, d_key=d_key, d=d, k=k, seed=0,
+                values=torch.empty((16, d), dtype=torch.float16, device="cuda"))
+    lk.pack()
+    lk.select()
+    staged = {}
+
+    def stage():
+        staged["rows"], staged["inv"], staged["num"] = pool.stage(lk.slots)
+
+    def read():
+        _lib.check(L.mpl_gather_wsum(_lib.ptr(staged["rows"]), _lib.MPL_F16, staged["rows"].shape[0], d,
+                                     _lib.ptr(staged["inv"]), _lib.ptr(lk.weights), M, H * k, 0, _lib.ptr(lk.out),
+                                     lk.stream), "gather")
+
+    def step():
+        lk.pack()
+        lk.select()
+        stage()
+        read()
+
+    stage()
+    torch.cuda.synchronize()
+    U = int(staged["num"].item())
+    t_stage = time_loop(torch, stage, iters, 2)
+    t_step = time_loop(torch, step, iters, 2)
+    link = U * d * 2 / (t_stage * 1e-3) / 1e9
+    del pool
+    return {"workload": "text-study lookup (8,192 tokens, H=4, k=16) on a 1,048,576-slot fp16 table in pinned "
+                        "host memory (RAM mode of the host tier)",
+            "unique_rows": U, "stage_ms": t_stage, "host_link_GBs": link, "ms_per_step": t_step,
+            "tokens_per_s": M / (t_step * 1e-3)}
+
+
 def generation_bench(torch):
     """Batched greedy generation through the backbone mirror
     (model_amd/model.py, generate.py) with two memory layers on a
@@ -492,6 +543,7 @@ def main():
         div = key_diversity_bench(torch, max(5, args.steps // 20))
 
     generation = None if args.no_generate else generation_bench(torch)
+    host = None if args.no_host else host_pool_bench(torch, max(5, args.steps // 20))
 
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
@@ -517,6 +569,7 @@ def main():
         "training_262k": train,
         "key_diversity_67M": div,
         "generation_268M": generation,
+        "host_pool_1M": host,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))
