@@ -391,7 +391,7 @@ def host_pool_bench(torch, iters):
     L = _lib.lib()
     M, H, n, d_key, d, k = 8192, 4, 1024, 256, 256, 16
     N = n * n
-    pool = hp.HostPool(N, d, dtype=np.float16, seed=0, trainable=False)
+    pool = hp.HostPool(N, d, dtype=np.float16, seed=0, optimizer="rowwise_adagrad")
     lk = Lookup(torch, L, M=M, H=H, n=n, d_key=d_key, d=d, k=k, seed=0,
                 values=torch.empty((16, d), dtype=torch.float16, device="cuda"))
     lk.pack()
@@ -418,11 +418,20 @@ def host_pool_bench(torch, iters):
     t_stage = time_loop(torch, stage, iters, 2)
     t_step = time_loop(torch, step, iters, 2)
     link = U * d * 2 / (t_stage * 1e-3) / 1e9
+    # the host tier's training step: row-wise Adagrad of the U touched rows,
+    # in place on the pinned table (train.py:250-258 -> host_pool.py:143-152)
+    flat = lk.slots.reshape(-1)
+    uniq = torch.unique(flat).to(torch.int32)
+    grads = torch.randn((uniq.numel(), d), device="cuda") * 1e-3
+    t_upd = time_loop(torch, lambda: pool.update(uniq, grads, 1, 1e-3), iters, 2)
+    upd_bytes = uniq.numel() * (2 * d * 2 + 2 * 4)  # fp16 row read + write, acc read + write, across the link
     del pool
     return {"workload": "text-study lookup (8,192 tokens, H=4, k=16) on a 1,048,576-slot fp16 table in pinned "
-                        "host memory (RAM mode of the host tier)",
+                        "host memory (RAM mode of the host tier), and the row-wise Adagrad step of the touched rows",
             "unique_rows": U, "stage_ms": t_stage, "host_link_GBs": link, "ms_per_step": t_step,
-            "tokens_per_s": M / (t_step * 1e-3)}
+            "tokens_per_s": M / (t_step * 1e-3),
+            "update_ms": t_upd, "update_rows_per_s": uniq.numel() / (t_upd * 1e-3),
+            "update_link_GBs": upd_bytes / (t_upd * 1e-3) / 1e9}
 
 
 def generation_bench(torch):
