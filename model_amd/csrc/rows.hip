@@ -212,12 +212,15 @@ __global__ __launch_bounds__(kSortThreads) void seg_count_kernel(const uint32_t*
 }
 
 // Segment u starts at sorted position seg_start[u] and has slot uniq[u];
-// seg_of[i] is the segment of position i.
+// seg_of[i] is the segment of position i.  Segment ids are clamped to
+// cap - 1 (the capacity of uniq / seg_start): only ids outside
+// [0, pool_size) can make more distinct values than that, and they then get
+// wrong results, never out-of-bounds writes.
 __global__ __launch_bounds__(kSortThreads) void seg_write_kernel(const uint32_t* __restrict__ s, int64_t n,
                                                                   const uint32_t* __restrict__ tile_base,
                                                                   int32_t* __restrict__ uniq,
                                                                   int32_t* __restrict__ seg_start,
-                                                                  int32_t* __restrict__ seg_of) {
+                                                                  int32_t* __restrict__ seg_of, int64_t cap) {
   __shared__ uint32_t wave_cnt[kSortThreads / kWave];
   __shared__ uint32_t seen;
   const int tid = threadIdx.x;
@@ -238,7 +241,7 @@ __global__ __launch_bounds__(kSortThreads) void seg_write_kernel(const uint32_t*
     // inclusive count of heads up to this lane, minus one
     const uint32_t incl = before + (uint32_t)__popcll(heads & (lanes_below(lane) | (1ull << lane)));
     if (valid) {
-      const uint32_t u = tb + incl - 1u;
+      const uint32_t u = (uint32_t)min((int64_t)(tb + incl - 1u), cap - 1);
       seg_of[i] = (int32_t)u;
       if (head) {
         uniq[u] = (int32_t)s[i];
@@ -500,8 +503,8 @@ __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* _
 }
 
 __global__ void seg_finish_kernel(const uint32_t* __restrict__ num_seg, int64_t n, int32_t* __restrict__ seg_start,
-                                  int32_t* __restrict__ num_unique) {
-  const uint32_t U = *num_seg;
+                                  int32_t* __restrict__ num_unique, int64_t cap) {
+  const uint32_t U = (uint32_t)min((int64_t)*num_seg, cap);
   seg_start[U] = (int32_t)n;
   *num_unique = (int32_t)U;
 }
@@ -851,8 +854,8 @@ static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayou
   }
   seg_count_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt);
   scan_exclusive_kernel<<<1, 1024, 0, s>>>(tile_cnt, L.ntiles, nseg);
-  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of);
-  seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique);
+  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of, L.cap);
+  seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique, L.cap);
   return Segments{vin, seg_start, seg_of, nseg};
 }
 

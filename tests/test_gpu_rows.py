@@ -89,6 +89,18 @@ def test_merge_empty(gpu_lib):
     assert m.uniq.shape[0] == 0 and int(m.num_unique.cpu()[0]) == 0
 
 
+def test_merge_tolerates_out_of_range_ids(gpu_lib):
+    """Ids outside [0, pool_size) (a caller's bug) give wrong rows but stay
+    inside the [cap] outputs: more fetches than slots, so more distinct ids
+    than cap can exist."""
+    P, N, d = 4096, 64, 16
+    bad = torch.as_tensor(np.random.default_rng(0).integers(-5, 6 * N, P).astype(np.int32), device="cuda")
+    m = R.merge_fetches(bad, None, torch.ones((P, d), device="cuda"), N)
+    torch.cuda.synchronize()
+    assert m.uniq.shape[0] == N and 0 < int(m.num_unique.cpu()[0]) <= N
+    assert torch.isfinite(m.rows).all()
+
+
 def test_merge_zipf_training_shape(gpu_lib):
     """8,192 tokens x 4 heads x 16 fetches = 524,288 Zipf(1.1) fetches over
     262,144 slots, d=256: exact distinct-slot set, column sums (linearity:
