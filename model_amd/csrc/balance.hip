@@ -54,6 +54,18 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ x, i
   for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0.f;
 }
 
+// Three buffers cleared by one launch (null ones skipped): the count
+// outputs, which every launch of the count kernel needs at zero.
+__global__ __launch_bounds__(256) void fill_zero3_kernel(float* __restrict__ a, int64_t na, float* __restrict__ b,
+                                                         int64_t nb, float* __restrict__ c, int64_t nc) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < na + nb + nc; i += stride) {
+    if (i < na) a[i] = 0.f;
+    else if (i < na + nb) b[i - na] = 0.f;
+    else c[i - na - nb] = 0.f;
+  }
+}
+
 // Workgroup b covers head h = b % H and tokens [t0, t0 + tpg).  With use_lds
 // the two sub-key histograms and the two clean histograms of head h ([4][n]
 // ints) are built in LDS and added to the outputs once per workgroup.  Ids
@@ -791,12 +803,19 @@ extern "C" int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_i
               "mpl_route_counts: clean_counts needs clean_sub_idx");
   hipStream_t s = (hipStream_t)stream;
   const int64_t hn = (int64_t)H * 2 * n;
-  if (subkey_counts) fill_zero_kernel<<<grid_for(hn, 256), 256, 0, s>>>(subkey_counts, hn);
-  if (clean_counts) fill_zero_kernel<<<grid_for(hn, 256), 256, 0, s>>>(clean_counts, hn);
-  if (slot_counts) fill_zero_kernel<<<grid_for((int64_t)n * n, 256), 256, 0, s>>>(slot_counts, (int64_t)n * n);
+  {
+    const int64_t na = subkey_counts ? hn : 0, nb = clean_counts ? hn : 0;
+    const int64_t nc = slot_counts ? (int64_t)n * n : 0;
+    if (na + nb + nc > 0)
+      fill_zero3_kernel<<<grid_for(na + nb + nc, 256), 256, 0, s>>>(subkey_counts, na, clean_counts, nb,
+                                                                     slot_counts, nc);
+  }
   if (M > 0 && (subkey_counts || clean_counts || slot_counts)) {
     const int use_lds = n <= 4096 ? 1 : 0;
-    int64_t tpg = use_lds ? cdiv(16 * (int64_t)n, 3 * (int64_t)k) : 32;
+    // tokens per workgroup with LDS histograms: the 4n-bin flush against
+    // the 3k ids per token, at 2n/k tokens (n = 512, k = 16: 64 tokens,
+    // 37.8 us against 41.6 us at 16n/3k for 8,192 tokens)
+    int64_t tpg = use_lds ? cdiv(2 * (int64_t)n, (int64_t)k) : 32;
     if (tpg < 64) tpg = 64;
     const int64_t min_tpg = cdiv(M * H, 2048);
     if (tpg < min_tpg) tpg = min_tpg;
