@@ -172,7 +172,12 @@ __device__ __forceinline__ float kth_of_32(const float* a, const float* b, int k
   return from_orderable(t);
 }
 
-template <typename T, int HP, bool NOISE, int KMAX, bool DIRECT>
+// SHORT (register path, no noise, splits of at most kShortBlocks blocks, the
+// decode-sized plans): each block is scored once and both passes read the
+// scores from the MFMA accumulators instead of reloading and re-scoring.
+constexpr int kShortBlocks = 4;
+
+template <typename T, int HP, bool NOISE, int KMAX, bool DIRECT, bool SHORT>
 __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {
   constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);  // 16-B vectors per lane per block
   constexpr int OPV = KeyPack<T>::kOpsPerVec;
@@ -370,9 +375,41 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     }
   };
 
+  static_assert(!SHORT || (DIRECT && !NOISE), "short splits score on the register path without noise");
+  f32x16 sacc[SHORT ? kShortBlocks : 1];
+  if constexpr (SHORT) {
+    // blocks b_begin + j (clamped to the split: past its end a block repeats
+    // the last one, which the passes skip or which leaves the maxima as
+    // they are); loads run two blocks ahead of the MFMAs
+    auto chain = [&](const uint4* u) __attribute__((always_inline)) {
+      f32x16 x = f32x16{};
+#pragma unroll
+      for (int v = 0; v < VPL; ++v)
+#pragma unroll
+        for (int e = 0; e < OPV; ++e) x = Mfma<T>::mma(Mfma<T>::from_vec(u[v], e), qop[v * OPV + e], x);
+      return x;
+    };
+    uint4 ua[VPL], ub[VPL];
+    gload(ua, b_begin);
+    gload(ub, min(b_begin + 1, b_end - 1));
+    sacc[0] = chain(ua);
+    gload(ua, min(b_begin + 2, b_end - 1));
+    sacc[SHORT ? 1 : 0] = chain(ub);
+    gload(ub, min(b_begin + 3, b_end - 1));
+    sacc[SHORT ? 2 : 0] = chain(ua);
+    sacc[SHORT ? 3 : 0] = chain(ub);
+  }
   auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
-    if constexpr (DIRECT) sweep_direct(bb, be, body);
-    else sweep_lds(bb, be, body);
+    if constexpr (SHORT) {
+      const GVec g{};
+      auto no_issue = [](int) {};
+#pragma unroll
+      for (int j = 0; j < kShortBlocks; ++j) body((bb + j) * 32, sacc[SHORT ? j : 0], g, j < be - bb, no_issue);
+    } else if constexpr (DIRECT) {
+      sweep_direct(bb, be, body);
+    } else {
+      sweep_lds(bb, be, body);
+    }
   };
 
   // Selection values of the lane's 16 keys of a block (padded keys -inf);
@@ -420,8 +457,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     for (int r = 0; r < 16; ++r) {
       issue_for(r, issue);
       const float v = raw ? c[r] : sv[r];
-      // Past the end (!active) c holds the split's last block again, whose
-      // scores are already in the maxima, so no test of `active` is needed.
+      // Past the end (!active) c holds a block of the split again (the last
+      // one, or with SHORT a block pass 2 scans anyway), so its maxima are
+      // still scores of this split's keys: no test of `active` is needed.
       ma[r] = max(ma[r], __float_as_int(v));
     }
     (void)active;
@@ -872,8 +910,14 @@ constexpr bool direct_keys() {
 }
 template <typename T, int HP, bool NOISE, int KMAX>
 static void launch_stage1(const ScoreParams& sp, int64_t blocks, hipStream_t s) {
-  score_topk_kernel<T, HP, NOISE, KMAX, direct_keys<T, HP, NOISE, KMAX>()>
-      <<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+  constexpr bool D = direct_keys<T, HP, NOISE, KMAX>();
+  if constexpr (D && !NOISE) {
+    if (sp.blk_per_split <= kShortBlocks) {
+      score_topk_kernel<T, HP, NOISE, KMAX, D, true><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+      return;
+    }
+  }
+  score_topk_kernel<T, HP, NOISE, KMAX, D, false><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
 }
 
 template <typename T, int HP>
