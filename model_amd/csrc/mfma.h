@@ -22,29 +22,32 @@ struct Mfma<_Float16> {
   }
   // B operand for chunk c: dims 16c + 8*(lane/32) + [0,8) of fp16 query row
   // q (fp16 scoring requires half % 8 == 0, so this is one aligned 16-byte
-  // load).  Unconditional and zeroed after: a guarded load compiles to a
-  // branch with its own wait, serialising every chunk.
+  // load).  The load is unconditional and lanes out of range are zeroed by a
+  // multiply with 0: a select of the loaded value is turned by the compiler
+  // into a branch around the load with its own wait, which serialises the
+  // chunks (one memory round trip each).  A lane out of range reads finite
+  // data of its own row (or row 0), so the product is 0.
   __device__ static Op load_q(const _Float16* q, bool valid, int half, int c, int lane) {
     const int d0 = 16 * c + 8 * (lane >> 5);
-    Op o = *(const half8*)(q + (d0 < half ? d0 : 0));
-#pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = (valid && d0 < half) ? o[i] : (_Float16)0.f;
-    return o;
+    const Op o = *(const half8*)(q + (d0 < half ? d0 : 0));
+    const _Float16 m = (valid && d0 < half) ? (_Float16)1.f : (_Float16)0.f;
+    return o * m;
   }
   __device__ static Op from_vec(uint4 u, int) { return __builtin_bit_cast(half8, u); }
   // Raw fp32 query dims 16c + 8*(lane/32) + [0,8): two aligned 16-byte loads,
-  // zeroed after when out of range; adds their squares to ss.
+  // zeroed when out of range by a multiply with 0 (as in load_q); adds their
+  // squares to ss.
   static constexpr int kQElems = 8;
   __device__ static void load_q_raw(const float* q, bool valid, int half, int c, int lane, float* x, float& ss) {
     const int d0 = 16 * c + 8 * (lane >> 5);
-    const bool ok = valid && d0 < half;
+    const float m = (valid && d0 < half) ? 1.f : 0.f;
     const float4* src = (const float4*)(q + (d0 < half ? d0 : 0));
     const float4 u = src[0], v = src[1];
     x[0] = u.x; x[1] = u.y; x[2] = u.z; x[3] = u.w;
     x[4] = v.x; x[5] = v.y; x[6] = v.z; x[7] = v.w;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      x[i] = ok ? x[i] : 0.f;
+      x[i] *= m;
       ss = fmaf(x[i], x[i], ss);
     }
   }
@@ -64,8 +67,7 @@ struct Mfma<float> {
   }
   __device__ static Op load_q(const float* q, bool valid, int half, int c, int lane) {
     const int d = 2 * c + (lane >> 5);
-    const float f = q[min(d, half - 1)];
-    return (valid && d < half) ? f : 0.f;
+    return q[min(d, half - 1)] * ((valid && d < half) ? 1.f : 0.f);
   }
   __device__ static Op from_vec(uint4 u, int e) {
     const unsigned w = e == 0 ? u.x : e == 1 ? u.y : e == 2 ? u.z : u.w;
@@ -74,8 +76,7 @@ struct Mfma<float> {
   static constexpr int kQElems = 1;
   __device__ static void load_q_raw(const float* q, bool valid, int half, int c, int lane, float* x, float& ss) {
     const int d = 2 * c + (lane >> 5);
-    const float f = q[min(d, half - 1)];
-    x[0] = (valid && d < half) ? f : 0.f;
+    x[0] = q[min(d, half - 1)] * ((valid && d < half) ? 1.f : 0.f);
     ss = fmaf(x[0], x[0], ss);
   }
   __device__ static Op scale_q(const float* x, float r) { return x[0] * r; }

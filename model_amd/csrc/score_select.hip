@@ -206,6 +206,26 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   // of each key block lane l scores keys 8*(r/4) + 4*par + r%4 (r < 16).
   const int64_t my_q = q0 + (lane & 31);
   const bool valid = my_q < p.M;
+
+  const uint4* kbase_ptr = p.packed + (int64_t)hc * p.nblk * TILE;
+  // The lane's VPL 16-byte vectors of key block blk (coalesced 1-KB loads).
+  auto gload = [&](uint4* dst, int blk) __attribute__((always_inline)) {
+    const uint4* src = kbase_ptr + (int64_t)blk * TILE + lane;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) dst[v] = src[v * kWave];
+  };
+  // SHORT: the split's blocks b_begin + j (clamped to the split, so past its
+  // end a block repeats the last one) are all requested here, before the
+  // query, so that keys and query arrive in one memory round trip; the
+  // scheduling barrier keeps the compiler from moving the loads down to
+  // their uses.
+  uint4 kv[SHORT ? kShortBlocks : 1][SHORT ? VPL : 1];
+  if constexpr (SHORT) {
+#pragma unroll
+    for (int j = 0; j < kShortBlocks; ++j) gload(kv[j], min(b_begin + j, b_end - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+
   Op qop[NCH];
   float ql = 1.f;
   if (p.query_mode == MPL_Q_NORMALIZED) {
@@ -246,7 +266,6 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   typedef float GVec __attribute__((ext_vector_type(NOISE ? 16 : 1)));
   constexpr int LPW = VPL >= WAVES ? VPL / WAVES : 1;
   static_assert(VPL < WAVES || VPL % WAVES == 0, "tile vectors must split over the waves");
-  const uint4* kbase_ptr = p.packed + (int64_t)hc * p.nblk * TILE;
   auto dma = [&](uint4* dst, int blk) __attribute__((always_inline)) {
     const uint4* src = kbase_ptr + (int64_t)blk * TILE;
 #pragma unroll
@@ -283,16 +302,11 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     return g;
   };
   // Register path (DIRECT): each wave loads its own A operand of block blk
-  // into registers, VPL coalesced 1-KB loads, while the MFMAs of the block
-  // before it run; no LDS tiles and no barriers.  Iteration j issues the
-  // loads of block j+2 into the registers of block j (whose MFMAs were issued
-  // in iteration j-1), then waits for block j+1, issued one iteration
-  // earlier (loads complete in order).
-  auto gload = [&](uint4* dst, int blk) __attribute__((always_inline)) {
-    const uint4* src = kbase_ptr + (int64_t)blk * TILE + lane;
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) dst[v] = src[v * kWave];
-  };
+  // into registers (gload) while the MFMAs of the block before it run; no
+  // LDS tiles and no barriers.  Iteration j issues the loads of block j+2
+  // into the registers of block j (whose MFMAs were issued in iteration
+  // j-1), then waits for block j+1, issued one iteration earlier (loads
+  // complete in order).
   auto sweep_direct = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
     const int nb = be - bb;
     if (nb <= 0) return;
@@ -378,26 +392,19 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   static_assert(!SHORT || (DIRECT && !NOISE), "short splits score on the register path without noise");
   f32x16 sacc[SHORT ? kShortBlocks : 1];
   if constexpr (SHORT) {
-    // blocks b_begin + j (clamped to the split: past its end a block repeats
-    // the last one, which the passes skip or which leaves the maxima as
-    // they are); loads run two blocks ahead of the MFMAs
-    auto chain = [&](const uint4* u) __attribute__((always_inline)) {
+    // the scores of the blocks loaded at kernel start (past the split's end a
+    // block repeats the last one, which the passes skip or which leaves the
+    // maxima as they are)
+#pragma unroll
+    for (int j = 0; j < kShortBlocks; ++j) {
       f32x16 x = f32x16{};
 #pragma unroll
       for (int v = 0; v < VPL; ++v)
 #pragma unroll
-        for (int e = 0; e < OPV; ++e) x = Mfma<T>::mma(Mfma<T>::from_vec(u[v], e), qop[v * OPV + e], x);
-      return x;
-    };
-    uint4 ua[VPL], ub[VPL];
-    gload(ua, b_begin);
-    gload(ub, min(b_begin + 1, b_end - 1));
-    sacc[0] = chain(ua);
-    gload(ua, min(b_begin + 2, b_end - 1));
-    sacc[SHORT ? 1 : 0] = chain(ub);
-    gload(ub, min(b_begin + 3, b_end - 1));
-    sacc[SHORT ? 2 : 0] = chain(ua);
-    sacc[SHORT ? 3 : 0] = chain(ub);
+        for (int e = 0; e < OPV; ++e)
+          x = Mfma<T>::mma(Mfma<T>::from_vec(kv[SHORT ? j : 0][SHORT ? v : 0], e), qop[v * OPV + e], x);
+      sacc[SHORT ? j : 0] = x;
+    }
   }
   auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
     if constexpr (SHORT) {
@@ -557,6 +564,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
 // ----------------------------------------------------------------- stage 2
 // Stage-1 results arrive as "lists": sel / clean / idx arrays in the layout
 // [split][M][hc][k] (sel absent without noise, where it equals clean).
+// Ties each loaded list entry to a register at this point.  A value used
+// only under a condition (an entry kept only when its id is valid) is
+// otherwise loaded inside a branch with a wait of its own, after the other
+// loads have returned: a second memory round trip.
+template <int N>
+__device__ __forceinline__ void pin_loaded(int (&id)[N], float (&sl)[N], float (&cc)[N]) {
+#pragma unroll
+  for (int t = 0; t < N; ++t) asm volatile("" ::"v"(id[t]), "v"(sl[t]), "v"(cc[t]));
+}
+
 struct PairParams {
   const float* sel;
   const float* clean;
@@ -690,46 +707,62 @@ __global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
   const int HC = 2 * p.H;
   const float* lsel = p.sel != nullptr ? p.sel : p.clean;
 
+  // The two codebooks' lists (dead rows read row 0 and enter as empty keys,
+  // whose payload is never output).  Both codebooks' entries of a batch of
+  // lists are requested before the first merge: one memory round trip per
+  // batch, and with one list no merge at all.
   u64 lk[2];
   float lc[2];
+  int64_t o0[2];
 #pragma unroll
-  for (int c = 0; c < 2; ++c) {
-    const int hc = 2 * h + c;
-    const int64_t o0 = ((int64_t)m * HC + hc) * K + r;
+  for (int c = 0; c < 2; ++c) o0[c] = ((int64_t)m * HC + 2 * h + c) * K + r;
+  if (p.S == 1) {
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      int id[1] = {p.idx[o0[c]]};
+      float sl[1] = {lsel[o0[c]]}, cc[1] = {p.clean[o0[c]]};
+      pin_loaded(id, sl, cc);
+      lc[c] = cc[0];
+      lk[c] = (live && id[0] >= 0) ? make_key(sl[0], id[0]) : 0ull;
+    }
+  } else {
+    constexpr int B = 8;
     const int64_t sstride = p.M * HC * K;
-    u64 acc = 0;
-    float pay = 0.f;
-    for (int s0 = 0; s0 < p.S; s0 += 4) {
-      int id[4];
-      float sl[4], cc[4];
+    for (int s0 = 0; s0 < p.S; s0 += B) {
+      int id[2][B];
+      float sl[2][B], cc[2][B];
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int64_t o = (int64_t)min(s0 + t, p.S - 1) * sstride + o0;  // clamped, unconditional
-        id[t] = p.idx[o];
-        sl[t] = lsel[o];
-        cc[t] = p.clean[o];
-      }
+      for (int c = 0; c < 2; ++c)
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        if (s0 + t < p.S) {  // uniform
-          const int i = live ? id[t] : -1;
-          const u64 kk = i >= 0 ? make_key(sl[t], i) : 0ull;
-          const float pc = live ? cc[t] : 0.f;
-          if (s0 + t == 0) {
-            acc = kk;
-            pay = pc;
-          } else {
-            g16::merge(acc, pay, kk, pc, r);
+        for (int t = 0; t < B; ++t) {
+          const int64_t o = (int64_t)min(s0 + t, p.S - 1) * sstride + o0[c];  // clamped, unconditional
+          id[c][t] = p.idx[o];
+          sl[c][t] = lsel[o];
+          cc[c][t] = p.clean[o];
+        }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) pin_loaded(id[c], sl[c], cc[c]);
+#pragma unroll
+      for (int c = 0; c < 2; ++c)
+#pragma unroll
+        for (int t = 0; t < B; ++t) {
+          if (s0 + t < p.S) {  // uniform
+            const u64 kk = (live && id[c][t] >= 0) ? make_key(sl[c][t], id[c][t]) : 0ull;
+            if (s0 + t == 0) {
+              lk[c] = kk;
+              lc[c] = cc[c][t];
+            } else {
+              g16::merge(lk[c], lc[c], kk, cc[c][t], r);
+            }
           }
         }
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+      if (live) {
+        p.sub_idx[o0[c]] = lk[c] ? key_index(lk[c]) : -1;
+        p.sub_scores[o0[c]] = lk[c] ? lc[c] : -INFINITY;
       }
-    }
-    lk[c] = acc;
-    lc[c] = pay;
-    if (p.S > 1 && live) {
-      p.sub_idx[o0] = acc ? key_index(acc) : -1;
-      p.sub_scores[o0] = acc ? pay : -INFINITY;
-    }
   }
   const bool a_ok = lk[0] != 0ull, b_ok = lk[1] != 0ull;
   const float a_sel = a_ok ? key_score(lk[0]) : -INFINITY;
@@ -812,30 +845,31 @@ __global__ __launch_bounds__(256) void merge_splits_k16(MergeParams p) {
   const int s2 = live ? (int)(g / p.rows) : 0;
   const float* lsel = p.sel != nullptr ? p.sel : p.clean;
   const int64_t sstride = p.rows * K;
+  // All lists of the chunk are requested before the first merge (one memory
+  // round trip).  Lists past p.S read the last list again and enter as empty
+  // keys; an empty key's payload is never output, so it is passed as loaded.
+  int id[kMergeChunk];
+  float sl[kMergeChunk], cc[kMergeChunk];
+#pragma unroll
+  for (int t = 0; t < kMergeChunk; ++t) {
+    const int s = min(s2 * kMergeChunk + t, p.S - 1);  // clamped, unconditional
+    const int64_t o = (int64_t)s * sstride + row * K + r;
+    id[t] = p.idx[o];
+    sl[t] = lsel[o];
+    cc[t] = p.clean[o];
+  }
+  pin_loaded(id, sl, cc);
   u64 acc = 0;
   float pay = 0.f;
 #pragma unroll
-  for (int t0 = 0; t0 < kMergeChunk; t0 += 4) {
-    int id[4];
-    float sl[4], cc[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const int s = min(s2 * kMergeChunk + t0 + t, p.S - 1);  // clamped, unconditional
-      const int64_t o = (int64_t)s * sstride + row * K + r;
-      id[t] = p.idx[o];
-      sl[t] = lsel[o];
-      cc[t] = p.clean[o];
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      const bool in = s2 * kMergeChunk + t0 + t < p.S;  // uniform per row
-      const u64 kk = (in && id[t] >= 0) ? make_key(sl[t], id[t]) : 0ull;
-      if (t0 + t == 0) {
-        acc = kk;
-        pay = cc[t];
-      } else {
-        g16::merge(acc, pay, kk, in ? cc[t] : 0.f, r);
-      }
+  for (int t = 0; t < kMergeChunk; ++t) {
+    const bool in = s2 * kMergeChunk + t < p.S;  // uniform per row
+    const u64 kk = (in && id[t] >= 0) ? make_key(sl[t], id[t]) : 0ull;
+    if (t == 0) {
+      acc = kk;
+      pay = cc[t];
+    } else {
+      g16::merge(acc, pay, kk, cc[t], r);
     }
   }
   if (live) {
