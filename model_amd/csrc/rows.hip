@@ -317,7 +317,7 @@ __device__ __forceinline__ float wave_sq(const RowVec<W> (&a)[VPL]) {
 
 template <int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
-    const uint32_t* __restrict__ sorted_p, const int32_t* __restrict__ seg_of, const int32_t* __restrict__ seg_start,
+    const uint32_t* __restrict__ sorted_p, const int32_t* __restrict__ seg_of,
     const float* __restrict__ weights, const float* __restrict__ g, int fpt, int nv, int64_t n,
     float* __restrict__ rows, float* __restrict__ row_sq, float* __restrict__ partial) {
   const int64_t r = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
@@ -331,9 +331,18 @@ __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
   for (int v = 0; v < VPL; ++v) acc[v].zero();
   int cur = seg_of[r0];
   bool first = true;
+  // Segments are runs of equal ids in sorted order, so only the range's
+  // first segment can start before r0 and only its last can end at or after
+  // r1: a segment lies inside the range unless it is the first and position
+  // r0 - 1 belongs to it, or the last and position r1 does.  Both tests are
+  // read here once, so emitting a segment needs no load of its bounds.
+  const int seg_first = cur;
+  const int seg_last = seg_of[r1 - 1];
+  const bool first_open = r0 > 0 && seg_of[r0 > 0 ? r0 - 1 : 0] == seg_first;
+  const bool last_open = r1 < n && seg_of[r1 < n ? r1 : n - 1] == seg_last;
   auto emit = [&](int seg) {
-    const int64_t s0 = seg_start[seg], s1 = seg_start[seg + 1];
-    if (s0 >= r0 && s1 <= r1) {
+    const bool open = (seg == seg_first && first_open) || (seg == seg_last && last_open);
+    if (!open) {
 #pragma unroll
       for (int v = 0; v < VPL; ++v) {
         const int c = lane + kWave * v;
@@ -791,7 +800,7 @@ static void launch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32
                           const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
                           int zero_padding, hipStream_t s) {
   const unsigned b1 = (unsigned)cdiv(L.nranges, kRowThreads / kWave);
-  seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq,
+  seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, weights, g, fpt, nv, P, rows, row_sq,
                                                        partial);
   seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, rows, row_sq, b1,
                                                              nseg, L.cap, pool_size, uniq, zero_padding);
