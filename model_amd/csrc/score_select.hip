@@ -772,34 +772,39 @@ __global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
   const float a_cl = lc[0], b_cl = lc[1];
   const float aok = a_ok ? 1.f : 0.f;
 
-  // row 0: (0, j) at lane j
-  u64 acc;
-  float pay;
-  {
-    const float a0 = g16::bcastf<0>(a_sel), a0c = g16::bcastf<0>(a_cl), a0k = g16::bcastf<0>(aok);
-    acc = (a0k != 0.f && b_ok) ? make_key(a0 + b_sel, r) : 0ull;
-    pay = a0c + b_cl;
+  // The grid's candidate lists, each sorted descending across the row:
+  // row i holds (i, j) for j < 16/(i+1) (rows 0..7), and list 8 the column
+  // (i, 0) of rows 8..15 at lane i - 8.  They are merged as a tree, so the
+  // merges of one level are independent and fill each other's exchange
+  // latencies.
+  u64 L[9];
+  float P[9];
+#define MPL_PAIR_ROW(I)                                                                                 \
+  {                                                                                                     \
+    const float ai = g16::bcastf<I>(a_sel), aic = g16::bcastf<I>(a_cl), aik = g16::bcastf<I>(aok);    \
+    L[I] = (r < K / (I + 1) && aik != 0.f && b_ok) ? make_key(ai + b_sel, I * K + r) : 0ull;           \
+    P[I] = aic + b_cl;                                                                                  \
   }
-  // rows 1..7: (i, j) for j < 16/(i+1)
-#define MPL_PAIR_ROW(I)                                                                               \
-  {                                                                                                   \
-    const float ai = g16::bcastf<I>(a_sel), aic = g16::bcastf<I>(a_cl), aik = g16::bcastf<I>(aok);  \
-    const u64 cand = (r < K / (I + 1) && aik != 0.f && b_ok) ? make_key(ai + b_sel, I * K + r) : 0ull; \
-    g16::merge(acc, pay, cand, aic + b_cl, r);                                                        \
-  }
-  MPL_PAIR_ROW(1) MPL_PAIR_ROW(2) MPL_PAIR_ROW(3) MPL_PAIR_ROW(4) MPL_PAIR_ROW(5) MPL_PAIR_ROW(6)
-  MPL_PAIR_ROW(7)
+  MPL_PAIR_ROW(0) MPL_PAIR_ROW(1) MPL_PAIR_ROW(2) MPL_PAIR_ROW(3) MPL_PAIR_ROW(4) MPL_PAIR_ROW(5)
+  MPL_PAIR_ROW(6) MPL_PAIR_ROW(7)
 #undef MPL_PAIR_ROW
-  // rows 8..15: only (i, 0) can reach the top 16; lane r takes row 8 + r
   {
     const float b0 = g16::bcastf<0>(b_sel), b0c = g16::bcastf<0>(b_cl);
     const bool b0_ok = b0 != -INFINITY;
     const float ar = __uint_as_float(g16::shl8(__float_as_uint(a_sel)));
     const float arc = __uint_as_float(g16::shl8(__float_as_uint(a_cl)));
     const float ark = __uint_as_float(g16::shl8(__float_as_uint(aok)));
-    const u64 cand = (r < 8 && ark != 0.f && b0_ok) ? make_key(ar + b0, (8 + r) * K) : 0ull;
-    g16::merge(acc, pay, cand, arc + b0c, r);
+    L[8] = (r < 8 && ark != 0.f && b0_ok) ? make_key(ar + b0, (8 + r) * K) : 0ull;
+    P[8] = arc + b0c;
   }
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) g16::merge(L[i], P[i], L[i + 1], P[i + 1], r);
+  g16::merge(L[0], P[0], L[2], P[2], r);
+  g16::merge(L[4], P[4], L[6], P[6], r);
+  g16::merge(L[0], P[0], L[4], P[4], r);
+  g16::merge(L[0], P[0], L[8], P[8], r);
+  const u64 acc = L[0];
+  const float pay = P[0];
 
   // lane r holds the rank-r slot
   const int flat = acc ? key_index(acc) : 0;

@@ -214,7 +214,11 @@ __device__ __forceinline__ float bcastf(float v) {
 
 // acc <- best 16 of (acc, b), both sorted descending across the row (lane r
 // holds rank r); payloads follow their keys.  Bitonic split against the
-// mirrored b, then a 4-stage bitonic merger.
+// mirrored b, then a 4-stage bitonic merger.  In a stage the lower lane of a
+// pair keeps the larger key and the upper lane the smaller: the upper lane
+// takes its partner's key unless that key is larger, so one compare serves
+// both (equal keys are only the empty key 0, whose swap changes nothing that
+// is output).
 __device__ __forceinline__ void merge(u64& acc, float& pay, u64 b, float bp, int r) {
   const u64 br = ((u64)mirror((uint32_t)(b >> 32)) << 32) | mirror((uint32_t)b);
   const float bpr = __uint_as_float(mirror(__float_as_uint(bp)));
@@ -225,8 +229,8 @@ __device__ __forceinline__ void merge(u64& acc, float& pay, u64 b, float bp, int
   {                                                       \
     const u64 o = xr64<S>(acc);                           \
     const float op = xrf<S>(pay);                         \
-    const bool lower = (r & S) == 0;                      \
-    const bool other = lower ? (o > acc) : (o < acc);     \
+    const bool upper = (r & S) != 0;                      \
+    const bool other = (o > acc) != upper;                \
     acc = other ? o : acc;                                \
     pay = other ? op : pay;                               \
   }
