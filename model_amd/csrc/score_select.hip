@@ -696,6 +696,74 @@ __global__ __launch_bounds__(256) void pair_kernel(PairParams p) {
 // pair_kernel for k == 16: the same algorithm on 16-lane rows with DPP /
 // swizzle exchanges (no LDS traffic) and compile-time row broadcasts; split
 // lists are loaded four at a time so their loads overlap.
+// The pair stage of one (token, head) on a 16-lane row, from the two
+// codebooks' final lists (lane r holds rank r of lk[c], clean score lc[c]):
+// memory.py:167-175.  Writes slots, flat indices and routing weights of a
+// live row.
+__device__ __forceinline__ void pair_tail_k16(const PairParams& p, const u64 (&lk)[2], const float (&lc)[2],
+                                              bool live, int64_t mh, int lane, int r) {
+  constexpr int K = 16;
+  const bool a_ok = lk[0] != 0ull, b_ok = lk[1] != 0ull;
+  const float a_sel = a_ok ? key_score(lk[0]) : -INFINITY;
+  const float b_sel = b_ok ? key_score(lk[1]) : -INFINITY;
+  const int a_id = a_ok ? key_index(lk[0]) : 0;
+  const int b_id = b_ok ? key_index(lk[1]) : 0;
+  const float a_cl = lc[0], b_cl = lc[1];
+  const float aok = a_ok ? 1.f : 0.f;
+
+  // The grid's candidate lists, each sorted descending across the row:
+  // row i holds (i, j) for j < 16/(i+1) (rows 0..7), and list 8 the column
+  // (i, 0) of rows 8..15 at lane i - 8.  They are merged as a tree, so the
+  // merges of one level are independent and fill each other's exchange
+  // latencies.
+  u64 L[9];
+  float P[9];
+#define MPL_PAIR_ROW(I)                                                                                 \
+  {                                                                                                     \
+    const float ai = g16::bcastf<I>(a_sel), aic = g16::bcastf<I>(a_cl), aik = g16::bcastf<I>(aok);    \
+    L[I] = (r < K / (I + 1) && aik != 0.f && b_ok) ? make_key(ai + b_sel, I * K + r) : 0ull;           \
+    P[I] = aic + b_cl;                                                                                  \
+  }
+  MPL_PAIR_ROW(0) MPL_PAIR_ROW(1) MPL_PAIR_ROW(2) MPL_PAIR_ROW(3) MPL_PAIR_ROW(4) MPL_PAIR_ROW(5)
+  MPL_PAIR_ROW(6) MPL_PAIR_ROW(7)
+#undef MPL_PAIR_ROW
+  {
+    const float b0 = g16::bcastf<0>(b_sel), b0c = g16::bcastf<0>(b_cl);
+    const bool b0_ok = b0 != -INFINITY;
+    const float ar = __uint_as_float(g16::shl8(__float_as_uint(a_sel)));
+    const float arc = __uint_as_float(g16::shl8(__float_as_uint(a_cl)));
+    const float ark = __uint_as_float(g16::shl8(__float_as_uint(aok)));
+    L[8] = (r < 8 && ark != 0.f && b0_ok) ? make_key(ar + b0, (8 + r) * K) : 0ull;
+    P[8] = arc + b0c;
+  }
+#pragma unroll
+  for (int i = 0; i < 8; i += 2) g16::merge(L[i], P[i], L[i + 1], P[i + 1], r);
+  g16::merge(L[0], P[0], L[2], P[2], r);
+  g16::merge(L[4], P[4], L[6], P[6], r);
+  g16::merge(L[0], P[0], L[4], P[4], r);
+  g16::merge(L[0], P[0], L[8], P[8], r);
+  const u64 acc = L[0];
+  const float pay = P[0];
+
+  // lane r holds the rank-r slot
+  const int flat = acc ? key_index(acc) : 0;
+  const int base = lane - r;
+  int ia = __shfl(a_id, base + flat / K);
+  int ib = __shfl(b_id, base + flat % K);
+  ia = (ia >= 0 && ia < p.n) ? ia : 0;  // ids come from keys < n; guards non-finite inputs
+  ib = (ib >= 0 && ib < p.n) ? ib : 0;
+  const float sc = acc ? pay : -INFINITY;
+  const float mx = g16::rmax(sc);
+  const float e = acc ? expf(sc - mx) : 0.f;
+  const float sum = g16::rsum(e);
+  if (live) {
+    const int64_t ob = mh * K + r;
+    p.slots[ob] = ia * p.n + ib;
+    p.flat_idx[ob] = flat;
+    p.weights[ob] = e / sum;
+  }
+}
+
 __global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
   constexpr int K = 16;
   const int lane = threadIdx.x & 63;
@@ -764,65 +832,7 @@ __global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
         p.sub_scores[o0[c]] = lk[c] ? lc[c] : -INFINITY;
       }
   }
-  const bool a_ok = lk[0] != 0ull, b_ok = lk[1] != 0ull;
-  const float a_sel = a_ok ? key_score(lk[0]) : -INFINITY;
-  const float b_sel = b_ok ? key_score(lk[1]) : -INFINITY;
-  const int a_id = a_ok ? key_index(lk[0]) : 0;
-  const int b_id = b_ok ? key_index(lk[1]) : 0;
-  const float a_cl = lc[0], b_cl = lc[1];
-  const float aok = a_ok ? 1.f : 0.f;
-
-  // The grid's candidate lists, each sorted descending across the row:
-  // row i holds (i, j) for j < 16/(i+1) (rows 0..7), and list 8 the column
-  // (i, 0) of rows 8..15 at lane i - 8.  They are merged as a tree, so the
-  // merges of one level are independent and fill each other's exchange
-  // latencies.
-  u64 L[9];
-  float P[9];
-#define MPL_PAIR_ROW(I)                                                                                 \
-  {                                                                                                     \
-    const float ai = g16::bcastf<I>(a_sel), aic = g16::bcastf<I>(a_cl), aik = g16::bcastf<I>(aok);    \
-    L[I] = (r < K / (I + 1) && aik != 0.f && b_ok) ? make_key(ai + b_sel, I * K + r) : 0ull;           \
-    P[I] = aic + b_cl;                                                                                  \
-  }
-  MPL_PAIR_ROW(0) MPL_PAIR_ROW(1) MPL_PAIR_ROW(2) MPL_PAIR_ROW(3) MPL_PAIR_ROW(4) MPL_PAIR_ROW(5)
-  MPL_PAIR_ROW(6) MPL_PAIR_ROW(7)
-#undef MPL_PAIR_ROW
-  {
-    const float b0 = g16::bcastf<0>(b_sel), b0c = g16::bcastf<0>(b_cl);
-    const bool b0_ok = b0 != -INFINITY;
-    const float ar = __uint_as_float(g16::shl8(__float_as_uint(a_sel)));
-    const float arc = __uint_as_float(g16::shl8(__float_as_uint(a_cl)));
-    const float ark = __uint_as_float(g16::shl8(__float_as_uint(aok)));
-    L[8] = (r < 8 && ark != 0.f && b0_ok) ? make_key(ar + b0, (8 + r) * K) : 0ull;
-    P[8] = arc + b0c;
-  }
-#pragma unroll
-  for (int i = 0; i < 8; i += 2) g16::merge(L[i], P[i], L[i + 1], P[i + 1], r);
-  g16::merge(L[0], P[0], L[2], P[2], r);
-  g16::merge(L[4], P[4], L[6], P[6], r);
-  g16::merge(L[0], P[0], L[4], P[4], r);
-  g16::merge(L[0], P[0], L[8], P[8], r);
-  const u64 acc = L[0];
-  const float pay = P[0];
-
-  // lane r holds the rank-r slot
-  const int flat = acc ? key_index(acc) : 0;
-  const int base = lane - r;
-  int ia = __shfl(a_id, base + flat / K);
-  int ib = __shfl(b_id, base + flat % K);
-  ia = (ia >= 0 && ia < p.n) ? ia : 0;  // ids come from keys < n; guards non-finite inputs
-  ib = (ib >= 0 && ib < p.n) ? ib : 0;
-  const float sc = acc ? pay : -INFINITY;
-  const float mx = g16::rmax(sc);
-  const float e = acc ? expf(sc - mx) : 0.f;
-  const float sum = g16::rsum(e);
-  if (live) {
-    const int64_t ob = mh * K + r;
-    p.slots[ob] = ia * p.n + ib;
-    p.flat_idx[ob] = flat;
-    p.weights[ob] = e / sum;
-  }
+  pair_tail_k16(p, lk, lc, live, mh, lane, r);
 }
 
 // Split lists are reduced eight at a time before stage 2 (k == 16 only).
@@ -882,6 +892,72 @@ __global__ __launch_bounds__(256) void merge_splits_k16(MergeParams p) {
     p.out_idx[o] = acc ? key_index(acc) : -1;
     p.out_clean[o] = acc ? pay : -INFINITY;
     if (p.out_sel != nullptr) p.out_sel[o] = acc ? key_score(acc) : -INFINITY;
+  }
+}
+
+// Stage 2 of a select with 8 < S <= 64 split lists (k == 16, the decode
+// plans) in one launch instead of a merge_splits_k16 level plus the pair
+// kernel: one workgroup per (token, head).  Row g of its 16 rows of 16 lanes
+// merges lists 8*(g%8) .. 8*(g%8)+7 of codebook g/8 (lists past S enter as
+// empty keys); the row lists meet in LDS, rows 0 and 8 merge their
+// codebook's eight (the codebook's top-k, written to sub_idx / sub_scores),
+// and row 0 runs the pair stage.
+constexpr int kWideMaxSplits = kMergeChunk * kMergeChunk;
+
+__global__ __launch_bounds__(256) void pair_wide_k16(PairParams p) {
+  constexpr int K = 16;
+  __shared__ u64 skey[16][K];
+  __shared__ float spay[16][K];
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = threadIdx.x >> 4;
+  const int c = g >> 3, chunk = g & 7;
+  const int64_t mh = blockIdx.x;  // the grid is exactly M * H workgroups
+  const int64_t m = mh / p.H;
+  const int h = (int)(mh % p.H);
+  const int HC = 2 * p.H;
+  const float* lsel = p.sel != nullptr ? p.sel : p.clean;
+  const int64_t o0 = ((int64_t)m * HC + 2 * h + c) * K + r;
+  const int64_t sstride = p.M * HC * K;
+  int id[kMergeChunk];
+  float sl[kMergeChunk], cc[kMergeChunk];
+#pragma unroll
+  for (int t = 0; t < kMergeChunk; ++t) {
+    const int64_t o = (int64_t)min(chunk * kMergeChunk + t, p.S - 1) * sstride + o0;  // clamped, unconditional
+    id[t] = p.idx[o];
+    sl[t] = lsel[o];
+    cc[t] = p.clean[o];
+  }
+  pin_loaded(id, sl, cc);
+  u64 acc = 0;
+  float pay = 0.f;
+#pragma unroll
+  for (int t = 0; t < kMergeChunk; ++t) {
+    const bool in = chunk * kMergeChunk + t < p.S;  // uniform per row
+    const u64 kk = (in && id[t] >= 0) ? make_key(sl[t], id[t]) : 0ull;
+    if (t == 0) {
+      acc = kk;
+      pay = cc[t];
+    } else {
+      g16::merge(acc, pay, kk, cc[t], r);
+    }
+  }
+  skey[g][r] = acc;
+  spay[g][r] = pay;
+  __syncthreads();
+  if (chunk == 0) {  // rows 0 and 8 read rows 1..7 and 9..15 and rewrite only their own entries
+#pragma unroll
+    for (int t = 1; t < kMergeChunk; ++t) g16::merge(acc, pay, skey[g + t][r], spay[g + t][r], r);
+    p.sub_idx[o0] = acc ? key_index(acc) : -1;
+    p.sub_scores[o0] = acc ? pay : -INFINITY;
+    skey[g][r] = acc;
+    spay[g][r] = pay;
+  }
+  __syncthreads();
+  if (g == 0) {
+    const u64 lk[2] = {skey[0][r], skey[8][r]};
+    const float lc[2] = {spay[0][r], spay[8][r]};
+    pair_tail_k16(p, lk, lc, true, mh, lane, r);
   }
 }
 
@@ -1111,6 +1187,10 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   // many splits (decode-sized batches): reduce the lists in parallel, eight
   // into one per level, so stage 2 merges at most 8 lists instead of a long
   // sequential chain
+  if (pair && k == 16 && pp.S > kMergeChunk && pp.S <= kWideMaxSplits) {
+    pair_wide_k16<<<(unsigned)(M * H), 256, 0, s>>>(pp);
+    return check_launch("mpl_score_select(stage 2)");
+  }
   float* r = w + (noise ? 3 : 2) * part;
   while (k == 16 && pp.S > kMergeChunk) {
     const int S2 = (int)cdiv(pp.S, kMergeChunk);

@@ -146,8 +146,7 @@ __device__ __forceinline__ void group_merge(u64& acc, float& pay, u64 b, float b
     const int s = (G / 2) >> st;
     const u64 o = shfl_xor_u64<G>(acc, s);
     const float op = __shfl_xor(pay, s, G);
-    const bool lower = (r & s) == 0;
-    const bool other = lower ? (o > acc) : (o < acc);
+    const bool other = (o > acc) != ((r & s) != 0);  // as in g16::merge
     acc = other ? o : acc;
     pay = other ? op : pay;
   }

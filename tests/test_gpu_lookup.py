@@ -76,6 +76,22 @@ def test_split_key_plan_small_batches(gpu_lib):
         oracle_check(pool, params, q, pool.lookup(params, q), min_tie_free=0.0)
 
 
+@pytest.mark.parametrize("M", [1, 40])
+def test_noise_with_split_plan(gpu_lib, M):
+    """Decode-sized batches with routing noise: 32 split lists per codebook
+    (n = 1,024) reduced in one stage-2 launch (k = 16), against the oracle
+    with the same Gumbel draw."""
+    n, H, d_key, d, k = 1024, 2, 64, 32, 16
+    pool = MemoryPool(n, H, d_key, d, k, routing_noise=1.0, values_dtype=torch.float16)
+    params = make_params(pool, 11, key_std=(d_key // 2) ** -0.5)
+    q = _queries(M, H, d_key, 12 + M)
+    g = torch.Generator(device="cuda").manual_seed(M)
+    u = torch.rand((M, H, 2, n), generator=g, device="cuda").clamp_(min=1e-30)
+    gumbel = -torch.log(-torch.log(u))
+    res = pool.lookup(params, q, train=True, gumbel=gumbel, noise_scale=0.5)
+    oracle_check(pool, params, q, res, gumbel=gumbel, noise_coef=0.5, min_tie_free=0.0)
+
+
 @pytest.mark.parametrize("dt", ["fp32", "fp16"])
 def test_noise_selects_on_noisy_scores_and_weights_stay_clean(gpu_lib, dt):
     """memory.py:155-178 with the Gumbel draw given to both sides."""
