@@ -76,6 +76,30 @@ def test_split_key_plan_small_batches(gpu_lib):
         oracle_check(pool, params, q, pool.lookup(params, q), min_tie_free=0.0)
 
 
+@pytest.mark.parametrize("dt", ["fp32", "fp16"])
+def test_exact_zero_scores_tie_by_index(gpu_lib, dt):
+    """Keys orthogonal to the query score exactly 0 and fill places 2..k:
+    the selection bound is then 0 itself, and those keys must still enter,
+    lowest index first (lax.top_k), next to the one key along the query."""
+    n, H, d_key, d, k = 64, 1, 16, 8, 4
+    half = d_key // 2
+    pool = MemoryPool(n, H, d_key, d, k, values_dtype=DT[dt])
+    params = make_params(pool, 1)
+    keys = torch.zeros((H, 2, n, half))
+    keys[..., 1] = 1.0
+    keys[..., 2] = 1.0
+    keys[:, :, 5] = 0.0
+    keys[:, :, 5, 0] = 1.0
+    params["sub_keys"] = keys.cuda()
+    q = torch.zeros((3, H, d_key))
+    q[..., 0] = 1.0
+    q[..., half] = 1.0
+    res = pool.lookup(params, q.cuda())
+    want = ol.top_k(np.einsum("hcnd,d->hcn", keys.numpy().astype(np.float64), np.eye(half)[0]), k)[1]
+    assert want[0, 0].tolist() == [5, 0, 1, 2]
+    assert res["sub_idx"].cpu().tolist() == [want.tolist()] * 3
+
+
 @pytest.mark.parametrize("M", [1, 40])
 def test_noise_with_split_plan(gpu_lib, M):
     """Decode-sized batches with routing noise: 32 split lists per codebook
