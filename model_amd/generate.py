@@ -40,8 +40,8 @@ class Generator:
 
     def _reset_cache(self):
         for c in self.cache:
-            c["k"].zero_()
-            c["v"].zero_()
+            for t in c.values():
+                t.zero_()
 
     def _ensure_graph(self):
         if not self.use_graph or self.graph is not None:

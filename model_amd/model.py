@@ -173,10 +173,14 @@ class MemoryPoolLM:
         return {"params": p}
 
     def init_cache(self, batch_size: int, device="cuda") -> List[Dict[str, torch.Tensor]]:
+        """Per layer the keys transposed, "kt" [B, heads, hd, max_len], and the
+        values, "v" [B, heads, max_len, hd]: both products of a decode step
+        then read their cache operand as stored, without a transposed copy of
+        the whole cache."""
         cfg = self.cfg
         hd = cfg.d_model // cfg.n_heads
-        shape = (batch_size, cfg.n_heads, cfg.max_len, hd)
-        return [{"k": torch.zeros(shape, device=device), "v": torch.zeros(shape, device=device)}
+        return [{"kt": torch.zeros((batch_size, cfg.n_heads, hd, cfg.max_len), device=device),
+                 "v": torch.zeros((batch_size, cfg.n_heads, cfg.max_len, hd), device=device)}
                 for _ in range(cfg.n_layers)]
 
     # ----------------------------------------------------------- forward
@@ -185,19 +189,22 @@ class MemoryPoolLM:
         B, T, d = h.shape
         hd = d // cfg.n_heads
 
-        def proj(nm):  # DenseGeneral to (heads, hd) -> [B, heads, T, hd]
-            w = p[nm]["kernel"].reshape(d, cfg.n_heads * hd)
-            return (torch.matmul(h, w).reshape(B, T, cfg.n_heads, hd) + p[nm]["bias"]).permute(0, 2, 1, 3)
-
-        q, k, v = proj("query") * (hd ** -0.5), proj("key"), proj("value")
+        # the three DenseGeneral projections to (heads, hd) as one product
+        names = ("query", "key", "value")
+        w = torch.cat([p[nm]["kernel"].reshape(d, cfg.n_heads * hd) for nm in names], 1)
+        b = torch.cat([p[nm]["bias"].reshape(cfg.n_heads * hd) for nm in names])
+        qkv = (torch.matmul(h, w) + b).reshape(B, T, 3, cfg.n_heads, hd)
+        q, k, v = (qkv[:, :, i].permute(0, 2, 1, 3) for i in range(3))  # [B, heads, T, hd]
+        q = q * (hd ** -0.5)
         if layer_cache is not None:  # decode: write position `positions`, attend to <= it
-            layer_cache["k"].index_copy_(2, positions, k)
+            layer_cache["kt"].index_copy_(3, positions, k.transpose(-1, -2))
             layer_cache["v"].index_copy_(2, positions, v)
-            k, v = layer_cache["k"], layer_cache["v"]
+            kt, v = layer_cache["kt"], layer_cache["v"]
             mask = (torch.arange(cfg.max_len, device=h.device) <= positions[:, None])[None, None]
         else:
+            kt = k.transpose(-1, -2).contiguous()
             mask = torch.ones((T, T), dtype=torch.bool, device=h.device).tril()[None, None]
-        s = torch.matmul(q, k.transpose(-1, -2).contiguous())
+        s = torch.matmul(q, kt)
         s = s.masked_fill(~mask, torch.finfo(s.dtype).min)
         a = torch.matmul(torch.softmax(s, dim=-1), v)  # [B, heads, T, hd]
         a = a.permute(0, 2, 1, 3).reshape(B, T, cfg.n_heads * hd)
@@ -243,7 +250,7 @@ class MemoryPoolLM:
                     layer_aux.append(aux)
             x = x + y
         x = _ln(x, p["ln_final"])
-        logits = torch.matmul(x, emb.t().contiguous())
+        logits = F.linear(x, emb)  # x . emb^T as one product, no transposed copy of the table
         return logits, _LazyMerged(layer_aux)
 
     __call__ = apply
