@@ -34,8 +34,18 @@ class Generator:
         self.use_graph = graph
 
     def _step(self):
-        logits, _ = self.model.apply({"params": self.params}, self.tok[:, None], positions=self.pos,
-                                     cache=self.cache)
+        # The step's products have one row per stream.  For such shapes
+        # hipBLASLt picks one-workgroup tiles; rocBLAS (torch's "cublas"
+        # backend on ROCm) ran the 64-stream step 20% faster.  The choice is
+        # torch's process-wide setting, so it is restored after the step (a
+        # captured step keeps the kernels it was captured with).
+        prev = torch.backends.cuda.preferred_blas_library()
+        torch.backends.cuda.preferred_blas_library("cublas")
+        try:
+            logits, _ = self.model.apply({"params": self.params}, self.tok[:, None], positions=self.pos,
+                                         cache=self.cache)
+        finally:
+            torch.backends.cuda.preferred_blas_library(prev)
         return logits[:, 0]
 
     def _reset_cache(self):
