@@ -166,10 +166,19 @@ class Lookup:
                                                p(self.slots), p(self.weights), self.M, self.H * self.k, 0,
                                                p(self.out), self.stream), "gather")
 
+    def lookup(self):
+        # selection and value read in one call: at H = 4, k = 16 the pair
+        # stage and the weighted row sum run as one kernel
+        p = self._lib.ptr
+        self._lib.check(self.L.mpl_lookup(
+            p(self.q), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
+            self._lib.MPL_F16, self.T, None, 0.0, p(self.ws), self.ws_bytes, p(self.sub_idx), p(self.sub_scores),
+            p(self.flat_idx), p(self.slots), p(self.weights), p(self.values), self._lib.MPL_F16, self.d, 0,
+            p(self.out), self.stream), "lookup")
+
     def step(self):
         self.pack()
-        self.select()
-        self.gather()
+        self.lookup()
 
 
 def time_loop(torch, fn, iters, warmup):
@@ -206,6 +215,7 @@ def kernel_breakdown(torch, lk, iters):
         "score_select_ms": time_loop(torch, lk.select, iters, 3),
         "score_topk_ms": time_loop(torch, lk.topk, iters, 3),
         "gather_wsum_ms": time_loop(torch, lk.gather, iters, 3),
+        "lookup_ms": time_loop(torch, lk.lookup, iters, 3),
     }
 
 

@@ -98,6 +98,26 @@ int mpl_score_select(const void* queries, int query_mode, float* q_len, const vo
                      int32_t* slots, float* weights, void* stream);
 
 /*
+ * memory.py:132-193 (MemoryPool.__call__'s forward read, model.py:112-113):
+ * mpl_score_select followed by the value read of mpl_gather_wsum, in one
+ * call.  Same arguments, workspace (mpl_score_select_workspace_bytes) and
+ * outputs as mpl_score_select, plus values [n*n, d] in values_dtype (MPL_F16
+ * or MPL_F32), shuffle_reads (memory.py:179) and out [M, d] fp32, which equal
+ * mpl_gather_wsum(values, values_dtype, n*n, d, slots, weights, M, H*k,
+ * shuffle_reads, out) bit for bit.  With H = 4 and k = 16 the pair stage and
+ * the value read run in one kernel (one wave per token) when the key range is
+ * scored in at most 8 splits or reduced to 8 lists.
+ */
+int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* packed_keys,
+               int64_t M, int H, int n, int half, int k, int score_dtype,
+               float temperature, const float* gumbel, float noise_coef,
+               void* workspace, size_t workspace_bytes,
+               int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
+               int32_t* slots, float* weights,
+               const void* values, int values_dtype, int d, int shuffle_reads,
+               float* out, void* stream);
+
+/*
  * memory.py:161-163 and 207 (_top_k of the select scores, or of the clean
  * scores for the balance loss's f): stage 1 of mpl_score_select alone, same
  * arguments and semantics, writing only sub_idx [M,H,2,k] and sub_scores

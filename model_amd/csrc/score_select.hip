@@ -52,6 +52,7 @@
 #include "layout.h"
 #include "mfma.h"
 #include "topk.h"
+#include "wsum.h"
 
 namespace mpl {
 
@@ -762,8 +763,11 @@ __global__ __launch_bounds__(256) void pair_kernel(PairParams p) {
 // codebooks' final lists (lane r holds rank r of lk[c], clean score lc[c]):
 // memory.py:167-175.  Writes slots, flat indices and routing weights of a
 // live row.
+// The lane's slot id (in [0, n*n)) and weight are also returned in slot_out
+// and w_out, for a value read fused behind the pair stage.
 __device__ __forceinline__ void pair_tail_k16(const PairParams& p, const u64 (&lk)[2], const float (&lc)[2],
-                                              bool live, int64_t mh, int lane, int r) {
+                                              bool live, int64_t mh, int lane, int r, int& slot_out,
+                                              float& w_out) {
   constexpr int K = 16;
   const bool a_ok = lk[0] != 0ull, b_ok = lk[1] != 0ull;
   const float a_sel = a_ok ? key_score(lk[0]) : -INFINITY;
@@ -818,31 +822,30 @@ __device__ __forceinline__ void pair_tail_k16(const PairParams& p, const u64 (&l
   const float mx = g16::rmax(sc);
   const float e = acc ? expf(sc - mx) : 0.f;
   const float sum = g16::rsum(e);
+  slot_out = ia * p.n + ib;
+  w_out = e / sum;
   if (live) {
     const int64_t ob = mh * K + r;
-    p.slots[ob] = ia * p.n + ib;
+    p.slots[ob] = slot_out;
     p.flat_idx[ob] = flat;
-    p.weights[ob] = e / sum;
+    p.weights[ob] = w_out;
   }
 }
 
-__global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
+// The two codebooks' final lists of row mh (lane r gets rank r of lk[c] and
+// its clean score lc[c]): one split list loaded, or S lists merged.
+__device__ __forceinline__ void pair_lists_k16(const PairParams& p, bool live, int64_t mh, int r, u64 (&lk)[2],
+                                               float (&lc)[2]) {
   constexpr int K = 16;
-  const int lane = threadIdx.x & 63;
-  const int r = lane & 15;
-  const int64_t mh = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
-  const bool live = mh < p.M * p.H;  // dead rows still join the exchanges
   const int64_t m = live ? mh / p.H : 0;
   const int h = live ? (int)(mh % p.H) : 0;
   const int HC = 2 * p.H;
   const float* lsel = p.sel != nullptr ? p.sel : p.clean;
 
-  // The two codebooks' lists (dead rows read row 0 and enter as empty keys,
-  // whose payload is never output).  Both codebooks' entries of a batch of
-  // lists are requested before the first merge: one memory round trip per
-  // batch, and with one list no merge at all.
-  u64 lk[2];
-  float lc[2];
+  // Dead rows read row 0 and enter as empty keys, whose payload is never
+  // output.  Both codebooks' entries of a batch of lists are requested before
+  // the first merge: one memory round trip per batch, and with one list no
+  // merge at all.
   int64_t o0[2];
 #pragma unroll
   for (int c = 0; c < 2; ++c) o0[c] = ((int64_t)m * HC + 2 * h + c) * K + r;
@@ -894,7 +897,53 @@ __global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
         p.sub_scores[o0[c]] = lk[c] ? lc[c] : -INFINITY;
       }
   }
-  pair_tail_k16(p, lk, lc, live, mh, lane, r);
+}
+
+__global__ __launch_bounds__(256) void pair_kernel_k16(PairParams p) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int64_t mh = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const bool live = mh < p.M * p.H;  // dead rows still join the exchanges
+  u64 lk[2];
+  float lc[2];
+  pair_lists_k16(p, live, mh, r, lk, lc);
+  int slot;
+  float w;
+  pair_tail_k16(p, lk, lc, live, mh, lane, r, slot, w);
+}
+
+// The value read of a fused lookup (memory.py:179-193): values [n*n, VR*16
+// bytes] of type V, read(s) = s or (s + N/2 + 1) % N (memory.py:179).
+struct ReadParams {
+  const void* values;
+  int shuffle;
+  float* out;  // [M, d] fp32
+};
+
+// Stage 2 and the value read in one kernel, for H = 4 and k = 16: the wave's
+// four 16-lane rows are the four heads of one token, so after the pair stage
+// lane h*16 + r holds that token's row h*k + r (slot and weight), exactly the
+// lane layout the weighted row sum takes.  While some waves run the pair
+// merges (VALU-bound), others have their row loads in flight.
+template <typename V, int VR>
+__global__ __launch_bounds__(256) void pair_read_k16(PairParams p, ReadParams rp) {
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int64_t mh = ((int64_t)blockIdx.x * 256 + threadIdx.x) >> 4;
+  const bool live = mh < p.M * 4;  // H = 4: a wave is live or dead as a whole
+  u64 lk[2];
+  float lc[2];
+  pair_lists_k16(p, live, mh, r, lk, lc);
+  int slot;
+  float w;
+  pair_tail_k16(p, lk, lc, live, mh, lane, r, slot, w);
+  if (!live) return;
+  const int64_t m = mh >> 2;
+  const int64_t N = (int64_t)p.n * p.n;
+  if (rp.shuffle) slot = (int)(((int64_t)slot + N / 2 + 1) % N);
+  Wsum<V, VR> acc;
+  acc.add_chunk((const uint4*)rp.values, slot, w, 64, lane);
+  acc.store(rp.out + m * (int64_t)(VR * Vec16<V>::kElems), lane);
 }
 
 // Split lists are reduced eight at a time before stage 2 (k == 16 only).
@@ -1019,7 +1068,9 @@ __global__ __launch_bounds__(256) void pair_wide_k16(PairParams p) {
   if (g == 0) {
     const u64 lk[2] = {skey[0][r], skey[8][r]};
     const float lc[2] = {spay[0][r], spay[8][r]};
-    pair_tail_k16(p, lk, lc, true, mh, lane, r);
+    int slot;
+    float w;
+    pair_tail_k16(p, lk, lc, true, mh, lane, r, slot, w);
   }
 }
 
@@ -1160,11 +1211,47 @@ extern "C" size_t mpl_score_topk_workspace_bytes(int64_t M, int H, int n, int ha
 
 // Both entry points: stage 1 (+ the split-list reduction); with `pair`, stage
 // 2 and the softmax as well.  Without `pair`, flat_idx/slots/weights are null.
+// The value read fused into stage 2 (pair_read_k16), when the shapes allow:
+// returns false (nothing launched) otherwise.
+struct LookupRead {
+  const void* values;
+  int dtype;  // MPL_F16 or MPL_F32
+  int d;
+  int shuffle;
+  float* out;
+};
+
+static bool launch_pair_read(const LookupRead& lr, const PairParams& pp, unsigned grid, hipStream_t s) {
+  const int esz = lr.dtype == MPL_F16 ? 2 : 4;
+  if (pp.H != 4 || pp.k != 16 || (lr.d * esz) % 16 != 0 || ((uintptr_t)lr.values % 16) != 0 ||
+      ((uintptr_t)lr.out % 16) != 0)
+    return false;
+  ReadParams rp;
+  rp.values = lr.values;
+  rp.shuffle = lr.shuffle;
+  rp.out = lr.out;
+  const int VR = lr.d * esz / 16;
+#define MPL_PR(V, vr)                                        \
+  if (VR == vr) {                                            \
+    pair_read_k16<V, vr><<<grid, 256, 0, s>>>(pp, rp);       \
+    return true;                                             \
+  }
+  if (lr.dtype == MPL_F16) {
+    MPL_PR(_Float16, 16) MPL_PR(_Float16, 32) MPL_PR(_Float16, 64)
+  } else {
+    MPL_PR(float, 32) MPL_PR(float, 64)
+  }
+#undef MPL_PR
+  return false;
+}
+
 static int select_impl(const char* who, bool pair, const void* queries, int query_mode, float* q_len,
                        const void* packed_keys, int64_t M, int H, int n, int half, int k, int score_dtype,
                        float temperature, const float* gumbel, float noise_coef, void* workspace,
                        size_t workspace_bytes, int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
-                       int32_t* slots, float* weights, void* stream) {
+                       int32_t* slots, float* weights, void* stream, const LookupRead* read = nullptr,
+                       bool* read_done = nullptr) {
+  if (read_done != nullptr) *read_done = false;
   clear_error();
   MPL_REQUIRE(M >= 0 && H > 0 && n > 0 && half > 0 && k > 0, MPL_EINVAL,
               "%s: bad sizes M=%lld H=%d n=%d half=%d k=%d", who, (long long)M, H, n, half, k);
@@ -1301,6 +1388,10 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   }
   const int G = k <= 16 ? 16 : 32;
   const unsigned g2 = (unsigned)cdiv(M * H * G, 256);
+  if (k == 16 && read != nullptr && launch_pair_read(*read, pp, g2, s)) {
+    *read_done = true;
+    return check_launch("mpl_lookup(stage 2 + value read)");
+  }
   if (k == 16) pair_kernel_k16<<<g2, 256, 0, s>>>(pp);
   else if (G == 16) pair_kernel<16><<<g2, 256, 0, s>>>(pp);
   else pair_kernel<32><<<g2, 256, 0, s>>>(pp);
@@ -1325,4 +1416,25 @@ extern "C" int mpl_score_topk(const void* queries, int query_mode, float* q_len,
   return select_impl("mpl_score_topk", false, queries, query_mode, q_len, packed_keys, M, H, n, half, k,
                      score_dtype, temperature, gumbel, noise_coef, workspace, workspace_bytes, sub_idx,
                      sub_scores, nullptr, nullptr, nullptr, stream);
+}
+
+extern "C" int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* packed_keys, int64_t M,
+                          int H, int n, int half, int k, int score_dtype, float temperature, const float* gumbel,
+                          float noise_coef, void* workspace, size_t workspace_bytes, int32_t* sub_idx,
+                          float* sub_scores, int32_t* flat_idx, int32_t* slots, float* weights,
+                          const void* values, int values_dtype, int d, int shuffle_reads, float* out,
+                          void* stream) {
+  clear_error();
+  MPL_REQUIRE(values_dtype == MPL_F16 || values_dtype == MPL_F32, MPL_EINVAL,
+              "mpl_lookup: values_dtype must be MPL_F16 or MPL_F32");
+  MPL_REQUIRE(d > 0, MPL_EINVAL, "mpl_lookup: bad d=%d", d);
+  MPL_REQUIRE(M == 0 || (values != nullptr && out != nullptr), MPL_EINVAL, "mpl_lookup: null buffer");
+  const LookupRead lr{values, values_dtype, d, shuffle_reads != 0, out};
+  bool done = false;
+  int rc = select_impl("mpl_lookup", true, queries, query_mode, q_len, packed_keys, M, H, n, half, k, score_dtype,
+                       temperature, gumbel, noise_coef, workspace, workspace_bytes, sub_idx, sub_scores, flat_idx,
+                       slots, weights, stream, &lr, &done);
+  if (rc || done || M == 0) return rc;
+  return mpl_gather_wsum(values, values_dtype, (int64_t)n * n, d, slots, weights, M, H * k, shuffle_reads,
+                              out, stream);
 }

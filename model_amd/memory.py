@@ -11,6 +11,8 @@ lookup runs in libmpl.so (include/mpl.h) on torch's current HIP stream:
                      scores + 2-stage top-k     memory.py:149-178
                      + routing softmax
   mpl_gather_wsum    value read                 memory.py:179-193
+  mpl_lookup         both of the above in one call (one kernel for
+                     stage 2 and the value read at H = 4, k = 16)
   mpl_route_counts,  routing statistics, and    memory.py:196-215
   mpl_balance_fwd    the balance loss
   mpl_key_diversity  key_diversity_loss         memory.py:230-240
@@ -272,14 +274,26 @@ class MemoryPool:
         flat_idx = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         slots = torch.empty((M, H, k), dtype=torch.int32, device=dev)
         weights = torch.empty((M, H, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_select(ptr(q), q_mode, ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
-                                 T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
-                                 ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
-              "mpl_score_select")
-
         out = torch.empty((M, d), dtype=torch.float32, device=dev)
         staged = None
-        if self.host_pool:
+        if not self.host_pool:
+            # selection and value read in one call (memory.py:132-193): with
+            # H = 4 and k = 16 the pair stage and the read share one kernel
+            values = params["values"]
+            if values.dtype not in (torch.float16, torch.float32) or not values.is_contiguous():
+                raise TypeError("values must be a contiguous float16/float32 [n*n, d_value] tensor")
+            if tuple(values.shape) != (self.pool_size, d):
+                raise ValueError(f"values must be [{self.pool_size}, {d}], got {tuple(values.shape)}")
+            check(L.mpl_lookup(ptr(q), q_mode, ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
+                               T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
+                               ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights),
+                               ptr(values), _dtype_code(values.dtype), d, int(bool(shuffle_reads)), ptr(out),
+                               stream), "mpl_lookup")
+        else:
+            check(L.mpl_score_select(ptr(q), q_mode, ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
+                                     T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
+                                     ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
+                  "mpl_score_select")
             # memory.py:182-183 (hp.fetch): the unique rows cross the host
             # link once into device memory; the weighted sum reads them there
             from . import host_pool as hp
@@ -291,13 +305,6 @@ class MemoryPool:
             staged = (rows, inverse.reshape(M, H, k))
             check(L.mpl_gather_wsum(ptr(rows), _dtype_code(rows.dtype), max(rows.shape[0], 1), d, ptr(staged[1]),
                                     ptr(weights), M, H * k, 0, ptr(out), stream), "mpl_gather_wsum")
-        else:
-            values = params["values"]
-            if values.dtype not in (torch.float16, torch.float32) or not values.is_contiguous():
-                raise TypeError("values must be a contiguous float16/float32 [n*n, d_value] tensor")
-            check(L.mpl_gather_wsum(ptr(values), _dtype_code(values.dtype), self.pool_size, d, ptr(slots),
-                                    ptr(weights), M, H * k, int(bool(shuffle_reads)), ptr(out), stream),
-                  "mpl_gather_wsum")
 
         noisy = gumbel is not None
         res = _Result()
