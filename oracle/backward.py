@@ -44,7 +44,7 @@ def lookup_backward(res: dict, values, g_out, *, n: int, query_scale: bool = Fal
     g = np.asarray(g_out, dtype=dtype).reshape(M, -1)
 
     rows = np.asarray(values)[read.reshape(-1)].astype(dtype).reshape(M, H, k, -1)
-    dw = np.einsum("md,mhkd->mhk", g, rows)                       # memory.py:192
+    dw = np.matmul(rows.reshape(M, H * k, -1), g[:, :, None]).reshape(M, H, k)  # memory.py:192
     ds = w * (dw - np.sum(w * dw, axis=-1, keepdims=True))         # softmax, memory.py:178
     fa, fb = res["flat_idx"] // k, res["flat_idx"] % k             # memory.py:167-175
     dsub = np.zeros((M, H, 2, k), dtype)
@@ -84,8 +84,13 @@ def lookup_backward(res: dict, values, g_out, *, n: int, query_scale: bool = Fal
         else:
             dcos += dps * T
 
-    dq_hat = np.einsum("mhcn,hcnd->mhcd", dcos, k_hat)
-    dk_hat = np.einsum("mhcn,mhcd->hcnd", dcos, q_hat)
+    # per codebook (h, c): dq_hat = dcos k_hat, dk_hat = dcos^T q_hat
+    dq_hat = np.empty_like(q_hat)
+    dk_hat = np.empty_like(k_hat)
+    for h in range(H):
+        for c in range(2):
+            dq_hat[:, h, c] = dcos[:, h, c] @ k_hat[h, c]
+            dk_hat[h, c] = dcos[:, h, c].T @ q_hat[:, h, c]
     dq = _l2_normalize_bwd(q, dq_hat)
     if query_scale:  # q_len = sqrt(sum q^2 + eps) / sqrt(half)   (memory.py:137)
         nrm = np.sqrt(np.sum(q * q, -1, keepdims=True) + 1e-6)

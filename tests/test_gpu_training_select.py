@@ -1,0 +1,94 @@
+"""GPU parity of the training-time selection and its backward at the
+training layer's widths (n_sub_keys = 512, H = 4, d_key = 256, k = 16 or 32,
+d_value = 256) against the oracle, with routing noise on as the reference
+trains (memory.py:155-164, train.py:378-416).
+
+fp16 scoring with noise at a sub-key half of 128 runs the stage-1 kernel
+that stages key blocks in LDS (k = 16 and k = 32 instantiations).  The
+Gumbel draw is the library's own fill (mpl_gumbel_noise, seeded through
+rngs["routing"]); the same tensor is handed to the oracle, so both sides
+select on identical noisy scores.  Slot sets must match on near-tie-free
+rows; weights (softmax of the clean scores) and gradients within the fp16
+tolerance of 1e-2 relative."""
+
+import numpy as np
+import pytest
+import torch
+
+from model_amd.memory import MemoryPool
+from oracle import backward as ob
+from oracle import lookup as ol
+from tests.gpu_helpers import make_params, oracle_check
+from tests.test_gpu_backward import _check, _setup, _with_selection
+
+pytestmark = pytest.mark.gpu
+
+N_SUB, H, D_KEY, D = 512, 4, 256, 256
+
+
+@pytest.mark.parametrize("k,M,noise_scale", [(16, 8192, 1.0), (16, 2048, 0.3), (32, 2048, 1.0)])
+def test_noisy_selection_training_widths(gpu_lib, k, M, noise_scale):
+    pool = MemoryPool(N_SUB, H, D_KEY, D, k, routing_noise=1.0, values_dtype=torch.float16)
+    params = make_params(pool, 41 + k, key_std=(D_KEY // 2) ** -0.5, value_std=0.02)
+    g = torch.Generator(device="cuda").manual_seed(42 + M)
+    q = torch.randn((M, H, D_KEY), generator=g, device="cuda")
+    print(f"noisy selection k={k} M={M} noise_scale={noise_scale}", flush=True)
+    res = pool.lookup(params, q, train=True, noise_scale=noise_scale, rngs={"routing": 1234 + k})
+    torch.cuda.synchronize()
+    gumbel = res["gumbel"]
+    assert gumbel is not None and tuple(gumbel.shape) == (M, H, 2, N_SUB)
+    oracle_check(pool, params, q, res, gumbel=gumbel, noise_coef=noise_scale)
+    # the noise moved picks: the clean lookup differs on some rows
+    clean = pool.lookup(params, q)
+    assert not torch.equal(clean["slots"], res["slots"])
+
+
+def _stage1_tie_free(scores: np.ndarray, k: int) -> np.ndarray:
+    """Rows of a stage-1 top-k whose k-th and (k+1)-th scores differ by more
+    than 1e-3 relative (the clean top-k of memory.py:207)."""
+    v, _ = ol.top_k(scores, k + 1)
+    return np.abs(v[..., k - 1] - v[..., k]) > 1e-3 * np.abs(v[..., k - 1])
+
+
+def test_training_backward_c4_with_noise(gpu_lib):
+    """The training layer at its full token count (8,192) with noise on and
+    balance coefficient 0.01: gradients of the queries, sub-keys and
+    log-temperature for the GPU's selection against oracle/backward.py.  The
+    balance loss's usage f comes from the clean stage-1 top-k (memory.py:207),
+    which is also checked against the oracle's on its tie-free rows."""
+    k, M, g_bal = 16, 8192, 0.01
+    pool, params, tq, q, keys, vals, g, log_t = _setup(
+        71, n=N_SUB, H=H, d_key=D_KEY, d=D, k=k, M=M, values_dtype=torch.float16, score_dtype=torch.float16,
+        query_scale=False, btg=False)
+    pool.routing_noise = 1.0
+    rngs = {"routing": 77}
+    res_gpu = pool.lookup(params, tq.detach(), train=True, rngs=rngs)
+    out, aux = pool.apply({"params": params}, tq, train=True, sparse_grad=True, rngs=rngs)
+    assert torch.equal(aux["slots"].reshape(M, H, k), res_gpu["slots"])  # same noise, same picks
+    loss = (out * torch.tensor(g, device="cuda")).sum() + g_bal * aux["balance_loss"]
+    gq, gk, gt = torch.autograd.grad(loss, [tq, params["sub_keys"], params["log_temperature"]])
+    torch.cuda.synchronize()
+
+    gum = res_gpu["gumbel"].cpu().numpy()
+    res = ol.lookup_forward(q, keys, vals, float(log_t), top_k_=k, gumbel=gum, noise_coef=1.0, dtype=np.float64)
+    ok, _ = ol.near_tie_free_rows(q, keys, float(log_t), top_k_=k, gumbel=gum, noise_coef=1.0)
+    assert ok.mean() > 0.5
+    slots = res_gpu["slots"].cpu().numpy()
+    np.testing.assert_array_equal(np.sort(slots[ok], -1), np.sort(res["slots"][ok], -1))
+    sel = _with_selection(res, res_gpu["sub_idx"].cpu().numpy(), res_gpu["flat_idx"].cpu().numpy(), slots)
+
+    # f from the GPU's clean stage-1 top-k, checked against the oracle's
+    clean = pool._clean_sub_idx(res_gpu["q"], res_gpu["packed"], res_gpu["score_code"], res_gpu["temperature"],
+                                M).cpu().numpy()
+    want_clean = ol.top_k(res["scores"], k)[1]
+    tf = _stage1_tie_free(res["scores"], k)
+    assert tf.mean() > 0.5
+    np.testing.assert_array_equal(np.sort(clean[tf], -1), np.sort(want_clean[tf], -1))
+    codebook = (np.arange(H)[:, None, None] * 2 + np.arange(2)[None, :, None]) * N_SUB
+    f = np.bincount((clean + codebook[None]).reshape(-1), minlength=H * 2 * N_SUB).reshape(H, 2, N_SUB) / (M * k)
+
+    ref = ob.lookup_backward(sel, vals, g, n=N_SUB, g_balance=g_bal, f=f)
+    _check(gq.cpu().numpy(), ref["d_queries"], 1e-2, "d_queries")
+    _check(gk.cpu().numpy(), ref["d_sub_keys"], 1e-2, "d_sub_keys")
+    _check(float(gt), ref["d_log_temperature"], 1e-2, "d_log_temperature",
+           float(np.abs(ref["d_cos"] * sel["cos"]).sum()))
