@@ -118,6 +118,26 @@ int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* pa
                float* out, void* stream);
 
 /*
+ * No counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
+ * mpl_lookup with the same arguments and outputs, minus the workspace: the
+ * selection's scratch is a fixed array of mpl_lookup_static_scratch_bytes()
+ * (32 MiB) on each GPU, held until the process ends; a lookup needing more
+ * (mpl_score_select_workspace_bytes above it, e.g. beyond about 65,000 tokens
+ * at n = 512) fails with MPL_EWORKSPACE.  Calls on one GPU share that array:
+ * calls that overlap in time on one GPU (other streams, other threads) race.
+ * Nothing is allocated; the current device must be the stream's device.
+ */
+size_t mpl_lookup_static_scratch_bytes(void);
+int mpl_lookup_static(const void* queries, int query_mode, float* q_len, const void* packed_keys,
+                      int64_t M, int H, int n, int half, int k, int score_dtype,
+                      float temperature, const float* gumbel, float noise_coef,
+                      int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
+                      int32_t* slots, float* weights,
+                      const void* values, int values_dtype, int d, int shuffle_reads,
+                      float* out, void* stream);
+
+/*
  * memory.py:161-163 and 207 (_top_k of the select scores, or of the clean
  * scores for the balance loss's f): stage 1 of mpl_score_select alone, same
  * arguments and semantics, writing only sub_idx [M,H,2,k] and sub_scores

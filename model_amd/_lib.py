@@ -30,6 +30,9 @@ SIGNATURES = {
     "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
     "mpl_lookup": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
                         _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
+    "mpl_lookup_static_scratch_bytes": (_SZ, []),
+    "mpl_lookup_static": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F,
+                               _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mpl_gumbel_noise": (_I, [_U64, _I64, _I, _P, _P]),
     "mpl_unique_slots_workspace_bytes": (_SZ, [_I64, _I64]),
     "mpl_unique_slots": (_I, [_P, _I64, _I64, _P, _SZ, _P, _P, _P, _P]),

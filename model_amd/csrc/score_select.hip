@@ -47,6 +47,7 @@
 
 #include <algorithm>
 #include <math.h>
+#include <mutex>
 
 #include "common.h"
 #include "layout.h"
@@ -1437,4 +1438,60 @@ extern "C" int mpl_lookup(const void* queries, int query_mode, float* q_len, con
   if (rc || done || M == 0) return rc;
   return mpl_gather_wsum(values, values_dtype, (int64_t)n * n, d, slots, weights, M, H * k, shuffle_reads,
                               out, stream);
+}
+
+// -------------------------------------------------- lookup without allocation
+// mpl_lookup_static: mpl_lookup with the selection's scratch in `scratch`, a
+// fixed array of kStaticScratchBytes on each GPU the library runs on (held
+// until the process ends), so the caller passes no workspace.  Each call
+// writes every byte of scratch it later reads (split lists, reduced lists,
+// noisy select scores) before reading it, so nothing is cleared between
+// calls.  Calls that overlap on one GPU share the array and race.
+constexpr size_t kStaticScratchBytes = (size_t)32 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxDevices];
+
+// Device address of the current device's copy of `scratch`.  In host code the
+// array's name is only a handle; the address is looked up once per device,
+// with that device current, and used from then on.
+static int static_scratch(void** addr) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  MPL_REQUIRE(e == hipSuccess, MPL_EHIP, "mpl_lookup_static: hipGetDevice: %s", hipGetErrorString(e));
+  MPL_REQUIRE(dev >= 0 && dev < kMaxDevices, MPL_EUNSUPPORTED, "mpl_lookup_static: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    MPL_REQUIRE(e == hipSuccess && p != nullptr, MPL_EHIP, "mpl_lookup_static: hipGetSymbolAddress: %s",
+                hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return MPL_OK;
+}
+
+extern "C" size_t mpl_lookup_static_scratch_bytes(void) { return kStaticScratchBytes; }
+
+extern "C" int mpl_lookup_static(const void* queries, int query_mode, float* q_len, const void* packed_keys,
+                                 int64_t M, int H, int n, int half, int k, int score_dtype, float temperature,
+                                 const float* gumbel, float noise_coef, int32_t* sub_idx, float* sub_scores,
+                                 int32_t* flat_idx, int32_t* slots, float* weights, const void* values,
+                                 int values_dtype, int d, int shuffle_reads, float* out, void* stream) {
+  clear_error();
+  const size_t need = mpl_score_select_workspace_bytes(M, H, n, half, k);
+  MPL_REQUIRE(need <= kStaticScratchBytes, MPL_EWORKSPACE,
+              "mpl_lookup_static: %lld tokens need %zu bytes of scratch, more than its fixed %zu; "
+              "split the batch or call mpl_lookup with a workspace",
+              (long long)M, need, kStaticScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = static_scratch(&ws);
+    if (rc) return rc;
+  }
+  return mpl_lookup(queries, query_mode, q_len, packed_keys, M, H, n, half, k, score_dtype, temperature, gumbel,
+                    noise_coef, ws, need, sub_idx, sub_scores, flat_idx, slots, weights, values, values_dtype, d,
+                    shuffle_reads, out, stream);
 }
