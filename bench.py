@@ -64,6 +64,8 @@ def parse():
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-generate", action="store_true")
     ap.add_argument("--no-host", action="store_true")
+    ap.add_argument("--only", choices=["text_study", "pool_67M_4096"], default=None,
+                    help="run one workload alone (for profiler runs) and print its timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
                          "scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes)")
@@ -98,21 +100,28 @@ def copy_calibration(torch):
 
 
 class Lookup:
-    """Preallocated buffers + direct C-ABI calls for one workload."""
+    """Preallocated buffers + direct C-ABI calls for one workload.
 
-    def __init__(self, torch, L, *, M, H, n, d_key, d, k, seed, values=None):
+    ``rotate`` = R independent token batches of M tokens each (queries and
+    every output), called in turn: call i works on batch i % R.  Rotating
+    batches whose fetched rows total more than the 256 MB Infinity Cache make
+    the timed value reads come from HBM rather than from rows a previous call
+    left in the cache."""
+
+    def __init__(self, torch, L, *, M, H, n, d_key, d, k, seed, values=None, rotate=1):
         from model_amd import _lib
 
         self.torch, self.L, self._lib = torch, L, _lib
         self.M, self.H, self.n, self.half, self.d, self.k = M, H, n, d_key // 2, d, k
+        self.R = R = max(1, int(rotate))
         dev = "cuda"
         g = torch.Generator(device=dev).manual_seed(seed)
         # hidden ~ N(0,1) [M, 256] through a Xavier-uniform 256 -> H*d_key query projection
         d_model = 256
-        hidden = torch.randn((M, d_model), generator=g, device=dev)
+        hidden = torch.randn((R * M, d_model), generator=g, device=dev)
         lim = math.sqrt(6.0 / (d_model + H * d_key))
         w_q = (torch.rand((d_model, H * d_key), generator=g, device=dev) * 2 - 1) * lim
-        self.q = (hidden @ w_q).reshape(M, H, 2, self.half).contiguous()
+        self.q = (hidden @ w_q).reshape(R * M, H, 2, self.half).contiguous()
         self.sub_keys = torch.randn((H, 2, n, self.half), generator=g, device=dev) * (self.half ** -0.5)
         if values is None:
             values = torch.empty((n * n, d), dtype=torch.float16, device=dev)
@@ -125,77 +134,100 @@ class Lookup:
         self.ws = torch.empty(max(1, self.ws_bytes), dtype=u8, device=dev)
         self.topk_ws_bytes = L.mpl_score_topk_workspace_bytes(M, H, n, self.half, k)
         self.topk_ws = torch.empty(max(1, self.topk_ws_bytes), dtype=u8, device=dev)
-        self.sub_idx = torch.empty((M, H, 2, k), dtype=i32, device=dev)
-        self.sub_scores = torch.empty((M, H, 2, k), dtype=f32, device=dev)
-        self.flat_idx = torch.empty((M, H, k), dtype=i32, device=dev)
-        self.slots = torch.empty((M, H, k), dtype=i32, device=dev)
-        self.weights = torch.empty((M, H, k), dtype=f32, device=dev)
-        self.out = torch.empty((M, d), dtype=f32, device=dev)
+        self.sub_idx = torch.empty((R * M, H, 2, k), dtype=i32, device=dev)
+        self.sub_scores = torch.empty((R * M, H, 2, k), dtype=f32, device=dev)
+        self.flat_idx = torch.empty((R * M, H, k), dtype=i32, device=dev)
+        self.slots = torch.empty((R * M, H, k), dtype=i32, device=dev)
+        self.weights = torch.empty((R * M, H, k), dtype=f32, device=dev)
+        self.out = torch.empty((R * M, d), dtype=f32, device=dev)
 
     @property
     def stream(self):
         # queried per call: under graph capture the current stream is the capture stream
         return self.torch.cuda.current_stream().cuda_stream
 
-    def pack(self):
+    def _p(self, t, i):
+        """Device address of batch i % R of a [R*M, ...] buffer."""
+        b = i % self.R
+        return t.data_ptr() + b * (t.numel() // self.R) * t.element_size()
+
+    def pack(self, i=0):
         p = self._lib.ptr
         # inference needs only the packed operand, not the fp32 normalised keys
         self._lib.check(self.L.mpl_pack_keys(p(self.sub_keys), self.H, self.n, self.half, self._lib.MPL_F16,
                                              None, p(self.packed), self.stream), "pack")
 
-    def select(self):
+    def select(self, i=0):
         # raw queries: the scoring kernel l2-normalises them (memory.py:136)
-        p = self._lib.ptr
+        b, p = self._p, self._lib.ptr
         self._lib.check(self.L.mpl_score_select(
-            p(self.q), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
+            b(self.q, i), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
             self._lib.MPL_F16,
-            self.T, None, 0.0, p(self.ws), self.ws_bytes, p(self.sub_idx), p(self.sub_scores), p(self.flat_idx),
-            p(self.slots), p(self.weights), self.stream), "select")
+            self.T, None, 0.0, p(self.ws), self.ws_bytes, b(self.sub_idx, i), b(self.sub_scores, i),
+            b(self.flat_idx, i), b(self.slots, i), b(self.weights, i), self.stream), "select")
 
-    def topk(self):
+    def topk(self, i=0):
         # stage 1 alone (score_topk_kernel, plus split merges when the keys are split)
-        p = self._lib.ptr
+        b, p = self._p, self._lib.ptr
         self._lib.check(self.L.mpl_score_topk(
-            p(self.q), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
-            self._lib.MPL_F16, self.T, None, 0.0, p(self.topk_ws), self.topk_ws_bytes, p(self.sub_idx),
-            p(self.sub_scores), self.stream), "topk")
+            b(self.q, i), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
+            self._lib.MPL_F16, self.T, None, 0.0, p(self.topk_ws), self.topk_ws_bytes, b(self.sub_idx, i),
+            b(self.sub_scores, i), self.stream), "topk")
 
-    def gather(self):
-        p = self._lib.ptr
-        self._lib.check(self.L.mpl_gather_wsum(p(self.values), self._lib.MPL_F16, self.n * self.n, self.d,
-                                               p(self.slots), p(self.weights), self.M, self.H * self.k, 0,
-                                               p(self.out), self.stream), "gather")
+    def gather(self, i=0):
+        b = self._p
+        self._lib.check(self.L.mpl_gather_wsum(self.values.data_ptr(), self._lib.MPL_F16, self.n * self.n, self.d,
+                                               b(self.slots, i), b(self.weights, i), self.M, self.H * self.k, 0,
+                                               b(self.out, i), self.stream), "gather")
 
-    def lookup(self):
+    def lookup(self, i=0):
         # selection and value read in one call: at H = 4, k = 16 the pair
         # stage and the weighted row sum run as one kernel
-        p = self._lib.ptr
+        b, p = self._p, self._lib.ptr
         self._lib.check(self.L.mpl_lookup(
-            p(self.q), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
-            self._lib.MPL_F16, self.T, None, 0.0, p(self.ws), self.ws_bytes, p(self.sub_idx), p(self.sub_scores),
-            p(self.flat_idx), p(self.slots), p(self.weights), p(self.values), self._lib.MPL_F16, self.d, 0,
-            p(self.out), self.stream), "lookup")
+            b(self.q, i), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
+            self._lib.MPL_F16, self.T, None, 0.0, p(self.ws), self.ws_bytes, b(self.sub_idx, i),
+            b(self.sub_scores, i), b(self.flat_idx, i), b(self.slots, i), b(self.weights, i),
+            self.values.data_ptr(), self._lib.MPL_F16, self.d, 0, b(self.out, i), self.stream), "lookup")
 
-    def step(self):
-        self.pack()
-        self.lookup()
+    def step(self, i=0):
+        self.pack(i)
+        self.lookup(i)
+
+    def fill_slots(self):
+        """Every batch's slots and weights (for timing the read alone)."""
+        for i in range(self.R):
+            self.select(i)
+
+
+# Token batches the headline cycles through: 4 x 8,192 tokens of queries
+# (134 MB) so that no step reads the queries the step before it read.
+HEADLINE_ROTATE = 4
+
+
+def large_rotation(M):
+    """Batches a 67M-slot workload cycles through: enough that the rows one
+    replay reads total about 1 GB (4x the 256 MB Infinity Cache), at most 64."""
+    per_call = M * 4 * 16 * 256 * 2
+    return int(max(1, min(64, math.ceil((1 << 30) / per_call))))
 
 
 def time_loop(torch, fn, iters, warmup):
-    """Average ms per call of fn: `iters` calls captured in one HIP graph,
-    replayed between HIP events on the current stream (the stream every entry
-    point is launched on), so host launch overhead is not measured."""
+    """Average ms per call of fn(i): `iters` calls (i = 0 .. iters-1, so a
+    rotating workload cycles through its batches) captured in one HIP graph
+    and replayed between HIP events on the current stream (the stream every
+    entry point is launched on), so host launch overhead is not measured."""
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
-        for _ in range(max(1, warmup)):
-            fn()
+        for i in range(max(1, warmup)):
+            fn(i)
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
-        for _ in range(iters):
-            fn()
+        for i in range(iters):
+            fn(i)
     graph.replay()  # warm replay
     torch.cuda.synchronize()
     a = torch.cuda.Event(enable_timing=True)
@@ -210,6 +242,7 @@ def time_loop(torch, fn, iters, warmup):
 
 
 def kernel_breakdown(torch, lk, iters):
+    lk.fill_slots()
     return {
         "pack_keys_ms": time_loop(torch, lk.pack, iters, 3),
         "score_select_ms": time_loop(torch, lk.select, iters, 3),
@@ -219,26 +252,46 @@ def kernel_breakdown(torch, lk, iters):
     }
 
 
+RIDGE = MFMA_F16_PEAK_TFLOPS * 1e12 / (HBM_PEAK_GBS * 1e9)  # FLOP per byte where the two roofs meet
+
+
+def topk_algorithmic(lk):
+    """Algorithmic work of one stage-1 launch (score_topk_kernel) on M tokens:
+    2*H*2*n*half FLOP of scoring per token (2048*n at d_key = 256) and the
+    bytes it must move: the fp32 queries read, the fp16 packed sub-keys read
+    once, the k (score, id) pairs per codebook written."""
+    flops = 2.0 * lk.H * 2 * lk.n * lk.half * lk.M
+    nbytes = lk.M * lk.H * 2 * lk.half * 4 + lk.H * 2 * lk.n * lk.half * 2 + lk.M * lk.H * 2 * lk.k * 8
+    return flops, nbytes
+
+
 def roofline_for(lk, br):
-    """The roofline of the stage-1 scoring kernel (score_topk_kernel, MFMA),
-    timed alone through mpl_score_topk: at the text-study shape the keys are
-    not split, so that call is exactly one launch of the kernel.  The headline
-    step runs norm_pack, score_topk and the fused stage-2 + value read
-    (pair_read_k16); score_topk is the longest of the three under the kernel
-    trace.  The value read's HBM roofline is reported at 67M slots, where the
-    table cannot sit in the Infinity Cache."""
-    score_flops = 2.0 * lk.H * 2 * lk.n * lk.half * lk.M  # 2048*n per token at d_key=256
-    s = score_flops / (br["score_topk_ms"] * 1e-3) / 1e12
-    return {"kernel": "score_topk", "bound": "mfma", "achieved": s, "peak": MFMA_F16_PEAK_TFLOPS,
-            "unit": "TFLOP/s", "frac": s / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("score_topk"),
-            "algorithmic_flops": score_flops}
+    """The roofline of the stage-1 scoring kernel (score_topk_kernel), timed
+    alone through mpl_score_topk: at the text-study shape the keys are not
+    split, so that call is exactly one launch of the kernel.  Its bound is
+    set by its arithmetic intensity against the MI355X ridge (312 FLOP/B):
+    at n = 512 it is about 200 FLOP/B, so HBM; at n = 8,192 with 4,096 tokens
+    it is far above the ridge, so MFMA."""
+    flops, nbytes = topk_algorithmic(lk)
+    sec = br["score_topk_ms"] * 1e-3
+    if flops / nbytes >= RIDGE:
+        a = flops / sec / 1e12
+        return {"kernel": "score_topk", "bound": "mfma", "achieved": a, "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": a / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("score_topk"),
+                "algorithmic_flops": flops, "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes}
+    a = nbytes / sec / 1e9
+    return {"kernel": "score_topk", "bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": a / HBM_PEAK_GBS, "traffic": measured_traffic("score_topk"), "algorithmic_bytes": nbytes,
+            "algorithmic_flops": flops, "flop_per_byte": flops / nbytes,
+            "mfma_frac": flops / sec / 1e12 / MFMA_F16_PEAK_TFLOPS}
 
 
 def gather_roofline(lk, br):
     gb = lk.M * lk.H * lk.k * lk.d * 2
     a = gb / (br["gather_wsum_ms"] * 1e-3) / 1e9
     return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
-            "algorithmic_bytes": gb}
+            "algorithmic_bytes": gb, "rotating_batches": lk.R,
+            "distinct_row_bytes_per_replay": gb * lk.R}
 
 
 def zipf_slots(M, H, k, N, s=1.1, seed=5):
@@ -286,7 +339,7 @@ def sparse_update_bench(torch, iters):
     acc = torch.zeros(N, device=dev)
     rest = torch.tensor([1e-4], device=dev)
 
-    def step():
+    def step(i=0):
         m = R.merge_fetches(slots, w, g_out, N)
         sg = R.clip_scale(m.row_sq, rest, 1.0)
         R.rowwise_adagrad(values, acc, m.uniq, m.rows, 3e-3, master=master, grad_scale=sg[0:1])
@@ -303,7 +356,7 @@ def sparse_update_bench(torch, iters):
     m1 = torch.zeros((N, d), device=dev)
     m2 = torch.zeros((N, d), device=dev)
 
-    def step_adam():
+    def step_adam(i=0):
         mm = R.merge_fetches(slots, w, g_out, N)
         sg = R.clip_scale(mm.row_sq, rest, 1.0)
         R.lazy_adam(values, m1, m2, mm.uniq, mm.rows, 3e-3, 7, master=master, grad_scale=sg[0:1])
@@ -392,7 +445,7 @@ def key_diversity_bench(torch, iters):
     loss = torch.empty(1, dtype=torch.float32, device="cuda")
     dk = torch.empty_like(keys)
 
-    def fn():
+    def fn(i=0):
         check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, ptr(ws), wsb, ptr(loss), ptr(dk),
                                   _lib.stream_ptr(keys.device)), "mpl_key_diversity")
 
@@ -421,15 +474,15 @@ def host_pool_bench(torch, iters):
     lk.select()
     staged = {}
 
-    def stage():
+    def stage(i=0):
         staged["rows"], staged["inv"], staged["num"] = pool.stage(lk.slots)
 
-    def read():
+    def read(i=0):
         _lib.check(L.mpl_gather_wsum(_lib.ptr(staged["rows"]), _lib.MPL_F16, staged["rows"].shape[0], d,
                                      _lib.ptr(staged["inv"]), _lib.ptr(lk.weights), M, H * k, 0, _lib.ptr(lk.out),
                                      lk.stream), "gather")
 
-    def step():
+    def step(i=0):
         lk.pack()
         lk.select()
         stage()
@@ -446,7 +499,7 @@ def host_pool_bench(torch, iters):
     flat = lk.slots.reshape(-1)
     uniq = torch.unique(flat).to(torch.int32)
     grads = torch.randn((uniq.numel(), d), device="cuda") * 1e-3
-    t_upd = time_loop(torch, lambda: pool.update(uniq, grads, 1, 1e-3), iters, 2)
+    t_upd = time_loop(torch, lambda i=0: pool.update(uniq, grads, 1, 1e-3), iters, 2)
     upd_bytes = uniq.numel() * (2 * d * 2 + 2 * 4)  # fp16 row read + write, acc read + write, across the link
     del pool
     return {"workload": "text-study lookup (8,192 tokens, H=4, k=16) on a 1,048,576-slot fp16 table in pinned "
@@ -491,35 +544,128 @@ def generation_bench(torch):
     return out
 
 
-def cpu_baseline(seconds: float):
-    """The numpy oracle (oracle/lookup.py) on the host cores: the same layer
-    shape (262,144 fp16 slots, H=4, d_key=256, k=16) on batches of 1,024
-    tokens, repeated for about `seconds` seconds."""
+def host_info():
+    """Host cores and model (os.cpu_count() and lscpu)."""
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() in ("Model name", "Socket(s)", "Core(s) per socket", "Thread(s) per core", "CPU(s)"):
+                info["lscpu_" + key.strip().lower().replace("(s)", "s").replace(" ", "_")] = val.strip()
+    except Exception as e:  # pragma: no cover
+        info["lscpu_error"] = str(e)
+    return info
+
+
+def cpu_workers():
+    """Worker threads for the CPU baselines: every core this process may use
+    (OMP_NUM_THREADS caps it where the box shares its cores between GPUs)."""
+    n = os.cpu_count() or 1
+    cap = os.environ.get("OMP_NUM_THREADS")
+    return max(1, min(n, int(cap))) if cap and cap.isdigit() else n
+
+
+def _cpu_run(task, chunks, seconds, workers):
+    """Calls task(i) for i = 0, 1, ... on `workers` threads (numpy releases
+    the GIL in its sorts and BLAS calls; BLAS itself is held to one thread
+    per worker) until `seconds` have passed; returns (tasks done, seconds)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+
+    done, t0 = 0, time.perf_counter()
+    with threadpool_limits(1), ThreadPoolExecutor(workers) as ex:
+        while True:
+            list(ex.map(task, range(done, done + chunks)))
+            done += chunks
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                return done, el
+
+
+def cpu_lookup_baseline(seconds: float, *, n, values_dtype, label):
+    """The numpy oracle (oracle/lookup.py, memory.py:132-193) on the host
+    cores: scoring on BLAS, top-k by partition and stable sort, the weighted
+    row read, on chunks of 256 tokens, one chunk per worker at a time."""
     from oracle import lookup as ol
 
-    try:
-        from threadpoolctl import threadpool_info
-
-        blas_threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
-    except Exception:  # pragma: no cover
-        blas_threads = 1
+    workers = cpu_workers()
     rng = np.random.default_rng(0)
-    H, n, half, k, d, M = 4, 512, 128, 16, 256, 1024
+    H, half, k, d, chunk = 4, 128, 16, 256, 256
     keys = (rng.standard_normal((H, 2, n, half)) * half ** -0.5).astype(np.float32)
-    values = (rng.standard_normal((n * n, d)) * 0.02).astype(np.float16)
+    values = (rng.standard_normal((n * n, d)) * 0.02).astype(values_dtype)
     w_q = ((rng.random((256, H * 2 * half)) * 2 - 1) * math.sqrt(6.0 / (256 + H * 2 * half))).astype(np.float32)
-    tokens, t0, runs = 0, time.perf_counter(), 0
-    while True:
-        q = (rng.standard_normal((M, 256)).astype(np.float32) @ w_q).reshape(M, H, 2 * half)
-        ol.lookup_forward(q, keys, values, np.log(10.0), top_k_=k, with_dense=False)
-        tokens += M
-        runs += 1
-        el = time.perf_counter() - t0
-        if el >= seconds or runs >= 64:
-            break
-    return {"value": tokens / el, "unit": "tokens/s", "cores": int(blas_threads), "kind": "port",
-            "sample": f"{runs} batches x {M} tokens of the 262,144-slot fp16 layer (numpy oracle, "
-                      f"BLAS scoring on {blas_threads} threads, sort-based top-k single-threaded), {el:.1f} s"}
+    qs = [(np.random.default_rng(100 + i).standard_normal((chunk, 256)).astype(np.float32) @ w_q)
+          .reshape(chunk, H, 2 * half) for i in range(workers)]
+
+    def task(i):
+        ol.lookup_forward(qs[i % workers], keys, values, np.log(10.0), top_k_=k, with_dense=False)
+
+    done, el = _cpu_run(task, workers, seconds, workers)
+    return {"value": done * chunk / el, "unit": "tokens/s", "cores": workers, "kind": "port",
+            "sample": f"{done} chunks x {chunk} tokens of the {label} layer ({n * n:,} {np.dtype(values_dtype).name} "
+                      f"slots, H=4, d_key=256, k=16) through the numpy oracle on {workers} threads "
+                      f"(BLAS one thread each), {el:.1f} s",
+            "host": host_info()}
+
+
+def cpu_train_baseline(seconds: float):
+    """The training step of the 262,144-slot layer through the numpy oracle:
+    forward with Gumbel routing noise (memory.py:132-193), the balance loss's
+    statistics (memory.py:196-213), the backward (oracle/backward.py) on
+    chunks of 256 tokens across the cores, then the sparse row merge, clip and
+    row-wise Adagrad of the step's fetches (train.py:146-172, 395-416).  One
+    step = 2,048 tokens."""
+    from oracle import backward as ob
+    from oracle import lookup as ol
+    from oracle import rows as orows
+
+    workers = cpu_workers()
+    rng = np.random.default_rng(0)
+    H, n, half, k, d, chunk, per_step = 4, 512, 128, 16, 256, 256, 2048
+    N = n * n
+    keys = (rng.standard_normal((H, 2, n, half)) * half ** -0.5).astype(np.float32)
+    values = (rng.standard_normal((N, d)) * 0.02).astype(np.float16)
+    master = values.astype(np.float32)
+    acc = np.zeros(N, np.float32)
+    q = rng.standard_normal((per_step, H, 2 * half)).astype(np.float32)
+    g = (rng.standard_normal((per_step, d)) * 1e-3).astype(np.float32)
+    gum = -np.log(-np.log(rng.random((per_step, H, 2, n)).clip(1e-30, 1 - 1e-7))).astype(np.float32)
+    parts = per_step // chunk
+
+    def chunk_fb(j):
+        sl = slice(j * chunk, (j + 1) * chunk)
+        res = ol.lookup_forward(q[sl], keys, values, np.log(10.0), top_k_=k, gumbel=gum[sl], noise_coef=1.0)
+        f = ol.aux_stats(res, n=n, noisy=True)["_f"]
+        ob.lookup_backward(res, values, g[sl], n=n, g_balance=0.01, f=f, dtype=np.float32)
+        return res["slots"], res["weights"]
+
+    from concurrent.futures import ThreadPoolExecutor
+
+    from threadpoolctl import threadpool_limits
+
+    steps, t0 = 0, time.perf_counter()
+    with threadpool_limits(1), ThreadPoolExecutor(workers) as ex:
+        while True:
+            outs = list(ex.map(chunk_fb, range(parts)))
+            slots = np.concatenate([o[0] for o in outs])
+            wts = np.concatenate([o[1] for o in outs])
+            uniq, rows = orows.fetched_row_grads([slots], [wts], [g], N)
+            sg, _ = orows.clip_scale(1e-4, rows, 1.0)
+            orows.rowwise_adagrad(values, acc, uniq, rows * np.float32(sg), 3e-3, master=master)
+            steps += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+    return {"value": steps * per_step / el, "unit": "tokens/s", "cores": min(workers, parts), "kind": "port",
+            "sample": f"{steps} steps x {per_step} tokens of the 262,144-slot training layer (fp16 table, fp32 "
+                      f"master): oracle forward with noise + balance statistics + backward on {parts} chunks of "
+                      f"{chunk} tokens across {min(workers, parts)} threads, then the row merge, clip and "
+                      f"row-wise Adagrad (single thread), {el:.1f} s",
+            "host": host_info()}
 
 
 def main():
@@ -538,8 +684,24 @@ def main():
         copy_calibration(torch)
         return
 
-    # ---- headline: 262,144 slots, 8,192 tokens
-    lk = Lookup(torch, L, M=8192, H=4, n=512, d_key=256, d=256, k=16, seed=0)
+    if args.only == "text_study":
+        lk = Lookup(torch, L, M=8192, H=4, n=512, d_key=256, d=256, k=16, seed=0, rotate=HEADLINE_ROTATE)
+        print(json.dumps({"only": args.only, "ms_per_step": time_loop(torch, lk.step, args.steps, args.warmup),
+                          "kernels": kernel_breakdown(torch, lk, args.steps)}))
+        return
+    if args.only == "pool_67M_4096":
+        vals = torch.empty((8192 * 8192, 256), dtype=torch.float16, device="cuda")
+        vals.normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(3))
+        lk3 = Lookup(torch, L, M=4096, H=4, n=8192, d_key=256, d=256, k=16, seed=4106, values=vals,
+                     rotate=large_rotation(4096))
+        br3 = kernel_breakdown(torch, lk3, args.steps)
+        print(json.dumps({"only": args.only, "rotating_batches": lk3.R, "kernels": br3,
+                          "gather_roofline": gather_roofline(lk3, br3)}))
+        return
+
+    # ---- headline: 262,144 slots, 8,192 tokens per step, successive steps on
+    # different token batches (as a layer sees them)
+    lk = Lookup(torch, L, M=8192, H=4, n=512, d_key=256, d=256, k=16, seed=0, rotate=HEADLINE_ROTATE)
     ms = time_loop(torch, lk.step, args.steps, args.warmup)
     value = lk.M / (ms * 1e-3)
     br = kernel_breakdown(torch, lk, max(20, args.steps // 2))
@@ -553,10 +715,11 @@ def main():
         vals.normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(3))
         sweep = {}
         for M in (1, 16, 256, 4096):
-            lk3 = Lookup(torch, L, M=M, H=4, n=n3, d_key=256, d=256, k=16, seed=10 + M, values=vals)
+            lk3 = Lookup(torch, L, M=M, H=4, n=n3, d_key=256, d=256, k=16, seed=10 + M, values=vals,
+                         rotate=large_rotation(M))
             it = max(10, args.steps // (4 if M == 4096 else 2))
             ms3 = time_loop(torch, lk3.step, it, max(3, args.warmup // 4))
-            entry = {"ms_per_step": ms3, "tokens_per_s": M / (ms3 * 1e-3)}
+            entry = {"ms_per_step": ms3, "tokens_per_s": M / (ms3 * 1e-3), "rotating_batches": lk3.R}
             # decode with fixed sub-keys (generation): MemoryPool caches the
             # packed keys per parameter version, so a step is mpl_lookup alone
             entry["cached_keys_ms_per_step"] = time_loop(torch, lk3.lookup, it, 3)
@@ -564,11 +727,14 @@ def main():
                 br3 = kernel_breakdown(torch, lk3, it)
                 entry["kernels"] = br3
                 entry["gather_roofline"] = gather_roofline(lk3, br3)
+                entry["score_topk_roofline"] = roofline_for(lk3, br3)
+                entry["score_topk_roofline"]["traffic"] = None
             sweep[str(M)] = entry
             del lk3
         del vals
         torch.cuda.empty_cache()
-        large = {"workload": "decode lookup, 67,108,864 fp16 slots (34 GB), H=4, d_key=256, k=16, d_value=256",
+        large = {"workload": "decode lookup, 67,108,864 fp16 slots (34 GB), H=4, d_key=256, k=16, d_value=256; "
+                             "calls cycle through rotating_batches token batches",
                  "by_tokens": sweep}
 
     train = div = None
@@ -580,7 +746,15 @@ def main():
     generation = None if args.no_generate else generation_bench(torch)
     host = None if args.no_host else host_pool_bench(torch, max(5, args.steps // 20))
 
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = cpu_more = None
+    if not args.no_cpu:
+        cpu = cpu_lookup_baseline(args.cpu_seconds, n=512, values_dtype=np.float16,
+                                  label="text-study")
+        cpu_more = {
+            "fact_task_16k_fp32": cpu_lookup_baseline(args.cpu_seconds / 2, n=128, values_dtype=np.float32,
+                                                      label="fact-task"),
+            "training_262k": cpu_train_baseline(args.cpu_seconds),
+        }
     line = {
         "metric": METRIC,
         "value": value,
@@ -606,6 +780,7 @@ def main():
         "generation_268M": generation,
         "host_pool_1M": host,
         "cpu_baseline": cpu,
+        "cpu_baselines_other": cpu_more,
     }
     print(json.dumps(line))
 
