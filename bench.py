@@ -72,17 +72,20 @@ def parse():
     return ap.parse_args()
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic_text_study_8192.json")
+TRAFFIC_FILES = {
+    "text_study": os.path.join(ROOT, "profiles", "traffic_text_study_8192.json"),
+    "pool_67M_4096": os.path.join(ROOT, "profiles", "traffic_67M_4096.json"),
+}
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` on the 8,192-token workload, from the
-    rocprofv3 FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (already
-    scaled by the copy-kernel calibration); None when not recorded."""
+def measured_traffic(kernel, workload="text_study"):
+    """HBM bytes per launch of `kernel` on a workload, from the rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs recorded in profiles/ (already scaled by the
+    copy-kernel calibration); None when not recorded."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(TRAFFIC_FILES[workload]) as f:
             rec = json.load(f)
-    except (OSError, ValueError):
+    except (OSError, ValueError, KeyError):
         return None
     k = rec.get("kernels", {}).get(kernel)
     return None if k is None else k.get("hbm_bytes_per_launch")
@@ -241,6 +244,29 @@ def time_loop(torch, fn, iters, warmup):
     return ms
 
 
+def time_direct(torch, fn, iters, warmup):
+    """Average ms per call of fn(i) launched back to back on the current
+    stream (no graph), between HIP events on that stream: per call, the
+    kernel's duration plus the launch gap between dispatches.  Used for a
+    single kernel's roofline; the host enqueues faster than these kernels
+    run, so the queue never drains."""
+    for i in range(max(1, warmup)):
+        fn(i)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    best = None
+    for _ in range(3):
+        a.record()
+        for i in range(iters):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        ms = a.elapsed_time(b) / iters
+        best = ms if best is None else min(best, ms)
+    return best
+
+
 def kernel_breakdown(torch, lk, iters):
     lk.fill_slots()
     return {
@@ -265,7 +291,7 @@ def topk_algorithmic(lk):
     return flops, nbytes
 
 
-def roofline_for(lk, br):
+def roofline_for(lk, br, workload="text_study"):
     """The roofline of the stage-1 scoring kernel (score_topk_kernel), timed
     alone through mpl_score_topk: at the text-study shape the keys are not
     split, so that call is exactly one launch of the kernel.  Its bound is
@@ -277,20 +303,28 @@ def roofline_for(lk, br):
     if flops / nbytes >= RIDGE:
         a = flops / sec / 1e12
         return {"kernel": "score_topk", "bound": "mfma", "achieved": a, "peak": MFMA_F16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": a / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("score_topk"),
+                "unit": "TFLOP/s", "frac": a / MFMA_F16_PEAK_TFLOPS, "traffic": measured_traffic("score_topk", workload),
                 "algorithmic_flops": flops, "algorithmic_bytes": nbytes, "flop_per_byte": flops / nbytes}
     a = nbytes / sec / 1e9
     return {"kernel": "score_topk", "bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": a / HBM_PEAK_GBS, "traffic": measured_traffic("score_topk"), "algorithmic_bytes": nbytes,
+            "frac": a / HBM_PEAK_GBS, "traffic": measured_traffic("score_topk", workload), "algorithmic_bytes": nbytes,
             "algorithmic_flops": flops, "flop_per_byte": flops / nbytes,
             "mfma_frac": flops / sec / 1e12 / MFMA_F16_PEAK_TFLOPS}
 
 
-def gather_roofline(lk, br):
+def gather_roofline(torch, lk, br, iters):
+    """HBM roofline of the value read alone (gather_wsum_kernel, one launch of
+    mpl_gather_wsum) over rotating batches: algorithmic bytes = the fetched
+    rows, M * H * k * d * 2 B.  ``achieved`` is from back-to-back launches
+    (the kernel duration plus the dispatch gap); the graph-replayed figure of
+    the kernel breakdown, which adds a graph node's gap, is given beside it."""
     gb = lk.M * lk.H * lk.k * lk.d * 2
-    a = gb / (br["gather_wsum_ms"] * 1e-3) / 1e9
-    return {"bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": a / HBM_PEAK_GBS,
-            "algorithmic_bytes": gb, "rotating_batches": lk.R,
+    ms = time_direct(torch, lk.gather, iters, lk.R)
+    a = gb / (ms * 1e-3) / 1e9
+    return {"kernel": "gather_wsum", "bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": a / HBM_PEAK_GBS, "ms_per_launch": ms, "algorithmic_bytes": gb,
+            "traffic": measured_traffic("gather_wsum", "pool_67M_4096") if (lk.n, lk.M) == (8192, 4096) else None,
+            "graph_replay_GBs": gb / (br["gather_wsum_ms"] * 1e-3) / 1e9, "rotating_batches": lk.R,
             "distinct_row_bytes_per_replay": gb * lk.R}
 
 
@@ -696,7 +730,7 @@ def main():
                      rotate=large_rotation(4096))
         br3 = kernel_breakdown(torch, lk3, args.steps)
         print(json.dumps({"only": args.only, "rotating_batches": lk3.R, "kernels": br3,
-                          "gather_roofline": gather_roofline(lk3, br3)}))
+                          "gather_roofline": gather_roofline(torch, lk3, br3, args.steps)}))
         return
 
     # ---- headline: 262,144 slots, 8,192 tokens per step, successive steps on
@@ -726,9 +760,8 @@ def main():
             if M == 4096:
                 br3 = kernel_breakdown(torch, lk3, it)
                 entry["kernels"] = br3
-                entry["gather_roofline"] = gather_roofline(lk3, br3)
-                entry["score_topk_roofline"] = roofline_for(lk3, br3)
-                entry["score_topk_roofline"]["traffic"] = None
+                entry["gather_roofline"] = gather_roofline(torch, lk3, br3, 4 * it)
+                entry["score_topk_roofline"] = roofline_for(lk3, br3, "pool_67M_4096")
             sweep[str(M)] = entry
             del lk3
         del vals

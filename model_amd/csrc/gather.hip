@@ -16,7 +16,7 @@ __global__ __launch_bounds__(kGatherThreads) void gather_wsum_kernel(
   const int64_t m = (int64_t)blockIdx.x * (kGatherThreads / kWave) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (m >= M) return;
-  Wsum<V, VR> acc;
+  Wsum<V, VR, 32> acc;
   const uint4* base = (const uint4*)values;
   for (int r0 = 0; r0 < R; r0 += kWave) {
     const int rr = r0 + lane;
