@@ -64,7 +64,7 @@ def parse():
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-generate", action="store_true")
     ap.add_argument("--no-host", action="store_true")
-    ap.add_argument("--only", choices=["text_study", "pool_67M_4096"], default=None,
+    ap.add_argument("--only", choices=["text_study", "pool_67M_4096", "host_file"], default=None,
                     help="run one workload alone (for profiler runs) and print its timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
@@ -544,6 +544,65 @@ def host_pool_bench(torch, iters):
             "update_link_GBs": upd_bytes / (t_upd * 1e-3) / 1e9}
 
 
+def host_pool_file_bench(torch, iters):
+    """The host tier's file mode (the reference's pool directory of .npy
+    files): the text-study lookup's unique rows read from a 1,048,576-slot
+    fp16 values.npy by the library's row-file reader into pinned staging and
+    copied to the GPU, with the page cache warm and after evicting it, and
+    the row-wise Adagrad step of those rows (read, GPU step on the staged
+    rows, write back)."""
+    import shutil
+    import tempfile
+
+    from model_amd import _lib
+    from model_amd import host_pool as hp
+
+    L = _lib.lib()
+    M, H, n, d_key, d, k = 8192, 4, 1024, 256, 256, 16
+    N = n * n
+    tmp = tempfile.mkdtemp(prefix="mpl_pool_", dir=os.environ.get("TMPDIR", "/tmp"))
+    try:
+        pool = hp.HostPool(N, d, path=tmp, dtype=np.float16, seed=0, optimizer="rowwise_adagrad")
+        lk = Lookup(torch, L, M=M, H=H, n=n, d_key=d_key, d=d, k=k, seed=0,
+                    values=torch.empty((16, d), dtype=torch.float16, device="cuda"))
+        lk.pack()
+        lk.select()
+        _, _, num = pool.stage(lk.slots)
+        torch.cuda.synchronize()
+        U = int(num.item())
+
+        def timed(fn, reps, before=None):
+            best = None
+            for _ in range(reps):
+                if before is not None:
+                    before()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                fn()
+                torch.cuda.synchronize()
+                dt = time.perf_counter() - t0
+                best = dt if best is None else min(best, dt)
+            return best * 1e3
+
+        warm = timed(lambda: pool.stage(lk.slots), iters)
+        cold = timed(lambda: pool.stage(lk.slots), 3, before=pool.evict_page_cache)
+        uniq = torch.unique(lk.slots.reshape(-1)).to(torch.int32)
+        grads = torch.randn((uniq.numel(), d), device="cuda") * 1e-3
+        upd = timed(lambda: pool.update(uniq, grads, 1, 1e-3), max(3, iters // 2))
+        pool.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    row_bytes = d * 2
+    return {"workload": "text-study lookup (8,192 tokens, H=4, k=16) reading a 1,048,576-slot fp16 values.npy "
+                        "(file mode of the host tier), and the row-wise Adagrad step of the touched rows",
+            "unique_rows": U, "stage_warm_ms": warm, "stage_warm_GBs": U * row_bytes / (warm * 1e-3) / 1e9,
+            "stage_after_evict_ms": cold, "stage_after_evict_GBs": U * row_bytes / (cold * 1e-3) / 1e9,
+            "update_ms": upd, "update_rows_per_s": uniq.numel() / (upd * 1e-3),
+            "note": "evict_page_cache is advisory (posix_fadvise DONTNEED); where the file system keeps the "
+                    "pages (e.g. tmpfs) the 'after evict' read is a page-cache read too",
+            "io_threads": hp._IO_THREADS, "dir": os.path.dirname(tmp)}
+
+
 def generation_bench(torch):
     """Batched greedy generation through the backbone mirror
     (model_amd/model.py, generate.py) with two memory layers on a
@@ -723,6 +782,9 @@ def main():
         print(json.dumps({"only": args.only, "ms_per_step": time_loop(torch, lk.step, args.steps, args.warmup),
                           "kernels": kernel_breakdown(torch, lk, args.steps)}))
         return
+    if args.only == "host_file":
+        print(json.dumps({"only": args.only, "host_pool_file_1M": host_pool_file_bench(torch, 5)}))
+        return
     if args.only == "pool_67M_4096":
         vals = torch.empty((8192 * 8192, 256), dtype=torch.float16, device="cuda")
         vals.normal_(0.0, 0.02, generator=torch.Generator(device="cuda").manual_seed(3))
@@ -777,7 +839,10 @@ def main():
         div = key_diversity_bench(torch, max(5, args.steps // 20))
 
     generation = None if args.no_generate else generation_bench(torch)
-    host = None if args.no_host else host_pool_bench(torch, max(5, args.steps // 20))
+    host = host_file = None
+    if not args.no_host:
+        host = host_pool_bench(torch, max(5, args.steps // 20))
+        host_file = host_pool_file_bench(torch, 5)
 
     cpu = cpu_more = None
     if not args.no_cpu:
@@ -812,6 +877,7 @@ def main():
         "key_diversity_67M": div,
         "generation_268M": generation,
         "host_pool_1M": host,
+        "host_pool_file_1M": host_file,
         "cpu_baseline": cpu,
         "cpu_baselines_other": cpu_more,
     }

@@ -118,6 +118,30 @@ int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* pa
                float* out, void* stream);
 
 /*
+ * Row files of the host tier's file mode (host_pool.py:90-108, 117-165: the
+ * reference's .npy memmaps, read and written by numpy on host threads).  A
+ * row file is `rows` rows of `row_bytes` bytes starting at byte data_offset
+ * of the file at `path` (the data of an .npy array).  mpl_rowfile_read copies
+ * rows ids[0..count) into dst (packed, in id order); mpl_rowfile_write
+ * writes src's packed rows to those ids; both split the list over up to
+ * `threads` host threads, copying through a shared mapping of the file
+ * (runs of consecutive ids as one copy; mpl_rowfile_sync makes written rows
+ * durable).  Ids outside [0, rows) fail with MPL_EINVAL
+ * before any transfer.  dst/src are host memory (pinned memory lets the GPU
+ * use it directly).  Host code only: no device work, no stream.
+ */
+int mpl_rowfile_open(const char* path, int64_t data_offset, int64_t row_bytes, int64_t rows, int writable,
+                     void** handle);
+int mpl_rowfile_read(void* handle, const int64_t* ids, int64_t count, void* dst, int threads);
+int mpl_rowfile_write(void* handle, const int64_t* ids, int64_t count, const void* src, int threads);
+int mpl_rowfile_sync(void* handle);
+/* host_pool.py:190-204: writes the file's dirty rows back, then asks the OS to
+ * drop its pages from the page cache (advisory), so the next reads come from
+ * the drive. */
+int mpl_rowfile_evict(void* handle);
+int mpl_rowfile_close(void* handle);
+
+/*
  * No counterpart in the reference: for callers that cannot allocate device
  * memory (code under HIP graph capture, serving loops that forbid hipMalloc).
  * mpl_lookup with the same arguments and outputs, minus the workspace: the

@@ -30,6 +30,12 @@ SIGNATURES = {
     "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
     "mpl_lookup": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
                         _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
+    "mpl_rowfile_open": (_I, [C.c_char_p, _I64, _I64, _I64, _I, C.POINTER(C.c_void_p)]),
+    "mpl_rowfile_read": (_I, [_P, _P, _I64, _P, _I]),
+    "mpl_rowfile_write": (_I, [_P, _P, _I64, _P, _I]),
+    "mpl_rowfile_sync": (_I, [_P]),
+    "mpl_rowfile_evict": (_I, [_P]),
+    "mpl_rowfile_close": (_I, [_P]),
     "mpl_lookup_static_scratch_bytes": (_SZ, []),
     "mpl_lookup_static": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F,
                                _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),

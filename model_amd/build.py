@@ -1,8 +1,9 @@
 """Builds libmpl.so (the C-ABI library of include/mpl.h) for gfx950 with hipcc.
 
 Usage: ``python -m model_amd.build`` (or ``__graft_entry__.build()``).  Each
-``csrc/*.hip`` file is compiled to an object in ``_build/`` in parallel, then
-linked into ``model_amd/libmpl.so`` (written atomically).
+``csrc/*.hip`` file (hipcc) and host-only ``csrc/*.cpp`` file (g++) is
+compiled to an object in ``_build/`` in parallel, then linked into
+``model_amd/libmpl.so`` (written atomically).
 """
 
 from __future__ import annotations
@@ -40,9 +41,24 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libmpl.so)")
 
 
+# Host-only C++ sources (csrc/*.cpp: no device code) are built with the host
+# compiler.
+HOST_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-Wall", "-Wno-unused-function"]
+
+
+def host_cxx() -> str:
+    for cand in (os.environ.get("CXX"), shutil.which("g++"), shutil.which("c++")):
+        if cand and os.path.exists(cand):
+            return cand
+    raise RuntimeError("no host C++ compiler (g++) found")
+
+
 def _compile(src: str, cc: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [cc, *FLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [host_cxx(), *HOST_FLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [cc, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
@@ -52,11 +68,11 @@ def _compile(src: str, cc: str) -> str:
 def build(verbose: bool = False, jobs: int = 8) -> str:
     cc = hipcc()
     os.makedirs(OBJ, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     with cf.ThreadPoolExecutor(max_workers=max(1, min(jobs, len(srcs)))) as ex:
         objs = list(ex.map(lambda s: _compile(s, cc), srcs))
     tmp = LIB + f".tmp{os.getpid()}"
-    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
+    cmd = [cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", "-o", tmp, *objs]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -2,8 +2,8 @@
 (mpl_unique_slots) against numpy's unique, row copies from device and pinned
 host tables (mpl_gather_rows), fetch in both modes, a MemoryPool reading a
 host pool against the same table in HBM (bit-exact: the same rows summed in
-the same order), and the pinned-table optimizer step on the GPU against the
-reference's host-thread step (host_pool.py:134-165)."""
+the same order), and the pool optimizer step (host_pool.py:134-165) in RAM
+and file mode against the trainer's optimizers restated in oracle/rows.py."""
 
 import ctypes
 
@@ -15,6 +15,7 @@ from model_amd import _lib
 from model_amd import host_pool as hp
 from model_amd import rows as R
 from model_amd.memory import MemoryPool
+from oracle import rows as orow
 from tests.gpu_helpers import make_params, zipf_slots
 
 pytestmark = pytest.mark.gpu
@@ -149,29 +150,55 @@ def test_memory_pool_on_host_equals_hbm_table(gpu_lib, shuffle, dtype):
         host_pool.apply({"params": hparams}, q.clone().requires_grad_(True), sparse_grad=False)
 
 
+@pytest.mark.parametrize("mode", ["ram", "file"])
 @pytest.mark.parametrize("optimizer,dtype", [("rowwise_adagrad", np.float32), ("rowwise_adagrad", np.float16),
                                              ("adam", np.float32), ("adam", np.float16)])
-def test_pinned_update_on_gpu_matches_host_step(gpu_lib, optimizer, dtype):
-    """The GPU step on the pinned rows against host_pool.py's numpy step on
-    an identical pool, three steps with padding and a clip factor."""
+def test_update_matches_trainer_optimizer(gpu_lib, tmp_path, mode, optimizer, dtype):
+    """Three steps on overlapping row sets with padding entries and a clip
+    factor, against oracle/rows.py (train.py:412-426; the pool's step s is
+    the trainer's 0-based step s - 1).  RAM mode updates the pinned rows in
+    place; file mode stages them from the .npy files and writes them back."""
     N, d = 3000, 64
-    a = hp.HostPool(N, d, dtype=dtype, seed=7, optimizer=optimizer)
-    b = hp.HostPool(N, d, dtype=dtype, seed=7, optimizer=optimizer)
+    pool = hp.HostPool(N, d, path=None if mode == "ram" else str(tmp_path / "pool"), dtype=dtype, seed=7,
+                       optimizer=optimizer)
+    vals = np.asarray(pool.values).copy()
+    acc = np.zeros(N, np.float32)
+    m = np.zeros((N, d), np.float32)
+    v = np.zeros((N, d), np.float32)
     rng = np.random.default_rng(1)
     for step in (1, 2, 3):
         uniq = np.concatenate([np.sort(rng.choice(N, 900, replace=False)), [N] * 5]).astype(np.int32)
+        rng.shuffle(uniq)
         grads = rng.standard_normal((uniq.size, d)).astype(np.float32)
-        scale = torch.tensor([0.5], device="cuda")
-        a.update(torch.as_tensor(uniq, device="cuda"), torch.as_tensor(grads, device="cuda"), step, 0.01,
-                 grad_scale=scale)
-        b.update(uniq, grads * np.float32(0.5), step, 0.01)
+        lr = 0.01 * step
+        if step == 2:  # numpy inputs, as the reference's trainer hands them over
+            pool.update(uniq, grads * np.float32(0.5), step, lr)
+        else:
+            pool.update(torch.as_tensor(uniq, device="cuda"), torch.as_tensor(grads, device="cuda"), step, lr,
+                        grad_scale=torch.tensor([0.5], device="cuda"))
+        if optimizer == "rowwise_adagrad":
+            orow.rowwise_adagrad(vals, acc, uniq, grads * np.float32(0.5), lr)
+        else:
+            orow.lazy_adam(vals, m, v, uniq, grads * np.float32(0.5), lr, step - 1)
     torch.cuda.synchronize()
     tol = dict(rtol=2e-6, atol=1e-6) if dtype == np.float32 else dict(rtol=2e-3, atol=1e-4)
-    np.testing.assert_allclose(np.asarray(a.values).astype(np.float64), np.asarray(b.values).astype(np.float64), **tol)
-    for key in ("acc", "m", "v"):
-        if getattr(a, key) is not None:
-            x, y = np.asarray(getattr(a, key)), np.asarray(getattr(b, key))
-            np.testing.assert_allclose(x, y, rtol=2e-6, atol=1e-6 * np.abs(y).max())
+    np.testing.assert_allclose(np.asarray(pool.values).astype(np.float64), vals.astype(np.float64), **tol)
+    if optimizer == "rowwise_adagrad":
+        np.testing.assert_allclose(np.asarray(pool.acc), acc, rtol=2e-6)
+    else:
+        np.testing.assert_allclose(np.asarray(pool.m), m, rtol=2e-6, atol=1e-6 * np.abs(m).max())
+        np.testing.assert_allclose(np.asarray(pool.v), v, rtol=2e-6, atol=1e-6 * np.abs(v).max())
+    if mode == "file":
+        # the rows written back are in the files, and a snapshot of them reloads
+        np.testing.assert_array_equal(np.load(str(tmp_path / "pool" / "values.npy")), np.asarray(pool.values))
+        pool.save(str(tmp_path / "snap"))
+        other = hp.HostPool(N, d, path=str(tmp_path / "other"), dtype=dtype, seed=8, optimizer=optimizer)
+        other.load(str(tmp_path / "snap"))
+        for key in ("values", "acc", "m", "v"):
+            if getattr(pool, key) is not None:
+                np.testing.assert_array_equal(np.asarray(getattr(other, key)), np.asarray(getattr(pool, key)))
+        with pytest.raises(ValueError):
+            pool.update(np.array([3, 3], np.int32), np.ones((2, d), np.float32), 4, 0.01)
 
 
 def test_sparse_row_update_on_host_pool(gpu_lib):
