@@ -130,7 +130,7 @@ class Lookup:
             values = torch.empty((n * n, d), dtype=torch.float16, device=dev)
             values.normal_(0.0, 0.02, generator=g)
         self.values = values
-        self.T = 10.0
+        self.T = torch.full((1,), 10.0, device=dev)  # the clamped temperature, a device scalar
         f32, i32, u8 = torch.float32, torch.int32, torch.uint8
         self.packed = torch.empty(L.mpl_packed_keys_bytes(H, n, self.half, _lib.MPL_F16), dtype=u8, device=dev)
         self.ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, self.half, k)
@@ -166,7 +166,7 @@ class Lookup:
         self._lib.check(self.L.mpl_score_select(
             b(self.q, i), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
             self._lib.MPL_F16,
-            self.T, None, 0.0, p(self.ws), self.ws_bytes, b(self.sub_idx, i), b(self.sub_scores, i),
+            p(self.T), None, None, p(self.ws), self.ws_bytes, b(self.sub_idx, i), b(self.sub_scores, i),
             b(self.flat_idx, i), b(self.slots, i), b(self.weights, i), self.stream), "select")
 
     def topk(self, i=0):
@@ -174,7 +174,7 @@ class Lookup:
         b, p = self._p, self._lib.ptr
         self._lib.check(self.L.mpl_score_topk(
             b(self.q, i), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
-            self._lib.MPL_F16, self.T, None, 0.0, p(self.topk_ws), self.topk_ws_bytes, b(self.sub_idx, i),
+            self._lib.MPL_F16, p(self.T), None, None, p(self.topk_ws), self.topk_ws_bytes, b(self.sub_idx, i),
             b(self.sub_scores, i), self.stream), "topk")
 
     def gather(self, i=0):
@@ -189,7 +189,7 @@ class Lookup:
         b, p = self._p, self._lib.ptr
         self._lib.check(self.L.mpl_lookup(
             b(self.q, i), self._lib.MPL_Q_RAW, None, p(self.packed), self.M, self.H, self.n, self.half, self.k,
-            self._lib.MPL_F16, self.T, None, 0.0, p(self.ws), self.ws_bytes, b(self.sub_idx, i),
+            self._lib.MPL_F16, p(self.T), None, None, p(self.ws), self.ws_bytes, b(self.sub_idx, i),
             b(self.sub_scores, i), b(self.flat_idx, i), b(self.slots, i), b(self.weights, i),
             self.values.data_ptr(), self._lib.MPL_F16, self.d, 0, b(self.out, i), self.stream), "lookup")
 

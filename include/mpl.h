@@ -17,6 +17,10 @@
  *     *_workspace_bytes() query;
  *   - return 0 on success, otherwise an MPL_E* code, with a message for the
  *     calling thread in mpl_last_error();
+ *   - scalars that change from step to step in training (the clamped
+ *     temperature, the routing-noise coefficient) are device fp32 scalars
+ *     (`const float*`), so a training step needs no host read and can be
+ *     captured in a HIP graph;
  *   - tensors are dense row-major in the shapes given; M = number of query
  *     tokens, H = heads, n = sub-keys per codebook, half = d_key / 2,
  *     k = top_k, N = n*n slots, d = d_value.
@@ -67,7 +71,8 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
 
 /*
  * memory.py:136-178: cosine scores of the queries [M,H,2,half] against the
- * packed keys, times `temperature` (already clamped, memory.py:143-146) and,
+ * packed keys, times `temperature` (a device fp32 scalar, already clamped,
+ * memory.py:143-146) and,
  * with query_scale, times q_len (memory.py:151-152).  `queries` is either
  *   query_mode MPL_Q_NORMALIZED: unit rows in score_dtype (fp16 for MPL_F16,
  *     fp32 for MPL_F32, e.g. from mpl_l2_normalize); q_len [M,H,2] is an
@@ -77,7 +82,9 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
  *     MPL_Q_RAW_SCALED the scores are also scaled by
  *     q_len = sqrt(sum q^2 + 1e-6) / sqrt(half), written to q_len if not NULL.
  * Optional routing noise select = scores + noise_coef *
- * gumbel with gumbel [M,H,2,n] fp32 (memory.py:155-159, NULL = no noise);
+ * gumbel with gumbel [M,H,2,n] fp32 (memory.py:155-159, NULL = no noise)
+ * and noise_coef a device fp32 scalar (routing_noise * noise_scale; read
+ * only with gumbel);
  * exact stage-1 top-k per codebook (ties: lowest sub-key index), exact
  * stage-2 top-k over the k*k candidates (ties: lowest flat index
  * rank_a*k + rank_b, memory.py:171), softmax of the clean slot scores.
@@ -92,7 +99,7 @@ int mpl_pack_keys(const float* sub_keys, int H, int n, int half, int score_dtype
 size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int half, int k);
 int mpl_score_select(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                      int64_t M, int H, int n, int half, int k, int score_dtype,
-                     float temperature, const float* gumbel, float noise_coef,
+                     const float* temperature, const float* gumbel, const float* noise_coef,
                      void* workspace, size_t workspace_bytes,
                      int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
                      int32_t* slots, float* weights, void* stream);
@@ -110,7 +117,7 @@ int mpl_score_select(const void* queries, int query_mode, float* q_len, const vo
  */
 int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                int64_t M, int H, int n, int half, int k, int score_dtype,
-               float temperature, const float* gumbel, float noise_coef,
+               const float* temperature, const float* gumbel, const float* noise_coef,
                void* workspace, size_t workspace_bytes,
                int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
                int32_t* slots, float* weights,
@@ -155,7 +162,7 @@ int mpl_rowfile_close(void* handle);
 size_t mpl_lookup_static_scratch_bytes(void);
 int mpl_lookup_static(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                       int64_t M, int H, int n, int half, int k, int score_dtype,
-                      float temperature, const float* gumbel, float noise_coef,
+                      const float* temperature, const float* gumbel, const float* noise_coef,
                       int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
                       int32_t* slots, float* weights,
                       const void* values, int values_dtype, int d, int shuffle_reads,
@@ -172,7 +179,7 @@ int mpl_lookup_static(const void* queries, int query_mode, float* q_len, const v
 size_t mpl_score_topk_workspace_bytes(int64_t M, int H, int n, int half, int k);
 int mpl_score_topk(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                    int64_t M, int H, int n, int half, int k, int score_dtype,
-                   float temperature, const float* gumbel, float noise_coef,
+                   const float* temperature, const float* gumbel, const float* noise_coef,
                    void* workspace, size_t workspace_bytes,
                    int32_t* sub_idx, float* sub_scores, void* stream);
 
@@ -322,7 +329,7 @@ int mpl_lookup_bwd_route(const float* g_out, const void* values, int values_dtyp
 int mpl_lookup_bwd_queries(const float* q, const float* q_len, const float* k_hat,
                            const int32_t* sub_idx, const float* d_sub, const float* sub_scores,
                            const float* dq_hat_extra, const float* dlen_extra, int64_t M, int H,
-                           int n, int half, int k, float temperature, float* d_queries, void* stream);
+                           int n, int half, int k, const float* temperature, float* d_queries, void* stream);
 
 /*
  * d_sub_keys [H,2,n,half] (the raw sub_keys' gradient): dk_hat[hc,key] =
@@ -334,7 +341,7 @@ int mpl_lookup_bwd_queries(const float* q, const float* q_len, const float* k_ha
 size_t mpl_lookup_bwd_keys_workspace_bytes(int64_t M, int H, int n, int half, int k);
 int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, const float* q_len,
                         const int32_t* sub_idx, const float* d_sub, const float* dk_hat_extra,
-                        int64_t M, int H, int n, int half, int k, float temperature,
+                        int64_t M, int H, int n, int half, int k, const float* temperature,
                         void* workspace, size_t workspace_bytes, float* d_sub_keys, void* stream);
 
 /*
@@ -406,7 +413,7 @@ int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_idx, int64_t
  */
 size_t mpl_balance_state_bytes(int64_t M, int H);
 int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
-                    int64_t M, int H, int n, int half, int k, float temperature, void* state, float* loss,
+                    int64_t M, int H, int n, int half, int k, const float* temperature, void* state, float* loss,
                     void* stream);
 
 /*
@@ -434,7 +441,7 @@ size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half);
 int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
                          const int32_t* sub_idx, const float* d_sub, const float* clean_counts, const void* state,
                          const float* g_balance, int balance_temperature_grad, int query_scale, int64_t M, int H,
-                         int n, int half, int k, float temperature, void* workspace, size_t workspace_bytes,
+                         int n, int half, int k, const float* temperature, void* workspace, size_t workspace_bytes,
                          float* dq_hat, float* dk_hat, float* dlen, float* dlogt, void* stream);
 
 #ifdef __cplusplus

@@ -25,10 +25,10 @@ SIGNATURES = {
     "mpl_packed_keys_bytes": (_SZ, [_I, _I, _I, _I]),
     "mpl_pack_keys": (_I, [_P, _I, _I, _I, _I, _P, _P, _P]),
     "mpl_score_select_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
-    "mpl_score_select": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
+    "mpl_score_select": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _SZ,
                               _P, _P, _P, _P, _P, _P]),
     "mpl_gather_wsum": (_I, [_P, _I, _I64, _I, _P, _P, _I64, _I, _I, _P, _P]),
-    "mpl_lookup": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ,
+    "mpl_lookup": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _SZ,
                         _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mpl_rowfile_open": (_I, [C.c_char_p, _I64, _I64, _I64, _I, C.POINTER(C.c_void_p)]),
     "mpl_rowfile_read": (_I, [_P, _P, _I64, _P, _I]),
@@ -37,7 +37,7 @@ SIGNATURES = {
     "mpl_rowfile_evict": (_I, [_P]),
     "mpl_rowfile_close": (_I, [_P]),
     "mpl_lookup_static_scratch_bytes": (_SZ, []),
-    "mpl_lookup_static": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F,
+    "mpl_lookup_static": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P,
                                _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mpl_gumbel_noise": (_I, [_U64, _I64, _I, _P, _P]),
     "mpl_unique_slots_workspace_bytes": (_SZ, [_I64, _I64]),
@@ -45,7 +45,7 @@ SIGNATURES = {
     "mpl_gather_rows": (_I, [_P, _I, _I64, _I, _P, _I64, _P, _P, _P]),
     "mpl_host_device_pointer": (_I, [_P, C.POINTER(C.c_void_p)]),
     "mpl_score_topk_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
-    "mpl_score_topk": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _F, _P, _F, _P, _SZ, _P, _P, _P]),
+    "mpl_score_topk": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P, _P, _P]),
     "mpl_merge_rows_workspace_bytes": (_SZ, [_I64, _I, _I64]),
     "mpl_merge_rows": (_I, [_P, _P, _I64, _I, _P, _I, _I64, _P, _SZ, _P, _P, _P, _P, _I, _P]),
     "mpl_clip_scale_workspace_bytes": (_SZ, []),
@@ -53,9 +53,9 @@ SIGNATURES = {
     "mpl_row_adagrad": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I, _I64, _F, _P, _P]),
     "mpl_row_adam": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I, _I64, _F, _I, _P, _P]),
     "mpl_lookup_bwd_route": (_I, [_P, _P, _I, _I64, _I, _P, _P, _P, _P, _I64, _I, _I, _I, _P, _P, _P, _P]),
-    "mpl_lookup_bwd_queries": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _F, _P, _P]),
+    "mpl_lookup_bwd_queries": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _P, _P, _P]),
     "mpl_lookup_bwd_keys_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
-    "mpl_lookup_bwd_keys": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _F, _P, _SZ, _P, _P]),
+    "mpl_lookup_bwd_keys": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _P, _P, _SZ, _P, _P]),
     "mpl_sum": (_I, [_P, _I64, _P, _P, _P]),
     "mpl_l2_normalize_bwd": (_I, [_P, _P, _I64, _I, _F, _P, _P, _P]),
     "mpl_key_diversity_workspace_bytes": (_SZ, [_I, _I, _I]),
@@ -63,9 +63,9 @@ SIGNATURES = {
     "mpl_revive_keys": (_I, [_P, _P, _P, _I64, _P, _P, _I, _I, _I, _F, _F, _P, _P]),
     "mpl_route_counts": (_I, [_P, _P, _I64, _I, _I, _I, _P, _P, _P, _P]),
     "mpl_balance_state_bytes": (_SZ, [_I64, _I]),
-    "mpl_balance_fwd": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "mpl_balance_fwd": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _P, _P, _P, _P]),
     "mpl_lookup_bwd_dense_workspace_bytes": (_SZ, [_I64, _I, _I, _I]),
-    "mpl_lookup_bwd_dense": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I64, _I, _I, _I, _I, _F, _P, _SZ,
+    "mpl_lookup_bwd_dense": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I64, _I, _I, _I, _I, _P, _P, _SZ,
                                   _P, _P, _P, _P, _P]),
 }
 

@@ -140,7 +140,7 @@ struct BalFwdParams {
   const uint4* packed;    // packed sub-keys (fp16 layout)
   const float* counts;    // clean counts [HC, n]
   float inv_mk;           // 1 / (M k)
-  float T;
+  const float* T;         // device scalar: the clamped temperature
   int scaled;             // T_eff = T * q_len
   int64_t M;
   int HC, n, half, nblk;
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_fwd_kernel(BalFwdParams p
 #pragma unroll
   for (int c = 0; c < NCH; ++c) qop[c] = MF::scale_q(x[c], rn);
   const float rho = p.scaled ? sqrtf(tot) / sqrtf((float)p.half) : 1.f;
-  const float t2 = p.T * rho * kLog2e;
+  const float t2 = *p.T * rho * kLog2e;
 
   const float* cnt = p.counts + (int64_t)hc * p.n;
   const uint4* kb = p.packed + (int64_t)hc * p.nblk * TILE;
@@ -376,8 +376,8 @@ __global__ __launch_bounds__(256) void bwd_max_kernel(const float* __restrict__ 
 __global__ __launch_bounds__(256) void bwd_scale_kernel(const float* __restrict__ counts,
                                                         const float2* __restrict__ part, int nparts, int n,
                                                         int HC, float inv_mk, const float* __restrict__ g, float coef,
-                                                        float T, int btg, int qs, float* __restrict__ sigma,
-                                                        float* __restrict__ S) {
+                                                        const float* __restrict__ Tp, int btg, int qs,
+                                                        float* __restrict__ sigma, float* __restrict__ S) {
   __shared__ float red[3][256];
   const int hc = blockIdx.x, tid = threadIdx.x;
   float fm = 0.f, dm = 0.f, qm = 0.f;
@@ -403,6 +403,7 @@ __global__ __launch_bounds__(256) void bwd_scale_kernel(const float* __restrict_
       const float p2 = exp2f(floorf(log2f(fmaxf((float)n * 0.25f, 1.f))));
       sigma[hc] = fmax > 0.f ? p2 / fmax : 1.f;
     }
+    const float T = *Tp;
     const float rho_r = qs ? red[2][0] : 1.f;
     const float rho_b = (btg && qs) ? red[2][0] : 1.f;
     float bound = T * rho_r * red[1][0];
@@ -421,7 +422,7 @@ struct BalGradParams {
   const float* sigma;   // [HC]
   const float* g;       // d loss / d balance (device scalar)
   float inv_mk, coef;   // 1 / (M k), n / (HC M)
-  float T;
+  const float* T;       // device scalar: the clamped temperature (DQ / DK; null for Div)
   int64_t M;
   int HC, n, half;
   int64_t fblk, sblk;  // blocks of 32 rows on the fixed / streamed side
@@ -460,6 +461,7 @@ template <int MODE, int HP>
 __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams p) {
   constexpr bool DK = MODE != kModeDQ;  // the fixed side is sub-keys
   constexpr bool DIV = MODE == kModeDiv;
+  const float Tv = DIV ? 0.f : *p.T;  // Div mode has no temperature (p.T null)
   constexpr int NCH = HP / 16;
   constexpr int ND = (HP + 31) / 32;
   constexpr int TN = NCH * kWave, TT = ND * 2 * kWave, TILE = TN + TT;
@@ -527,7 +529,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       const float sc = p.qlen_rt != nullptr ? p.qlen_rt[m * p.HC + hc] : 1.f;
       rrel[i] = (int)rel;
       rq[i] = qlo;
-      rval[i] = p.d_sub[o] * sc * p.T;
+      rval[i] = p.d_sub[o] * sc * Tv;
     }
   };
   auto rstore = [&](int x) __attribute__((always_inline)) {
@@ -645,7 +647,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   }
   // DQ: c T (rho) / sigma * acc; DK: S * acc; Div: coef * acc.  Rows of
   // the output are the fixed rows
-  float scale = DIV ? p.coef : (MODE == kModeDK ? p.dk_scale[hc] : cc * p.T / sig);
+  float scale = DIV ? p.coef : (MODE == kModeDK ? p.dk_scale[hc] : cc * Tv / sig);
   if (!DK && p.rho != nullptr) scale *= p.rho[(valid ? my_f : 0) * p.HC + hc];
   if (!DK && p.u != nullptr) {
     const float ut = usum + partner(usum, par);
@@ -683,9 +685,10 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float4* __restrict
 
 // dlen[m, hc] = T u (query_scale); part[m, hc] = T rho u (d log_t terms).
 __global__ __launch_bounds__(256) void balance_temp_kernel(const float* __restrict__ u, const float* __restrict__ rho,
-                                                           int64_t M, int HC, float T, float* __restrict__ dlen,
-                                                           float* __restrict__ part) {
+                                                           int64_t M, int HC, const float* __restrict__ Tp,
+                                                           float* __restrict__ dlen, float* __restrict__ part) {
   __shared__ float red[256];
+  const float T = *Tp;
   const int64_t total = M * HC;
   float acc = 0.f;
   for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
@@ -834,14 +837,14 @@ extern "C" size_t mpl_balance_state_bytes(int64_t M, int H) {
 }
 
 extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
-                               int64_t M, int H, int n, int half, int k, float temperature, void* state,
+                               int64_t M, int H, int n, int half, int k, const float* temperature, void* state,
                                float* loss, void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_balance_fwd: bad shape");
   MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
               "mpl_balance_fwd: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
-  MPL_REQUIRE(loss != nullptr && (M == 0 || (queries && packed_keys && clean_counts && state)), MPL_EINVAL,
-              "mpl_balance_fwd: null buffer");
+  MPL_REQUIRE(loss != nullptr && (M == 0 || (queries && packed_keys && clean_counts && state && temperature)),
+              MPL_EINVAL, "mpl_balance_fwd: null buffer");
   hipStream_t s = (hipStream_t)stream;
   const int HC = 2 * H;
   if (M == 0) {
@@ -882,7 +885,7 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
                                     const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
                                     const float* clean_counts, const void* state, const float* g_balance,
                                     int balance_temperature_grad, int query_scale, int64_t M, int H, int n,
-                                    int half, int k, float temperature, void* workspace, size_t workspace_bytes,
+                                    int half, int k, const float* temperature, void* workspace, size_t workspace_bytes,
                                     float* dq_hat, float* dk_hat, float* dlen, float* dlogt, void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_lookup_bwd_dense: bad shape");
@@ -906,7 +909,7 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
       fill_zero_kernel<<<grid_for(M * HC * half, 256), 256, 0, s>>>(dq_hat, M * HC * half);
     return check_launch("mpl_lookup_bwd_dense");
   }
-  MPL_REQUIRE(q_hat && k_hat && packed_keys, MPL_EINVAL, "mpl_lookup_bwd_dense: null buffer");
+  MPL_REQUIRE(q_hat && k_hat && packed_keys && temperature, MPL_EINVAL, "mpl_lookup_bwd_dense: null buffer");
   MPL_REQUIRE(!bal || (clean_counts && state && dq_hat), MPL_EINVAL,
               "mpl_lookup_bwd_dense: the balance term needs clean_counts, state and dq_hat");
   const BwdLayout L = bwd_layout(M, H, n, half);

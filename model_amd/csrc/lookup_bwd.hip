@@ -173,10 +173,11 @@ __global__ __launch_bounds__(kBwdThreads) void queries_bwd_kernel(
     const float* __restrict__ q, const float* __restrict__ q_len, const float* __restrict__ k_hat,
     const int32_t* __restrict__ sub_idx, const float* __restrict__ d_sub, const float* __restrict__ sub_scores,
     const float* __restrict__ extra, const float* __restrict__ dlen_extra, int64_t rows, int HC, int n, int half,
-    int k, float T, float eps, float* __restrict__ dq) {
+    int k, const float* __restrict__ Tp, float eps, float* __restrict__ dq) {
   const int64_t row = ((int64_t)blockIdx.x * kBwdThreads + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   if (row >= rows) return;
+  const float T = *Tp;
   const int hc = (int)(row % HC);
   const float ql = q_len != nullptr ? q_len[row] : 1.f;
   const float scale = T * ql;
@@ -246,10 +247,12 @@ __global__ __launch_bounds__(kBwdThreads) void queries_bwd_kernel(
 
 // ------------------------------------------------------------------- keys
 __global__ void keys_bwd_prep_kernel(const int32_t* __restrict__ sub_idx, const float* __restrict__ d_sub,
-                                     const float* __restrict__ q_len, int64_t P, int HC, int n, int k, float T,
-                                     int32_t* __restrict__ kid, float* __restrict__ kw) {
+                                     const float* __restrict__ q_len, int64_t P, int HC, int n, int k,
+                                     const float* __restrict__ Tp, int32_t* __restrict__ kid,
+                                     float* __restrict__ kw) {
   const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (p >= P) return;
+  const float T = *Tp;
   const int64_t row = p / k;  // (m, h, c)
   const int hc = (int)(row % HC);
   const int key = sub_idx[p];
@@ -386,12 +389,12 @@ extern "C" int mpl_lookup_bwd_route(const float* g_out, const void* values, int 
 extern "C" int mpl_lookup_bwd_queries(const float* q, const float* q_len, const float* k_hat, const int32_t* sub_idx,
                                       const float* d_sub, const float* sub_scores, const float* dq_hat_extra,
                                       const float* dlen_extra, int64_t M, int H, int n, int half, int k,
-                                      float temperature, float* d_queries, void* stream) {
+                                      const float* temperature, float* d_queries, void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H > 0 && n > 0 && k > 0 && half > 0, MPL_EINVAL, "mpl_lookup_bwd_queries: bad sizes");
   MPL_REQUIRE(half <= 2 * kWave, MPL_EUNSUPPORTED, "mpl_lookup_bwd_queries: half must be <= 128");
   if (M == 0) return MPL_OK;
-  MPL_REQUIRE(q && k_hat && sub_idx && d_sub && d_queries && (q_len == nullptr || sub_scores), MPL_EINVAL,
+  MPL_REQUIRE(q && k_hat && sub_idx && d_sub && d_queries && temperature && (q_len == nullptr || sub_scores), MPL_EINVAL,
               "mpl_lookup_bwd_queries: null buffer");
   const int64_t rows = M * H * 2;
   queries_bwd_kernel<<<(unsigned)cdiv(rows, kBwdThreads / kWave), kBwdThreads, 0, (hipStream_t)stream>>>(
@@ -407,7 +410,7 @@ extern "C" size_t mpl_lookup_bwd_keys_workspace_bytes(int64_t M, int H, int n, i
 
 extern "C" int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, const float* q_len,
                                    const int32_t* sub_idx, const float* d_sub, const float* dk_hat_extra, int64_t M,
-                                   int H, int n, int half, int k, float temperature, void* workspace,
+                                   int H, int n, int half, int k, const float* temperature, void* workspace,
                                    size_t workspace_bytes, float* d_sub_keys, void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H > 0 && n > 0 && k > 0 && half > 0, MPL_EINVAL, "mpl_lookup_bwd_keys: bad sizes");
@@ -427,7 +430,7 @@ extern "C" int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, co
                                                d_sub_keys);
     return check_launch("mpl_lookup_bwd_keys");
   }
-  MPL_REQUIRE(q_hat && sub_idx && d_sub, MPL_EINVAL, "mpl_lookup_bwd_keys: null buffer");
+  MPL_REQUIRE(q_hat && sub_idx && d_sub && temperature, MPL_EINVAL, "mpl_lookup_bwd_keys: null buffer");
   const KeysLayout L = keys_layout(M, H, n, half, k);
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_lookup_bwd_keys: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);

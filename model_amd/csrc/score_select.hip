@@ -79,7 +79,8 @@ struct ScoreParams {
   int query_mode;       // MPL_Q_NORMALIZED / MPL_Q_RAW / MPL_Q_RAW_SCALED
   const uint4* packed;  // packed keys
   const float* gumbel;  // [M, HC, n] or null
-  float T, noise_coef;
+  const float* T;           // device scalar: the clamped temperature
+  const float* noise_coef;  // device scalar routing_noise * noise_scale (read with noise only)
   int noise_vec;  // gumbel rows 16-byte aligned (base aligned, n % 4 == 0)
   int64_t M;
   int HC, n, half, k, nblk, splits, blk_per_split;
@@ -249,6 +250,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   const int lane = tid & 63;
   const int par = lane >> 5;  // key parity class of this lane
   const int hc = blockIdx.x % p.HC;
+  const float Tv = *p.T;
+  const float coef = NOISE ? *p.noise_coef : 0.f;
   const int split = (blockIdx.x / p.HC) % p.splits;
   const int64_t qb = blockIdx.x / (p.HC * p.splits);
   const int64_t q0 = qb * kQueriesPerGroup + wave * kQueriesPerWave;
@@ -477,13 +480,13 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   // With noise, clean_at(c, r) is the clean score of element r; it is
   // recomputed where needed rather than kept in 16 more registers.
   auto clean_at = [&](const f32x16& c, int r) __attribute__((always_inline)) {
-    float v = c[r] * p.T;
+    float v = c[r] * Tv;
     return v * ql;  // ql == 1 without query_scale
   };
   auto lane_scores = [&](int kb, const f32x16& c, const GVec& g, float* sv) __attribute__((always_inline)) {
 #pragma unroll
     for (int r = 0; r < 16; ++r)
-      sv[r] = NOISE ? __builtin_fmaf(p.noise_coef, g[NOISE ? r : 0], clean_at(c, r)) : c[r];
+      sv[r] = NOISE ? __builtin_fmaf(coef, g[NOISE ? r : 0], clean_at(c, r)) : c[r];
     if (kb + 32 > p.n) {  // wave-uniform: only the last block can hold padded keys
 #pragma unroll
       for (int r = 0; r < 16; ++r)
@@ -612,7 +615,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
           clean = st.top.pay[NOISE ? r : 0];
           sel = key_score(kk);
         } else {
-          clean = key_score(kk) * p.T;
+          clean = key_score(kk) * Tv;
           clean *= ql;  // ql == 1 without query_scale
           sel = clean;
         }
@@ -1248,7 +1251,7 @@ static bool launch_pair_read(const LookupRead& lr, const PairParams& pp, unsigne
 
 static int select_impl(const char* who, bool pair, const void* queries, int query_mode, float* q_len,
                        const void* packed_keys, int64_t M, int H, int n, int half, int k, int score_dtype,
-                       float temperature, const float* gumbel, float noise_coef, void* workspace,
+                       const float* temperature, const float* gumbel, const float* noise_coef, void* workspace,
                        size_t workspace_bytes, int32_t* sub_idx, float* sub_scores, int32_t* flat_idx,
                        int32_t* slots, float* weights, void* stream, const LookupRead* read = nullptr,
                        bool* read_done = nullptr) {
@@ -1266,6 +1269,8 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   if (M == 0) return MPL_OK;
   MPL_REQUIRE(queries && packed_keys && sub_idx && sub_scores && (!pair || (flat_idx && slots && weights)),
               MPL_EINVAL, "%s: null buffer", who);
+  MPL_REQUIRE(temperature != nullptr && (gumbel == nullptr || noise_coef != nullptr), MPL_EINVAL,
+              "%s: null temperature (or noise_coef with gumbel) device scalar", who);
   MPL_REQUIRE(query_mode == MPL_Q_NORMALIZED || query_mode == MPL_Q_RAW || query_mode == MPL_Q_RAW_SCALED,
               MPL_EINVAL, "%s: bad query_mode %d", who, query_mode);
   const bool noise = gumbel != nullptr;
@@ -1401,7 +1406,7 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
 
 extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_len, const void* packed_keys,
                                 int64_t M, int H, int n, int half, int k, int score_dtype,
-                                float temperature, const float* gumbel, float noise_coef,
+                                const float* temperature, const float* gumbel, const float* noise_coef,
                                 void* workspace, size_t workspace_bytes, int32_t* sub_idx,
                                 float* sub_scores, int32_t* flat_idx, int32_t* slots,
                                 float* weights, void* stream) {
@@ -1411,8 +1416,8 @@ extern "C" int mpl_score_select(const void* queries, int query_mode, float* q_le
 }
 
 extern "C" int mpl_score_topk(const void* queries, int query_mode, float* q_len, const void* packed_keys,
-                              int64_t M, int H, int n, int half, int k, int score_dtype, float temperature,
-                              const float* gumbel, float noise_coef, void* workspace, size_t workspace_bytes,
+                              int64_t M, int H, int n, int half, int k, int score_dtype, const float* temperature,
+                              const float* gumbel, const float* noise_coef, void* workspace, size_t workspace_bytes,
                               int32_t* sub_idx, float* sub_scores, void* stream) {
   return select_impl("mpl_score_topk", false, queries, query_mode, q_len, packed_keys, M, H, n, half, k,
                      score_dtype, temperature, gumbel, noise_coef, workspace, workspace_bytes, sub_idx,
@@ -1420,8 +1425,8 @@ extern "C" int mpl_score_topk(const void* queries, int query_mode, float* q_len,
 }
 
 extern "C" int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* packed_keys, int64_t M,
-                          int H, int n, int half, int k, int score_dtype, float temperature, const float* gumbel,
-                          float noise_coef, void* workspace, size_t workspace_bytes, int32_t* sub_idx,
+                          int H, int n, int half, int k, int score_dtype, const float* temperature, const float* gumbel,
+                          const float* noise_coef, void* workspace, size_t workspace_bytes, int32_t* sub_idx,
                           float* sub_scores, int32_t* flat_idx, int32_t* slots, float* weights,
                           const void* values, int values_dtype, int d, int shuffle_reads, float* out,
                           void* stream) {
@@ -1476,8 +1481,8 @@ static int static_scratch(void** addr) {
 extern "C" size_t mpl_lookup_static_scratch_bytes(void) { return kStaticScratchBytes; }
 
 extern "C" int mpl_lookup_static(const void* queries, int query_mode, float* q_len, const void* packed_keys,
-                                 int64_t M, int H, int n, int half, int k, int score_dtype, float temperature,
-                                 const float* gumbel, float noise_coef, int32_t* sub_idx, float* sub_scores,
+                                 int64_t M, int H, int n, int half, int k, int score_dtype, const float* temperature,
+                                 const float* gumbel, const float* noise_coef, int32_t* sub_idx, float* sub_scores,
                                  int32_t* flat_idx, int32_t* slots, float* weights, const void* values,
                                  int values_dtype, int d, int shuffle_reads, float* out, void* stream) {
   clear_error();

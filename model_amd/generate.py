@@ -5,7 +5,11 @@ the backbone with its memory reads (MemoryPool: libmpl.so).  The decode step
 has static shapes (token batch [B], position as a device tensor), so it is
 captured once in a HIP graph and replayed; the next input token (the prompt's
 or the argmax of the step's logits) is chosen on the device, so a whole
-generation is queued without a host round trip per token.
+generation is queued without a host round trip per token.  The reference's
+jitted step takes the parameters on every call; here a generate() call
+re-captures the step when a parameter was replaced or the pool's sub-keys or
+log-temperature changed in place since the capture (weights updated in
+place are read live by the graph).
 """
 
 from __future__ import annotations
@@ -31,6 +35,7 @@ class Generator:
         self.pos = torch.zeros(1, dtype=torch.int64, device=self.device)
         self.logits = None
         self.graph = None
+        self._captured_state = None
         self.use_graph = graph
 
     def _step(self):
@@ -53,10 +58,34 @@ class Generator:
             for t in c.values():
                 t.zero_()
 
+    def _param_state(self):
+        """What a captured step depends on besides its inputs: the storage of
+        every parameter (the graph reads the weights where they were at
+        capture), and the in-place version of the pool's sub-keys and
+        log-temperature (their packed operand and clamped value are computed
+        before capture and baked in)."""
+        flat = []
+
+        def walk(t):
+            if isinstance(t, dict):
+                for k in sorted(t):
+                    walk(t[k])
+            elif isinstance(t, torch.Tensor):
+                flat.append(t.data_ptr())
+
+        walk(self.params)
+        pool = self.params.get("pool", {})
+        frozen = tuple((pool[k].data_ptr(), pool[k]._version) for k in ("sub_keys", "log_temperature") if k in pool)
+        return tuple(flat), frozen
+
     def _ensure_graph(self):
-        if not self.use_graph or self.graph is not None:
+        if not self.use_graph:
             return
-        # warm up on a side stream (key packing, temperature read, workspaces)
+        state = self._param_state()
+        if self.graph is not None and state == self._captured_state:
+            return
+        self.graph = None  # parameters moved or the pool's keys changed: capture again
+        # warm up on a side stream (key packing, temperature, workspaces)
         side = torch.cuda.Stream(self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(side):
@@ -64,9 +93,17 @@ class Generator:
                 self._step()
         torch.cuda.current_stream(self.device).wait_stream(side)
         torch.cuda.synchronize(self.device)
-        self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.logits = self._step()
+        pool = self.model.pool
+        if pool is not None:
+            pool.frozen_under_capture = True  # keys and temperature are fixed while the graph replays
+        try:
+            self.graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph):
+                self.logits = self._step()
+        finally:
+            if pool is not None:
+                pool.frozen_under_capture = False
+        self._captured_state = state
 
     def generate(self, prompt, n_new: int, temperature: float = 0.0, seed: int = 0,
                  keep_logits: bool = True, sync_each_step: bool = False) -> Dict[str, object]:

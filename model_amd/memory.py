@@ -45,30 +45,47 @@ def _dtype_code(dt: torch.dtype) -> int:
     raise TypeError(f"unsupported dtype {dt} (float16 or float32)")
 
 
+def _capturing() -> bool:
+    return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
+
+
 class _KeyCache:
     """Normalised + MFMA-packed sub-keys, rebuilt when the parameter changes
-    (tracked by storage pointer and torch's in-place version counter)."""
+    (tracked by storage pointer and torch's in-place version counter).
+
+    Under HIP graph capture the pack is recorded into the graph (so every
+    replay packs the keys as they are then) unless ``frozen``: a caller that
+    keeps the keys fixed across replays (the generator's decode step) sets it
+    and re-captures when the keys change."""
 
     def __init__(self):
         self.key = None
         self.k_hat = None
         self.packed = None
+        self.frozen = False
 
     def get(self, sub_keys: torch.Tensor, score_code: int):
         key = (sub_keys.data_ptr(), sub_keys._version, tuple(sub_keys.shape), score_code)
+        if _capturing() and not self.frozen:
+            return self._pack(sub_keys, score_code)
         if key != self.key:
-            H, _, n, half = sub_keys.shape
-            L = _lib.lib()
-            nbytes = L.mpl_packed_keys_bytes(H, n, half, score_code)
-            if nbytes == 0:
-                raise _lib.MplError(f"unsupported key shape {tuple(sub_keys.shape)}")
-            src = sub_keys.detach().float().contiguous()
-            k_hat = torch.empty_like(src)
-            packed = torch.empty(nbytes, dtype=torch.uint8, device=src.device)
-            check(L.mpl_pack_keys(ptr(src), H, n, half, score_code, ptr(k_hat), ptr(packed),
-                                  _lib.stream_ptr(src.device)), "mpl_pack_keys")
-            self.key, self.k_hat, self.packed = key, k_hat, packed
+            self.k_hat, self.packed = self._pack(sub_keys, score_code)
+            self.key = key
         return self.k_hat, self.packed
+
+    @staticmethod
+    def _pack(sub_keys: torch.Tensor, score_code: int):
+        H, _, n, half = sub_keys.shape
+        L = _lib.lib()
+        nbytes = L.mpl_packed_keys_bytes(H, n, half, score_code)
+        if nbytes == 0:
+            raise _lib.MplError(f"unsupported key shape {tuple(sub_keys.shape)}")
+        src = sub_keys.detach().float().contiguous()
+        k_hat = torch.empty_like(src)
+        packed = torch.empty(nbytes, dtype=torch.uint8, device=src.device)
+        check(L.mpl_pack_keys(ptr(src), H, n, half, score_code, ptr(k_hat), ptr(packed),
+                              _lib.stream_ptr(src.device)), "mpl_pack_keys")
+        return k_hat, packed
 
 
 class LazyAux(dict):
@@ -171,8 +188,19 @@ class MemoryPool:
         self.score_dtype = score_dtype
         self._keys = _KeyCache()
         self._temp_key = None
-        self._temp_val = None
         self._temp_tensor = None
+
+    @property
+    def frozen_under_capture(self) -> bool:
+        """When True, a HIP graph captured around a lookup reuses the packed
+        keys and temperature computed before the capture instead of
+        recomputing them in the graph (for callers that keep the sub-keys and
+        log_temperature fixed while the graph is replayed)."""
+        return self._keys.frozen
+
+    @frozen_under_capture.setter
+    def frozen_under_capture(self, value: bool) -> None:
+        self._keys.frozen = bool(value)
 
     @property
     def pool_size(self) -> int:
@@ -201,19 +229,19 @@ class MemoryPool:
             raise ValueError(f"values must be [{self.pool_size}, {self.d_value}], got {tuple(values.shape)}")
         return {"params": {"sub_keys": keys, "values": values, "log_temperature": log_t}}
 
-    def temperature(self, log_temperature: torch.Tensor) -> float:
-        """memory.py:143-146 value of the clamped temperature (host float,
-        re-read only when the parameter changes)."""
+    def temperature(self, log_temperature: torch.Tensor) -> torch.Tensor:
+        """memory.py:143-146: the clamped temperature exp(clip(log_t, ln
+        min_temperature, ln max_temperature)) as a device fp32 scalar [1],
+        computed on the device (no host read), cached per parameter version
+        outside graph capture."""
         key = (log_temperature.data_ptr(), log_temperature._version)
-        if key != self._temp_key:
-            lt = float(log_temperature.detach().float().cpu())
-            lo = math.log(self.min_temperature)
-            hi = math.log(self.max_temperature)
-            lt32 = torch.tensor(lt, dtype=torch.float32).clamp(lo, hi)
-            self._temp_val = float(torch.exp(lt32))
-            self._temp_tensor = torch.tensor(self._temp_val, dtype=torch.float32, device=log_temperature.device)
-            self._temp_key = key
-        return self._temp_val
+        if (_capturing() and not self._keys.frozen) or key != self._temp_key:
+            lt = log_temperature.detach().reshape(1).to(torch.float32)
+            t = torch.exp(lt.clamp(math.log(self.min_temperature), math.log(self.max_temperature)))
+            if _capturing() and not self._keys.frozen:
+                return t
+            self._temp_tensor, self._temp_key = t, key
+        return self._temp_tensor
 
     # -------------------------------------------------------------- call
     def apply(self, variables: Dict[str, Any], queries: torch.Tensor, *, train: bool = False,
@@ -257,14 +285,18 @@ class MemoryPool:
         k_hat, packed = self._keys.get(params["sub_keys"], score_code)
         T = self.temperature(params["log_temperature"])
 
-        noise_coef = 0.0
+        noise_coef = None  # device scalar routing_noise * noise_scale (memory.py:157)
         if gumbel is None and train and self.routing_noise > 0:
             # memory.py:156: Gumbel(0,1) over the score shape, one fill pass
             gumbel = torch.empty((M, H, 2, n), dtype=torch.float32, device=dev)
             check(L.mpl_gumbel_noise(routing_seed(rngs), M * H * 2, n, ptr(gumbel), stream), "mpl_gumbel_noise")
         if gumbel is not None:
-            ns = float(noise_scale) if not isinstance(noise_scale, torch.Tensor) else float(noise_scale.detach().cpu())
-            noise_coef = float(self.routing_noise) * ns
+            if isinstance(noise_scale, torch.Tensor):  # an annealed, traced noise_scale stays on the device
+                noise_coef = noise_scale.detach().to(device=dev, dtype=torch.float32).reshape(1) * float(
+                    self.routing_noise)
+            else:
+                noise_coef = torch.full((1,), float(self.routing_noise) * float(noise_scale), dtype=torch.float32,
+                                        device=dev)
             gumbel = gumbel.reshape(M, H, 2, n).float().contiguous()
 
         ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
@@ -285,13 +317,13 @@ class MemoryPool:
             if tuple(values.shape) != (self.pool_size, d):
                 raise ValueError(f"values must be [{self.pool_size}, {d}], got {tuple(values.shape)}")
             check(L.mpl_lookup(ptr(q), q_mode, ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
-                               T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
+                               ptr(T), ptr(gumbel), ptr(noise_coef), ptr(ws), ws_bytes, ptr(sub_idx),
                                ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights),
                                ptr(values), _dtype_code(values.dtype), d, int(bool(shuffle_reads)), ptr(out),
                                stream), "mpl_lookup")
         else:
             check(L.mpl_score_select(ptr(q), q_mode, ptr(q_len), ptr(packed), M, H, n, half, k, score_code,
-                                     T, ptr(gumbel), noise_coef, ptr(ws), ws_bytes, ptr(sub_idx),
+                                     ptr(T), ptr(gumbel), ptr(noise_coef), ptr(ws), ws_bytes, ptr(sub_idx),
                                      ptr(sub_scores), ptr(flat_idx), ptr(slots), ptr(weights), stream),
                   "mpl_score_select")
             # memory.py:182-183 (hp.fetch): the unique rows cross the host
@@ -316,7 +348,7 @@ class MemoryPool:
         aux = LazyAux({
             "slots": slots.reshape(*lead, H, k),
             "weights": weights.reshape(*lead, H, k),
-            "temperature": self._temp_tensor,
+            "temperature": T.reshape(()),
         }, stats, queries=lambda: res["q_hat"], top1_weight=lambda: weights.max(-1).values.mean())
         res.update({
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
@@ -352,7 +384,7 @@ class MemoryPool:
             state = torch.empty(max(L.mpl_balance_state_bytes(M, H), 16), dtype=torch.uint8, device=dev)
             loss = torch.empty(1, dtype=torch.float32, device=dev)
             check(L.mpl_balance_fwd(ptr(res["q"]), scaled, ptr(packed), ptr(clean_counts), M, H, n, half, k,
-                                    float(T), ptr(state), ptr(loss), stream), "mpl_balance_fwd")
+                                    ptr(T), ptr(state), ptr(loss), stream), "mpl_balance_fwd")
             stats.update(balance_loss=loss.reshape(()), _counts=clean_counts, _state=state)
             return stats
         f = clean_counts / (M * k)
@@ -377,8 +409,8 @@ class MemoryPool:
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
         sub_idx = torch.empty((M, H, 2, k), dtype=torch.int32, device=dev)
         sub_scores = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
-        check(L.mpl_score_topk(ptr(q), q_mode, None, ptr(packed), M, H, n, half, k, score_code, T,
-                               None, 0.0, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores), _lib.stream_ptr(dev)),
+        check(L.mpl_score_topk(ptr(q), q_mode, None, ptr(packed), M, H, n, half, k, score_code, ptr(T),
+                               None, None, ptr(ws), ws_bytes, ptr(sub_idx), ptr(sub_scores), _lib.stream_ptr(dev)),
               "mpl_score_topk(clean)")
         return sub_idx
 
@@ -553,7 +585,7 @@ class _LookupFunction(torch.autograd.Function):
             check(L.mpl_lookup_bwd_dense(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
                                          ptr(d_sub), ptr(ctx.internal["_counts"]) if bal else None,
                                          ptr(ctx.internal["_state"]) if bal else None, ptr(gb), int(btg),
-                                         int(bool(pool.query_scale)), M, H, n, half, k, float(T), ptr(ws), wsb,
+                                         int(bool(pool.query_scale)), M, H, n, half, k, ptr(T), ptr(ws), wsb,
                                          ptr(dq_extra), ptr(dk_hat), ptr(dlen_extra), ptr(dlogt_extra), stream),
                   "mpl_lookup_bwd_dense")
             check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
@@ -581,13 +613,13 @@ class _LookupFunction(torch.autograd.Function):
         dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
         check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
                                        ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
-                                       float(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
+                                       ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
         # sub-keys (fp32 scoring or no tokens): sort-by-key segmented sum
         if not dense:
             wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
             ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
             check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
-                                        ptr(dk_extra), M, H, n, half, k, float(T), ptr(ws), wsb, ptr(dk), stream),
+                                        ptr(dk_extra), M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
                   "mpl_lookup_bwd_keys")
         # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
         dlt = torch.empty(1, dtype=torch.float32, device=dev)

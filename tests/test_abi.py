@@ -44,7 +44,7 @@ def test_size_queries_without_gpu():
 
 def test_invalid_arguments_are_reported_not_launched():
     L = _lib.lib()
-    rc = L.mpl_score_select(None, 0, None, None, 10, 4, 8, 128, 20, _lib.MPL_F16, 10.0, None, 0.0,
+    rc = L.mpl_score_select(None, 0, None, None, 10, 4, 8, 128, 20, _lib.MPL_F16, None, None, None,
                             None, 0, None, None, None, None, None, None, None)
     assert rc == 4  # MPL_EUNSUPPORTED: k > n
     assert b"k <= min(n, 32)" in L.mpl_last_error()

@@ -64,3 +64,24 @@ def test_checkpoint_round_trip_drives_the_backbone(gpu_lib):
         a, _ = model.apply(params, toks)
         b, _ = model.apply({"params": back}, toks)
     assert torch.equal(a, b)
+
+
+def test_generator_follows_pool_parameters_changed_in_place(gpu_lib):
+    """The captured decode step bakes in the packed sub-keys and the clamped
+    temperature; after an in-place update of sub_keys or log_temperature (an
+    optimizer step) the next generate() must use the new values, as an eager
+    step does."""
+    cfg = ModelConfig(vocab_size=300, max_len=40, d_model=64, n_heads=4, n_layers=2, ffn_mult=2, n_sub_keys=64,
+                      pool_heads=4, d_key=64, d_value=64, top_k=8, memory_layers=(0, 1))
+    params = MemoryPoolLM(cfg).init(5)
+    prompt = np.random.default_rng(3).integers(0, 300, (4, 10))
+    gen = Generator(cfg, params, batch_size=4, graph=True)
+    before = gen.generate(prompt, n_new=8)
+    pool = params["params"]["pool"]
+    with torch.no_grad():
+        pool["sub_keys"].mul_(-1.0).add_(0.3)  # in place: same storage, new version
+        pool["log_temperature"].add_(1.0)
+    after = gen.generate(prompt, n_new=8)
+    eager = Generator(cfg, params, batch_size=4, graph=False).generate(prompt, n_new=8)
+    assert torch.equal(after["logits"], eager["logits"])
+    assert not torch.equal(after["logits"], before["logits"])

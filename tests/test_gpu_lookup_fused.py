@@ -26,6 +26,7 @@ def _run(M, H, n, d_key, d, k, vdt, shuffle, seed):
     s = torch.cuda.current_stream().cuda_stream
     _lib.check(L.mpl_pack_keys(ptr(keys), H, n, half, _lib.MPL_F16, None, ptr(packed), s), "pack")
     wsb = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
+    T = torch.full((1,), 10.0, device="cuda")  # the clamped temperature, a device scalar
     outs = []
     for fused in (False, True):
         ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
@@ -35,7 +36,7 @@ def _run(M, H, n, d_key, d, k, vdt, shuffle, seed):
              "slots": torch.full((M, H, k), -7, dtype=torch.int32, device="cuda"),
              "weights": torch.full((M, H, k), 7.0, device="cuda"),
              "out": torch.full((M, d), 7.0, device="cuda")}
-        sel = (ptr(q), _lib.MPL_Q_RAW, None, ptr(packed), M, H, n, half, k, _lib.MPL_F16, 10.0, None, 0.0,
+        sel = (ptr(q), _lib.MPL_Q_RAW, None, ptr(packed), M, H, n, half, k, _lib.MPL_F16, ptr(T), None, None,
                ptr(ws), wsb, ptr(o["sub_idx"]), ptr(o["sub_scores"]), ptr(o["flat_idx"]), ptr(o["slots"]),
                ptr(o["weights"]))
         if fused:
@@ -72,9 +73,9 @@ def test_lookup_zero_tokens_and_errors(gpu_lib):
     L = _lib.lib()
     s = torch.cuda.current_stream().cuda_stream
     # M = 0 launches nothing and succeeds
-    assert L.mpl_lookup(None, _lib.MPL_Q_RAW, None, None, 0, 4, 64, 64, 16, _lib.MPL_F16, 10.0, None, 0.0,
+    assert L.mpl_lookup(None, _lib.MPL_Q_RAW, None, None, 0, 4, 64, 64, 16, _lib.MPL_F16, None, None, None,
                         None, 0, None, None, None, None, None, None, _lib.MPL_F16, 256, 0, None, s) == 0
     # a bad values dtype is reported, not launched
-    rc = L.mpl_lookup(None, _lib.MPL_Q_RAW, None, None, 4, 4, 64, 64, 16, _lib.MPL_F16, 10.0, None, 0.0,
+    rc = L.mpl_lookup(None, _lib.MPL_Q_RAW, None, None, 4, 4, 64, 64, 16, _lib.MPL_F16, None, None, None,
                       None, 0, None, None, None, None, None, None, 99, 256, 0, None, s)
     assert rc != 0 and b"values_dtype" in L.mpl_last_error()

@@ -37,6 +37,8 @@ def _run(M, H, n, d_key, k, score, noise, seed):
         _lib.check(L.mpl_l2_normalize(_lib.ptr(q), M * H * 2, half, 1e-6, _lib.ptr(qn), None, None, st), "norm")
         q, mode = qn, _lib.MPL_Q_NORMALIZED
     T, coef = 10.0, (0.7 if noise else 0.0)
+    T_dev = torch.full((1,), T, device="cuda")  # device scalars, as the C ABI takes them
+    coef_dev = torch.full((1,), coef, device="cuda") if noise else None
     i32, f32 = torch.int32, torch.float32
     outs = {}
     for name in ("select", "topk"):
@@ -48,14 +50,14 @@ def _run(M, H, n, d_key, k, score, noise, seed):
             fi = torch.empty((M, H, k), dtype=i32, device="cuda")
             sl = torch.empty((M, H, k), dtype=i32, device="cuda")
             w = torch.empty((M, H, k), dtype=f32, device="cuda")
-            _lib.check(L.mpl_score_select(_lib.ptr(q), mode, None, _lib.ptr(packed), M, H, n, half, k, score, T,
-                                          _lib.ptr(gum), coef, _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
+            _lib.check(L.mpl_score_select(_lib.ptr(q), mode, None, _lib.ptr(packed), M, H, n, half, k, score,
+                                          _lib.ptr(T_dev), _lib.ptr(gum), _lib.ptr(coef_dev), _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
                                           _lib.ptr(fi), _lib.ptr(sl), _lib.ptr(w), st), "select")
         else:
             wsb = L.mpl_score_topk_workspace_bytes(M, H, n, half, k)
             ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
-            _lib.check(L.mpl_score_topk(_lib.ptr(q), mode, None, _lib.ptr(packed), M, H, n, half, k, score, T,
-                                        _lib.ptr(gum), coef, _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
+            _lib.check(L.mpl_score_topk(_lib.ptr(q), mode, None, _lib.ptr(packed), M, H, n, half, k, score,
+                                        _lib.ptr(T_dev), _lib.ptr(gum), _lib.ptr(coef_dev), _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
                                         st), "topk")
         torch.cuda.synchronize()
         outs[name] = (sub_idx.cpu().numpy(), sub_sc.cpu().numpy())

@@ -46,7 +46,9 @@ def _call(L, static, q, packed, values, gumbel, coef):
     o = _outputs(M)
     p = _lib.ptr
     st = _lib.stream_ptr(q.device)
-    head = (p(q), _lib.MPL_Q_RAW, None, p(packed), M, H, N_SUB, HALF, K, _lib.MPL_F16, 10.0, p(gumbel), coef)
+    T = torch.full((1,), 10.0, device="cuda")  # device scalars, as the C ABI takes them
+    c = torch.full((1,), coef, device="cuda") if gumbel is not None else None
+    head = (p(q), _lib.MPL_Q_RAW, None, p(packed), M, H, N_SUB, HALF, K, _lib.MPL_F16, p(T), p(gumbel), p(c))
     tail = (p(o["sub_idx"]), p(o["sub_scores"]), p(o["flat_idx"]), p(o["slots"]), p(o["weights"]), p(values),
             _lib.MPL_F16, D, 0, p(o["out"]), st)
     if static:
@@ -88,7 +90,7 @@ def test_static_lookup_refuses_oversized_batch(gpu_lib, table):
     M, n = 70000, 512
     need = L.mpl_score_select_workspace_bytes(M, H, n, HALF, K)
     assert need > L.mpl_lookup_static_scratch_bytes()
-    rc = L.mpl_lookup_static(None, _lib.MPL_Q_RAW, None, None, M, H, n, HALF, K, _lib.MPL_F16, 10.0, None, 0.0,
+    rc = L.mpl_lookup_static(None, _lib.MPL_Q_RAW, None, None, M, H, n, HALF, K, _lib.MPL_F16, None, None, None,
                              None, None, None, None, None, None, _lib.MPL_F16, D, 0, None, None)
     assert rc == 3  # MPL_EWORKSPACE
     assert b"scratch" in L.mpl_last_error()
