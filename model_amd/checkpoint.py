@@ -20,6 +20,9 @@ the reference, memory.py:104-109) is converted chunk by chunk into the
 requested dtype (fp16 by default), so a table larger than host memory is
 never held whole on the host.  ``pool_params`` returns the MemoryPool
 parameter dict of a loaded tree; ``save_params`` writes the same format.
+``load_train_state`` / ``save_train_state`` do the same for the trainer's
+resumable TrainState checkpoint (train.py:36-44, 559-583), whose pool
+optimizer state SparseRowUpdate.resume / .train_state_pool map.
 """
 
 from __future__ import annotations
@@ -174,6 +177,8 @@ def _pack_tree(tree, path, values_dtype):
     if isinstance(tree, dict):
         return {str(k): _pack_tree(v, path + (str(k),), values_dtype) for k, v in tree.items()}
     arr = _to_numpy(tree)
+    if arr.ndim == 0 and path == ("step",):  # the TrainState step: a numpy scalar (ext 3), as Flax writes it
+        return msgpack.ExtType(EXT_NPSCALAR, _ndarray_bytes(arr))
     if path[-2:] == POOL_PATH and values_dtype is not None:
         arr = arr.astype(values_dtype)
     arr = np.ascontiguousarray(arr)
@@ -199,3 +204,41 @@ def save_params(dst: Union[str, io.BufferedIOBase], tree: Dict[str, Any],
         os.replace(tmp, dst)
     else:
         dst.write(payload)
+
+
+# ------------------------------------------------------------ train states
+TRAIN_STATE_KEYS = ("step", "params", "opt_state", "subkey_usage", "slot_usage", "pool_m", "pool_v")
+
+
+def load_train_state(src: Union[str, bytes, io.BufferedIOBase], device: Union[str, torch.device] = "cuda",
+                     values_dtype: Optional[torch.dtype] = None) -> Dict[str, Any]:
+    """The resumable checkpoint of train.py:559-583: the msgpack of the
+    TrainState dataclass (train.py:36-44), fields {step, params, opt_state,
+    subkey_usage, slot_usage, pool_m, pool_v}, read leaf by leaf like
+    load_params.  ``values_dtype`` None keeps the stored fp32 value table
+    (the master copy a resumed sparse update needs; SparseRowUpdate.resume
+    derives the fp16 table from it).  ``step`` is returned as an int."""
+    state = load_params(src, device=device, values_dtype=values_dtype)
+    missing = [k for k in TRAIN_STATE_KEYS if k not in state]
+    if missing:
+        raise ValueError(f"not a TrainState checkpoint: missing {missing}")
+    step = state["step"]
+    state["step"] = int(step.item() if isinstance(step, torch.Tensor) else step)
+    return state
+
+
+def save_train_state(dst: Union[str, io.BufferedIOBase], *, step: int, params: Dict[str, Any],
+                     opt_state: Any, subkey_usage: torch.Tensor, slot_usage: torch.Tensor,
+                     pool_m: torch.Tensor, pool_v: torch.Tensor) -> None:
+    """Writes a TrainState checkpoint in the reference's layout (field order
+    of train.py:36-44; ``step`` an int32 scalar; the pool table fp32)."""
+    tree = {
+        "step": np.array(int(step), dtype=np.int32),
+        "params": params,
+        "opt_state": opt_state if opt_state is not None else {},
+        "subkey_usage": subkey_usage,
+        "slot_usage": slot_usage,
+        "pool_m": pool_m,
+        "pool_v": pool_v,
+    }
+    save_params(dst, tree, values_dtype=np.float32)

@@ -118,6 +118,29 @@ class _LazyMerged(dict):
         return dict.keys(self)
 
 
+def _make_dropout(rate: float, rngs, device):
+    """Inverted dropout at ``rate`` (model.py:91, 122 with train=True): keeps
+    each element with probability 1 - rate and scales the kept ones by
+    1 / (1 - rate).  ``rngs["dropout"]`` (an int seed or a torch.Generator
+    on the device) draws the masks; otherwise torch's default generator.
+    The mask stream differs from Flax's."""
+    if not 0.0 <= rate < 1.0:
+        raise ValueError(f"dropout rate must be in [0, 1), got {rate}")
+    r = None if rngs is None else rngs.get("dropout")
+    gen = None
+    if isinstance(r, torch.Generator):
+        gen = r
+    elif r is not None:
+        gen = torch.Generator(device=device).manual_seed(int(r))
+    keep = 1.0 - rate
+
+    def drop(t: torch.Tensor) -> torch.Tensor:
+        mask = torch.rand(t.shape, generator=gen, device=t.device, dtype=t.dtype) < keep
+        return t * mask * (1.0 / keep)
+
+    return drop
+
+
 class MemoryPoolLM:
     """model.py:15-127."""
 
@@ -184,7 +207,7 @@ class MemoryPoolLM:
                 for _ in range(cfg.n_layers)]
 
     # ----------------------------------------------------------- forward
-    def _attention(self, p, h, layer_cache, positions):
+    def _attention(self, p, h, layer_cache, positions, drop=None):
         cfg = self.cfg
         B, T, d = h.shape
         hd = d // cfg.n_heads
@@ -206,7 +229,10 @@ class MemoryPoolLM:
             mask = torch.ones((T, T), dtype=torch.bool, device=h.device).tril()[None, None]
         s = torch.matmul(q, kt)
         s = s.masked_fill(~mask, torch.finfo(s.dtype).min)
-        a = torch.matmul(torch.softmax(s, dim=-1), v)  # [B, heads, T, hd]
+        w = torch.softmax(s, dim=-1)
+        if drop is not None:  # dropout on the attention weights (Flax MultiHeadDotProductAttention dropout_rate)
+            w = drop(w)
+        a = torch.matmul(w, v)  # [B, heads, T, hd]
         a = a.permute(0, 2, 1, 3).reshape(B, T, cfg.n_heads * hd)
         return torch.matmul(a, p["out"]["kernel"].reshape(cfg.n_heads * hd, d)) + p["out"]["bias"]
 
@@ -226,10 +252,11 @@ class MemoryPoolLM:
             x = emb[tokens] + p["pos_embed"][positions][None]
         if self.decode and (cache is None or positions is None):
             raise ValueError("decode mode needs cache and positions")
+        drop = _make_dropout(cfg.dropout, rngs, x.device) if (train and cfg.dropout > 0) else None
         layer_aux = []
         for i in range(cfg.n_layers):
             h = _ln(x, p[f"ln_attn_{i}"])
-            x = x + self._attention(p[f"attn_{i}"], h, cache[i] if self.decode else None, positions)
+            x = x + self._attention(p[f"attn_{i}"], h, cache[i] if self.decode else None, positions, drop)
             h = _ln(x, p[f"ln_ffn_{i}"])
             mem_layer = self.pool is not None and i in cfg.memory_layers
             y = torch.zeros_like(x)
@@ -248,6 +275,8 @@ class MemoryPoolLM:
                     gate = F.silu(_dense(h_gate, p[f"mem_gate_{i}"]))
                     y = y + _dense(mem * gate, p[f"mem_out_{i}"])
                     layer_aux.append(aux)
+            if drop is not None:  # model.py:122: dropout on the layer's residual branch
+                y = drop(y)
             x = x + y
         x = _ln(x, p["ln_final"])
         logits = F.linear(x, emb)  # x . emb^T as one product, no transposed copy of the table

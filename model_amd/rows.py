@@ -205,6 +205,49 @@ class SparseRowUpdate:
             self.v = torch.zeros((N, d), dtype=torch.float32, device=dev)
         self.step = 0
 
+    def resume(self, state: Dict) -> None:
+        """Continues from a TrainState checkpoint (checkpoint.load_train_state,
+        train.py:36-44, 559-583): the step count (state.step, the 0-based
+        step of the next update), and the pool optimizer state: row-wise
+        Adagrad's accumulator is TrainState.pool_v [N] (pool_m is empty,
+        train.py:284-285); lazy Adam's moments are pool_m, pool_v [N, d].
+        With an fp32 master the master takes the checkpoint's fp32 table
+        (params/pool/values) and the table its cast."""
+        if self.host is not None:
+            raise ValueError("a host pool keeps its own state: load it with HostPool.load (train.py:576)")
+        N, d = self.values.shape
+        self.step = int(state["step"])
+        pm, pv = state["pool_m"], state["pool_v"]
+        if self.optimizer == "rowwise_adagrad":
+            if tuple(pv.shape) != (N,):
+                raise ValueError(f"pool_v must be [{N}] for rowwise_adagrad, got {tuple(pv.shape)}")
+            self.acc.copy_(pv)
+        else:
+            if tuple(pm.shape) != (N, d) or tuple(pv.shape) != (N, d):
+                raise ValueError(f"pool_m / pool_v must be [{N}, {d}] for adam, got {tuple(pm.shape)}, {tuple(pv.shape)}")
+            self.m.copy_(pm)
+            self.v.copy_(pv)
+        table = state["params"]["pool"]["values"] if "values" in state["params"].get("pool", {}) else None
+        if table is not None:
+            if tuple(table.shape) != (N, d):
+                raise ValueError(f"params/pool/values must be [{N}, {d}], got {tuple(table.shape)}")
+            if self.master is not None:
+                self.master.copy_(table)
+            self.values.copy_(table)
+
+    def train_state_pool(self) -> Dict[str, torch.Tensor]:
+        """The pool fields of a TrainState for checkpoint.save_train_state:
+        step, pool_m, pool_v (and the fp32 table to store as
+        params/pool/values: the master when kept)."""
+        dev = self.values.device
+        empty = torch.zeros(0, dtype=torch.float32, device=dev)
+        if self.optimizer == "rowwise_adagrad":
+            pm, pv = empty, self.acc
+        else:
+            pm, pv = self.m, self.v
+        table = self.master if self.master is not None else self.values.float()
+        return {"step": self.step, "pool_m": pm, "pool_v": pv, "values": table}
+
     def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
                  rest_sq: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
         N = self.host.n_slots if self.host is not None else self.values.shape[0]

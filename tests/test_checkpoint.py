@@ -77,3 +77,71 @@ def test_fixture_is_current():
         finally:
             mk.OUT = old
         assert open(path, "rb").read() == open(OUT, "rb").read()
+
+
+# ------------------------------------------------------------ train states
+from tests.golden import make_flax_train_state_fixture as ts_fix  # noqa: E402
+
+
+def test_train_state_fixtures_are_the_committed_bytes(tmp_path):
+    for opt, path in ts_fix.OUT.items():
+        with open(path, "rb") as f:
+            committed = f.read()
+        ts_fix.OUT[opt] = str(tmp_path / os.path.basename(path))
+        try:
+            ts_fix.main()
+            with open(ts_fix.OUT[opt], "rb") as f:
+                assert f.read() == committed
+        finally:
+            ts_fix.OUT[opt] = path
+
+
+@pytest.mark.parametrize("opt", ["adagrad", "adam"])
+def test_reads_train_state_and_resumes_row_update(opt):
+    from model_amd import rows as R
+
+    want = ts_fix.arrays(opt)
+    st = ck.load_train_state(ts_fix.OUT[opt], device="cpu")
+    assert st["step"] == ts_fix.STEP
+    np.testing.assert_array_equal(st["params"]["pool"]["values"].numpy(), want["params"]["pool"]["values"])
+    assert st["params"]["pool"]["values"].dtype == torch.float32  # kept fp32: the master copy
+    np.testing.assert_array_equal(st["subkey_usage"].numpy(), want["subkey_usage"])
+    assert int(st["opt_state"]["1"]["count"]) == ts_fix.STEP and st["opt_state"]["0"] == {}
+    N, d = want["params"]["pool"]["values"].shape
+    table = torch.zeros((N, d), dtype=torch.float16)
+    upd = R.SparseRowUpdate(table, optimizer="rowwise_adagrad" if opt == "adagrad" else "adam")
+    upd.resume(st)
+    assert upd.step == ts_fix.STEP
+    np.testing.assert_array_equal(upd.master.numpy(), want["params"]["pool"]["values"])
+    np.testing.assert_array_equal(table.numpy(), want["params"]["pool"]["values"].astype(np.float16))
+    if opt == "adagrad":
+        np.testing.assert_array_equal(upd.acc.numpy(), want["pool_v"])
+    else:
+        np.testing.assert_array_equal(upd.m.numpy(), want["pool_m"])
+        np.testing.assert_array_equal(upd.v.numpy(), want["pool_v"])
+    # the wrong optimizer's layout is refused
+    other = R.SparseRowUpdate(torch.zeros((N, d)), optimizer="adam" if opt == "adagrad" else "rowwise_adagrad")
+    with pytest.raises(ValueError):
+        other.resume(st)
+
+
+def test_train_state_writer_round_trip():
+    from model_amd import rows as R
+
+    st = ck.load_train_state(ts_fix.OUT["adam"], device="cpu")
+    N, d = st["params"]["pool"]["values"].shape
+    upd = R.SparseRowUpdate(torch.zeros((N, d), dtype=torch.float16), optimizer="adam")
+    upd.resume(st)
+    pool = upd.train_state_pool()
+    params = dict(st["params"])
+    params["pool"] = dict(params["pool"], values=pool["values"])
+    buf = io.BytesIO()
+    ck.save_train_state(buf, step=pool["step"], params=params, opt_state=st["opt_state"],
+                        subkey_usage=st["subkey_usage"], slot_usage=st["slot_usage"], pool_m=pool["pool_m"],
+                        pool_v=pool["pool_v"])
+    back = ck.load_train_state(buf.getvalue(), device="cpu")
+    assert back["step"] == st["step"]
+    for k in ("pool_m", "pool_v", "subkey_usage", "slot_usage"):
+        assert torch.equal(back[k], st[k]), k
+    assert torch.equal(back["params"]["pool"]["values"], st["params"]["pool"]["values"])
+    assert torch.equal(back["opt_state"]["1"]["mu"]["router_1"]["kernel"], st["opt_state"]["1"]["mu"]["router_1"]["kernel"])
