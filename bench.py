@@ -17,6 +17,9 @@ Also reported in the same JSON line:
   * ``training_262k``: the training step of the same layer (forward +
     backward + sparse row-wise Adagrad) and the sparse row update alone on
     Zipf(1.1)-skewed routing;
+  * ``fact_task_16k_fp32``: the fact-task layer (16,384 fp32 slots, 1,024
+    tokens) on fp32 MFMA scoring: the forward read, and a training step whose
+    balance and key-diversity terms run on fp32 MFMA tiles;
   * ``key_diversity_67M``: key_diversity_loss and its gradient on the
     67M-slot layer's codebooks (H=4, n=8,192): the n x n Gram tiles on MFMA;
   * ``generation_268M``: end-to-end batched greedy generation, 4-layer
@@ -64,7 +67,7 @@ def parse():
     ap.add_argument("--no-train", action="store_true")
     ap.add_argument("--no-generate", action="store_true")
     ap.add_argument("--no-host", action="store_true")
-    ap.add_argument("--only", choices=["text_study", "pool_67M_4096", "host_file"], default=None,
+    ap.add_argument("--only", choices=["text_study", "pool_67M_4096", "host_file", "fact_task"], default=None,
                     help="run one workload alone (for profiler runs) and print its timings")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only run a plain 512 MiB device copy 10 times (the reference kernel for "
@@ -458,6 +461,63 @@ def train_step_bench(torch, iters):
             "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events"}
 
 
+def fact_task_bench(torch, iters):
+    """The fact-task layer on the GPU, fp32 throughout (fp32 table, fp32
+    MFMA scoring): 1,024 tokens (B=8, T=128), 16,384 slots (n_sub_keys=128),
+    H=4, d_key=256, k=16, d_value=256.  `lookup`: the forward read alone.
+    `train_step`: forward with routing noise + backward through a 256->1024
+    query projection, the sub-keys and log-temperature, with the balance loss
+    (0.01) and the fp32 key-diversity loss (0.01), whose dense terms run on
+    v_mfma_f32_32x32x2_f32 tiles."""
+    from model_amd.memory import MemoryPool, key_diversity_loss
+
+    M, H, n, d_key, d, k = 1024, 4, 128, 256, 256, 16
+    dev = "cuda"
+    pool = MemoryPool(n, H, d_key, d, k, values_dtype=torch.float32)
+    assert pool.score_dtype == torch.float32
+    g = torch.Generator(device=dev).manual_seed(11)
+    keys = (torch.randn((H, 2, n, d_key // 2), generator=g, device=dev) * (d_key // 2) ** -0.5).requires_grad_(True)
+    values = torch.empty((n * n, d), dtype=torch.float32, device=dev).normal_(0.0, 0.02, generator=g)
+    log_t = torch.tensor(math.log(10.0), device=dev, requires_grad=True)
+    params = {"sub_keys": keys, "values": values, "log_temperature": log_t}
+    hidden = torch.randn((M, 256), generator=g, device=dev)
+    lim = math.sqrt(6.0 / (256 + H * d_key))
+    w_q = ((torch.rand((256, H * d_key), generator=g, device=dev) * 2 - 1) * lim).requires_grad_(True)
+    g_out = torch.randn((M, d), generator=g, device=dev) * 1e-3
+    q0 = (hidden @ w_q).detach().reshape(M, H, d_key).contiguous()
+
+    def fwd(i=0):
+        pool.lookup(params, q0)
+
+    def step(i=0):
+        q = (hidden @ w_q).reshape(M, H, d_key)
+        out, aux = pool.apply({"params": params}, q, train=True, rngs={"routing": i})
+        loss = (out * g_out).sum() + 0.01 * aux["balance_loss"] + 0.01 * key_diversity_loss(keys, torch.float32)
+        torch.autograd.grad(loss, [w_q, keys, log_t])
+
+    def eager(fn, n_iter):  # no graph capture: the training step is timed as it runs
+        for i in range(3):
+            fn(i)
+        torch.cuda.synchronize()
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        a.record()
+        for i in range(n_iter):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n_iter
+
+    ms_fwd = eager(fwd, iters * 4)
+    ms_step = eager(step, iters)
+    return {"workload": "fact-task layer, fp32: 1,024 tokens, 16,384 fp32 slots, H=4, d_key=256, k=16, d_value=256",
+            "lookup": {"ms": ms_fwd, "tokens_per_s": M / (ms_fwd * 1e-3)},
+            "train_step": {"ms": ms_step, "tokens_per_s": M / (ms_step * 1e-3),
+                           "what": "forward with routing noise + backward, balance 0.01 and fp32 key diversity "
+                                   "0.01 on fp32 MFMA tiles (no value update)"},
+            "timing": "eager, HIP events"}
+
+
 def key_diversity_bench(torch, iters):
     """key_diversity_loss and its gradient with respect to the normalised
     sub-keys (memory.py:230-240) for the 67M-slot layer's codebooks (H=4,
@@ -474,14 +534,14 @@ def key_diversity_bench(torch, iters):
     packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, _lib.MPL_F16), dtype=torch.uint8, device="cuda")
     check(L.mpl_pack_keys(ptr(keys), H, n, half, _lib.MPL_F16, ptr(k_hat), ptr(packed),
                           _lib.stream_ptr(keys.device)), "mpl_pack_keys")
-    wsb = L.mpl_key_diversity_workspace_bytes(H, n, half)
+    wsb = L.mpl_key_diversity_workspace_bytes(H, n, half, _lib.MPL_F16)
     ws = torch.empty(wsb, dtype=torch.uint8, device="cuda")
     loss = torch.empty(1, dtype=torch.float32, device="cuda")
     dk = torch.empty_like(keys)
 
     def fn(i=0):
-        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, ptr(ws), wsb, ptr(loss), ptr(dk),
-                                  _lib.stream_ptr(keys.device)), "mpl_key_diversity")
+        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, _lib.MPL_F16, ptr(ws), wsb, ptr(loss),
+                                  ptr(dk), _lib.stream_ptr(keys.device)), "mpl_key_diversity")
 
     ms = time_loop(torch, fn, iters, 3)
     flops = 2 * (2.0 * 2 * H * n * n * half)
@@ -782,6 +842,9 @@ def main():
         print(json.dumps({"only": args.only, "ms_per_step": time_loop(torch, lk.step, args.steps, args.warmup),
                           "kernels": kernel_breakdown(torch, lk, args.steps)}))
         return
+    if args.only == "fact_task":
+        print(json.dumps({"only": args.only, "fact_task_16k_fp32": fact_task_bench(torch, 10)}))
+        return
     if args.only == "host_file":
         print(json.dumps({"only": args.only, "host_pool_file_1M": host_pool_file_bench(torch, 5)}))
         return
@@ -832,11 +895,12 @@ def main():
                              "calls cycle through rotating_batches token batches",
                  "by_tokens": sweep}
 
-    train = div = None
+    train = div = fact = None
     if not args.no_train:
         train = {"train_step": train_step_bench(torch, max(5, args.steps // 20)),
                  "sparse_update_zipf": sparse_update_bench(torch, max(10, args.steps // 10))}
         div = key_diversity_bench(torch, max(5, args.steps // 20))
+        fact = fact_task_bench(torch, max(5, args.steps // 20))
 
     generation = None if args.no_generate else generation_bench(torch)
     host = host_file = None
@@ -875,6 +939,7 @@ def main():
         "pool_67M": large,
         "training_262k": train,
         "key_diversity_67M": div,
+        "fact_task_16k_fp32": fact,
         "generation_268M": generation,
         "host_pool_1M": host,
         "host_pool_file_1M": host_file,

@@ -1,6 +1,6 @@
 /*
  * mpl.h -- C ABI of the MI355X (gfx950) memory-layer lookup library
- * (libmpl.so, built from model_amd/csrc/*.hip).
+ * (libmpl.so, built from the HIP sources in model_amd/csrc).
  *
  * The reference (KumarDev7/model) has no FFI: its operator is the Flax module
  * `MemoryPool` (memory_pool_model/memory.py:64-227) plus the trainer's sparse
@@ -356,15 +356,16 @@ int mpl_l2_normalize_bwd(const float* x, const float* dy, int64_t rows, int dim,
 /*
  * key_diversity_loss (memory.py:230-240): with G[h,c] = K_hat K_hat^T the
  * cosine Gram matrix of each codebook, loss [1] = sum of the squared
- * off-diagonal entries / (H * 2 * n * (n - 1)), the Gram tiles on fp16 MFMA
- * (half % 8 == 0, half <= 128).  If d_k_hat [H,2,n,half] != NULL it receives
+ * off-diagonal entries / (H * 2 * n * (n - 1)), the Gram tiles on MFMA in
+ * score_dtype: MPL_F16 (half % 8 == 0, half <= 128) or MPL_F32 (half <=
+ * 128).  If d_k_hat [H,2,n,half] != NULL it receives
  * d loss / d k_hat = 4 / (H * 2 * n * (n - 1)) * (G - diag G) K_hat (the
  * raw sub-keys' gradient follows with mpl_l2_normalize_bwd).  k_hat and
- * packed_keys from mpl_pack_keys (MPL_F16).
+ * packed_keys from mpl_pack_keys with the same score_dtype.
  */
-size_t mpl_key_diversity_workspace_bytes(int H, int n, int half);
-int mpl_key_diversity(const float* k_hat, const void* packed_keys, int H, int n, int half, void* workspace,
-                      size_t workspace_bytes, float* loss, float* d_k_hat, void* stream);
+size_t mpl_key_diversity_workspace_bytes(int H, int n, int half, int score_dtype);
+int mpl_key_diversity(const float* k_hat, const void* packed_keys, int H, int n, int half, int score_dtype,
+                      void* workspace, size_t workspace_bytes, float* loss, float* d_k_hat, void* stream);
 
 /*
  * revive_dead_keys (memory.py:243-281), in place: in every codebook the
@@ -400,25 +401,26 @@ int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_idx, int64_t
                      float* subkey_counts, float* clean_counts, float* slot_counts, void* stream);
 
 /*
- * memory.py:209-213 (fp16 scoring: half % 8 == 0, half <= 128): the
- * load-balance loss
+ * memory.py:209-213: the load-balance loss
  *   balance = n * mean_{h,c} sum_n f[h,c,n] * mean_m softmax_n(z[m,h,c,:])
  * with z = cos(q, k_n) * T * (q_len if scaled), f = clean_counts / (M k), the
- * cosine on fp16 MFMA tiles and each softmax taken over all n sub-keys in
- * one online pass.  `scaled` = balance_temperature_grad && query_scale (the
+ * cosine on MFMA tiles of score_dtype (MPL_F16: half % 8 == 0, half <= 128;
+ * MPL_F32: half <= 128) and each softmax taken over all n sub-keys in one
+ * online pass.  `scaled` = balance_temperature_grad && query_scale (the
  * balance logits are then the query-scaled scores).  queries: raw fp32
  * [M,H,2,half] (normalised inside).  packed_keys: from mpl_pack_keys with
- * MPL_F16.  `state` (mpl_balance_state_bytes) receives per (token, codebook)
- * the softmax statistics that mpl_lookup_bwd_dense needs; loss [1].
+ * score_dtype.  `state` (mpl_balance_state_bytes) receives per (token,
+ * codebook) the softmax statistics that mpl_lookup_bwd_dense needs; loss [1]
+ * (NaN when M = 0: f and the token mean are then 0/0, as in the reference).
  */
 size_t mpl_balance_state_bytes(int64_t M, int H);
 int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
-                    int64_t M, int H, int n, int half, int k, const float* temperature, void* state, float* loss,
-                    void* stream);
+                    int64_t M, int H, int n, int half, int k, int score_dtype, const float* temperature, void* state,
+                    float* loss, void* stream);
 
 /*
- * The dense-over-n part of the lookup backward (fp16 scoring) on MFMA tiles
- * that recompute the scores:
+ * The dense-over-n part of the lookup backward on MFMA tiles of score_dtype
+ * (as mpl_balance_fwd) that recompute the scores:
  *   dk_hat [H,2,n,half], written: d/d(normalised sub-keys) of
  *     - the routed term (sub_idx, d_sub [M,H,2,k] non-NULL): the selected
  *       scores' gradient d_sub * T (* q_len with query_scale) against the
@@ -432,17 +434,18 @@ int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, c
  *     (query_scale only) and dlogt [1], the balance's d q_len and d log_t
  *     shares.
  * q_hat from mpl_l2_normalize; k_hat and packed_keys from mpl_pack_keys
- * (MPL_F16); clean_counts and state from mpl_route_counts / mpl_balance_fwd
+ * (score_dtype); clean_counts and state from mpl_route_counts / mpl_balance_fwd
  * of the same inputs; q_len [M,H,2] with query_scale.  The raw sub-keys'
  * gradient follows with mpl_l2_normalize_bwd.  Nothing of size [M, n] is
  * formed; no atomics.
  */
-size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half);
+size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half, int score_dtype);
 int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
                          const int32_t* sub_idx, const float* d_sub, const float* clean_counts, const void* state,
                          const float* g_balance, int balance_temperature_grad, int query_scale, int64_t M, int H,
-                         int n, int half, int k, const float* temperature, void* workspace, size_t workspace_bytes,
-                         float* dq_hat, float* dk_hat, float* dlen, float* dlogt, void* stream);
+                         int n, int half, int k, int score_dtype, const float* temperature, void* workspace,
+                         size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
+                         void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,5 +1,6 @@
 // Training-side routing statistics and the load-balance loss of
-// memory.py:196-215 on the GPU (fp16 MFMA scoring).
+// memory.py:196-215 on the GPU, on the MFMA tiles of the scoring precision
+// (fp16: v_mfma_f32_32x32x16_f16; fp32: v_mfma_f32_32x32x2_f32).
 //
 //   route_counts_kernel  subkey_counts from the final slots (memory.py:199-204),
 //                        the clean stage-1 counts behind f (:206-208) and
@@ -47,11 +48,62 @@ constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kRtPitch = 36;  // floats per key row of the routed-term tile (32 queries + bank padding)
 
-typedef Mfma<_Float16> MF;
+// Operand shapes of one scoring precision E (_Float16: v_mfma_f32_32x32x16_f16,
+// float: v_mfma_f32_32x32x2_f32) as the balance kernels use them:
+//   NCH  MFMAs per 32-row block (K = half padded to HP);
+//   NV   16-byte vectors per lane per block of a normal pack (layout.h);
+//   OPV  MFMA operands per 16-byte vector;
+//   RPO  score-tile registers that form one contraction operand (the tile
+//        rows of register r are 8(r/4) + 4(l/32) + r%4), and NOP = 16 / RPO
+//        contraction MFMAs per 32-dim block of the output;
+//   TVPD 16-byte vectors per lane per 32-dim block of a transposed pack.
+template <typename E>
+struct BalOps;
+
+template <>
+struct BalOps<_Float16> {
+  typedef Mfma<_Float16> MF;
+  typedef KeyPack<_Float16> KP;
+  static constexpr int kRowsPerOp = 8;
+  static constexpr int kElemsPerVec = 8;
+  __device__ static half8 from_rows(const float* g) {
+    half8 h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)g[j];
+    return h;
+  }
+};
+
+template <>
+struct BalOps<float> {
+  typedef Mfma<float> MF;
+  typedef KeyPack<float> KP;
+  static constexpr int kRowsPerOp = 1;
+  static constexpr int kElemsPerVec = 4;
+  __device__ static float from_rows(const float* g) { return g[0]; }
+};
+
+template <typename E, int HP>
+struct BalShape {
+  typedef BalOps<E> Ops;
+  static constexpr int NCH = HP / Ops::KP::kChunk;
+  static constexpr int NV = Ops::KP::vectors_per_lane(HP);
+  static constexpr int OPV = Ops::KP::kOpsPerVec;
+  static constexpr int RPO = Ops::kRowsPerOp;
+  static constexpr int NOP = 16 / RPO;
+  static constexpr int TVPD = 16 / Ops::kElemsPerVec;
+  static constexpr int ND = (HP + 31) / 32;
+  static_assert(NCH == NV * OPV, "a normal pack holds every MFMA operand of a block");
+  static_assert(NOP == TVPD * OPV, "a transposed pack holds every contraction operand of a block");
+};
 
 // ------------------------------------------------------------- counting
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* __restrict__ x, int64_t n) {
   for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0.f;
+}
+
+__global__ __launch_bounds__(64) void fill_value_kernel(float* __restrict__ x, int64_t n, float v) {
+  for (int64_t i = blockIdx.x * 64 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 64) x[i] = v;
 }
 
 // Three buffers cleared by one launch (null ones skipped): the count
@@ -137,7 +189,7 @@ __global__ __launch_bounds__(256) void route_counts_kernel(const int32_t* __rest
 // ------------------------------------------------------------- forward
 struct BalFwdParams {
   const float* q;         // raw queries [M, HC, half]
-  const uint4* packed;    // packed sub-keys (fp16 layout)
+  const uint4* packed;    // packed sub-keys (layout.h, the kernel's precision)
   const float* counts;    // clean counts [HC, n]
   float inv_mk;           // 1 / (M k)
   const float* T;         // device scalar: the clamped temperature
@@ -192,10 +244,12 @@ __device__ __forceinline__ float partner(float v, int par) {
   return par ? a : b;
 }
 
-template <int HP>
+template <typename E, int HP>
 __global__ __launch_bounds__(kBalThreads) void balance_fwd_kernel(BalFwdParams p) {
-  constexpr int NCH = HP / 16;
-  constexpr int TILE = NCH * kWave;
+  typedef BalShape<E, HP> Sh;
+  typedef typename Sh::Ops::MF MF;
+  constexpr int NCH = Sh::NCH, OPV = Sh::OPV;
+  constexpr int TILE = Sh::NV * kWave;
   __shared__ uint4 tiles[2][TILE];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, par = lane >> 5;
@@ -205,13 +259,13 @@ __global__ __launch_bounds__(kBalThreads) void balance_fwd_kernel(BalFwdParams p
 
   // the raw query, normalised (memory.py:30-31, 136-137)
   const float* qrow = p.q + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
-  float x[NCH][8];
+  float x[NCH][MF::kQElems];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < NCH; ++c) MF::load_q_raw(qrow, valid, p.half, c, lane, x[c], ss);
   const float tot = ss + partner(ss, par) + 1e-6f;
   const float rn = 1.0f / sqrtf(tot);
-  half8 qop[NCH];
+  typename MF::Op qop[NCH];
 #pragma unroll
   for (int c = 0; c < NCH; ++c) qop[c] = MF::scale_q(x[c], rn);
   const float rho = p.scaled ? sqrtf(tot) / sqrtf((float)p.half) : 1.f;
@@ -230,7 +284,8 @@ __global__ __launch_bounds__(kBalThreads) void balance_fwd_kernel(BalFwdParams p
     if (blk + 1 < p.nblk) st.load(kb + (int64_t)(blk + 1) * TILE, tid);
     f32x16 acc = f32x16{};
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) acc = MF::mma(MF::from_vec(tiles[cur][c * kWave + lane], 0), qop[c], acc);
+    for (int c = 0; c < NCH; ++c)
+      acc = MF::mma(MF::from_vec(tiles[cur][(c / OPV) * kWave + lane], c % OPV), qop[c], acc);
     float z[16], fv[16];
     float bm = -INFINITY;
 #pragma unroll
@@ -286,22 +341,25 @@ __global__ __launch_bounds__(1024) void balance_loss_kernel(const float* __restr
 
 // ------------------------------------------------------------- backward
 // Operand packs of fp32 rows X(hc, row, d) = X[hc*s_hc + row*s_row + d]
-// (rows >= nrows and dims >= half are zero), optionally times scale(hc, row):
+// (rows >= nrows and dims >= half are zero), optionally times scale(hc, row),
+// converted to the precision E:
 //   normal      out[hc][blk][v][lane]: lane l holds row 32 blk + l%32, dims
-//               16v + 8(l/32) + [0,8) (the scoring operand, as the sub-key
-//               pack of layout.h);
-//   transposed  out[hc][blk][db][c][lane]: lane l holds dim 32 db + l%32 of
-//               rows 32 blk + 16c + 8(j/4) + 4(l/32) + j%4, j < 8: the A
-//               operand that meets a score tile's registers 8c..8c+7 as the
-//               B operand (see the tile layout in mfma.h).
-template <bool TRANS, int HP>
+//               KeyPack<E>::dim_of(v, i, l) (the scoring operand, as the
+//               sub-key pack of layout.h);
+//   transposed  out[hc][blk][db][w][lane]: element i of vector w holds dim
+//               32 db + l%32 of row 32 blk + 8(r/4) + 4(l/32) + r%4 with
+//               r = w * (elements per vector) + i: the A operand that meets
+//               the score tile's registers as the B operand (fp16: registers
+//               8w..8w+7 in one MFMA; fp32: register r in MFMA r).
+template <bool TRANS, typename E, int HP>
 __global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict__ X, int64_t s_hc, int64_t s_row,
                                                         int64_t nrows, int HC, int half,
                                                         const float* __restrict__ scale, int64_t sc_hc,
                                                         int64_t sc_row, int64_t nblk, uint4* __restrict__ out) {
-  constexpr int NCH = HP / 16;
-  constexpr int ND = (HP + 31) / 32;
-  constexpr int PER_BLK = TRANS ? ND * 2 : NCH;  // 16-byte vectors per lane per block
+  typedef BalShape<E, HP> Sh;
+  typedef typename Sh::Ops::KP KP;
+  constexpr int EPV = Sh::Ops::kElemsPerVec;
+  constexpr int PER_BLK = TRANS ? Sh::ND * Sh::TVPD : Sh::NV;  // 16-byte vectors per lane per block
   const int64_t total = (int64_t)HC * nblk * PER_BLK * kWave;
   for (int64_t t = blockIdx.x * 256 + threadIdx.x; t < total; t += (int64_t)gridDim.x * 256) {
     const int lane = (int)(t % kWave);
@@ -310,26 +368,28 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict_
     const int64_t blk = (u / PER_BLK) % nblk;
     const int hc = (int)(u / PER_BLK / nblk);
     const float* base = X + (int64_t)hc * s_hc;
-    float e[8];
+    float e[EPV];
     if (!TRANS) {
       const int64_t row = blk * 32 + (lane & 31);
-      const int d0 = 16 * w + 8 * (lane >> 5);
-      const bool ok = row < nrows && d0 < half;
-      const float sc = (ok && scale != nullptr) ? scale[hc * sc_hc + row * sc_row] : 1.f;
+      const float sc = (row < nrows && scale != nullptr) ? scale[hc * sc_hc + row * sc_row] : 1.f;
 #pragma unroll
-      for (int i = 0; i < 8; ++i) e[i] = ok ? base[row * s_row + d0 + i] * sc : 0.f;
+      for (int i = 0; i < EPV; ++i) {
+        const int d = KP::dim_of(w, i, lane);
+        e[i] = (row < nrows && d < half) ? base[row * s_row + d] * sc : 0.f;
+      }
     } else {
-      const int c = w & 1, db = w >> 1;
+      const int wv = w % Sh::TVPD, db = w / Sh::TVPD;
       const int d = 32 * db + (lane & 31);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int64_t row = blk * 32 + 16 * c + 8 * (j >> 2) + 4 * (lane >> 5) + (j & 3);
+      for (int i = 0; i < EPV; ++i) {
+        const int r = wv * EPV + i;
+        const int64_t row = blk * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         const bool ok = row < nrows && d < half;
         const float sc = (ok && scale != nullptr) ? scale[hc * sc_hc + row * sc_row] : 1.f;
-        e[j] = ok ? base[row * s_row + d] * sc : 0.f;
+        e[i] = ok ? base[row * s_row + d] * sc : 0.f;
       }
     }
-    out[t] = KeyPack<_Float16>::pack(e);
+    out[t] = KP::pack(e);
   }
 }
 
@@ -414,9 +474,9 @@ __global__ __launch_bounds__(256) void bwd_scale_kernel(const float* __restrict_
 }
 
 struct BalGradParams {
-  const uint4* fix;     // fixed side, normal pack [HC][fblk][NCH][64]
-  const uint4* str;     // streamed side, normal pack [HC][sblk][NCH][64]
-  const uint4* strT;    // streamed side, transposed pack [HC][sblk][ND][2][64]
+  const uint4* fix;     // fixed side, normal pack [HC][fblk][NV][64]
+  const uint4* str;     // streamed side, normal pack [HC][sblk][NV][64]
+  const uint4* strT;    // streamed side, transposed pack [HC][sblk][ND][TVPD][64]
   const float4* state;  // [HC, M] from the forward
   const float* counts;  // clean counts [HC, n]
   const float* sigma;   // [HC]
@@ -455,16 +515,19 @@ enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2 };
 // key_diversity_loss); the operand is the off-diagonal cosine itself and each
 // lane also sums its squares into u[workgroup * 256 + thread].
 // Each streamed block: score tile C (rows = streamed, columns = fixed), the
-// operand g in fp16, and for every 32-dim block db of the output
-// acc[db] += strT[db] . g  (two MFMAs, K = 16 rows each).
-template <int MODE, int HP>
+// operand g in the kernel's precision, and for every 32-dim block db of the
+// output acc[db] += strT[db] . g (fp16: two MFMAs, K = 16 rows each; fp32:
+// sixteen, K = 2 rows each).
+template <int MODE, typename E, int HP>
 __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams p) {
+  typedef BalShape<E, HP> Sh;
+  typedef typename Sh::Ops Ops;
+  typedef typename Ops::MF MF;
   constexpr bool DK = MODE != kModeDQ;  // the fixed side is sub-keys
   constexpr bool DIV = MODE == kModeDiv;
   const float Tv = DIV ? 0.f : *p.T;  // Div mode has no temperature (p.T null)
-  constexpr int NCH = HP / 16;
-  constexpr int ND = (HP + 31) / 32;
-  constexpr int TN = NCH * kWave, TT = ND * 2 * kWave, TILE = TN + TT;
+  constexpr int NCH = Sh::NCH, OPV = Sh::OPV, ND = Sh::ND;
+  constexpr int TN = Sh::NV * kWave, TT = ND * Sh::TVPD * kWave, TILE = TN + TT;
   __shared__ uint4 tiles[2][TILE];
   __shared__ __attribute__((aligned(16)))
   float rtile[MODE == kModeDK ? 2 : 1][MODE == kModeDK ? kRowsPerGroup : 1][MODE == kModeDK ? kRtPitch : 1];
@@ -484,11 +547,11 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   const bool valid = my_f < nfix;
   const int64_t fbc = fb < p.fblk ? fb : p.fblk - 1;
 
-  half8 fop[NCH];
+  typename MF::Op fop[NCH];
   {
     const uint4* src = p.fix + ((int64_t)hc * p.fblk + fbc) * TN;
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) fop[c] = MF::from_vec(src[c * kWave + lane], 0);
+    for (int c = 0; c < NCH; ++c) fop[c] = MF::from_vec(src[(c / OPV) * kWave + lane], c % OPV);
   }
   const float sig = (MODE == kModeDQ) ? p.sigma[hc] : 1.f;
   const float fs = p.inv_mk * sig;  // scaled f per count
@@ -575,7 +638,8 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     }
     f32x16 acc = f32x16{};
 #pragma unroll
-    for (int c = 0; c < NCH; ++c) acc = MF::mma(MF::from_vec(tiles[cur][c * kWave + lane], 0), fop[c], acc);
+    for (int c = 0; c < NCH; ++c)
+      acc = MF::mma(MF::from_vec(tiles[cur][(c / OPV) * kWave + lane], c % OPV), fop[c], acc);
     float gv[16], rtv[16];
     if (route) {
       // this lane's routed entries: key f_loc, queries 8 g4 + 4 par + [0, 4)
@@ -617,19 +681,16 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       gv[r] = (rv && valid) ? pe * diff : 0.f;
       if (!DK) usum = fmaf(gv[r], acc[r], usum);
     }
-    half8 b0, b1;
+    typename MF::Op gop[Sh::NOP];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      b0[j] = (_Float16)gv[j];
-      b1[j] = (_Float16)gv[8 + j];
-    }
+    for (int o = 0; o < Sh::NOP; ++o) gop[o] = Ops::from_rows(gv + o * Sh::RPO);
     const uint4* tt = tiles[cur] + TN;
     if (!DIV || grad) {
 #pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        gacc[db] = MF::mma(MF::from_vec(tt[(db * 2) * kWave + lane], 0), b0, gacc[db]);
-        gacc[db] = MF::mma(MF::from_vec(tt[(db * 2 + 1) * kWave + lane], 0), b1, gacc[db]);
-      }
+      for (int db = 0; db < ND; ++db)
+#pragma unroll
+        for (int o = 0; o < Sh::NOP; ++o)
+          gacc[db] = MF::mma(MF::from_vec(tt[(db * Sh::TVPD + o / OPV) * kWave + lane], o % OPV), gop[o], gacc[db]);
     }
     if (more) {
       stn.store(tiles[cur ^ 1], tid);
@@ -656,29 +717,49 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   if (!valid) return;
   float* orow = DK ? p.out + (((int64_t)split * p.HC + hc) * p.n + my_f) * p.half
                    : p.out + (my_f * p.HC + hc) * (int64_t)p.half;
+  // lane l holds dims 32 db + 8 g4 + 4 (l/32) + [0, 4) in registers 4 g4 + [0, 4)
+  const bool vec = (p.half & 3) == 0;  // rows of whole, aligned float4s
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
     for (int g4 = 0; g4 < 4; ++g4) {
       const int d = 32 * db + 8 * g4 + 4 * par;
-      if (d < p.half)
+      if (d >= p.half) continue;
+      if (vec) {
         *(float4*)(orow + d) = make_float4(gacc[db][4 * g4] * scale, gacc[db][4 * g4 + 1] * scale,
                                            gacc[db][4 * g4 + 2] * scale, gacc[db][4 * g4 + 3] * scale);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (d + i < p.half) orow[d + i] = gacc[db][4 * g4 + i] * scale;
+      }
     }
 }
 
-// out[i] = sum over s of part[s][i], in split order (count % 4 == 0).
-__global__ __launch_bounds__(256) void split_sum_kernel(const float4* __restrict__ part, int splits, int64_t count4,
-                                                        float4* __restrict__ out) {
-  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < count4; i += (int64_t)gridDim.x * 256) {
-    float4 s = part[i];
-    for (int k = 1; k < splits; ++k) {
-      const float4 v = part[(int64_t)k * count4 + i];
-      s.x += v.x;
-      s.y += v.y;
-      s.z += v.z;
-      s.w += v.w;
+// out[i] = sum over s of part[s][i] (part [splits][count]), in split order:
+// float4s while count % 4 == 0, else one float per thread.
+__global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict__ part, int splits, int64_t count,
+                                                        float* __restrict__ out) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  if ((count & 3) == 0) {
+    const int64_t count4 = count / 4;
+    const float4* p4 = (const float4*)part;
+    for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < count4; i += stride) {
+      float4 s = p4[i];
+      for (int k = 1; k < splits; ++k) {
+        const float4 v = p4[(int64_t)k * count4 + i];
+        s.x += v.x;
+        s.y += v.y;
+        s.z += v.z;
+        s.w += v.w;
+      }
+      ((float4*)out)[i] = s;
     }
+    return;
+  }
+  for (int64_t i = blockIdx.x * 256 + threadIdx.x; i < count; i += stride) {
+    float s = part[i];
+    for (int k = 1; k < splits; ++k) s += part[(int64_t)k * count + i];
     out[i] = s;
   }
 }
@@ -719,7 +800,46 @@ __global__ __launch_bounds__(1024) void sum_plain_kernel(const float* __restrict
 
 size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-bool balance_shape_ok(int half) { return half >= 8 && half <= 128 && half % 8 == 0; }
+// fp16 operands are read as 8-dim vectors; fp32 ones one dim per lane.
+bool balance_shape_ok(int half, bool f32) {
+  return f32 ? (half >= 1 && half <= 128) : (half >= 8 && half <= 128 && half % 8 == 0);
+}
+
+// Host view of BalShape: the padded width and the 16-byte vectors per lane
+// of a 32-row block in the normal and transposed packs.
+struct PackDims {
+  int HP, NV, ND, TVPD;
+};
+
+PackDims pack_dims(int half, bool f32) {
+  PackDims d;
+  d.HP = f32 ? KeyPack<float>::padded_half(half) : KeyPack<_Float16>::padded_half(half);
+  d.NV = f32 ? KeyPack<float>::vectors_per_lane(d.HP) : KeyPack<_Float16>::vectors_per_lane(d.HP);
+  d.ND = (d.HP + 31) / 32;
+  d.TVPD = f32 ? 4 : 2;
+  return d;
+}
+
+// MACRO(E, HP) for the precision and padded width of a launch.
+#define MPL_BAL_DISPATCH(F32, HPV, MACRO) \
+  do {                                     \
+    if (F32) {                             \
+      switch (HPV) {                       \
+        case 8: MACRO(float, 8); break;    \
+        case 16: MACRO(float, 16); break;  \
+        case 32: MACRO(float, 32); break;  \
+        case 64: MACRO(float, 64); break;  \
+        default: MACRO(float, 128); break; \
+      }                                    \
+    } else {                               \
+      switch (HPV) {                       \
+        case 16: MACRO(_Float16, 16); break;  \
+        case 32: MACRO(_Float16, 32); break;  \
+        case 64: MACRO(_Float16, 64); break;  \
+        default: MACRO(_Float16, 128); break; \
+      }                                    \
+    }                                      \
+  } while (0)
 
 unsigned grid_for(int64_t items, int64_t per_block, unsigned cap = 4096) {
   int64_t g = cdiv(items, per_block);
@@ -729,16 +849,15 @@ unsigned grid_for(int64_t items, int64_t per_block, unsigned cap = 4096) {
 
 struct BwdLayout {
   size_t qn, qt, kt, sigma, dks, mx, part, u, tpart, total;
-  int HP, NCH, ND, splits, mx_groups;
+  PackDims pd;
+  int splits, mx_groups;
   int64_t mblk, nblk, sbps, mx_tpg;
 };
 
-BwdLayout bwd_layout(int64_t M, int H, int n, int half) {
+BwdLayout bwd_layout(int64_t M, int H, int n, int half, bool f32) {
   BwdLayout L;
   const int HC = 2 * H;
-  L.HP = KeyPack<_Float16>::padded_half(half);
-  L.NCH = L.HP / 16;
-  L.ND = (L.HP + 31) / 32;
+  L.pd = pack_dims(half, f32);
   L.mblk = cdiv(M, 32);
   L.nblk = cdiv(n, 32);
   // the sub-key-side pass: HC * ceil(n / 128) workgroups, the query range
@@ -749,13 +868,14 @@ BwdLayout bwd_layout(int64_t M, int H, int n, int half) {
   if (sp < 1) sp = 1;
   L.sbps = cdiv(L.mblk, sp);
   L.splits = (int)cdiv(L.mblk, L.sbps);
+  const size_t tvec = (size_t)L.pd.ND * L.pd.TVPD * kWave * 16;  // bytes per block of a transposed pack
   size_t o = 0;
   L.qn = o;
-  o += al256((size_t)HC * L.mblk * L.NCH * kWave * 16);
+  o += al256((size_t)HC * L.mblk * L.pd.NV * kWave * 16);
   L.qt = o;
-  o += al256((size_t)HC * L.mblk * L.ND * 2 * kWave * 16);
+  o += al256((size_t)HC * L.mblk * tvec);
   L.kt = o;
-  o += al256((size_t)HC * L.nblk * L.ND * 2 * kWave * 16);
+  o += al256((size_t)HC * L.nblk * tvec);
   L.sigma = o;
   o += al256((size_t)HC * 4);
   L.dks = o;
@@ -775,19 +895,14 @@ BwdLayout bwd_layout(int64_t M, int H, int n, int half) {
 }
 
 template <bool TRANS>
-void launch_pack(int HP, const float* X, int64_t s_hc, int64_t s_row, int64_t nrows, int HC, int half,
-                 const float* scale, int64_t sc_hc, int64_t sc_row, int64_t nblk, uint4* out, hipStream_t s) {
-  const int ND = (HP + 31) / 32;
-  const int64_t total = (int64_t)HC * nblk * (TRANS ? ND * 2 : HP / 16) * kWave;
+void launch_pack(const PackDims& pd, bool f32, const float* X, int64_t s_hc, int64_t s_row, int64_t nrows, int HC,
+                 int half, const float* scale, int64_t sc_hc, int64_t sc_row, int64_t nblk, uint4* out,
+                 hipStream_t s) {
+  const int64_t total = (int64_t)HC * nblk * (TRANS ? pd.ND * pd.TVPD : pd.NV) * kWave;
   const unsigned g = grid_for(total, 256, 8192);
-#define MPL_PACK(HPV) \
-  pack_rows_kernel<TRANS, HPV><<<g, 256, 0, s>>>(X, s_hc, s_row, nrows, HC, half, scale, sc_hc, sc_row, nblk, out)
-  switch (HP) {
-    case 16: MPL_PACK(16); break;
-    case 32: MPL_PACK(32); break;
-    case 64: MPL_PACK(64); break;
-    default: MPL_PACK(128); break;
-  }
+#define MPL_PACK(EV, HPV) \
+  pack_rows_kernel<TRANS, EV, HPV><<<g, 256, 0, s>>>(X, s_hc, s_row, nrows, HC, half, scale, sc_hc, sc_row, nblk, out)
+  MPL_BAL_DISPATCH(f32, pd.HP, MPL_PACK);
 #undef MPL_PACK
 }
 
@@ -837,18 +952,22 @@ extern "C" size_t mpl_balance_state_bytes(int64_t M, int H) {
 }
 
 extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, const float* clean_counts,
-                               int64_t M, int H, int n, int half, int k, const float* temperature, void* state,
-                               float* loss, void* stream) {
+                               int64_t M, int H, int n, int half, int k, int score_dtype, const float* temperature,
+                               void* state, float* loss, void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_balance_fwd: bad shape");
-  MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
-              "mpl_balance_fwd: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL, "mpl_balance_fwd: bad score_dtype %d",
+              score_dtype);
+  const bool f32 = score_dtype == MPL_F32;
+  MPL_REQUIRE(balance_shape_ok(half, f32), MPL_EUNSUPPORTED,
+              "mpl_balance_fwd: %s scoring needs %s (half = %d)", f32 ? "fp32" : "fp16",
+              f32 ? "half <= 128" : "half %% 8 == 0 and half <= 128", half);
   MPL_REQUIRE(loss != nullptr && (M == 0 || (queries && packed_keys && clean_counts && state && temperature)),
               MPL_EINVAL, "mpl_balance_fwd: null buffer");
   hipStream_t s = (hipStream_t)stream;
   const int HC = 2 * H;
-  if (M == 0) {
-    fill_zero_kernel<<<1, 256, 0, s>>>(loss, 1);
+  if (M == 0) {  // f = counts / (M k) and the mean over tokens are 0/0 (memory.py:208-213)
+    fill_value_kernel<<<1, 64, 0, s>>>(loss, 1, __builtin_nanf(""));
     return check_launch("mpl_balance_fwd");
   }
   BalFwdParams p;
@@ -866,31 +985,34 @@ extern "C" int mpl_balance_fwd(const float* queries, int scaled, const void* pac
   p.state = (float4*)state;
   p.parts = (float*)((float4*)state + M * HC);
   const unsigned grid = (unsigned)fwd_groups(M, H);
-  switch (KeyPack<_Float16>::padded_half(half)) {
-    case 16: balance_fwd_kernel<16><<<grid, kBalThreads, 0, s>>>(p); break;
-    case 32: balance_fwd_kernel<32><<<grid, kBalThreads, 0, s>>>(p); break;
-    case 64: balance_fwd_kernel<64><<<grid, kBalThreads, 0, s>>>(p); break;
-    default: balance_fwd_kernel<128><<<grid, kBalThreads, 0, s>>>(p); break;
-  }
+#define MPL_FWD(EV, HPV) balance_fwd_kernel<EV, HPV><<<grid, kBalThreads, 0, s>>>(p)
+  MPL_BAL_DISPATCH(f32, pack_dims(half, f32).HP, MPL_FWD);
+#undef MPL_FWD
   balance_loss_kernel<<<1, 1024, 0, s>>>(p.parts, grid, (float)((double)n / ((double)HC * M)), loss);
   return check_launch("mpl_balance_fwd");
 }
 
-extern "C" size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half) {
-  if (M < 0 || H < 1 || n < 1 || !balance_shape_ok(half)) return 0;
-  return bwd_layout(M, H, n, half).total;
+extern "C" size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half, int score_dtype) {
+  const bool f32 = score_dtype == MPL_F32;
+  if (M < 0 || H < 1 || n < 1 || (score_dtype != MPL_F16 && !f32) || !balance_shape_ok(half, f32)) return 0;
+  return bwd_layout(M, H, n, half, f32).total;
 }
 
 extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat,
                                     const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
                                     const float* clean_counts, const void* state, const float* g_balance,
                                     int balance_temperature_grad, int query_scale, int64_t M, int H, int n,
-                                    int half, int k, const float* temperature, void* workspace, size_t workspace_bytes,
-                                    float* dq_hat, float* dk_hat, float* dlen, float* dlogt, void* stream) {
+                                    int half, int k, int score_dtype, const float* temperature, void* workspace,
+                                    size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
+                                    void* stream) {
   clear_error();
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_lookup_bwd_dense: bad shape");
-  MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
-              "mpl_lookup_bwd_dense: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
+              "mpl_lookup_bwd_dense: bad score_dtype %d", score_dtype);
+  const bool f32 = score_dtype == MPL_F32;
+  MPL_REQUIRE(balance_shape_ok(half, f32), MPL_EUNSUPPORTED,
+              "mpl_lookup_bwd_dense: %s scoring needs %s (half = %d)", f32 ? "fp32" : "fp16",
+              f32 ? "half <= 128" : "half %% 8 == 0 and half <= 128", half);
   const bool bal = g_balance != nullptr;
   const bool routed = sub_idx != nullptr || d_sub != nullptr;
   const bool btg = bal && balance_temperature_grad != 0;
@@ -912,7 +1034,7 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   MPL_REQUIRE(q_hat && k_hat && packed_keys && temperature, MPL_EINVAL, "mpl_lookup_bwd_dense: null buffer");
   MPL_REQUIRE(!bal || (clean_counts && state && dq_hat), MPL_EINVAL,
               "mpl_lookup_bwd_dense: the balance term needs clean_counts, state and dq_hat");
-  const BwdLayout L = bwd_layout(M, H, n, half);
+  const BwdLayout L = bwd_layout(M, H, n, half, f32);
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_lookup_bwd_dense: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
   char* ws = (char*)workspace;
@@ -927,9 +1049,10 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   float* tpart = (float*)(ws + L.tpart);
   const float* rho = scaled ? q_len : nullptr;
 
-  launch_pack<false>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
-  launch_pack<true>(L.HP, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);
-  if (bal) launch_pack<true>(L.HP, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
+  launch_pack<false>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
+  launch_pack<true>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);
+  if (bal)
+    launch_pack<true>(L.pd, f32, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
   const float inv_mk = (float)(1.0 / ((double)M * k));
   const float coef = (float)((double)n / ((double)HC * M));
   bwd_max_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC, k,
@@ -983,19 +1106,14 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   pk.k = k;
   pk.dk_scale = dks;
   const unsigned gk = (unsigned)(HC * cdiv(n, kRowsPerGroup) * L.splits);
-#define MPL_GRAD(HPV)                                                                     \
-  if (bal) balance_grad_kernel<kModeDQ, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
-  balance_grad_kernel<kModeDK, HPV><<<gk, kBalThreads, 0, s>>>(pk)
-  switch (L.HP) {
-    case 16: MPL_GRAD(16); break;
-    case 32: MPL_GRAD(32); break;
-    case 64: MPL_GRAD(64); break;
-    default: MPL_GRAD(128); break;
-  }
+#define MPL_GRAD(EV, HPV)                                                        \
+  if (bal) balance_grad_kernel<kModeDQ, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
+  balance_grad_kernel<kModeDK, EV, HPV><<<gk, kBalThreads, 0, s>>>(pk)
+  MPL_BAL_DISPATCH(f32, L.pd.HP, MPL_GRAD);
 #undef MPL_GRAD
   if (L.splits > 1) {
-    const int64_t c4 = (int64_t)HC * n * half / 4;
-    split_sum_kernel<<<grid_for(c4, 256), 256, 0, s>>>((const float4*)part, L.splits, c4, (float4*)dk_hat);
+    const int64_t cnt = (int64_t)HC * n * half;
+    split_sum_kernel<<<grid_for(cnt, 256), 256, 0, s>>>(part, L.splits, cnt, dk_hat);
   }
   if (btg) {
     const unsigned gt = grid_for(M * HC, 256);
@@ -1010,15 +1128,15 @@ namespace {
 
 struct DivLayout {
   size_t kt, part, lpart, total;
-  int HP, splits;
+  PackDims pd;
+  int splits;
   int64_t nblk, sbps, groups;
 };
 
-DivLayout div_layout(int H, int n, int half) {
+DivLayout div_layout(int H, int n, int half, bool f32) {
   DivLayout L;
   const int HC = 2 * H;
-  L.HP = KeyPack<_Float16>::padded_half(half);
-  const int ND = (L.HP + 31) / 32;
+  L.pd = pack_dims(half, f32);
   L.nblk = cdiv(n, 32);
   const int64_t kgroups = (int64_t)HC * cdiv(n, kRowsPerGroup);
   int64_t sp = cdiv(512, kgroups);
@@ -1029,7 +1147,7 @@ DivLayout div_layout(int H, int n, int half) {
   L.groups = kgroups * L.splits;
   size_t o = 0;
   L.kt = o;
-  o += al256((size_t)HC * L.nblk * ND * 2 * kWave * 16);
+  o += al256((size_t)HC * L.nblk * L.pd.ND * L.pd.TVPD * kWave * 16);
   L.part = o;
   o += al256((size_t)L.splits * HC * n * half * 4);
   L.lpart = o;
@@ -1041,20 +1159,24 @@ DivLayout div_layout(int H, int n, int half) {
 }  // namespace
 }  // namespace mpl
 
-extern "C" size_t mpl_key_diversity_workspace_bytes(int H, int n, int half) {
-  if (H < 1 || n < 1 || !balance_shape_ok(half)) return 0;
-  return div_layout(H, n, half).total;
+extern "C" size_t mpl_key_diversity_workspace_bytes(int H, int n, int half, int score_dtype) {
+  const bool f32 = score_dtype == MPL_F32;
+  if (H < 1 || n < 1 || (score_dtype != MPL_F16 && !f32) || !balance_shape_ok(half, f32)) return 0;
+  return div_layout(H, n, half, f32).total;
 }
 
 extern "C" int mpl_key_diversity(const float* k_hat, const void* packed_keys, int H, int n, int half,
-                                 void* workspace, size_t workspace_bytes, float* loss, float* d_k_hat,
-                                 void* stream) {
+                                 int score_dtype, void* workspace, size_t workspace_bytes, float* loss,
+                                 float* d_k_hat, void* stream) {
   clear_error();
   MPL_REQUIRE(H >= 1 && n >= 1, MPL_EINVAL, "mpl_key_diversity: bad shape");
-  MPL_REQUIRE(balance_shape_ok(half), MPL_EUNSUPPORTED,
-              "mpl_key_diversity: fp16 scoring needs half %% 8 == 0 and half <= 128 (half = %d)", half);
+  MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL, "mpl_key_diversity: bad score_dtype %d",
+              score_dtype);
+  const bool f32 = score_dtype == MPL_F32;
+  MPL_REQUIRE(balance_shape_ok(half, f32), MPL_EUNSUPPORTED, "mpl_key_diversity: %s Gram tiles need %s (half = %d)",
+              f32 ? "fp32" : "fp16", f32 ? "half <= 128" : "half %% 8 == 0 and half <= 128", half);
   MPL_REQUIRE(k_hat && packed_keys && loss, MPL_EINVAL, "mpl_key_diversity: null buffer");
-  const DivLayout L = div_layout(H, n, half);
+  const DivLayout L = div_layout(H, n, half, f32);
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_key_diversity: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
   hipStream_t s = (hipStream_t)stream;
@@ -1063,7 +1185,7 @@ extern "C" int mpl_key_diversity(const float* k_hat, const void* packed_keys, in
   uint4* kt = (uint4*)(ws + L.kt);
   float* part = (float*)(ws + L.part);
   float* lpart = (float*)(ws + L.lpart);
-  launch_pack<true>(L.HP, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
+  launch_pack<true>(L.pd, f32, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
   // D = H * 2 * n * (n - 1) (memory.py:240); n = 1 gives 0/0 as the reference
   const double D = (double)HC * n * (double)(n - 1);
   BalGradParams p = {};
@@ -1082,15 +1204,12 @@ extern "C" int mpl_key_diversity(const float* k_hat, const void* packed_keys, in
   p.out = d_k_hat == nullptr ? nullptr : (L.splits == 1 ? d_k_hat : part);
   p.u = lpart;
   const unsigned g = (unsigned)L.groups;
-  switch (L.HP) {
-    case 16: balance_grad_kernel<kModeDiv, 16><<<g, kBalThreads, 0, s>>>(p); break;
-    case 32: balance_grad_kernel<kModeDiv, 32><<<g, kBalThreads, 0, s>>>(p); break;
-    case 64: balance_grad_kernel<kModeDiv, 64><<<g, kBalThreads, 0, s>>>(p); break;
-    default: balance_grad_kernel<kModeDiv, 128><<<g, kBalThreads, 0, s>>>(p); break;
-  }
+#define MPL_DIV(EV, HPV) balance_grad_kernel<kModeDiv, EV, HPV><<<g, kBalThreads, 0, s>>>(p)
+  MPL_BAL_DISPATCH(f32, L.pd.HP, MPL_DIV);
+#undef MPL_DIV
   if (d_k_hat != nullptr && L.splits > 1) {
-    const int64_t c4 = (int64_t)HC * n * half / 4;
-    split_sum_kernel<<<grid_for(c4, 256), 256, 0, s>>>((const float4*)part, L.splits, c4, (float4*)d_k_hat);
+    const int64_t cnt = (int64_t)HC * n * half;
+    split_sum_kernel<<<grid_for(cnt, 256), 256, 0, s>>>(part, L.splits, cnt, d_k_hat);
   }
   sum_plain_kernel<<<1, 1024, 0, s>>>(lpart, L.groups, 1.0 / D, loss);
   return check_launch("mpl_key_diversity");

@@ -95,7 +95,7 @@ class LazyAux(dict):
     ``top1_weight`` each on their own, the first time they are read."""
 
     _LAZY = ("balance_loss", "subkey_counts", "slot_counts")
-    _INTERNAL = ("_f", "_p", "_cos", "_counts", "_state")
+    _INTERNAL = ("_counts", "_state")
 
     def __init__(self, eager: Dict[str, Any], compute, **lazy):
         super().__init__(eager)
@@ -362,8 +362,8 @@ class MemoryPool:
     def _routing_stats(self, params, res, k_hat, T, q_len, sub_idx, slots, weights, noisy,
                        packed, score_code, M):
         """memory.py:196-215 from the selected ids: the counts on the GPU
-        (mpl_route_counts); the balance loss fused over the MFMA score tiles
-        (mpl_balance_fwd) with fp16 scoring, else from the dense cosine."""
+        (mpl_route_counts) and the balance loss fused over the MFMA score
+        tiles of the scoring precision (mpl_balance_fwd)."""
         H, n, k = self.heads, self.n_sub_keys, self.top_k
         half = self.d_key // 2
         dev = sub_idx.device
@@ -379,24 +379,12 @@ class MemoryPool:
         check(L.mpl_route_counts(ptr(slots), ptr(clean), M, H, n, k, ptr(subkey_counts), ptr(clean_counts),
                                  ptr(slot_counts), stream), "mpl_route_counts")
         stats = {"subkey_counts": subkey_counts, "slot_counts": slot_counts}
-        if score_code == MPL_F16 and M > 0:
-            scaled = int(bool(self.balance_temperature_grad and self.query_scale))
-            state = torch.empty(max(L.mpl_balance_state_bytes(M, H), 16), dtype=torch.uint8, device=dev)
-            loss = torch.empty(1, dtype=torch.float32, device=dev)
-            check(L.mpl_balance_fwd(ptr(res["q"]), scaled, ptr(packed), ptr(clean_counts), M, H, n, half, k,
-                                    ptr(T), ptr(state), ptr(loss), stream), "mpl_balance_fwd")
-            stats.update(balance_loss=loss.reshape(()), _counts=clean_counts, _state=state)
-            return stats
-        f = clean_counts / (M * k)
-        q_hat = res["q_hat"]
-        cos = torch.einsum("mhcd,hcnd->mhcn", q_hat, k_hat)
-        if self.balance_temperature_grad:
-            p_scores = cos * T * (q_len[..., None] if q_len is not None else 1.0)
-        else:
-            p_scores = cos * T
-        p = torch.softmax(p_scores, dim=-1)
-        P = p.mean(0)
-        stats.update(balance_loss=n * torch.mean(torch.sum(f * P, dim=-1)), _f=f, _p=p, _cos=cos)
+        scaled = int(bool(self.balance_temperature_grad and self.query_scale))
+        state = torch.empty(max(L.mpl_balance_state_bytes(M, H), 16), dtype=torch.uint8, device=dev)
+        loss = torch.empty(1, dtype=torch.float32, device=dev)
+        check(L.mpl_balance_fwd(ptr(res["q"]) if M > 0 else None, scaled, ptr(packed), ptr(clean_counts), M, H, n,
+                                half, k, score_code, ptr(T), ptr(state), ptr(loss), stream), "mpl_balance_fwd")
+        stats.update(balance_loss=loss.reshape(()), _counts=clean_counts, _state=state)
         return stats
 
     def _clean_sub_idx(self, q, packed, score_code, T, M):
@@ -421,27 +409,28 @@ def _fp16_gram_ok(half: int) -> bool:
 
 
 class _KeyDiversity(torch.autograd.Function):
-    """memory.py:230-240 on fp16 MFMA Gram tiles (mpl_key_diversity); the
-    gradient with respect to the normalised keys is formed in the forward
-    (one pass over the Gram tiles) and taken through the l2-normalisation
-    backward (mpl_l2_normalize_bwd) with the upstream gradient."""
+    """memory.py:230-240 on MFMA Gram tiles (mpl_key_diversity) in fp16 or
+    fp32; the gradient with respect to the normalised keys is formed in the
+    forward (one pass over the Gram tiles) and taken through the
+    l2-normalisation backward (mpl_l2_normalize_bwd) with the upstream
+    gradient."""
 
     @staticmethod
-    def forward(ctx, sub_keys):
+    def forward(ctx, sub_keys, code):
         H, C, n, half = sub_keys.shape
         dev = sub_keys.device
         L = _lib.lib()
         stream = _lib.stream_ptr(dev)
         src = sub_keys.detach().float().contiguous()
         k_hat = torch.empty_like(src)
-        packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, MPL_F16), dtype=torch.uint8, device=dev)
-        check(L.mpl_pack_keys(ptr(src), H, n, half, MPL_F16, ptr(k_hat), ptr(packed), stream), "mpl_pack_keys")
-        wsb = L.mpl_key_diversity_workspace_bytes(H, n, half)
+        packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, code), dtype=torch.uint8, device=dev)
+        check(L.mpl_pack_keys(ptr(src), H, n, half, code, ptr(k_hat), ptr(packed), stream), "mpl_pack_keys")
+        wsb = L.mpl_key_diversity_workspace_bytes(H, n, half, code)
         ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
         loss = torch.empty(1, dtype=torch.float32, device=dev)
         dk = torch.empty_like(src) if ctx.needs_input_grad[0] else None
-        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, ptr(ws), wsb, ptr(loss), ptr(dk), stream),
-              "mpl_key_diversity")
+        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, code, ptr(ws), wsb, ptr(loss), ptr(dk),
+                                  stream), "mpl_key_diversity")
         ctx.save_for_backward(src, dk)
         ctx.dtype = sub_keys.dtype
         return loss.reshape(())
@@ -454,23 +443,25 @@ class _KeyDiversity(torch.autograd.Function):
         gs = g.reshape(1).float().contiguous()
         check(_lib.lib().mpl_l2_normalize_bwd(ptr(src), ptr(dk), H * C * n, half, NORM_EPS, ptr(gs), ptr(dx),
                                               _lib.stream_ptr(src.device)), "mpl_l2_normalize_bwd")
-        return dx.to(ctx.dtype)
+        return dx.to(ctx.dtype), None
 
 
-def key_diversity_loss(sub_keys: torch.Tensor) -> torch.Tensor:
+def key_diversity_loss(sub_keys: torch.Tensor, score_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """memory.py:230-240: mean squared off-diagonal cosine inside each
-    sub-key codebook, differentiable with respect to ``sub_keys``.  Sub-key
-    widths the fp16 Gram kernel does not take (d_key/2 not a multiple of 8 or
-    above 128) use the dense cosine through library GEMMs."""
+    sub-key codebook, differentiable with respect to ``sub_keys``.  The Gram
+    tiles run on MFMA in ``score_dtype``: fp16 (sub-key widths d_key/2 that
+    are multiples of 8, up to 128) or fp32 (any width up to 128, the
+    reference's precision).  By default fp16 where it applies, else fp32; a
+    pool passes its own scoring precision (``MemoryPool.score_dtype``)."""
     if sub_keys.device.type != "cuda":
         raise RuntimeError("key_diversity_loss runs on the GPU only (libmpl.so)")
     H, C, n, half = sub_keys.shape
-    if _fp16_gram_ok(half):
-        return _KeyDiversity.apply(sub_keys)
-    keys = sub_keys.float() * torch.rsqrt((sub_keys.float() ** 2).sum(-1, keepdim=True) + NORM_EPS)
-    gram = torch.matmul(keys, keys.transpose(-1, -2).contiguous())
-    off = gram * (1.0 - torch.eye(n, device=sub_keys.device))
-    return off.pow(2).sum() / (H * C * n * (n - 1))
+    if score_dtype is None:
+        score_dtype = torch.float16 if _fp16_gram_ok(half) else torch.float32
+    if half > 128 or (score_dtype == torch.float16 and not _fp16_gram_ok(half)):
+        raise ValueError(f"key_diversity_loss: no {score_dtype} Gram kernel for sub-key width {half} "
+                         "(fp16: multiples of 8 up to 128; fp32: up to 128)")
+    return _KeyDiversity.apply(sub_keys, _dtype_code(score_dtype))
 
 
 def revive_dead_keys(sub_keys: torch.Tensor, subkey_usage: torch.Tensor, queries: torch.Tensor, rng,
@@ -564,15 +555,18 @@ class _LookupFunction(torch.autograd.Function):
                                      ptr(res["sub_scores"]), M, H, k, vshuffle, None,
                                      ptr(d_sub), ptr(dlogt_part), stream), "mpl_lookup_bwd_route")
 
-        # dense over n: the balance loss (memory.py:208-213) and, with fp16
-        # scoring, the whole sub-key gradient on MFMA tiles
-        dq_extra = dk_extra = dlen_extra = dlogt_extra = None
+        # dense over n on MFMA tiles of the scoring precision: the balance
+        # loss (memory.py:208-213) together with the routed sub-key term.
+        # Without the balance term, fp32 scoring takes the routed term alone
+        # from a sort-by-key segmented sum (O(M k) instead of O(M n)).
+        dq_extra = dlen_extra = dlogt_extra = None
         btg = pool.balance_temperature_grad
         raw_keys = sub_keys.detach().float().contiguous()
         dk = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
-        dense = M > 0 and res["score_code"] == MPL_F16 and _fp16_gram_ok(half)
+        bal = g_balance is not None and "_state" in ctx.internal
+        code = res["score_code"]
+        dense = M > 0 and (code == MPL_F16 or bal)
         if dense:
-            bal = g_balance is not None and "_state" in ctx.internal
             dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
             gb = None
             if bal:
@@ -580,46 +574,29 @@ class _LookupFunction(torch.autograd.Function):
                 dlen_extra = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if (btg and q_len is not None) else None
                 dlogt_extra = torch.empty(1, dtype=torch.float32, device=dev) if btg else None
                 gb = g_balance.reshape(1).float().contiguous()
-            wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half)
+            wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half, code)
             ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
             check(L.mpl_lookup_bwd_dense(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
                                          ptr(d_sub), ptr(ctx.internal["_counts"]) if bal else None,
                                          ptr(ctx.internal["_state"]) if bal else None, ptr(gb), int(btg),
-                                         int(bool(pool.query_scale)), M, H, n, half, k, ptr(T), ptr(ws), wsb,
+                                         int(bool(pool.query_scale)), M, H, n, half, k, code, ptr(T), ptr(ws), wsb,
                                          ptr(dq_extra), ptr(dk_hat), ptr(dlen_extra), ptr(dlogt_extra), stream),
                   "mpl_lookup_bwd_dense")
             check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
                                          stream), "mpl_l2_normalize_bwd")
-        elif g_balance is not None and M > 0:
-            f, p = ctx.internal["_f"], ctx.internal["_p"]
-            a = g_balance.reshape(()).float() * (n / (2.0 * H * M))
-            dp = a * f[None]
-            dps = p * (dp - (p * dp).sum(-1, keepdim=True))
-            scale = T * (q_len[..., None] if (btg and q_len is not None) else 1.0)
-            dcos = (dps * scale).contiguous()
-            hc_first = dcos.permute(1, 2, 0, 3).reshape(2 * H, M, n)
-            kh = k_hat.reshape(2 * H, n, half)
-            qh = q_hat.permute(1, 2, 0, 3).reshape(2 * H, M, half).contiguous()
-            dq_extra = torch.bmm(hc_first, kh).reshape(H, 2, M, half).permute(2, 0, 1, 3).contiguous()
-            dk_extra = torch.bmm(hc_first.transpose(1, 2).contiguous(), qh).reshape(H, 2, n, half).contiguous()
-            if btg:
-                cos = ctx.internal["_cos"]
-                scores = cos * T * (q_len[..., None] if q_len is not None else 1.0)
-                dlogt_extra = (dps * scores).sum().reshape(1).float()
-                if q_len is not None:
-                    dlen_extra = (dps * cos * T).sum(-1).contiguous()
 
         # queries
         dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
         check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
                                        ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
                                        ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
-        # sub-keys (fp32 scoring or no tokens): sort-by-key segmented sum
+        # sub-keys (fp32 scoring without the balance term, or no tokens):
+        # sort-by-key segmented sum
         if not dense:
             wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
             ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
             check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
-                                        ptr(dk_extra), M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
+                                        None, M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
                   "mpl_lookup_bwd_keys")
         # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
         dlt = torch.empty(1, dtype=torch.float32, device=dev)

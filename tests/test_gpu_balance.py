@@ -1,11 +1,12 @@
 """Routing counts and the fused load-balance loss on the GPU (include/mpl.h
-mpl_route_counts, mpl_balance_fwd, mpl_balance_bwd) against the oracle
+mpl_route_counts, mpl_balance_fwd, mpl_lookup_bwd_dense) against the oracle
 (oracle/lookup.py aux_stats and oracle/backward.py lookup_backward, fp64).
 
 Counts are integers and must match exactly.  The balance loss and its
-gradients come from fp16 MFMA score tiles: the loss is checked to 1e-3
-relative, the gradients to 1e-2 of their largest magnitude (the fp16-path
-tolerance), d log_temperature against the sum of the magnitudes of its
+gradients come from MFMA score tiles of the scoring precision.  fp16: the
+loss is checked to 1e-3 relative, the gradients to 1e-2 of their largest
+magnitude (the fp16-path tolerance); fp32: 1e-5 for both.  d
+log_temperature is measured against the sum of the magnitudes of its
 terms."""
 
 import numpy as np
@@ -120,10 +121,54 @@ def test_balance_loss_and_gradients(gpu_lib, n, H, d_key, M, k, qs, btg, seed):
         assert float(gt) == 0.0  # T is stop-gradient in the balance logits (memory.py:210)
 
 
+@pytest.mark.parametrize("n,H,d_key,M,k,qs,btg,seed", [
+    (128, 4, 256, 1024, 16, False, False, 51),  # the fact-task layer: fp32, 16,384 slots, 1,024 tokens
+    (100, 2, 20, 77, 8, True, True, 52),        # half = 10 (not a multiple of 8), ragged n and M
+    (300, 1, 64, 513, 4, False, True, 53),      # query range split over workgroups, temperature gradient
+    (40, 2, 6, 33, 5, True, False, 54),         # half = 3: the narrowest padded width (8)
+])
+def test_balance_loss_and_gradients_fp32(gpu_lib, n, H, d_key, M, k, qs, btg, seed):
+    """memory.py:208-213 with fp32 scoring on v_mfma_f32_32x32x2_f32 tiles
+    (mpl_balance_fwd / mpl_lookup_bwd_dense with MPL_F32): loss and the
+    gradients through the raw queries, raw sub-keys and log_temperature,
+    against the fp64 oracle for the GPU's selection, to 1e-5."""
+    pool, params, tq, q, keys, vals, _, log_t = _setup(
+        seed, n=n, H=H, d_key=d_key, d=16, k=k, M=M, values_dtype=torch.float32, score_dtype=torch.float32,
+        query_scale=qs, btg=btg)
+    res_gpu = pool.lookup(params, tq.detach())
+    out, aux = pool.apply({"params": params}, tq, sparse_grad=True)
+    assert "_state" in aux.internal
+    gq, gk, gt = torch.autograd.grad(aux["balance_loss"], [tq, params["sub_keys"], params["log_temperature"]])
+    res = ol.lookup_forward(q, keys, vals, float(log_t), top_k_=k, query_scale=qs, dtype=np.float64)
+    sel = _with_selection(res, res_gpu["sub_idx"].cpu().numpy(), res_gpu["flat_idx"].cpu().numpy(),
+                          res_gpu["slots"].cpu().numpy())
+    ao = ol.aux_stats(sel, n=n, noisy=False, balance_temperature_grad=btg)
+    np.testing.assert_allclose(float(aux["balance_loss"]), ao["balance_loss"], rtol=1e-5)
+    ref = ob.lookup_backward(sel, vals, np.zeros((M, 16)), n=n, query_scale=qs, g_balance=1.0, f=ao["_f"],
+                             balance_temperature_grad=btg)
+    _check(gq.cpu().numpy(), ref["d_queries"], 1e-5, "d_queries")
+    _check(gk.cpu().numpy(), ref["d_sub_keys"], 1e-5, "d_sub_keys")
+    if btg:
+        lt_scale = float(np.abs(ref["d_cos"] * sel["cos"]).sum())
+        _check(float(gt), ref["d_log_temperature"], 1e-5, "d_log_temperature", lt_scale)
+    else:
+        assert float(gt) == 0.0
+
+
+def test_balance_loss_of_no_tokens_is_nan(gpu_lib):
+    """memory.py:208-213 with M = 0: f = counts / (M k) and the mean over
+    tokens are both 0/0."""
+    for sd in (torch.float16, torch.float32):
+        pool, params, tq, *_ = _setup(55, n=64, H=2, d_key=32, d=16, k=4, M=3, values_dtype=torch.float16,
+                                      score_dtype=sd, query_scale=False, btg=False)
+        out, aux = pool.apply({"params": params}, tq[:0])
+        assert out.shape == (0, 16) and torch.isnan(aux["balance_loss"])
+
+
 def test_balance_scales_with_upstream_gradient_and_matches_dense_path(gpu_lib):
-    """The fused path against the library-GEMM path of the same module
-    (fp32 scoring) on one input: the losses agree to the fp16 scoring error
-    and the gradients scale linearly with the balance coefficient."""
+    """The fp16 path against the fp32 path of the same module on one input:
+    the losses agree to the fp16 scoring error and the gradients scale
+    linearly with the balance coefficient."""
     n, H, d_key, M, k = 128, 2, 64, 200, 8
     pool16, params, tq, *_ = _setup(41, n=n, H=H, d_key=d_key, d=16, k=k, M=M, values_dtype=torch.float16,
                                     score_dtype=torch.float16, query_scale=False, btg=False)

@@ -3,9 +3,10 @@
 against the oracle (oracle/lookup.py key_diversity_loss / revive_dead_keys,
 oracle/backward.py key_diversity_backward; fp64).
 
-key_diversity_loss runs on fp16 MFMA Gram tiles: the loss is checked to
-2e-3 relative and its gradient to 1e-2 of the largest magnitude (the fp16
-path tolerance).  revive_dead_keys is fp32 elementwise work: 1e-6."""
+key_diversity_loss runs on fp16 or fp32 MFMA Gram tiles.  fp16: the loss is
+checked to 2e-3 relative and its gradient to 1e-2 of the largest magnitude
+(the fp16 path tolerance); fp32: 1e-5 for both.  revive_dead_keys is fp32
+elementwise work: 1e-6."""
 
 import numpy as np
 import pytest
@@ -36,6 +37,27 @@ def test_key_diversity_loss_and_gradient(gpu_lib, H, n, half, seed):
     ref = 3.0 * ob.key_diversity_backward(raw)
     err = np.abs(g.cpu().numpy() - ref).max() / np.abs(ref).max()
     assert err <= 1e-2, f"d sub_keys: max error {err:.3g} of the largest magnitude"
+
+
+@pytest.mark.parametrize("H,n,half,seed", [
+    (4, 128, 128, 11),  # the fact-task codebooks
+    (2, 100, 10, 12),   # half = 10: only the fp32 tiles take it
+    (1, 300, 3, 13),    # half = 3, query range split
+    (1, 2, 64, 14),     # two keys
+])
+def test_key_diversity_fp32(gpu_lib, H, n, half, seed):
+    rng = np.random.default_rng(seed)
+    raw = (rng.standard_normal((H, 2, n, half)) * 0.7).astype(np.float32)
+    t = torch.tensor(raw, device="cuda", requires_grad=True)
+    loss = mem.key_diversity_loss(t, torch.float32)
+    (g,) = torch.autograd.grad(3.0 * loss, [t])
+    np.testing.assert_allclose(float(loss), ol.key_diversity_loss(raw), rtol=1e-5)
+    ref = 3.0 * ob.key_diversity_backward(raw)
+    err = np.abs(g.cpu().numpy() - ref).max() / np.abs(ref).max()
+    assert err <= 1e-5, f"d sub_keys: max error {err:.3g} of the largest magnitude"
+    if half % 8:
+        with pytest.raises(ValueError):
+            mem.key_diversity_loss(t, torch.float16)
 
 
 def test_key_diversity_collapsed_codebook_is_one(gpu_lib):
