@@ -41,11 +41,12 @@ constexpr int kRowThreads = 256;                       // four rows (waves) per 
 
 __device__ __forceinline__ uint64_t lanes_below(int lane) { return (1ull << lane) - 1ull; }
 
-// Mask of the valid lanes whose 8-bit digit equals this lane's.
+// Mask of the valid lanes whose BITS-bit digit equals this lane's.
+template <int BITS>
 __device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid) {
   uint64_t peers = __ballot(valid);
 #pragma unroll
-  for (int b = 0; b < 8; ++b) {
+  for (int b = 0; b < BITS; ++b) {
     const bool bit = (digit >> b) & 1u;
     const uint64_t m = __ballot(bit);
     peers &= bit ? m : ~m;
@@ -54,21 +55,25 @@ __device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid) {
 }
 
 // ------------------------------------------------------------ radix sort
+// Digits of BITS = 8, 9 or 10 bits (2^BITS bins), chosen per key width so
+// that the passes are as few as possible (pool sizes up to 2^20: two passes).
+template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n,
                                                                    int shift, uint32_t* __restrict__ hist,
                                                                    int64_t ntiles) {
-  __shared__ uint32_t h[256];
+  constexpr int BINS = 1 << BITS;
+  __shared__ uint32_t h[BINS];
   const int tid = threadIdx.x;
-  h[tid] = 0;
+  for (int i = tid; i < BINS; i += kSortThreads) h[i] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
 #pragma unroll
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = base + r * kSortThreads + tid;
-    if (i < n) atomicAdd(&h[(keys[i] >> shift) & 255u], 1u);  // integer LDS counts: order-free
+    if (i < n) atomicAdd(&h[(keys[i] >> shift) & (BINS - 1)], 1u);  // integer LDS counts: order-free
   }
   __syncthreads();
-  hist[(int64_t)tid * ntiles + blockIdx.x] = h[tid];
+  for (int i = tid; i < BINS; i += kSortThreads) hist[(int64_t)i * ntiles + blockIdx.x] = h[i];
 }
 
 // In-place exclusive scan of a[0, len) by one workgroup; *total (if not
@@ -132,31 +137,49 @@ __global__ __launch_bounds__(1024) void digit_scan_kernel(uint32_t* __restrict__
 
 // Stable scatter of one radix pass.  vals_in == null means the identity
 // (values = input positions).  hist_scan holds each digit's scan over tiles;
-// the digits' starting offsets are the scan of `totals`, done here in LDS.
+// the digits' starting offsets are the scan of `totals`, done here in LDS
+// (thread t owns digits [t PER, t PER + PER)).
+template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in, uint32_t* __restrict__ keys_out,
     uint32_t* __restrict__ vals_out, int64_t n, int shift, const uint32_t* __restrict__ hist_scan, int64_t ntiles,
     const uint32_t* __restrict__ totals) {
-  __shared__ uint32_t tile_off[256];
-  __shared__ uint32_t seen[256];  // keys of each digit in earlier rounds of this tile
-  __shared__ uint32_t wave_cnt[kSortThreads / kWave][256];
+  constexpr int BINS = 1 << BITS;
+  constexpr int PER = BINS / kSortThreads;  // digits per thread
+  constexpr int WAVES = kSortThreads / kWave;
+  static_assert(PER >= 1 && BINS % kWave == 0, "at least one digit per thread");
+  __shared__ uint32_t tile_off[BINS];
+  __shared__ uint32_t seen[BINS];  // keys of each digit in earlier rounds of this tile
+  __shared__ uint32_t wave_cnt[WAVES][BINS];
+  __shared__ uint32_t wsum[WAVES];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   {  // digit base = exclusive scan of the digit totals
-    const uint32_t t = totals[tid];
-    uint32_t x = t;
+    uint32_t t[PER];
+    uint32_t own = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      t[j] = totals[tid * PER + j];
+      own += t[j];
+    }
+    uint32_t x = own;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
       const uint32_t y = __shfl_up(x, off);
       if (lane >= off) x += y;
     }
-    if (lane == kWave - 1) wave_cnt[0][wave] = x;
+    if (lane == kWave - 1) wsum[wave] = x;
     __syncthreads();
-    uint32_t before = 0;
-    for (int w = 0; w < wave; ++w) before += wave_cnt[0][w];
-    tile_off[tid] = before + x - t + hist_scan[(int64_t)tid * ntiles + blockIdx.x];
-    seen[tid] = 0;
+    uint32_t run = x - own;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int d = tid * PER + j;
+      tile_off[d] = run + hist_scan[(int64_t)d * ntiles + blockIdx.x];
+      seen[d] = 0;
+      run += t[j];
+    }
     __syncthreads();
   }
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
@@ -165,11 +188,13 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
     const bool valid = i < n;
     const uint32_t key = keys_in[valid ? i : 0];
     const uint32_t val = vals_in != nullptr ? vals_in[valid ? i : 0] : (uint32_t)i;
-    const uint32_t digit = (key >> shift) & 255u;
-    const uint64_t peers = digit_peers(digit, valid);
+    const uint32_t digit = (key >> shift) & (BINS - 1);
+    const uint64_t peers = digit_peers<BITS>(digit, valid);
     const uint32_t rank = (uint32_t)__popcll(peers & lanes_below(lane));
+    // this wave's row of counts: zeroed and filled by the wave itself (its
+    // LDS accesses complete in order), read by all after the barrier
 #pragma unroll
-    for (int j = 0; j < 4; ++j) wave_cnt[wave][lane * 4 + j] = 0;
+    for (int j = 0; j < BINS / kWave; ++j) wave_cnt[wave][lane * (BINS / kWave) + j] = 0;
     if (valid && rank == 0) wave_cnt[wave][digit] = (uint32_t)__popcll(peers);
     __syncthreads();
     uint32_t before = 0;
@@ -180,10 +205,14 @@ __global__ __launch_bounds__(kSortThreads) void radix_scatter_kernel(
       vals_out[pos] = val;
     }
     __syncthreads();
-    uint32_t add = 0;
 #pragma unroll
-    for (int w = 0; w < kSortThreads / kWave; ++w) add += wave_cnt[w][tid];
-    seen[tid] += add;
+    for (int j = 0; j < PER; ++j) {
+      const int d = tid * PER + j;
+      uint32_t add = 0;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) add += wave_cnt[w][d];
+      seen[d] += add;
+    }
     __syncthreads();
   }
 }
@@ -315,11 +344,20 @@ __device__ __forceinline__ float wave_sq(const RowVec<W> (&a)[VPL]) {
   return s;
 }
 
+// Thread 0 of workgroup 0 also finishes the segment table (seg_start[U] =
+// n, num_unique = U, U clamped to cap), which the fix-up launches read.
 template <int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
     const uint32_t* __restrict__ sorted_p, const int32_t* __restrict__ seg_of,
     const float* __restrict__ weights, const float* __restrict__ g, int fpt, int nv, int64_t n,
-    float* __restrict__ rows, float* __restrict__ row_sq, float* __restrict__ partial) {
+    float* __restrict__ rows, float* __restrict__ row_sq, float* __restrict__ partial,
+    const uint32_t* __restrict__ num_seg, int32_t* __restrict__ seg_start, int32_t* __restrict__ num_unique,
+    int64_t cap) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    const uint32_t U = (uint32_t)min((int64_t)*num_seg, cap);
+    seg_start[U] = (int32_t)n;
+    *num_unique = (int32_t)U;
+  }
   const int64_t r = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t r0 = r * kRangeLen;
@@ -363,8 +401,11 @@ __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
   // lane (coalesced), and broadcast with shuffles; the g rows of the next
   // batch of B entries load while the current batch is accumulated (B rows
   // of VPL vectors per buffer, so the registers do not grow with the width).
+  // At 8,192 tokens x 64 fetches of d = 256 the merge took 151 / 137 / 140 /
+  // 141 us with B = 8 / 4 / 2 / 1: the g rows come from L2 and the Infinity
+  // Cache (512 MB per call), and deeper batches only add cache pressure.
   static_assert(kRangeLen == 2 * kWave, "two entries per lane");
-  constexpr int B = VPL >= 8 ? 1 : 8 / VPL;
+  constexpr int B = VPL >= 4 ? 1 : 4 / VPL;
   uint32_t pe[2];
   int se[2];
   float we[2];
@@ -447,16 +488,82 @@ __device__ __forceinline__ void pad_rows(const uint32_t* __restrict__ num_seg, i
   }
 }
 
-// Segments that cross range boundaries: one wave per range, which finishes
-// the segment that starts in it and continues past its end (the last segment
-// of the range), adding that segment's partial rows in range order.  Rows of
-// segments inside one range were written by seg_reduce_kernel.  The same
-// launch pads rows [U, cap) with its last workgroups, so the bandwidth-bound
-// padding runs beside the latency-bound chains of hot segments.
+// Segments that cross range boundaries are finished in two levels, so that a
+// hot row spanning hundreds of ranges is summed by many waves at once in a
+// fixed order.  Level 1 (seg_fix_chunks_kernel): for a crossing segment
+// spanning ranges [ra, rb], the ranges are cut into chunks of kFixChunk
+// starting at ra; the wave of a chunk's first range adds the chunk's
+// partial rows in range order into chunk[head][which] (which = 1 when the
+// segment starts in that range, so that the two crossing segments a range
+// can head, the one it continues and the one it starts, use different
+// rows).  Level 2 (seg_fixup_kernel): the wave of range ra adds the chunk
+// rows in chunk order and writes the segment's row and squared norm.  Rows
+// of segments inside one range were written by seg_reduce_kernel.  The
+// level-2 launch also pads rows [U, cap) with its last workgroups.
+constexpr int kFixChunk = 32;
+
+// PB rows of partial-style storage (stride 2 rows per index) added in
+// index order: rows idx(b), b = 0 .. count-1, PB loads in flight.
+template <int W, int VPL, int PB, typename Idx>
+__device__ __forceinline__ void add_rows(const float* __restrict__ src, int nv, int lane, int64_t count, Idx idx,
+                                         RowVec<W> (&acc)[VPL]) {
+  for (int64_t b0 = 0; b0 < count; b0 += PB) {
+    RowVec<W> p[PB][VPL];
+#pragma unroll
+    for (int b = 0; b < PB; ++b) {
+      const int64_t row = idx(b0 + b < count ? b0 + b : count - 1);
+#pragma unroll
+      for (int v = 0; v < VPL; ++v) {
+        const int c = lane + kWave * v;
+        p[b][v].load(src, row * nv + c, c < nv);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < PB; ++b)
+      if (b0 + b < count)
+#pragma unroll
+        for (int v = 0; v < VPL; ++v) acc[v].add(p[b][v]);
+  }
+}
+
+template <int W, int VPL>
+__global__ __launch_bounds__(kRowThreads) void seg_fix_chunks_kernel(const int32_t* __restrict__ seg_start,
+                                                                      const int32_t* __restrict__ seg_of, int64_t n,
+                                                                      int nv, const float* __restrict__ partial,
+                                                                      float* __restrict__ chunk) {
+  const int64_t r = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int64_t r0 = r * kRangeLen;
+  if (r0 >= n) return;
+  const int64_t r1 = r0 + kRangeLen < n ? r0 + kRangeLen : n;
+  const int uf = seg_of[r0], ul = seg_of[r1 - 1];
+  constexpr int PB = VPL >= 8 ? 4 : 32 / VPL;
+  for (int t = 0; t < 2; ++t) {  // the segment this range continues, then the one it ends with
+    if (t == 1 && ul == uf) break;
+    const int u = t == 0 ? uf : ul;
+    const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
+    const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
+    if (ra == rb || (r - ra) % kFixChunk != 0) continue;  // inside one range, or not a chunk head here
+    const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
+    const int64_t count = (rb - r + 1) < kFixChunk ? (rb - r + 1) : kFixChunk;
+    RowVec<W> acc[VPL];
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) acc[v].zero();
+    add_rows<W, VPL, PB>(partial, nv, lane, count,
+                         [&](int64_t b) { const int64_t q = r + b; return q * 2 + (q == ra ? slot_a : 0); }, acc);
+    const int64_t out = r * 2 + (r == ra ? 1 : 0);
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int c = lane + kWave * v;
+      if (c < nv) acc[v].store(chunk, out * nv + c);
+    }
+  }
+}
+
 template <int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* __restrict__ seg_start,
                                                                  const int32_t* __restrict__ seg_of, int64_t n,
-                                                                 int nv, const float* __restrict__ partial,
+                                                                 int nv, const float* __restrict__ chunk,
                                                                  float* __restrict__ rows,
                                                                  float* __restrict__ row_sq, int64_t fix_blocks,
                                                                  const uint32_t* __restrict__ num_seg, int64_t cap,
@@ -477,31 +584,14 @@ __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* _
   const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
   const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
   if (ra == rb || ra != r) return;  // inside one range, or another wave's segment
-  const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
   RowVec<W> acc[VPL];
 #pragma unroll
   for (int v = 0; v < VPL; ++v) acc[v].zero();
-  // hot rows span hundreds of ranges: PB partial rows in flight (32 row
-  // vectors per lane)
   constexpr int PB = VPL >= 8 ? 4 : 32 / VPL;
-  for (int64_t q0 = ra; q0 <= rb; q0 += PB) {
-    RowVec<W> p[PB][VPL];
-#pragma unroll
-    for (int b = 0; b < PB; ++b) {
-      const int64_t q = q0 + b <= rb ? q0 + b : rb;
-      const int slot = q == ra ? slot_a : 0;
-#pragma unroll
-      for (int v = 0; v < VPL; ++v) {
-        const int c = lane + kWave * v;
-        p[b][v].load(partial, (q * 2 + slot) * nv + c, c < nv);
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < PB; ++b)
-      if (q0 + b <= rb)
-#pragma unroll
-        for (int v = 0; v < VPL; ++v) acc[v].add(p[b][v]);
-  }
+  const int64_t nchunks = (rb - ra) / kFixChunk + 1;
+  add_rows<W, VPL, PB>(chunk, nv, lane, nchunks,
+                       [&](int64_t j) { const int64_t h = ra + j * kFixChunk; return h * 2 + (j == 0 ? 1 : 0); },
+                       acc);
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = lane + kWave * v;
@@ -566,7 +656,7 @@ __global__ __launch_bounds__(256) void clip_finish_kernel(const double* __restri
 // One wave per row, grid-stride over the cap rows (a fixed grid: most of the
 // cap rows are padding when routing is skewed).  A row of d elements is nv
 // vectors of W (4 when d % 4 == 0, else 1); lane l owns vectors l, l+64, ...
-constexpr int kOptBlocks = 1024;
+constexpr int kOptBlocks = 2048;
 
 template <typename V, int W>
 struct TableVec;
@@ -608,7 +698,11 @@ __global__ __launch_bounds__(kRowThreads) void row_adagrad_kernel(V* __restrict_
                                                                    const float* __restrict__ rows, int64_t cap, int d,
                                                                    int64_t N, float lr,
                                                                    const float* __restrict__ grad_scale) {
-  constexpr int R = VPL >= 16 ? 1 : 2;  // rows in flight per wave (one for very wide rows)
+  // rows in flight per wave: four for rows of up to 256 fp32 (one vector per
+  // lane), one for very wide rows.  With 2,048 workgroups, 71.5k touched
+  // rows of d = 256 update in 47.8 us (51.0 us with two rows and 1,024
+  // workgroups; non-temporal row loads were slower, 51.6 us).
+  constexpr int R = VPL >= 16 ? 1 : (VPL == 1 ? 4 : 2);
   const int lane = threadIdx.x & 63;
   const int64_t nw = (int64_t)gridDim.x * (kRowThreads / kWave);
   const int64_t wid = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
@@ -754,8 +848,8 @@ __global__ __launch_bounds__(kRowThreads) void row_adam_kernel(V* __restrict__ v
 // ------------------------------------------------------------ host side
 struct MergeLayout {
   int64_t ntiles, nranges, cap;
-  int passes;
-  size_t keys[2], vals[2], hist, tile_cnt, counters, totals, seg_start, seg_of, partial, total;
+  int passes, digit_bits;
+  size_t keys[2], vals[2], hist, tile_cnt, counters, totals, seg_start, seg_of, partial, chunk, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -767,7 +861,9 @@ static MergeLayout merge_layout(int64_t P, int d, int64_t pool_size) {
   L.cap = P < pool_size ? P : pool_size;
   int bits = 0;
   while (bits < 62 && ((int64_t)1 << bits) < pool_size) ++bits;
-  L.passes = bits <= 8 ? 1 : (bits + 7) / 8;
+  // fewest passes of at most 10 bits, each digit at least 8 bits wide
+  L.passes = bits <= 10 ? 1 : (bits + 9) / 10;
+  L.digit_bits = std::max(8, (int)cdiv(bits, L.passes));
   const int64_t nfl = d;  // partial rows: d floats
   size_t o = 0;
   for (int b = 0; b < 2; ++b) {
@@ -777,44 +873,47 @@ static MergeLayout merge_layout(int64_t P, int d, int64_t pool_size) {
     o += align256((size_t)P * 4);
   }
   L.hist = o;
-  o += align256((size_t)256 * L.ntiles * 4);
+  o += align256(((size_t)1 << L.digit_bits) * L.ntiles * 4);
   L.tile_cnt = o;
   o += align256((size_t)L.ntiles * 4);
   L.counters = o;  // [0]: segment count
   o += 256;
   L.totals = o;  // digit totals of a radix pass
-  o += 1024;
+  o += align256(((size_t)1 << L.digit_bits) * 4);
   L.seg_start = o;
   o += align256((size_t)(L.cap + 1) * 4);
   L.seg_of = o;
   o += align256((size_t)P * 4);
   L.partial = o;
   o += align256((size_t)L.nranges * 2 * nfl * 4);
+  L.chunk = o;  // first-level fix-up rows, indexed like the partial rows
+  o += align256((size_t)L.nranges * 2 * nfl * 4);
   L.total = o;
   return L;
 }
 
 template <int W, int VPL>
-static void launch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32_t* seg_start, const float* weights,
+static void launch_reduce(const uint32_t* sp, int32_t* seg_of, int32_t* seg_start, const float* weights,
                           const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
-                          const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
-                          int zero_padding, hipStream_t s) {
+                          float* chunk, const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
+                          int32_t* num_unique, int zero_padding, hipStream_t s) {
   const unsigned b1 = (unsigned)cdiv(L.nranges, kRowThreads / kWave);
-  seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, weights, g, fpt, nv, P, rows, row_sq,
-                                                       partial);
-  seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, rows, row_sq, b1,
+  seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, weights, g, fpt, nv, P, rows, row_sq, partial,
+                                                       nseg, seg_start, num_unique, L.cap);
+  seg_fix_chunks_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, chunk);
+  seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, chunk, rows, row_sq, b1,
                                                              nseg, L.cap, pool_size, uniq, zero_padding);
 }
 
 template <int W>
-static void dispatch_reduce(const uint32_t* sp, const int32_t* seg_of, const int32_t* seg_start, const float* weights,
+static void dispatch_reduce(const uint32_t* sp, int32_t* seg_of, int32_t* seg_start, const float* weights,
                             const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
-                            const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
-                            int zero_padding, hipStream_t s) {
+                            float* chunk, const MergeLayout& L, const uint32_t* nseg, int64_t pool_size,
+                            int32_t* uniq, int32_t* num_unique, int zero_padding, hipStream_t s) {
   const int vpl = (int)cdiv(nv, kWave);
-#define MPL_REDUCE(V)                                                                                              \
-  launch_reduce<W, V>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq, partial, L, nseg, pool_size, \
-                      uniq, zero_padding, s)
+#define MPL_REDUCE(V)                                                                                               \
+  launch_reduce<W, V>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq, partial, chunk, L, nseg,      \
+                      pool_size, uniq, num_unique, zero_padding, s)
   if (vpl <= 1) MPL_REDUCE(1);
   else if (vpl <= 2) MPL_REDUCE(2);
   else if (vpl <= 4) MPL_REDUCE(4);
@@ -837,8 +936,10 @@ struct Segments {
   uint32_t* nseg;
 };
 
+// finish = false leaves seg_start[U] and num_unique to the caller's next
+// kernel (seg_reduce_kernel does it for mpl_merge_rows).
 static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayout& L, char* ws, int32_t* uniq,
-                              int32_t* num_unique, hipStream_t s) {
+                              int32_t* num_unique, bool finish, hipStream_t s) {
   uint32_t* keys[2] = {(uint32_t*)(ws + L.keys[0]), (uint32_t*)(ws + L.keys[1])};
   uint32_t* vals[2] = {(uint32_t*)(ws + L.vals[0]), (uint32_t*)(ws + L.vals[1])};
   uint32_t* hist = (uint32_t*)(ws + L.hist);
@@ -852,11 +953,20 @@ static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayou
   const uint32_t* vin = nullptr;
   int cur = 0;
   for (int pass = 0; pass < L.passes; ++pass) {
-    const int shift = 8 * pass;
-    radix_hist_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);
-    digit_scan_kernel<<<256, 1024, 0, s>>>(hist, L.ntiles, totals);
-    radix_scatter_kernel<<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles,
-                                                     totals);
+    const int shift = L.digit_bits * pass;
+#define MPL_RADIX(B)                                                                                        \
+  radix_hist_kernel<B><<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);                          \
+  digit_scan_kernel<<<1u << B, 1024, 0, s>>>(hist, L.ntiles, totals);                                       \
+  radix_scatter_kernel<B><<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles, \
+                                                      totals)
+    if (L.digit_bits <= 8) {
+      MPL_RADIX(8);
+    } else if (L.digit_bits == 9) {
+      MPL_RADIX(9);
+    } else {
+      MPL_RADIX(10);
+    }
+#undef MPL_RADIX
     kin = keys[cur];
     vin = vals[cur];
     cur ^= 1;
@@ -864,7 +974,7 @@ static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayou
   seg_count_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt);
   scan_exclusive_kernel<<<1, 1024, 0, s>>>(tile_cnt, L.ntiles, nseg);
   seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of, L.cap);
-  seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique, L.cap);
+  if (finish) seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique, L.cap);
   return Segments{vin, seg_start, seg_of, nseg};
 }
 
@@ -905,7 +1015,7 @@ extern "C" int mpl_unique_slots(const int32_t* slots, int64_t P, int64_t pool_si
   const MergeLayout L = merge_layout(P, 4, pool_size > P ? pool_size : P);
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_unique_slots: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
-  const Segments sg = sort_segments((const uint32_t*)slots, P, L, (char*)workspace, uniq, num_unique, s);
+  const Segments sg = sort_segments((const uint32_t*)slots, P, L, (char*)workspace, uniq, num_unique, true, s);
   unique_finish_kernel<<<(unsigned)cdiv(P, 256), 256, 0, s>>>(sg.pos, sg.seg_of, P, num_unique, pool_size, uniq,
                                                               inverse);
   return check_launch("mpl_unique_slots");
@@ -938,7 +1048,7 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_merge_rows: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
   char* ws = (char*)workspace;
-  const Segments sg = sort_segments((const uint32_t*)slots, P, L, ws, uniq, num_unique, s);
+  const Segments sg = sort_segments((const uint32_t*)slots, P, L, ws, uniq, num_unique, false, s);
   int rc = check_launch("mpl_merge_rows(sort)");
   if (rc) return rc;
   const uint32_t* vin = sg.pos;
@@ -946,12 +1056,13 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   int32_t* seg_of = sg.seg_of;
   uint32_t* nseg = sg.nseg;
   float* partial = (float*)(ws + L.partial);
+  float* chunk = (float*)(ws + L.chunk);
   if (d % 4 == 0)
-    dispatch_reduce<4>(vin, seg_of, seg_start, weights, g, fetches_per_token, d / 4, P, rows, row_sq, partial, L,
-                       nseg, pool_size, uniq, zero_padding, s);
+    dispatch_reduce<4>(vin, seg_of, seg_start, weights, g, fetches_per_token, d / 4, P, rows, row_sq, partial, chunk,
+                       L, nseg, pool_size, uniq, num_unique, zero_padding, s);
   else
-    dispatch_reduce<1>(vin, seg_of, seg_start, weights, g, fetches_per_token, d, P, rows, row_sq, partial, L, nseg,
-                       pool_size, uniq, zero_padding, s);
+    dispatch_reduce<1>(vin, seg_of, seg_start, weights, g, fetches_per_token, d, P, rows, row_sq, partial, chunk, L,
+                       nseg, pool_size, uniq, num_unique, zero_padding, s);
   return check_launch("mpl_merge_rows(reduce)");
 }
 
