@@ -195,6 +195,20 @@ int mpl_score_topk(const void* queries, int query_mode, float* q_len, const void
 int mpl_gumbel_noise(uint64_t seed, int64_t rows, int n, float* out, void* stream);
 
 /*
+ * Synthetic tables of the pool's shapes, defined by a hash so that the CPU
+ * can regenerate any rows of a table larger than host memory (the values
+ * init of memory.py:104-109 is jax.random.normal; this stands in for it in
+ * benchmarks).  Fills out [rows, cols] (dtype MPL_F16 or MPL_F32) with the
+ * elements of table rows row0 .. row0 + rows - 1:
+ *   index = row * cols + col, h = splitmix64(splitmix64(seed) ^ index),
+ *   u1 = ((h >> 40) + 1) / 2^24, u2 = (h & 0xFFFFFF) / 2^24,
+ *   value = (dtype)(float)(sqrt(-2 ln u1) cos(2 pi u2) * scale), in fp64.
+ * splitmix64: the SplitMix64 finalizer (Steele, Lea & Flood 2014).
+ */
+int mpl_hash_normal_fill(void* out, int dtype, int64_t rows, int cols, uint64_t seed, float scale, int64_t row0,
+                         void* stream);
+
+/*
  * memory.py:179-193: out[m,:] = sum_r weights[m,r] * values[read(slots[m,r]),:]
  * over the R = H*k rows of each token, fp32 accumulation; values [N,d] in
  * values_dtype (MPL_F16 or MPL_F32); read(s) = s, or (s + N/2 + 1) % N when

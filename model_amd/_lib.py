@@ -62,6 +62,7 @@ SIGNATURES = {
     "mpl_key_diversity": (_I, [_P, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),
     "mpl_revive_keys": (_I, [_P, _P, _P, _I64, _P, _P, _I, _I, _I, _F, _F, _P, _P]),
     "mpl_route_counts": (_I, [_P, _P, _I64, _I, _I, _I, _P, _P, _P, _P]),
+    "mpl_hash_normal_fill": (_I, [_P, _I, _I64, _I, _U64, _F, _I64, _P]),
     "mpl_balance_state_bytes": (_SZ, [_I64, _I]),
     "mpl_balance_fwd": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "mpl_lookup_bwd_dense_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
