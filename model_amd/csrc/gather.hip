@@ -9,14 +9,14 @@ namespace mpl {
 
 constexpr int kGatherThreads = 256;
 
-template <typename V, int VR>
+template <typename V, int VR, bool NT>
 __global__ __launch_bounds__(kGatherThreads) void gather_wsum_kernel(
     const V* __restrict__ values, int64_t N, const int32_t* __restrict__ slots,
     const float* __restrict__ weights, int64_t M, int R, int shuffle, float* __restrict__ out) {
   const int64_t m = (int64_t)blockIdx.x * (kGatherThreads / kWave) + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
   if (m >= M) return;
-  Wsum<V, VR, 32> acc;
+  Wsum<V, VR, 32, NT> acc;
   const uint4* base = (const uint4*)values;
   for (int r0 = 0; r0 < R; r0 += kWave) {
     const int rr = r0 + lane;
@@ -58,10 +58,14 @@ static int gather_impl(const V* values, int64_t N, int d, const int32_t* slots, 
   const unsigned blocks = (unsigned)cdiv(M, kGatherThreads / kWave);
   if (bytes % 16 == 0 && ((uintptr_t)values % 16) == 0 && ((uintptr_t)out % 16) == 0) {
     const int VR = (int)(bytes / 16);
+    const bool nt = N * bytes > kStreamTableBytes;
     switch (VR) {
-#define MPL_G(vr)                                                                                      \
-  case vr:                                                                                             \
-    gather_wsum_kernel<V, vr><<<blocks, kGatherThreads, 0, s>>>(values, N, slots, w, M, R, shuffle, out); \
+#define MPL_G(vr)                                                                                              \
+  case vr:                                                                                                     \
+    if (nt)                                                                                                    \
+      gather_wsum_kernel<V, vr, true><<<blocks, kGatherThreads, 0, s>>>(values, N, slots, w, M, R, shuffle, out); \
+    else                                                                                                       \
+      gather_wsum_kernel<V, vr, false><<<blocks, kGatherThreads, 0, s>>>(values, N, slots, w, M, R, shuffle, out); \
     return check_launch("mpl_gather_wsum");
       MPL_G(1) MPL_G(2) MPL_G(4) MPL_G(8) MPL_G(16) MPL_G(32) MPL_G(64) MPL_G(128) MPL_G(256)
 #undef MPL_G

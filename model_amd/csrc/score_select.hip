@@ -929,7 +929,7 @@ struct ReadParams {
 // lane h*16 + r holds that token's row h*k + r (slot and weight), exactly the
 // lane layout the weighted row sum takes.  While some waves run the pair
 // merges (VALU-bound), others have their row loads in flight.
-template <typename V, int VR>
+template <typename V, int VR, bool NT>
 __global__ __launch_bounds__(256) void pair_read_k16(PairParams p, ReadParams rp) {
   const int lane = threadIdx.x & 63;
   const int r = lane & 15;
@@ -945,7 +945,7 @@ __global__ __launch_bounds__(256) void pair_read_k16(PairParams p, ReadParams rp
   const int64_t m = mh >> 2;
   const int64_t N = (int64_t)p.n * p.n;
   if (rp.shuffle) slot = (int)(((int64_t)slot + N / 2 + 1) % N);
-  Wsum<V, VR> acc;
+  Wsum<V, VR, 16, NT> acc;
   acc.add_chunk((const uint4*)rp.values, slot, w, 64, lane);
   acc.store(rp.out + m * (int64_t)(VR * Vec16<V>::kElems), lane);
 }
@@ -1235,10 +1235,14 @@ static bool launch_pair_read(const LookupRead& lr, const PairParams& pp, unsigne
   rp.shuffle = lr.shuffle;
   rp.out = lr.out;
   const int VR = lr.d * esz / 16;
-#define MPL_PR(V, vr)                                        \
-  if (VR == vr) {                                            \
-    pair_read_k16<V, vr><<<grid, 256, 0, s>>>(pp, rp);       \
-    return true;                                             \
+  const bool nt = (int64_t)pp.n * pp.n * lr.d * esz > kStreamTableBytes;
+#define MPL_PR(V, vr)                                               \
+  if (VR == vr) {                                                   \
+    if (nt)                                                         \
+      pair_read_k16<V, vr, true><<<grid, 256, 0, s>>>(pp, rp);      \
+    else                                                            \
+      pair_read_k16<V, vr, false><<<grid, 256, 0, s>>>(pp, rp);     \
+    return true;                                                    \
   }
   if (lr.dtype == MPL_F16) {
     MPL_PR(_Float16, 16) MPL_PR(_Float16, 32) MPL_PR(_Float16, 64)

@@ -13,15 +13,25 @@
 
 namespace mpl {
 
-// A 16-byte load marked non-temporal: rows of the value table are read once
-// per lookup, and with the hint they do not displace other lines in L2 and
-// the Infinity Cache.  At 4,096 tokens on the 34 GB table it takes the read
-// from about 4.8 to 5.5 TB/s (measured on MI355X, random 512-byte rows).
+// A 16-byte load marked non-temporal: with the hint the rows do not
+// displace other lines in L2 and the Infinity Cache.  Which load a table's
+// rows get depends on whether the table can stay in the 256 MB Infinity
+// Cache between lookups:
+//   - larger tables are streamed: a row is read once per lookup and not again
+//     before it would be evicted, so the hint helps (4,096 tokens on the
+//     34 GB table: 24.5 us per read non-temporal, 28.3 us plain);
+//   - tables that fit are read again by the next lookup: ordinary loads keep
+//     them resident (8,192 tokens on the 134 MB table: 39.4 us plain, 48.4 us
+//     non-temporal, whose rows came from HBM every time).
+// Both measured on MI355X, random 512-byte rows, rotating token batches.
 typedef uint32_t u32x4_nt __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_nt(const uint4* p) {
   const u32x4_nt v = __builtin_nontemporal_load((const u32x4_nt*)p);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+
+// Value tables above this many bytes are read with non-temporal loads.
+constexpr int64_t kStreamTableBytes = (int64_t)192 << 20;
 
 template <typename V>
 struct Vec16;
@@ -58,7 +68,7 @@ struct Vec16<float> {
 // with NBR = 16 and 26.2 us with all 32 loads forced ahead of the sums.  The
 // fused stage-2 kernel keeps 16.  Batching never changes the order of the
 // sums, so every NBR gives the same bits.
-template <typename V, int VR, int NBR = 16>
+template <typename V, int VR, int NBR = 16, bool NT = true>
 struct Wsum {
   static constexpr int LPR = VR <= kWave ? VR : kWave;
   static constexpr int RPI = kWave / LPR;
@@ -93,7 +103,7 @@ struct Wsum {
         wv[b] = ok ? w : 0.f;
         const uint4* src = base + (int64_t)s * VR + col;
 #pragma unroll
-        for (int v = 0; v < VPL; ++v) buf[b][v] = load_nt(src + v * kWave);
+        for (int v = 0; v < VPL; ++v) buf[b][v] = NT ? load_nt(src + v * kWave) : src[v * kWave];
       }
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
