@@ -58,7 +58,7 @@
 namespace mpl {
 
 #ifndef MPL_CAND
-#define MPL_CAND 22
+#define MPL_CAND 30
 #endif
 constexpr int kCand = MPL_CAND;  // per-lane candidate buffer (entries)
 #ifndef MPL_SCORE_THREADS
@@ -568,13 +568,16 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       for (int e = 0; e < 8; ++e) {
         const int r = 8 * q + e;
         issue_for(r, issue);
+        // Every lane writes the element at its next free entry and keeps
+        // it only when it is a candidate: no exec-mask changes per element
+        // (7 -> 4 instructions).  A kept-or-not write lands at or past the
+        // lane's last candidate, which the flush does not read, and the
+        // flush check before each group of 8 leaves 8 free entries.
         const float x = sv[r];
-        if (active && x > st.thr) {
-          lds_at(cscore, st.off) = x;
-          lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
-          if (NOISE) lds_at(cpay, st.off) = clean_at(c, r);
-          st.off += kEntryBytes;
-        }
+        lds_at(cscore, st.off) = x;
+        lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
+        if (NOISE) lds_at(cpay, st.off) = clean_at(c, r);
+        st.off += (active && x > st.thr) ? kEntryBytes : 0u;
       }
     }
   });
