@@ -1081,6 +1081,88 @@ __global__ __launch_bounds__(256) void pair_wide_k16(PairParams p) {
   }
 }
 
+// pair_wide_k16 fused with the value read, for H = 4: one workgroup per
+// token, quarter h (256 threads) merges head h's split lists and runs its
+// pair stage exactly as pair_wide_k16 does; the four heads' 16 (slot,
+// weight) rows meet in LDS and wave 0 reads the token's 64 rows with the
+// weighted row sum of wsum.h (the lane layout gather_wsum_kernel uses, so
+// `out` equals the two-launch path bit for bit).  Decode-sized batches: one
+// launch and one dependent memory round trip fewer than pair_wide_k16 +
+// gather_wsum_kernel.
+template <typename V, int VR, bool NT>
+__global__ __launch_bounds__(1024) void pair_wide_read_k16(PairParams p, ReadParams rp) {
+  constexpr int K = 16;
+  __shared__ u64 skey[4][16][K];
+  __shared__ float spay[4][16][K];
+  __shared__ int srow_slot[4 * K];
+  __shared__ float srow_w[4 * K];
+  const int h = threadIdx.x >> 8;  // head of this quarter (H = 4)
+  const int t = threadIdx.x & 255;
+  const int lane = threadIdx.x & 63;
+  const int r = lane & 15;
+  const int g = t >> 4;
+  const int c = g >> 3, chunk = g & 7;
+  const int64_t m = blockIdx.x;  // the grid is exactly M workgroups
+  const int64_t mh = m * 4 + h;
+  const int HC = 8;
+  const float* lsel = p.sel != nullptr ? p.sel : p.clean;
+  const int64_t o0 = ((int64_t)m * HC + 2 * h + c) * K + r;
+  const int64_t sstride = p.M * HC * K;
+  int id[kMergeChunk];
+  float sl[kMergeChunk], cc[kMergeChunk];
+#pragma unroll
+  for (int i = 0; i < kMergeChunk; ++i) {
+    const int64_t o = (int64_t)min(chunk * kMergeChunk + i, p.S - 1) * sstride + o0;  // clamped, unconditional
+    id[i] = p.idx[o];
+    sl[i] = lsel[o];
+    cc[i] = p.clean[o];
+  }
+  pin_loaded(id, sl, cc);
+  u64 acc = 0;
+  float pay = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMergeChunk; ++i) {
+    const bool in = chunk * kMergeChunk + i < p.S;  // uniform per row
+    const u64 kk = (in && id[i] >= 0) ? make_key(sl[i], id[i]) : 0ull;
+    if (i == 0) {
+      acc = kk;
+      pay = cc[i];
+    } else {
+      g16::merge(acc, pay, kk, cc[i], r);
+    }
+  }
+  skey[h][g][r] = acc;
+  spay[h][g][r] = pay;
+  __syncthreads();
+  if (chunk == 0) {  // rows 0 and 8 of each quarter read rows 1..7 and 9..15 and rewrite only their own
+#pragma unroll
+    for (int i = 1; i < kMergeChunk; ++i) g16::merge(acc, pay, skey[h][g + i][r], spay[h][g + i][r], r);
+    p.sub_idx[o0] = acc ? key_index(acc) : -1;
+    p.sub_scores[o0] = acc ? pay : -INFINITY;
+    skey[h][g][r] = acc;
+    spay[h][g][r] = pay;
+  }
+  __syncthreads();
+  if (g == 0) {  // lanes 0-15 of the quarter's first wave
+    const u64 lk[2] = {skey[h][0][r], skey[h][8][r]};
+    const float lc[2] = {spay[h][0][r], spay[h][8][r]};
+    int slot;
+    float w;
+    pair_tail_k16(p, lk, lc, true, mh, lane, r, slot, w);
+    srow_slot[h * K + r] = slot;
+    srow_w[h * K + r] = w;
+  }
+  __syncthreads();
+  if (threadIdx.x < kWave) {  // wave 0: lane i holds row i = h * 16 + r of the token
+    const int64_t N = (int64_t)p.n * p.n;
+    int slot = srow_slot[lane];
+    if (rp.shuffle) slot = (int)(((int64_t)slot + N / 2 + 1) % N);
+    Wsum<V, VR, 16, NT> sum;
+    sum.add_chunk((const uint4*)rp.values, slot, srow_w[lane], 64, lane);
+    sum.store(rp.out + m * (int64_t)(VR * Vec16<V>::kElems), lane);
+  }
+}
+
 // ---------------------------------------------------------------- host side
 struct Plan {
   int splits, blk_per_split, nblk, kmax, pass1_blocks;
@@ -1256,6 +1338,37 @@ static bool launch_pair_read(const LookupRead& lr, const PairParams& pp, unsigne
   return false;
 }
 
+// The value read fused into pair_wide_k16 (pair_wide_read_k16): same shape
+// conditions as launch_pair_read; returns false (nothing launched) otherwise.
+static bool launch_pair_wide_read(const LookupRead& lr, const PairParams& pp, hipStream_t s) {
+  const int esz = lr.dtype == MPL_F16 ? 2 : 4;
+  if (pp.H != 4 || pp.k != 16 || (lr.d * esz) % 16 != 0 || ((uintptr_t)lr.values % 16) != 0 ||
+      ((uintptr_t)lr.out % 16) != 0)
+    return false;
+  ReadParams rp;
+  rp.values = lr.values;
+  rp.shuffle = lr.shuffle;
+  rp.out = lr.out;
+  const int VR = lr.d * esz / 16;
+  const bool nt = (int64_t)pp.n * pp.n * lr.d * esz > kStreamTableBytes;
+  const unsigned grid = (unsigned)pp.M;
+#define MPL_PWR(V, vr)                                                   \
+  if (VR == vr) {                                                        \
+    if (nt)                                                              \
+      pair_wide_read_k16<V, vr, true><<<grid, 1024, 0, s>>>(pp, rp);     \
+    else                                                                 \
+      pair_wide_read_k16<V, vr, false><<<grid, 1024, 0, s>>>(pp, rp);    \
+    return true;                                                         \
+  }
+  if (lr.dtype == MPL_F16) {
+    MPL_PWR(_Float16, 16) MPL_PWR(_Float16, 32) MPL_PWR(_Float16, 64)
+  } else {
+    MPL_PWR(float, 32) MPL_PWR(float, 64)
+  }
+#undef MPL_PWR
+  return false;
+}
+
 static int select_impl(const char* who, bool pair, const void* queries, int query_mode, float* q_len,
                        const void* packed_keys, int64_t M, int H, int n, int half, int k, int score_dtype,
                        const float* temperature, const float* gumbel, const float* noise_coef, void* workspace,
@@ -1350,6 +1463,10 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   // into one per level, so stage 2 merges at most 8 lists instead of a long
   // sequential chain
   if (pair && k == 16 && pp.S > kMergeChunk && pp.S <= kWideMaxSplits) {
+    if (read != nullptr && M > 0 && launch_pair_wide_read(*read, pp, s)) {
+      *read_done = true;
+      return check_launch("mpl_lookup(wide stage 2 + value read)");
+    }
     pair_wide_k16<<<(unsigned)(M * H), 256, 0, s>>>(pp);
     return check_launch("mpl_score_select(stage 2)");
   }
