@@ -68,7 +68,7 @@ def parse():
     ap.add_argument("--no-generate", action="store_true")
     ap.add_argument("--no-host", action="store_true")
     ap.add_argument("--only", choices=["text_study", "pool_67M_4096", "host_file", "fact_task", "sparse_update",
-                                         "cpu_67M", "generation"],
+                                         "cpu_67M", "generation", "train"],
                     default=None,
                     help="run one workload alone (for profiler runs) and print its timings")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -890,6 +890,9 @@ def main():
         lk = Lookup(torch, L, M=8192, H=4, n=512, d_key=256, d=256, k=16, seed=0, rotate=HEADLINE_ROTATE)
         print(json.dumps({"only": args.only, "ms_per_step": time_loop(torch, lk.step, args.steps, args.warmup),
                           "kernels": kernel_breakdown(torch, lk, args.steps)}))
+        return
+    if args.only == "train":
+        print(json.dumps({"only": args.only, "train_step": train_step_bench(torch, 10)}))
         return
     if args.only == "generation":
         print(json.dumps({"only": args.only, "generation_268M": generation_bench(torch)}))
