@@ -6,7 +6,8 @@ Ids bit-exact; scores bit-exact to mpl_score_select's (the same kernels and
 the same exact list merges), and within fp16-scoring rounding of the
 oracle's fp64 scores on near-tie-free rows.  Shapes cover one split, split
 lists reduced by merge levels (k = 16) and by the pair kernel (k != 16),
-routing noise, and fp32 scoring."""
+routing noise, and fp32 scoring, up to the 67M- and 268M-slot key widths
+(n = 8,192 and 16,384) with k = 8, 16 and 32."""
 
 import numpy as np
 import pytest
@@ -71,6 +72,11 @@ def _run(M, H, n, d_key, k, score, noise, seed):
     (37, 2, 64, 16, 4, _lib.MPL_F16, False),       # k != 16 with splits: pair kernel
     (5, 2, 640, 32, 16, _lib.MPL_F16, True),       # noise with splits
     (40, 2, 96, 12, 8, _lib.MPL_F32, True),        # fp32 scoring, noise, ragged n
+    (256, 4, 8192, 256, 32, _lib.MPL_F16, False),  # k = 32 at the 67M-slot width: split lists, pair kernel
+    (64, 4, 8192, 256, 8, _lib.MPL_F16, False),    # k = 8 at n = 8,192
+    (300, 4, 8192, 256, 16, _lib.MPL_F16, True),   # routing noise at n = 8,192 (split noisy stage 1)
+    (1, 4, 16384, 256, 16, _lib.MPL_F16, False),   # one token at the 268M-slot width: 64 splits
+    (100, 2, 4096, 64, 16, _lib.MPL_F32, False),   # fp32 scoring at n = 4,096 with splits
 ])
 def test_topk_equals_select_stage1(gpu_lib, M, H, n, d_key, k, score, noise):
     q, khat, gum, T, coef, outs = _run(M, H, n, d_key, k, score, noise, seed=M + n + k)
@@ -88,7 +94,9 @@ def test_topk_equals_select_stage1(gpu_lib, M, H, n, d_key, k, score, noise):
     srt = -np.sort(-sel, axis=-1)
     gap = srt[..., k - 1] - (srt[..., k] if n > k else -np.inf)
     free = gap > 2.5 * 2.0 ** -11 * T
-    assert free.mean() > 0.5
+    # wide key ranges crowd the k-th score (n = 8,192, k = 32: about a quarter
+    # of the rows are tie-free), so the floor on checked rows drops there
+    assert free.mean() > (0.5 if n <= 2048 else 0.2) and free.sum() >= 1
     # the set is fixed there; the order inside it may swap near-tied entries
     got_ids = outs["topk"][0][free]
     np.testing.assert_array_equal(np.sort(got_ids, -1), np.sort(want[free], -1))
