@@ -41,6 +41,10 @@ enum { MPL_OK = 0, MPL_EINVAL = 1, MPL_EHIP = 2, MPL_EWORKSPACE = 3, MPL_EUNSUPP
 /* query_mode of mpl_score_select */
 enum { MPL_Q_NORMALIZED = 0, MPL_Q_RAW = 1, MPL_Q_RAW_SCALED = 2 };
 
+/* activation and weight_layout of mpl_rows_linear */
+enum { MPL_ACT_NONE = 0, MPL_ACT_GELU_TANH = 1, MPL_ACT_SILU = 2 };
+enum { MPL_W_IN_OUT = 0, MPL_W_OUT_IN = 1 };
+
 /* Library version (major*10000 + minor*100 + patch). */
 int mpl_version(void);
 
@@ -453,6 +457,42 @@ int mpl_balance_fwd(const float* queries, int scaled, const void* packed_keys, c
  * gradient follows with mpl_l2_normalize_bwd.  Nothing of size [M, n] is
  * formed; no atomics.
  */
+/*
+ * One decode step of the backbone's causal self-attention with its
+ * key/value cache (model.py:29-91 in decode mode, called once per token by
+ * generate.py:31-34; Flax's MultiHeadDotProductAttention with decode=True).
+ * qkv [batch, 3, heads, head_dim] fp32 is the fused query/key/value
+ * projection of the new token of each stream (biases added), position a
+ * device int64 scalar shared by every stream.  Writes the new key to
+ * k_cache_t [batch, heads, head_dim, max_len] and the new value to
+ * v_cache [batch, heads, max_len, head_dim] at that position, then
+ * out [batch, heads, head_dim] = softmax_t((scale * q) . k_t) v_t over
+ * t <= position.  head_dim is 16, 32, 64, 128 or 256; max_len <= 8192.  A position
+ * outside [0, max_len) writes nothing to the caches and NaN to out.
+ */
+int mpl_decode_attention(const float* qkv, int64_t batch, int heads, int head_dim, int max_len,
+                         const int64_t* position, float* k_cache_t, float* v_cache, float* out, float scale,
+                         void* stream);
+
+/*
+ * A dense layer of the backbone over a few rows (model.py:29-127: the
+ * query/key/value, output, feed-forward, router, gate and mem_out products
+ * and embed.attend), with its neighbours fused in:
+ *   a = x [rows, K] fp32;  a = LayerNorm(a) * ln_scale + ln_bias if ln_scale
+ *   (mean and biased variance over K, ln_eps inside the square root);
+ *   a = a * x_mul if x_mul [rows, K];
+ *   out [rows, N] = act(a . W + bias) + residual
+ * W is [K, N] (MPL_W_IN_OUT, a Dense kernel) or [N, K] (MPL_W_OUT_IN, the
+ * embedding table of embed.attend); bias [N], residual [rows, N] and x_mul
+ * may be NULL; activation MPL_ACT_NONE, MPL_ACT_GELU_TANH
+ * (0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))) or MPL_ACT_SILU.
+ * K is a multiple of 4; x, x_mul, W, ln_scale and ln_bias are 16-byte
+ * aligned; out may be the residual but not x or x_mul.  Deterministic.
+ */
+int mpl_rows_linear(const float* x, const float* x_mul, const float* ln_scale, const float* ln_bias, float ln_eps,
+                    const float* weight, int weight_layout, const float* bias, int activation,
+                    const float* residual, int64_t rows, int K, int N, float* out, void* stream);
+
 size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half, int score_dtype);
 int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
                          const int32_t* sub_idx, const float* d_sub, const float* clean_counts, const void* state,

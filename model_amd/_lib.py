@@ -14,6 +14,8 @@ LIB_PATH = os.path.join(HERE, "libmpl.so")
 
 MPL_F32, MPL_F16 = 0, 1
 MPL_Q_NORMALIZED, MPL_Q_RAW, MPL_Q_RAW_SCALED = 0, 1, 2
+MPL_ACT_NONE, MPL_ACT_GELU_TANH, MPL_ACT_SILU = 0, 1, 2
+MPL_W_IN_OUT, MPL_W_OUT_IN = 0, 1
 
 # name -> (restype, argtypes); the C ABI of include/mpl.h
 _P, _I, _I64, _F, _SZ = C.c_void_p, C.c_int, C.c_int64, C.c_float, C.c_size_t
@@ -63,6 +65,8 @@ SIGNATURES = {
     "mpl_revive_keys": (_I, [_P, _P, _P, _I64, _P, _P, _I, _I, _I, _F, _F, _P, _P]),
     "mpl_route_counts": (_I, [_P, _P, _I64, _I, _I, _I, _P, _P, _P, _P]),
     "mpl_hash_normal_fill": (_I, [_P, _I, _I64, _I, _U64, _F, _I64, _P]),
+    "mpl_decode_attention": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _F, _P]),
+    "mpl_rows_linear": (_I, [_P, _P, _P, _P, _F, _P, _I, _P, _I, _P, _I64, _I, _I, _P, _P]),
     "mpl_balance_state_bytes": (_SZ, [_I64, _I]),
     "mpl_balance_fwd": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P]),
     "mpl_lookup_bwd_dense_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),

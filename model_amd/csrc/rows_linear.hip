@@ -1,0 +1,293 @@
+// Dense layers of the backbone for a few rows at a time (one decode step:
+// one row per stream), with what surrounds them in model.py:29-127 fused in:
+//
+//   a   = x                          (rows [R, K] fp32)
+//   a   = LayerNorm(a) * g + beta    if ln_scale (flax LayerNorm: mean and
+//                                    biased variance over K, eps inside the
+//                                    square root)
+//   a   = a * x_mul                  if x_mul (the gated memory read
+//                                    mem * gate before mem_out)
+//   out = act(a . W + bias) + residual        act: none, gelu (tanh form), silu
+//
+// W is [K, N] (a Dense kernel) or [N, K] (the embedding table read by
+// embed.attend).  Library GEMMs pick tiles for large matrices; here the
+// products are R x K x N with R = a few dozen rows (one per stream), which
+// leaves a 16-row tile per workgroup and makes the length of each thread's
+// dependent chain of loads the cost.  So K is split over all 256 threads of
+// the workgroup that owns a 16 x 16 output tile: lane (ks, cp) of wave w
+// takes the float4 columns j = 8w + ks, +32, +64, ... of K for the output
+// columns 2cp and 2cp + 1 and all 16 rows (32 accumulators), so each thread
+// issues 16 row loads and 2 weight loads per float4 of K, all independent.
+// The 8 K-slices of a wave are then added by a shuffle reduce-scatter
+// (xor 32, 16, 8: each step halves the values a lane holds), the 4 waves'
+// partial tiles through LDS in a fixed order, so results are deterministic.
+// LayerNorm statistics of the tile's rows are computed first (two passes
+// over each row: mean, then centred variance) and the normalisation is
+// applied to the operand as it is loaded.
+#include <math.h>
+
+#include "common.h"
+
+namespace mpl {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kTR = 16;  // rows per tile
+constexpr int kTN = 16;  // columns per tile
+constexpr int kSlices = kThreads / 8;  // K-slices per workgroup
+
+struct LinearArgs {
+  const float* x;
+  const float* x_mul;
+  const float* ln_scale;
+  const float* ln_bias;
+  const float* w;
+  const float* bias;
+  const float* residual;
+  float* out;
+  int64_t rows;
+  int K, N, act;
+  float eps;
+};
+
+__device__ __forceinline__ float activate(float v, int act) {
+  if (act == MPL_ACT_GELU_TANH) {
+    // 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
+    const float inner = 0.7978845608028654f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(inner));
+  }
+  if (act == MPL_ACT_SILU) return v / (1.0f + expf(-v));
+  return v;
+}
+
+// One reduce-scatter step over lanes l and l ^ OFF: of the C values a lane
+// holds, the lane with bit OFF set keeps (and receives the partner's copy of)
+// the upper half, the other the lower half.
+template <int C, int OFF>
+__device__ __forceinline__ void scatter_step(float* v, int lane) {
+  const bool up = (lane & OFF) != 0;
+#pragma unroll
+  for (int q = 0; q < C / 2; ++q) {
+    const float send = up ? v[q] : v[q + C / 2];
+    const float keep = up ? v[q + C / 2] : v[q];
+    v[q] = keep + __shfl_xor(send, OFF);
+  }
+}
+
+template <int LAYOUT, bool LN, bool MUL>
+__global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
+  __shared__ float red[kThreads / kWave][kTR * kTN];
+  __shared__ float s_mean[kTR], s_rstd[kTR];
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int64_t r0 = (int64_t)blockIdx.y * kTR;
+  const int n0 = blockIdx.x * kTN;
+  const int K = a.K, K4 = K / 4;
+  const int nrows = (int)min<int64_t>(kTR, a.rows - r0);  // valid rows of this tile
+
+  // operands that do not depend on the row statistics are requested first:
+  // the epilogue's bias and residual element of this thread and the weights
+  // of its first K-slice
+  const int erow = tid / kTN, ecol = tid % kTN;  // kTR * kTN == kThreads
+  const int en = n0 + ecol;
+  const bool eval = erow < nrows && en < a.N;
+  const int64_t eat = (r0 + erow) * a.N + en;
+  const float ebias = (eval && a.bias) ? a.bias[en] : 0.0f;
+  const float eres = (eval && a.residual) ? a.residual[eat] : 0.0f;
+
+  const int cp = lane % 8, ks = lane / 8;
+  const int c0 = n0 + 2 * cp;
+  const bool cval = c0 < a.N, cval1 = c0 + 1 < a.N;
+  const bool pairs = (a.N & 1) == 0;  // [K, N] rows hold aligned column pairs
+  const float4 zero = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  auto load_w = [&](int k, float4& w0, float4& w1) {
+    w0 = zero;
+    w1 = zero;
+    if (LAYOUT == MPL_W_OUT_IN) {
+      if (cval) w0 = *(const float4*)(a.w + (int64_t)c0 * K + k);
+      if (cval1) w1 = *(const float4*)(a.w + (int64_t)(c0 + 1) * K + k);
+    } else if (cval1 && pairs) {
+      const float2 u0 = *(const float2*)(a.w + (int64_t)k * a.N + c0);
+      const float2 u1 = *(const float2*)(a.w + (int64_t)(k + 1) * a.N + c0);
+      const float2 u2 = *(const float2*)(a.w + (int64_t)(k + 2) * a.N + c0);
+      const float2 u3 = *(const float2*)(a.w + (int64_t)(k + 3) * a.N + c0);
+      w0 = make_float4(u0.x, u1.x, u2.x, u3.x);
+      w1 = make_float4(u0.y, u1.y, u2.y, u3.y);
+    } else if (cval) {
+      const float* wc = a.w + (int64_t)k * a.N + c0;
+      w0 = make_float4(wc[0], wc[a.N], wc[2 * (int64_t)a.N], wc[3 * (int64_t)a.N]);
+      if (cval1) w1 = make_float4(wc[1], wc[a.N + 1], wc[2 * (int64_t)a.N + 1], wc[3 * (int64_t)a.N + 1]);
+    }
+  };
+  const int j0 = wave * 8 + ks;
+  float4 nw0 = zero, nw1 = zero;
+  if (j0 < K4) load_w(4 * j0, nw0, nw1);
+
+  if (LN) {
+    // 16 threads per row (consecutive lanes); a thread's part of the row is
+    // kept in registers between the two passes when it has at most kHold
+    // float4s (K <= 512), and read again otherwise
+    constexpr int TPR = kThreads / kTR;
+    constexpr int kHold = 8;
+    const int row = tid / TPR, part = tid % TPR;
+    const float4* xr = (const float4*)(a.x + (r0 + (row < nrows ? row : 0)) * K);
+    const bool hold = K4 <= kHold * TPR;
+    float4 xv[kHold];
+    float s = 0.0f;
+    if (row < nrows) {
+      if (hold) {
+#pragma unroll
+        for (int h = 0; h < kHold; ++h) {
+          const int j = part + h * TPR;
+          xv[h] = j < K4 ? xr[j] : zero;
+        }
+#pragma unroll
+        for (int h = 0; h < kHold; ++h) s += (xv[h].x + xv[h].y) + (xv[h].z + xv[h].w);
+      } else {
+        for (int j = part; j < K4; j += TPR) {
+          const float4 v = xr[j];
+          s += (v.x + v.y) + (v.z + v.w);
+        }
+      }
+    }
+    for (int off = TPR / 2; off >= 1; off >>= 1) s += __shfl_xor(s, off, TPR);
+    const float mean = s / (float)K;
+    float q = 0.0f;
+    if (row < nrows) {
+      if (hold) {
+#pragma unroll
+        for (int h = 0; h < kHold; ++h) {
+          if (part + h * TPR < K4) {
+            const float d0 = xv[h].x - mean, d1 = xv[h].y - mean, d2 = xv[h].z - mean, d3 = xv[h].w - mean;
+            q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+          }
+        }
+      } else {
+        for (int j = part; j < K4; j += TPR) {
+          const float4 v = xr[j];
+          const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+          q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+      }
+    }
+    for (int off = TPR / 2; off >= 1; off >>= 1) q += __shfl_xor(q, off, TPR);
+    if (part == 0) {
+      s_mean[row] = mean;
+      s_rstd[row] = rsqrtf(q / (float)K + a.eps);
+    }
+    __syncthreads();
+  }
+
+  const float* xt = a.x + r0 * K;
+  const float* mt = MUL ? a.x_mul + r0 * K : nullptr;
+  float mean[kTR], rstd[kTR];
+#pragma unroll
+  for (int i = 0; i < kTR; ++i) {
+    mean[i] = LN ? s_mean[i] : 0.0f;
+    rstd[i] = LN ? s_rstd[i] : 0.0f;
+  }
+  float acc[2 * kTR];  // acc[2 i + c]: row i, column c0 + c
+#pragma unroll
+  for (int e = 0; e < 2 * kTR; ++e) acc[e] = 0.0f;
+
+#pragma unroll 2
+  for (int j = j0; j < K4; j += kSlices) {
+    const int k = 4 * j;
+    const float4 w0 = nw0, w1 = nw1;
+    if (j + kSlices < K4) load_w(k + 4 * kSlices, nw0, nw1);  // the next slice's weights
+    float4 g = zero, be = zero;
+    if (LN) {
+      g = *(const float4*)(a.ln_scale + k);
+      be = *(const float4*)(a.ln_bias + k);
+    }
+#pragma unroll
+    for (int i = 0; i < kTR; ++i) {
+      float4 v = i < nrows ? *(const float4*)(xt + (int64_t)i * K + k) : zero;
+      if (LN) {
+        v.x = (v.x - mean[i]) * rstd[i] * g.x + be.x;
+        v.y = (v.y - mean[i]) * rstd[i] * g.y + be.y;
+        v.z = (v.z - mean[i]) * rstd[i] * g.z + be.z;
+        v.w = (v.w - mean[i]) * rstd[i] * g.w + be.w;
+      }
+      if (MUL) {
+        const float4 m = i < nrows ? *(const float4*)(mt + (int64_t)i * K + k) : zero;
+        v.x *= m.x;
+        v.y *= m.y;
+        v.z *= m.z;
+        v.w *= m.w;
+      }
+      acc[2 * i] = fmaf(v.x, w0.x, acc[2 * i]);
+      acc[2 * i] = fmaf(v.y, w0.y, acc[2 * i]);
+      acc[2 * i] = fmaf(v.z, w0.z, acc[2 * i]);
+      acc[2 * i] = fmaf(v.w, w0.w, acc[2 * i]);
+      acc[2 * i + 1] = fmaf(v.x, w1.x, acc[2 * i + 1]);
+      acc[2 * i + 1] = fmaf(v.y, w1.y, acc[2 * i + 1]);
+      acc[2 * i + 1] = fmaf(v.z, w1.z, acc[2 * i + 1]);
+      acc[2 * i + 1] = fmaf(v.w, w1.w, acc[2 * i + 1]);
+    }
+  }
+
+  // the wave's 8 K-slices (lane bits 3..5): afterwards lane (ks, cp) holds
+  // the sums of acc[4 ks + q], q < 4, i.e. rows 2 ks + q / 2, column 2 cp + q % 2
+  scatter_step<32, 32>(acc, lane);
+  scatter_step<16, 16>(acc, lane);
+  scatter_step<8, 8>(acc, lane);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) red[wave][(2 * ks + q / 2) * kTN + 2 * cp + q % 2] = acc[q];
+  __syncthreads();
+  if (eval) {
+    const int o = tid;
+    float v = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
+    v = activate(v + ebias, a.act);
+    a.out[eat] = v + eres;
+  }
+}
+
+template <int LAYOUT>
+void launch_rows_linear(const LinearArgs& a, bool ln, bool mul, hipStream_t s) {
+  const dim3 grid((unsigned)cdiv(a.N, kTN), (unsigned)cdiv(a.rows, kTR));
+  if (ln && mul)
+    rows_linear_kernel<LAYOUT, true, true><<<grid, kThreads, 0, s>>>(a);
+  else if (ln)
+    rows_linear_kernel<LAYOUT, true, false><<<grid, kThreads, 0, s>>>(a);
+  else if (mul)
+    rows_linear_kernel<LAYOUT, false, true><<<grid, kThreads, 0, s>>>(a);
+  else
+    rows_linear_kernel<LAYOUT, false, false><<<grid, kThreads, 0, s>>>(a);
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+}  // namespace mpl
+
+using namespace mpl;
+
+extern "C" int mpl_rows_linear(const float* x, const float* x_mul, const float* ln_scale, const float* ln_bias,
+                               float ln_eps, const float* weight, int weight_layout, const float* bias, int activation,
+                               const float* residual, int64_t rows, int K, int N, float* out, void* stream) {
+  clear_error();
+  MPL_REQUIRE(rows >= 0 && K >= 4 && K % 4 == 0 && N >= 1, MPL_EINVAL,
+              "mpl_rows_linear: rows=%lld K=%d N=%d (K must be a positive multiple of 4, N positive)",
+              (long long)rows, K, N);
+  MPL_REQUIRE(weight_layout == MPL_W_IN_OUT || weight_layout == MPL_W_OUT_IN, MPL_EINVAL,
+              "mpl_rows_linear: bad weight_layout %d", weight_layout);
+  MPL_REQUIRE(activation == MPL_ACT_NONE || activation == MPL_ACT_GELU_TANH || activation == MPL_ACT_SILU,
+              MPL_EINVAL, "mpl_rows_linear: bad activation %d", activation);
+  MPL_REQUIRE((ln_scale == nullptr) == (ln_bias == nullptr), MPL_EINVAL,
+              "mpl_rows_linear: ln_scale and ln_bias go together");
+  MPL_REQUIRE(rows <= (int64_t)65535 * 16, MPL_EINVAL, "mpl_rows_linear: rows=%lld above %d", (long long)rows,
+              65535 * 16);
+  if (rows == 0) return MPL_OK;
+  MPL_REQUIRE(x && weight && out, MPL_EINVAL, "mpl_rows_linear: null x, weight or out");
+  MPL_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(x_mul) && aligned16(ln_scale) && aligned16(ln_bias),
+              MPL_EINVAL, "mpl_rows_linear: x, x_mul, weight, ln_scale and ln_bias must be 16-byte aligned");
+  MPL_REQUIRE(out != x && out != x_mul, MPL_EINVAL, "mpl_rows_linear: out may alias residual only");
+  LinearArgs a{x, x_mul, ln_scale, ln_bias, weight, bias, residual, out, rows, K, N, activation, ln_eps};
+  hipStream_t s = (hipStream_t)stream;
+  const bool ln = ln_scale != nullptr, mul = x_mul != nullptr;
+  if (weight_layout == MPL_W_OUT_IN)
+    launch_rows_linear<MPL_W_OUT_IN>(a, ln, mul, s);
+  else
+    launch_rows_linear<MPL_W_IN_OUT>(a, ln, mul, s);
+  return check_launch("mpl_rows_linear");
+}

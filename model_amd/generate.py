@@ -7,9 +7,11 @@ captured once in a HIP graph and replayed; the next input token (the prompt's
 or the argmax of the step's logits) is chosen on the device, so a whole
 generation is queued without a host round trip per token.  The reference's
 jitted step takes the parameters on every call; here a generate() call
-re-captures the step when a parameter was replaced or the pool's sub-keys or
-log-temperature changed in place since the capture (weights updated in
-place are read live by the graph).
+re-captures the step when a parameter was replaced, or when one that the
+step reads through a copy made before capture (the pool's sub-keys and
+log-temperature, the attention's query/key/value weights) changed in place
+since the capture (other weights updated in place are read live by the
+graph).
 """
 
 from __future__ import annotations
@@ -61,9 +63,10 @@ class Generator:
     def _param_state(self):
         """What a captured step depends on besides its inputs: the storage of
         every parameter (the graph reads the weights where they were at
-        capture), and the in-place version of the pool's sub-keys and
-        log-temperature (their packed operand and clamped value are computed
-        before capture and baked in)."""
+        capture), and the in-place version of the parameters it reads through
+        copies made before capture: the pool's sub-keys and log-temperature
+        (packed operand, clamped value) and the attention's query/key/value
+        weights (one fused projection)."""
         flat = []
 
         def walk(t):
@@ -75,8 +78,9 @@ class Generator:
 
         walk(self.params)
         pool = self.params.get("pool", {})
-        frozen = tuple((pool[k].data_ptr(), pool[k]._version) for k in ("sub_keys", "log_temperature") if k in pool)
-        return tuple(flat), frozen
+        copied = [pool[k] for k in ("sub_keys", "log_temperature") if k in pool]
+        copied += self.model.copied_parameters(self.params)
+        return tuple(flat), tuple((t.data_ptr(), t._version) for t in copied)
 
     def _ensure_graph(self):
         if not self.use_graph:

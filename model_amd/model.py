@@ -19,7 +19,12 @@ shapes follow the Flax modules, so a checkpoint of the reference
 With ``decode=True`` the attention keeps a key/value cache of max_len
 positions per layer (Flax's decode mode): one token per call at a position
 given as a device tensor, so a decode step has static shapes and can be
-captured in a HIP graph (model_amd/generate.py).
+captured in a HIP graph (model_amd/generate.py).  On the GPU a decode step
+is libmpl.so launches: the attention of the new token (cache write, scores,
+softmax, weighted values; mpl_decode_attention) and every dense layer with
+the layer norm before it and its activation and residual add after it
+(mpl_rows_linear), on a fused query/key/value projection whose weights are
+concatenated once per parameter version, not on every step.
 """
 
 from __future__ import annotations
@@ -71,6 +76,69 @@ class ModelConfig:
 
 def _dense(x, p):
     return torch.matmul(x, p["kernel"]) + p["bias"]
+
+
+_ACT = {None: 0, "gelu_tanh": 1, "silu": 2}
+
+
+def rows_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
+                out_in: bool = False, ln: Optional[Dict[str, torch.Tensor]] = None, eps: float = LN_EPS,
+                x_mul: Optional[torch.Tensor] = None, act: Optional[str] = None,
+                residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """mpl_rows_linear: act((LayerNorm(x) if ln else x) * x_mul . W + bias)
+    + residual for x [rows, K] fp32 on the GPU.  W is a Dense kernel [K, N]
+    (any [K, ...] shape, flattened) or, with out_in, a table [N, K] (the
+    embedding of embed.attend)."""
+    from . import _lib
+
+    rows, K = x.shape
+    W = weight.reshape(-1, K) if out_in else weight.reshape(K, -1)
+    N = W.shape[0] if out_in else W.shape[1]
+    ts = [x, W] + [t for t in (bias, x_mul, residual) if t is not None]
+    if ln is not None:
+        ts += [ln["scale"], ln["bias"]]
+    for t in ts:
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.device != x.device:
+            raise ValueError("rows_linear: operands must be contiguous fp32 on one device")
+    if x.device.type != "cuda":
+        raise ValueError("rows_linear runs on the GPU only (libmpl.so)")
+    if ((bias is not None and bias.numel() != N) or (x_mul is not None and x_mul.shape != x.shape)
+            or (residual is not None and residual.shape != (rows, N))
+            or (ln is not None and (ln["scale"].numel() != K or ln["bias"].numel() != K))):
+        raise ValueError(f"rows_linear: operand shapes do not fit x {tuple(x.shape)} and W {tuple(W.shape)}")
+    out = torch.empty((rows, N), dtype=torch.float32, device=x.device)
+    P = _lib.ptr
+    _lib.check(_lib.lib().mpl_rows_linear(
+        P(x), P(x_mul), P(None if ln is None else ln["scale"]), P(None if ln is None else ln["bias"]), float(eps),
+        P(W), _lib.MPL_W_OUT_IN if out_in else _lib.MPL_W_IN_OUT, P(bias), _ACT[act], P(residual), rows, K, N,
+        P(out), _lib.stream_ptr(x.device)), "mpl_rows_linear")
+    return out
+
+
+def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, layer_cache: Dict[str, torch.Tensor], heads: int,
+                     scale: float) -> torch.Tensor:
+    """mpl_decode_attention: qkv [B, 3 * heads * hd] fp32 (query, key and
+    value of the new token, biases added) -> [B, heads * hd]; writes the key
+    and value into layer_cache ("kt" [B, heads, hd, max_len], "v" [B, heads,
+    max_len, hd]) at positions[0] first."""
+    from . import _lib
+
+    kt, v = layer_cache["kt"], layer_cache["v"]
+    B, H, hd, L = kt.shape
+    if (H != heads or qkv.shape != (B, 3 * H * hd) or v.shape != (B, H, L, hd) or positions.numel() != 1
+            or positions.dtype != torch.int64):
+        raise ValueError(f"decode_attention: qkv {tuple(qkv.shape)}, kt {tuple(kt.shape)}, v {tuple(v.shape)}, "
+                         f"positions {tuple(positions.shape)} {positions.dtype} do not fit together")
+    for t in (qkv, kt, v):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.device != qkv.device:
+            raise ValueError("decode_attention: qkv and caches must be contiguous fp32 on one device")
+    if qkv.device.type != "cuda" or positions.device != qkv.device:
+        raise ValueError("decode_attention: qkv, caches and positions must be on the same GPU")
+    out = torch.empty((B, H * hd), dtype=torch.float32, device=qkv.device)
+    _lib.check(_lib.lib().mpl_decode_attention(qkv.data_ptr(), B, H, hd, L, positions.data_ptr(), kt.data_ptr(),
+                                               v.data_ptr(), out.data_ptr(), float(scale),
+                                               _lib.stream_ptr(qkv.device)), "mpl_decode_attention")
+    return out
 
 
 def _ln(x, p):
@@ -146,6 +214,7 @@ class MemoryPoolLM:
 
     def __init__(self, cfg: ModelConfig, decode: bool = False):
         self.cfg, self.decode = cfg, decode
+        self._qkv_cache: Dict[int, Tuple[tuple, torch.Tensor, torch.Tensor]] = {}
         self.pool = None
         if cfg.use_memory:
             self.pool = MemoryPool(cfg.n_sub_keys, cfg.pool_heads, cfg.d_key, cfg.d_value, cfg.top_k,
@@ -207,6 +276,76 @@ class MemoryPoolLM:
                 for _ in range(cfg.n_layers)]
 
     # ----------------------------------------------------------- forward
+    @staticmethod
+    def _qkv_sources(pa) -> List[torch.Tensor]:
+        return [pa[nm][part] for nm in ("query", "key", "value") for part in ("kernel", "bias")]
+
+    def copied_parameters(self, p) -> List[torch.Tensor]:
+        """The parameters a GPU decode step reads through copies made before
+        a HIP-graph capture (the fused query/key/value weights) rather than
+        from their own storage: a captured step is stale once any of them
+        changes in place."""
+        if not self.decode:
+            return []
+        return [t for i in range(self.cfg.n_layers) for t in self._qkv_sources(p[f"attn_{i}"])]
+
+    def _fused_qkv(self, i: int, pa) -> Tuple[torch.Tensor, torch.Tensor]:
+        """[d, 3 * heads * hd] kernel and [3 * heads * hd] bias of layer i's
+        three projections, rebuilt when one of them was replaced or changed
+        in place (storage and version key)."""
+        src = self._qkv_sources(pa)
+        key = tuple((t.data_ptr(), t._version) for t in src)
+        hit = self._qkv_cache.get(i)
+        if hit is not None and hit[0] == key:
+            return hit[1], hit[2]
+        d = self.cfg.d_model
+        with torch.no_grad():
+            w = torch.cat([src[j].reshape(d, -1) for j in (0, 2, 4)], 1)
+            b = torch.cat([src[j].reshape(-1) for j in (1, 3, 5)])
+        self._qkv_cache[i] = (key, w, b)
+        return w, b
+
+    def _decode_step_gpu(self, p, tokens, positions, cache, noise_scale, rngs):
+        """One decode step on the GPU (inference: no autograd, no dropout):
+        the computation of the general path of apply() for T = 1, with every
+        dense layer of a block one mpl_rows_linear launch that also applies
+        the layer norm before it, its activation and the residual add after
+        it, and the attention one mpl_decode_attention launch per layer.  With
+        memory_ffn the residual branch's two terms are added to x one after
+        the other (x + ffn, then + mem_out)."""
+        cfg = self.cfg
+        B = tokens.shape[0]
+        d, H = cfg.d_model, cfg.n_heads
+        hd = d // H
+        emb = p["embed"]["embedding"]
+        layer_aux = []
+        with torch.no_grad():
+            x = emb[tokens[:, 0]] + p["pos_embed"][positions]  # [B, d]
+            for i in range(cfg.n_layers):
+                pa = p[f"attn_{i}"]
+                w, b = self._fused_qkv(i, pa)
+                qkv = rows_linear(x, w, b, ln=p[f"ln_attn_{i}"])
+                a = decode_attention(qkv, positions, cache[i], H, hd ** -0.5)
+                x = rows_linear(a, pa["out"]["kernel"], pa["out"]["bias"], residual=x)
+                ln = p[f"ln_ffn_{i}"]
+                mem_layer = self.pool is not None and i in cfg.memory_layers
+                x_in = x
+                if not mem_layer or cfg.memory_ffn:
+                    fi, fo = p[f"ffn_in_{i}"], p[f"ffn_out_{i}"]
+                    hid = rows_linear(x_in, fi["kernel"], fi["bias"], ln=ln, act="gelu_tanh")
+                    x = rows_linear(hid, fo["kernel"], fo["bias"], residual=x)
+                if mem_layer:
+                    r, g, mo = p[f"router_{i}"], p[f"mem_gate_{i}"], p[f"mem_out_{i}"]
+                    q = rows_linear(x_in, r["kernel"], r["bias"], ln=ln).reshape(B, cfg.pool_heads, cfg.d_key)
+                    mem, aux = self.pool.apply({"params": p["pool"]}, q, noise_scale=noise_scale, rngs=rngs)
+                    gate = rows_linear(x_in, g["kernel"], g["bias"], ln=ln, act="silu")
+                    x = rows_linear(mem.float().contiguous(), mo["kernel"], mo["bias"], x_mul=gate, residual=x)
+                    layer_aux.append(aux)
+            # the vocabulary product is a plain 64 x 256 x 16,384-class GEMM: the library's
+            # tiles run it faster than 16-row tiles would
+            logits = F.linear(_ln(x, p["ln_final"]), emb)[:, None]
+        return logits, _LazyMerged(layer_aux)
+
     def _attention(self, p, h, layer_cache, positions, drop=None):
         cfg = self.cfg
         B, T, d = h.shape
@@ -245,6 +384,9 @@ class MemoryPoolLM:
         cfg = self.cfg
         p = variables["params"] if "params" in variables else variables
         B, T = tokens.shape
+        if (self.decode and tokens.is_cuda and cache is not None and positions is not None and T == 1 and not train
+                and not pool_off and not route_through_pool and probes is None and not shuffle_pool):
+            return self._decode_step_gpu(p, tokens, positions, cache, noise_scale, rngs)
         emb = p["embed"]["embedding"]
         if positions is None:
             x = emb[tokens] + p["pos_embed"][None, :T]

@@ -85,3 +85,22 @@ def test_generator_follows_pool_parameters_changed_in_place(gpu_lib):
     eager = Generator(cfg, params, batch_size=4, graph=False).generate(prompt, n_new=8)
     assert torch.equal(after["logits"], eager["logits"])
     assert not torch.equal(after["logits"], before["logits"])
+
+
+def test_generator_follows_attention_weights_changed_in_place(gpu_lib):
+    """The GPU decode step reads the query/key/value weights through one
+    fused copy made before capture; after an in-place update of one of them
+    the next generate() must re-capture and use the new weights."""
+    cfg = ModelConfig(vocab_size=300, max_len=40, d_model=64, n_heads=4, n_layers=2, ffn_mult=2, n_sub_keys=64,
+                      pool_heads=4, d_key=64, d_value=64, top_k=8, memory_layers=(1,))
+    params = MemoryPoolLM(cfg).init(6)
+    prompt = np.random.default_rng(4).integers(0, 300, (3, 10))
+    gen = Generator(cfg, params, batch_size=3, graph=True)
+    before = gen.generate(prompt, n_new=6)
+    with torch.no_grad():
+        params["params"]["attn_0"]["query"]["kernel"].mul_(-2.0)
+        params["params"]["attn_1"]["value"]["bias"].add_(0.5)
+    after = gen.generate(prompt, n_new=6)
+    eager = Generator(cfg, params, batch_size=3, graph=False).generate(prompt, n_new=6)
+    assert torch.equal(after["logits"], eager["logits"])
+    assert not torch.equal(after["logits"], before["logits"])

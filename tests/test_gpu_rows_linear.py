@@ -1,0 +1,91 @@
+"""mpl_rows_linear (the backbone's dense layers of a decode step, with the
+layer norm before them, the activation and the residual add after them
+fused in; model.py:29-127) against the oracle's layer_norm, dense,
+gelu_tanh and silu (oracle/backbone.py, pinned in
+tests/test_oracle_backbone.py) in fp64: fp32 accumulation within 2e-5 of
+the result's largest magnitude, over row counts around the tile heights (16
+and 64 rows), K up to 1024, outputs up to the vocabulary width and of odd
+width, both weight layouts, and every optional operand on and off."""
+
+import numpy as np
+import pytest
+import torch
+
+from model_amd.model import rows_linear
+from oracle import backbone as ob
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    # rows, K, N, out_in, ln, mul, act, bias, residual
+    (1, 256, 768, False, True, False, None, True, False),
+    (5, 16, 4, False, False, False, None, True, True),
+    (64, 256, 1024, False, True, False, "gelu_tanh", True, False),
+    (64, 1024, 256, False, False, False, None, True, True),
+    (70, 256, 256, False, True, False, "silu", True, False),
+    (17, 256, 48, False, False, True, None, True, True),
+    (64, 256, 4096, True, True, False, None, False, False),
+    (130, 64, 2048, True, False, False, None, False, False),
+    (3, 32, 300, True, True, False, None, False, False),
+    (33, 128, 96, False, True, True, "silu", False, True),
+    (2, 32, 51, False, True, False, None, True, True),  # odd N: column pairs split
+    (4, 32, 50, True, True, False, None, False, False),
+    (19, 64, 50, False, False, False, "gelu_tanh", True, False),
+]
+
+
+@pytest.mark.parametrize("rows,K,N,out_in,ln,mul,act,bias,residual", CASES)
+def test_rows_linear_matches_oracle(gpu_lib, rows, K, N, out_in, ln, mul, act, bias, residual):
+    rng = np.random.default_rng(rows * 7919 + K * 31 + N)
+    x = rng.standard_normal((rows, K)) * 1.5 + 0.3
+    W = rng.standard_normal((N, K) if out_in else (K, N)) * K ** -0.5
+    b = rng.standard_normal(N) * 0.1 if bias else None
+    lnp = {"scale": 1.0 + 0.1 * rng.standard_normal(K), "bias": 0.1 * rng.standard_normal(K)} if ln else None
+    m = rng.standard_normal((rows, K)) if mul else None
+    res = rng.standard_normal((rows, N)) if residual else None
+    f32 = [t.astype(np.float32) if t is not None else None for t in (x, W, b, m, res)]
+    x, W, b, m, res = [t.astype(np.float64) if t is not None else None for t in f32]  # the inputs as stored
+    if lnp is not None:
+        lnp = {k: v.astype(np.float32).astype(np.float64) for k, v in lnp.items()}
+
+    a = ob.layer_norm(x, lnp) if ln else x
+    if mul:
+        a = a * m
+    want = ob.dense(a, {"kernel": W.T if out_in else W, "bias": b if b is not None else np.zeros(N)})
+    if act == "gelu_tanh":
+        want = ob.gelu_tanh(want)
+    elif act == "silu":
+        want = ob.silu(want)
+    if residual:
+        want = want + res
+
+    cuda = [torch.as_tensor(t, device="cuda") if t is not None else None for t in f32]
+    xt, Wt, bt, mt, rt = cuda
+    lnt = {k: torch.as_tensor(v, dtype=torch.float32, device="cuda") for k, v in lnp.items()} if ln else None
+    got = rows_linear(xt, Wt, bt, out_in=out_in, ln=lnt, x_mul=mt, act=act, residual=rt)
+    assert got.shape == (rows, N)
+    err = np.abs(got.double().cpu().numpy() - want).max() / np.abs(want).max()
+    assert err <= 2e-5, f"relative error {err:.3g}"
+
+
+def test_rows_linear_is_deterministic_and_accepts_residual_as_output(gpu_lib):
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn((64, 1024), generator=g, device="cuda")
+    W = torch.randn((1024, 256), generator=g, device="cuda")
+    r = torch.randn((64, 256), generator=g, device="cuda")
+    a = rows_linear(x, W, residual=r)
+    b = rows_linear(x, W, residual=r)
+    assert torch.equal(a, b)
+
+
+def test_rows_linear_rejects_bad_operands(gpu_lib):
+    x = torch.zeros((4, 30), device="cuda")
+    with pytest.raises(Exception, match="multiple of 4"):
+        rows_linear(x, torch.zeros((30, 8), device="cuda"))
+    x = torch.zeros((4, 32), device="cuda")
+    with pytest.raises(ValueError):
+        rows_linear(x, torch.zeros((32, 8), device="cuda"), torch.zeros(7, device="cuda"))
+    with pytest.raises(ValueError):
+        rows_linear(x.half(), torch.zeros((32, 8), device="cuda"))
+    with pytest.raises(Exception, match="16-byte aligned"):
+        rows_linear(torch.zeros(4 * 32 + 1, device="cuda")[1:].view(4, 32), torch.zeros((32, 8), device="cuda"))
