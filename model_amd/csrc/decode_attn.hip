@@ -3,7 +3,7 @@
 // MultiHeadDotProductAttention with decode=True, one new token per stream at
 // a position shared by every stream, generate.py:31-34).
 //
-// Per (stream b, head h) one workgroup of 256 threads:
+// Per (stream b, head h) one workgroup of 512 threads:
 //   q, k, v  <- the fused query/key/value projection row of stream b
 //               (qkv [B, 3, heads, hd], biases added; q times `scale`)
 //   kt[b, h, :, p] = k,  v_cache[b, h, p, :] = v          (the cache write)
@@ -26,7 +26,7 @@
 namespace mpl {
 namespace {
 
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kMaxLen = 8192;
 
 __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) {
@@ -43,17 +43,26 @@ __device__ __forceinline__ float block_reduce(float v, float* red, bool is_max) 
   return r;
 }
 
+__device__ __forceinline__ void fma4(float4& acc, float w, const float4& v) {
+  acc.x = fmaf(w, v.x, acc.x);
+  acc.y = fmaf(w, v.y, acc.y);
+  acc.z = fmaf(w, v.z, acc.z);
+  acc.w = fmaf(w, v.w, acc.w);
+}
+
 template <int HD>
 __global__ __launch_bounds__(kThreads) void decode_attention_kernel(const float* __restrict__ qkv, int heads,
                                                                      int max_len, const int64_t* __restrict__ position,
                                                                      float* __restrict__ kt, float* __restrict__ vc,
                                                                      float* __restrict__ out, float scale) {
-  constexpr int G = kThreads / HD;  // groups of HD lanes in the weighted sum
-  constexpr int U = 16;             // positions per unrolled step of a group
-  constexpr int DC = HD < 64 ? HD : 64;  // key dims loaded at once per position
-  extern __shared__ float sc[];     // [max_len] scores, then their exponentials
-  __shared__ float qs[HD], kn[HD], vn[HD];
-  __shared__ float part[kThreads];
+  constexpr int LP = HD / 4;         // lanes per value row (float4 each)
+  constexpr int G = kThreads / LP;   // value-row groups
+  constexpr int U = HD <= 64 ? 12 : 4;  // value rows per group loaded at once
+  constexpr int DC = HD <= 64 ? HD : 32;  // key dims loaded at once per position
+  extern __shared__ float sc[];      // [max_len] scores, then their exponentials
+  __shared__ float qs[HD], kn[HD];
+  __shared__ float4 vn4[LP];
+  __shared__ float4 part[G][LP];
   __shared__ float red[kThreads / kWave];
   const int tid = threadIdx.x;
   const int bh = blockIdx.x;
@@ -71,13 +80,33 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(const float*
   const float* row = qkv + (size_t)b * 3 * heads * HD;
   float* ktb = kt + (size_t)bh * HD * max_len;
   float* vb = vc + (size_t)bh * max_len * HD;
+  const int g = tid / LP, l4 = tid - g * LP;  // value-row group, float4 of the row
+  const float4* vb4 = (const float4*)vb;
+
+  // cache reads that do not depend on the new token go out first: the first
+  // DC dims of this thread's first key column (position tid) and the first U
+  // value rows of its group (positions g, g + G, ...); positions at or after
+  // p read position 0 (in bounds) and are not used
+  float kv0[DC];
+  {
+    const float* col = ktb + (tid < p ? tid : 0);
+#pragma unroll
+    for (int j = 0; j < DC; ++j) kv0[j] = col[(size_t)j * max_len];
+  }
+  float4 vv0[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int t = g + u * G;
+    vv0[u] = vb4[(size_t)(t < p ? t : 0) * LP + l4];
+  }
+
   if (tid < HD) {
     const float q = row[h * HD + tid] * scale;
     const float k = row[(heads + h) * HD + tid];
     const float v = row[(2 * heads + h) * HD + tid];
     qs[tid] = q;
     kn[tid] = k;
-    vn[tid] = v;
+    ((float*)vn4)[tid] = v;
     ktb[(size_t)tid * max_len + p] = k;
     vb[(size_t)p * HD + tid] = v;
   }
@@ -91,11 +120,17 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(const float*
       for (int d = 0; d < HD; ++d) s = fmaf(qs[d], kn[d], s);
     } else {
       const float* col = ktb + t;
-#pragma unroll
+      const bool first = t == tid;
+#pragma unroll 1
       for (int d0 = 0; d0 < HD; d0 += DC) {
         float kv[DC];
+        if (d0 == 0 && first) {
 #pragma unroll
-        for (int j = 0; j < DC; ++j) kv[j] = col[(size_t)(d0 + j) * max_len];
+          for (int j = 0; j < DC; ++j) kv[j] = kv0[j];
+        } else {
+#pragma unroll
+          for (int j = 0; j < DC; ++j) kv[j] = col[(size_t)(d0 + j) * max_len];
+        }
 #pragma unroll
         for (int j = 0; j < DC; ++j) s = fmaf(qs[d0 + j], kv[j], s);
       }
@@ -113,33 +148,34 @@ __global__ __launch_bounds__(kThreads) void decode_attention_kernel(const float*
   sum = block_reduce(sum, red, false);  // its barriers also publish sc[]
 
   // weighted sum of the values: group g takes positions t = g, g + G, ...
-  // (U, then 4, then 1 per step, loads first); lane d of a group owns dimension d;
-  // position p itself comes from LDS
-  const int g = tid / HD, d = tid - g * HD;
-  float acc = 0.0f;
-  int t = g;
-  for (; t + (U - 1) * G < p; t += U * G) {
-    float vv[U];
+  // (the first U from the registers loaded at the start, then U per step,
+  // loads first); lane l4 of a group owns dims 4 l4 .. 4 l4 + 3; position p
+  // itself comes from LDS
+  float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
 #pragma unroll
-    for (int u = 0; u < U; ++u) vv[u] = vb[(size_t)(t + u * G) * HD + d];
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc = fmaf(sc[t + u * G], vv[u], acc);
+  for (int u = 0; u < U; ++u) {
+    const int t = g + u * G;
+    if (t < p) fma4(acc, sc[t], vv0[u]);
   }
-  for (; t + 3 * G < p; t += 4 * G) {
-    float vv[4];
+  int t = g + U * G;
+  for (; t < p; t += U * G) {
+    float4 vv[U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) vv[u] = vb[(size_t)(t + u * G) * HD + d];
+    for (int u = 0; u < U; ++u) {
+      const int tu = t + u * G;
+      vv[u] = vb4[(size_t)(tu < p ? tu : 0) * LP + l4];
+    }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc = fmaf(sc[t + u * G], vv[u], acc);
+    for (int u = 0; u < U; ++u)
+      if (t + u * G < p) fma4(acc, sc[t + u * G], vv[u]);
   }
-  for (; t < p; t += G) acc = fmaf(sc[t], vb[(size_t)t * HD + d], acc);
-  if (t == p) acc = fmaf(sc[p], vn[d], acc);
-  part[tid] = acc;
+  if (p % G == g) fma4(acc, sc[p], vn4[l4]);  // the group whose sequence reaches p
+  part[g][l4] = acc;
   __syncthreads();
   if (tid < HD) {
+    const int q4 = tid / 4, e = tid % 4;
     float a = 0.0f;
-#pragma unroll
-    for (int j = 0; j < G; ++j) a += part[j * HD + tid];
+    for (int j = 0; j < G; ++j) a += ((const float*)&part[j][q4])[e];
     o[tid] = a / sum;
   }
 }

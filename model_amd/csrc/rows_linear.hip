@@ -12,18 +12,20 @@
 // W is [K, N] (a Dense kernel) or [N, K] (the embedding table read by
 // embed.attend).  Library GEMMs pick tiles for large matrices; here the
 // products are R x K x N with R = a few dozen rows (one per stream), which
-// leaves a 16-row tile per workgroup and makes the length of each thread's
-// dependent chain of loads the cost.  So K is split over all 256 threads of
-// the workgroup that owns a 16 x 16 output tile: lane (ks, cp) of wave w
-// takes the float4 columns j = 8w + ks, +32, +64, ... of K for the output
-// columns 2cp and 2cp + 1 and all 16 rows (32 accumulators), so each thread
-// issues 16 row loads and 2 weight loads per float4 of K, all independent.
-// The 8 K-slices of a wave are then added by a shuffle reduce-scatter
-// (xor 32, 16, 8: each step halves the values a lane holds), the 4 waves'
-// partial tiles through LDS in a fixed order, so results are deterministic.
-// LayerNorm statistics of the tile's rows are computed first (two passes
-// over each row: mean, then centred variance) and the normalisation is
-// applied to the operand as it is loaded.
+// leaves a 16-row tile per workgroup and makes the number of dependent
+// memory round trips of a thread the cost.  So K is split over all 512
+// threads of the workgroup that owns a 16 x 16 output tile: lane (ks, cp) of
+// wave w takes the float4 columns j = 8w + ks, +64, +128, ... of K for the
+// output columns 2cp and 2cp + 1 and all 16 rows (32 accumulators), and
+// issues the row and weight loads of two such columns before the first FMA
+// (one column per thread at K = 256, two batches at K = 1,024).  The 8
+// K-slices of a wave are then added by a shuffle reduce-scatter (xor 32, 16,
+// 8: each step halves the values a lane holds), the 8 waves' partial tiles
+// through LDS in a fixed order, so results are deterministic.  LayerNorm
+// statistics of the tile's rows are computed first (two passes over each
+// row, mean then centred variance, from registers) while the first weights
+// are in flight, and the normalisation is applied to the operand as it is
+// loaded.
 #include <math.h>
 
 #include "common.h"
@@ -31,9 +33,10 @@
 namespace mpl {
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kTR = 16;  // rows per tile
-constexpr int kTN = 16;  // columns per tile
+constexpr int kThreads = 512;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kTR = 16;                // rows per tile
+constexpr int kTN = 16;                // columns per tile
 constexpr int kSlices = kThreads / 8;  // K-slices per workgroup
 
 struct LinearArgs {
@@ -74,9 +77,18 @@ __device__ __forceinline__ void scatter_step(float* v, int lane) {
   }
 }
 
-template <int LAYOUT, bool LN, bool MUL>
+__device__ __forceinline__ void fma4(float& acc, const float4& v, const float4& w) {
+  acc = fmaf(v.x, w.x, acc);
+  acc = fmaf(v.y, w.y, acc);
+  acc = fmaf(v.z, w.z, acc);
+  acc = fmaf(v.w, w.w, acc);
+}
+
+// U: K columns per thread whose loads are in flight together (1 when a
+// thread has a single column, K <= 4 * kSlices)
+template <int LAYOUT, bool LN, bool MUL, int U>
 __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
-  __shared__ float red[kThreads / kWave][kTR * kTN];
+  __shared__ float red[kWaves][kTR * kTN];
   __shared__ float s_mean[kTR], s_rstd[kTR];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int64_t r0 = (int64_t)blockIdx.y * kTR;
@@ -85,11 +97,11 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
   const int nrows = (int)min<int64_t>(kTR, a.rows - r0);  // valid rows of this tile
 
   // operands that do not depend on the row statistics are requested first:
-  // the epilogue's bias and residual element of this thread and the weights
-  // of its first K-slice
-  const int erow = tid / kTN, ecol = tid % kTN;  // kTR * kTN == kThreads
+  // the epilogue's bias and residual element of this thread (threads below
+  // kTR * kTN) and the weights of its first K columns
+  const int erow = tid / kTN, ecol = tid % kTN;
   const int en = n0 + ecol;
-  const bool eval = erow < nrows && en < a.N;
+  const bool eval = tid < kTR * kTN && erow < nrows && en < a.N;
   const int64_t eat = (r0 + erow) * a.N + en;
   const float ebias = (eval && a.bias) ? a.bias[en] : 0.0f;
   const float eres = (eval && a.residual) ? a.residual[eat] : 0.0f;
@@ -119,29 +131,70 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     }
   };
   const int j0 = wave * 8 + ks;
-  float4 nw0 = zero, nw1 = zero;
-  if (j0 < K4) load_w(4 * j0, nw0, nw1);
+  // the columns of a batch: j, j + kSlices, ..., clamped to the last valid
+  // column (their loads stay in bounds; a clamped column is not accumulated)
+  float4 w0[U], w1[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int j = min(j0 + u * kSlices, K4 - 1);
+    load_w(4 * j, w0[u], w1[u]);
+  }
+
+  // the first batch of rows (and x_mul rows, LayerNorm scale and shift) is
+  // requested before the row statistics too: the loads do not depend on them
+  const float* xt = a.x + r0 * K;
+  const float* mt = MUL ? a.x_mul + r0 * K : nullptr;
+  float4 xv[U][kTR];
+  float4 mv[LN && MUL ? U : 1][kTR];  // x_mul rows, applied after the normalisation
+  float4 g[U], be[U];
+  auto load_batch = [&](int jb) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int k = 4 * min(jb + u * kSlices, K4 - 1);
+      g[u] = LN ? *(const float4*)(a.ln_scale + k) : zero;
+      be[u] = LN ? *(const float4*)(a.ln_bias + k) : zero;
+#pragma unroll
+      for (int i = 0; i < kTR; ++i) {
+        // rows past the end read row 0 (in bounds) and are never stored
+        const int64_t off = (int64_t)(i < nrows ? i : 0) * K + k;
+        float4 v = *(const float4*)(xt + off);
+        if (MUL) {
+          const float4 m = *(const float4*)(mt + off);
+          if (LN) {
+            mv[LN && MUL ? u : 0][i] = m;
+          } else {
+            v.x *= m.x;
+            v.y *= m.y;
+            v.z *= m.z;
+            v.w *= m.w;
+          }
+        }
+        xv[u][i] = v;
+      }
+    }
+  };
+  load_batch(j0);
 
   if (LN) {
-    // 16 threads per row (consecutive lanes); a thread's part of the row is
+    // 32 threads per row (consecutive lanes); a thread's part of the row is
     // kept in registers between the two passes when it has at most kHold
     // float4s (K <= 512), and read again otherwise
     constexpr int TPR = kThreads / kTR;
-    constexpr int kHold = 8;
+    constexpr int kHold = 4;
     const int row = tid / TPR, part = tid % TPR;
     const float4* xr = (const float4*)(a.x + (r0 + (row < nrows ? row : 0)) * K);
     const bool hold = K4 <= kHold * TPR;
-    float4 xv[kHold];
+    float4 hv[kHold];
     float s = 0.0f;
     if (row < nrows) {
       if (hold) {
 #pragma unroll
         for (int h = 0; h < kHold; ++h) {
           const int j = part + h * TPR;
-          xv[h] = j < K4 ? xr[j] : zero;
+          hv[h] = j < K4 ? xr[j] : zero;
         }
 #pragma unroll
-        for (int h = 0; h < kHold; ++h) s += (xv[h].x + xv[h].y) + (xv[h].z + xv[h].w);
+        for (int h = 0; h < kHold; ++h) s += (hv[h].x + hv[h].y) + (hv[h].z + hv[h].w);
       } else {
         for (int j = part; j < K4; j += TPR) {
           const float4 v = xr[j];
@@ -157,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
 #pragma unroll
         for (int h = 0; h < kHold; ++h) {
           if (part + h * TPR < K4) {
-            const float d0 = xv[h].x - mean, d1 = xv[h].y - mean, d2 = xv[h].z - mean, d3 = xv[h].w - mean;
+            const float d0 = hv[h].x - mean, d1 = hv[h].y - mean, d2 = hv[h].z - mean, d3 = hv[h].w - mean;
             q += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
           }
         }
@@ -177,52 +230,49 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     __syncthreads();
   }
 
-  const float* xt = a.x + r0 * K;
-  const float* mt = MUL ? a.x_mul + r0 * K : nullptr;
-  float mean[kTR], rstd[kTR];
-#pragma unroll
-  for (int i = 0; i < kTR; ++i) {
-    mean[i] = LN ? s_mean[i] : 0.0f;
-    rstd[i] = LN ? s_rstd[i] : 0.0f;
-  }
   float acc[2 * kTR];  // acc[2 i + c]: row i, column c0 + c
 #pragma unroll
   for (int e = 0; e < 2 * kTR; ++e) acc[e] = 0.0f;
 
-#pragma unroll 2
-  for (int j = j0; j < K4; j += kSlices) {
-    const int k = 4 * j;
-    const float4 w0 = nw0, w1 = nw1;
-    if (j + kSlices < K4) load_w(k + 4 * kSlices, nw0, nw1);  // the next slice's weights
-    float4 g = zero, be = zero;
-    if (LN) {
-      g = *(const float4*)(a.ln_scale + k);
-      be = *(const float4*)(a.ln_bias + k);
+  for (int jb = j0; jb < K4; jb += U * kSlices) {
+    if (jb != j0) load_batch(jb);  // the first batch was requested before the statistics
+    // the next batch's weights go out before this batch's arithmetic
+    float4 nw0[U], nw1[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int j = min(jb + (U + u) * kSlices, K4 - 1);
+      if (jb + U * kSlices < K4) load_w(4 * j, nw0[u], nw1[u]);
     }
 #pragma unroll
-    for (int i = 0; i < kTR; ++i) {
-      float4 v = i < nrows ? *(const float4*)(xt + (int64_t)i * K + k) : zero;
-      if (LN) {
-        v.x = (v.x - mean[i]) * rstd[i] * g.x + be.x;
-        v.y = (v.y - mean[i]) * rstd[i] * g.y + be.y;
-        v.z = (v.z - mean[i]) * rstd[i] * g.z + be.z;
-        v.w = (v.w - mean[i]) * rstd[i] * g.w + be.w;
+    for (int u = 0; u < U; ++u) {
+      if (jb + u * kSlices >= K4) break;  // a clamped column of the last batch
+#pragma unroll
+      for (int i = 0; i < kTR; ++i) {
+        float4 v = xv[u][i];
+        if (LN) {
+          const float mean = s_mean[i], rstd = s_rstd[i];
+          v.x = (v.x - mean) * rstd * g[u].x + be[u].x;
+          v.y = (v.y - mean) * rstd * g[u].y + be[u].y;
+          v.z = (v.z - mean) * rstd * g[u].z + be[u].z;
+          v.w = (v.w - mean) * rstd * g[u].w + be[u].w;
+          if (MUL) {
+            const float4 m = mv[LN && MUL ? u : 0][i];
+            v.x *= m.x;
+            v.y *= m.y;
+            v.z *= m.z;
+            v.w *= m.w;
+          }
+        }
+        fma4(acc[2 * i], v, w0[u]);
+        fma4(acc[2 * i + 1], v, w1[u]);
       }
-      if (MUL) {
-        const float4 m = i < nrows ? *(const float4*)(mt + (int64_t)i * K + k) : zero;
-        v.x *= m.x;
-        v.y *= m.y;
-        v.z *= m.z;
-        v.w *= m.w;
+    }
+    if (jb + U * kSlices < K4) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        w0[u] = nw0[u];
+        w1[u] = nw1[u];
       }
-      acc[2 * i] = fmaf(v.x, w0.x, acc[2 * i]);
-      acc[2 * i] = fmaf(v.y, w0.y, acc[2 * i]);
-      acc[2 * i] = fmaf(v.z, w0.z, acc[2 * i]);
-      acc[2 * i] = fmaf(v.w, w0.w, acc[2 * i]);
-      acc[2 * i + 1] = fmaf(v.x, w1.x, acc[2 * i + 1]);
-      acc[2 * i + 1] = fmaf(v.y, w1.y, acc[2 * i + 1]);
-      acc[2 * i + 1] = fmaf(v.z, w1.z, acc[2 * i + 1]);
-      acc[2 * i + 1] = fmaf(v.w, w1.w, acc[2 * i + 1]);
     }
   }
 
@@ -236,7 +286,9 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
   __syncthreads();
   if (eval) {
     const int o = tid;
-    float v = ((red[0][o] + red[1][o]) + red[2][o]) + red[3][o];
+    float v = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) v += red[w][o];
     v = activate(v + ebias, a.act);
     a.out[eat] = v + eres;
   }
@@ -245,14 +297,19 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
 template <int LAYOUT>
 void launch_rows_linear(const LinearArgs& a, bool ln, bool mul, hipStream_t s) {
   const dim3 grid((unsigned)cdiv(a.N, kTN), (unsigned)cdiv(a.rows, kTR));
+  // two columns in flight only for the plain product with more than one
+  // column per thread (the feed-forward output, K = 1,024): with a layer
+  // norm or x_mul the second batch of row registers would spill
   if (ln && mul)
-    rows_linear_kernel<LAYOUT, true, true><<<grid, kThreads, 0, s>>>(a);
+    rows_linear_kernel<LAYOUT, true, true, 1><<<grid, kThreads, 0, s>>>(a);
   else if (ln)
-    rows_linear_kernel<LAYOUT, true, false><<<grid, kThreads, 0, s>>>(a);
+    rows_linear_kernel<LAYOUT, true, false, 1><<<grid, kThreads, 0, s>>>(a);
   else if (mul)
-    rows_linear_kernel<LAYOUT, false, true><<<grid, kThreads, 0, s>>>(a);
+    rows_linear_kernel<LAYOUT, false, true, 1><<<grid, kThreads, 0, s>>>(a);
+  else if (a.K / 4 > kSlices)
+    rows_linear_kernel<LAYOUT, false, false, 2><<<grid, kThreads, 0, s>>>(a);
   else
-    rows_linear_kernel<LAYOUT, false, false><<<grid, kThreads, 0, s>>>(a);
+    rows_linear_kernel<LAYOUT, false, false, 1><<<grid, kThreads, 0, s>>>(a);
 }
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
