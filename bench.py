@@ -107,6 +107,25 @@ def copy_calibration(torch):
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "launches": 10}))
 
 
+_COPY_PEAK = {}
+
+
+def measured_copy_peak(torch):
+    """Bandwidth of a plain 1 GiB device-to-device copy (torch's copy kernel),
+    read + written bytes over the time of one copy, best of 3 x 10 launches:
+    the measured reference the gather's HBM figure is also reported
+    against.  Cached per process."""
+    if "GBs" not in _COPY_PEAK:
+        n = 1 << 30
+        src = torch.empty(n, dtype=torch.uint8, device="cuda").random_(0, 255)
+        dst = torch.empty_like(src)
+        ms = time_direct(torch, lambda i: dst.copy_(src), 10, 2)
+        _COPY_PEAK["GBs"] = 2 * n / (ms * 1e-3) / 1e9
+        del src, dst
+        torch.cuda.empty_cache()
+    return _COPY_PEAK["GBs"]
+
+
 class Lookup:
     """Preallocated buffers + direct C-ABI calls for one workload.
 
@@ -324,12 +343,15 @@ def gather_roofline(torch, lk, br, iters):
     mpl_gather_wsum) over rotating batches: algorithmic bytes = the fetched
     rows, M * H * k * d * 2 B.  ``achieved`` is from back-to-back launches
     (the kernel duration plus the dispatch gap); the graph-replayed figure of
-    the kernel breakdown, which adds a graph node's gap, is given beside it."""
+    the kernel breakdown, which adds a graph node's gap, is given beside it,
+    and so is the fraction of a measured device-copy bandwidth."""
     gb = lk.M * lk.H * lk.k * lk.d * 2
     ms = time_direct(torch, lk.gather, iters, lk.R)
     a = gb / (ms * 1e-3) / 1e9
+    cp = measured_copy_peak(torch)
     return {"kernel": "gather_wsum", "bound": "hbm", "achieved": a, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": a / HBM_PEAK_GBS, "ms_per_launch": ms, "algorithmic_bytes": gb,
+            "frac": a / HBM_PEAK_GBS, "copy_peak_GBs": cp, "frac_of_copy_peak": a / cp,
+            "ms_per_launch": ms, "algorithmic_bytes": gb,
             "traffic": measured_traffic("gather_wsum", "pool_67M_4096") if (lk.n, lk.M) == (8192, 4096) else None,
             "graph_replay_GBs": gb / (br["gather_wsum_ms"] * 1e-3) / 1e9, "rotating_batches": lk.R,
             "distinct_row_bytes_per_replay": gb * lk.R}
