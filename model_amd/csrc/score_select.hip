@@ -113,12 +113,39 @@ __device__ __forceinline__ W& lds_at(W* arr, uint32_t byte_off) {
   return *(W*)((char*)arr + byte_off);
 }
 
-// Merges the lane's buffered candidates (entries lane0, lane0 + kEntryBytes,
-// ... below st.off) into its list, empties the buffer and refreshes the
-// threshold.  Wave-uniform control flow.
+// KMAX-th largest key of the union of the lane pair's two sorted lists (the
+// partner lane's arrives through v_permlane32_swap): the element-wise max of
+// the own list and the partner's reversed list is the union's top KMAX as a
+// bitonic sequence, so its minimum is the KMAX-th largest.  Both lanes of the
+// pair get the same key; 0 when the union holds fewer than KMAX keys.
 template <int KMAX, bool NOISE>
+__device__ __forceinline__ u64 pair_kth_key(const TopList<KMAX, NOISE>& top, int par) {
+  u64 m = ~0ull;
+#pragma unroll
+  for (int j = 0; j < KMAX; ++j) {
+    float lo = __uint_as_float((uint32_t)top.key[j]), lo2 = lo;
+    float hi = __uint_as_float((uint32_t)(top.key[j] >> 32)), hi2 = hi;
+    half_swap(lo, lo2);
+    half_swap(hi, hi2);
+    const u64 other = ((u64)__float_as_uint(par ? hi : hi2) << 32) | __float_as_uint(par ? lo : lo2);
+    const u64 own = top.key[KMAX - 1 - j];
+    const u64 c = own > other ? own : other;
+    m = c < m ? c : m;
+  }
+  return m;
+}
+
+// Merges the lane's buffered candidates (entries lane0, lane0 + kEntryBytes,
+// ... below st.off) into its list, empties the buffer and, with REFRESH,
+// raises the threshold.  With k == KMAX the new threshold is the k-th best of
+// both lanes of the query together (its k-th best so far), otherwise the
+// lane's own k-th.  A key still to come that ties it loses on its larger
+// index, so '>' against it keeps every key that can still enter.  Wave-uniform
+// control flow.
+template <bool REFRESH, int KMAX, bool NOISE>
 __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
-                                           const float* pay, uint32_t lane0, bool valid, int k, float base_thr) {
+                                           const float* pay, uint32_t lane0, bool valid, int k, float base_thr,
+                                           int par) {
   const int cnt = (int)((st.off - lane0) / kEntryBytes);
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
@@ -138,9 +165,9 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
     st.top.template merge<8>(ch, cp);
   }
   st.off = lane0;
-  if (valid) {
-    const u64 kk = st.top.at(k - 1);
-    st.thr = kk ? key_score(kk) : base_thr;
+  if (REFRESH) {
+    const u64 kk = k == KMAX ? pair_kth_key<KMAX, NOISE>(st.top, par) : st.top.at(k - 1);
+    if (valid) st.thr = kk ? key_score(kk) : base_thr;
   }
 }
 
@@ -563,7 +590,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
       if (active && __ballot(st.off > flush_at) != 0)
-        flush_lane<KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr);
+        flush_lane<true, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int r = 8 * q + e;
@@ -581,7 +608,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       }
     }
   });
-  flush_lane<KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr);
+  flush_lane<false, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
 
   // Merge the two lanes' lists of the query: the partner's sorted list
   // arrives through v_permlane32_swap and is bitonic-merged (keys of the two
