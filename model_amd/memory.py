@@ -260,6 +260,35 @@ class MemoryPool:
 
     __call__ = apply
 
+    def forward_backward(self, variables: Dict[str, Any], queries: torch.Tensor, g_out: torch.Tensor,
+                         g_balance: Optional[torch.Tensor] = None, *, train: bool = True,
+                         noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
+                         rngs: Optional[Dict[str, Any]] = None):
+        """The forward of memory.py:119-227 and its backward for a given
+        upstream gradient, without torch autograd: returns
+        (out, aux, (d queries, d sub_keys, d log_temperature)).  The values
+        get no dense gradient (the trainer's sparse_grad=True path: the rows
+        come from aux["slots"], aux["weights"] and g_out).  ``g_balance`` is
+        the gradient of aux["balance_loss"] (None: no balance term).  Only
+        library kernels and tensor allocations, and no host read, so a whole
+        training step built on it can be captured in one HIP graph; the
+        results equal apply() followed by torch.autograd.grad bit for bit."""
+        params = variables["params"] if "params" in variables else variables
+        res = self.lookup(params, queries, train=train, noise_scale=noise_scale, shuffle_reads=shuffle_reads,
+                          rngs=rngs)
+        aux = res["aux"]
+        internal = {}
+        if g_balance is not None:
+            aux["balance_loss"]  # computes f and p (memory.py:196-213)
+            internal = aux.internal
+        sub_keys = params["sub_keys"]
+        shapes = (tuple(queries.shape), queries.dtype, sub_keys.dtype, params["log_temperature"].dtype)
+        values = params["values"] if "values" in params else sub_keys.new_empty(0)
+        dq, dk, dlt, _ = _lookup_backward(self, res, internal, sub_keys.detach(), values.detach(), shapes, g_out,
+                                          g_balance, bool(shuffle_reads), False)
+        out = res["out"].reshape(*tuple(queries.shape[:-2]), self.d_value)
+        return out, aux, (dq, dk, dlt)
+
     def lookup(self, params, queries: torch.Tensor, *, train: bool = False,
                noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
                rngs: Optional[Dict[str, Any]] = None, gumbel: Optional[torch.Tensor] = None) -> Dict[str, Any]:
@@ -525,97 +554,109 @@ class _LookupFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_out, g_balance):
-        pool, res, opts = ctx.pool, ctx.res, ctx.opts
         sub_keys, values = ctx.saved_tensors
-        q_shape, q_dtype, k_dtype, t_dtype = ctx.shapes
-        H, n, k, d = pool.heads, pool.n_sub_keys, pool.top_k, pool.d_value
-        half = pool.d_key // 2
-        q = res["q"]
-        M = q.shape[0]
-        dev = q.device
-        L = _lib.lib()
-        stream = _lib.stream_ptr(dev)
-        T = res["temperature"]
-        q_hat, q_len, k_hat = res["q_hat"], res["q_len"], res["k_hat"]
-        if g_out is None:
-            g_out = torch.zeros((M, d), dtype=torch.float32, device=dev)
-        g_out = g_out.reshape(M, d).float().contiguous()
+        need_dv = ctx.needs_input_grad[3] and not ctx.opts["sparse_grad"]
+        dq, dk, dlt, dv = _lookup_backward(ctx.pool, ctx.res, ctx.internal, sub_keys, values, ctx.shapes, g_out,
+                                           g_balance, bool(ctx.opts["shuffle_reads"]), need_dv)
+        return dq, dk, dlt, dv, None, None
 
-        # route: dw, softmax backward, scatter to the stage-1 ranks
-        d_sub = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
-        dlogt_part = torch.empty(max(M, 1), dtype=torch.float32, device=dev)
-        if res["staged"] is not None:  # host pool: the staged unique rows, indexed by inverse
-            vals, vslots = res["staged"]
-            vN, vshuffle = max(vals.shape[0], 1), 0
-        else:
-            vals, vslots = values.detach(), res["slots"]
-            vN, vshuffle = pool.pool_size, int(bool(opts["shuffle_reads"]))
-        check(L.mpl_lookup_bwd_route(ptr(g_out), ptr(vals), _dtype_code(vals.dtype), vN, d,
-                                     ptr(vslots), ptr(res["weights"]), ptr(res["flat_idx"]),
-                                     ptr(res["sub_scores"]), M, H, k, vshuffle, None,
-                                     ptr(d_sub), ptr(dlogt_part), stream), "mpl_lookup_bwd_route")
 
-        # dense over n on MFMA tiles of the scoring precision: the balance
-        # loss (memory.py:208-213) together with the routed sub-key term.
-        # Without the balance term, fp32 scoring takes the routed term alone
-        # from a sort-by-key segmented sum (O(M k) instead of O(M n)).
-        dq_extra = dlen_extra = dlogt_extra = None
-        btg = pool.balance_temperature_grad
-        raw_keys = sub_keys.detach().float().contiguous()
-        dk = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
-        bal = g_balance is not None and "_state" in ctx.internal
-        code = res["score_code"]
-        dense = M > 0 and (code == MPL_F16 or bal)
-        if dense:
-            dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
-            gb = None
-            if bal:
-                dq_extra = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
-                dlen_extra = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if (btg and q_len is not None) else None
-                dlogt_extra = torch.empty(1, dtype=torch.float32, device=dev) if btg else None
-                gb = g_balance.reshape(1).float().contiguous()
-            wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half, code)
-            ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
-            check(L.mpl_lookup_bwd_dense(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
-                                         ptr(d_sub), ptr(ctx.internal["_counts"]) if bal else None,
-                                         ptr(ctx.internal["_state"]) if bal else None, ptr(gb), int(btg),
-                                         int(bool(pool.query_scale)), M, H, n, half, k, code, ptr(T), ptr(ws), wsb,
-                                         ptr(dq_extra), ptr(dk_hat), ptr(dlen_extra), ptr(dlogt_extra), stream),
-                  "mpl_lookup_bwd_dense")
-            check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
-                                         stream), "mpl_l2_normalize_bwd")
+def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_balance, shuffle_reads: bool,
+                     need_dv: bool):
+    """The backward of memory.py:136-213 on the GPU for one forward result
+    ``res`` of MemoryPool.lookup: (d queries, d sub_keys, d log_temperature,
+    d values or None).  ``g_balance`` is the gradient of the balance loss
+    (None: no balance term); ``internal`` holds the balance statistics of the
+    forward.  Only library kernels and tensor allocations: no host read."""
+    q_shape, q_dtype, k_dtype, t_dtype = shapes
+    H, n, k, d = pool.heads, pool.n_sub_keys, pool.top_k, pool.d_value
+    half = pool.d_key // 2
+    q = res["q"]
+    M = q.shape[0]
+    dev = q.device
+    L = _lib.lib()
+    stream = _lib.stream_ptr(dev)
+    T = res["temperature"]
+    q_hat, q_len, k_hat = res["q_hat"], res["q_len"], res["k_hat"]
+    if g_out is None:
+        g_out = torch.zeros((M, d), dtype=torch.float32, device=dev)
+    g_out = g_out.reshape(M, d).float().contiguous()
 
-        # queries
-        dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
-        check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
-                                       ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
-                                       ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
-        # sub-keys (fp32 scoring without the balance term, or no tokens):
-        # sort-by-key segmented sum
-        if not dense:
-            wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
-            ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-            check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
-                                        None, M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
-                  "mpl_lookup_bwd_keys")
-        # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
-        dlt = torch.empty(1, dtype=torch.float32, device=dev)
-        check(L.mpl_sum(ptr(dlogt_part), M, ptr(dlogt_extra), ptr(dlt), stream), "mpl_sum")
+    # route: dw, softmax backward, scatter to the stage-1 ranks
+    d_sub = torch.empty((M, H, 2, k), dtype=torch.float32, device=dev)
+    dlogt_part = torch.empty(max(M, 1), dtype=torch.float32, device=dev)
+    if res["staged"] is not None:  # host pool: the staged unique rows, indexed by inverse
+        vals, vslots = res["staged"]
+        vN, vshuffle = max(vals.shape[0], 1), 0
+    else:
+        vals, vslots = values.detach(), res["slots"]
+        vN, vshuffle = pool.pool_size, int(shuffle_reads)
+    check(L.mpl_lookup_bwd_route(ptr(g_out), ptr(vals), _dtype_code(vals.dtype), vN, d,
+                                 ptr(vslots), ptr(res["weights"]), ptr(res["flat_idx"]),
+                                 ptr(res["sub_scores"]), M, H, k, vshuffle, None,
+                                 ptr(d_sub), ptr(dlogt_part), stream), "mpl_lookup_bwd_route")
 
-        # values: dense gradient only when the table is differentiated (sparse_grad=False)
-        dv = None
-        if ctx.needs_input_grad[3] and not opts["sparse_grad"]:
-            N = pool.pool_size
-            sl = res["slots"].long()
-            if opts["shuffle_reads"]:
-                sl = (sl + N // 2 + 1) % N
-            from .rows import merge_fetches
-            m = merge_fetches(sl.to(torch.int32), res["weights"], g_out, N)
-            dv_ext = torch.zeros((N + 1, d), dtype=torch.float32, device=dev)
-            dv_ext.index_copy_(0, m.uniq.long(), m.rows)  # padding rows (all zero) land on row N
-            dv = dv_ext[:N].to(values.dtype)
+    # dense over n on MFMA tiles of the scoring precision: the balance
+    # loss (memory.py:208-213) together with the routed sub-key term.
+    # Without the balance term, fp32 scoring takes the routed term alone
+    # from a sort-by-key segmented sum (O(M k) instead of O(M n)).
+    dq_extra = dlen_extra = dlogt_extra = None
+    btg = pool.balance_temperature_grad
+    raw_keys = sub_keys.detach().float().contiguous()
+    dk = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+    bal = g_balance is not None and "_state" in internal
+    code = res["score_code"]
+    dense = M > 0 and (code == MPL_F16 or bal)
+    if dense:
+        dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+        gb = None
+        if bal:
+            dq_extra = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
+            dlen_extra = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if (btg and q_len is not None) else None
+            dlogt_extra = torch.empty(1, dtype=torch.float32, device=dev) if btg else None
+            gb = g_balance.reshape(1).float().contiguous()
+        wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half, code)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+        check(L.mpl_lookup_bwd_dense(ptr(q_hat), ptr(q_len), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
+                                     ptr(d_sub), ptr(internal["_counts"]) if bal else None,
+                                     ptr(internal["_state"]) if bal else None, ptr(gb), int(btg),
+                                     int(bool(pool.query_scale)), M, H, n, half, k, code, ptr(T), ptr(ws), wsb,
+                                     ptr(dq_extra), ptr(dk_hat), ptr(dlen_extra), ptr(dlogt_extra), stream),
+              "mpl_lookup_bwd_dense")
+        check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
+                                     stream), "mpl_l2_normalize_bwd")
 
-        return (dq.reshape(q_shape).to(q_dtype), dk.to(k_dtype), dlt.reshape(()).to(t_dtype), dv, None, None)
+    # queries
+    dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
+    check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
+                                   ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
+                                   ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
+    # sub-keys (fp32 scoring without the balance term, or no tokens):
+    # sort-by-key segmented sum
+    if not dense:
+        wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
+                                    None, M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
+              "mpl_lookup_bwd_keys")
+    # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
+    dlt = torch.empty(1, dtype=torch.float32, device=dev)
+    check(L.mpl_sum(ptr(dlogt_part), M, ptr(dlogt_extra), ptr(dlt), stream), "mpl_sum")
+
+    # values: dense gradient only when the table is differentiated (sparse_grad=False)
+    dv = None
+    if need_dv:
+        N = pool.pool_size
+        sl = res["slots"].long()
+        if shuffle_reads:
+            sl = (sl + N // 2 + 1) % N
+        from .rows import merge_fetches
+        m = merge_fetches(sl.to(torch.int32), res["weights"], g_out, N)
+        dv_ext = torch.zeros((N + 1, d), dtype=torch.float32, device=dev)
+        dv_ext.index_copy_(0, m.uniq.long(), m.rows)  # padding rows (all zero) land on row N
+        dv = dv_ext[:N].to(values.dtype)
+
+    return dq.reshape(q_shape).to(q_dtype), dk.to(k_dtype), dlt.reshape(()).to(t_dtype), dv
 
 
 def _lookup_with_grad(pool, params, queries, *, train, sparse_grad, noise_scale, shuffle_reads, rngs):
