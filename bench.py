@@ -482,11 +482,33 @@ def train_step_bench(torch, iters):
     b.record()
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / iters
+
+    # The same step without torch autograd (MemoryPool.forward_backward and
+    # key_diversity_value_and_grad; the projection's gradient as a product),
+    # captured in one HIP graph and replayed.
+    from model_amd.memory import key_diversity_value_and_grad
+    g_bal = torch.full((), 0.01, device=dev)
+    g_div = torch.full((), 0.01, device=dev)
+
+    def step_graph(_i):
+        with torch.no_grad():
+            q = (hidden @ w_q).reshape(M, H, d_key)
+            out, aux, (dq, dk, dlt) = pool.forward_backward({"params": params}, q, g_out, g_bal, train=True)
+            _, dk_div = key_diversity_value_and_grad(keys, g_div)
+            gk = dk + dk_div
+            gw = hidden.t() @ dq.reshape(M, H * d_key)
+            rest = (gw.square().sum() + gk.square().sum() + dlt.square()).reshape(1)
+            upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest)
+
+    ms_graph = time_loop(torch, step_graph, iters, 3)
     return {"workload": "training step of the text-study layer: 8,192 tokens, 262,144 fp16 slots + fp32 master, "
                         "forward with Gumbel routing noise + backward (queries through a 256->1024 projection, "
                         "sub-keys, log-temperature, "
                         "balance loss 0.01, key diversity loss 0.01, probe gradient) + sparse row-wise Adagrad",
-            "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events"}
+            "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events",
+            "graph_ms_per_step": ms_graph, "graph_tokens_per_s": M / (ms_graph * 1e-3),
+            "graph_timing": "the same step through MemoryPool.forward_backward (no torch autograd), "
+                            f"{iters} steps captured in one HIP graph and replayed between HIP events"}
 
 
 def fact_task_bench(torch, iters):

@@ -437,6 +437,38 @@ def _fp16_gram_ok(half: int) -> bool:
     return half % 8 == 0 and half <= 128
 
 
+def _key_diversity_fwd(sub_keys: torch.Tensor, code: int, need_grad: bool):
+    """memory.py:230-240 on MFMA Gram tiles (mpl_key_diversity): the loss
+    [1], the fp32 keys and, with need_grad, d loss / d k_hat (formed in the
+    same pass over the Gram tiles)."""
+    H, C, n, half = sub_keys.shape
+    dev = sub_keys.device
+    L = _lib.lib()
+    stream = _lib.stream_ptr(dev)
+    src = sub_keys.detach().float().contiguous()
+    k_hat = torch.empty_like(src)
+    packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, code), dtype=torch.uint8, device=dev)
+    check(L.mpl_pack_keys(ptr(src), H, n, half, code, ptr(k_hat), ptr(packed), stream), "mpl_pack_keys")
+    wsb = L.mpl_key_diversity_workspace_bytes(H, n, half, code)
+    ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+    loss = torch.empty(1, dtype=torch.float32, device=dev)
+    dk = torch.empty_like(src) if need_grad else None
+    check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, code, ptr(ws), wsb, ptr(loss), ptr(dk), stream),
+          "mpl_key_diversity")
+    return loss, src, dk
+
+
+def _key_diversity_bwd(src: torch.Tensor, dk: torch.Tensor, g: torch.Tensor) -> torch.Tensor:
+    """The l2-normalisation backward (mpl_l2_normalize_bwd) of d k_hat scaled
+    by the upstream gradient g (a device scalar): d loss / d sub_keys, fp32."""
+    H, C, n, half = src.shape
+    dx = torch.empty_like(src)
+    gs = g.reshape(1).float().contiguous()
+    check(_lib.lib().mpl_l2_normalize_bwd(ptr(src), ptr(dk), H * C * n, half, NORM_EPS, ptr(gs), ptr(dx),
+                                          _lib.stream_ptr(src.device)), "mpl_l2_normalize_bwd")
+    return dx
+
+
 class _KeyDiversity(torch.autograd.Function):
     """memory.py:230-240 on MFMA Gram tiles (mpl_key_diversity) in fp16 or
     fp32; the gradient with respect to the normalised keys is formed in the
@@ -446,20 +478,7 @@ class _KeyDiversity(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, sub_keys, code):
-        H, C, n, half = sub_keys.shape
-        dev = sub_keys.device
-        L = _lib.lib()
-        stream = _lib.stream_ptr(dev)
-        src = sub_keys.detach().float().contiguous()
-        k_hat = torch.empty_like(src)
-        packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, code), dtype=torch.uint8, device=dev)
-        check(L.mpl_pack_keys(ptr(src), H, n, half, code, ptr(k_hat), ptr(packed), stream), "mpl_pack_keys")
-        wsb = L.mpl_key_diversity_workspace_bytes(H, n, half, code)
-        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
-        loss = torch.empty(1, dtype=torch.float32, device=dev)
-        dk = torch.empty_like(src) if ctx.needs_input_grad[0] else None
-        check(L.mpl_key_diversity(ptr(k_hat), ptr(packed), H, n, half, code, ptr(ws), wsb, ptr(loss), ptr(dk),
-                                  stream), "mpl_key_diversity")
+        loss, src, dk = _key_diversity_fwd(sub_keys, code, ctx.needs_input_grad[0])
         ctx.save_for_backward(src, dk)
         ctx.dtype = sub_keys.dtype
         return loss.reshape(())
@@ -467,12 +486,19 @@ class _KeyDiversity(torch.autograd.Function):
     @staticmethod
     def backward(ctx, g):
         src, dk = ctx.saved_tensors
-        H, C, n, half = src.shape
-        dx = torch.empty_like(src)
-        gs = g.reshape(1).float().contiguous()
-        check(_lib.lib().mpl_l2_normalize_bwd(ptr(src), ptr(dk), H * C * n, half, NORM_EPS, ptr(gs), ptr(dx),
-                                              _lib.stream_ptr(src.device)), "mpl_l2_normalize_bwd")
-        return dx.to(ctx.dtype), None
+        return _key_diversity_bwd(src, dk, g).to(ctx.dtype), None
+
+
+def _key_diversity_code(sub_keys: torch.Tensor, score_dtype: Optional[torch.dtype]) -> int:
+    if sub_keys.device.type != "cuda":
+        raise RuntimeError("key_diversity_loss runs on the GPU only (libmpl.so)")
+    H, C, n, half = sub_keys.shape
+    if score_dtype is None:
+        score_dtype = torch.float16 if _fp16_gram_ok(half) else torch.float32
+    if half > 128 or (score_dtype == torch.float16 and not _fp16_gram_ok(half)):
+        raise ValueError(f"key_diversity_loss: no {score_dtype} Gram kernel for sub-key width {half} "
+                         "(fp16: multiples of 8 up to 128; fp32: up to 128)")
+    return _dtype_code(score_dtype)
 
 
 def key_diversity_loss(sub_keys: torch.Tensor, score_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
@@ -482,15 +508,17 @@ def key_diversity_loss(sub_keys: torch.Tensor, score_dtype: Optional[torch.dtype
     are multiples of 8, up to 128) or fp32 (any width up to 128, the
     reference's precision).  By default fp16 where it applies, else fp32; a
     pool passes its own scoring precision (``MemoryPool.score_dtype``)."""
-    if sub_keys.device.type != "cuda":
-        raise RuntimeError("key_diversity_loss runs on the GPU only (libmpl.so)")
-    H, C, n, half = sub_keys.shape
-    if score_dtype is None:
-        score_dtype = torch.float16 if _fp16_gram_ok(half) else torch.float32
-    if half > 128 or (score_dtype == torch.float16 and not _fp16_gram_ok(half)):
-        raise ValueError(f"key_diversity_loss: no {score_dtype} Gram kernel for sub-key width {half} "
-                         "(fp16: multiples of 8 up to 128; fp32: up to 128)")
-    return _KeyDiversity.apply(sub_keys, _dtype_code(score_dtype))
+    return _KeyDiversity.apply(sub_keys, _key_diversity_code(sub_keys, score_dtype))
+
+
+def key_diversity_value_and_grad(sub_keys: torch.Tensor, g: torch.Tensor,
+                                 score_dtype: Optional[torch.dtype] = None):
+    """key_diversity_loss and its gradient with respect to ``sub_keys`` for
+    the upstream gradient ``g`` (a device scalar), without torch autograd:
+    (loss [], d sub_keys).  The same kernels as key_diversity_loss + autograd,
+    for training steps captured in a HIP graph."""
+    loss, src, dk = _key_diversity_fwd(sub_keys, _key_diversity_code(sub_keys, score_dtype), True)
+    return loss.reshape(()), _key_diversity_bwd(src, dk, g).to(sub_keys.dtype)
 
 
 def revive_dead_keys(sub_keys: torch.Tensor, subkey_usage: torch.Tensor, queries: torch.Tensor, rng,

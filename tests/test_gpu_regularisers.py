@@ -72,6 +72,20 @@ def test_key_diversity_collapsed_codebook_is_one(gpu_lib):
     assert float(g.abs().max()) <= 1e-2 * float(d.abs().max()) / float(d.norm())
 
 
+@pytest.mark.parametrize("score_dtype", [torch.float16, torch.float32])
+def test_key_diversity_value_and_grad_equals_autograd(gpu_lib, score_dtype):
+    """key_diversity_value_and_grad (no torch autograd, for captured training
+    steps) runs the same kernels as key_diversity_loss + autograd: equal bit
+    for bit, loss and gradient, for an upstream gradient of 0.01."""
+    raw = torch.randn((2, 2, 256, 64), device="cuda").requires_grad_(True)
+    g = torch.full((), 0.01, device="cuda")
+    loss = mem.key_diversity_loss(raw, score_dtype)
+    (ga,) = torch.autograd.grad(loss, [raw], grad_outputs=[g])
+    lm, gm = mem.key_diversity_value_and_grad(raw, g, score_dtype)
+    assert torch.equal(loss.detach(), lm)
+    assert gm.dtype == ga.dtype and torch.equal(ga, gm)
+
+
 def test_key_diversity_without_grad(gpu_lib):
     raw = torch.randn((1, 2, 96, 32), device="cuda")
     with torch.no_grad():
