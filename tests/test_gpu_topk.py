@@ -102,3 +102,56 @@ def test_topk_equals_select_stage1(gpu_lib, M, H, n, d_key, k, score, noise):
     np.testing.assert_array_equal(np.sort(got_ids, -1), np.sort(want[free], -1))
     clean = np.take_along_axis((cos * T)[free], got_ids.astype(np.int64), -1)
     np.testing.assert_allclose(outs["topk"][1][free], clean, rtol=0, atol=2.0 ** -11 * T)
+
+
+@pytest.mark.parametrize("M", [16, 4096])
+def test_repeated_keys_tie_by_index_across_flushes(gpu_lib, M):
+    """Exact ties through the select pass's flushes at the 67M-slot key width
+    (n = 8,192): each codebook holds 16 distinct key vectors, each repeated
+    512 times at random places, so a query's best score is reached by 512
+    keys at once and the lane buffers overflow many times.  The top 16 are
+    then the 16 lowest indices holding the best vector (lax.top_k's order,
+    memory.py:34-57), which a flush threshold taken from both lanes of the
+    query must keep: a later key that ties the k-th best loses on its larger
+    index.  Checked on rows whose best and second-best distinct vectors are
+    apart by more than the fp16-scoring error."""
+    L = _lib.lib()
+    H, n, half, k, nv = 1, 8192, 128, 16, 16
+    rng = np.random.default_rng(11)
+    base = rng.standard_normal((H, 2, nv, half))
+    assign = np.stack([np.stack([rng.permutation(n) % nv for _ in range(2)]) for _ in range(H)])  # [H, 2, n]
+    keys_np = np.take_along_axis(base, assign[..., None], axis=2)  # [H, 2, n, half]
+    q_np = rng.standard_normal((M, H, 2, half))
+    keys = torch.tensor(keys_np, dtype=torch.float32, device="cuda")
+    q = torch.tensor(q_np, dtype=torch.float32, device="cuda")
+    score = _lib.MPL_F16
+    packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, score), dtype=torch.uint8, device="cuda")
+    khat = torch.empty_like(keys)
+    st = _lib.stream_ptr(q.device)
+    _lib.check(L.mpl_pack_keys(_lib.ptr(keys), H, n, half, score, _lib.ptr(khat), _lib.ptr(packed), st), "pack")
+    T_dev = torch.full((1,), 10.0, device="cuda")
+    wsb = L.mpl_score_topk_workspace_bytes(M, H, n, half, k)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    sub_idx = torch.full((M, H, 2, k), -7, dtype=torch.int32, device="cuda")
+    sub_sc = torch.empty((M, H, 2, k), dtype=torch.float32, device="cuda")
+    _lib.check(L.mpl_score_topk(_lib.ptr(q), _lib.MPL_Q_RAW, None, _lib.ptr(packed), M, H, n, half, k, score,
+                                _lib.ptr(T_dev), None, None, _lib.ptr(ws), wsb, _lib.ptr(sub_idx), _lib.ptr(sub_sc),
+                                st), "topk")
+    got = sub_idx.cpu().numpy()
+    sc = sub_sc.cpu().numpy()
+    # fp64 cosine of each query with each distinct vector
+    qn = q_np / np.linalg.norm(q_np, axis=-1, keepdims=True)
+    bn = base / np.linalg.norm(base, axis=-1, keepdims=True)
+    cos = np.einsum("mhcd,hcvd->mhcv", qn, bn)
+    order = np.argsort(-cos, axis=-1)
+    best = order[..., 0]
+    srt = np.take_along_axis(cos, order, -1)
+    free = (srt[..., 0] - srt[..., 1]) > 2.5 * 2.0 ** -11
+    assert free.mean() > 0.5
+    checked = 0
+    for m, h, c in zip(*np.nonzero(free)):
+        want = np.nonzero(assign[h, c] == best[m, h, c])[0][:k]
+        np.testing.assert_array_equal(got[m, h, c], want, err_msg=f"row {m} head {h} codebook {c}")
+        assert np.all(sc[m, h, c] == sc[m, h, c, 0])  # one exact score for every copy
+        checked += 1
+    assert checked >= 1
