@@ -699,6 +699,22 @@ def host_pool_file_bench(torch, iters):
 
         warm = timed(lambda: pool.stage(lk.slots), iters)
         cold = timed(lambda: pool.stage(lk.slots), 3, before=pool.evict_page_cache)
+        # the same reads with O_DIRECT (no page cache: every row from the
+        # drive), for the whole batch and for a decode-sized one (64 tokens)
+        direct = {}
+        ddir = hp.HostPool(N, d, path=tmp, dtype=np.float16, trainable=False, direct_io=True,
+                           name="bench-direct") if pool._arrays["values"].direct_supported else None
+        dec = lk.slots[:64]
+        _, _, num_dec = pool.stage(dec)
+        torch.cuda.synchronize()
+        U_dec = int(num_dec.item())
+        direct["decode_unique_rows"] = U_dec
+        direct["decode_stage_warm_ms"] = timed(lambda: pool.stage(dec), iters)
+        if ddir is not None:
+            direct["stage_direct_ms"] = timed(lambda: ddir.stage(lk.slots), 3)
+            direct["stage_direct_row_GBs"] = U * d * 2 / (direct["stage_direct_ms"] * 1e-3) / 1e9
+            direct["decode_stage_direct_ms"] = timed(lambda: ddir.stage(dec), iters)
+            ddir.close()
         uniq = torch.unique(lk.slots.reshape(-1)).to(torch.int32)
         grads = torch.randn((uniq.numel(), d), device="cuda") * 1e-3
         upd = timed(lambda: pool.update(uniq, grads, 1, 1e-3), max(3, iters // 2))
@@ -713,7 +729,10 @@ def host_pool_file_bench(torch, iters):
             "update_ms": upd, "update_rows_per_s": uniq.numel() / (upd * 1e-3),
             "note": "evict_page_cache is advisory (posix_fadvise DONTNEED); where the file system keeps the "
                     "pages (e.g. tmpfs) the 'after evict' read is a page-cache read too",
-            "io_threads": hp._IO_THREADS, "dir": os.path.dirname(tmp)}
+            "direct_io": direct if ddir is not None else dict(direct, unsupported="O_DIRECT refused here"),
+            "direct_note": "direct_io reads 4 KiB-aligned spans around the rows with O_DIRECT (no page cache); "
+                           "decode_*: the unique rows of the first 64 tokens (4 heads x 16 rows each)",
+            "io_threads": hp._IO_THREADS, "direct_io_threads": hp._DIRECT_THREADS, "dir": os.path.dirname(tmp)}
 
 
 def generation_bench(torch):

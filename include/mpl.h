@@ -144,6 +144,15 @@ int mpl_lookup(const void* queries, int query_mode, float* q_len, const void* pa
 int mpl_rowfile_open(const char* path, int64_t data_offset, int64_t row_bytes, int64_t rows, int writable,
                      void** handle);
 int mpl_rowfile_read(void* handle, const int64_t* ids, int64_t count, void* dst, int threads);
+/* The reads of host_pool.py:117-127 (HostPool.gather of a file-backed pool)
+ * without the page cache: as mpl_rowfile_read, through a descriptor of the
+ * file opened with O_DIRECT; each thread reads the 4 KiB-aligned spans around
+ * its rows (neighbouring spans merged into reads of up to 1 MiB) and copies
+ * the rows out, so rows come from the drive and nothing stays cached.
+ * MPL_EUNSUPPORTED where the file system refuses O_DIRECT (tmpfs);
+ * mpl_rowfile_direct_supported tells beforehand (1 or 0). */
+int mpl_rowfile_read_direct(void* handle, const int64_t* ids, int64_t count, void* dst, int threads);
+int mpl_rowfile_direct_supported(void* handle);
 int mpl_rowfile_write(void* handle, const int64_t* ids, int64_t count, const void* src, int threads);
 int mpl_rowfile_sync(void* handle);
 /* host_pool.py:190-204: writes the file's dirty rows back, then asks the OS to

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libmpl.so")
 
 MPL_F32, MPL_F16 = 0, 1
+MPL_OK, MPL_EINVAL, MPL_EHIP, MPL_EWORKSPACE, MPL_EUNSUPPORTED = 0, 1, 2, 3, 4  # include/mpl.h status codes
 MPL_Q_NORMALIZED, MPL_Q_RAW, MPL_Q_RAW_SCALED = 0, 1, 2
 MPL_ACT_NONE, MPL_ACT_GELU_TANH, MPL_ACT_SILU = 0, 1, 2
 MPL_W_IN_OUT, MPL_W_OUT_IN = 0, 1
@@ -34,6 +35,8 @@ SIGNATURES = {
                         _P, _P, _P, _P, _P, _P, _I, _I, _I, _P, _P]),
     "mpl_rowfile_open": (_I, [C.c_char_p, _I64, _I64, _I64, _I, C.POINTER(C.c_void_p)]),
     "mpl_rowfile_read": (_I, [_P, _P, _I64, _P, _I]),
+    "mpl_rowfile_read_direct": (_I, [_P, _P, _I64, _P, _I]),
+    "mpl_rowfile_direct_supported": (_I, [_P]),
     "mpl_rowfile_write": (_I, [_P, _P, _I64, _P, _I]),
     "mpl_rowfile_sync": (_I, [_P]),
     "mpl_rowfile_evict": (_I, [_P]),

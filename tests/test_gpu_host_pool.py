@@ -103,11 +103,12 @@ def test_host_device_pointer_rejects_pageable_memory(gpu_lib):
     assert rc != 0 and b"not pinned" in _lib.lib().mpl_last_error()
 
 
-@pytest.mark.parametrize("mode,dtype", [("ram", np.float32), ("ram", np.float16), ("memmap", np.float16)])
+@pytest.mark.parametrize("mode,dtype", [("ram", np.float32), ("ram", np.float16), ("memmap", np.float16),
+                                        ("direct", np.float16)])
 def test_fetch_matches_take(gpu_lib, tmp_path, mode, dtype):
     N, d = 4096, 32
     pool = hp.HostPool(N, d, path=None if mode == "ram" else str(tmp_path / "pool"), dtype=dtype, seed=5,
-                       trainable=False)
+                       trainable=False, direct_io=mode == "direct")
     slots = torch.as_tensor(zipf_slots(50, 4, 16, N).astype(np.int32), device="cuda")
     got = hp.fetch(pool.name, slots, d)
     torch.cuda.synchronize()

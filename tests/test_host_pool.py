@@ -65,6 +65,19 @@ def test_gather_clips_and_converts(tmp_path):
     assert pool.pop_gather_seconds() > 0 and pool.pop_gather_seconds() == 0
 
 
+def test_gather_direct_io_equals_mapped(tmp_path):
+    """A file-mode pool with direct_io reads its rows with O_DIRECT (no page
+    cache): the same rows as the mapped reads."""
+    mapped = HostPool(3000, 40, path=str(tmp_path / "d"), dtype=np.float16, trainable=False, seed=7)
+    if not mapped._arrays["values"].direct_supported:
+        with pytest.raises(OSError):
+            HostPool(3000, 40, path=str(tmp_path / "d"), dtype=np.float16, trainable=False, direct_io=True)
+        pytest.skip("this file system refuses O_DIRECT")
+    direct = HostPool(3000, 40, path=str(tmp_path / "d"), dtype=np.float16, trainable=False, direct_io=True)
+    idx = np.concatenate([np.unique(np.random.default_rng(1).integers(0, 3000, 900)), [2999, 0, 17]])
+    np.testing.assert_array_equal(direct.gather(idx), mapped.gather(idx))
+
+
 def test_save_load_roundtrip(tmp_path):
     a = HostPool(40, 4, path=str(tmp_path / "x"), optimizer="adam", seed=2)
     a.values[5] = 3.0
@@ -120,6 +133,65 @@ def test_rowfile_read_matches_numpy(tmp_path, dtype, d):
         assert b"outside" in L.mpl_last_error() and not out.any()
         # a read-only file refuses writes
         assert L.mpl_rowfile_write(h, ids.ctypes.data, 1, out.ctypes.data, 1) != 0
+    finally:
+        L.mpl_rowfile_close(h)
+
+
+@pytest.mark.parametrize("dtype,d,N", [(np.float16, 256, 5000), (np.float32, 3, 5000), (np.float32, 64, 5000),
+                                       (np.float32, 1500, 900)])
+def test_rowfile_read_direct_matches_numpy(tmp_path, dtype, d, N):
+    """O_DIRECT reads (no page cache) return the rows numpy reads: sorted
+    unique ids (the host tier's lookups), ids out of order and repeated, a
+    long consecutive run (spans merged up to 1 MiB), rows that cross 4 KiB
+    blocks (the .npy header shifts the rows), rows larger than a block
+    (d = 1500 fp32: 6,000 bytes), and the last row of the file, whose span
+    ends past the end of the file."""
+    rng = np.random.default_rng(d + N)
+    arr = rng.standard_normal((N, d)).astype(dtype)
+    f, off = _npy(tmp_path, arr)
+    row_bytes = d * np.dtype(dtype).itemsize
+    h = _open(f, off, row_bytes, N, 0)
+    L = _lib.lib()
+    try:
+        if not L.mpl_rowfile_direct_supported(h):
+            ids = np.arange(3, dtype=np.int64)
+            out = np.zeros((3, d), dtype)
+            assert L.mpl_rowfile_read_direct(h, ids.ctypes.data, 3, out.ctypes.data, 1) == _lib.MPL_EUNSUPPORTED
+            pytest.skip("this file system refuses O_DIRECT")
+        uniq = np.unique(rng.integers(0, N, N // 3)).astype(np.int64)
+        mixed = np.concatenate([rng.integers(0, N, 700), np.arange(100, 600), [0, N - 1, N - 1, 5, 4]])
+        for ids in (uniq, mixed.astype(np.int64), np.array([N - 1], np.int64)):
+            for threads in (1, 7):
+                out = np.full((ids.size, d), 9, dtype)
+                _lib.check(L.mpl_rowfile_read_direct(h, ids.ctypes.data, ids.size, out.ctypes.data, threads),
+                           "read_direct")
+                np.testing.assert_array_equal(out, arr[ids])
+        bad = np.array([3, -1], dtype=np.int64)
+        out = np.zeros((2, d), dtype)
+        assert L.mpl_rowfile_read_direct(h, bad.ctypes.data, 2, out.ctypes.data, 1) != 0
+        assert b"outside" in L.mpl_last_error() and not out.any()
+    finally:
+        L.mpl_rowfile_close(h)
+
+
+def test_rowfile_read_direct_sees_rows_written_through_the_mapping(tmp_path):
+    """Rows written through the shared mapping and not yet synced are what a
+    direct read returns (the kernel writes the dirty range back first)."""
+    rng = np.random.default_rng(4)
+    N, d = 4000, 64
+    arr = rng.standard_normal((N, d)).astype(np.float32)
+    f, off = _npy(tmp_path, arr)
+    h = _open(f, off, d * 4, N)
+    L = _lib.lib()
+    try:
+        if not L.mpl_rowfile_direct_supported(h):
+            pytest.skip("this file system refuses O_DIRECT")
+        ids = np.unique(rng.integers(0, N, 500)).astype(np.int64)
+        new = rng.standard_normal((ids.size, d)).astype(np.float32)
+        _lib.check(L.mpl_rowfile_write(h, ids.ctypes.data, ids.size, new.ctypes.data, 4), "write")
+        out = np.zeros_like(new)
+        _lib.check(L.mpl_rowfile_read_direct(h, ids.ctypes.data, ids.size, out.ctypes.data, 4), "read_direct")
+        np.testing.assert_array_equal(out, new)
     finally:
         L.mpl_rowfile_close(h)
 
