@@ -484,6 +484,23 @@ int mpl_decode_attention(const float* qkv, int64_t batch, int heads, int head_di
                          void* stream);
 
 /*
+ * The greedy generator's token step (generate.py:44-61) on the GPU, so that
+ * a decode step and its token choice replay as one HIP graph.  For each of
+ * `rows` streams, with p = *position and P = *prompt_len (device int64
+ * scalars): the next token is prompt[b, p + 1] while p + 1 < P (prompt
+ * [rows, prompt_stride] int64, P <= prompt_stride), else the first index of
+ * the maximum of logits[b, 0..vocab) (fp32; NaN counts as the maximum, as
+ * torch.argmax); it is written to token[b], and generated tokens to
+ * out[b, p + 1 - P] (out [rows, out_stride] int64, indices >= out_cap
+ * dropped).  Then *position becomes p + 1.  `done` is a device uint32 that
+ * must be 0 before the first call; each call leaves it 0.  Calls on one
+ * `done` must not overlap.
+ */
+int mpl_decode_next_token(const float* logits, int64_t rows, int64_t vocab, const int64_t* prompt,
+                          int64_t prompt_stride, const int64_t* prompt_len, int64_t* position, int64_t* token,
+                          int64_t* out, int64_t out_stride, int64_t out_cap, uint32_t* done, void* stream);
+
+/*
  * A dense layer of the backbone over a few rows (model.py:29-127: the
  * query/key/value, output, feed-forward, router, gate and mem_out products
  * and embed.attend), with its neighbours fused in:

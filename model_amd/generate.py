@@ -5,7 +5,10 @@ the backbone with its memory reads (MemoryPool: libmpl.so).  The decode step
 has static shapes (token batch [B], position as a device tensor), so it is
 captured once in a HIP graph and replayed; the next input token (the prompt's
 or the argmax of the step's logits) is chosen on the device, so a whole
-generation is queued without a host round trip per token.  The reference's
+generation is queued without a host round trip per token.  For greedy
+decoding a second graph also holds that choice (mpl_decode_next_token: the
+prompt feed or the argmax, the output write and the position advance), so a
+step is one replay with no other launch.  The reference's
 jitted step takes the parameters on every call; here a generate() call
 re-captures the step when a parameter was replaced, or when one that the
 step reads through a copy made before capture (the pool's sub-keys and
@@ -35,8 +38,17 @@ class Generator:
         self.cache = self.model.init_cache(batch_size, self.device)
         self.tok = torch.zeros(batch_size, dtype=torch.int64, device=self.device)
         self.pos = torch.zeros(1, dtype=torch.int64, device=self.device)
+        # the greedy graph's token step: prompt, its length and the generated
+        # tokens stay on the device ([B, max_len] each)
+        L = mcfg.max_len
+        self.prompt_buf = torch.zeros((batch_size, L), dtype=torch.int64, device=self.device)
+        self.out_buf = torch.zeros((batch_size, L), dtype=torch.int64, device=self.device)
+        self.plen = torch.zeros(1, dtype=torch.int64, device=self.device)
+        self.done = torch.zeros(1, dtype=torch.int32, device=self.device)  # the kernel's count, left at 0
         self.logits = None
         self.graph = None
+        self.graph_greedy = None
+        self.logits_greedy = None
         self._captured_state = None
         self.use_graph = graph
 
@@ -54,6 +66,20 @@ class Generator:
         finally:
             torch.backends.cuda.preferred_blas_library(prev)
         return logits[:, 0]
+
+    def _next_token(self, logits):
+        """generate.py:44-61 for greedy decoding on the device: the next prompt
+        token or the argmax of ``logits`` into self.tok, generated tokens into
+        self.out_buf, then the position advanced (mpl_decode_next_token)."""
+        from . import _lib
+
+        lg = logits.float().contiguous()
+        B, V = lg.shape
+        P = _lib.ptr
+        _lib.check(_lib.lib().mpl_decode_next_token(
+            P(lg), B, V, P(self.prompt_buf), self.prompt_buf.shape[1], P(self.plen), P(self.pos), P(self.tok),
+            P(self.out_buf), self.out_buf.shape[1], self.out_buf.shape[1], P(self.done),
+            _lib.stream_ptr(self.device)), "mpl_decode_next_token")
 
     def _reset_cache(self):
         for c in self.cache:
@@ -88,7 +114,7 @@ class Generator:
         state = self._param_state()
         if self.graph is not None and state == self._captured_state:
             return
-        self.graph = None  # parameters moved or the pool's keys changed: capture again
+        self.graph = self.graph_greedy = None  # parameters moved or the pool's keys changed: capture again
         # warm up on a side stream (key packing, temperature, workspaces)
         side = torch.cuda.Stream(self.device)
         side.wait_stream(torch.cuda.current_stream(self.device))
@@ -104,6 +130,12 @@ class Generator:
             self.graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph):
                 self.logits = self._step()
+            # the greedy step: the same decode step, then the token choice
+            # (the position it advances is reset by every generate())
+            self.graph_greedy = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.graph_greedy):
+                self.logits_greedy = self._step()
+                self._next_token(self.logits_greedy)
         finally:
             if pool is not None:
                 pool.frozen_under_capture = False
@@ -130,6 +162,8 @@ class Generator:
         B, P = prompt.shape
         self._ensure_graph()
         self._reset_cache()
+        if temperature <= 0 and self.graph_greedy is not None:
+            return self._generate_greedy_graph(prompt, n_new, keep_logits, sync_each_step)
         gen = torch.Generator(device=self.device).manual_seed(int(seed)) if temperature > 0 else None
         out, logits_all, times = [], [], []
         self.tok.copy_(prompt[:, 0])
@@ -156,6 +190,28 @@ class Generator:
                 torch.cuda.synchronize(self.device)
                 times.append(time.perf_counter() - t0)
         toks = torch.stack(out, 1) if out else torch.zeros((B, 0), dtype=torch.int64, device=self.device)
+        return {"tokens": toks,
+                "logits": torch.stack(logits_all, 1) if keep_logits else None,
+                "step_seconds": np.array(times)}
+
+    def _generate_greedy_graph(self, prompt, n_new, keep_logits, sync_each_step):
+        """Greedy generation as replays of the greedy graph alone: prompt,
+        position, input token and generated tokens live on the device."""
+        B, P = prompt.shape
+        self.prompt_buf[:, :P].copy_(prompt)
+        self.plen.fill_(P)
+        self.pos.fill_(0)
+        self.tok.copy_(prompt[:, 0])
+        logits_all, times = [], []
+        for _ in range(P + n_new - 1):
+            t0 = time.perf_counter()
+            self.graph_greedy.replay()
+            if keep_logits:
+                logits_all.append(self.logits_greedy.clone())
+            if sync_each_step:
+                torch.cuda.synchronize(self.device)
+                times.append(time.perf_counter() - t0)
+        toks = self.out_buf[:, :n_new].clone()
         return {"tokens": toks,
                 "logits": torch.stack(logits_all, 1) if keep_logits else None,
                 "step_seconds": np.array(times)}

@@ -104,3 +104,41 @@ def test_generator_follows_attention_weights_changed_in_place(gpu_lib):
     eager = Generator(cfg, params, batch_size=3, graph=False).generate(prompt, n_new=6)
     assert torch.equal(after["logits"], eager["logits"])
     assert not torch.equal(after["logits"], before["logits"])
+
+
+@pytest.mark.parametrize("V", [1000, 999, 16384])
+def test_next_token_kernel_matches_torch(gpu_lib, V):
+    """mpl_decode_next_token (the greedy graph's token step, generate.py:44-61):
+    the prompt's next token while it lasts, then torch.argmax of the logits
+    (first maximal index, ties and NaN included, all -inf gives 0), the
+    generated tokens written in order, and the position advanced by one per
+    call with the workgroup count left at 0."""
+    from model_amd import _lib
+
+    B, Lmax, P = 7, 12, 3
+    g = torch.Generator(device="cuda").manual_seed(9)
+    prompt = torch.randint(0, V, (B, Lmax), generator=g, device="cuda")
+    plen = torch.full((1,), P, dtype=torch.int64, device="cuda")
+    pos = torch.zeros(1, dtype=torch.int64, device="cuda")
+    tok = torch.zeros(B, dtype=torch.int64, device="cuda")
+    out = torch.full((B, Lmax), -1, dtype=torch.int64, device="cuda")
+    done = torch.zeros(1, dtype=torch.int32, device="cuda")
+    want_out = []
+    for step in range(8):
+        logits = torch.randn((B, V), generator=g, device="cuda")
+        logits[0, 17] = logits[0, V - 90] = 50.0  # a tie: the first index wins
+        logits[1, :] = 3.0  # all equal: index 0
+        logits[2, 555] = float("nan")  # NaN counts as the maximum
+        logits[3, :] = float("-inf")  # nothing above -inf: index 0
+        logits[4, V - 1] = 99.0  # the last element
+        _lib.check(_lib.lib().mpl_decode_next_token(
+            _lib.ptr(logits), B, V, _lib.ptr(prompt), Lmax, _lib.ptr(plen), _lib.ptr(pos), _lib.ptr(tok),
+            _lib.ptr(out), Lmax, Lmax, _lib.ptr(done), _lib.stream_ptr(logits.device)), "next_token")
+        want = prompt[:, step + 1] if step + 1 < P else torch.argmax(logits, -1)
+        if step + 1 >= P:
+            want_out.append(want)
+        assert torch.equal(tok, want), step
+        assert int(pos.item()) == step + 1 and int(done.item()) == 0
+    assert torch.equal(out[:, :len(want_out)], torch.stack(want_out, 1))
+    assert bool((out[:, len(want_out):] == -1).all())
+    assert tok[0].item() in (17,) and tok[1].item() == 0 and tok[2].item() == 555 and tok[3].item() == 0
