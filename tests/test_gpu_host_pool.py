@@ -147,6 +147,13 @@ def test_memory_pool_on_host_equals_hbm_table(gpu_lib, shuffle, dtype):
         outs.append(torch.autograd.grad(loss, [qq, keys]))
     for x, y in zip(*outs):
         assert torch.equal(x, y)
+    # the same gradients from forward_backward (no autograd), on the host pool
+    keys = hparams["sub_keys"].detach().clone().requires_grad_(True)
+    g_out = torch.linspace(-1, 1, d, device="cuda").expand(40, d).contiguous()
+    _, _, (gq, gk, _) = host_pool.forward_backward({"params": dict(hparams, sub_keys=keys)}, q, g_out,
+                                                   torch.full((), 0.01, device="cuda"), train=False,
+                                                   shuffle_reads=shuffle)
+    assert torch.equal(gq, outs[1][0]) and torch.equal(gk, outs[1][1])
     with pytest.raises(ValueError):
         host_pool.apply({"params": hparams}, q.clone().requires_grad_(True), sparse_grad=False)
 
