@@ -142,10 +142,14 @@ __device__ __forceinline__ u64 pair_kth_key(const TopList<KMAX, NOISE>& top, int
 // lane's own k-th.  A key still to come that ties it loses on its larger
 // index, so '>' against it keeps every key that can still enter.  Wave-uniform
 // control flow.
+//
+// `empty` (wave-uniform): no flush has filled the list yet, so the first
+// chunk, sorted, is the list's head as it stands (the rest of the list is
+// empty keys) and needs no merge.
 template <bool REFRESH, int KMAX, bool NOISE>
 __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
                                            const float* pay, uint32_t lane0, bool valid, int k, float base_thr,
-                                           int par) {
+                                           int par, bool empty = false) {
   const int cnt = (int)((st.off - lane0) / kEntryBytes);
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
@@ -162,7 +166,15 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
       cp[i] = (NOISE && in) ? lds_at(pay, o) : 0.f;
     }
     sort8<NOISE>(ch, cp);
-    st.top.template merge<8>(ch, cp);
+    if (empty && c0 == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st.top.key[i] = ch[i];
+        if (NOISE) st.top.pay[NOISE ? i : 0] = cp[i];
+      }
+    } else {
+      st.top.template merge<8>(ch, cp);
+    }
   }
   st.off = lane0;
   if (REFRESH) {
@@ -235,6 +247,12 @@ __device__ __forceinline__ float kth_of_pair16(const float* own, int par, int k)
     float a = __uint_as_float(v[15 - i]), b = a;
     half_swap(a, b);  // the partner's entry 15 - i
     t[i] = max(v[i], __float_as_uint(par ? a : b));
+  }
+  if (k == 16) {  // the 16th largest of the 32 is the smallest of the top 16
+    uint32_t m = t[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) m = min(m, t[i]);
+    return from_orderable(m);
   }
 #pragma unroll
   for (int stride = 8; stride >= 1; stride >>= 1) {
@@ -583,14 +601,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   st.top.init();
   st.thr = valid ? base_thr : INFINITY;
   st.off = lane0;
+  bool flushed = false;  // wave-uniform: a flush inside the pass has filled the list
   sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
                             __attribute__((always_inline)) {
     float sv[16];
     lane_scores(kb, c, g, sv);
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      if (active && __ballot(st.off > flush_at) != 0)
+      if (active && __ballot(st.off > flush_at) != 0) {
         flush_lane<true, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
+        flushed = true;
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const int r = 8 * q + e;
@@ -608,7 +629,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       }
     }
   });
-  flush_lane<false, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
+  flush_lane<false, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par, !flushed);
 
   // Merge the two lanes' lists of the query: the partner's sorted list
   // arrives through v_permlane32_swap and is bitonic-merged (keys of the two
