@@ -655,25 +655,45 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   }
 
   if (valid && par == 0) {
-    // Lists [split][M][hc][k]: lane l < 32 writes its query's k entries.
+    // Lists [split][M][hc][k]: lane l < 32 writes its query's k entries,
+    // as 16-byte vectors when k == KMAX and the rows are 16-byte aligned.
     const int64_t o = (((int64_t)split * p.M + my_q) * p.HC + hc) * p.k;
+    float cl[KMAX], se[KMAX];
+    int id[KMAX];
 #pragma unroll
     for (int r = 0; r < KMAX; ++r) {
-      if (r < p.k) {
-        const u64 kk = st.top.key[r];
-        float clean, sel;
-        if (NOISE) {
-          clean = st.top.pay[NOISE ? r : 0];
-          sel = key_score(kk);
-        } else {
-          clean = key_score(kk) * Tv;
-          clean *= ql;  // ql == 1 without query_scale
-          sel = clean;
+      const u64 kk = st.top.key[r];
+      float clean, sel;
+      if (NOISE) {
+        clean = st.top.pay[NOISE ? r : 0];
+        sel = key_score(kk);
+      } else {
+        clean = key_score(kk) * Tv;
+        clean *= ql;  // ql == 1 without query_scale
+        sel = clean;
+      }
+      if (kk == 0) clean = sel = -INFINITY;
+      cl[r] = clean;
+      se[r] = sel;
+      id[r] = kk ? key_index(kk) : -1;
+    }
+    const bool vec = p.k == KMAX && ((uintptr_t)(p.out_clean + o) & 15) == 0 &&
+                     ((uintptr_t)(p.out_idx + o) & 15) == 0 && (!NOISE || ((uintptr_t)(p.out_sel + o) & 15) == 0);
+    if (vec) {
+#pragma unroll
+      for (int r = 0; r < KMAX; r += 4) {
+        *(float4*)(p.out_clean + o + r) = make_float4(cl[r], cl[r + 1], cl[r + 2], cl[r + 3]);
+        *(int4*)(p.out_idx + o + r) = make_int4(id[r], id[r + 1], id[r + 2], id[r + 3]);
+        if (NOISE) *(float4*)(p.out_sel + o + r) = make_float4(se[r], se[r + 1], se[r + 2], se[r + 3]);
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < KMAX; ++r) {
+        if (r < p.k) {
+          if (NOISE) p.out_sel[o + r] = se[r];
+          p.out_clean[o + r] = cl[r];
+          p.out_idx[o + r] = id[r];
         }
-        if (kk == 0) clean = sel = -INFINITY;
-        if (NOISE) p.out_sel[o + r] = sel;
-        p.out_clean[o + r] = clean;
-        p.out_idx[o + r] = kk ? key_index(kk) : -1;
       }
     }
   }
