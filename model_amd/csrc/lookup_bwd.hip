@@ -245,6 +245,95 @@ __global__ __launch_bounds__(kBwdThreads) void queries_bwd_kernel(
   }
 }
 
+// queries_bwd_kernel for half = 128 with 16-byte rows: a 512-byte k-hat row
+// is 32 lanes x 16 B, so one load instruction covers two of the row's
+// entries (2b in lanes 0-31, 2b+1 in lanes 32-63) and a row takes a quarter
+// of the dword form's load instructions (which are what bounds that form:
+// 32 of them per wave, each one address per lane).  Each half-wave sums its
+// entries in order, then the two halves are added.
+__global__ __launch_bounds__(kBwdThreads) void queries_bwd_128_kernel(
+    const float* __restrict__ q, const float* __restrict__ q_len, const float* __restrict__ k_hat,
+    const int32_t* __restrict__ sub_idx, const float* __restrict__ d_sub, const float* __restrict__ sub_scores,
+    const float* __restrict__ extra, const float* __restrict__ dlen_extra, int64_t rows, int HC, int n, int k,
+    const float* __restrict__ Tp, float eps, float* __restrict__ dq) {
+  constexpr int HALF = 128;
+  const int64_t row = ((int64_t)blockIdx.x * kBwdThreads + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  if (row >= rows) return;
+  const int sub = lane >> 5, col = lane & 31;
+  const float T = *Tp;
+  const int hc = (int)(row % HC);
+  const float ql = q_len != nullptr ? q_len[row] : 1.f;
+  const float scale = T * ql;
+  const int li = lane < k ? lane : 0;
+  const int key_l = sub_idx[row * k + li];
+  const float g_l = d_sub[row * k + li];
+  float dlen = 0.f;
+  if (q_len != nullptr) {
+    const float s_l = sub_scores[row * k + li];
+    float t = lane < k ? g_l * (s_l / ql) : 0.f;  // cos * T
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+    dlen = t;
+  }
+  const float4* kh = (const float4*)(k_hat + (int64_t)hc * n * HALF);
+  float dy[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int i0 = 0; i0 < k; i0 += 16) {
+    float4 kv[8];
+    float gs[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int e = i0 + 2 * b + sub;
+      const int i = e < k ? e : 0;
+      const int key = __shfl(key_l, i);
+      const float g = __shfl(g_l, i);
+      const bool ok = e < k && key >= 0 && key < n;
+      gs[b] = ok ? g * scale : 0.f;
+      kv[b] = kh[(int64_t)(ok ? key : 0) * (HALF / 4) + col];
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      dy[0] = fmaf(gs[b], kv[b].x, dy[0]);
+      dy[1] = fmaf(gs[b], kv[b].y, dy[1]);
+      dy[2] = fmaf(gs[b], kv[b].z, dy[2]);
+      dy[3] = fmaf(gs[b], kv[b].w, dy[3]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 4; ++t) dy[t] += __shfl_xor(dy[t], 32);  // both halves now hold dims 4col .. 4col+3
+  if (q_len != nullptr && dlen_extra != nullptr) dlen += dlen_extra[row];
+  const float4 xv = ((const float4*)(q + row * HALF))[col];
+  const float x[4] = {xv.x, xv.y, xv.z, xv.w};
+  if (extra != nullptr) {
+    const float4 ev = ((const float4*)(extra + row * HALF))[col];
+    dy[0] += ev.x;
+    dy[1] += ev.y;
+    dy[2] += ev.z;
+    dy[3] += ev.w;
+  }
+  float xdy = 0.f, ss = 0.f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    xdy = fmaf(x[t], dy[t], xdy);
+    ss = fmaf(x[t], x[t], ss);
+  }
+#pragma unroll
+  for (int off = 16; off >= 1; off >>= 1) {  // within each half-wave
+    xdy += __shfl_xor(xdy, off);
+    ss += __shfl_xor(ss, off);
+  }
+  const float s = ss + eps;
+  const float r = 1.f / sqrtf(s);
+  const float r3 = r * r * r;
+  const float lenf = q_len != nullptr ? dlen * r / sqrtf((float)HALF) : 0.f;
+  if (sub == 0) {
+    float o[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) o[t] = r * dy[t] - r3 * xdy * x[t] + lenf * x[t];
+    ((float4*)(dq + row * HALF))[col] = make_float4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 // ------------------------------------------------------------------- keys
 __global__ void keys_bwd_prep_kernel(const int32_t* __restrict__ sub_idx, const float* __restrict__ d_sub,
                                      const float* __restrict__ q_len, int64_t P, int HC, int n, int k,
@@ -393,13 +482,21 @@ extern "C" int mpl_lookup_bwd_queries(const float* q, const float* q_len, const 
   clear_error();
   MPL_REQUIRE(M >= 0 && H > 0 && n > 0 && k > 0 && half > 0, MPL_EINVAL, "mpl_lookup_bwd_queries: bad sizes");
   MPL_REQUIRE(half <= 2 * kWave, MPL_EUNSUPPORTED, "mpl_lookup_bwd_queries: half must be <= 128");
+  MPL_REQUIRE(k <= kWave, MPL_EUNSUPPORTED, "mpl_lookup_bwd_queries: k must be <= %d", kWave);
   if (M == 0) return MPL_OK;
   MPL_REQUIRE(q && k_hat && sub_idx && d_sub && d_queries && temperature && (q_len == nullptr || sub_scores), MPL_EINVAL,
               "mpl_lookup_bwd_queries: null buffer");
   const int64_t rows = M * H * 2;
-  queries_bwd_kernel<<<(unsigned)cdiv(rows, kBwdThreads / kWave), kBwdThreads, 0, (hipStream_t)stream>>>(
-      q, q_len, k_hat, sub_idx, d_sub, sub_scores, dq_hat_extra, dlen_extra, rows, 2 * H, n, half, k, temperature,
-      1e-6f, d_queries);
+  const auto a16 = [](const void* p) { return ((uintptr_t)p & 15) == 0; };
+  const unsigned grid = (unsigned)cdiv(rows, kBwdThreads / kWave);
+  if (half == 128 && a16(q) && a16(k_hat) && a16(d_queries) && a16(dq_hat_extra))
+    queries_bwd_128_kernel<<<grid, kBwdThreads, 0, (hipStream_t)stream>>>(
+        q, q_len, k_hat, sub_idx, d_sub, sub_scores, dq_hat_extra, dlen_extra, rows, 2 * H, n, k, temperature, 1e-6f,
+        d_queries);
+  else
+    queries_bwd_kernel<<<grid, kBwdThreads, 0, (hipStream_t)stream>>>(
+        q, q_len, k_hat, sub_idx, d_sub, sub_scores, dq_hat_extra, dlen_extra, rows, 2 * H, n, half, k, temperature,
+        1e-6f, d_queries);
   return check_launch("mpl_lookup_bwd_queries");
 }
 

@@ -180,3 +180,48 @@ def test_dense_sub_key_gradient_fp16_scoring(gpu_lib, n, H, d_key, k, M, qs, btg
     _check(gk.cpu().numpy(), ref["d_sub_keys"], 1e-2, "d_sub_keys")
     _check(gq.cpu().numpy(), ref["d_queries"], 1e-2, "d_queries")
     _check(float(gt), ref["d_log_temperature"], 1e-2, "d_log_temperature", float(np.abs(ref["d_cos"] * sel["cos"]).sum()))
+
+
+@pytest.mark.parametrize("with_len", [False, True])
+def test_queries_backward_16_byte_form_equals_dword_form(gpu_lib, with_len):
+    """mpl_lookup_bwd_queries at half = 128 runs a kernel with 16-byte loads
+    (two key rows per load instruction) when q, k_hat, the extra d q-hat term
+    and d_queries are 16-byte aligned, and the dword kernel otherwise.  The
+    two differ only in the order the key rows are summed; entries with key
+    id -1 (unfilled ranks) and every optional input are exercised."""
+    from model_amd import _lib
+
+    L = gpu_lib
+    M, H, n, half, k = 300, 4, 512, 128, 16
+    rows = M * H * 2
+    g = torch.Generator(device="cuda").manual_seed(71)
+    dev = "cuda"
+    q = torch.randn((rows, half), generator=g, device=dev)
+    k_hat = torch.nn.functional.normalize(torch.randn((2 * H, n, half), generator=g, device=dev), dim=-1)
+    sub_idx = torch.randint(0, n, (rows, k), generator=g, device=dev, dtype=torch.int32)
+    sub_idx[::7, k - 3:] = -1
+    d_sub = torch.randn((rows, k), generator=g, device=dev)
+    sub_scores = torch.randn((rows, k), generator=g, device=dev)
+    extra = torch.randn((rows, half), generator=g, device=dev) * 0.1
+    q_len = (torch.rand((rows,), generator=g, device=dev) + 0.5) if with_len else None
+    dlen_extra = torch.randn((rows,), generator=g, device=dev) if with_len else None
+    T = torch.full((1,), 7.5, device=dev)
+    p = _lib.ptr
+
+    def run(off):
+        # copies shifted by `off` floats: off = 1 leaves them 4-byte aligned only
+        def place(t):
+            buf = torch.zeros(t.numel() + 4, device=dev)
+            v = buf[off:off + t.numel()].view(t.shape)
+            v.copy_(t)
+            return buf, v
+        (_, qv), (_, kv), (_, ev), (_, ov) = place(q), place(k_hat), place(extra), place(torch.zeros_like(q))
+        _lib.check(L.mpl_lookup_bwd_queries(p(qv), p(q_len), p(kv), p(sub_idx), p(d_sub), p(sub_scores), p(ev),
+                                            p(dlen_extra), M, H, n, half, k, p(T), p(ov),
+                                            torch.cuda.current_stream().cuda_stream), "queries")
+        torch.cuda.synchronize()
+        return ov.clone()
+
+    fast, dword = run(0), run(1)
+    assert torch.isfinite(fast).all()
+    torch.testing.assert_close(fast, dword, rtol=1e-5, atol=1e-5 * float(dword.abs().max()))
