@@ -428,6 +428,41 @@ __global__ __launch_bounds__(256) void bwd_max_kernel(const float* __restrict__ 
   }
 }
 
+// bwd_max_kernel in one coalesced pass, when a token's HC * k entries of
+// d_sub are V = HC * k / 4 16-byte vectors and V and HC divide 256: thread
+// t reads vector t % V of every (256 / V)-th token, which always lies in
+// codebook (t % V) / (k / 4); the threads of a codebook then meet in LDS.
+// The same maxima as bwd_max_kernel (a maximum does not depend on order).
+__global__ __launch_bounds__(256) void bwd_max_vec_kernel(const float* __restrict__ d_sub,
+                                                          const float* __restrict__ q_len, int64_t M, int HC, int k,
+                                                          int64_t tpg, float2* __restrict__ part) {
+  __shared__ float red[2][256];
+  const int tid = threadIdx.x;
+  const int V = HC * k / 4;
+  const int64_t t0 = (int64_t)blockIdx.x * tpg;
+  const int64_t t1 = t0 + tpg < M ? t0 + tpg : M;
+  float dm = 0.f, qm = 0.f;
+  if (d_sub != nullptr) {
+    const float4* d4 = (const float4*)d_sub;
+    for (int64_t m = t0 + tid / V; m < t1; m += 256 / V) {
+      const float4 v = d4[m * V + tid % V];
+      dm = fmaxf(dm, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+    }
+  }
+  if (q_len != nullptr)
+    for (int64_t m = t0 + tid / HC; m < t1; m += 256 / HC) qm = fmaxf(qm, q_len[m * HC + tid % HC]);
+  red[0][tid] = dm;
+  red[1][tid] = qm;
+  __syncthreads();
+  if (tid < HC) {
+    float a = 0.f, b = 0.f;
+    for (int j = tid * (k / 4); j < 256; j += V)  // vectors of codebook tid: (j % V) / (k / 4) == tid
+      for (int i = 0; i < k / 4; ++i) a = fmaxf(a, red[0][j + i]);
+    for (int j = tid; j < 256; j += HC) b = fmaxf(b, red[1][j]);
+    part[(int64_t)blockIdx.x * HC + tid] = make_float2(a, b);
+  }
+}
+
 // Per codebook: sigma = 2^floor(log2(n/4)) / max f (the d q_hat operand
 // scale, f = counts / (M k)) and S = (bound on |d cos| of the sub-key pass) /
 // 2^14, the bound being T (max q_len if query_scale) max |d_sub| plus the
@@ -1055,8 +1090,13 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
     launch_pack<true>(L.pd, f32, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
   const float inv_mk = (float)(1.0 / ((double)M * k));
   const float coef = (float)((double)n / ((double)HC * M));
-  bwd_max_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC, k,
-                                             L.mx_tpg, mx);
+  const int vpt = HC * k / 4;
+  if (k % 4 == 0 && 256 % vpt == 0 && 256 % HC == 0 && ((uintptr_t)d_sub & 15) == 0)
+    bwd_max_vec_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC,
+                                                   k, L.mx_tpg, mx);
+  else
+    bwd_max_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC, k,
+                                               L.mx_tpg, mx);
   bwd_scale_kernel<<<HC, 256, 0, s>>>(bal ? clean_counts : nullptr, mx, L.mx_groups, n, HC, inv_mk,
                                       bal ? g_balance : nullptr, coef, temperature, btg ? 1 : 0, query_scale ? 1 : 0,
                                       bal ? sigma : nullptr, dks);

@@ -15,9 +15,10 @@
 // fmix32 is the 32-bit finalizer of MurmurHash3 (Appleby; public domain): a
 // bijection on 32-bit words.  u takes JAX's values: 23-bit multiples of
 // 2^-23 below 1, clamped below at the smallest normal float, so g lies in
-// [-4.47, 15.9] like jax.random.gumbel's.  The logs are the accurate
-// (ocml) logf, not the hardware log2 approximation: -log(u) near u = 1 is a
-// small number whose relative precision the second log needs.
+// [-4.47, 15.9] like jax.random.gumbel's.  The inner log is the accurate
+// (ocml) logf: -log(u) near u = 1 is a small number whose relative precision
+// the outer log needs.  The outer log is the hardware log2 times ln 2, whose
+// error is absolute near its zero (e = 1) and relative elsewhere.
 #include <float.h>
 #include <math.h>
 
@@ -37,7 +38,12 @@ __device__ __forceinline__ uint32_t fmix32(uint32_t x) {
 __device__ __forceinline__ float gumbel_of(uint32_t rk, int j) {
   const uint32_t h = fmix32(rk + (uint32_t)j);
   const float u = fmaxf((float)(h >> 9) * 0x1p-23f, FLT_MIN);
-  return -logf(-logf(u));
+  // e = -log(u) lies in [2^-23, 87.4]; near u = 1 it is small and the outer
+  // log needs its relative precision, so it takes the accurate logf.  The
+  // outer log only needs absolute precision where its result is near 0
+  // (e near 1), which the hardware log2 gives: ln 2 * log2(e).
+  const float e = -logf(u);
+  return -0x1.62e43p-1f * __builtin_amdgcn_logf(e);
 }
 
 // One thread per four consecutive elements of a row.
