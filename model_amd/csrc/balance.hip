@@ -393,6 +393,55 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict_
   }
 }
 
+// Both fp16 packs of unscaled rows with half == HP (pack_rows_kernel<false>
+// and <true> of the same rows) from one read of them: workgroup (hc, blk)
+// stages the block's 32 rows x HP fp32 dims in LDS with 16-byte loads, then
+// writes the normal pack (a vector is 8 consecutive dims of one row) and the
+// transposed pack (a vector is one dim of 8 rows) from the tile.  The same
+// fp16 values in the same places as the two separate launches.
+template <int HP>
+__global__ __launch_bounds__(256) void pack_rows_both_f16_kernel(const float* __restrict__ X, int64_t s_hc,
+                                                                 int64_t s_row, int64_t nrows, int64_t nblk,
+                                                                 uint4* __restrict__ out_n, uint4* __restrict__ out_t) {
+  constexpr int PITCH = HP + 4;  // floats per staged row (16-byte aligned rows, shifted banks)
+  constexpr int V4 = HP / 4;     // 16-byte vectors per row
+  constexpr int NV = HP / 16;    // normal pack: vectors per lane per block
+  constexpr int NT = HP / 16;    // transposed pack: HP / 32 dim groups x 2 vectors
+  __shared__ float tile[32 * PITCH];
+  const int64_t blk = blockIdx.x % nblk;
+  const int64_t hc = blockIdx.x / nblk;
+  const float* base = X + hc * s_hc;
+  for (int t = threadIdx.x; t < 32 * V4; t += 256) {
+    const int rr = t / V4, c4 = t % V4;
+    const int64_t row = blk * 32 + rr;
+    const float4 v = row < nrows ? *(const float4*)(base + row * s_row + 4 * c4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    *(float4*)(tile + rr * PITCH + 4 * c4) = v;
+  }
+  __syncthreads();
+  const int64_t ob = (hc * nblk + blk) * (int64_t)(NV * kWave);
+  for (int t = threadIdx.x; t < NV * kWave; t += 256) {
+    const int v = t / kWave, l = t % kWave;
+    const float* src = tile + (l & 31) * PITCH + 16 * v + 8 * (l >> 5);
+    const float4 a = *(const float4*)src, b = *(const float4*)(src + 4);
+    const float e[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    half8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) h[i] = (_Float16)e[i];
+    out_n[ob + t] = __builtin_bit_cast(uint4, h);
+  }
+  for (int t = threadIdx.x; t < NT * kWave; t += 256) {
+    const int w = t / kWave, l = t % kWave;
+    const int wv = w & 1, d = 32 * (w >> 1) + (l & 31);
+    half8 h;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int r = wv * 8 + i;
+      h[i] = (_Float16)tile[(8 * (r >> 2) + 4 * (l >> 5) + (r & 3)) * PITCH + d];
+    }
+    out_t[ob + t] = __builtin_bit_cast(uint4, h);
+  }
+}
+
 // Per codebook maxima of |d_sub| and q_len over a range of tokens: workgroup
 // b covers tokens [b * tpg, (b + 1) * tpg) and writes part[b][hc] =
 // (max |d_sub|, max q_len).  Maxima do not depend on the order of the
@@ -1084,8 +1133,17 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   float* tpart = (float*)(ws + L.tpart);
   const float* rho = scaled ? q_len : nullptr;
 
-  launch_pack<false>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
-  launch_pack<true>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);
+  const bool both = !f32 && L.pd.HP == half && (half == 64 || half == 128) && ((uintptr_t)q_hat & 15) == 0;
+  if (both && half == 128)
+    pack_rows_both_f16_kernel<128><<<(unsigned)(HC * L.mblk), 256, 0, s>>>(q_hat, half, (int64_t)HC * half, M, L.mblk,
+                                                                           qn, qt);
+  else if (both)
+    pack_rows_both_f16_kernel<64><<<(unsigned)(HC * L.mblk), 256, 0, s>>>(q_hat, half, (int64_t)HC * half, M, L.mblk,
+                                                                          qn, qt);
+  if (!both) {
+    launch_pack<false>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
+    launch_pack<true>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);
+  }
   if (bal)
     launch_pack<true>(L.pd, f32, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
   const float inv_mk = (float)(1.0 / ((double)M * k));
