@@ -122,6 +122,8 @@ __global__ __launch_bounds__(kBwdThreads) void route_bwd_kernel(
     float* __restrict__ dlogt_part) {
   __shared__ float dw_s[kBwdThreads / kWave][kMaxRows];
   __shared__ float ds_s[kBwdThreads / kWave][kMaxRows];
+  __shared__ float w_s[kBwdThreads / kWave][kMaxRows];
+  __shared__ int f_s[kBwdThreads / kWave][kMaxRows];
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int64_t m = (int64_t)blockIdx.x * (kBwdThreads / kWave) + wave;
@@ -129,6 +131,14 @@ __global__ __launch_bounds__(kBwdThreads) void route_bwd_kernel(
   const int R = H * k;
   float* dw = dw_s[wave];
   float* ds = ds_s[wave];
+  // the token's weights and rank pairs, read once (coalesced) for the loops
+  // below, which then take them from LDS in the same order
+  float* wl = w_s[wave];
+  int* fl = f_s[wave];
+  for (int r = lane; r < R; r += kWave) {
+    wl[r] = weights[m * R + r];
+    fl[r] = flat_idx[m * R + r];
+  }
   if (FAST)
     row_dots_512<V>(values, N, slots, m, R, shuffle, g_out, dw, lane);
   else
@@ -139,8 +149,8 @@ __global__ __launch_bounds__(kBwdThreads) void route_bwd_kernel(
   for (int r = lane; r < R; r += kWave) {
     const int h = r / k;
     float s = 0.f;
-    for (int j = 0; j < k; ++j) s = fmaf(weights[m * R + h * k + j], dw[h * k + j], s);
-    const float w = weights[m * R + r];
+    for (int j = 0; j < k; ++j) s = fmaf(wl[h * k + j], dw[h * k + j], s);
+    const float w = wl[r];
     ds[r] = w * (dw[r] - s);
     if (d_weights != nullptr) d_weights[m * R + r] = dw[r];
   }
@@ -154,7 +164,7 @@ __global__ __launch_bounds__(kBwdThreads) void route_bwd_kernel(
     const int i = o % k;
     float acc = 0.f;
     for (int j = 0; j < k; ++j) {
-      const int f = flat_idx[m * R + h * k + j];
+      const int f = fl[h * k + j];
       const int rank = c == 0 ? f / k : f % k;
       acc += rank == i ? ds[h * k + j] : 0.f;
     }
