@@ -182,17 +182,18 @@ def test_dense_sub_key_gradient_fp16_scoring(gpu_lib, n, H, d_key, k, M, qs, btg
     _check(float(gt), ref["d_log_temperature"], 1e-2, "d_log_temperature", float(np.abs(ref["d_cos"] * sel["cos"]).sum()))
 
 
-@pytest.mark.parametrize("with_len", [False, True])
-def test_queries_backward_16_byte_form_equals_dword_form(gpu_lib, with_len):
+@pytest.mark.parametrize("with_len,k", [(False, 16), (True, 16), (True, 5), (False, 37)])
+def test_queries_backward_16_byte_form_equals_dword_form(gpu_lib, with_len, k):
     """mpl_lookup_bwd_queries at half = 128 runs a kernel with 16-byte loads
     (two key rows per load instruction) when q, k_hat, the extra d q-hat term
     and d_queries are 16-byte aligned, and the dword kernel otherwise.  The
     two differ only in the order the key rows are summed; entries with key
-    id -1 (unfilled ranks) and every optional input are exercised."""
+    id -1 (unfilled ranks), every optional input, and entry counts that do
+    not fill the half-waves' batches of 8 are exercised."""
     from model_amd import _lib
 
     L = gpu_lib
-    M, H, n, half, k = 300, 4, 512, 128, 16
+    M, H, n, half = 300, 4, 512, 128
     rows = M * H * 2
     g = torch.Generator(device="cuda").manual_seed(71)
     dev = "cuda"
