@@ -501,6 +501,19 @@ int mpl_decode_next_token(const float* logits, int64_t rows, int64_t vocab, cons
                           int64_t* out, int64_t out_stride, int64_t out_cap, uint32_t* done, void* stream);
 
 /*
+ * The input rows of a decode step (model.py:29-127: the token embedding plus
+ * the position embedding, for one token per stream): for each of `rows`
+ * streams, out[b, :] = emb[token[b], :] + pos_emb[*position, :] (emb
+ * [vocab, d] and pos_emb [max_pos, d] fp32, token int64 [rows], position a
+ * device int64 scalar, out [rows, d] fp32).  d is a multiple of 4 and emb,
+ * pos_emb and out are 16-byte aligned.  The same bits as the two indexings
+ * and the add.  A token outside [0, vocab) or a position outside
+ * [0, max_pos) writes a NaN row.
+ */
+int mpl_decode_embed(const float* emb, int64_t vocab, const float* pos_emb, int64_t max_pos, int d,
+                     const int64_t* token, const int64_t* position, int64_t rows, float* out, void* stream);
+
+/*
  * A dense layer of the backbone over a few rows (model.py:29-127: the
  * query/key/value, output, feed-forward, router, gate and mem_out products
  * and embed.attend), with its neighbours fused in:

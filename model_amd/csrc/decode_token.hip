@@ -12,6 +12,9 @@
 //   token[b] = next;  out[b, p + 1 - prompt_len] = next  (generated tokens)
 // The last workgroup to finish (an atomic count, reset by that workgroup)
 // advances *position to p + 1, after every workgroup has read p.
+//
+// The step's input rows (embedding plus position embedding) are one launch
+// too: decode_embed_kernel below.
 #include <math.h>
 
 #include "common.h"
@@ -133,6 +136,28 @@ __global__ __launch_bounds__(kTokThreads) void next_token_kernel(const float* __
   }
 }
 
+// The decode step's input rows (model.py:29-127, the embedding and position
+// embedding of one token per stream): out[b] = emb[token[b]] + pos_emb[*position],
+// one fp32 add per element as the two indexings and the add compute it.  A
+// workgroup of 64 threads per stream, one 16-byte vector per thread and pass.
+// An id outside its table writes a NaN row.
+__global__ __launch_bounds__(64) void decode_embed_kernel(const float* __restrict__ emb,
+                                                          const float* __restrict__ pos_emb,
+                                                          const int64_t* __restrict__ token,
+                                                          const int64_t* __restrict__ position, int64_t vocab,
+                                                          int64_t max_pos, int d4, float* __restrict__ out) {
+  const int64_t b = blockIdx.x;
+  const int64_t t = token[b], p = *position;
+  const bool ok = t >= 0 && t < vocab && p >= 0 && p < max_pos;
+  const float4* e = (const float4*)emb + (ok ? t : 0) * d4;
+  const float4* q = (const float4*)pos_emb + (ok ? p : 0) * d4;
+  float4* o = (float4*)out + b * d4;
+  for (int j = threadIdx.x; j < d4; j += 64) {
+    const float4 a = e[j], c = q[j];
+    o[j] = ok ? make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w) : make_float4(NAN, NAN, NAN, NAN);
+  }
+}
+
 }  // namespace
 }  // namespace mpl
 
@@ -153,4 +178,21 @@ extern "C" int mpl_decode_next_token(const float* logits, int64_t rows, int64_t 
   next_token_kernel<<<(unsigned)rows, kTokThreads, 0, (hipStream_t)stream>>>(
       logits, vocab, prompt, prompt_stride, prompt_len, position, token, out, out_stride, out_cap, done);
   return check_launch("mpl_decode_next_token");
+}
+
+extern "C" int mpl_decode_embed(const float* emb, int64_t vocab, const float* pos_emb, int64_t max_pos, int d,
+                                const int64_t* token, const int64_t* position, int64_t rows, float* out,
+                                void* stream) {
+  clear_error();
+  MPL_REQUIRE(rows >= 0 && vocab > 0 && max_pos > 0 && d > 0 && d % 4 == 0, MPL_EINVAL,
+              "mpl_decode_embed: bad sizes rows=%lld vocab=%lld max_pos=%lld d=%d", (long long)rows,
+              (long long)vocab, (long long)max_pos, d);
+  MPL_REQUIRE(rows < ((int64_t)1 << 31), MPL_EINVAL, "mpl_decode_embed: rows=%lld too large", (long long)rows);
+  if (rows == 0) return MPL_OK;
+  MPL_REQUIRE(emb && pos_emb && token && position && out, MPL_EINVAL, "mpl_decode_embed: null buffer");
+  MPL_REQUIRE(((uintptr_t)emb & 15) == 0 && ((uintptr_t)pos_emb & 15) == 0 && ((uintptr_t)out & 15) == 0,
+              MPL_EINVAL, "mpl_decode_embed: emb, pos_emb and out must be 16-byte aligned");
+  decode_embed_kernel<<<(unsigned)rows, 64, 0, (hipStream_t)stream>>>(emb, pos_emb, token, position, vocab, max_pos,
+                                                                      d / 4, out);
+  return check_launch("mpl_decode_embed");
 }

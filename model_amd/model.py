@@ -81,6 +81,33 @@ def _dense(x, p):
 _ACT = {None: 0, "gelu_tanh": 1, "silu": 2}
 
 
+def decode_embed(emb: torch.Tensor, pos_emb: torch.Tensor, tokens: torch.Tensor,
+                 position: torch.Tensor) -> torch.Tensor:
+    """mpl_decode_embed: emb[tokens] + pos_emb[position] for one token per
+    stream (tokens int64 [B], position a device int64 tensor [1]), in one
+    launch; the same bits as the two indexings and the add.  An id outside
+    its table gives a NaN row."""
+    from . import _lib
+
+    for t in (emb, pos_emb):
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.dim() != 2 or t.device != tokens.device:
+            raise ValueError("decode_embed: tables must be contiguous 2-d fp32 on the tokens' device")
+    tok = tokens.reshape(-1)
+    if tok.dtype != torch.int64 or not tok.is_contiguous() or position.dtype != torch.int64:
+        raise ValueError("decode_embed: tokens and position must be contiguous int64")
+    if tokens.device.type != "cuda":
+        raise ValueError("decode_embed runs on the GPU only (libmpl.so)")
+    B, d = tok.numel(), emb.shape[1]
+    if pos_emb.shape[1] != d:
+        raise ValueError(f"decode_embed: widths {d} and {pos_emb.shape[1]} differ")
+    out = torch.empty((B, d), dtype=torch.float32, device=tokens.device)
+    P = _lib.ptr
+    _lib.check(_lib.lib().mpl_decode_embed(P(emb), emb.shape[0], P(pos_emb), pos_emb.shape[0], d, P(tok),
+                                           P(position), B, P(out), _lib.stream_ptr(tokens.device)),
+               "mpl_decode_embed")
+    return out
+
+
 def rows_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None, *,
                 out_in: bool = False, ln: Optional[Dict[str, torch.Tensor]] = None, eps: float = LN_EPS,
                 x_mul: Optional[torch.Tensor] = None, act: Optional[str] = None,
@@ -320,7 +347,13 @@ class MemoryPoolLM:
         emb = p["embed"]["embedding"]
         layer_aux = []
         with torch.no_grad():
-            x = emb[tokens[:, 0]] + p["pos_embed"][positions]  # [B, d]
+            pe = p["pos_embed"]
+            if (emb.shape[1] % 4 == 0 and tokens.dtype == torch.int64 and positions.dtype == torch.int64
+                    and all(t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0
+                            for t in (emb, pe))):
+                x = decode_embed(emb, pe, tokens[:, 0].contiguous(), positions)  # [B, d], one launch
+            else:
+                x = emb[tokens[:, 0]] + pe[positions]
             for i in range(cfg.n_layers):
                 pa = p[f"attn_{i}"]
                 w, b = self._fused_qkv(i, pa)

@@ -142,3 +142,25 @@ def test_next_token_kernel_matches_torch(gpu_lib, V):
     assert torch.equal(out[:, :len(want_out)], torch.stack(want_out, 1))
     assert bool((out[:, len(want_out):] == -1).all())
     assert tok[0].item() in (17,) and tok[1].item() == 0 and tok[2].item() == 555 and tok[3].item() == 0
+
+
+@pytest.mark.parametrize("B,V,P,d", [(64, 16384, 512, 256), (3, 17, 9, 8)])
+def test_decode_embed_matches_torch(gpu_lib, B, V, P, d):
+    """mpl_decode_embed (the decode step's input rows in one launch) equals
+    emb[tokens] + pos_emb[position] bit for bit, and an out-of-range token
+    or position gives NaN rows rather than a read outside the tables."""
+    from model_amd.model import decode_embed
+
+    g = torch.Generator(device="cuda").manual_seed(B + V)
+    emb = torch.randn((V, d), generator=g, device="cuda")
+    pos_emb = torch.randn((P, d), generator=g, device="cuda")
+    tok = torch.randint(0, V, (B,), generator=g, device="cuda")
+    for p in (0, P - 1, P // 2):
+        pos = torch.tensor([p], dtype=torch.int64, device="cuda")
+        assert torch.equal(decode_embed(emb, pos_emb, tok, pos), emb[tok] + pos_emb[pos])
+    bad = tok.clone()
+    bad[0] = V
+    out = decode_embed(emb, pos_emb, bad, torch.tensor([1], dtype=torch.int64, device="cuda"))
+    assert torch.isnan(out[0]).all() and torch.isfinite(out[1:]).all()
+    out = decode_embed(emb, pos_emb, tok, torch.tensor([P], dtype=torch.int64, device="cuda"))
+    assert torch.isnan(out).all()
