@@ -101,6 +101,53 @@ __device__ __forceinline__ void row_dots_512(const V* values, int64_t N, const i
   if (row < R) dw_lds[row] = part[0];
 }
 
+// dw of the R rows of token m into LDS, 1 KB rows (d = 256 fp32 or d = 512
+// fp16), R <= 64: one row per 16-byte load instruction (64 lanes x 16 B),
+// eight rows in flight; lane partial dots are reduce-scattered across the 64
+// lanes (xor 32, 16, 8, 4, 2, 1), leaving row `lane` in each lane.
+template <typename V>
+__device__ __forceinline__ void row_dots_1k(const V* values, int64_t N, const int32_t* slots, int64_t m, int R,
+                                            int shuffle, const float* g, float* dw_lds, int lane) {
+  constexpr int VE = RowLoad<V>::kElems;
+  float gv[VE];
+#pragma unroll
+  for (int e = 0; e < VE; ++e) gv[e] = g[m * (kWave * VE) + lane * VE + e];
+  const int myrow = lane < R ? lane : 0;
+  const int64_t myslot = read_slot(slots[m * R + myrow], N, shuffle);
+  float part[kWave];
+  const uint4* base = (const uint4*)values;
+#pragma unroll
+  for (int i0 = 0; i0 < kWave; i0 += 8) {
+    uint4 buf[8];
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      const int row = i0 + b;
+      const int64_t s = __shfl((int)myslot, row < R ? row : 0);
+      buf[b] = base[s * kWave + lane];
+    }
+#pragma unroll
+    for (int b = 0; b < 8; ++b) {
+      float f[VE];
+      RowLoad<V>::unpack(buf[b], f);
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < VE; ++e) acc = fmaf(gv[e], f[e], acc);
+      part[i0 + b] = acc;
+    }
+  }
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) {
+    const bool hi = (lane & s) != 0;
+#pragma unroll
+    for (int j = 0; j < s; ++j) {
+      const float keep = hi ? part[j + s] : part[j];
+      const float send = hi ? part[j] : part[j + s];
+      part[j] = keep + __shfl_xor(send, s);
+    }
+  }
+  if (lane < R) dw_lds[lane] = part[0];
+}
+
 template <typename V>
 __device__ __forceinline__ void row_dots_generic(const V* values, int64_t N, int d, const int32_t* slots, int64_t m,
                                                  int R, int shuffle, const float* g, float* dw_lds, int lane) {
@@ -114,7 +161,8 @@ __device__ __forceinline__ void row_dots_generic(const V* values, int64_t N, int
   }
 }
 
-template <typename V, bool FAST>
+// MODE 1: 512-byte rows (row_dots_512); 2: 1 KB rows (row_dots_1k); 0: any d.
+template <typename V, int MODE>
 __global__ __launch_bounds__(kBwdThreads) void route_bwd_kernel(
     const float* __restrict__ g_out, const V* __restrict__ values, int64_t N, int d, const int32_t* __restrict__ slots,
     const float* __restrict__ weights, const int32_t* __restrict__ flat_idx, const float* __restrict__ sub_scores,
@@ -139,8 +187,10 @@ __global__ __launch_bounds__(kBwdThreads) void route_bwd_kernel(
     wl[r] = weights[m * R + r];
     fl[r] = flat_idx[m * R + r];
   }
-  if (FAST)
+  if (MODE == 1)
     row_dots_512<V>(values, N, slots, m, R, shuffle, g_out, dw, lane);
+  else if (MODE == 2)
+    row_dots_1k<V>(values, N, slots, m, R, shuffle, g_out, dw, lane);
   else
     row_dots_generic<V>(values, N, d, slots, m, R, shuffle, g_out, dw, lane);
   __builtin_amdgcn_wave_barrier();
@@ -469,17 +519,20 @@ extern "C" int mpl_lookup_bwd_route(const float* g_out, const void* values, int 
   hipStream_t s = (hipStream_t)stream;
   const unsigned blocks = (unsigned)cdiv(M, kBwdThreads / kWave);
   const int esz = values_dtype == MPL_F16 ? 2 : 4;
-  const bool fast = (int64_t)d * esz == 512 && H * k <= kWave && ((uintptr_t)values % 16) == 0;
+  const bool vec = H * k <= kWave && ((uintptr_t)values % 16) == 0;
+  const int mode = !vec ? 0 : (int64_t)d * esz == 512 ? 1 : (int64_t)d * esz == 1024 ? 2 : 0;
 #define MPL_RB(V, F)                                                                                             \
   route_bwd_kernel<V, F><<<blocks, kBwdThreads, 0, s>>>(g_out, (const V*)values, N, d, slots, weights, flat_idx, \
                                                         sub_scores, M, H, k, shuffle_reads, d_weights, d_sub,    \
                                                         dlogt_part)
   if (values_dtype == MPL_F16) {
-    if (fast) MPL_RB(_Float16, true);
-    else MPL_RB(_Float16, false);
+    if (mode == 1) MPL_RB(_Float16, 1);
+    else if (mode == 2) MPL_RB(_Float16, 2);
+    else MPL_RB(_Float16, 0);
   } else {
-    if (fast) MPL_RB(float, true);
-    else MPL_RB(float, false);
+    if (mode == 1) MPL_RB(float, 1);
+    else if (mode == 2) MPL_RB(float, 2);
+    else MPL_RB(float, 0);
   }
 #undef MPL_RB
   return check_launch("mpl_lookup_bwd_route");

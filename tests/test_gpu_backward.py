@@ -226,3 +226,42 @@ def test_queries_backward_16_byte_form_equals_dword_form(gpu_lib, with_len, k):
     fast, dword = run(0), run(1)
     assert torch.isfinite(fast).all()
     torch.testing.assert_close(fast, dword, rtol=1e-5, atol=1e-5 * float(dword.abs().max()))
+
+
+@pytest.mark.parametrize("dtype,d", [(torch.float32, 256), (torch.float16, 512)])
+def test_route_backward_1k_rows_equal_generic_form(gpu_lib, dtype, d):
+    """mpl_lookup_bwd_route with 1 KB value rows (fp32 d = 256, fp16 d = 512)
+    reads a row per 16-byte load instruction and reduce-scatters the lane
+    dots; with the table 4-byte aligned only it takes the per-element loop.
+    The two differ only in the order each dot is summed."""
+    from model_amd import _lib
+
+    M, H, k, N = 200, 4, 16, 4096
+    g = torch.Generator(device="cuda").manual_seed(d)
+    vals = (torch.randn((N, d), generator=g, device="cuda") * 0.05).to(dtype)
+    slots = torch.randint(0, N, (M, H, k), generator=g, device="cuda", dtype=torch.int32)
+    w = torch.rand((M, H, k), generator=g, device="cuda")
+    w = w / w.sum(-1, keepdim=True)
+    flat = torch.randint(0, k * k, (M, H, k), generator=g, device="cuda", dtype=torch.int32)
+    sub_scores = torch.randn((M, H, 2, k), generator=g, device="cuda")
+    g_out = torch.randn((M, d), generator=g, device="cuda") * 1e-3
+    vdt = _lib.MPL_F16 if dtype == torch.float16 else _lib.MPL_F32
+    p = _lib.ptr
+
+    def run(off):
+        buf = torch.zeros(N * d + 8, dtype=dtype, device="cuda")
+        v = buf[off:off + N * d].view(N, d)
+        v.copy_(vals)
+        dw = torch.empty((M, H, k), device="cuda")
+        ds = torch.empty((M, H, 2, k), device="cuda")
+        lt = torch.empty((M,), device="cuda")
+        _lib.check(gpu_lib.mpl_lookup_bwd_route(p(g_out), p(v), vdt, N, d, p(slots), p(w), p(flat), p(sub_scores),
+                                                M, H, k, 0, p(dw), p(ds), p(lt),
+                                                torch.cuda.current_stream().cuda_stream), "route")
+        torch.cuda.synchronize()
+        return dw, ds, lt
+
+    off = 2 if dtype == torch.float16 else 1  # 4 bytes: not 16-byte aligned
+    for a, b in zip(run(0), run(off)):
+        assert torch.isfinite(a).all()
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5 * float(b.abs().max()))
