@@ -468,7 +468,7 @@ def train_step_bench(torch, iters):
         out, aux = pool.apply({"params": params}, q, train=True, sparse_grad=True)
         loss = ((out + probe) * g_out).sum() + 0.01 * aux["balance_loss"] + 0.01 * key_diversity_loss(keys)
         gw, gk, gt, gp = torch.autograd.grad(loss, [w_q, keys, log_t, probe])
-        rest = (gw.square().sum() + gk.square().sum() + gt.square()).reshape(1)
+        rest = R.sum_squares([gw, gk, gt])
         upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: gp}, [0], rest_sq=rest)
 
     for _ in range(3):
@@ -497,7 +497,7 @@ def train_step_bench(torch, iters):
             _, dk_div = key_diversity_value_and_grad(keys, g_div)
             gk = dk + dk_div
             gw = hidden.t() @ dq.reshape(M, H * d_key)
-            rest = (gw.square().sum() + gk.square().sum() + dlt.square()).reshape(1)
+            rest = R.sum_squares([gw, gk, dlt])  # no memset node in the captured step
             upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest)
 
     ms_graph = time_loop(torch, step_graph, iters, 3)

@@ -170,7 +170,8 @@ int mpl_rowfile_close(void* handle);
  * (mpl_score_select_workspace_bytes above it, e.g. beyond about 65,000 tokens
  * at n = 512) fails with MPL_EWORKSPACE.  Calls on one GPU share that array:
  * calls that overlap in time on one GPU (other streams, other threads) race.
- * Nothing is allocated; the current device must be the stream's device.
+ * Nothing is allocated; the current device must be the stream's device
+ * (checked: MPL_EINVAL otherwise).
  */
 size_t mpl_lookup_static_scratch_bytes(void);
 int mpl_lookup_static(const void* queries, int query_mode, float* q_len, const void* packed_keys,
@@ -302,6 +303,18 @@ int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fe
 size_t mpl_clip_scale_workspace_bytes(void);
 int mpl_clip_scale(const float* row_sq, int64_t cap, const float* rest_sq, float grad_clip,
                    float* scale_gnorm, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * train.py:395-397 (the dense part of optax.global_norm's square):
+ * out[0] = (add ? add[0] : 0) + sum over the count <= 8 fp32 buffers
+ * x[j] [n[j]] of x^2.  x and n are host arrays of device pointers and sizes.
+ * fp64 accumulation in a fixed order (256 chunks of the joined buffers, then
+ * one block): bitwise reproducible, no atomics and no memset, so it may be
+ * captured in a HIP graph.  workspace: mpl_sum_squares_workspace_bytes().
+ */
+size_t mpl_sum_squares_workspace_bytes(void);
+int mpl_sum_squares(const float* const* x, const int64_t* n, int count, const float* add, float* out,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * train.py:412-416 (row-wise Adagrad, in place): for each u < cap with

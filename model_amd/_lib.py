@@ -55,6 +55,8 @@ SIGNATURES = {
     "mpl_merge_rows": (_I, [_P, _P, _I64, _I, _P, _I, _I64, _P, _SZ, _P, _P, _P, _P, _I, _P]),
     "mpl_clip_scale_workspace_bytes": (_SZ, []),
     "mpl_clip_scale": (_I, [_P, _I64, _P, _F, _P, _P, _SZ, _P]),
+    "mpl_sum_squares_workspace_bytes": (_SZ, []),
+    "mpl_sum_squares": (_I, [_P, _P, _I, _P, _P, _P, _SZ, _P]),
     "mpl_row_adagrad": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I, _I64, _F, _P, _P]),
     "mpl_row_adam": (_I, [_P, _I, _P, _P, _P, _P, _P, _I64, _I, _I64, _F, _I, _P, _P]),
     "mpl_lookup_bwd_route": (_I, [_P, _P, _I, _I64, _I, _P, _P, _P, _P, _I64, _I, _I, _I, _P, _P, _P, _P]),

@@ -176,9 +176,10 @@ def _to_numpy(t) -> np.ndarray:
 def _pack_tree(tree, path, values_dtype):
     if isinstance(tree, dict):
         return {str(k): _pack_tree(v, path + (str(k),), values_dtype) for k, v in tree.items()}
+    # every leaf, 0-d ones included, is an ndarray (ext 1): the reference writes
+    # to_bytes(jax.device_get(state)), and device_get turns each jax array,
+    # the int32 step and optax's counts among them, into an ndarray
     arr = _to_numpy(tree)
-    if arr.ndim == 0 and path == ("step",):  # the TrainState step: a numpy scalar (ext 3), as Flax writes it
-        return msgpack.ExtType(EXT_NPSCALAR, _ndarray_bytes(arr))
     if path[-2:] == POOL_PATH and values_dtype is not None:
         arr = arr.astype(values_dtype)
     arr = np.ascontiguousarray(arr)

@@ -652,6 +652,46 @@ __global__ __launch_bounds__(256) void clip_finish_kernel(const double* __restri
   }
 }
 
+// Sum of squares over up to kSqMaxBufs buffers, read as one array in order
+// (buffer 0's elements, then buffer 1's, ...): block b sums chunk b of that
+// array in fp64, the finish adds the chunks in order.  Same two-stage shape
+// as the clip's row sum, so the result is bitwise reproducible.
+constexpr int kSqMaxBufs = 8;
+struct SqBufs {
+  const float* x[kSqMaxBufs];
+  int64_t end[kSqMaxBufs];  // exclusive prefix ends of the buffers in the joined array
+  int count;
+};
+
+__global__ __launch_bounds__(256) void sum_sq_chunks_kernel(SqBufs bufs, double* __restrict__ chunk_sums) {
+  __shared__ double part[256];
+  const int64_t total = bufs.end[bufs.count - 1];
+  const int64_t per = cdiv(total, kSumBlocks);
+  const int64_t b0 = (int64_t)blockIdx.x * per;
+  const int64_t b1 = b0 + per < total ? b0 + per : total;
+  double s = 0.0;
+  int64_t start = 0;
+  for (int j = 0; j < bufs.count; ++j) {
+    const int64_t lo = b0 > start ? b0 : start;
+    const int64_t hi = b1 < bufs.end[j] ? b1 : bufs.end[j];
+    const float* __restrict__ x = bufs.x[j];
+    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+      const double v = (double)x[i - start];
+      s += v * v;
+    }
+    start = bufs.end[j];
+  }
+  const double t = block_sum_f64(s, part);
+  if (threadIdx.x == 0) chunk_sums[blockIdx.x] = t;
+}
+
+__global__ __launch_bounds__(256) void sum_finish_kernel(const double* __restrict__ chunk_sums,
+                                                         const float* __restrict__ add, float* __restrict__ out) {
+  __shared__ double part[256];
+  const double t = block_sum_f64(chunk_sums[threadIdx.x], part);
+  if (threadIdx.x == 0) out[0] = (float)(t + (add != nullptr ? (double)*add : 0.0));
+}
+
 // ---------------------------------------------------------- optimizers
 // One wave per row, grid-stride over the cap rows (a fixed grid: most of the
 // cap rows are padding when routing is skewed).  A row of d elements is nv
@@ -1079,6 +1119,38 @@ extern "C" int mpl_clip_scale(const float* row_sq, int64_t cap, const float* res
   sum_chunks_kernel<<<kSumBlocks, 256, 0, s>>>(row_sq, cap, (double*)workspace);
   clip_finish_kernel<<<1, 256, 0, s>>>((const double*)workspace, rest_sq, grad_clip, scale_gnorm);
   return check_launch("mpl_clip_scale");
+}
+
+extern "C" size_t mpl_sum_squares_workspace_bytes() { return kSumBlocks * sizeof(double); }
+
+extern "C" int mpl_sum_squares(const float* const* x, const int64_t* n, int count, const float* add, float* out,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  MPL_REQUIRE(count >= 0 && count <= kSqMaxBufs && out != nullptr && (count == 0 || (x && n)), MPL_EINVAL,
+              "mpl_sum_squares: bad arguments (count %d, at most %d buffers)", count, kSqMaxBufs);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= kSumBlocks * sizeof(double), MPL_EWORKSPACE,
+              "mpl_sum_squares: workspace of %zu bytes needed", (size_t)kSumBlocks * sizeof(double));
+  SqBufs b{};
+  int64_t total = 0;
+  int used = 0;
+  for (int j = 0; j < count; ++j) {
+    MPL_REQUIRE(n[j] >= 0 && (n[j] == 0 || x[j] != nullptr), MPL_EINVAL, "mpl_sum_squares: buffer %d: bad size or null", j);
+    if (n[j] == 0) continue;
+    total += n[j];
+    b.x[used] = x[j];
+    b.end[used] = total;
+    ++used;
+  }
+  if (used == 0) {  // an empty sum: out = add (or 0), one element, still a kernel
+    b.x[0] = nullptr;
+    b.end[0] = 0;
+    used = 1;
+  }
+  b.count = used;
+  hipStream_t s = (hipStream_t)stream;
+  sum_sq_chunks_kernel<<<kSumBlocks, 256, 0, s>>>(b, (double*)workspace);
+  sum_finish_kernel<<<1, 256, 0, s>>>((const double*)workspace, add, out);
+  return check_launch("mpl_sum_squares");
 }
 
 extern "C" int mpl_row_adagrad(void* values, int values_dtype, float* master, float* acc, const int32_t* uniq,

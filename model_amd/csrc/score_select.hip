@@ -1685,6 +1685,17 @@ extern "C" int mpl_lookup_static(const void* queries, int query_mode, float* q_l
               (long long)M, need, kStaticScratchBytes);
   void* ws = nullptr;
   if (need > 0) {
+    // the scratch is the current device's copy: the stream must be on that device
+    int cur = -1;
+    hipDevice_t sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    MPL_REQUIRE(e == hipSuccess, MPL_EHIP, "mpl_lookup_static: hipGetDevice: %s", hipGetErrorString(e));
+    e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    MPL_REQUIRE(e == hipSuccess, MPL_EHIP, "mpl_lookup_static: hipStreamGetDevice: %s", hipGetErrorString(e));
+    MPL_REQUIRE((int)sdev == cur, MPL_EINVAL,
+                "mpl_lookup_static: the stream belongs to device %d but device %d is current; make the stream's "
+                "device current before the call",
+                (int)sdev, cur);
     const int rc = static_scratch(&ws);
     if (rc) return rc;
   }

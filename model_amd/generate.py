@@ -29,7 +29,10 @@ from .model import MemoryPoolLM, ModelConfig
 
 
 class Generator:
-    """generate.py:23-65.  ``graph=False`` runs the decode step eagerly."""
+    """generate.py:23-65.  ``graph=False`` runs the decode step eagerly.
+    With a file-mode host pool (rows read from the pool's .npy files on host
+    threads) the step is not capturable and runs eagerly whatever ``graph``
+    says; a RAM-mode host pool (pinned table read by the GPU) captures."""
 
     def __init__(self, mcfg: ModelConfig, params, batch_size: int = 1, graph: bool = True, device="cuda"):
         self.mcfg, self.batch_size, self.device = mcfg, batch_size, torch.device(device)
@@ -106,13 +109,36 @@ class Generator:
         pool = self.params.get("pool", {})
         copied = [pool[k] for k in ("sub_keys", "log_temperature") if k in pool]
         copied += self.model.copied_parameters(self.params)
-        return tuple(flat), tuple((t.data_ptr(), t._version) for t in copied)
+        # identity too: a tensor replaced by a new one at the same address has
+        # its version counter back at 0.  The state holds the tensors, so no
+        # other tensor can take their ids while it is kept.
+        return tuple(flat), tuple((t, id(t), t.data_ptr(), t._version) for t in copied)
+
+    @staticmethod
+    def _same_state(a, b) -> bool:
+        if a is None or b is None or a[0] != b[0] or len(a[1]) != len(b[1]):
+            return False
+        return all(x[0] is y[0] and x[1:] == y[1:] for x, y in zip(a[1], b[1]))
+
+    def _host_pool_off_device(self) -> bool:
+        """True when the memory layers read a host pool in file mode: its rows
+        are staged through host threads after a device-to-host read of the
+        distinct ids, which a captured graph cannot hold."""
+        pool = self.model.pool
+        if pool is None or not pool.host_pool:
+            return False
+        from . import host_pool as hp
+
+        return not hp.get(pool.host_pool).on_device_path
 
     def _ensure_graph(self):
         if not self.use_graph:
             return
+        if self._host_pool_off_device():
+            self.graph = self.graph_greedy = None  # file-mode host pool: every step runs eagerly
+            return
         state = self._param_state()
-        if self.graph is not None and state == self._captured_state:
+        if self.graph is not None and self._same_state(state, self._captured_state):
             return
         self.graph = self.graph_greedy = None  # parameters moved or the pool's keys changed: capture again
         # warm up on a side stream (key packing, temperature, workspaces)

@@ -51,7 +51,9 @@ def _capturing() -> bool:
 
 class _KeyCache:
     """Normalised + MFMA-packed sub-keys, rebuilt when the parameter changes
-    (tracked by storage pointer and torch's in-place version counter).
+    (tracked by tensor identity, storage pointer and torch's in-place
+    version counter: a new tensor at a freed tensor's address, whose version
+    counter starts again at 0, is a change).
 
     Under HIP graph capture the pack is recorded into the graph (so every
     replay packs the keys as they are then) unless ``frozen``: a caller that
@@ -60,6 +62,7 @@ class _KeyCache:
 
     def __init__(self):
         self.key = None
+        self.src = None  # the keys tensor the cache was built from (held, so its identity stays unique)
         self.k_hat = None
         self.packed = None
         self.frozen = False
@@ -68,9 +71,9 @@ class _KeyCache:
         key = (sub_keys.data_ptr(), sub_keys._version, tuple(sub_keys.shape), score_code)
         if _capturing() and not self.frozen:
             return self._pack(sub_keys, score_code)
-        if key != self.key:
+        if key != self.key or sub_keys is not self.src:
             self.k_hat, self.packed = self._pack(sub_keys, score_code)
-            self.key = key
+            self.key, self.src = key, sub_keys
         return self.k_hat, self.packed
 
     @staticmethod
@@ -188,6 +191,7 @@ class MemoryPool:
         self.score_dtype = score_dtype
         self._keys = _KeyCache()
         self._temp_key = None
+        self._temp_src = None
         self._temp_tensor = None
 
     @property
@@ -235,12 +239,13 @@ class MemoryPool:
         computed on the device (no host read), cached per parameter version
         outside graph capture."""
         key = (log_temperature.data_ptr(), log_temperature._version)
-        if (_capturing() and not self._keys.frozen) or key != self._temp_key:
+        if ((_capturing() and not self._keys.frozen) or key != self._temp_key
+                or log_temperature is not self._temp_src):
             lt = log_temperature.detach().reshape(1).to(torch.float32)
             t = torch.exp(lt.clamp(math.log(self.min_temperature), math.log(self.max_temperature)))
             if _capturing() and not self._keys.frozen:
                 return t
-            self._temp_tensor, self._temp_key = t, key
+            self._temp_tensor, self._temp_key, self._temp_src = t, key, log_temperature
         return self._temp_tensor
 
     # -------------------------------------------------------------- call
@@ -568,6 +573,7 @@ class _LookupFunction(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, queries, sub_keys, log_temperature, values, pool, opts):
+        _refuse_capture()
         params = {"sub_keys": sub_keys, "values": values, "log_temperature": log_temperature}
         res = pool.lookup(params, queries.detach(), train=opts["train"], noise_scale=opts["noise_scale"],
                           shuffle_reads=opts["shuffle_reads"], rngs=opts["rngs"])
@@ -582,6 +588,7 @@ class _LookupFunction(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, g_out, g_balance):
+        _refuse_capture()  # a forward run eagerly and a backward captured: refused too
         sub_keys, values = ctx.saved_tensors
         need_dv = ctx.needs_input_grad[3] and not ctx.opts["sparse_grad"]
         dq, dk, dlt, dv = _lookup_backward(ctx.pool, ctx.res, ctx.internal, sub_keys, values, ctx.shapes, g_out,
@@ -687,7 +694,19 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
     return dq.reshape(q_shape).to(q_dtype), dk.to(k_dtype), dlt.reshape(()).to(t_dtype), dv
 
 
+_CAPTURE_MSG = ("MemoryPool: torch autograd through the lookup is not supported under HIP graph capture (a "
+                "captured autograd training step crashed torch's graph instantiation on this stack); capture "
+                "MemoryPool.forward_backward instead, which runs the same forward and backward kernels without "
+                "autograd, or run the autograd step eagerly")
+
+
+def _refuse_capture() -> None:
+    if _capturing():
+        raise RuntimeError(_CAPTURE_MSG)
+
+
 def _lookup_with_grad(pool, params, queries, *, train, sparse_grad, noise_scale, shuffle_reads, rngs):
+    _refuse_capture()  # before any library call or allocation
     opts = {"train": train, "sparse_grad": sparse_grad, "noise_scale": noise_scale,
             "shuffle_reads": shuffle_reads, "rngs": rngs}
     if pool.host_pool and not sparse_grad:

@@ -6,6 +6,7 @@ Host mirror of the sparse half of the reference training step
   * ``fetched_row_grads(aux, probe_grads, layers, pool_size)``  train.py:146-163
   * ``merge_rows(slots, contribs, pool_size)``                 train.py:166-172
   * ``clip_scale(row_sq, rest_sq, grad_clip)``                 train.py:395-399
+  * ``sum_squares(tensors, add)`` (the dense gradients' norm)   train.py:395-397
   * ``rowwise_adagrad(...)``                                   train.py:412-416
   * ``lazy_adam(...)``                                         train.py:417-426
   * ``warmup_cosine(step, lr, warmup_steps, steps)``           train.py:100-103
@@ -17,6 +18,7 @@ scale are device scalars, so a step never synchronises with the host.
 
 from __future__ import annotations
 
+import ctypes as C
 import math
 from dataclasses import dataclass
 from typing import Dict, Optional, Sequence
@@ -123,6 +125,30 @@ def clip_scale(row_sq: torch.Tensor, rest_sq: Optional[torch.Tensor], grad_clip:
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     check(L.mpl_clip_scale(ptr(row_sq.contiguous()), row_sq.shape[0], ptr(rest_sq), float(grad_clip), ptr(out),
                            ptr(ws), wsb, _lib.stream_ptr(dev)), "mpl_clip_scale")
+    return out
+
+
+def sum_squares(tensors: Sequence[torch.Tensor], add: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """train.py:395-397: the squared global norm of the dense gradients,
+    sum of x^2 over ``tensors`` (fp32, at most 8; each made contiguous) plus
+    ``add`` (a device scalar or None), as a device fp32 tensor [1].  Fixed
+    order with fp64 accumulation, no memset: it captures in a HIP graph, where
+    torch's multi-block sum records a memset of its semaphores."""
+    if len(tensors) > 8:
+        head = sum_squares(tensors[:8], add)
+        return sum_squares(tensors[8:], head)
+    dev = tensors[0].device if tensors else add.device
+    xs = [t.detach().reshape(-1).float().contiguous() for t in tensors]
+    out = torch.empty(1, dtype=torch.float32, device=dev)
+    if add is not None:
+        add = add.reshape(1).float().contiguous()
+    L = _lib.lib()
+    wsb = L.mpl_sum_squares_workspace_bytes()
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    ptrs = (C.c_void_p * max(len(xs), 1))(*[x.data_ptr() for x in xs])
+    ns = (C.c_int64 * max(len(xs), 1))(*[x.numel() for x in xs])
+    check(L.mpl_sum_squares(C.cast(ptrs, C.c_void_p), C.cast(ns, C.c_void_p), len(xs), ptr(add), ptr(out), ptr(ws),
+                            wsb, _lib.stream_ptr(dev)), "mpl_sum_squares")
     return out
 
 

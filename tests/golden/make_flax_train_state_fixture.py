@@ -4,10 +4,25 @@ checkpoints laid out as the reference's save_checkpoint writes them
 dataclass, fields step, params, opt_state, subkey_usage, slot_usage, pool_m,
 pool_v).  Built from raw msgpack primitives only, as flax >= 0.8.5 encodes
 them (maps; arrays as ext type 1 holding msgpack((shape, dtype name, C-order
-bytes)); numpy scalars such as the int32 step as ext type 3), so the reader
-is checked against the published encoding, not against its own writer.
+bytes))), so the reader is checked against the published encoding, not
+against its own writer.  The reference writes to_bytes(jax.device_get(state)):
+device_get turns every jax array, the 0-d int32 step and optax's counts
+included, into a numpy ndarray, which Flax writes as ext type 1 (ext type 3
+is for numpy scalars, which such a state does not hold).
 Row-wise Adagrad keeps its accumulator in pool_v [N] with an empty pool_m
 (train.py:284-285); lazy Adam keeps both moments [N, d] (train.py:286-287).
+
+opt_state restates the layout of the sparse-mode optimizer (train.py:106-132,
+clip=False): optax.chain(optax.adamw(schedule, mask=...), scale_pool_values),
+a tuple of (adamw's chain state, EmptyState).  adamw's state is the tuple
+(ScaleByAdamState(count, mu, nu), MaskedState(inner_state=EmptyState) of the
+masked weight decay, ScaleByScheduleState(count)).  Flax writes a tuple as a
+map with keys "0", "1", ..., a NamedTuple as a map of its fields and an
+EmptyState as an empty map.  optax is absent here, so this nesting is
+restated from optax's published sources (>= 0.2.3, requirements.txt:3) and
+is an approximation of what a given optax version writes; the reader treats
+opt_state as an opaque nested tree, so its layout does not change what is
+read.
 
 Run: python tests/golden/make_flax_train_state_fixture.py
 """
@@ -60,12 +75,16 @@ def _enc(tree):
 def main():
     for opt, path in OUT.items():
         a = arrays(opt)
-        step = _ext(np.array(STEP, dtype=np.int32), code=3)
-        # optax chain(clip_by_global_norm, adamw) state over the dense params:
-        # a tuple -> {"0": EmptyState {}, "1": ScaleByAdamState {count, mu, nu}, ...}
-        dense = {"router_1": a["params"]["router_1"]}
-        opt_state = {"0": {}, "1": {"count": _ext(np.array(STEP, dtype=np.int32), code=3),
-                                     "mu": _enc(dense), "nu": _enc(dense)}, "2": {}}
+        step = _ext(np.array(STEP, dtype=np.int32))
+        # chain(adamw, scale_pool_values) over the dense params (the pool values
+        # are split out in sparse mode, train.py:76-87)
+        dense = {"router_1": a["params"]["router_1"],
+                 "pool": {k: v for k, v in a["params"]["pool"].items() if k != "values"}}
+        count = _ext(np.array(STEP, dtype=np.int32))
+        adamw = {"0": {"count": count, "mu": _enc(dense), "nu": _enc(dense)},  # ScaleByAdamState
+                 "1": {"inner_state": {}},                                   # MaskedState(EmptyState)
+                 "2": {"count": count}}                                      # ScaleByScheduleState
+        opt_state = {"0": adamw, "1": {}}
         state = {"step": step, "params": _enc(a["params"]), "opt_state": opt_state,
                  "subkey_usage": _ext(a["subkey_usage"]), "slot_usage": _ext(a["slot_usage"]),
                  "pool_m": _ext(a["pool_m"]), "pool_v": _ext(a["pool_v"])}

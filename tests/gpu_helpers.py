@@ -31,10 +31,12 @@ def make_params(pool: MemoryPool, seed: int, *, key_std=None, value_std=None, de
 
 
 def oracle_check(pool: MemoryPool, params, queries: torch.Tensor, res, *, gumbel=None, noise_coef=0.0,
-                 shuffle_reads=False, min_tie_free=0.5):
-    """Asserts parity of one GPU lookup result `res` against the oracle."""
+                 shuffle_reads=False, min_tie_free=0.5, tol=None):
+    """Asserts parity of one GPU lookup result `res` against the oracle
+    (``tol``: the relative tolerance, by default the parity rule's for the
+    pool's scoring precision)."""
     H, n, k, d = pool.heads, pool.n_sub_keys, pool.top_k, pool.d_value
-    tol = TOL[pool.score_dtype]
+    tol = TOL[pool.score_dtype] if tol is None else tol
     q = queries.detach().float().cpu().numpy()
     keys = params["sub_keys"].detach().float().cpu().numpy()
     log_t = float(params["log_temperature"].cpu())

@@ -72,3 +72,6 @@ def test_row_entry_points_validate_before_launch():
     assert L.mpl_clip_scale_workspace_bytes() >= 8
     rc = L.mpl_clip_scale(None, 10, None, 1.0, None, None, 0, None)
     assert rc == 1
+    assert L.mpl_sum_squares_workspace_bytes() >= 8
+    rc = L.mpl_sum_squares(None, None, 9, None, None, None, 0, None)
+    assert rc == 1 and b"at most 8" in L.mpl_last_error()

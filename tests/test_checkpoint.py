@@ -4,7 +4,9 @@ written by model_amd/checkpoint.py, on the CPU.
 tests/golden/flax_params_small.msgpack is encoded from raw msgpack
 primitives the way flax.serialization.to_bytes encodes a parameter tree
 (tests/golden/make_flax_params_fixture.py): array leaves as ext type 1,
-numpy scalars as ext type 3, and the value table as a chunked array."""
+numpy scalars as ext type 3 (read; the writer, like the reference's
+to_bytes(device_get(state)), emits only ndarrays), and the value table as a
+chunked array."""
 
 import io
 import os
@@ -106,7 +108,10 @@ def test_reads_train_state_and_resumes_row_update(opt):
     np.testing.assert_array_equal(st["params"]["pool"]["values"].numpy(), want["params"]["pool"]["values"])
     assert st["params"]["pool"]["values"].dtype == torch.float32  # kept fp32: the master copy
     np.testing.assert_array_equal(st["subkey_usage"].numpy(), want["subkey_usage"])
-    assert int(st["opt_state"]["1"]["count"]) == ts_fix.STEP and st["opt_state"]["0"] == {}
+    adamw = st["opt_state"]["0"]
+    assert int(adamw["0"]["count"]) == ts_fix.STEP and int(adamw["2"]["count"]) == ts_fix.STEP
+    assert adamw["1"] == {"inner_state": {}} and st["opt_state"]["1"] == {}
+    assert "values" not in adamw["0"]["mu"]["pool"]
     N, d = want["params"]["pool"]["values"].shape
     table = torch.zeros((N, d), dtype=torch.float16)
     upd = R.SparseRowUpdate(table, optimizer="rowwise_adagrad" if opt == "adagrad" else "adam")
@@ -144,4 +149,14 @@ def test_train_state_writer_round_trip():
     for k in ("pool_m", "pool_v", "subkey_usage", "slot_usage"):
         assert torch.equal(back[k], st[k]), k
     assert torch.equal(back["params"]["pool"]["values"], st["params"]["pool"]["values"])
-    assert torch.equal(back["opt_state"]["1"]["mu"]["router_1"]["kernel"], st["opt_state"]["1"]["mu"]["router_1"]["kernel"])
+    mu = ("0", "0", "mu", "router_1", "kernel")
+    a, b = back["opt_state"], st["opt_state"]
+    for k in mu:
+        a, b = a[k], b[k]
+    assert torch.equal(a, b)
+    # every leaf is written as Flax writes device_get'd arrays: ext type 1, the 0-d step too
+    import msgpack
+
+    raw = msgpack.unpackb(buf.getvalue(), raw=False, strict_map_key=False)
+    assert isinstance(raw["step"], msgpack.ExtType) and raw["step"].code == 1
+    assert raw["opt_state"]["0"]["0"]["count"].code == 1

@@ -228,15 +228,19 @@ def test_queries_backward_16_byte_form_equals_dword_form(gpu_lib, with_len, k):
     torch.testing.assert_close(fast, dword, rtol=1e-5, atol=1e-5 * float(dword.abs().max()))
 
 
+@pytest.mark.parametrize("shuffle", [0, 1])
+@pytest.mark.parametrize("H,k", [(4, 16), (2, 16), (4, 8)])
 @pytest.mark.parametrize("dtype,d", [(torch.float32, 256), (torch.float16, 512)])
-def test_route_backward_1k_rows_equal_generic_form(gpu_lib, dtype, d):
+def test_route_backward_1k_rows_equal_generic_form(gpu_lib, dtype, d, H, k, shuffle):
     """mpl_lookup_bwd_route with 1 KB value rows (fp32 d = 256, fp16 d = 512)
     reads a row per 16-byte load instruction and reduce-scatters the lane
     dots; with the table 4-byte aligned only it takes the per-element loop.
-    The two differ only in the order each dot is summed."""
+    The two differ only in the order each dot is summed.  H * k = 64 fills
+    the wave; 32 leaves lanes without a row (they read row 0 and drop it);
+    shuffle_reads reads (slot + N/2 + 1) % N in both forms."""
     from model_amd import _lib
 
-    M, H, k, N = 200, 4, 16, 4096
+    M, N = 200, 4096
     g = torch.Generator(device="cuda").manual_seed(d)
     vals = (torch.randn((N, d), generator=g, device="cuda") * 0.05).to(dtype)
     slots = torch.randint(0, N, (M, H, k), generator=g, device="cuda", dtype=torch.int32)
@@ -256,7 +260,7 @@ def test_route_backward_1k_rows_equal_generic_form(gpu_lib, dtype, d):
         ds = torch.empty((M, H, 2, k), device="cuda")
         lt = torch.empty((M,), device="cuda")
         _lib.check(gpu_lib.mpl_lookup_bwd_route(p(g_out), p(v), vdt, N, d, p(slots), p(w), p(flat), p(sub_scores),
-                                                M, H, k, 0, p(dw), p(ds), p(lt),
+                                                M, H, k, shuffle, p(dw), p(ds), p(lt),
                                                 torch.cuda.current_stream().cuda_stream), "route")
         torch.cuda.synchronize()
         return dw, ds, lt

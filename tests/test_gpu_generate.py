@@ -164,3 +164,106 @@ def test_decode_embed_matches_torch(gpu_lib, B, V, P, d):
     assert torch.isnan(out[0]).all() and torch.isfinite(out[1:]).all()
     out = decode_embed(emb, pos_emb, tok, torch.tensor([P], dtype=torch.int64, device="cuda"))
     assert torch.isnan(out).all()
+
+
+@pytest.mark.parametrize("mode", ["ram", "file"])
+@pytest.mark.parametrize("graph", [True, False])
+def test_kv_cache_decoding_matches_full_forward_host_pool(gpu_lib, tmp_path, mode, graph):
+    """tests/test_memory_pool.py:486-502 [host]: an fp16 HostPool (generate.py
+    over host_pool.py:206-220): decode logits equal the full forward at atol
+    1e-4, and tokens and logits equal a generator over the same table in HBM.
+    RAM mode captures the decode step (the GPU reads the pinned table); file
+    mode runs it eagerly whatever ``graph`` says."""
+    from model_amd import host_pool as hp
+
+    base = _cfg(torch.float16)
+    pool = hp.HostPool(base.pool_size, base.d_value, path=None if mode == "ram" else str(tmp_path / "pool"),
+                       trainable=False, dtype=np.float16, seed=4)
+    cfg = ModelConfig(**{**base.__dict__, "host_pool": pool.name})
+    toks = torch.tensor(np.random.default_rng(0).integers(0, 50, (2, 12)), device="cuda")
+    model = MemoryPoolLM(cfg)
+    params = model.init(1)
+    assert "values" not in params["params"]["pool"]
+    with torch.no_grad():
+        full, _ = model.apply(params, toks)
+    gen = Generator(cfg, params, batch_size=2, graph=graph)
+    res = gen.generate(toks.cpu().numpy(), n_new=3)
+    np.testing.assert_allclose(res["logits"][:, :12].cpu().numpy(), full.cpu().numpy(), atol=1e-4)
+    assert res["tokens"].shape == (2, 3)
+    assert (gen.graph is not None) == (graph and mode == "ram")
+    # the same parameters with the pool's table in HBM
+    hbm = {"params": dict(params["params"])}
+    hbm["params"]["pool"] = dict(params["params"]["pool"],
+                                 values=torch.from_numpy(np.asarray(pool.values)).to("cuda"))
+    ref = Generator(base, hbm, batch_size=2, graph=graph).generate(toks.cpu().numpy(), n_new=3)
+    assert torch.equal(res["tokens"], ref["tokens"])
+    np.testing.assert_allclose(res["logits"].cpu().numpy(), ref["logits"].cpu().numpy(), rtol=0, atol=1e-6)
+    # a second generation over the captured step starts clean
+    again = gen.generate(toks.cpu().numpy(), n_new=3)
+    assert torch.equal(again["tokens"], res["tokens"]) and torch.equal(again["logits"], res["logits"])
+
+
+def test_generator_follows_pool_parameters_replaced(gpu_lib):
+    """A pool parameter replaced by a new tensor of the same shape between
+    generate() calls (possibly at the freed tensor's address, where its
+    version counter starts again at 0) is a change: the next generate()
+    uses the new keys and temperature, as an eager step does."""
+    cfg = ModelConfig(vocab_size=300, max_len=40, d_model=64, n_heads=4, n_layers=2, ffn_mult=2, n_sub_keys=64,
+                      pool_heads=4, d_key=64, d_value=64, top_k=8, memory_layers=(0, 1))
+    params = MemoryPoolLM(cfg).init(7)
+    prompt = np.random.default_rng(5).integers(0, 300, (4, 10))
+    gen = Generator(cfg, params, batch_size=4, graph=True)
+    before = gen.generate(prompt, n_new=8)
+    pool = params["params"]["pool"]
+    new_keys = (pool["sub_keys"] * -1.0 + 0.3).contiguous()
+    new_lt = pool["log_temperature"] + 0.7
+    del pool["sub_keys"], pool["log_temperature"]
+    pool["sub_keys"], pool["log_temperature"] = new_keys, new_lt
+    after = gen.generate(prompt, n_new=8)
+    eager = Generator(cfg, params, batch_size=4, graph=False).generate(prompt, n_new=8)
+    assert torch.equal(after["logits"], eager["logits"])
+    assert not torch.equal(after["logits"], before["logits"])
+
+
+def test_generation_at_the_268M_slot_shapes(gpu_lib):
+    """A short greedy generation at the 268M-slot decode shapes: n_sub_keys
+    16,384 (268,435,456 fp16 slots, 137 GB), vocab 16,384, d_model 256, 4
+    layers with memory layers 1 and 3, 64 streams, 16 prompt tokens and 8
+    new ones.  The captured step equals the eager one bit for bit, and the
+    decode logits equal the full forward over the same tokens within the
+    fp16 rule (1e-2 of the largest |logit|: near-tied slots may be chosen
+    differently by the two paths' query rounding)."""
+    n, d, B, P, new = 16384, 256, 64, 16, 8
+    cfg = ModelConfig(vocab_size=16384, max_len=P + new, d_model=256, n_layers=4, n_heads=4, ffn_mult=4,
+                      memory_layers=(1, 3), n_sub_keys=n, pool_heads=4, d_key=256, d_value=d, top_k=16,
+                      values_dtype=torch.float16)
+    free, _ = torch.cuda.mem_get_info()
+    if free < 150 * 2 ** 30:
+        pytest.skip(f"needs 150 GiB of free device memory, {free / 2 ** 30:.0f} GiB free")
+    g = torch.Generator(device="cuda").manual_seed(17)
+    values = torch.empty((n * n, d), dtype=torch.float16, device="cuda")
+    values.normal_(0.0, 0.02, generator=g)
+    print("268M-slot table filled", flush=True)
+    try:
+        model = MemoryPoolLM(cfg)
+        params = model.init(0, pool_values=values)
+        prompt = torch.randint(0, cfg.vocab_size, (B, P), generator=g, device="cuda")
+        a = Generator(cfg, params, batch_size=B, graph=True).generate(prompt, n_new=new)
+        b = Generator(cfg, params, batch_size=B, graph=False).generate(prompt, n_new=new)
+        print("graph and eager generations done", flush=True)
+        assert torch.equal(a["tokens"], b["tokens"]) and torch.equal(a["logits"], b["logits"])
+        seq = torch.cat([prompt, a["tokens"][:, :-1]], 1)  # the tokens every decode step was fed
+        with torch.no_grad():
+            full, _ = model.apply(params, seq)
+        lg = a["logits"].float()
+        assert lg.shape == full.shape == (B, P + new - 1, cfg.vocab_size)
+        scale = float(full.abs().max())
+        err = float((lg - full).abs().max())
+        assert err <= 1e-2 * scale, (err, scale)
+        close = ((lg - full).abs().amax(-1) <= 1e-4 * scale).float().mean()
+        print(f"max |decode - full| {err:.3g} of max |logit| {scale:.3g}; positions within 1e-4 of it: "
+              f"{float(close):.1%}", flush=True)
+    finally:
+        del values
+        params = None
+        torch.cuda.empty_cache()

@@ -159,6 +159,26 @@ def test_clip_scale(gpu_lib):
     assert float(s[0]) == 1.0
 
 
+def test_sum_squares_fixed_order(gpu_lib):
+    """The dense part of the global norm (train.py:395-397) over several
+    buffers (ragged sizes, an empty one, one below the chunk count) plus a
+    device scalar: the fp64 sum within 1e-7 relative, the empty sum, and the
+    same bits on a repeat."""
+    rng = np.random.default_rng(8)
+    arrs = [rng.standard_normal(n).astype(np.float32) for n in (262144, 0, 7, 524288 + 13, 1)]
+    add = np.float32(3.25)
+    ts = [torch.as_tensor(a, device="cuda") for a in arrs]
+    got = R.sum_squares(ts, torch.tensor([add], device="cuda"))
+    want = sum(float((a.astype(np.float64) ** 2).sum()) for a in arrs) + float(add)
+    assert abs(float(got) / want - 1.0) < 1e-7
+    assert torch.equal(got, R.sum_squares(ts, torch.tensor([add], device="cuda")))
+    assert float(R.sum_squares([ts[1]], None)) == 0.0
+    assert float(R.sum_squares([], torch.tensor([2.5], device="cuda"))) == 2.5
+    # nine buffers: two calls chained through ``add``
+    many = R.sum_squares([ts[2]] * 9)
+    assert abs(float(many) / (9 * float((arrs[2].astype(np.float64) ** 2).sum())) - 1.0) < 1e-7
+
+
 def test_adagrad_known_answer(gpu_lib):
     """tests:505-513: ones on rows [3, 7] + padding 1000: only rows 3 and 7
     change, acc[3] == 1.0."""

@@ -61,7 +61,7 @@ def test_autograd_training_step_graph_replays_match_eager(gpu_lib):
         out, aux = pool.apply({"params": {"sub_keys": keys, "values": values, "log_temperature": log_t}}, q,
                               train=True, sparse_grad=True, noise_scale=noise_scale, rngs={"routing": 5})
         gq, gk, gt = torch.autograd.grad([out, aux["balance_loss"]], [q, keys, log_t], grad_outputs=[g_out, g_bal])
-        rest = (gk.square().sum() + gt.square()).reshape(1)
+        rest = R.sum_squares([gk, gt])  # fixed order, no memset node in the graph
         upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest)
         return gq, gk, gt
 
@@ -151,7 +151,7 @@ def test_training_step_graph_replays_match_eager(gpu_lib):
         params = {"sub_keys": keys, "values": values, "log_temperature": log_t}
         out, aux, (gq, gk, gt) = pool.forward_backward({"params": params}, q, g_out, g_bal, train=True,
                                                        noise_scale=noise_scale, rngs={"routing": 5})
-        rest = (gk.square().sum() + gt.square()).reshape(1)
+        rest = R.sum_squares([gk, gt])  # fixed order, no memset node in the graph
         upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest)
         return out, gq, gk, gt
 
@@ -185,3 +185,75 @@ def test_training_step_graph_replays_match_eager(gpu_lib):
         assert not torch.equal(values, values0)  # the step did update rows
         torch.randn(4096, device="cuda").sum().item()  # unrelated eager work between replays
         print("replay", i, "equal", flush=True)
+
+
+def _graph_node_types(graph):
+    """Node types of a captured graph (keep_graph=True), read through the
+    HIP runtime's hipGraphGetNodes / hipGraphNodeGetType."""
+    import ctypes as C
+
+    hip = C.CDLL("libamdhip64.so")
+    g = C.c_void_p(int(graph.raw_cuda_graph()))
+    n = C.c_size_t(0)
+    assert hip.hipGraphGetNodes(g, None, C.byref(n)) == 0
+    nodes = (C.c_void_p * n.value)()
+    assert hip.hipGraphGetNodes(g, nodes, C.byref(n)) == 0
+    types = []
+    for i in range(n.value):
+        t = C.c_int(-1)
+        assert hip.hipGraphNodeGetType(C.c_void_p(nodes[i]), C.byref(t)) == 0
+        types.append(t.value)
+    return types
+
+
+def test_captured_training_step_has_no_memset_nodes(gpu_lib):
+    """The captured step (forward with noise, backward, the dense gradients'
+    norm, merge, clip, Adagrad) records no memset node, which has given wrong
+    results on replays after the first on these GPUs.  The graph still
+    replays to the eager result."""
+    pool, keys0, values0, q0, g_out = _setup()
+    g_bal = torch.full((), 0.01, device="cuda")
+    keys, values = keys0.clone(), values0.clone()
+    log_t = torch.tensor(math.log(12.0), device="cuda")
+    upd = R.SparseRowUpdate(values, lr=1e-3, pool_lr_mult=3.0, warmup_steps=0, steps=1000, grad_clip=1.0)
+    acc0, master0 = upd.acc.clone(), upd.master.clone()
+
+    def reset():
+        keys.copy_(keys0)
+        values.copy_(values0)
+        upd.acc.copy_(acc0)
+        upd.master.copy_(master0)
+        upd.step = 0
+
+    def step():
+        params = {"sub_keys": keys, "values": values, "log_temperature": log_t}
+        out, aux, (gq, gk, gt) = pool.forward_backward({"params": params}, q0, g_out, g_bal, train=True,
+                                                       rngs={"routing": 9})
+        rest = R.sum_squares([gk, gt])
+        upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest)
+        return out, gk
+
+    reset()
+    want = [t.clone() for t in step()] + [values.clone()]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        reset()
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    reset()
+    graph = torch.cuda.CUDAGraph(keep_graph=True)
+    with torch.cuda.graph(graph):
+        outs = step()
+    types = _graph_node_types(graph)
+    print("graph nodes by type:", {t: types.count(t) for t in set(types)}, flush=True)
+    assert types.count(0) > 20  # kernel nodes
+    assert types.count(2) == 0, "memset node in the captured step"
+    graph.instantiate()
+    for i in range(2):
+        reset()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, a, b in zip(("out", "d_sub_keys", "values"), list(outs) + [values], want):
+            assert torch.equal(a, b), (i, name)

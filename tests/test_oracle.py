@@ -197,7 +197,8 @@ def test_balance_loss_detects_collapse():
 
 
 # ------------------------------------------------------------------ A13
-def _torch_forward(q, raw_keys, values, log_t, res, *, n, query_scale, balance_temperature_grad, f):
+def _torch_forward(q, raw_keys, values, log_t, res, *, n, query_scale, balance_temperature_grad, f,
+                   min_t=10.0, max_t=100.0):
     """Independent torch restatement of memory.py:136-213 with the selection
     held fixed at the oracle's (sub_idx, flat_idx)."""
     H, _, _, half = raw_keys.shape
@@ -207,7 +208,7 @@ def _torch_forward(q, raw_keys, values, log_t, res, *, n, query_scale, balance_t
     q_len = torch.sqrt((qq * qq).sum(-1, keepdim=True) + 1e-6) / np.sqrt(half)
     qh = qq * torch.rsqrt((qq * qq).sum(-1, keepdim=True) + 1e-6)
     kh = raw_keys * torch.rsqrt((raw_keys * raw_keys).sum(-1, keepdim=True) + 1e-6)
-    lt = log_t + (torch.clamp(log_t, np.log(10.0), np.log(100.0)) - log_t).detach()
+    lt = log_t + (torch.clamp(log_t, np.log(min_t), np.log(max_t)) - log_t).detach()
     T = torch.exp(lt)
     cos = torch.einsum("mhcd,hcnd->mhcn", qh, kh)
     scores = cos * T
@@ -226,12 +227,21 @@ def _torch_forward(q, raw_keys, values, log_t, res, *, n, query_scale, balance_t
     return out, bal
 
 
-@pytest.mark.parametrize("query_scale,btg,g_bal", [(False, False, 0.0), (True, False, 0.7), (False, True, 1.3)])
-def test_backward_matches_torch_autograd(query_scale, btg, g_bal):
+@pytest.mark.parametrize("query_scale,btg,g_bal,log_t,min_t,max_t", [
+    (False, False, 0.0, np.log(20.0), 10.0, 100.0),
+    (True, False, 0.7, np.log(20.0), 10.0, 100.0),
+    (False, True, 1.3, np.log(20.0), 10.0, 100.0),
+    # the clamp engaged (memory.py:143-146): below the floor, above the ceiling
+    (False, False, 0.5, np.log(2.0), 5.0, 100.0),
+    (False, True, 0.9, np.log(2.0), 10.0, 100.0),
+    (True, True, 0.4, np.log(500.0), 10.0, 100.0),
+])
+def test_backward_matches_torch_autograd(query_scale, btg, g_bal, log_t, min_t, max_t):
     q, keys, values = _inputs(11, M=12, n=16, d_key=8)
     raw = keys * 1.7  # non-unit raw keys so the normalisation backward matters
-    log_t = np.log(20.0)
-    res = ol.lookup_forward(q, raw, values, log_t, top_k_=K, query_scale=query_scale, dtype=np.float64)
+    res = ol.lookup_forward(q, raw, values, log_t, top_k_=K, query_scale=query_scale, dtype=np.float64,
+                            min_temperature=min_t, max_temperature=max_t)
+    assert res["temperature"] == np.float64(np.exp(np.clip(log_t, np.log(min_t), np.log(max_t))))
     aux = ol.aux_stats(res, n=16, noisy=False, balance_temperature_grad=btg)
     g = np.random.default_rng(12).standard_normal((12, D_VALUE))
     got = ob.lookup_backward(res, values, g, n=16, query_scale=query_scale, g_balance=g_bal,
@@ -241,7 +251,7 @@ def test_backward_matches_torch_autograd(query_scale, btg, g_bal):
     tv = torch.tensor(values, dtype=torch.float64, requires_grad=True)
     tl = torch.tensor(log_t, dtype=torch.float64, requires_grad=True)
     out, bal = _torch_forward(tq, tk, tv, tl, res, n=16, query_scale=query_scale,
-                              balance_temperature_grad=btg, f=aux["_f"])
+                              balance_temperature_grad=btg, f=aux["_f"], min_t=min_t, max_t=max_t)
     loss = (out * torch.tensor(g)).sum() + g_bal * bal
     loss.backward()
     np.testing.assert_allclose(got["d_queries"], tq.grad.numpy(), rtol=1e-9, atol=1e-12)
