@@ -183,6 +183,45 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
   }
 }
 
+// The final flush of a lane pair (lanes l and l + 32 share a query): the
+// pair's buffered candidates are read as one sequence (the par-0 lane's
+// column, cnt0 entries from base0, then the par-1 lane's from base1) and
+// each lane merges an even share of it, entries [s, t), into its own list;
+// the pair merge that follows combines the two lists.  A wave runs as many
+// chunks of 8 as its fullest lane needs, so the split takes the wave's count
+// from that of its fullest lane to that of its fullest pair, halved.
+template <int KMAX, bool NOISE>
+__device__ __forceinline__ void flush_pair_range(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
+                                                 const float* pay, int s, int t, int cnt0, uint32_t base0,
+                                                 uint32_t base1, bool empty) {
+  const int cnt = t - s;
+#pragma unroll 1
+  for (int c0 = 0; c0 < kCand; c0 += 8) {
+    if (__ballot(c0 < cnt) == 0) break;
+    u64 ch[8];
+    float cp[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const bool in = c0 + i < cnt;
+      const int e = s + c0 + i;
+      const uint32_t o = !in ? base0 : e < cnt0 ? base0 + (uint32_t)e * kEntryBytes
+                                                : base1 + (uint32_t)(e - cnt0) * kEntryBytes;
+      ch[i] = in ? make_key(lds_at(cs, o), (int)lds_at(ci, o)) : 0ull;
+      cp[i] = (NOISE && in) ? lds_at(pay, o) : 0.f;
+    }
+    sort8<NOISE>(ch, cp);
+    if (empty && c0 == 0) {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        st.top.key[i] = ch[i];
+        if (NOISE) st.top.pay[NOISE ? i : 0] = cp[i];
+      }
+    } else {
+      st.top.template merge<8>(ch, cp);
+    }
+  }
+}
+
 // k-th largest (k <= 32) of the 32 floats a[0..15], b[0..15]: bitonic sort
 // of the orderable bit patterns (max/min only), then a masked pick.
 __device__ __forceinline__ float kth_of_32(const float* a, const float* b, int k) {
@@ -448,7 +487,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   // buffer, then read block j+1 and run body() on block j with the next
   // block's MFMAs interleaved.  Past the end, DMAs copy clamped duplicates
   // and the one extra MFMA group scores one; nobody reads either.
-  auto sweep_lds = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
+  auto sweep_lds_on = [&](uint4* tile0, uint4* tile1, int bb, int be, auto&& body) __attribute__((always_inline)) {
     const int nb = be - bb;
     if (nb <= 0) return;
     dma(tile0, bb);
@@ -471,7 +510,14 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     // hold the wave's issue slot until each finishes.
     auto step = [&](int j, f32x16& c, f32x16& d, const uint4* rd, uint4* wr) __attribute__((always_inline)) {
       wait_vmcnt_le<kNoiseLoads>();
-      asm volatile("s_barrier" ::: "memory");
+      // The wave's reads of `wr` (block j, read in iteration j - 1) must have
+      // returned before any wave's DMA overwrites it: the compiler may sink
+      // the MFMAs that consume them below this barrier, and with them the
+      // wait for the reads.  A read still in flight when the DMA lands can
+      // return a torn 16-byte vector (half of each key block), whose score
+      // belongs to no key and can raise the bound pass's maxima above every
+      // real score.
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       dma(wr, min(bb + j + 2, be - 1));
       uint4 u[VPL];
 #pragma unroll
@@ -488,6 +534,9 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       step(j, x, y, tile1, tile0);
       step(j + 1, y, x, tile0, tile1);
     }
+  };
+  auto sweep_lds = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
+    sweep_lds_on(tile0, tile1, bb, be, body);
   };
 
   static_assert(!SHORT || (DIRECT && !NOISE), "short splits score on the register path without noise");
@@ -556,8 +605,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
 #pragma unroll
     for (int i = r * NCH / 16; i < (r + 1) * NCH / 16; ++i) issue(i);
   };
-  sweep(b_begin, p1_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
-                             __attribute__((always_inline)) {
+  auto bound_body = [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
+                        __attribute__((always_inline)) {
     float sv[16];
     const bool raw = !NOISE && kb + 32 <= p.n;  // wave-uniform
     if (!raw) lane_scores(kb, c, g, sv);
@@ -571,7 +620,22 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       ma[r] = max(ma[r], __float_as_int(v));
     }
     (void)active;
-  });
+  };
+  // The register path's bound pass streams each key block once per
+  // workgroup: the waves' 8 KB loads from L2 held the pass at the L2's
+  // delivery rate.  The block goes to LDS by DMA and both waves read it, in
+  // two tiles laid over the candidate arrays (unused until the select pass,
+  // which starts after every DMA has landed and both waves are past the
+  // last tile read).  The select pass keeps register-loaded keys.
+  constexpr bool LDS_BOUND = DIRECT && !SHORT && !NOISE && sizeof(cscore) >= TILE * sizeof(uint4) &&
+                             sizeof(cindex) >= TILE * sizeof(uint4);
+  if constexpr (LDS_BOUND) {
+    sweep_lds_on((uint4*)cscore, (uint4*)cindex, b_begin, p1_end, bound_body);
+    wait_vmcnt_le<0>();
+    __syncthreads();
+  } else {
+    sweep(b_begin, p1_end, bound_body);
+  }
   float fa[16];  // own maxima
 #pragma unroll
   for (int r = 0; r < 16; ++r) fa[r] = __int_as_float(ma[r]);
@@ -629,7 +693,17 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       }
     }
   });
-  flush_lane<false, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par, !flushed);
+  {
+    const int cnt_own = (int)((st.off - lane0) / kEntryBytes);
+    float ca = __int_as_float(cnt_own), cb = ca;
+    half_swap(ca, cb);
+    const int cnt_par = __float_as_int(par ? ca : cb);  // the partner lane's count
+    const int cnt0 = par ? cnt_par : cnt_own;            // the par-0 lane's count
+    const int tot = cnt_own + cnt_par, h = (tot + 1) >> 1;
+    const uint32_t base0 = par ? lane0 - 4u * 32u : lane0;  // the par-0 lane's column
+    flush_pair_range<KMAX, NOISE>(st, cscore, cindex, cpay, par ? h : 0, par ? tot : h, cnt0, base0,
+                                  base0 + 4u * 32u, !flushed);
+  }
 
   // Merge the two lanes' lists of the query: the partner's sorted list
   // arrives through v_permlane32_swap and is bitonic-merged (keys of the two

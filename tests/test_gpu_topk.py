@@ -155,3 +155,42 @@ def test_repeated_keys_tie_by_index_across_flushes(gpu_lib, M):
         assert np.all(sc[m, h, c] == sc[m, h, c, 0])  # one exact score for every copy
         checked += 1
     assert checked >= 1
+
+
+@pytest.mark.parametrize("M,n,noise", [(8192, 512, False), (8192, 512, True), (4096, 8192, False)])
+def test_stage1_repeats_bit_for_bit(gpu_lib, M, n, noise):
+    """The stage-1 kernel's LDS key tiles (the bound pass of the register
+    path; both passes with routing noise) are overwritten by DMA while the
+    waves go on: a read of a tile still in flight when the next block's DMA
+    lands returns a torn vector, a score of no key, which can lift the bound
+    above the k-th best and drop candidates, differently from run to run.
+    Eight launches on the same inputs at the text-study and 67M-slot key
+    widths, with and without noise, must give identical ids and scores."""
+    L = _lib.lib()
+    H, half, k = 4, 128, 16
+    g = torch.Generator(device="cuda").manual_seed(n + M + int(noise))
+    q = torch.randn((M, H, 2, half), generator=g, device="cuda")
+    keys = torch.randn((H, 2, n, half), generator=g, device="cuda") * half ** -0.5
+    gum = -torch.log(-torch.log(torch.rand((M, H, 2, n), generator=g, device="cuda").clamp_(1e-20, 1 - 1e-7))) \
+        if noise else None
+    st = _lib.stream_ptr(q.device)
+    packed = torch.empty(L.mpl_packed_keys_bytes(H, n, half, _lib.MPL_F16), dtype=torch.uint8, device="cuda")
+    _lib.check(L.mpl_pack_keys(_lib.ptr(keys), H, n, half, _lib.MPL_F16, None, _lib.ptr(packed), st), "pack")
+    T = torch.full((1,), 10.0, device="cuda")
+    coef = torch.full((1,), 1.0, device="cuda") if noise else None
+    wsb = L.mpl_score_topk_workspace_bytes(M, H, n, half, k)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device="cuda")
+    first = None
+    for it in range(8):
+        sub_idx = torch.full((M, H, 2, k), -7, dtype=torch.int32, device="cuda")
+        sub_sc = torch.full((M, H, 2, k), 7.0, device="cuda")
+        _lib.check(L.mpl_score_topk(_lib.ptr(q), _lib.MPL_Q_RAW, None, _lib.ptr(packed), M, H, n, half, k,
+                                    _lib.MPL_F16, _lib.ptr(T), _lib.ptr(gum), _lib.ptr(coef), _lib.ptr(ws), wsb,
+                                    _lib.ptr(sub_idx), _lib.ptr(sub_sc), st), "topk")
+        torch.cuda.synchronize()
+        if first is None:
+            first = (sub_idx, sub_sc)
+            assert bool((sub_idx >= 0).all()) and bool((sub_idx < n).all())
+        else:
+            assert torch.equal(sub_idx, first[0]), f"run {it}: {int((sub_idx != first[0]).sum())} ids differ"
+            assert torch.equal(sub_sc, first[1]), f"run {it}: scores differ"
