@@ -310,6 +310,43 @@ __device__ __forceinline__ float kth_of_pair16(const float* own, int par, int k)
   return from_orderable(r);
 }
 
+// The wave's MFMA query operand: lane l holds query row my_q (= the wave's
+// first query + l % 32), dims 16c + 8*(l/32) + [0,8) of chunk c (fp16; the
+// fp32 tile's map for fp32), and ql, the row's length factor (1 without
+// query_scale / q_len).  Rows out of range (!valid) are zeros.  With
+// write_qlen, mode RAW_SCALED also stores ql to out_qlen.
+template <typename T, int NCH>
+__device__ __forceinline__ void query_operand(const ScoreParams& p, int hc, int64_t my_q, bool valid, int lane,
+                                              bool write_qlen, typename Mfma<T>::Op (&qop)[NCH], float& ql) {
+  const int par = lane >> 5;
+  ql = 1.f;
+  if (p.query_mode == MPL_Q_NORMALIZED) {
+    const T* qrow = (const T*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::load_q(qrow, valid, p.half, c, lane);
+    if (p.q_len != nullptr) ql = p.q_len[(valid ? my_q : 0) * p.HC + hc];
+  } else {
+    // Raw fp32 queries, normalised here (memory.py:30-31, 136-137): the
+    // lane pair holds the row's 2*NCH*8 dims, so one half-swap completes
+    // the sum of squares.
+    const float* qrow = (const float*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
+    float x[NCH][Mfma<T>::kQElems];
+    float ss = 0.f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) Mfma<T>::load_q_raw(qrow, valid, p.half, c, lane, x[c], ss);
+    float a = ss, b = ss;
+    half_swap(a, b);
+    const float tot = ss + (par ? a : b) + 1e-6f;
+    const float rn = 1.0f / sqrtf(tot);
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::scale_q(x[c], rn);
+    if (p.query_mode == MPL_Q_RAW_SCALED) {
+      ql = sqrtf(tot) / sqrtf((float)p.half);
+      if (p.out_qlen != nullptr && valid && write_qlen && par == 0) p.out_qlen[my_q * p.HC + hc] = ql;
+    }
+  }
+}
+
 // SHORT (register path, no noise, splits of at most kShortBlocks blocks, the
 // decode-sized plans): each block is scored once and both passes read the
 // scores from the MFMA accumulators instead of reloading and re-scoring.
@@ -367,32 +404,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   }
 
   Op qop[NCH];
-  float ql = 1.f;
-  if (p.query_mode == MPL_Q_NORMALIZED) {
-    const T* qrow = (const T*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::load_q(qrow, valid, p.half, c, lane);
-    if (p.q_len != nullptr) ql = p.q_len[(valid ? my_q : 0) * p.HC + hc];
-  } else {
-    // Raw fp32 queries, normalised here (memory.py:30-31, 136-137): the
-    // lane pair holds the row's 2*NCH*8 dims, so one half-swap completes
-    // the sum of squares.
-    const float* qrow = (const float*)p.q_hat + (valid ? (my_q * p.HC + hc) * (int64_t)p.half : 0);
-    float x[NCH][Mfma<T>::kQElems];
-    float ss = 0.f;
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) Mfma<T>::load_q_raw(qrow, valid, p.half, c, lane, x[c], ss);
-    float a = ss, b = ss;
-    half_swap(a, b);
-    const float tot = ss + (par ? a : b) + 1e-6f;
-    const float rn = 1.0f / sqrtf(tot);
-#pragma unroll
-    for (int c = 0; c < NCH; ++c) qop[c] = Mfma<T>::scale_q(x[c], rn);
-    if (p.query_mode == MPL_Q_RAW_SCALED) {
-      ql = sqrtf(tot) / sqrtf((float)p.half);
-      if (p.out_qlen != nullptr && valid && split == 0 && par == 0) p.out_qlen[my_q * p.HC + hc] = ql;
-    }
-  }
+  float ql;
+  query_operand<T, NCH>(p, hc, my_q, valid, lane, split == 0, qop, ql);
   const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
   const uint32_t lane0 = 4u * (uint32_t)(wave * kCand * kWave + lane);  // the lane's first buffer entry
   const uint32_t flush_at = lane0 + (uint32_t)(kCand - 8) * kEntryBytes;
@@ -768,6 +781,130 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
           p.out_clean[o + r] = cl[r];
           p.out_idx[o + r] = id[r];
         }
+      }
+    }
+  }
+}
+
+// ------------------------------------------------------- decode stage 1
+// Decode-sized batches (M <= kDecodeMaxQ tokens, fp16 scoring, no routing
+// noise): score_topk_decode<HP, MQ, WPG>.  A workgroup of WPG waves takes
+// one codebook hc and 64*WPG consecutive keys, two key blocks per wave, for
+// all M queries.  Scoring is score_topk_kernel's MFMA chain with the
+// operands swapped (queries the A operand, keys the B operand): the tile's
+// lane l holds key l % 32 and, in register q < 4, query q, and every score
+// equals score_topk_kernel's bit for bit (the same products summed in the
+// same order).  One v_permlane32_swap puts each query's 64 scores of the two
+// blocks one per lane; a 64-lane bitonic sort leaves the wave's best 16 in
+// lanes 0-15; the workgroup's lists meet in LDS and are reduced four at a
+// time.  No bound pass and no candidate buffers: a decode wave has 64 keys
+// per query, and the kernel's length is its memory round trip and the
+// dependent exchange chain.
+constexpr int kDecodeMaxQ = 4;
+#ifndef MPL_DECODE_WAVES
+#define MPL_DECODE_WAVES 4
+#endif
+constexpr int kDecodeWaves = MPL_DECODE_WAVES;  // waves per workgroup (4, 8 or 16)
+static_assert(kDecodeWaves == 4 || kDecodeWaves == 8 || kDecodeWaves == 16, "decode workgroup of 4, 8 or 16 waves");
+
+template <int HP, int MQ, int WPG>
+__global__ __launch_bounds__(64 * WPG) void score_topk_decode(ScoreParams p) {
+  typedef _Float16 T;
+  constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);
+  constexpr int TILE = VPL * kWave;
+  constexpr int NG = WPG / 4;  // workgroup lists after the first reduction
+  typedef typename Mfma<T>::Op Op;
+  __shared__ u64 wl[WPG][MQ][16];
+  __shared__ u64 gl[NG > 1 ? NG : 1][MQ][16];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int hc = blockIdx.x % p.HC;
+  const int split = blockIdx.x / p.HC;
+  const int b0 = split * p.blk_per_split + 2 * wave;  // the wave's blocks b0, b0 + 1
+  const uint4* kb = p.packed + (int64_t)hc * p.nblk * TILE;
+  // Both blocks' B operands (clamped past the last block; those keys are
+  // dropped below), requested before the query: one memory round trip.
+  uint4 kv[2][VPL];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const uint4* src = kb + (int64_t)min(b0 + j, p.nblk - 1) * TILE + lane;
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) kv[j][v] = src[v * kWave];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  const int64_t my_q = lane & 31;
+  const bool valid = my_q < p.M;
+  Op qop[VPL];
+  float ql;
+  query_operand<T, VPL>(p, hc, my_q, valid, lane, split == 0 && wave == 0, qop, ql);
+  f32x16 x0 = f32x16{}, x1 = f32x16{};
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    x0 = Mfma<T>::mma(qop[v], Mfma<T>::from_vec(kv[0][v], 0), x0);
+    x1 = Mfma<T>::mma(qop[v], Mfma<T>::from_vec(kv[1][v], 0), x1);
+  }
+  // Query q's scores: block b0 in lanes 0-31, block b0 + 1 in lanes 32-63.
+  const int idx = (b0 + (lane >> 5)) * 32 + (lane & 31);
+  u64 key[MQ];
+#pragma unroll
+  for (int q = 0; q < MQ; ++q) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x0[q]), __float_as_uint(x1[q]), false, false);
+    const float s = __uint_as_float(r[0]);
+    // padded keys and scores that are not above -inf (NaN included) are
+    // never selected, as in score_topk_kernel
+    key[q] = (idx < p.n && s > -INFINITY) ? make_key(s, idx) : 0ull;
+  }
+  w64::sort64_desc<MQ>(key, lane);
+  if (lane < 16) {
+#pragma unroll
+    for (int q = 0; q < MQ; ++q) wl[wave][q][lane] = key[q];
+  }
+  __syncthreads();
+  // lane i of a reducing wave loads entry i % 16 of list i / 16 of its group
+  // of four, lists 1 and 3 reversed; lists past the end are empty
+  auto load4 = [&](const u64 (*lists)[MQ][16], int first, int count) __attribute__((always_inline)) {
+    const int t = lane >> 4, e = lane & 15;
+    const int ent = (t & 1) ? 15 - e : e;
+const int li = min(first + t, count - 1);
+#pragma unroll
+    for (int q = 0; q < MQ; ++q) {
+      const u64 kk = lists[li][q][ent];
+      key[q] = first + t < count ? kk : 0ull;
+    }
+    w64::best16_of4<MQ>(key, lane);
+  };
+  if constexpr (NG > 1) {
+    if (wave < NG) {
+      load4(wl, 4 * wave, WPG);
+      if (lane < 16) {
+#pragma unroll
+        for (int q = 0; q < MQ; ++q) gl[wave][q][lane] = key[q];
+      }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    load4(gl, 0, NG);
+  } else {
+    if (wave != 0) return;
+    load4(wl, 0, WPG);
+  }
+  // Lists [split][M][hc][k]: lane r < k writes rank r of each query.
+  const float Tv = *p.T;
+  float qls[MQ];  // query q's length factor, from lane q
+#pragma unroll
+  for (int q = 0; q < MQ; ++q) qls[q] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ql), q));
+  if (lane < p.k) {
+#pragma unroll
+    for (int q = 0; q < MQ; ++q) {
+      if (q < p.M) {
+        const float qlq = qls[q];
+        const u64 kk = key[q];
+        float clean = key_score(kk) * Tv;
+        clean *= qlq;  // 1 without query_scale
+        const int64_t o = (((int64_t)split * p.M + q) * p.HC + hc) * p.k + lane;
+        p.out_clean[o] = kk ? clean : -INFINITY;
+        p.out_idx[o] = kk ? key_index(kk) : -1;
       }
     }
   }
@@ -1305,6 +1442,168 @@ __global__ __launch_bounds__(1024) void pair_wide_read_k16(PairParams p, ReadPar
   }
 }
 
+// Stage 2 + value read for decode plans: 8 < S <= kDecodeMaxSplits split
+// lists, no noise (the lists' select score is the clean score, so a list
+// entry is its key alone), H = 4, k = 16, one row group per lane (VR <= 64).
+// One workgroup of 16 waves per token, every exchange on the VALU:
+//   1. wave w takes 16 lists of one codebook of head w % 4 (four groups of
+//      four, w64::best16_of4): 64 lists per head become 16, in LDS;
+//   2. wave h (< 4) reduces its head's 16 to one list per codebook (the
+//      codebooks' top-k, written to sub_idx / sub_scores), then runs the
+//      pair stage: of the k*k pairs (i, j) only the 50 with
+//      (i+1)(j+1) <= 16 can be among the best 16 (every pair (i', j') with
+//      i' <= i, j' <= j ranks before (i, j)), one per lane, and a 64-lane
+//      sort orders them by (select sum desc, flat index i*k + j asc), as
+//      memory.py:171-175; the softmax of the clean sums (memory.py:178) is
+//      pair_tail_k16's, row exchanges included, so weights match it bit
+//      for bit;
+//   3. each head's wave issues the loads of its 16 rows as soon as its
+//      weights are known (one memory round trip per head, the four heads
+//      overlapping) and puts them in LDS; wave 0 then adds the token's row
+//      groups in add_chunk's order, so `out` equals the two-launch path.
+constexpr int kDecodeMaxSplits = 32;
+
+template <typename V, int VR, bool NT>
+__global__ __launch_bounds__(1024) void pair_decode_read_k16(PairParams p, ReadParams rp) {
+  constexpr int K = 16;
+  typedef Wsum<V, VR, 16, NT> Sum;
+  static_assert(Sum::VPL == 1, "one vector per lane per row group");
+  constexpr int RPI = Sum::RPI, LPR = Sum::LPR;
+  constexpr int GROUPS = 64 / RPI;  // row groups of the token's 64 rows
+  constexpr int HG = GROUPS / 4;     // row groups of one head
+  __shared__ u64 l1[4][2][8][K];     // [head][codebook][list][rank] after step 1
+  __shared__ u64 l2[4][4][K];        // [head][list] within step 2
+  __shared__ u64 pab[4][2][K];       // [head][codebook] final lists
+  __shared__ int srow_slot[4 * K];
+  __shared__ float srow_w[4 * K];
+  __shared__ uint4 rows[GROUPS][kWave];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t m = blockIdx.x;  // the grid is exactly M workgroups
+  const int HC = 8;
+  const int64_t sstride = p.M * HC * K;
+  {
+    // step 1: wave w, head h = w % 4, codebook cb = (w / 4) >> 1 of the
+    // head, lists 16 * ((w / 4) & 1) + 4 * grp + lane / 16 (odd ones of a
+    // group reversed), past S empty
+    const int h = wave & 3, sub = wave >> 2, cb = sub >> 1;
+    const int c = 2 * h + cb;
+    const int t = lane >> 4, e = lane & 15;
+    const int ent = (t & 1) ? 15 - e : e;
+    int id[4];
+    float cl[4];
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const int s = 16 * (sub & 1) + 4 * grp + t;
+      const int64_t o = (int64_t)min(s, p.S - 1) * sstride + (m * HC + c) * K + ent;  // clamped, unconditional
+      id[grp] = p.idx[o];
+      cl[grp] = p.clean[o];
+    }
+    u64 key[4];
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      const int s = 16 * (sub & 1) + 4 * grp + t;
+      key[grp] = (s < p.S && id[grp] >= 0) ? make_key(cl[grp], id[grp]) : 0ull;
+    }
+    w64::best16_of4<4>(key, lane);
+    if (lane < K) {
+#pragma unroll
+      for (int grp = 0; grp < 4; ++grp) l1[h][cb][4 * (sub & 1) + grp][lane] = key[grp];
+    }
+  }
+  __syncthreads();
+  if (wave < 4) {
+    const int h = wave;
+    const int t = lane >> 4, e = lane & 15;
+    // step 2a: group g (cb = g >> 1) holds lists 4 * (g & 1) + t of codebook cb
+    u64 key[4];
+#pragma unroll
+    for (int g = 0; g < 4; ++g) key[g] = l1[h][g >> 1][4 * (g & 1) + t][(t & 1) ? 15 - e : e];
+    w64::best16_of4<4>(key, lane);
+    if (lane < K) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) l2[h][g][lane] = key[g];
+    }
+    // step 2b: lanes 0-31 hold codebook 0's two lists, lanes 32-63
+    // codebook 1's (second of each reversed): one bitonic split and a
+    // 16-lane merger leave codebook 0 in lanes 0-15, codebook 1 in 32-47
+    u64 v[1] = {l2[h][t][(t & 1) ? 15 - e : e]};
+    {
+      const u64 o = w64::xr64<16>(v[0], lane);
+      v[0] = o > v[0] ? o : v[0];
+    }
+    w64::merge_down<8, 1>(v, lane, true);
+    const u64 fk = v[0];
+    if ((lane & 16) == 0) {  // lanes 0-15: codebook 2h, lanes 32-47: 2h + 1
+      const int cb = lane >> 5;
+      const int64_t o0 = (m * HC + 2 * h + cb) * K + e;
+      p.sub_idx[o0] = fk ? key_index(fk) : -1;
+      p.sub_scores[o0] = fk ? key_score(fk) : -INFINITY;
+      pab[h][cb][e] = fk;
+    }
+    // the pair stage: lane l < 50 takes candidate (i, j), the l-th pair with
+    // (i+1)(j+1) <= 16 in row-major order
+    int pi = 0, pj = lane;
+    bool found = false;
+#pragma unroll
+    for (int i = 0; i < K; ++i) {
+      const int cnt = K / (i + 1);
+      const bool here = !found && pj < cnt;
+      pi = here ? i : pi;
+      pj = (!found && !here) ? pj - cnt : pj;
+      found = found || here;
+    }
+    const u64 ka = pab[h][0][pi], kb = pab[h][1][found ? pj : 0];
+    const bool ok = found && ka != 0ull && kb != 0ull;
+    u64 pk[1] = {ok ? make_key(key_score(ka) + key_score(kb), pi * K + pj) : 0ull};
+    w64::sort64_desc<1>(pk, lane);
+    const u64 acc = pk[0];
+    // lane r < 16 holds the rank-r pair (as pair_tail_k16)
+    const int flat = acc ? key_index(acc) : 0;
+    const u64 wa = pab[h][0][flat / K], wb = pab[h][1][flat % K];
+    int ia = wa ? key_index(wa) : 0;
+    int ib = wb ? key_index(wb) : 0;
+    ia = (ia >= 0 && ia < p.n) ? ia : 0;  // ids come from keys < n; guards non-finite inputs
+    ib = (ib >= 0 && ib < p.n) ? ib : 0;
+    const float pay = (wa ? key_score(wa) : -INFINITY) + (wb ? key_score(wb) : -INFINITY);
+    const float sc = acc ? pay : -INFINITY;
+    const float mx = g16::rmax(sc);
+    const float ex = acc ? expf(sc - mx) : 0.f;
+    const float sum = g16::rsum(ex);
+    const int slot = ia * p.n + ib;
+    const float w = ex / sum;
+    const int64_t mh = m * 4 + h;
+    if (lane < K) {
+      const int64_t ob = mh * K + lane;
+      p.slots[ob] = slot;
+      p.flat_idx[ob] = flat;
+      p.weights[ob] = w;
+      srow_w[h * K + lane] = w;
+    }
+    // step 3: the head's rows (row groups HG * h ..), loaded at once
+    const int64_t N = (int64_t)p.n * p.n;
+    const int rs = rp.shuffle ? (int)(((int64_t)slot + N / 2 + 1) % N) : slot;
+    uint4 buf[HG];
+#pragma unroll
+    for (int g = 0; g < HG; ++g) {
+      const int rr = g * RPI + lane / LPR;  // row of the head, 0..15
+      const int sr = __shfl(rs, rr);
+      const uint4* src = (const uint4*)rp.values + (int64_t)sr * VR + lane % LPR;
+      buf[g] = NT ? load_nt(src) : *src;
+    }
+#pragma unroll
+    for (int g = 0; g < HG; ++g) rows[h * HG + g][lane] = buf[g];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    Sum acc;
+#pragma unroll
+    for (int g = 0; g < GROUPS; ++g) acc.add_vec(rows[g][lane], srow_w[g * RPI + lane / LPR]);
+    acc.store(rp.out + m * (int64_t)(VR * Vec16<V>::kElems), lane);
+  }
+}
+
 // ---------------------------------------------------------------- host side
 struct Plan {
   int splits, blk_per_split, nblk, kmax, pass1_blocks;
@@ -1339,6 +1638,21 @@ static Plan make_plan(int64_t M, int H, int n, int k) {
   pl.kmax = k <= 16 ? 16 : 32;
   const int p1 = pl.blk_per_split / MPL_PASS1_DIV;
   pl.pass1_blocks = std::min(pl.blk_per_split, std::max(MPL_PASS1_MIN, p1));
+  return pl;
+}
+
+// Decode plans (score_topk_decode): M <= kDecodeMaxQ tokens and k <= 16,
+// with fp16 scoring and no noise; a split is one workgroup's 64*WPG keys.
+static bool decode_shape(int64_t M, int k) { return M >= 1 && M <= kDecodeMaxQ && k <= 16; }
+
+static Plan make_decode_plan(int n) {
+  Plan pl;
+  pl.nblk = (int)cdiv(n, 32);
+  pl.qblocks = 1;
+  pl.blk_per_split = 2 * kDecodeWaves;
+  pl.splits = (int)cdiv(pl.nblk, pl.blk_per_split);
+  pl.kmax = 16;
+  pl.pass1_blocks = 0;
   return pl;
 }
 
@@ -1377,6 +1691,26 @@ static void launch_stage1(const ScoreParams& sp, int64_t blocks, hipStream_t s) 
     }
   }
   score_topk_kernel<T, HP, NOISE, KMAX, D, false><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+}
+
+template <int HP>
+static void launch_decode(const ScoreParams& sp, int64_t blocks, hipStream_t s) {
+  const unsigned g = (unsigned)blocks;
+  constexpr int W = kDecodeWaves;
+  if (sp.M == 1) score_topk_decode<HP, 1, W><<<g, 64 * W, 0, s>>>(sp);
+  else if (sp.M == 2) score_topk_decode<HP, 2, W><<<g, 64 * W, 0, s>>>(sp);
+  else score_topk_decode<HP, 4, W><<<g, 64 * W, 0, s>>>(sp);
+}
+
+static int dispatch_decode(const ScoreParams& sp, int64_t blocks, int HP, hipStream_t s) {
+  switch (HP) {
+    case 16: launch_decode<16>(sp, blocks, s); break;
+    case 32: launch_decode<32>(sp, blocks, s); break;
+    case 64: launch_decode<64>(sp, blocks, s); break;
+    case 128: launch_decode<128>(sp, blocks, s); break;
+    default: return MPL_EUNSUPPORTED;
+  }
+  return MPL_OK;
 }
 
 template <typename T, int HP>
@@ -1425,19 +1759,25 @@ static size_t topk_extra_bytes(const Plan& pl, int64_t M, int H, int k) {
   return (pl.splits > 1 && k != 16) ? (size_t)M * H * k * 3 * 4 : 0;
 }
 
+// The sizes cover every plan a call of these shapes may take (the decode
+// plan depends on the scoring type and noise, which the size query lacks).
 extern "C" size_t mpl_score_select_workspace_bytes(int64_t M, int H, int n, int half, int k) {
   (void)half;
   if (M <= 0 || H <= 0 || n <= 0 || k <= 0) return 0;
-  const Plan pl = make_plan(M, H, n, k);
-  return ws_bytes(pl, M, H, k, true);
+  size_t need = ws_bytes(make_plan(M, H, n, k), M, H, k, true);
+  if (decode_shape(M, k)) need = std::max(need, ws_bytes(make_decode_plan(n), M, H, k, false));
+  return need;
 }
 
 extern "C" size_t mpl_score_topk_workspace_bytes(int64_t M, int H, int n, int half, int k) {
   (void)half;
   if (M <= 0 || H <= 0 || n <= 0 || k <= 0) return 0;
-  const Plan pl = make_plan(M, H, n, k);
-  const size_t extra = topk_extra_bytes(pl, M, H, k);
-  return (ws_bytes(pl, M, H, k, true) + 255) / 256 * 256 + extra;
+  auto need = [&](const Plan& pl, bool noise) {
+    return (ws_bytes(pl, M, H, k, noise) + 255) / 256 * 256 + topk_extra_bytes(pl, M, H, k);
+  };
+  size_t b = need(make_plan(M, H, n, k), true);
+  if (decode_shape(M, k)) b = std::max(b, need(make_decode_plan(n), false));
+  return b;
 }
 
 // Both entry points: stage 1 (+ the split-list reduction); with `pair`, stage
@@ -1511,6 +1851,38 @@ static bool launch_pair_wide_read(const LookupRead& lr, const PairParams& pp, hi
   return false;
 }
 
+// The decode stage 2 fused with the value read (pair_decode_read_k16): the
+// conditions of launch_pair_read and one row group per lane (VR <= 64);
+// returns false (nothing launched) otherwise.
+static bool launch_pair_decode_read(const LookupRead& lr, const PairParams& pp, hipStream_t s) {
+  const int esz = lr.dtype == MPL_F16 ? 2 : 4;
+  if (pp.H != 4 || pp.k != 16 || pp.sel != nullptr || pp.S > kDecodeMaxSplits || (lr.d * esz) % 16 != 0 ||
+      ((uintptr_t)lr.values % 16) != 0 || ((uintptr_t)lr.out % 16) != 0)
+    return false;
+  ReadParams rp;
+  rp.values = lr.values;
+  rp.shuffle = lr.shuffle;
+  rp.out = lr.out;
+  const int VR = lr.d * esz / 16;
+  const bool nt = (int64_t)pp.n * pp.n * lr.d * esz > kStreamTableBytes;
+  const unsigned grid = (unsigned)pp.M;
+#define MPL_PDR(V, vr)                                                    \
+  if (VR == vr) {                                                         \
+    if (nt)                                                               \
+      pair_decode_read_k16<V, vr, true><<<grid, 1024, 0, s>>>(pp, rp);    \
+    else                                                                  \
+      pair_decode_read_k16<V, vr, false><<<grid, 1024, 0, s>>>(pp, rp);   \
+    return true;                                                          \
+  }
+  if (lr.dtype == MPL_F16) {
+    MPL_PDR(_Float16, 16) MPL_PDR(_Float16, 32) MPL_PDR(_Float16, 64)
+  } else {
+    MPL_PDR(float, 32) MPL_PDR(float, 64)
+  }
+#undef MPL_PDR
+  return false;
+}
+
 static int select_impl(const char* who, bool pair, const void* queries, int query_mode, float* q_len,
                        const void* packed_keys, int64_t M, int H, int n, int half, int k, int score_dtype,
                        const float* temperature, const float* gumbel, const float* noise_coef, void* workspace,
@@ -1536,7 +1908,8 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   MPL_REQUIRE(query_mode == MPL_Q_NORMALIZED || query_mode == MPL_Q_RAW || query_mode == MPL_Q_RAW_SCALED,
               MPL_EINVAL, "%s: bad query_mode %d", who, query_mode);
   const bool noise = gumbel != nullptr;
-  const Plan pl = make_plan(M, H, n, k);
+  const bool decode = !noise && score_dtype == MPL_F16 && decode_shape(M, k);
+  const Plan pl = decode ? make_decode_plan(n) : make_plan(M, H, n, k);
   const size_t sel_need = ws_bytes(pl, M, H, k, noise);
   const size_t extra = pair ? 0 : topk_extra_bytes(pl, M, H, k);
   const size_t extra_at = (sel_need + 255) / 256 * 256;
@@ -1579,7 +1952,8 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   }
   const int HP = score_dtype == MPL_F16 ? KeyPack<_Float16>::padded_half(half) : KeyPack<float>::padded_half(half);
   const int64_t blocks = pl.qblocks * pl.splits * HC;
-  int rc = dispatch_stage1(sp, blocks, score_dtype, HP, noise, pl.kmax, s);
+  int rc = decode ? dispatch_decode(sp, blocks, HP, s)
+                  : dispatch_stage1(sp, blocks, score_dtype, HP, noise, pl.kmax, s);
   if (rc) {
     set_error("%s: unsupported padded half %d", who, HP);
     return rc;
@@ -1605,6 +1979,10 @@ static int select_impl(const char* who, bool pair, const void* queries, int quer
   // into one per level, so stage 2 merges at most 8 lists instead of a long
   // sequential chain
   if (pair && k == 16 && pp.S > kMergeChunk && pp.S <= kWideMaxSplits) {
+    if (read != nullptr && pp.S <= kDecodeMaxSplits && launch_pair_decode_read(*read, pp, s)) {
+      *read_done = true;
+      return check_launch("mpl_lookup(decode stage 2 + value read)");
+    }
     if (read != nullptr && M > 0 && launch_pair_wide_read(*read, pp, s)) {
       *read_done = true;
       return check_launch("mpl_lookup(wide stage 2 + value read)");

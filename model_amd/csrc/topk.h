@@ -255,3 +255,93 @@ __device__ __forceinline__ float rsum(float v) {
 
 }  // namespace g16
 }  // namespace mpl
+
+namespace mpl {
+
+// ------------------------------------------------ whole-wave sorted lists
+// Exchanges with lane ^ S across the 64-lane wave, on the VALU only: DPP
+// inside 16-lane rows for S < 16 (xor 4 as a shift left and a shift right
+// on alternate banks of 4 lanes), v_permlane16_swap / v_permlane32_swap for
+// 16 and 32.  Bitonic sorts and merges of u64 keys (the order of make_key).
+namespace w64 {
+
+template <int S>
+__device__ __forceinline__ uint32_t xr(uint32_t v, int lane) {
+  if constexpr (S == 1) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+  } else if constexpr (S == 2) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false);  // quad_perm 2,3,0,1
+  } else if constexpr (S == 4) {
+    // banks 0 and 2 of a row (lanes 0-3, 8-11) take lane + 4 (row_shl:4),
+    // banks 1 and 3 take lane - 4 (row_shr:4)
+    const int t = __builtin_amdgcn_update_dpp(0, (int)v, 0x104, 0xF, 0x5, false);
+    return (uint32_t)__builtin_amdgcn_update_dpp(t, (int)v, 0x114, 0xF, 0xA, false);
+  } else if constexpr (S == 8) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false);  // row_ror:8
+  } else if constexpr (S == 16) {
+    // odd rows of the first operand swap with even rows of the second
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    return (lane & 16) ? r[0] : r[1];
+  } else {
+    static_assert(S == 32, "lane xor of 1, 2, 4, 8, 16 or 32");
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return (lane & 32) ? r[0] : r[1];
+  }
+}
+
+template <int S>
+__device__ __forceinline__ u64 xr64(u64 v, int lane) {
+  return ((u64)xr<S>((uint32_t)(v >> 32), lane) << 32) | xr<S>((uint32_t)v, lane);
+}
+
+// One compare-exchange stage with lane ^ S on N independent lists: the lane
+// keeps the larger key when keep_max, else the smaller.
+template <int S, int N>
+__device__ __forceinline__ void stage(u64 (&v)[N], int lane, bool keep_max) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const u64 o = xr64<S>(v[i], lane);
+    v[i] = ((o > v[i]) == keep_max) ? o : v[i];
+  }
+}
+
+// Bitonic merge of stages S, S/2, ..., 1: each aligned group of 2S lanes
+// holding a bitonic sequence ends sorted, descending where desc.
+template <int S, int N>
+__device__ __forceinline__ void merge_down(u64 (&v)[N], int lane, bool desc) {
+  stage<S, N>(v, lane, ((lane & S) == 0) == desc);
+  if constexpr (S > 1) merge_down<S / 2, N>(v, lane, desc);
+}
+
+// Sorts the wave's 64 keys of each list descending: lane r ends with rank r.
+template <int N>
+__device__ __forceinline__ void sort64_desc(u64 (&v)[N], int lane) {
+  merge_down<1, N>(v, lane, (lane & 2) == 0);
+  merge_down<2, N>(v, lane, (lane & 4) == 0);
+  merge_down<4, N>(v, lane, (lane & 8) == 0);
+  merge_down<8, N>(v, lane, (lane & 16) == 0);
+  merge_down<16, N>(v, lane, (lane & 32) == 0);
+  merge_down<32, N>(v, lane, true);
+}
+
+// Best 16 of four sorted 16-key lists, lane i holding entry i % 16 of list
+// i / 16, lists 1 and 3 in reverse order (so lanes 0-31 and 32-63 are each
+// a bitonic sequence).  Lanes 0-15 end with the best 16, descending.
+template <int N>
+__device__ __forceinline__ void best16_of4(u64 (&v)[N], int lane) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) {  // lists 0+1 -> lanes 0-15, lists 2+3 -> lanes 32-47 (bitonic split)
+    const u64 o = xr64<16>(v[i], lane);
+    v[i] = o > v[i] ? o : v[i];
+  }
+  merge_down<8, N>(v, lane, (lane & 32) == 0);  // lanes 0-15 descending, 32-47 ascending
+#pragma unroll
+  for (int i = 0; i < N; ++i) {
+    const u64 o = xr64<32>(v[i], lane);
+    v[i] = o > v[i] ? o : v[i];
+  }
+  merge_down<8, N>(v, lane, true);
+}
+
+}  // namespace w64
+}  // namespace mpl

@@ -118,6 +118,17 @@ struct Wsum {
     }
   }
 
+  // Adds one row group already loaded (VR <= 64: one vector per lane) with
+  // its weight: the arithmetic add_chunk does for row group b, so a caller
+  // adding groups 0, 1, ... in order gets add_chunk's bits.
+  __device__ __forceinline__ void add_vec(uint4 u, float w) {
+    static_assert(VPL == 1, "one vector per lane per row group");
+    float f[VE];
+    Vec16<V>::unpack(u, f);
+#pragma unroll
+    for (int e = 0; e < VE; ++e) acc[0][e] = fmaf(w, f[e], acc[0][e]);
+  }
+
   // Sums the row groups across lanes and writes the token's d outputs.
   __device__ __forceinline__ void store(float* o, int lane) {
 #pragma unroll
