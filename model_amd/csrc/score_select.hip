@@ -1445,10 +1445,11 @@ __global__ __launch_bounds__(1024) void pair_wide_read_k16(PairParams p, ReadPar
 // Stage 2 + value read for decode plans: 8 < S <= kDecodeMaxSplits split
 // lists, no noise (the lists' select score is the clean score, so a list
 // entry is its key alone), H = 4, k = 16, one row group per lane (VR <= 64).
-// One workgroup of 16 waves per token, every exchange on the VALU:
-//   1. wave w takes 16 lists of one codebook of head w % 4 (four groups of
-//      four, w64::best16_of4): 64 lists per head become 16, in LDS;
-//   2. wave h (< 4) reduces its head's 16 to one list per codebook (the
+// One workgroup of 16 waves per token, every exchange on the VALU.  SC (32
+// or 64) is the split capacity:
+//   1. wave w takes SC/2 lists of one codebook of head w % 4 (groups of four,
+//      w64::best16_of4): the SC lists of a codebook become SC/4, in LDS;
+//   2. wave h (< 4) reduces its head's lists to one per codebook (the
 //      codebooks' top-k, written to sub_idx / sub_scores), then runs the
 //      pair stage: of the k*k pairs (i, j) only the 50 with
 //      (i+1)(j+1) <= 16 can be among the best 16 (every pair (i', j') with
@@ -1461,20 +1462,22 @@ __global__ __launch_bounds__(1024) void pair_wide_read_k16(PairParams p, ReadPar
 //      weights are known (one memory round trip per head, the four heads
 //      overlapping) and puts them in LDS; wave 0 then adds the token's row
 //      groups in add_chunk's order, so `out` equals the two-launch path.
-constexpr int kDecodeMaxSplits = 32;
+constexpr int kDecodeMaxSplits = 64;
 
-template <typename V, int VR, bool NT>
+template <typename V, int VR, bool NT, int SC>
 __global__ __launch_bounds__(1024) void pair_decode_read_k16(PairParams p, ReadParams rp) {
   constexpr int K = 16;
   typedef Wsum<V, VR, 16, NT> Sum;
   static_assert(Sum::VPL == 1, "one vector per lane per row group");
+  static_assert(SC == 32 || SC == 64, "split capacity 32 or 64");
   constexpr int RPI = Sum::RPI, LPR = Sum::LPR;
   constexpr int GROUPS = 64 / RPI;  // row groups of the token's 64 rows
   constexpr int HG = GROUPS / 4;     // row groups of one head
-  __shared__ u64 l1[4][2][8][K];     // [head][codebook][list][rank] after step 1
-  __shared__ u64 l2[4][4][K];        // [head][list] within step 2
-  __shared__ u64 pab[4][2][K];       // [head][codebook] final lists
-  __shared__ int srow_slot[4 * K];
+  constexpr int G1 = SC / 8;         // groups of four lists per wave in step 1
+  constexpr int GPC = G1 / 2;        // groups per codebook in step 2
+  __shared__ u64 l1[4][2][2 * G1][K];  // [head][codebook][list][rank] after step 1
+  __shared__ u64 l2[4][G1][K];         // [head][list] within step 2
+  __shared__ u64 pab[4][2][K];         // [head][codebook] final lists
   __shared__ float srow_w[4 * K];
   __shared__ uint4 rows[GROUPS][kWave];
 
@@ -1483,58 +1486,63 @@ __global__ __launch_bounds__(1024) void pair_decode_read_k16(PairParams p, ReadP
   const int64_t m = blockIdx.x;  // the grid is exactly M workgroups
   const int HC = 8;
   const int64_t sstride = p.M * HC * K;
+  const int t = lane >> 4, e = lane & 15;
+  const int ent = (t & 1) ? 15 - e : e;  // list t of a group of four, odd ones reversed
   {
     // step 1: wave w, head h = w % 4, codebook cb = (w / 4) >> 1 of the
-    // head, lists 16 * ((w / 4) & 1) + 4 * grp + lane / 16 (odd ones of a
-    // group reversed), past S empty
+    // head, lists (SC/2) * ((w / 4) & 1) + 4 * grp + t; past S empty
     const int h = wave & 3, sub = wave >> 2, cb = sub >> 1;
     const int c = 2 * h + cb;
-    const int t = lane >> 4, e = lane & 15;
-    const int ent = (t & 1) ? 15 - e : e;
-    int id[4];
-    float cl[4];
+    int id[G1];
+    float cl[G1];
 #pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      const int s = 16 * (sub & 1) + 4 * grp + t;
+    for (int grp = 0; grp < G1; ++grp) {
+      const int s = (SC / 2) * (sub & 1) + 4 * grp + t;
       const int64_t o = (int64_t)min(s, p.S - 1) * sstride + (m * HC + c) * K + ent;  // clamped, unconditional
       id[grp] = p.idx[o];
       cl[grp] = p.clean[o];
     }
-    u64 key[4];
+    u64 key[G1];
 #pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      const int s = 16 * (sub & 1) + 4 * grp + t;
+    for (int grp = 0; grp < G1; ++grp) {
+      const int s = (SC / 2) * (sub & 1) + 4 * grp + t;
       key[grp] = (s < p.S && id[grp] >= 0) ? make_key(cl[grp], id[grp]) : 0ull;
     }
-    w64::best16_of4<4>(key, lane);
+    w64::best16_of4<G1>(key, lane);
     if (lane < K) {
 #pragma unroll
-      for (int grp = 0; grp < 4; ++grp) l1[h][cb][4 * (sub & 1) + grp][lane] = key[grp];
+      for (int grp = 0; grp < G1; ++grp) l1[h][cb][G1 * (sub & 1) + grp][lane] = key[grp];
     }
   }
   __syncthreads();
   if (wave < 4) {
     const int h = wave;
-    const int t = lane >> 4, e = lane & 15;
-    // step 2a: group g (cb = g >> 1) holds lists 4 * (g & 1) + t of codebook cb
-    u64 key[4];
+    // step 2a: group g holds lists 4 * (g % GPC) + t of codebook g / GPC
+    u64 key[G1];
 #pragma unroll
-    for (int g = 0; g < 4; ++g) key[g] = l1[h][g >> 1][4 * (g & 1) + t][(t & 1) ? 15 - e : e];
-    w64::best16_of4<4>(key, lane);
+    for (int g = 0; g < G1; ++g) key[g] = l1[h][g / GPC][4 * (g % GPC) + t][ent];
+    w64::best16_of4<G1>(key, lane);
     if (lane < K) {
 #pragma unroll
-      for (int g = 0; g < 4; ++g) l2[h][g][lane] = key[g];
+      for (int g = 0; g < G1; ++g) l2[h][g][lane] = key[g];
     }
-    // step 2b: lanes 0-31 hold codebook 0's two lists, lanes 32-63
-    // codebook 1's (second of each reversed): one bitonic split and a
-    // 16-lane merger leave codebook 0 in lanes 0-15, codebook 1 in 32-47
-    u64 v[1] = {l2[h][t][(t & 1) ? 15 - e : e]};
-    {
+    // step 2b: each codebook's GPC lists to one, codebook 0 in lanes 0-15
+    // and codebook 1 in lanes 32-47
+    u64 fk;
+    if constexpr (GPC == 2) {
+      // lanes 0-31 hold codebook 0's two lists, lanes 32-63 codebook 1's
+      // (second of each reversed): one bitonic split and a 16-lane merger
+      u64 v[1] = {l2[h][t][ent]};
       const u64 o = w64::xr64<16>(v[0], lane);
       v[0] = o > v[0] ? o : v[0];
+      w64::merge_down<8, 1>(v, lane, true);
+      fk = v[0];
+    } else {
+      u64 v[2] = {l2[h][t][ent], l2[h][4 + t][ent]};  // a group of four per codebook
+      w64::best16_of4<2>(v, lane);
+      const u64 b = w64::xr64<32>(v[1], lane);  // codebook 1's list to lanes 32-47
+      fk = (lane & 32) ? b : v[0];
     }
-    w64::merge_down<8, 1>(v, lane, true);
-    const u64 fk = v[0];
     if ((lane & 16) == 0) {  // lanes 0-15: codebook 2h, lanes 32-47: 2h + 1
       const int cb = lane >> 5;
       const int64_t o0 = (m * HC + 2 * h + cb) * K + e;
@@ -1866,13 +1874,20 @@ static bool launch_pair_decode_read(const LookupRead& lr, const PairParams& pp, 
   const int VR = lr.d * esz / 16;
   const bool nt = (int64_t)pp.n * pp.n * lr.d * esz > kStreamTableBytes;
   const unsigned grid = (unsigned)pp.M;
-#define MPL_PDR(V, vr)                                                    \
-  if (VR == vr) {                                                         \
-    if (nt)                                                               \
-      pair_decode_read_k16<V, vr, true><<<grid, 1024, 0, s>>>(pp, rp);    \
-    else                                                                  \
-      pair_decode_read_k16<V, vr, false><<<grid, 1024, 0, s>>>(pp, rp);   \
-    return true;                                                          \
+#define MPL_PDR(V, vr)                                                          \
+  if (VR == vr) {                                                               \
+    if (pp.S <= 32) {                                                           \
+      if (nt)                                                                   \
+        pair_decode_read_k16<V, vr, true, 32><<<grid, 1024, 0, s>>>(pp, rp);    \
+      else                                                                      \
+        pair_decode_read_k16<V, vr, false, 32><<<grid, 1024, 0, s>>>(pp, rp);   \
+    } else {                                                                    \
+      if (nt)                                                                   \
+        pair_decode_read_k16<V, vr, true, 64><<<grid, 1024, 0, s>>>(pp, rp);    \
+      else                                                                      \
+        pair_decode_read_k16<V, vr, false, 64><<<grid, 1024, 0, s>>>(pp, rp);   \
+    }                                                                           \
+    return true;                                                                \
   }
   if (lr.dtype == MPL_F16) {
     MPL_PDR(_Float16, 16) MPL_PDR(_Float16, 32) MPL_PDR(_Float16, 64)

@@ -2,9 +2,10 @@
 followed by mpl_gather_wsum, through the C ABI: every output bit for bit.
 Covers the fused stage-2 + read kernel (H = 4, k = 16: fp16 rows of 128, 256
 and 512 elements, fp32 rows, shuffled reads, split-key plans whose lists are
-merged before stage 2), the decode plan whose 9-64 split lists are merged by
-the fused wide kernel (pair_wide_read_k16), and the shapes that fall back to
-two launches (other H or k, row widths without a fused variant)."""
+merged before stage 2), the plans with 9-64 split lists (decode sizes),
+whose lists the fused decode stage 2 (pair_decode_read_k16) reduces, and the
+shapes that fall back to two launches (other H or k, row widths without a
+fused variant)."""
 
 import pytest
 import torch
@@ -58,9 +59,12 @@ def _run(M, H, n, d_key, d, k, vdt, shuffle, seed):
     (333, 4, 128, 128, 512, 16, torch.float16, 1),    # 512-wide rows, shuffled reads
     (64, 4, 1024, 256, 256, 16, torch.float16, 0),    # split-key plan merged before stage 2
     (16, 4, 1024, 256, 256, 16, torch.float16, 1),
-    (1, 4, 1024, 256, 256, 16, torch.float16, 0),     # decode: one token, 32 split lists (wide fused read)
-    (5, 4, 1024, 256, 256, 16, torch.float32, 1),     # decode, fp32 rows, shuffled reads
-    (3, 4, 2048, 128, 128, 16, torch.float16, 0),     # decode, 64 split lists, 128-wide rows
+    (1, 4, 1024, 256, 256, 16, torch.float16, 0),     # decode: one token, 4 split lists
+    (5, 4, 1024, 256, 256, 16, torch.float32, 1),     # 32 split lists, fp32 rows, shuffled reads
+    (3, 4, 2048, 128, 128, 16, torch.float16, 0),     # decode: 8 split lists, 128-wide rows
+    (2, 4, 4096, 256, 128, 16, torch.float16, 1),     # decode: 16 split lists, shuffled reads
+    (20, 4, 4096, 256, 128, 16, torch.float16, 0),    # 64 split lists
+    (9, 4, 2500, 256, 256, 16, torch.float32, 0),     # 40 split lists (ragged n), fp32 rows
     (300, 2, 128, 64, 256, 16, torch.float16, 0),     # H = 2: two launches
     (300, 4, 128, 64, 256, 8, torch.float16, 0),      # k = 8: two launches
     (300, 4, 128, 64, 96, 16, torch.float16, 0),      # 96-wide rows: two launches
