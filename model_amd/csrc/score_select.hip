@@ -146,7 +146,7 @@ __device__ __forceinline__ u64 pair_kth_key(const TopList<KMAX, NOISE>& top, int
 // `empty` (wave-uniform): no flush has filled the list yet, so the first
 // chunk, sorted, is the list's head as it stands (the rest of the list is
 // empty keys) and needs no merge.
-template <bool REFRESH, int KMAX, bool NOISE>
+template <bool REFRESH, int KMAX, bool NOISE, int CAP>
 __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
                                            const float* pay, uint32_t lane0, bool valid, int k, float base_thr,
                                            int par, bool empty = false) {
@@ -154,7 +154,7 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
 #pragma unroll 1
-  for (int c0 = 0; c0 < kCand; c0 += 8) {
+  for (int c0 = 0; c0 < CAP; c0 += 8) {
     if (__ballot(c0 < cnt) == 0) break;
     u64 ch[8];
     float cp[8];
@@ -190,13 +190,13 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
 // the pair merge that follows combines the two lists.  A wave runs as many
 // chunks of 8 as its fullest lane needs, so the split takes the wave's count
 // from that of its fullest lane to that of its fullest pair, halved.
-template <int KMAX, bool NOISE>
+template <int KMAX, bool NOISE, int CAP>
 __device__ __forceinline__ void flush_pair_range(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
                                                  const float* pay, int s, int t, int cnt0, uint32_t base0,
                                                  uint32_t base1, bool empty) {
   const int cnt = t - s;
 #pragma unroll 1
-  for (int c0 = 0; c0 < kCand; c0 += 8) {
+  for (int c0 = 0; c0 < CAP; c0 += 8) {
     if (__ballot(c0 < cnt) == 0) break;
     u64 ch[8];
     float cp[8];
@@ -347,24 +347,36 @@ __device__ __forceinline__ void query_operand(const ScoreParams& p, int hc, int6
   }
 }
 
-// SHORT (register path, no noise, splits of at most kShortBlocks blocks, the
-// decode-sized plans): each block is scored once and both passes read the
-// scores from the MFMA accumulators instead of reloading and re-scoring.
-constexpr int kShortBlocks = 4;
+// Short splits (SB = 4 or 8 blocks at most, no noise: the decode-sized
+// plans): the workgroup copies all of the split's key blocks into LDS by LDS
+// DMA at kernel start, each wave scores every block once from there, and
+// both passes read the scores from the MFMA accumulators instead of
+// reloading and re-scoring.  The key tiles lie in the candidate arrays,
+// which the select pass takes over after a barrier; the arrays hold 64
+// entries per lane, so SB = 4 needs no overflow check inside the pass and
+// SB = 8 one per block from the fifth on.  SB = 0: the streaming passes.
+constexpr int kShortCand = 64;
+template <typename T, int HP>
+constexpr bool short_fits(int sb) {
+  return sb * KeyPack<T>::vectors_per_lane(HP) * kWave * 16 <= 2 * (kScoreThreads / kWave) * kShortCand * kWave * 4;
+}
 
-template <typename T, int HP, bool NOISE, int KMAX, bool DIRECT, bool SHORT>
+template <typename T, int HP, bool NOISE, int KMAX, bool DIRECT, int SB>
 __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {
   constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);  // 16-B vectors per lane per block
   constexpr int OPV = KeyPack<T>::kOpsPerVec;
   constexpr int NCH = VPL * OPV;                         // MFMA chunks per block
   constexpr int TILE = VPL * kWave;                      // uint4 per key block
   constexpr int WAVES = kScoreThreads / kWave;
+  constexpr bool SHORT = SB > 0;
   typedef typename Mfma<T>::Op Op;
+  static_assert(!SHORT || (!NOISE && short_fits<T, HP>(SB)), "short splits: no noise, key tiles fit the arrays");
 
-  __shared__ uint4 tile0[TILE], tile1[TILE];
-  __shared__ float cscore[WAVES * kCand * kWave];
-  __shared__ uint32_t cindex[WAVES * kCand * kWave];
-  __shared__ float cpay[NOISE ? WAVES * kCand * kWave : 1];
+  constexpr int CAND = SHORT ? kShortCand : kCand;
+  __shared__ uint4 tile0[DIRECT || SHORT ? 1 : TILE], tile1[DIRECT || SHORT ? 1 : TILE];  // the LDS path's key tiles
+  __shared__ float cscore[WAVES * CAND * kWave];
+  __shared__ uint32_t cindex[WAVES * CAND * kWave];
+  __shared__ float cpay[NOISE ? WAVES * CAND * kWave : 1];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -391,32 +403,10 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
 #pragma unroll
     for (int v = 0; v < VPL; ++v) dst[v] = src[v * kWave];
   };
-  // SHORT: the split's blocks b_begin + j (clamped to the split, so past its
-  // end a block repeats the last one) are all requested here, before the
-  // query, so that keys and query arrive in one memory round trip; the
-  // scheduling barrier keeps the compiler from moving the loads down to
-  // their uses.
-  uint4 kv[SHORT ? kShortBlocks : 1][SHORT ? VPL : 1];
-  if constexpr (SHORT) {
-#pragma unroll
-    for (int j = 0; j < kShortBlocks; ++j) gload(kv[j], min(b_begin + j, b_end - 1));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  Op qop[NCH];
-  float ql;
-  query_operand<T, NCH>(p, hc, my_q, valid, lane, split == 0, qop, ql);
-  const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
-  const uint32_t lane0 = 4u * (uint32_t)(wave * kCand * kWave + lane);  // the lane's first buffer entry
-  const uint32_t flush_at = lane0 + (uint32_t)(kCand - 8) * kEntryBytes;
-
-  // Key blocks stream into two LDS buffers by LDS DMA (global_load_lds: no
-  // registers, no LDS store instructions).  Wave w copies the tile's 16-byte
-  // vectors w, w+WAVES, ... (with fewer vectors than waves, several waves
-  // copy the same bytes).  The buffers are separate arrays used in a
-  // compile-time alternation, so the compiler sees which buffer each LDS read
-  // touches and does not drain the in-flight DMA of the other one before it.
-  typedef float GVec __attribute__((ext_vector_type(NOISE ? 16 : 1)));
+  // Key blocks reach LDS by LDS DMA (global_load_lds: no registers, no LDS
+  // store instructions).  Wave w copies the tile's 16-byte vectors w,
+  // w+WAVES, ... (with fewer vectors than waves, several waves copy the same
+  // bytes).
   constexpr int LPW = VPL >= WAVES ? VPL / WAVES : 1;
   static_assert(VPL < WAVES || VPL % WAVES == 0, "tile vectors must split over the waves");
   auto dma = [&](uint4* dst, int blk) __attribute__((always_inline)) {
@@ -428,6 +418,30 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
                                        0);
     }
   };
+  // Short splits: tile j of the split in the candidate arrays (TPA tiles in
+  // each), requested here for all blocks b_begin + j (clamped to the split,
+  // so past its end a block repeats the last one) before the query, so that
+  // keys and query arrive in one memory round trip.
+  constexpr int TPA = (int)(sizeof(cscore) / (TILE * sizeof(uint4)));
+  auto short_tile = [&](int j) __attribute__((always_inline)) {
+    return j < TPA ? (uint4*)cscore + j * TILE : (uint4*)cindex + (j - TPA) * TILE;
+  };
+  if constexpr (SHORT) {
+#pragma unroll
+    for (int j = 0; j < SB; ++j) dma(short_tile(j), min(b_begin + j, b_end - 1));
+  }
+
+  Op qop[NCH];
+  float ql;
+  query_operand<T, NCH>(p, hc, my_q, valid, lane, split == 0, qop, ql);
+  const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
+  const uint32_t lane0 = 4u * (uint32_t)(wave * CAND * kWave + lane);  // the lane's first buffer entry
+  const uint32_t flush_at = lane0 + (uint32_t)(kCand - 8) * kEntryBytes;
+
+  // The streaming LDS path: two key buffers, separate arrays used in a
+  // compile-time alternation, so the compiler sees which buffer each LDS read
+  // touches and does not drain the in-flight DMA of the other one before it.
+  typedef float GVec __attribute__((ext_vector_type(NOISE ? 16 : 1)));
   // The lane's 16 noise values of block blk (keys 8*(r/4) + 4*par + r%4):
   // four 16-byte loads when the block is whole and the rows are 16-byte
   // aligned (noise_vec), else 16 clamped scalar loads.  The waits below count
@@ -552,29 +566,35 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     sweep_lds_on(tile0, tile1, bb, be, body);
   };
 
-  static_assert(!SHORT || (DIRECT && !NOISE), "short splits score on the register path without noise");
-  f32x16 sacc[SHORT ? kShortBlocks : 1];
+  f32x16 sacc[SHORT ? SB : 1];
   if constexpr (SHORT) {
-    // the scores of the blocks loaded at kernel start (past the split's end a
-    // block repeats the last one, which the passes skip or which leaves the
-    // maxima as they are)
+    // every wave's DMA (and its query loads) landed: the scores of the
+    // split's blocks (past the split's end a block repeats the last one,
+    // which the passes skip or which leaves the maxima as they are)
+    wait_vmcnt_le<0>();
+    __syncthreads();
 #pragma unroll
-    for (int j = 0; j < kShortBlocks; ++j) {
+    for (int j = 0; j < SB; ++j) {
+      const uint4* tl = short_tile(j);
       f32x16 x = f32x16{};
 #pragma unroll
-      for (int v = 0; v < VPL; ++v)
+      for (int v = 0; v < VPL; ++v) {
+        const uint4 u = tl[v * kWave + lane];
 #pragma unroll
-        for (int e = 0; e < OPV; ++e)
-          x = Mfma<T>::mma(Mfma<T>::from_vec(kv[SHORT ? j : 0][SHORT ? v : 0], e), qop[v * OPV + e], x);
+        for (int e = 0; e < OPV; ++e) x = Mfma<T>::mma(Mfma<T>::from_vec(u, e), qop[v * OPV + e], x);
+      }
       sacc[SHORT ? j : 0] = x;
     }
+    // both waves' tile reads are done before the select pass writes
+    // candidates over the tiles
+    __syncthreads();
   }
   auto sweep = [&](int bb, int be, auto&& body) __attribute__((always_inline)) {
     if constexpr (SHORT) {
       const GVec g{};
       auto no_issue = [](int) {};
 #pragma unroll
-      for (int j = 0; j < kShortBlocks; ++j) body((bb + j) * 32, sacc[SHORT ? j : 0], g, j < be - bb, no_issue);
+      for (int j = 0; j < SB; ++j) body((bb + j) * 32, sacc[SHORT ? j : 0], g, j < be - bb, no_issue);
     } else if constexpr (DIRECT) {
       sweep_direct(bb, be, body);
     } else {
@@ -679,33 +699,59 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   st.thr = valid ? base_thr : INFINITY;
   st.off = lane0;
   bool flushed = false;  // wave-uniform: a flush inside the pass has filled the list
-  sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
-                            __attribute__((always_inline)) {
-    float sv[16];
-    lane_scores(kb, c, g, sv);
+  // Every lane writes the element at its next free entry and keeps it only
+  // when it is a candidate: no exec-mask changes per element (7 -> 4
+  // instructions).  A kept-or-not write lands at or past the lane's last
+  // candidate, which the flush does not read; the overflow checks leave room
+  // for every element written before the next one.
+  auto append8 = [&](int kb, const f32x16& c, const float* sv, bool active, int q, auto&& issue)
+                     __attribute__((always_inline)) {
 #pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      if (active && __ballot(st.off > flush_at) != 0) {
-        flush_lane<true, KMAX, NOISE>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
+    for (int e = 0; e < 8; ++e) {
+      const int r = 8 * q + e;
+      issue_for(r, issue);
+      const float x = sv[r];
+      lds_at(cscore, st.off) = x;
+      lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
+      if (NOISE) lds_at(cpay, st.off) = clean_at(c, r);
+      st.off += (active && x > st.thr) ? kEntryBytes : 0u;
+    }
+  };
+  if constexpr (SHORT) {
+    // block j adds at most 16 entries to the 16 * j before it: from the
+    // block that could overflow on, a check flushes above CAND - 16
+    const uint32_t flush16 = lane0 + (uint32_t)(CAND - 16) * kEntryBytes;
+    auto no_issue = [](int) {};
+#pragma unroll
+    for (int j = 0; j < SB; ++j) {
+      const int kb = (b_begin + j) * 32;
+      const bool active = j < b_end - b_begin;
+      if (16 * (j + 1) > CAND && active && __ballot(st.off > flush16) != 0) {
+        flush_lane<true, KMAX, NOISE, CAND>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
         flushed = true;
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int r = 8 * q + e;
-        issue_for(r, issue);
-        // Every lane writes the element at its next free entry and keeps
-        // it only when it is a candidate: no exec-mask changes per element
-        // (7 -> 4 instructions).  A kept-or-not write lands at or past the
-        // lane's last candidate, which the flush does not read, and the
-        // flush check before each group of 8 leaves 8 free entries.
-        const float x = sv[r];
-        lds_at(cscore, st.off) = x;
-        lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
-        if (NOISE) lds_at(cpay, st.off) = clean_at(c, r);
-        st.off += (active && x > st.thr) ? kEntryBytes : 0u;
-      }
+      float sv[16];
+      const GVec g{};
+      lane_scores(kb, sacc[SHORT ? j : 0], g, sv);
+      append8(kb, sacc[SHORT ? j : 0], sv, active, 0, no_issue);
+      append8(kb, sacc[SHORT ? j : 0], sv, active, 1, no_issue);
     }
-  });
+  } else {
+    sweep(b_begin, b_end, [&](int kb, const f32x16& c, const GVec& g, bool active, auto&& issue)
+                              __attribute__((always_inline)) {
+      float sv[16];
+      lane_scores(kb, c, g, sv);
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        // the flush check before each group of 8 leaves 8 free entries
+        if (active && __ballot(st.off > flush_at) != 0) {
+          flush_lane<true, KMAX, NOISE, CAND>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
+          flushed = true;
+        }
+        append8(kb, c, sv, active, q, issue);
+      }
+    });
+  }
   {
     const int cnt_own = (int)((st.off - lane0) / kEntryBytes);
     float ca = __int_as_float(cnt_own), cb = ca;
@@ -714,7 +760,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     const int cnt0 = par ? cnt_par : cnt_own;            // the par-0 lane's count
     const int tot = cnt_own + cnt_par, h = (tot + 1) >> 1;
     const uint32_t base0 = par ? lane0 - 4u * 32u : lane0;  // the par-0 lane's column
-    flush_pair_range<KMAX, NOISE>(st, cscore, cindex, cpay, par ? h : 0, par ? tot : h, cnt0, base0,
+    flush_pair_range<KMAX, NOISE, CAND>(st, cscore, cindex, cpay, par ? h : 0, par ? tot : h, cnt0, base0,
                                   base0 + 4u * 32u, !flushed);
   }
 
@@ -1692,13 +1738,19 @@ constexpr bool direct_keys() {
 template <typename T, int HP, bool NOISE, int KMAX>
 static void launch_stage1(const ScoreParams& sp, int64_t blocks, hipStream_t s) {
   constexpr bool D = direct_keys<T, HP, NOISE, KMAX>();
-  if constexpr (D && !NOISE) {
-    if (sp.blk_per_split <= kShortBlocks) {
-      score_topk_kernel<T, HP, NOISE, KMAX, D, true><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+  if constexpr (!NOISE && short_fits<T, HP>(4)) {
+    if (sp.blk_per_split <= 4) {
+      score_topk_kernel<T, HP, NOISE, KMAX, false, 4><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
       return;
     }
   }
-  score_topk_kernel<T, HP, NOISE, KMAX, D, false><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+  if constexpr (!NOISE && short_fits<T, HP>(8)) {
+    if (sp.blk_per_split <= 8) {
+      score_topk_kernel<T, HP, NOISE, KMAX, false, 8><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
+      return;
+    }
+  }
+  score_topk_kernel<T, HP, NOISE, KMAX, D, 0><<<(unsigned)blocks, kScoreThreads, 0, s>>>(sp);
 }
 
 template <int HP>

@@ -104,19 +104,20 @@ def test_topk_equals_select_stage1(gpu_lib, M, H, n, d_key, k, score, noise):
     np.testing.assert_allclose(outs["topk"][1][free], clean, rtol=0, atol=2.0 ** -11 * T)
 
 
-@pytest.mark.parametrize("M", [16, 4096])
-def test_repeated_keys_tie_by_index_across_flushes(gpu_lib, M):
-    """Exact ties through the select pass's flushes at the 67M-slot key width
-    (n = 8,192): each codebook holds 16 distinct key vectors, each repeated
-    512 times at random places, so a query's best score is reached by 512
-    keys at once and the lane buffers overflow many times.  The top 16 are
-    then the 16 lowest indices holding the best vector (lax.top_k's order,
-    memory.py:34-57), which a flush threshold taken from both lanes of the
-    query must keep: a later key that ties the k-th best loses on its larger
-    index.  Checked on rows whose best and second-best distinct vectors are
-    apart by more than the fp16-scoring error."""
+@pytest.mark.parametrize("M,n", [(16, 8192), (4096, 8192), (16, 16384), (64, 16384)])
+def test_repeated_keys_tie_by_index_across_flushes(gpu_lib, M, n):
+    """Exact ties through the select pass's flushes at the 67M- and 268M-slot
+    key widths (n = 8,192 and 16,384; at 16 and 64 tokens the short splits of
+    4 and 8 blocks): each codebook holds 16 distinct key vectors, each
+    repeated n / 16 times at random places, so a query's best score is
+    reached by that many keys at once and the lane buffers overflow many
+    times.  The top 16 are then the 16 lowest indices holding the best vector
+    (lax.top_k's order, memory.py:34-57), which a flush threshold taken from
+    both lanes of the query must keep: a later key that ties the k-th best
+    loses on its larger index.  Checked on rows whose best and second-best
+    distinct vectors are apart by more than the fp16-scoring error."""
     L = _lib.lib()
-    H, n, half, k, nv = 1, 8192, 128, 16, 16
+    H, half, k, nv = 1, 128, 16, 16
     rng = np.random.default_rng(11)
     base = rng.standard_normal((H, 2, nv, half))
     assign = np.stack([np.stack([rng.permutation(n) % nv for _ in range(2)]) for _ in range(H)])  # [H, 2, n]
