@@ -545,6 +545,21 @@ int mpl_rows_linear(const float* x, const float* x_mul, const float* ln_scale, c
                     const float* weight, int weight_layout, const float* bias, int activation,
                     const float* residual, int64_t rows, int K, int N, float* out, void* stream);
 
+/*
+ * Two dense layers of the same (layer-normalised) rows as one product: the
+ * memory layer's router and gate (model.py:110 and 118, both on
+ * h = LayerNorm(x), model.py:98).  weight [K, N1 + N2] is the two
+ * Dense kernels side by side (MPL_W_IN_OUT), bias [N1 + N2] (or NULL);
+ *   out1 [rows, N1] = act1(a . weight[:, :N1] + bias[:N1])
+ *   out2 [rows, N2] = act2(a . weight[:, N1:] + bias[N1:])
+ * with a as in mpl_rows_linear (no x_mul, no residual).  Each output equals
+ * mpl_rows_linear of its layer bit for bit.  No counterpart in the
+ * reference's interface: it saves a decode step one launch per memory layer.
+ */
+int mpl_rows_linear_pair(const float* x, const float* ln_scale, const float* ln_bias, float ln_eps,
+                         const float* weight, const float* bias, int activation1, int activation2, int64_t rows,
+                         int K, int N1, int N2, float* out1, float* out2, void* stream);
+
 size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half, int score_dtype);
 int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
                          const int32_t* sub_idx, const float* d_sub, const float* clean_counts, const void* state,

@@ -51,6 +51,10 @@ struct LinearArgs {
   int64_t rows;
   int K, N, act;
   float eps;
+  // two layers of one input as one product: output columns [n1, N) go to
+  // out2 [rows, N - n1] with activation act2 (n1 == N: one layer)
+  float* out2;
+  int n1, act2;
 };
 
 __device__ __forceinline__ float activate(float v, int act) {
@@ -289,8 +293,13 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     float v = 0.0f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) v += red[w][o];
-    v = activate(v + ebias, a.act);
-    a.out[eat] = v + eres;
+    if (en < a.n1) {
+      v = activate(v + ebias, a.act);
+      a.out[(r0 + erow) * a.n1 + en] = v + eres;
+    } else {
+      v = activate(v + ebias, a.act2);
+      a.out2[(r0 + erow) * (a.N - a.n1) + (en - a.n1)] = v + eres;
+    }
   }
 }
 
@@ -339,7 +348,8 @@ extern "C" int mpl_rows_linear(const float* x, const float* x_mul, const float* 
   MPL_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(x_mul) && aligned16(ln_scale) && aligned16(ln_bias),
               MPL_EINVAL, "mpl_rows_linear: x, x_mul, weight, ln_scale and ln_bias must be 16-byte aligned");
   MPL_REQUIRE(out != x && out != x_mul, MPL_EINVAL, "mpl_rows_linear: out may alias residual only");
-  LinearArgs a{x, x_mul, ln_scale, ln_bias, weight, bias, residual, out, rows, K, N, activation, ln_eps};
+  LinearArgs a{x, x_mul, ln_scale, ln_bias, weight, bias, residual, out, rows, K, N, activation, ln_eps,
+               nullptr, N, activation};
   hipStream_t s = (hipStream_t)stream;
   const bool ln = ln_scale != nullptr, mul = x_mul != nullptr;
   if (weight_layout == MPL_W_OUT_IN)
@@ -347,4 +357,30 @@ extern "C" int mpl_rows_linear(const float* x, const float* x_mul, const float* 
   else
     launch_rows_linear<MPL_W_IN_OUT>(a, ln, mul, s);
   return check_launch("mpl_rows_linear");
+}
+
+extern "C" int mpl_rows_linear_pair(const float* x, const float* ln_scale, const float* ln_bias, float ln_eps,
+                                    const float* weight, const float* bias, int activation1, int activation2,
+                                    int64_t rows, int K, int N1, int N2, float* out1, float* out2, void* stream) {
+  clear_error();
+  MPL_REQUIRE(rows >= 0 && K >= 4 && K % 4 == 0 && N1 >= 1 && N2 >= 1, MPL_EINVAL,
+              "mpl_rows_linear_pair: rows=%lld K=%d N1=%d N2=%d (K a positive multiple of 4, N1 and N2 positive)",
+              (long long)rows, K, N1, N2);
+  auto act_ok = [](int act) { return act == MPL_ACT_NONE || act == MPL_ACT_GELU_TANH || act == MPL_ACT_SILU; };
+  MPL_REQUIRE(act_ok(activation1) && act_ok(activation2), MPL_EINVAL, "mpl_rows_linear_pair: bad activation %d / %d",
+              activation1, activation2);
+  MPL_REQUIRE((ln_scale == nullptr) == (ln_bias == nullptr), MPL_EINVAL,
+              "mpl_rows_linear_pair: ln_scale and ln_bias go together");
+  MPL_REQUIRE(rows <= (int64_t)65535 * 16, MPL_EINVAL, "mpl_rows_linear_pair: rows=%lld above %d", (long long)rows,
+              65535 * 16);
+  MPL_REQUIRE((int64_t)N1 + N2 < ((int64_t)1 << 31), MPL_EINVAL, "mpl_rows_linear_pair: N1 + N2 too large");
+  if (rows == 0) return MPL_OK;
+  MPL_REQUIRE(x && weight && out1 && out2, MPL_EINVAL, "mpl_rows_linear_pair: null x, weight, out1 or out2");
+  MPL_REQUIRE(aligned16(x) && aligned16(weight) && aligned16(ln_scale) && aligned16(ln_bias), MPL_EINVAL,
+              "mpl_rows_linear_pair: x, weight, ln_scale and ln_bias must be 16-byte aligned");
+  MPL_REQUIRE(out1 != x && out2 != x && out1 != out2, MPL_EINVAL, "mpl_rows_linear_pair: outputs may not alias");
+  LinearArgs a{x, nullptr, ln_scale, ln_bias, weight, bias, nullptr, out1, rows, K, N1 + N2, activation1, ln_eps,
+               out2, N1, activation2};
+  launch_rows_linear<MPL_W_IN_OUT>(a, ln_scale != nullptr, false, (hipStream_t)stream);
+  return check_launch("mpl_rows_linear_pair");
 }

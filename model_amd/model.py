@@ -142,6 +142,41 @@ def rows_linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tens
     return out
 
 
+def rows_linear_pair(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], n1: int, *,
+                     ln: Optional[Dict[str, torch.Tensor]] = None, eps: float = LN_EPS, act1: Optional[str] = None,
+                     act2: Optional[str] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """mpl_rows_linear_pair: two Dense layers of the same (LayerNorm(x) if
+    ln else x) rows as one launch, weight [K, n1 + n2] their kernels side by
+    side and bias [n1 + n2]; returns (act1(. W[:, :n1] + b[:n1]),
+    act2(. W[:, n1:] + b[n1:])), each equal to rows_linear of its layer."""
+    from . import _lib
+
+    rows, K = x.shape
+    W = weight.reshape(K, -1)
+    N = W.shape[1]
+    n2 = N - n1
+    ts = [x, W] + ([bias] if bias is not None else [])
+    if ln is not None:
+        ts += [ln["scale"], ln["bias"]]
+    for t in ts:
+        if t.dtype != torch.float32 or not t.is_contiguous() or t.device != x.device:
+            raise ValueError("rows_linear_pair: operands must be contiguous fp32 on one device")
+    if x.device.type != "cuda":
+        raise ValueError("rows_linear_pair runs on the GPU only (libmpl.so)")
+    if (not 0 < n1 < N or (bias is not None and bias.numel() != N)
+            or (ln is not None and (ln["scale"].numel() != K or ln["bias"].numel() != K))):
+        raise ValueError(f"rows_linear_pair: operand shapes do not fit x {tuple(x.shape)}, W {tuple(W.shape)}, "
+                         f"n1 {n1}")
+    out1 = torch.empty((rows, n1), dtype=torch.float32, device=x.device)
+    out2 = torch.empty((rows, n2), dtype=torch.float32, device=x.device)
+    P = _lib.ptr
+    _lib.check(_lib.lib().mpl_rows_linear_pair(
+        P(x), P(None if ln is None else ln["scale"]), P(None if ln is None else ln["bias"]), float(eps), P(W),
+        P(bias), _ACT[act1], _ACT[act2], rows, K, n1, n2, P(out1), P(out2), _lib.stream_ptr(x.device)),
+        "mpl_rows_linear_pair")
+    return out1, out2
+
+
 def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, layer_cache: Dict[str, torch.Tensor], heads: int,
                      scale: float) -> torch.Tensor:
     """mpl_decode_attention: qkv [B, 3 * heads * hd] fp32 (query, key and
@@ -242,6 +277,7 @@ class MemoryPoolLM:
     def __init__(self, cfg: ModelConfig, decode: bool = False):
         self.cfg, self.decode = cfg, decode
         self._qkv_cache: Dict[int, Tuple[tuple, torch.Tensor, torch.Tensor]] = {}
+        self._rg_cache: Dict[int, Tuple[tuple, torch.Tensor, torch.Tensor]] = {}
         self.pool = None
         if cfg.use_memory:
             self.pool = MemoryPool(cfg.n_sub_keys, cfg.pool_heads, cfg.d_key, cfg.d_value, cfg.top_k,
@@ -309,12 +345,37 @@ class MemoryPoolLM:
 
     def copied_parameters(self, p) -> List[torch.Tensor]:
         """The parameters a GPU decode step reads through copies made before
-        a HIP-graph capture (the fused query/key/value weights) rather than
-        from their own storage: a captured step is stale once any of them
-        changes in place."""
+        a HIP-graph capture (the fused query/key/value weights, and the
+        router and gate weights of the memory layers) rather than from their
+        own storage: a captured step is stale once any of them changes in
+        place."""
         if not self.decode:
             return []
-        return [t for i in range(self.cfg.n_layers) for t in self._qkv_sources(p[f"attn_{i}"])]
+        out = [t for i in range(self.cfg.n_layers) for t in self._qkv_sources(p[f"attn_{i}"])]
+        if self.pool is not None:
+            out += [t for i in self.cfg.memory_layers if i < self.cfg.n_layers
+                    for t in self._router_gate_sources(p, i)]
+        return out
+
+    @staticmethod
+    def _router_gate_sources(p, i: int) -> List[torch.Tensor]:
+        return [p[nm][part] for nm in (f"router_{i}", f"mem_gate_{i}") for part in ("kernel", "bias")]
+
+    def _fused_router_gate(self, p, i: int) -> Tuple[torch.Tensor, torch.Tensor]:
+        """[d, pool_heads * d_key + d_value] kernel and bias of memory layer
+        i's router and gate side by side, rebuilt when one of them was
+        replaced or changed in place (storage and version key)."""
+        src = self._router_gate_sources(p, i)
+        key = tuple((t.data_ptr(), t._version) for t in src)
+        hit = self._rg_cache.get(i)
+        if hit is not None and hit[0] == key:
+            return hit[1], hit[2]
+        d = self.cfg.d_model
+        with torch.no_grad():
+            w = torch.cat([src[0].reshape(d, -1), src[2].reshape(d, -1)], 1)
+            b = torch.cat([src[1].reshape(-1), src[3].reshape(-1)])
+        self._rg_cache[i] = (key, w, b)
+        return w, b
 
     def _fused_qkv(self, i: int, pa) -> Tuple[torch.Tensor, torch.Tensor]:
         """[d, 3 * heads * hd] kernel and [3 * heads * hd] bias of layer i's
@@ -368,10 +429,12 @@ class MemoryPoolLM:
                     hid = rows_linear(x_in, fi["kernel"], fi["bias"], ln=ln, act="gelu_tanh")
                     x = rows_linear(hid, fo["kernel"], fo["bias"], residual=x)
                 if mem_layer:
-                    r, g, mo = p[f"router_{i}"], p[f"mem_gate_{i}"], p[f"mem_out_{i}"]
-                    q = rows_linear(x_in, r["kernel"], r["bias"], ln=ln).reshape(B, cfg.pool_heads, cfg.d_key)
+                    # the router and the gate read the same LayerNorm(x): one launch
+                    mo = p[f"mem_out_{i}"]
+                    wrg, brg = self._fused_router_gate(p, i)
+                    q, gate = rows_linear_pair(x_in, wrg, brg, cfg.pool_heads * cfg.d_key, ln=ln, act2="silu")
+                    q = q.reshape(B, cfg.pool_heads, cfg.d_key)
                     mem, aux = self.pool.apply({"params": p["pool"]}, q, noise_scale=noise_scale, rngs=rngs)
-                    gate = rows_linear(x_in, g["kernel"], g["bias"], ln=ln, act="silu")
                     x = rows_linear(mem.float().contiguous(), mo["kernel"], mo["bias"], x_mul=gate, residual=x)
                     layer_aux.append(aux)
             # the vocabulary product is a plain 64 x 256 x 16,384-class GEMM: the library's

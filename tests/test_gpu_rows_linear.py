@@ -89,3 +89,32 @@ def test_rows_linear_rejects_bad_operands(gpu_lib):
         rows_linear(x.half(), torch.zeros((32, 8), device="cuda"))
     with pytest.raises(Exception, match="16-byte aligned"):
         rows_linear(torch.zeros(4 * 32 + 1, device="cuda")[1:].view(4, 32), torch.zeros((32, 8), device="cuda"))
+
+
+@pytest.mark.parametrize("rows,K,n1,n2,ln,act1,act2,bias", [
+    (64, 256, 1024, 256, True, None, "silu", True),  # the memory layer's router and gate
+    (5, 16, 12, 8, True, None, "silu", True),
+    (37, 64, 20, 44, False, "gelu_tanh", None, False),  # tiles across the split, no layer norm
+    (70, 128, 17, 15, True, "silu", "gelu_tanh", True),  # odd widths: column pairs across the split
+])
+def test_rows_linear_pair_equals_two_layers(gpu_lib, rows, K, n1, n2, ln, act1, act2, bias):
+    """mpl_rows_linear_pair against mpl_rows_linear of each layer: the same
+    bits, since every output column is the same product in both."""
+    from model_amd.model import rows_linear_pair
+
+    g = torch.Generator(device="cuda").manual_seed(rows + K + n1)
+    x = torch.randn((rows, K), generator=g, device="cuda")
+    w1 = torch.randn((K, n1), generator=g, device="cuda") * K ** -0.5
+    w2 = torch.randn((K, n2), generator=g, device="cuda") * K ** -0.5
+    b1 = torch.randn(n1, generator=g, device="cuda") if bias else None
+    b2 = torch.randn(n2, generator=g, device="cuda") if bias else None
+    lnp = {"scale": torch.rand(K, generator=g, device="cuda") + 0.5,
+           "bias": torch.randn(K, generator=g, device="cuda")} if ln else None
+    w = torch.cat([w1, w2], 1).contiguous()
+    b = torch.cat([b1, b2]) if bias else None
+    o1, o2 = rows_linear_pair(x, w, b, n1, ln=lnp, act1=act1, act2=act2)
+    r1 = rows_linear(x, w1, b1, ln=lnp, act=act1)
+    r2 = rows_linear(x, w2, b2, ln=lnp, act=act2)
+    torch.cuda.synchronize()
+    assert o1.shape == (rows, n1) and o2.shape == (rows, n2)
+    assert torch.equal(o1, r1) and torch.equal(o2, r2)
