@@ -68,7 +68,7 @@ def parse():
     ap.add_argument("--no-generate", action="store_true")
     ap.add_argument("--no-host", action="store_true")
     ap.add_argument("--only", choices=["text_study", "pool_67M_4096", "host_file", "fact_task", "sparse_update",
-                                         "cpu_67M", "generation", "train", "stage1", "stage1_67M"],
+                                         "cpu_67M", "generation", "train", "stage1", "stage1_67M", "decode"],
                     default=None,
                     help="run one workload alone (for profiler runs) and print its timings")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -1040,6 +1040,26 @@ def main():
         return
     if args.only == "host_file":
         print(json.dumps({"only": args.only, "host_pool_file_1M": host_pool_file_bench(torch, 5)}))
+        return
+    if args.only == "decode":
+        # decode-sized lookups with cached packed keys (mpl_lookup alone): the
+        # 67,108,864-slot table at 1, 16 and 64 tokens, and the
+        # 268,435,456-slot table (n = 16,384, 137 GB) at 64 tokens (the
+        # generation workload's lookup), each on a table of every slot
+        out = {}
+        for n_d, Ms in ((8192, (1, 16, 64)), (16384, (64,))):
+            vals = torch.empty((n_d * n_d, 256), dtype=torch.float16, device="cuda")
+            hash_normal_(vals, 3, 0.02)
+            for M in Ms:
+                lkd = Lookup(torch, L, M=M, H=4, n=n_d, d_key=256, d=256, k=16, seed=10 + M, values=vals,
+                             rotate=large_rotation(M) if n_d == 8192 else 4)
+                lkd.pack()
+                out[f"n{n_d}_M{M}"] = {"cached_keys_ms_per_step": time_loop(torch, lkd.lookup, 50, 5),
+                                       "slots": n_d * n_d, "tokens": M}
+                del lkd
+            del vals
+            torch.cuda.empty_cache()
+        print(json.dumps({"only": args.only, "decode": out}))
         return
     if args.only == "pool_67M_4096":
         vals = torch.empty((8192 * 8192, 256), dtype=torch.float16, device="cuda")
