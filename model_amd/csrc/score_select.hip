@@ -61,6 +61,10 @@ namespace mpl {
 #define MPL_CAND 30
 #endif
 constexpr int kCand = MPL_CAND;  // per-lane candidate buffer (entries)
+#ifndef MPL_NOISE_CAND
+#define MPL_NOISE_CAND 22
+#endif
+constexpr int kNoiseCand = MPL_NOISE_CAND;  // the same with routing noise
 #ifndef MPL_SCORE_THREADS
 #define MPL_SCORE_THREADS 128
 #endif
@@ -91,15 +95,15 @@ struct ScoreParams {
 };
 
 // Per-lane selection state of the stage-1 kernel.  Candidates are appended
-// to the lane's column of three LDS arrays of [waves][kCand][64] words
-// (score, key index, clean score with noise); `off` is the byte offset of the
-// lane's next free entry, the same in all three.  Entries of a column are
-// 4*64 bytes apart.  The stores address the __shared__ arrays directly (array
-// + byte offset, not a loop-carried pointer), so the compiler can tell them
-// from the LDS-DMA writes of the key tiles (it does not wait for the
-// in-flight DMA before an append) and folds each array's LDS address into
-// the instruction's offset field: an append is one add and two or three
-// ds_write_b32 from one address register.
+// to the lane's column of two LDS arrays of [waves][entries][64] words
+// (score, key index; with noise the score is the clean one, cand_entry);
+// `off` is the byte offset of the lane's next free entry, the same in both.
+// Entries of a column are 4*64 bytes apart.  The stores address the
+// __shared__ arrays directly (array + byte offset, not a loop-carried
+// pointer), so the compiler can tell them from the LDS-DMA writes of the key
+// tiles (it does not wait for the in-flight DMA before an append) and folds
+// each array's LDS address into the instruction's offset field: an append is
+// one add and a ds_write2st64_b32 from one address register.
 template <int KMAX, bool NOISE>
 struct LaneSel {
   TopList<KMAX, NOISE> top;
@@ -135,6 +139,27 @@ __device__ __forceinline__ u64 pair_kth_key(const TopList<KMAX, NOISE>& top, int
   return m;
 }
 
+// Key (and clean-score payload, with noise) of a buffered candidate at byte
+// offset o.  Without noise the score array holds the select score.  With
+// noise it holds the clean score, and the select score is formed again as
+// the select pass formed it, fma(coef, gumbel[idx], clean), from the lane's
+// noise row: the same bits, and one LDS array per candidate fewer.  Entries
+// past the lane's count (!in) give the empty key.
+template <bool NOISE>
+__device__ __forceinline__ void cand_entry(const float* cs, const uint32_t* ci, const float* grow, float coef,
+                                           uint32_t o, bool in, u64& key, float& pay) {
+  const float v = lds_at(cs, o);
+  const int id = in ? (int)lds_at(ci, o) : 0;
+  if (NOISE) {
+    const float g = grow[id];  // id < n: padded keys are never buffered
+    key = in ? make_key(__builtin_fmaf(coef, g, v), id) : 0ull;
+    pay = in ? v : 0.f;
+  } else {
+    key = in ? make_key(v, id) : 0ull;
+    pay = 0.f;
+  }
+}
+
 // Merges the lane's buffered candidates (entries lane0, lane0 + kEntryBytes,
 // ... below st.off) into its list, empties the buffer and, with REFRESH,
 // raises the threshold.  With k == KMAX the new threshold is the k-th best of
@@ -148,8 +173,8 @@ __device__ __forceinline__ u64 pair_kth_key(const TopList<KMAX, NOISE>& top, int
 // empty keys) and needs no merge.
 template <bool REFRESH, int KMAX, bool NOISE, int CAP>
 __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
-                                           const float* pay, uint32_t lane0, bool valid, int k, float base_thr,
-                                           int par, bool empty = false) {
+                                           const float* grow, float coef, uint32_t lane0, bool valid, int k,
+                                           float base_thr, int par, bool empty = false) {
   const int cnt = (int)((st.off - lane0) / kEntryBytes);
   // Rolled on purpose: this body is inlined at five sites of the block loop
   // and unrolled copies overflow the instruction cache.
@@ -159,12 +184,8 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
     u64 ch[8];
     float cp[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const bool in = c0 + i < cnt;
-      const uint32_t o = lane0 + (uint32_t)(c0 + i) * kEntryBytes;
-      ch[i] = in ? make_key(lds_at(cs, o), (int)lds_at(ci, o)) : 0ull;
-      cp[i] = (NOISE && in) ? lds_at(pay, o) : 0.f;
-    }
+    for (int i = 0; i < 8; ++i)
+      cand_entry<NOISE>(cs, ci, grow, coef, lane0 + (uint32_t)(c0 + i) * kEntryBytes, c0 + i < cnt, ch[i], cp[i]);
     sort8<NOISE>(ch, cp);
     if (empty && c0 == 0) {
 #pragma unroll
@@ -192,8 +213,8 @@ __device__ __forceinline__ void flush_lane(LaneSel<KMAX, NOISE>& st, const float
 // from that of its fullest lane to that of its fullest pair, halved.
 template <int KMAX, bool NOISE, int CAP>
 __device__ __forceinline__ void flush_pair_range(LaneSel<KMAX, NOISE>& st, const float* cs, const uint32_t* ci,
-                                                 const float* pay, int s, int t, int cnt0, uint32_t base0,
-                                                 uint32_t base1, bool empty) {
+                                                 const float* grow, float coef, int s, int t, int cnt0,
+                                                 uint32_t base0, uint32_t base1, bool empty) {
   const int cnt = t - s;
 #pragma unroll 1
   for (int c0 = 0; c0 < CAP; c0 += 8) {
@@ -206,8 +227,7 @@ __device__ __forceinline__ void flush_pair_range(LaneSel<KMAX, NOISE>& st, const
       const int e = s + c0 + i;
       const uint32_t o = !in ? base0 : e < cnt0 ? base0 + (uint32_t)e * kEntryBytes
                                                 : base1 + (uint32_t)(e - cnt0) * kEntryBytes;
-      ch[i] = in ? make_key(lds_at(cs, o), (int)lds_at(ci, o)) : 0ull;
-      cp[i] = (NOISE && in) ? lds_at(pay, o) : 0.f;
+      cand_entry<NOISE>(cs, ci, grow, coef, o, in, ch[i], cp[i]);
     }
     sort8<NOISE>(ch, cp);
     if (empty && c0 == 0) {
@@ -361,8 +381,18 @@ constexpr bool short_fits(int sb) {
   return sb * KeyPack<T>::vectors_per_lane(HP) * kWave * 16 <= 2 * (kScoreThreads / kWave) * kShortCand * kWave * 4;
 }
 
+// Minimum waves per SIMD the compiler allocates registers for: the noisy
+// fp16 selection with k <= 16 is held to two (its 38.5 KB of LDS per
+// workgroup allows two per SIMD; without the bound it took 259 registers and
+// ran at one).
+template <typename T, bool NOISE, int KMAX>
+constexpr int stage1_min_waves() {
+  return (NOISE && KMAX == 16 && sizeof(T) == 2) ? 2 : 1;
+}
+
 template <typename T, int HP, bool NOISE, int KMAX, bool DIRECT, int SB>
-__global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p) {
+__global__ __launch_bounds__(kScoreThreads, (stage1_min_waves<T, NOISE, KMAX>())) void score_topk_kernel(
+    ScoreParams p) {
   constexpr int VPL = KeyPack<T>::vectors_per_lane(HP);  // 16-B vectors per lane per block
   constexpr int OPV = KeyPack<T>::kOpsPerVec;
   constexpr int NCH = VPL * OPV;                         // MFMA chunks per block
@@ -372,11 +402,13 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   typedef typename Mfma<T>::Op Op;
   static_assert(!SHORT || (!NOISE && short_fits<T, HP>(SB)), "short splits: no noise, key tiles fit the arrays");
 
-  constexpr int CAND = SHORT ? kShortCand : kCand;
+  // with noise the buffer holds two arrays of 22 entries per lane (clean
+  // score and index), so that with the key tiles a workgroup takes 38.5 KB of
+  // LDS and two fit each SIMD
+  constexpr int CAND = SHORT ? kShortCand : (NOISE ? kNoiseCand : kCand);
   __shared__ uint4 tile0[DIRECT || SHORT ? 1 : TILE], tile1[DIRECT || SHORT ? 1 : TILE];  // the LDS path's key tiles
   __shared__ float cscore[WAVES * CAND * kWave];
   __shared__ uint32_t cindex[WAVES * CAND * kWave];
-  __shared__ float cpay[NOISE ? WAVES * CAND * kWave : 1];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -436,7 +468,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
   query_operand<T, NCH>(p, hc, my_q, valid, lane, split == 0, qop, ql);
   const float* grow = NOISE ? p.gumbel + ((valid ? my_q : 0) * p.HC + hc) * (int64_t)p.n : nullptr;
   const uint32_t lane0 = 4u * (uint32_t)(wave * CAND * kWave + lane);  // the lane's first buffer entry
-  const uint32_t flush_at = lane0 + (uint32_t)(kCand - 8) * kEntryBytes;
+  const uint32_t flush_at = lane0 + (uint32_t)(CAND - 8) * kEntryBytes;
 
   // The streaming LDS path: two key buffers, separate arrays used in a
   // compile-time alternation, so the compiler sees which buffer each LDS read
@@ -711,9 +743,8 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       const int r = 8 * q + e;
       issue_for(r, issue);
       const float x = sv[r];
-      lds_at(cscore, st.off) = x;
+      lds_at(cscore, st.off) = NOISE ? clean_at(c, r) : x;  // with noise the clean score (cand_entry)
       lds_at(cindex, st.off) = (uint32_t)(kb + 8 * (r >> 2) + 4 * par + (r & 3));
-      if (NOISE) lds_at(cpay, st.off) = clean_at(c, r);
       st.off += (active && x > st.thr) ? kEntryBytes : 0u;
     }
   };
@@ -727,7 +758,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       const int kb = (b_begin + j) * 32;
       const bool active = j < b_end - b_begin;
       if (16 * (j + 1) > CAND && active && __ballot(st.off > flush16) != 0) {
-        flush_lane<true, KMAX, NOISE, CAND>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
+        flush_lane<true, KMAX, NOISE, CAND>(st, cscore, cindex, grow, coef, lane0, valid, p.k, base_thr, par);
         flushed = true;
       }
       float sv[16];
@@ -745,7 +776,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
       for (int q = 0; q < 2; ++q) {
         // the flush check before each group of 8 leaves 8 free entries
         if (active && __ballot(st.off > flush_at) != 0) {
-          flush_lane<true, KMAX, NOISE, CAND>(st, cscore, cindex, cpay, lane0, valid, p.k, base_thr, par);
+          flush_lane<true, KMAX, NOISE, CAND>(st, cscore, cindex, grow, coef, lane0, valid, p.k, base_thr, par);
           flushed = true;
         }
         append8(kb, c, sv, active, q, issue);
@@ -760,7 +791,7 @@ __global__ __launch_bounds__(kScoreThreads) void score_topk_kernel(ScoreParams p
     const int cnt0 = par ? cnt_par : cnt_own;            // the par-0 lane's count
     const int tot = cnt_own + cnt_par, h = (tot + 1) >> 1;
     const uint32_t base0 = par ? lane0 - 4u * 32u : lane0;  // the par-0 lane's column
-    flush_pair_range<KMAX, NOISE, CAND>(st, cscore, cindex, cpay, par ? h : 0, par ? tot : h, cnt0, base0,
+    flush_pair_range<KMAX, NOISE, CAND>(st, cscore, cindex, grow, coef, par ? h : 0, par ? tot : h, cnt0, base0,
                                   base0 + 4u * 32u, !flushed);
   }
 
