@@ -615,6 +615,10 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   __shared__ uint4 tiles[2][TILE];
   __shared__ __attribute__((aligned(16)))
   float rtile[MODE == kModeDK ? 2 : 1][MODE == kModeDK ? kRowsPerGroup : 1][MODE == kModeDK ? kRtPitch : 1];
+  // kModeDK: the forward state of the streamed block's 32 queries, staged
+  // with the block's tiles (one block ahead, double-buffered) so that the
+  // per-element reads come from LDS instead of global memory
+  __shared__ float4 sstate[MODE == kModeDK ? 2 : 1][MODE == kModeDK ? 32 : 1];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, par = lane >> 5;
   const int hc = blockIdx.x % p.HC;
@@ -687,6 +691,18 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
 
   const int64_t sb0 = (int64_t)split * p.sblk_per_split;
   const int64_t sb1 = sb0 + p.sblk_per_split < p.sblk ? sb0 + p.sblk_per_split : p.sblk;
+  constexpr bool SST = MODE == kModeDK;
+  const bool sst = SST && bal && tid < 32;  // the threads that stage a block's states
+  float4 st_next = make_float4(0.f, 0.f, 0.f, 0.f);
+  auto sload = [&](int64_t b) __attribute__((always_inline)) {
+    if (sst) {
+      const int64_t row = b * 32 + tid;
+      st_next = sth[row < nstr ? row : nstr - 1];
+    }
+  };
+  auto sstore = [&](int x) __attribute__((always_inline)) {
+    if (sst) sstate[SST ? x : 0][SST ? tid : 0] = st_next;
+  };
   f32x16 gacc[ND];
 #pragma unroll
   for (int db = 0; db < ND; ++db) gacc[db] = f32x16{};
@@ -708,8 +724,10 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   if (sb0 < sb1) {
     stn.load(sN + sb0 * TN, tid);
     stt.load(sT + sb0 * TT, tid);
+    sload(sb0);
     stn.store(tiles[0], tid);
     stt.store(tiles[0] + TN, tid);
+    sstore(0);
   }
   __syncthreads();
   for (int64_t sb = sb0; sb < sb1; ++sb) {
@@ -718,6 +736,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     if (more) {
       stn.load(sN + (sb + 1) * TN, tid);
       stt.load(sT + (sb + 1) * TT, tid);
+      sload(sb + 1);
       if (route) rload(sb + 1);
     }
     f32x16 acc = f32x16{};
@@ -753,7 +772,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
         // d cos / S: balance c p (f - r) T_eff plus the routed d_sub T (q_len)
         float g = route ? rtv[r] : 0.f;
         if (bal) {
-          const float4 s = sth[rc];  // the streamed query's state
+          const float4 s = sstate[SST ? cur : 0][SST ? 8 * (r >> 2) + 4 * par + (r & 3) : 0];  // the streamed query's state
           g += exp2f(acc[r] * s.z - s.x) * (ffix - s.y) * (s.z * kLn2) * cc;
         }
         gv[r] = (rv && valid) ? g * invS : 0.f;
@@ -779,6 +798,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
     if (more) {
       stn.store(tiles[cur ^ 1], tid);
       stt.store(tiles[cur ^ 1] + TN, tid);
+      sstore(cur ^ 1);
       if (route) rstore(cur ^ 1);
     }
     __syncthreads();
