@@ -520,7 +520,8 @@ def train_step_bench(torch, iters):
         loss = ((out + probe) * g_out).sum() + 0.01 * aux["balance_loss"] + 0.01 * key_diversity_loss(keys)
         gw, gk, gt, gp = torch.autograd.grad(loss, [w_q, keys, log_t, probe])
         rest = R.sum_squares([gw, gk, gt])
-        upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: gp}, [0], rest_sq=rest)
+        # the per-step slot counts (memory.py:215) come from the merge's sort
+        upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: gp}, [0], rest_sq=rest, count_slots=True)
 
     for _ in range(3):
         step()
@@ -549,13 +550,15 @@ def train_step_bench(torch, iters):
             gk = dk + dk_div
             gw = hidden.t() @ dq.reshape(M, H * d_key)
             rest = R.sum_squares([gw, gk, dlt])  # no memset node in the captured step
-            upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest)
+            upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest,
+                count_slots=True)
 
     ms_graph = time_loop(torch, step_graph, iters, 3)
     return {"workload": "training step of the text-study layer: 8,192 tokens, 262,144 fp16 slots + fp32 master, "
                         "forward with Gumbel routing noise + backward (queries through a 256->1024 projection, "
                         "sub-keys, log-temperature, "
-                        "balance loss 0.01, key diversity loss 0.01, probe gradient) + sparse row-wise Adagrad",
+                        "balance loss 0.01, key diversity loss 0.01, probe gradient) + sparse row-wise Adagrad "
+                        "+ routing statistics (sub-key counts, per-slot fetch counts from the row merge)",
             "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events",
             "graph_ms_per_step": ms_graph, "graph_tokens_per_s": M / (ms_graph * 1e-3),
             "graph_timing": "the same step through MemoryPool.forward_backward (no torch autograd), "

@@ -293,6 +293,20 @@ int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fe
                    void* stream);
 
 /*
+ * mpl_merge_rows that also writes slot_counts [pool_size] fp32, the number of
+ * fetches of every slot (memory.py:215: zeros(pool_size).at[slots].add(1),
+ * summed over the merged layers as model.py:136 sums the layers' counts),
+ * from the segments of the same sort: no atomics.  It replaces the per-fetch
+ * histogram of mpl_route_counts for a training step that merges the fetched
+ * rows anyway.  No counterpart in the reference (which takes the counts from
+ * the forward's aux).  Same workspace as mpl_merge_rows.
+ */
+int mpl_merge_rows_counts(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
+                          const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
+                          int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, int zero_padding,
+                          float* slot_counts, void* stream);
+
+/*
  * train.py:395-397: gnorm = sqrt(rest_sq + sum(row_sq)) and
  * scale = min(1, grad_clip / (gnorm + 1e-6)); scale_gnorm[0] = scale,
  * scale_gnorm[1] = gnorm (device memory).  rest_sq (device, may be NULL = 0)

@@ -53,6 +53,7 @@ SIGNATURES = {
     "mpl_score_topk": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P, _SZ, _P, _P, _P]),
     "mpl_merge_rows_workspace_bytes": (_SZ, [_I64, _I, _I64]),
     "mpl_merge_rows": (_I, [_P, _P, _I64, _I, _P, _I, _I64, _P, _SZ, _P, _P, _P, _P, _I, _P]),
+    "mpl_merge_rows_counts": (_I, [_P, _P, _I64, _I, _P, _I, _I64, _P, _SZ, _P, _P, _P, _P, _I, _P, _P]),
     "mpl_clip_scale_workspace_bytes": (_SZ, []),
     "mpl_clip_scale": (_I, [_P, _I64, _P, _F, _P, _P, _SZ, _P]),
     "mpl_sum_squares_workspace_bytes": (_SZ, []),

@@ -121,11 +121,14 @@ __global__ __launch_bounds__(256) void fill_zero3_kernel(float* __restrict__ a, 
 // Workgroup b covers head h = b % H and tokens [t0, t0 + tpg).  With use_lds
 // the two sub-key histograms and the two clean histograms of head h ([4][n]
 // ints) are built in LDS and added to the outputs once per workgroup.  Ids
-// outside their range are not counted.
+// outside their range are not counted.  P2: k and n are powers of two
+// (kshift = log2 k, nshift = log2 n), so the id positions and the slot's
+// sub-key pair come from shifts and masks rather than integer divisions.
+template <bool P2>
 __global__ __launch_bounds__(256) void route_counts_kernel(const int32_t* __restrict__ slots,
                                                            const int32_t* __restrict__ clean, int64_t M, int H,
-                                                           int n, int k, int64_t tpg, int use_lds,
-                                                           float* __restrict__ sub_counts,
+                                                           int n, int k, int kshift, int nshift, int64_t tpg,
+                                                           int use_lds, float* __restrict__ sub_counts,
                                                            float* __restrict__ clean_counts,
                                                            float* __restrict__ slot_counts) {
   extern __shared__ int hist[];
@@ -141,31 +144,35 @@ __global__ __launch_bounds__(256) void route_counts_kernel(const int32_t* __rest
     __syncthreads();
   }
   if (t1 > t0) {
-    const int64_t ne = (t1 - t0) * k;
-    for (int64_t e = tid; e < ne; e += 256) {
-      const int64_t m = t0 + e / k;
-      const int j = (int)(e % k);
-      const int s = slots[(m * H + h) * k + j];
+    // ids of token m, head h: slots[(m H + h) k + j], clean[(m H + h) 2k + c k + j]
+    const int ne = (int)(t1 - t0) * k;
+    const int32_t* sbase = slots + (t0 * H + h) * k;
+    for (int e = tid; e < ne; e += 256) {
+      const int mm = P2 ? e >> kshift : e / k;
+      const int j = e - mm * k;
+      const int s = sbase[(int64_t)mm * H * k + j];
       if (s < 0 || s >= N) continue;
       if (slot_counts != nullptr) unsafeAtomicAdd(&slot_counts[s], 1.0f);
       if (do_sub) {
-        const int a = s / n, b = s - a * n;
+        const int a = P2 ? s >> nshift : s / n;
+        const int b2 = s - a * n;
         if (use_lds) {
           atomicAdd(&hist[a], 1);
-          atomicAdd(&hist[n + b], 1);
+          atomicAdd(&hist[n + b2], 1);
         } else {
           unsafeAtomicAdd(&sub_counts[(2 * h) * n + a], 1.0f);
-          unsafeAtomicAdd(&sub_counts[(2 * h + 1) * n + b], 1.0f);
+          unsafeAtomicAdd(&sub_counts[(2 * h + 1) * n + b2], 1.0f);
         }
       }
     }
     if (do_clean) {
-      const int64_t nc = (t1 - t0) * 2 * k;
-      for (int64_t e = tid; e < nc; e += 256) {
-        const int64_t m = t0 + e / (2 * k);
-        const int r = (int)(e % (2 * k));  // c * k + j
-        const int c = r / k;
-        const int i = clean[(m * H + h) * 2 * k + r];
+      const int nc = (int)(t1 - t0) * 2 * k;
+      const int32_t* cbase = clean + (t0 * H + h) * 2 * k;
+      for (int e = tid; e < nc; e += 256) {
+        const int mm = P2 ? e >> (kshift + 1) : e / (2 * k);
+        const int r = e - mm * 2 * k;  // c * k + j
+        const int c = P2 ? r >> kshift : r / k;
+        const int i = cbase[(int64_t)mm * H * 2 * k + r];
         if (i < 0 || i >= n) continue;
         if (use_lds)
           atomicAdd(&hist[(2 + c) * n + i], 1);
@@ -178,7 +185,7 @@ __global__ __launch_bounds__(256) void route_counts_kernel(const int32_t* __rest
     __syncthreads();
     for (int i = tid; i < 4 * n; i += 256) {
       const int v = hist[i];
-      const int which = i / n, key = i - which * n;
+      const int which = P2 ? i >> nshift : i / n, key = i - which * n;
       float* dst = which < 2 ? sub_counts : (do_clean ? clean_counts : nullptr);
       if (v == 0 || dst == nullptr) continue;
       unsafeAtomicAdd(&dst[(2 * h + (which & 1)) * n + key], (float)v);
@@ -1042,8 +1049,15 @@ extern "C" int mpl_route_counts(const int32_t* slots, const int32_t* clean_sub_i
     const int64_t min_tpg = cdiv(M * H, 2048);
     if (tpg < min_tpg) tpg = min_tpg;
     const int64_t groups = (int64_t)H * cdiv(M, tpg);
-    route_counts_kernel<<<(unsigned)groups, 256, use_lds ? 16 * n : 0, s>>>(
-        slots, clean_sub_idx, M, H, n, k, tpg, use_lds, subkey_counts, clean_counts, slot_counts);
+    MPL_REQUIRE(tpg * 2 * k < ((int64_t)1 << 31), MPL_EUNSUPPORTED, "mpl_route_counts: k too large");
+    const bool p2 = (k & (k - 1)) == 0 && (n & (n - 1)) == 0;
+    const int kshift = p2 ? __builtin_ctz((unsigned)k) : 0, nshift = p2 ? __builtin_ctz((unsigned)n) : 0;
+#define MPL_RC(P) \
+  route_counts_kernel<P><<<(unsigned)groups, 256, use_lds ? 16 * n : 0, s>>>( \
+      slots, clean_sub_idx, M, H, n, k, kshift, nshift, tpg, use_lds, subkey_counts, clean_counts, slot_counts)
+    if (p2) MPL_RC(true);
+    else MPL_RC(false);
+#undef MPL_RC
   }
   return check_launch("mpl_route_counts");
 }

@@ -57,13 +57,19 @@ __device__ __forceinline__ uint64_t digit_peers(uint32_t digit, bool valid) {
 // ------------------------------------------------------------ radix sort
 // Digits of BITS = 8, 9 or 10 bits (2^BITS bins), chosen per key width so
 // that the passes are as few as possible (pool sizes up to 2^20: two passes).
+// zero_out[0, zero_n), when not null, is cleared on the side (the per-slot
+// fetch counts that the segment kernels fill in later).
 template <int BITS>
 __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t* __restrict__ keys, int64_t n,
                                                                    int shift, uint32_t* __restrict__ hist,
-                                                                   int64_t ntiles) {
+                                                                   int64_t ntiles, float* __restrict__ zero_out,
+                                                                   int64_t zero_n) {
   constexpr int BINS = 1 << BITS;
   __shared__ uint32_t h[BINS];
   const int tid = threadIdx.x;
+  if (zero_out != nullptr)
+    for (int64_t i = (int64_t)blockIdx.x * kSortThreads + tid; i < zero_n; i += (int64_t)gridDim.x * kSortThreads)
+      zero_out[i] = 0.f;
   for (int i = tid; i < BINS; i += kSortThreads) h[i] = 0;
   __syncthreads();
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
@@ -468,10 +474,21 @@ __global__ __launch_bounds__(kRowThreads) void seg_reduce_kernel(
 // Rows [U, cap): slot pool_size, zero row, zero norm (jnp.unique's
 // fill_value and segment_sum's empty segments, train.py:166-172), by the
 // workgroups [fix_blocks, gridDim) of the fix-up launch.
+// slot_counts (when not null, cleared beforehand): the length of each
+// segment of an id inside [0, pool_size), at that id.  Segment u ends where
+// u + 1 starts (seg_start[U] = n, written by the reduce kernel).
 __device__ __forceinline__ void pad_rows(const uint32_t* __restrict__ num_seg, int64_t cap, int d, int64_t pool_size,
                                          int32_t* __restrict__ uniq, float* __restrict__ rows,
-                                         float* __restrict__ row_sq, int64_t t0, int64_t stride) {
+                                         float* __restrict__ row_sq, int64_t t0, int64_t stride,
+                                         const int32_t* __restrict__ seg_start, float* __restrict__ slot_counts) {
   const int64_t U = *num_seg;
+  if (slot_counts != nullptr) {
+    const int64_t Uc = U < cap ? U : cap;
+    for (int64_t u = t0; u < Uc; u += stride) {
+      const uint32_t id = (uint32_t)uniq[u];
+      if (id < (uint64_t)pool_size) slot_counts[id] = (float)(seg_start[u + 1] - seg_start[u]);
+    }
+  }
   for (int64_t u = U + t0; u < cap; u += stride) {
     uniq[u] = (int32_t)pool_size;
     row_sq[u] = 0.f;
@@ -568,11 +585,11 @@ __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* _
                                                                  float* __restrict__ row_sq, int64_t fix_blocks,
                                                                  const uint32_t* __restrict__ num_seg, int64_t cap,
                                                                  int64_t pool_size, int32_t* __restrict__ uniq,
-                                                                 int zero_padding) {
+                                                                 int zero_padding, float* __restrict__ slot_counts) {
   if ((int64_t)blockIdx.x >= fix_blocks) {
     pad_rows(num_seg, cap, nv * W, pool_size, uniq, zero_padding ? rows : nullptr, row_sq,
              ((int64_t)blockIdx.x - fix_blocks) * kRowThreads + threadIdx.x,
-             ((int64_t)gridDim.x - fix_blocks) * kRowThreads);
+             ((int64_t)gridDim.x - fix_blocks) * kRowThreads, seg_start, slot_counts);
     return;
   }
   const int64_t r = ((int64_t)blockIdx.x * kRowThreads + threadIdx.x) >> 6;
@@ -609,6 +626,10 @@ __global__ void seg_finish_kernel(const uint32_t* __restrict__ num_seg, int64_t 
 }
 
 __global__ void store_zero_kernel(int32_t* p) { *p = 0; }
+
+__global__ __launch_bounds__(256) void zero_floats_kernel(float* __restrict__ x, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256) x[i] = 0.f;
+}
 
 // ---------------------------------------------------------- global norm
 // train.py:395-396 over the rows: sum of row_sq in a fixed order (fp64), then
@@ -936,24 +957,26 @@ template <int W, int VPL>
 static void launch_reduce(const uint32_t* sp, int32_t* seg_of, int32_t* seg_start, const float* weights,
                           const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
                           float* chunk, const MergeLayout& L, const uint32_t* nseg, int64_t pool_size, int32_t* uniq,
-                          int32_t* num_unique, int zero_padding, hipStream_t s) {
+                          int32_t* num_unique, int zero_padding, float* slot_counts, hipStream_t s) {
   const unsigned b1 = (unsigned)cdiv(L.nranges, kRowThreads / kWave);
   seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, weights, g, fpt, nv, P, rows, row_sq, partial,
                                                        nseg, seg_start, num_unique, L.cap);
   seg_fix_chunks_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, chunk);
   seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, chunk, rows, row_sq, b1,
-                                                             nseg, L.cap, pool_size, uniq, zero_padding);
+                                                             nseg, L.cap, pool_size, uniq, zero_padding,
+                                                             slot_counts);
 }
 
 template <int W>
 static void dispatch_reduce(const uint32_t* sp, int32_t* seg_of, int32_t* seg_start, const float* weights,
                             const float* g, int fpt, int nv, int64_t P, float* rows, float* row_sq, float* partial,
                             float* chunk, const MergeLayout& L, const uint32_t* nseg, int64_t pool_size,
-                            int32_t* uniq, int32_t* num_unique, int zero_padding, hipStream_t s) {
+                            int32_t* uniq, int32_t* num_unique, int zero_padding, float* slot_counts,
+                            hipStream_t s) {
   const int vpl = (int)cdiv(nv, kWave);
 #define MPL_REDUCE(V)                                                                                               \
   launch_reduce<W, V>(sp, seg_of, seg_start, weights, g, fpt, nv, P, rows, row_sq, partial, chunk, L, nseg,      \
-                      pool_size, uniq, num_unique, zero_padding, s)
+                      pool_size, uniq, num_unique, zero_padding, slot_counts, s)
   if (vpl <= 1) MPL_REDUCE(1);
   else if (vpl <= 2) MPL_REDUCE(2);
   else if (vpl <= 4) MPL_REDUCE(4);
@@ -979,7 +1002,8 @@ struct Segments {
 // finish = false leaves seg_start[U] and num_unique to the caller's next
 // kernel (seg_reduce_kernel does it for mpl_merge_rows).
 static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayout& L, char* ws, int32_t* uniq,
-                              int32_t* num_unique, bool finish, hipStream_t s) {
+                              int32_t* num_unique, bool finish, hipStream_t s, float* zero_out = nullptr,
+                              int64_t zero_n = 0) {
   uint32_t* keys[2] = {(uint32_t*)(ws + L.keys[0]), (uint32_t*)(ws + L.keys[1])};
   uint32_t* vals[2] = {(uint32_t*)(ws + L.vals[0]), (uint32_t*)(ws + L.vals[1])};
   uint32_t* hist = (uint32_t*)(ws + L.hist);
@@ -995,7 +1019,8 @@ static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayou
   for (int pass = 0; pass < L.passes; ++pass) {
     const int shift = L.digit_bits * pass;
 #define MPL_RADIX(B)                                                                                        \
-  radix_hist_kernel<B><<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles);                          \
+  radix_hist_kernel<B><<<nt, kSortThreads, 0, s>>>(kin, P, shift, hist, L.ntiles, pass == 0 ? zero_out : nullptr, \
+                                                   zero_n);                                                       \
   digit_scan_kernel<<<1u << B, 1024, 0, s>>>(hist, L.ntiles, totals);                                       \
   radix_scatter_kernel<B><<<nt, kSortThreads, 0, s>>>(kin, vin, keys[cur], vals[cur], P, shift, hist, L.ntiles, \
                                                       totals)
@@ -1066,11 +1091,10 @@ extern "C" size_t mpl_merge_rows_workspace_bytes(int64_t P, int d, int64_t pool_
   return merge_layout(P, d, pool_size).total;
 }
 
-extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
-                              const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
-                              int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, int zero_padding,
-                              void* stream) {
-  clear_error();
+static int merge_rows_impl(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
+                           const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
+                           int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, int zero_padding,
+                           float* slot_counts, void* stream) {
   MPL_REQUIRE(P >= 0 && fetches_per_token > 0 && d > 0 && pool_size > 0, MPL_EINVAL,
               "mpl_merge_rows: bad sizes P=%lld fetches_per_token=%d d=%d pool_size=%lld", (long long)P,
               fetches_per_token, d, (long long)pool_size);
@@ -1081,6 +1105,7 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   if (P == 0) {
     MPL_REQUIRE(num_unique != nullptr, MPL_EINVAL, "mpl_merge_rows: null num_unique");
     store_zero_kernel<<<1, 1, 0, s>>>(num_unique);  // a kernel, not a memset: safe under graph capture
+    if (slot_counts != nullptr) zero_floats_kernel<<<(unsigned)std::min<int64_t>(cdiv(pool_size, 256), 4096), 256, 0, s>>>(slot_counts, pool_size);
     return check_launch("mpl_merge_rows");
   }
   MPL_REQUIRE(slots && g && uniq && rows && row_sq && num_unique, MPL_EINVAL, "mpl_merge_rows: null buffer");
@@ -1088,7 +1113,8 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
               "mpl_merge_rows: workspace of %zu bytes needed, %zu given", L.total, workspace_bytes);
   char* ws = (char*)workspace;
-  const Segments sg = sort_segments((const uint32_t*)slots, P, L, ws, uniq, num_unique, false, s);
+  const Segments sg = sort_segments((const uint32_t*)slots, P, L, ws, uniq, num_unique, false, s, slot_counts,
+                                    slot_counts != nullptr ? pool_size : 0);
   int rc = check_launch("mpl_merge_rows(sort)");
   if (rc) return rc;
   const uint32_t* vin = sg.pos;
@@ -1099,11 +1125,30 @@ extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_
   float* chunk = (float*)(ws + L.chunk);
   if (d % 4 == 0)
     dispatch_reduce<4>(vin, seg_of, seg_start, weights, g, fetches_per_token, d / 4, P, rows, row_sq, partial, chunk,
-                       L, nseg, pool_size, uniq, num_unique, zero_padding, s);
+                       L, nseg, pool_size, uniq, num_unique, zero_padding, slot_counts, s);
   else
     dispatch_reduce<1>(vin, seg_of, seg_start, weights, g, fetches_per_token, d, P, rows, row_sq, partial, chunk, L,
-                       nseg, pool_size, uniq, num_unique, zero_padding, s);
+                       nseg, pool_size, uniq, num_unique, zero_padding, slot_counts, s);
   return check_launch("mpl_merge_rows(reduce)");
+}
+
+extern "C" int mpl_merge_rows(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
+                              const float* g, int d, int64_t pool_size, void* workspace, size_t workspace_bytes,
+                              int32_t* uniq, float* rows, float* row_sq, int32_t* num_unique, int zero_padding,
+                              void* stream) {
+  clear_error();
+  return merge_rows_impl(slots, weights, P, fetches_per_token, g, d, pool_size, workspace, workspace_bytes, uniq,
+                         rows, row_sq, num_unique, zero_padding, nullptr, stream);
+}
+
+extern "C" int mpl_merge_rows_counts(const int32_t* slots, const float* weights, int64_t P, int fetches_per_token,
+                                     const float* g, int d, int64_t pool_size, void* workspace,
+                                     size_t workspace_bytes, int32_t* uniq, float* rows, float* row_sq,
+                                     int32_t* num_unique, int zero_padding, float* slot_counts, void* stream) {
+  clear_error();
+  MPL_REQUIRE(slot_counts != nullptr, MPL_EINVAL, "mpl_merge_rows_counts: null slot_counts");
+  return merge_rows_impl(slots, weights, P, fetches_per_token, g, d, pool_size, workspace, workspace_bytes, uniq,
+                         rows, row_sq, num_unique, zero_padding, slot_counts, stream);
 }
 
 extern "C" size_t mpl_clip_scale_workspace_bytes() { return kSumBlocks * sizeof(double); }

@@ -93,11 +93,13 @@ class _KeyCache:
 
 class LazyAux(dict):
     """The ``aux`` dict of memory.py:217-226.  ``slots``, ``weights`` and
-    ``temperature`` are stored; ``balance_loss``, ``subkey_counts`` and
-    ``slot_counts`` are computed together, and ``queries`` and
-    ``top1_weight`` each on their own, the first time they are read."""
+    ``temperature`` are stored; ``balance_loss`` and ``subkey_counts`` are
+    computed together, and ``slot_counts``, ``queries`` and ``top1_weight``
+    each on their own, the first time they are read (a training step that
+    merges the fetched rows takes ``slot_counts`` from the merge instead:
+    SparseRowUpdate(count_slots=True))."""
 
-    _LAZY = ("balance_loss", "subkey_counts", "slot_counts")
+    _LAZY = ("balance_loss", "subkey_counts")
     _INTERNAL = ("_counts", "_state")
 
     def __init__(self, eager: Dict[str, Any], compute, **lazy):
@@ -193,6 +195,19 @@ class MemoryPool:
         self._temp_key = None
         self._temp_src = None
         self._temp_tensor = None
+        self._constants = {}
+
+    def _constant(self, value: float, dev) -> torch.Tensor:
+        """A device fp32 scalar [1] holding ``value``, made once per (value,
+        device) and reused (read-only), so a step does not launch a fill for
+        it every call."""
+        key = (float(value), str(dev))
+        t = self._constants.get(key)
+        if t is None:
+            if _capturing():  # not cached from inside a capture: the graph keeps its own
+                return torch.full((1,), float(value), dtype=torch.float32, device=dev)
+            t = self._constants[key] = torch.full((1,), float(value), dtype=torch.float32, device=dev)
+        return t
 
     @property
     def frozen_under_capture(self) -> bool:
@@ -329,8 +344,7 @@ class MemoryPool:
                 noise_coef = noise_scale.detach().to(device=dev, dtype=torch.float32).reshape(1) * float(
                     self.routing_noise)
             else:
-                noise_coef = torch.full((1,), float(self.routing_noise) * float(noise_scale), dtype=torch.float32,
-                                        device=dev)
+                noise_coef = self._constant(float(self.routing_noise) * float(noise_scale), dev)
             gumbel = gumbel.reshape(M, H, 2, n).float().contiguous()
 
         ws_bytes = L.mpl_score_select_workspace_bytes(M, H, n, half, k)
@@ -383,7 +397,8 @@ class MemoryPool:
             "slots": slots.reshape(*lead, H, k),
             "weights": weights.reshape(*lead, H, k),
             "temperature": T.reshape(()),
-        }, stats, queries=lambda: res["q_hat"], top1_weight=lambda: weights.max(-1).values.mean())
+        }, stats, queries=lambda: res["q_hat"], top1_weight=lambda: weights.max(-1).values.mean(),
+            slot_counts=lambda: self._slot_counts(slots, M))
         res.update({
             "out": out.reshape(*lead, d), "aux": aux, "q": q, "q_len": q_len,
             "k_hat": k_hat, "packed": packed, "score_code": score_code, "temperature": T, "sub_idx": sub_idx, "sub_scores": sub_scores,
@@ -409,10 +424,9 @@ class MemoryPool:
             clean = sub_idx
         subkey_counts = torch.empty((H, 2, n), dtype=torch.float32, device=dev)
         clean_counts = torch.empty((H, 2, n), dtype=torch.float32, device=dev)
-        slot_counts = torch.empty(self.pool_size, dtype=torch.float32, device=dev)
         check(L.mpl_route_counts(ptr(slots), ptr(clean), M, H, n, k, ptr(subkey_counts), ptr(clean_counts),
-                                 ptr(slot_counts), stream), "mpl_route_counts")
-        stats = {"subkey_counts": subkey_counts, "slot_counts": slot_counts}
+                                 None, stream), "mpl_route_counts")
+        stats = {"subkey_counts": subkey_counts}
         scaled = int(bool(self.balance_temperature_grad and self.query_scale))
         state = torch.empty(max(L.mpl_balance_state_bytes(M, H), 16), dtype=torch.uint8, device=dev)
         loss = torch.empty(1, dtype=torch.float32, device=dev)
@@ -420,6 +434,15 @@ class MemoryPool:
                                 half, k, score_code, ptr(T), ptr(state), ptr(loss), stream), "mpl_balance_fwd")
         stats.update(balance_loss=loss.reshape(()), _counts=clean_counts, _state=state)
         return stats
+
+    def _slot_counts(self, slots, M):
+        """memory.py:215: zeros(pool_size).at[slots].add(1), fp32."""
+        H, n, k = self.heads, self.n_sub_keys, self.top_k
+        dev = slots.device
+        out = torch.empty(self.pool_size, dtype=torch.float32, device=dev)
+        check(_lib.lib().mpl_route_counts(ptr(slots), None, M, H, n, k, None, None, ptr(out), _lib.stream_ptr(dev)),
+              "mpl_route_counts(slots)")
+        return out
 
     def _clean_sub_idx(self, q, packed, score_code, T, M):
         """memory.py:207: the stage-1 top-k of the clean scores (no stage 2)."""

@@ -52,11 +52,14 @@ class MergedRows:
 
 
 def merge_fetches(slots: torch.Tensor, weights: Optional[torch.Tensor], g: torch.Tensor,
-                  pool_size: int, zero_padding: bool = True) -> MergedRows:
+                  pool_size: int, zero_padding: bool = True,
+                  slot_counts: Optional[torch.Tensor] = None) -> MergedRows:
     """Sum weights[p] * g[p // fpt] per distinct slot, fpt = P / g.shape[0]
     (the fetches of one token are consecutive).  zero_padding=False leaves
     the padding rows [num_unique, cap) unwritten (the row optimizers skip
-    them)."""
+    them).  ``slot_counts`` (a contiguous fp32 [pool_size] tensor, or None)
+    receives the number of fetches of every slot (memory.py:215), taken from
+    the segments of the same sort."""
     dev = g.device
     slots = slots.reshape(-1).to(torch.int32).contiguous()
     P = slots.shape[0]
@@ -81,9 +84,17 @@ def merge_fetches(slots: torch.Tensor, weights: Optional[torch.Tensor], g: torch
     num_unique = torch.empty(1, dtype=torch.int32, device=dev)
     wsb = L.mpl_merge_rows_workspace_bytes(P, d, pool_size)
     ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
-    check(L.mpl_merge_rows(ptr(slots), ptr(weights), P, fpt, ptr(g), d, pool_size, ptr(ws), wsb, ptr(uniq),
-                           ptr(rows), ptr(row_sq), ptr(num_unique), int(bool(zero_padding)), _lib.stream_ptr(dev)),
-          "mpl_merge_rows")
+    if slot_counts is not None:
+        if (slot_counts.dtype != torch.float32 or not slot_counts.is_contiguous()
+                or slot_counts.numel() != pool_size or slot_counts.device != dev):
+            raise ValueError(f"slot_counts must be a contiguous fp32 [{pool_size}] tensor on {dev}")
+        check(L.mpl_merge_rows_counts(ptr(slots), ptr(weights), P, fpt, ptr(g), d, pool_size, ptr(ws), wsb,
+                                      ptr(uniq), ptr(rows), ptr(row_sq), ptr(num_unique), int(bool(zero_padding)),
+                                      ptr(slot_counts), _lib.stream_ptr(dev)), "mpl_merge_rows_counts")
+    else:
+        check(L.mpl_merge_rows(ptr(slots), ptr(weights), P, fpt, ptr(g), d, pool_size, ptr(ws), wsb, ptr(uniq),
+                               ptr(rows), ptr(row_sq), ptr(num_unique), int(bool(zero_padding)),
+                               _lib.stream_ptr(dev)), "mpl_merge_rows")
     return MergedRows(uniq, rows, row_sq, num_unique)
 
 
@@ -95,8 +106,9 @@ def merge_rows(slots: torch.Tensor, contribs: torch.Tensor, pool_size: int):
 
 
 def fetched_row_grads_full(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int,
-                           zero_padding: bool = True) -> MergedRows:
-    """train.py:146-163 with the extra outputs (row norms, distinct count)."""
+                           zero_padding: bool = True, slot_counts: Optional[torch.Tensor] = None) -> MergedRows:
+    """train.py:146-163 with the extra outputs (row norms, distinct count,
+    and with ``slot_counts`` the fetch count of every slot over the layers)."""
     slots, weights, grads = [], [], []
     for layer, sl, w in zip(layers, aux["slots"], aux["weights"]):
         g = probe_grads[layer]
@@ -105,7 +117,10 @@ def fetched_row_grads_full(aux: Dict, probe_grads, layers: Sequence[int], pool_s
         slots.append(sl.reshape(-1, hk).reshape(-1))
         weights.append(w.detach().reshape(-1))
         grads.append(g.reshape(-1, d))
-    return merge_fetches(torch.cat(slots), torch.cat(weights), torch.cat(grads), pool_size, zero_padding)
+    if len(slots) == 1:  # one layer: its own tensors (views), no concatenated copies
+        return merge_fetches(slots[0], weights[0], grads[0], pool_size, zero_padding, slot_counts)
+    return merge_fetches(torch.cat(slots), torch.cat(weights), torch.cat(grads), pool_size, zero_padding,
+                         slot_counts)
 
 
 def fetched_row_grads(aux: Dict, probe_grads, layers: Sequence[int], pool_size: int):
@@ -275,9 +290,18 @@ class SparseRowUpdate:
         return {"step": self.step, "pool_m": pm, "pool_v": pv, "values": table}
 
     def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
-                 rest_sq: Optional[torch.Tensor] = None) -> Dict[str, torch.Tensor]:
+                 rest_sq: Optional[torch.Tensor] = None, count_slots: bool = False) -> Dict[str, torch.Tensor]:
+        """One update from the fetches of ``layers`` (aux["slots"][i],
+        aux["weights"][i], probe_grads[layer]).  With count_slots the result
+        also holds "slot_counts" [N] fp32, the fetches of every slot summed
+        over the layers (the aux slot_counts of memory.py:215 / model.py:136
+        that train.py:456 folds into the usage average), from the merge's
+        own sort instead of a separate histogram."""
         N = self.host.n_slots if self.host is not None else self.values.shape[0]
-        merged = fetched_row_grads_full(aux, probe_grads, layers, N, zero_padding=False)  # optimizers skip padding
+        dev = self.values.device if self.values is not None else aux["slots"][0].device
+        counts = torch.empty(N, dtype=torch.float32, device=dev) if count_slots else None
+        merged = fetched_row_grads_full(aux, probe_grads, layers, N, zero_padding=False,  # optimizers skip padding
+                                        slot_counts=counts)
         sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip)
         lr = warmup_cosine(self.step, self.lr, self.warmup_steps, self.steps) * self.pool_lr_mult
         scale = sg[0:1]
@@ -288,5 +312,8 @@ class SparseRowUpdate:
         else:
             lazy_adam(self.values, self.m, self.v, merged.uniq, merged.rows, lr, self.step, self.master, scale)
         self.step += 1
-        return {"grad_scale": sg[0], "grad_norm": sg[1], "rows_updated": merged.num_unique[0],
-                "uniq": merged.uniq, "row_grads": merged.rows}
+        out = {"grad_scale": sg[0], "grad_norm": sg[1], "rows_updated": merged.num_unique[0],
+               "uniq": merged.uniq, "row_grads": merged.rows}
+        if counts is not None:
+            out["slot_counts"] = counts
+        return out

@@ -65,6 +65,8 @@ def test_row_entry_points_validate_before_launch():
     assert rc == 1
     rc = L.mpl_merge_rows(None, None, 64, 16, None, 8, N, None, 0, None, None, None, None, 1, None)
     assert rc == 1 and b"null buffer" in L.mpl_last_error()
+    rc = L.mpl_merge_rows_counts(None, None, 64, 16, None, 8, N, None, 0, None, None, None, None, 1, None, None)
+    assert rc == 1 and b"null slot_counts" in L.mpl_last_error()
     rc = L.mpl_row_adagrad(None, 5, None, None, None, None, 10, 8, N, 0.1, None, None)
     assert rc == 1 and b"values_dtype" in L.mpl_last_error()
     rc = L.mpl_row_adam(None, _lib.MPL_F16, None, None, None, None, None, 10, 8, N, 0.1, -1, None, None)

@@ -294,3 +294,59 @@ def test_merge_without_zero_padding(gpu_lib, zipf):
     assert torch.equal(a.rows[:U], b.rows[:U])
     assert torch.equal(a.row_sq, b.row_sq)
     assert bool((a.rows[U:] == 0).all())
+
+
+@pytest.mark.parametrize("case", ["reference", "uniform", "zipf", "empty"])
+def test_merge_slot_counts(gpu_lib, case):
+    """mpl_merge_rows_counts: the per-slot fetch counts (memory.py:215,
+    np.bincount here) from the merge's segments, exact, written over a
+    buffer that held other values; the merged rows are bitwise those of
+    mpl_merge_rows."""
+    rng = np.random.default_rng(21)
+    if case == "reference":      # more fetches than slots: every slot repeats
+        M, fpt, N, d = 37, 8, 16, 12
+        slots = rng.integers(0, N, M * fpt).astype(np.int32)
+    elif case == "uniform":      # fewer fetches than slots
+        M, fpt, N, d = 300, 16, 1 << 14, 24
+        slots = rng.integers(0, N, M * fpt).astype(np.int32)
+    elif case == "zipf":         # the training shape
+        M, H, k, N, d = 8192, 4, 16, 262144, 256
+        fpt = H * k
+        slots = zipf_slots(M, H, k, N).reshape(-1)
+    else:
+        M, fpt, N, d = 0, 4, 64, 8
+        slots = np.zeros(0, np.int32)
+    w = rng.random(M * fpt).astype(np.float32)
+    g = rng.standard_normal((M, d)).astype(np.float32)
+    ts, tw, tg = (torch.as_tensor(x, device="cuda") for x in (slots, w, g))
+    counts = torch.full((N,), 7.0, device="cuda")
+    a = R.merge_fetches(ts, tw, tg, N, slot_counts=counts)
+    b = R.merge_fetches(ts, tw, tg, N)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(counts.cpu().numpy(), np.bincount(slots, minlength=N).astype(np.float32))
+    assert torch.equal(a.uniq, b.uniq) and torch.equal(a.rows, b.rows) and torch.equal(a.row_sq, b.row_sq)
+    assert int(a.num_unique[0]) == np.unique(slots).shape[0]
+
+
+def test_sparse_row_update_counts_slots(gpu_lib):
+    """SparseRowUpdate(count_slots=True) on two layers: the counts summed
+    over the layers (model.py:136), and the update itself unchanged."""
+    rng = np.random.default_rng(22)
+    B, T, H, k, N, d = 2, 64, 4, 8, 2048, 32
+    aux = {"slots": [], "weights": []}
+    probes = {}
+    for layer in (0, 2):
+        aux["slots"].append(torch.as_tensor(rng.integers(0, N, (B, T, H, k)).astype(np.int32), device="cuda"))
+        aux["weights"].append(torch.as_tensor(rng.random((B, T, H, k)).astype(np.float32), device="cuda"))
+        probes[layer] = torch.as_tensor(rng.standard_normal((B, T, d)).astype(np.float32), device="cuda")
+    v0 = torch.as_tensor((rng.standard_normal((N, d)) * 0.02).astype(np.float32), device="cuda")
+    va, vb = v0.clone(), v0.clone()
+    ua = R.SparseRowUpdate(va, lr=1e-2, grad_clip=1.0)
+    ub = R.SparseRowUpdate(vb, lr=1e-2, grad_clip=1.0)
+    oa = ua(aux, probes, [0, 2], count_slots=True)
+    ob = ub(aux, probes, [0, 2])
+    torch.cuda.synchronize()
+    assert "slot_counts" not in ob
+    ref = sum(np.bincount(s.cpu().numpy().reshape(-1), minlength=N) for s in aux["slots"])
+    np.testing.assert_array_equal(oa["slot_counts"].cpu().numpy(), ref.astype(np.float32))
+    assert torch.equal(va, vb) and torch.equal(ua.acc, ub.acc)
