@@ -582,6 +582,28 @@ int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_
                          size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
                          void* stream);
 
+/*
+ * mpl_lookup_bwd_dense and mpl_lookup_bwd_queries in one (memory.py:150-164
+ * and 208-213 through the query normalisation, memory.py:136-141): the
+ * routed d q_hat (d_sub * T at each query's k selected sub-keys) joins the
+ * balance term in the dense query pass, on the fp16 / fp32 MFMA operand of
+ * the sub-key pass's scale, and the pass ends with the l2 normalisation
+ * backward, writing d_queries [M, 2H, half] fp32 (the gradient with respect
+ * to the raw queries; eps as in mpl_lookup_bwd_queries) and d k_hat as
+ * mpl_lookup_bwd_dense does.  queries [M, 2H, half] are the raw queries
+ * (16-byte aligned when half % 4 == 0), q_hat their normalisation.  Only
+ * with the balance term, without query_scale or balance_temperature_grad,
+ * and k <= 16 (MPL_EUNSUPPORTED otherwise).  Same workspace as
+ * mpl_lookup_bwd_dense.  No counterpart in the reference's interface (XLA
+ * fuses its own backward): it saves the separate routed query pass.
+ */
+int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const float* k_hat,
+                                 const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
+                                 const float* clean_counts, const void* state, const float* g_balance, int64_t M,
+                                 int H, int n, int half, int k, int score_dtype, const float* temperature,
+                                 void* workspace, size_t workspace_bytes, float eps, float* d_queries,
+                                 float* dk_hat, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -582,16 +582,20 @@ struct BalGradParams {
   const float* rho;  // DQ: [M, HC] output scale (q_len in the balance logits) or null
   float* out;        // DQ: d q_hat [M, HC, half]; DK: partial d k_hat [splits, HC, n, half]
   float* u;          // DQ: [HC, M] c sum_n p (f - r) cos, or null; Div: per-workgroup sums of squares
-  // kModeDK only
+  // kModeDK and kModeDQR
   int bal;                // balance terms on (g, state, counts valid)
   const int32_t* sub_idx; // routed term: stage-1 ids [M, HC, k], or null
   const float* d_sub;     // routed term: d sub_scores [M, HC, k]
   const float* qlen_rt;   // routed term: q_len [M, HC] with query_scale, or null
   int k;
   const float* dk_scale;  // [HC] operand scale S: the operand is dcos / S, d k_hat = S * acc
+  // kModeDQR only
+  const float* q_raw;     // raw queries [M, HC, half]
+  float eps;              // the l2 normalisation's epsilon
+  float* dq;              // d queries [M, HC, half] (through the normalisation)
 };
 
-enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2 };
+enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2, kModeDQR = 3 };
 
 // kModeDQ: the fixed side is 32 queries per wave (B operand), sub-key blocks
 // stream.  kModeDK: the fixed side is 32 sub-keys per wave, blocks of 32
@@ -602,6 +606,13 @@ enum { kModeDQ = 0, kModeDK = 1, kModeDiv = 2 };
 // 128 sub-keys are scattered into an LDS tile [key][query] one block ahead;
 // every lane reads its 16 entries and zeroes them, so the tile is clean when
 // its buffer comes round again.
+// kModeDQR: kModeDQ with the routed term of the queries (d_sub * T of
+// memory.py:150-163 at the k selected sub-keys of each query) in the same
+// operand, over the same scale S as kModeDK (the bound of both terms), the
+// routed entries of the workgroup's 128 queries held in registers and
+// scattered into an LDS tile [query][key] one key block ahead; the epilogue
+// takes d q_hat through the l2 normalisation backward to d queries (no
+// query_scale, no balance temperature gradient).
 // kModeDiv: both sides are the sub-keys of one codebook (the Gram matrix of
 // key_diversity_loss); the operand is the off-diagonal cosine itself and each
 // lane also sums its squares into u[workgroup * 256 + thread].
@@ -614,25 +625,28 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   typedef BalShape<E, HP> Sh;
   typedef typename Sh::Ops Ops;
   typedef typename Ops::MF MF;
-  constexpr bool DK = MODE != kModeDQ;  // the fixed side is sub-keys
+  constexpr bool DK = MODE == kModeDK || MODE == kModeDiv;  // the fixed side is sub-keys
   constexpr bool DIV = MODE == kModeDiv;
+  constexpr bool DQR = MODE == kModeDQR;
+  constexpr bool RT = MODE == kModeDK || DQR;  // an LDS tile of routed entries [fixed row][streamed row]
   const float Tv = DIV ? 0.f : *p.T;  // Div mode has no temperature (p.T null)
   constexpr int NCH = Sh::NCH, OPV = Sh::OPV, ND = Sh::ND;
   constexpr int TN = Sh::NV * kWave, TT = ND * Sh::TVPD * kWave, TILE = TN + TT;
   __shared__ uint4 tiles[2][TILE];
   __shared__ __attribute__((aligned(16)))
-  float rtile[MODE == kModeDK ? 2 : 1][MODE == kModeDK ? kRowsPerGroup : 1][MODE == kModeDK ? kRtPitch : 1];
-  // kModeDK: the forward state of the streamed block's 32 queries, staged
-  // with the block's tiles (one block ahead, double-buffered) so that the
+  float rtile[RT ? 2 : 1][RT ? kRowsPerGroup : 1][RT ? kRtPitch : 1];
+  // kModeDK: the forward state of the streamed block's 32 queries; kModeDQ
+  // and kModeDQR: the clean counts of its 32 sub-keys (in .x); staged with
+  // the block's tiles (one block ahead, double-buffered) so that the
   // per-element reads come from LDS instead of global memory
-  __shared__ float4 sstate[MODE == kModeDK ? 2 : 1][MODE == kModeDK ? 32 : 1];
+  __shared__ float4 sstate[MODE != kModeDiv ? 2 : 1][MODE != kModeDiv ? 32 : 1];
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, par = lane >> 5;
   const int hc = blockIdx.x % p.HC;
   const int64_t rest = blockIdx.x / p.HC;
   const int split = (int)(rest % p.splits);
   const int64_t fg = rest / p.splits;
-  const bool route = MODE == kModeDK && p.sub_idx != nullptr;
+  const bool route = RT && p.sub_idx != nullptr;
   const bool bal = MODE != kModeDK || p.bal != 0;
   const int64_t fb = fg * kBalWaves + wave;  // this wave's fixed block
   const int64_t nfix = DK ? p.n : p.M;
@@ -653,13 +667,14 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   const float* cnt = bal && !DIV ? p.counts + (int64_t)hc * p.n : nullptr;
   const float4* sth = bal && !DIV ? p.state + (int64_t)hc * p.M : nullptr;
   const float cc = (bal && !DIV) ? *p.g * p.coef : 1.f;
-  const float invS = MODE == kModeDK ? 1.f / p.dk_scale[hc] : 1.f;
+  const float invS = RT ? 1.f / p.dk_scale[hc] : 1.f;
+  const float a1 = cc * Tv * invS;  // kModeDQR: the balance term's factor on the operand
   // per-lane constants of the fixed row
   float4 fst = make_float4(0.f, 0.f, 0.f, 0.f);
   float ffix = 0.f;
   if (MODE == kModeDK && bal)
     ffix = cnt[valid ? my_f : 0] * p.inv_mk;
-  else if (MODE == kModeDQ)
+  else if (MODE == kModeDQ || DQR)
     fst = sth[valid ? my_f : 0];
   const float rs_fix = fst.y * sig;
   const int64_t k0 = fg * kRowsPerGroup;  // kModeDK: the workgroup's first sub-key
@@ -693,18 +708,52 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   auto rstore = [&](int x) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < kRtPer; ++i)
-      if (MODE == kModeDK && rrel[i] >= 0) rtile[MODE == kModeDK ? x : 0][MODE == kModeDK ? rrel[i] : 0][MODE == kModeDK ? rq[i] : 0] = rval[i];
+      if (MODE == kModeDK && rrel[i] >= 0) rtile[RT ? x : 0][RT ? rrel[i] : 0][RT ? rq[i] : 0] = rval[i];
+  };
+  // kModeDQR: entry e = tid + 256 i of the workgroup's 128 queries x k
+  // (k <= 16: at most 8 per thread), id and d_sub T / S, loaded once;
+  // qstore writes those of key block b to rtile[x][query][id - 32 b]
+  constexpr int kRtQ = DQR ? 8 : 1;
+  int qid[kRtQ], qrow[kRtQ];
+  float qval[kRtQ];
+  if constexpr (DQR) {
+#pragma unroll
+    for (int i = 0; i < kRtQ; ++i) {
+      const int e = tid + i * kBalThreads;
+      qid[i] = -1;
+      qrow[i] = 0;
+      qval[i] = 0.f;
+      if (e >= kRowsPerGroup * p.k) continue;
+      const int ql = e / p.k, j = e - ql * p.k;
+      const int64_t m = fg * kRowsPerGroup + ql;
+      if (m >= p.M) continue;
+      const int64_t o = (m * p.HC + hc) * p.k + j;
+      const int id = p.sub_idx[o];
+      if (id < 0 || id >= p.n) continue;
+      qid[i] = id;
+      qrow[i] = ql;
+      qval[i] = p.d_sub[o] * Tv * invS;
+    }
+  }
+  auto qstore = [&](int x, int64_t b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kRtQ; ++i)
+      if (DQR && qid[i] >= 0 && (qid[i] >> 5) == b) rtile[RT ? x : 0][RT ? qrow[i] : 0][RT ? (qid[i] & 31) : 0] = qval[i];
   };
 
   const int64_t sb0 = (int64_t)split * p.sblk_per_split;
   const int64_t sb1 = sb0 + p.sblk_per_split < p.sblk ? sb0 + p.sblk_per_split : p.sblk;
-  constexpr bool SST = MODE == kModeDK;
+  constexpr bool SST = MODE != kModeDiv;
   const bool sst = SST && bal && tid < 32;  // the threads that stage a block's states
   float4 st_next = make_float4(0.f, 0.f, 0.f, 0.f);
   auto sload = [&](int64_t b) __attribute__((always_inline)) {
     if (sst) {
       const int64_t row = b * 32 + tid;
-      st_next = sth[row < nstr ? row : nstr - 1];
+      const int64_t rc = row < nstr ? row : nstr - 1;
+      if (MODE == kModeDK)
+        st_next = sth[rc];
+      else
+        st_next.x = cnt[rc];
     }
   };
   auto sstore = [&](int x) __attribute__((always_inline)) {
@@ -721,11 +770,12 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   Stage<TT> stt;
   if (route) {
     float* rt = &rtile[0][0][0];
-    for (int i = tid; i < 2 * kRowsPerGroup * kRtPitch; i += kBalThreads) rt[MODE == kModeDK ? i : 0] = 0.f;
+    for (int i = tid; i < 2 * kRowsPerGroup * kRtPitch; i += kBalThreads) rt[RT ? i : 0] = 0.f;
     __syncthreads();
     if (sb0 < sb1) {
       rload(sb0);
       rstore(0);
+      qstore(0, sb0);
     }
   }
   if (sb0 < sb1) {
@@ -755,7 +805,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       // this lane's routed entries: key f_loc, queries 8 g4 + 4 par + [0, 4)
 #pragma unroll
       for (int g4 = 0; g4 < 4; ++g4) {
-        float4* src = (float4*)&rtile[MODE == kModeDK ? cur : 0][MODE == kModeDK ? f_loc : 0][MODE == kModeDK ? 8 * g4 + 4 * par : 0];
+        float4* src = (float4*)&rtile[RT ? cur : 0][RT ? f_loc : 0][RT ? 8 * g4 + 4 * par : 0];
         const float4 v = *src;
         *src = make_float4(0.f, 0.f, 0.f, 0.f);
         rtv[4 * g4] = v.x;
@@ -786,7 +836,11 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
         continue;
       } else {
         pe = exp2f(acc[r] * fst.z - fst.x);
-        diff = cnt[rc] * fs - rs_fix;
+        diff = sstate[SST ? cur : 0][SST ? 8 * (r >> 2) + 4 * par + (r & 3) : 0].x * fs - rs_fix;
+      }
+      if (DQR) {  // c p (f - r) T / S plus the routed d_sub T / S
+        gv[r] = (rv && valid) ? __builtin_fmaf(pe * diff, a1, rtv[r]) : 0.f;
+        continue;
       }
       gv[r] = (rv && valid) ? pe * diff : 0.f;
       if (!DK) usum = fmaf(gv[r], acc[r], usum);
@@ -807,6 +861,7 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
       stt.store(tiles[cur ^ 1] + TN, tid);
       sstore(cur ^ 1);
       if (route) rstore(cur ^ 1);
+      qstore(cur ^ 1, sb + 1);
     }
     __syncthreads();
   }
@@ -819,6 +874,64 @@ __global__ __launch_bounds__(kBalThreads) void balance_grad_kernel(BalGradParams
   }
   // DQ: c T (rho) / sigma * acc; DK: S * acc; Div: coef * acc.  Rows of
   // the output are the fixed rows
+  if constexpr (DQR) {
+    // d q_hat = S acc; d q = (d q_hat - q_hat (q_hat . d q_hat)) / |q|, as
+    // r dy - r^3 (x . dy) x with r = 1 / sqrt(|x|^2 + eps) (lane l holds dims
+    // 32 db + 8 g4 + 4 (l/32) + [0, 4) of query l % 32; the partner lane the rest)
+    const float S = p.dk_scale[hc];
+    const int64_t ro = ((valid ? my_f : 0) * p.HC + hc) * (int64_t)p.half;
+    const bool vec = (p.half & 3) == 0;  // whole float4s (the host checks the alignment)
+    float xv[ND][16];
+    float xdy = 0.f, ss = 0.f;
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * db + 8 * g4 + 4 * par;
+        float x[4] = {0.f, 0.f, 0.f, 0.f};
+        if (valid && vec && d < p.half) {
+          const float4 v = *(const float4*)(p.q_raw + ro + d);
+          x[0] = v.x;
+          x[1] = v.y;
+          x[2] = v.z;
+          x[3] = v.w;
+        } else if (valid && !vec) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) x[i] = d + i < p.half ? p.q_raw[ro + d + i] : 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float dy = gacc[db][4 * g4 + i] * S;
+          gacc[db][4 * g4 + i] = dy;
+          xv[db][4 * g4 + i] = x[i];
+          xdy = fmaf(x[i], dy, xdy);
+          ss = fmaf(x[i], x[i], ss);
+        }
+      }
+    xdy += partner(xdy, par);
+    ss += partner(ss, par);
+    const float rr = 1.f / sqrtf(ss + p.eps);
+    const float r3x = rr * rr * rr * xdy;
+    if (!valid) return;
+    float* orow = p.dq + ro;
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; ++g4) {
+        const int d = 32 * db + 8 * g4 + 4 * par;
+        float o[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = rr * gacc[db][4 * g4 + i] - r3x * xv[db][4 * g4 + i];
+        if (vec) {
+          if (d < p.half) *(float4*)(orow + d) = make_float4(o[0], o[1], o[2], o[3]);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (d + i < p.half) orow[d + i] = o[i];
+        }
+      }
+    return;
+  }
   float scale = DIV ? p.coef : (MODE == kModeDK ? p.dk_scale[hc] : cc * Tv / sig);
   if (!DK && p.rho != nullptr) scale *= p.rho[(valid ? my_f : 0) * p.HC + hc];
   if (!DK && p.u != nullptr) {
@@ -1116,14 +1229,16 @@ extern "C" size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, 
   return bwd_layout(M, H, n, half, f32).total;
 }
 
-extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat,
-                                    const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
-                                    const float* clean_counts, const void* state, const float* g_balance,
-                                    int balance_temperature_grad, int query_scale, int64_t M, int H, int n,
-                                    int half, int k, int score_dtype, const float* temperature, void* workspace,
-                                    size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
-                                    void* stream) {
-  clear_error();
+// q_raw / d_queries (both or neither): the fused form (kModeDQR) that also
+// takes the routed d q_hat and the normalisation backward, writing d queries
+// instead of the balance d q_hat.
+static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const float* k_hat,
+                                 const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
+                                 const float* clean_counts, const void* state, const float* g_balance,
+                                 int balance_temperature_grad, int query_scale, int64_t M, int H, int n, int half,
+                                 int k, int score_dtype, const float* temperature, void* workspace,
+                                 size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
+                                 const float* q_raw, float eps, float* d_queries, void* stream) {
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_lookup_bwd_dense: bad shape");
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
               "mpl_lookup_bwd_dense: bad score_dtype %d", score_dtype);
@@ -1135,6 +1250,15 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   const bool routed = sub_idx != nullptr || d_sub != nullptr;
   const bool btg = bal && balance_temperature_grad != 0;
   const bool scaled = btg && query_scale != 0;
+  const bool fused = d_queries != nullptr;
+  if (fused) {
+    MPL_REQUIRE(M > 0 && bal && sub_idx != nullptr && d_sub != nullptr && q_raw != nullptr, MPL_EINVAL,
+                "mpl_lookup_bwd_dense_queries: needs tokens, the balance term, the routed term and the queries");
+    MPL_REQUIRE(!btg && query_scale == 0 && k <= 16, MPL_EUNSUPPORTED,
+                "mpl_lookup_bwd_dense_queries: only without query_scale and balance_temperature_grad, k <= 16");
+    MPL_REQUIRE((half & 3) != 0 || ((uintptr_t)q_raw & 15) == 0, MPL_EINVAL,
+                "mpl_lookup_bwd_dense_queries: queries must be 16-byte aligned");
+  }
   MPL_REQUIRE(dk_hat != nullptr && (!btg || dlogt != nullptr), MPL_EINVAL, "mpl_lookup_bwd_dense: null output");
   MPL_REQUIRE(!routed || (sub_idx != nullptr && d_sub != nullptr), MPL_EINVAL,
               "mpl_lookup_bwd_dense: sub_idx and d_sub go together");
@@ -1150,7 +1274,7 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
     return check_launch("mpl_lookup_bwd_dense");
   }
   MPL_REQUIRE(q_hat && k_hat && packed_keys && temperature, MPL_EINVAL, "mpl_lookup_bwd_dense: null buffer");
-  MPL_REQUIRE(!bal || (clean_counts && state && dq_hat), MPL_EINVAL,
+  MPL_REQUIRE(!bal || (clean_counts && state && (dq_hat || fused)), MPL_EINVAL,
               "mpl_lookup_bwd_dense: the balance term needs clean_counts, state and dq_hat");
   const BwdLayout L = bwd_layout(M, H, n, half, f32);
   MPL_REQUIRE(workspace != nullptr && workspace_bytes >= L.total, MPL_EWORKSPACE,
@@ -1218,6 +1342,17 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   pq.sblk_per_split = L.nblk;
   pq.out = dq_hat;
   pq.u = btg ? u : nullptr;
+  if (fused) {
+    pq.out = nullptr;
+    pq.u = nullptr;
+    pq.sub_idx = sub_idx;
+    pq.d_sub = d_sub;
+    pq.k = k;
+    pq.dk_scale = dks;
+    pq.q_raw = q_raw;
+    pq.eps = eps;
+    pq.dq = d_queries;
+  }
   const unsigned gq = (unsigned)(HC * cdiv(M, kRowsPerGroup));
   // d k_hat (balance and routed terms): fixed = sub-keys, streamed = queries
   BalGradParams pk = p;
@@ -1238,8 +1373,9 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   pk.k = k;
   pk.dk_scale = dks;
   const unsigned gk = (unsigned)(HC * cdiv(n, kRowsPerGroup) * L.splits);
-#define MPL_GRAD(EV, HPV)                                                        \
-  if (bal) balance_grad_kernel<kModeDQ, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq); \
+#define MPL_GRAD(EV, HPV)                                                                \
+  if (fused) balance_grad_kernel<kModeDQR, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq);      \
+  else if (bal) balance_grad_kernel<kModeDQ, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq);    \
   balance_grad_kernel<kModeDK, EV, HPV><<<gk, kBalThreads, 0, s>>>(pk)
   MPL_BAL_DISPATCH(f32, L.pd.HP, MPL_GRAD);
 #undef MPL_GRAD
@@ -1253,6 +1389,33 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
     sum_plain_kernel<<<1, 1024, 0, s>>>(tpart, gt, 1.0, dlogt);
   }
   return check_launch("mpl_lookup_bwd_dense");
+}
+
+extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat,
+                                    const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
+                                    const float* clean_counts, const void* state, const float* g_balance,
+                                    int balance_temperature_grad, int query_scale, int64_t M, int H, int n,
+                                    int half, int k, int score_dtype, const float* temperature, void* workspace,
+                                    size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
+                                    void* stream) {
+  clear_error();
+  return lookup_bwd_dense_impl(q_hat, q_len, k_hat, packed_keys, sub_idx, d_sub, clean_counts, state, g_balance,
+                               balance_temperature_grad, query_scale, M, H, n, half, k, score_dtype, temperature,
+                               workspace, workspace_bytes, dq_hat, dk_hat, dlen, dlogt, nullptr, 0.f, nullptr,
+                               stream);
+}
+
+extern "C" int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const float* k_hat,
+                                            const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
+                                            const float* clean_counts, const void* state, const float* g_balance,
+                                            int64_t M, int H, int n, int half, int k, int score_dtype,
+                                            const float* temperature, void* workspace, size_t workspace_bytes,
+                                            float eps, float* d_queries, float* dk_hat, void* stream) {
+  clear_error();
+  MPL_REQUIRE(d_queries != nullptr, MPL_EINVAL, "mpl_lookup_bwd_dense_queries: null d_queries");
+  return lookup_bwd_dense_impl(q_hat, nullptr, k_hat, packed_keys, sub_idx, d_sub, clean_counts, state, g_balance,
+                               0, 0, M, H, n, half, k, score_dtype, temperature, workspace, workspace_bytes,
+                               nullptr, dk_hat, nullptr, nullptr, queries, eps, d_queries, stream);
 }
 
 namespace mpl {

@@ -35,6 +35,9 @@ from . import _lib
 from ._lib import MPL_F16, MPL_F32, check, ptr
 
 NORM_EPS = 1e-6
+# The routed query gradient inside the dense balance pass where it applies
+# (mpl_lookup_bwd_dense_queries); False keeps the separate query pass.
+FUSED_QUERY_BWD = True
 
 
 def _dtype_code(dt: torch.dtype) -> int:
@@ -665,7 +668,22 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
     bal = g_balance is not None and "_state" in internal
     code = res["score_code"]
     dense = M > 0 and (code == MPL_F16 or bal)
-    if dense:
+    # the routed query gradient inside the balance pass (one launch fewer)
+    fused_q = (FUSED_QUERY_BWD and dense and bal and not btg and not pool.query_scale and k <= 16
+               and (half % 4 or q.data_ptr() % 16 == 0))
+    dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
+    if fused_q:
+        dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
+        gb = g_balance.reshape(1).float().contiguous()
+        wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half, code)
+        ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+        check(L.mpl_lookup_bwd_dense_queries(ptr(q_hat), ptr(q), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
+                                             ptr(d_sub), ptr(internal["_counts"]), ptr(internal["_state"]), ptr(gb),
+                                             M, H, n, half, k, code, ptr(T), ptr(ws), wsb, NORM_EPS, ptr(dq),
+                                             ptr(dk_hat), stream), "mpl_lookup_bwd_dense_queries")
+        check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
+                                     stream), "mpl_l2_normalize_bwd")
+    elif dense:
         dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
         gb = None
         if bal:
@@ -685,10 +703,10 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
                                      stream), "mpl_l2_normalize_bwd")
 
     # queries
-    dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
-    check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
-                                   ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
-                                   ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
+    if not fused_q:
+        check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
+                                       ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
+                                       ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
     # sub-keys (fp32 scoring without the balance term, or no tokens):
     # sort-by-key segmented sum
     if not dense:

@@ -92,3 +92,34 @@ def test_training_backward_c4_with_noise(gpu_lib):
     _check(gk.cpu().numpy(), ref["d_sub_keys"], 1e-2, "d_sub_keys")
     _check(float(gt), ref["d_log_temperature"], 1e-2, "d_log_temperature",
            float(np.abs(ref["d_cos"] * sel["cos"]).sum()))
+
+
+@pytest.mark.parametrize("values_dtype,M", [(torch.float16, 8192), (torch.float16, 300), (torch.float32, 1000)])
+def test_fused_query_backward_equals_separate_pass(gpu_lib, monkeypatch, values_dtype, M):
+    """mpl_lookup_bwd_dense_queries (the routed d q_hat inside the balance
+    query pass, then the normalisation backward) against the separate
+    passes (mpl_lookup_bwd_dense + mpl_lookup_bwd_queries) on the same
+    forward: d queries within 2e-3 of max |d q| in fp16 (the routed term
+    rides the fp16 MFMA operand there) and 1e-5 in fp32; the sub-key and
+    log-temperature gradients are those of the separate path bit for bit."""
+    from model_amd import memory as mem
+    k = 16
+    pool = MemoryPool(N_SUB if values_dtype == torch.float16 else 64, H, D_KEY, D, k, routing_noise=1.0,
+                      values_dtype=values_dtype)
+    params = make_params(pool, 77, key_std=(D_KEY // 2) ** -0.5, value_std=0.02)
+    g = torch.Generator(device="cuda").manual_seed(78)
+    q = torch.randn((M, H, D_KEY), generator=g, device="cuda")
+    g_out = torch.randn((M, D), generator=g, device="cuda") * 1e-3
+    g_bal = torch.full((), 0.01, device="cuda")
+    print(f"fused query backward {values_dtype} M={M}", flush=True)
+    out = {}
+    for fused in (True, False):
+        monkeypatch.setattr(mem, "FUSED_QUERY_BWD", fused)
+        o, aux, grads = pool.forward_backward(params, q, g_out, g_bal, train=True, rngs={"routing": 5})
+        out[fused] = [t.clone() for t in grads]
+    torch.cuda.synchronize()
+    (dqa, dka, dla), (dqb, dkb, dlb) = out[True], out[False]
+    tol = 2e-3 if values_dtype == torch.float16 else 1e-5
+    err = float((dqa - dqb).abs().max()) / float(dqb.abs().max())
+    assert err <= tol, f"d queries: {err:.3g} of max |d q| > {tol}"
+    assert torch.equal(dka, dkb) and torch.equal(dla, dlb)
