@@ -591,7 +591,9 @@ int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_
  * backward, writing d_queries [M, 2H, half] fp32 (the gradient with respect
  * to the raw queries; eps as in mpl_lookup_bwd_queries) and d k_hat as
  * mpl_lookup_bwd_dense does.  queries [M, 2H, half] are the raw queries
- * (16-byte aligned when half % 4 == 0), q_hat their normalisation.  Only
+ * (16-byte aligned when half % 4 == 0), q_hat their normalisation, or NULL
+ * with fp16 scoring at half = 64 or 128: the operand packs then normalise
+ * the raw queries themselves, to the same bits as mpl_l2_normalize.  Only
  * with the balance term, without query_scale or balance_temperature_grad,
  * and k <= 16 (MPL_EUNSUPPORTED otherwise).  Same workspace as
  * mpl_lookup_bwd_dense.  No counterpart in the reference's interface (XLA

@@ -406,15 +406,21 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const float* __restrict_
 // writes the normal pack (a vector is 8 consecutive dims of one row) and the
 // transposed pack (a vector is one dim of 8 rows) from the tile.  The same
 // fp16 values in the same places as the two separate launches.
-template <int HP>
+// NORM: X holds raw rows, normalised here exactly as l2norm_kernel does
+// (16 partial sums of squares per row, j = l, l + 16, ... by fma from 0,
+// joined in its xor-butterfly order, then x * (1 / sqrt(sum + eps))), so the
+// packs equal those of the normalised rows bit for bit.
+template <int HP, bool NORM>
 __global__ __launch_bounds__(256) void pack_rows_both_f16_kernel(const float* __restrict__ X, int64_t s_hc,
                                                                  int64_t s_row, int64_t nrows, int64_t nblk,
-                                                                 uint4* __restrict__ out_n, uint4* __restrict__ out_t) {
+                                                                 float eps, uint4* __restrict__ out_n,
+                                                                 uint4* __restrict__ out_t) {
   constexpr int PITCH = HP + 4;  // floats per staged row (16-byte aligned rows, shifted banks)
   constexpr int V4 = HP / 4;     // 16-byte vectors per row
   constexpr int NV = HP / 16;    // normal pack: vectors per lane per block
   constexpr int NT = HP / 16;    // transposed pack: HP / 32 dim groups x 2 vectors
   __shared__ float tile[32 * PITCH];
+  __shared__ float psum[NORM ? 32 : 1][NORM ? 17 : 1];
   const int64_t blk = blockIdx.x % nblk;
   const int64_t hc = blockIdx.x / nblk;
   const float* base = X + hc * s_hc;
@@ -425,6 +431,32 @@ __global__ __launch_bounds__(256) void pack_rows_both_f16_kernel(const float* __
     *(float4*)(tile + rr * PITCH + 4 * c4) = v;
   }
   __syncthreads();
+  if constexpr (NORM) {
+    for (int t = threadIdx.x; t < 32 * 16; t += 256) {
+      const int rr = t >> 4, l = t & 15;
+      float sq = 0.f;
+      for (int j = l; j < HP; j += 16) sq = fmaf(tile[rr * PITCH + j], tile[rr * PITCH + j], sq);
+      psum[NORM ? rr : 0][NORM ? l : 0] = sq;
+    }
+    __syncthreads();
+    if (threadIdx.x < 32) {
+      const float* ps = psum[NORM ? threadIdx.x : 0];
+      float t8[8], t4[4];
+#pragma unroll
+      for (int l = 0; l < 8; ++l) t8[l] = ps[l] + ps[l + 8];
+#pragma unroll
+      for (int l = 0; l < 4; ++l) t4[l] = t8[l] + t8[l + 4];
+      const float v0 = t4[0] + t4[2], v1 = t4[1] + t4[3];
+      const float tot = (v0 + v1) + eps;
+      psum[NORM ? threadIdx.x : 0][NORM ? 16 : 0] = 1.0f / sqrtf(tot);
+    }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 32 * HP; t += 256) {
+      const int rr = t / HP, j = t % HP;
+      tile[rr * PITCH + j] = tile[rr * PITCH + j] * psum[NORM ? rr : 0][NORM ? 16 : 0];
+    }
+    __syncthreads();
+  }
   const int64_t ob = (hc * nblk + blk) * (int64_t)(NV * kWave);
   for (int t = threadIdx.x; t < NV * kWave; t += 256) {
     const int v = t / kWave, l = t % kWave;
@@ -1273,7 +1305,8 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
       fill_zero_kernel<<<grid_for(M * HC * half, 256), 256, 0, s>>>(dq_hat, M * HC * half);
     return check_launch("mpl_lookup_bwd_dense");
   }
-  MPL_REQUIRE(q_hat && k_hat && packed_keys && temperature, MPL_EINVAL, "mpl_lookup_bwd_dense: null buffer");
+  MPL_REQUIRE((q_hat || fused) && k_hat && packed_keys && temperature, MPL_EINVAL,
+              "mpl_lookup_bwd_dense: null buffer");
   MPL_REQUIRE(!bal || (clean_counts && state && (dq_hat || fused)), MPL_EINVAL,
               "mpl_lookup_bwd_dense: the balance term needs clean_counts, state and dq_hat");
   const BwdLayout L = bwd_layout(M, H, n, half, f32);
@@ -1291,13 +1324,23 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
   float* tpart = (float*)(ws + L.tpart);
   const float* rho = scaled ? q_len : nullptr;
 
-  const bool both = !f32 && L.pd.HP == half && (half == 64 || half == 128) && ((uintptr_t)q_hat & 15) == 0;
-  if (both && half == 128)
-    pack_rows_both_f16_kernel<128><<<(unsigned)(HC * L.mblk), 256, 0, s>>>(q_hat, half, (int64_t)HC * half, M, L.mblk,
-                                                                           qn, qt);
-  else if (both)
-    pack_rows_both_f16_kernel<64><<<(unsigned)(HC * L.mblk), 256, 0, s>>>(q_hat, half, (int64_t)HC * half, M, L.mblk,
-                                                                          qn, qt);
+  // without q_hat (fused form only) the packs normalise the raw queries
+  const bool norm = q_hat == nullptr;
+  const float* qsrc = norm ? q_raw : q_hat;
+  const bool both = !f32 && L.pd.HP == half && (half == 64 || half == 128) && ((uintptr_t)qsrc & 15) == 0;
+  MPL_REQUIRE(both || !norm, MPL_EINVAL, "mpl_lookup_bwd_dense: q_hat is needed here (only fp16 scoring at half "
+              "64 or 128 packs the raw queries)");
+#define MPL_PACK_BOTH(HPV, NRM)                                                                               \
+  pack_rows_both_f16_kernel<HPV, NRM><<<(unsigned)(HC * L.mblk), 256, 0, s>>>(qsrc, half, (int64_t)HC * half, M, \
+                                                                              L.mblk, eps, qn, qt)
+  if (both && half == 128) {
+    if (norm) MPL_PACK_BOTH(128, true);
+    else MPL_PACK_BOTH(128, false);
+  } else if (both) {
+    if (norm) MPL_PACK_BOTH(64, true);
+    else MPL_PACK_BOTH(64, false);
+  }
+#undef MPL_PACK_BOTH
   if (!both) {
     launch_pack<false>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
     launch_pack<true>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);

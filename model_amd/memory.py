@@ -38,6 +38,9 @@ NORM_EPS = 1e-6
 # The routed query gradient inside the dense balance pass where it applies
 # (mpl_lookup_bwd_dense_queries); False keeps the separate query pass.
 FUSED_QUERY_BWD = True
+# In that pass, fp16 operand packs made from the raw queries (normalised in
+# the pack, the same bits as the fp32 q_hat pass); False packs q_hat.
+RAW_QUERY_PACK = True
 
 
 def _dtype_code(dt: torch.dtype) -> int:
@@ -638,7 +641,7 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
     L = _lib.lib()
     stream = _lib.stream_ptr(dev)
     T = res["temperature"]
-    q_hat, q_len, k_hat = res["q_hat"], res["q_len"], res["k_hat"]
+    q_len, k_hat = res["q_len"], res["k_hat"]
     if g_out is None:
         g_out = torch.zeros((M, d), dtype=torch.float32, device=dev)
     g_out = g_out.reshape(M, d).float().contiguous()
@@ -677,6 +680,10 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
         gb = g_balance.reshape(1).float().contiguous()
         wsb = L.mpl_lookup_bwd_dense_workspace_bytes(M, H, n, half, code)
         ws = torch.empty(max(wsb, 256), dtype=torch.uint8, device=dev)
+        # fp16 operands at half 64 / 128 are packed from the raw queries
+        # (normalised in the pack): no fp32 q_hat pass
+        raw_pack = RAW_QUERY_PACK and code == MPL_F16 and half in (64, 128)
+        q_hat = None if raw_pack else res["q_hat"]
         check(L.mpl_lookup_bwd_dense_queries(ptr(q_hat), ptr(q), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
                                              ptr(d_sub), ptr(internal["_counts"]), ptr(internal["_state"]), ptr(gb),
                                              M, H, n, half, k, code, ptr(T), ptr(ws), wsb, NORM_EPS, ptr(dq),
@@ -684,6 +691,7 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
         check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
                                      stream), "mpl_l2_normalize_bwd")
     elif dense:
+        q_hat = res["q_hat"]
         dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
         gb = None
         if bal:
@@ -712,7 +720,7 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
     if not dense:
         wsb = max(L.mpl_lookup_bwd_keys_workspace_bytes(M, H, n, half, k), 256)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-        check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(q_hat), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
+        check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(res["q_hat"]), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
                                     None, M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
               "mpl_lookup_bwd_keys")
     # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)

@@ -123,3 +123,28 @@ def test_fused_query_backward_equals_separate_pass(gpu_lib, monkeypatch, values_
     err = float((dqa - dqb).abs().max()) / float(dqb.abs().max())
     assert err <= tol, f"d queries: {err:.3g} of max |d q| > {tol}"
     assert torch.equal(dka, dkb) and torch.equal(dla, dlb)
+
+
+@pytest.mark.parametrize("d_key", [256, 128])
+def test_raw_query_pack_equals_q_hat_pack(gpu_lib, monkeypatch, d_key):
+    """The fused query pass with its fp16 operand packs made from the raw
+    queries (normalised inside the pack) gives the gradients of the same
+    pass fed the fp32 q_hat of mpl_l2_normalize, bit for bit (half = 128
+    and 64)."""
+    from model_amd import memory as mem
+    M, k = 1000, 16
+    pool = MemoryPool(128, H, d_key, 64, k, routing_noise=1.0, values_dtype=torch.float16)
+    params = make_params(pool, 91, key_std=(d_key // 2) ** -0.5, value_std=0.02)
+    g = torch.Generator(device="cuda").manual_seed(92)
+    q = torch.randn((M, H, d_key), generator=g, device="cuda") * 3.0
+    g_out = torch.randn((M, 64), generator=g, device="cuda") * 1e-3
+    g_bal = torch.full((), 0.01, device="cuda")
+    print(f"raw query pack d_key={d_key}", flush=True)
+    out = {}
+    for raw in (True, False):
+        monkeypatch.setattr(mem, "RAW_QUERY_PACK", raw)
+        _, _, grads = pool.forward_backward(params, q, g_out, g_bal, train=True, rngs={"routing": 9})
+        out[raw] = [t.clone() for t in grads]
+    torch.cuda.synchronize()
+    for a, b in zip(out[True], out[False]):
+        assert torch.equal(a, b)
