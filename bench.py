@@ -535,19 +535,18 @@ def train_step_bench(torch, iters):
     torch.cuda.synchronize()
     ms = a.elapsed_time(b) / iters
 
-    # The same step without torch autograd (MemoryPool.forward_backward and
-    # key_diversity_value_and_grad; the projection's gradient as a product),
+    # The same step without torch autograd (MemoryPool.forward_backward with
+    # the key diversity term; the projection's gradient as a product),
     # captured in one HIP graph and replayed.
-    from model_amd.memory import key_diversity_value_and_grad
     g_bal = torch.full((), 0.01, device=dev)
     g_div = torch.full((), 0.01, device=dev)
 
     def step_graph(_i):
         with torch.no_grad():
             q = (hidden @ w_q).reshape(M, H, d_key)
-            out, aux, (dq, dk, dlt) = pool.forward_backward({"params": params}, q, g_out, g_bal, train=True)
-            _, dk_div = key_diversity_value_and_grad(keys, g_div)
-            gk = dk + dk_div
+            # the key diversity term's gradient joins d sub_keys inside the call
+            out, aux, (dq, gk, dlt) = pool.forward_backward({"params": params}, q, g_out, g_bal, train=True,
+                                                            g_diversity=g_div)
             gw = hidden.t() @ dq.reshape(M, H * d_key)
             rest = R.sum_squares([gw, gk, dlt])  # no memset node in the captured step
             upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest,

@@ -583,28 +583,38 @@ int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_
                          void* stream);
 
 /*
- * mpl_lookup_bwd_dense and mpl_lookup_bwd_queries in one (memory.py:150-164
- * and 208-213 through the query normalisation, memory.py:136-141): the
- * routed d q_hat (d_sub * T at each query's k selected sub-keys) joins the
- * balance term in the dense query pass, on the fp16 / fp32 MFMA operand of
- * the sub-key pass's scale, and the pass ends with the l2 normalisation
- * backward, writing d_queries [M, 2H, half] fp32 (the gradient with respect
- * to the raw queries; eps as in mpl_lookup_bwd_queries) and d k_hat as
- * mpl_lookup_bwd_dense does.  queries [M, 2H, half] are the raw queries
- * (16-byte aligned when half % 4 == 0), q_hat their normalisation, or NULL
- * with fp16 scoring at half = 64 or 128: the operand packs then normalise
- * the raw queries themselves, to the same bits as mpl_l2_normalize.  Only
- * with the balance term, without query_scale or balance_temperature_grad,
- * and k <= 16 (MPL_EUNSUPPORTED otherwise).  Same workspace as
- * mpl_lookup_bwd_dense.  No counterpart in the reference's interface (XLA
- * fuses its own backward): it saves the separate routed query pass.
+ * The dense backward of a training step in one call (memory.py:136-164 and
+ * 208-213; train.py's key diversity term, memory.py:230-240): what
+ * mpl_lookup_bwd_dense, mpl_lookup_bwd_queries, mpl_key_diversity and the two
+ * l2 normalisation backwards of the sub-keys compute, with fewer passes.
+ *  - d_queries [M, 2H, half] fp32: the gradient with respect to the raw
+ *    queries.  The routed d q_hat (d_sub * T at each query's k selected
+ *    sub-keys) joins the balance term in the dense query pass, on the
+ *    fp16 / fp32 MFMA operand at the sub-key pass's scale, and the pass ends
+ *    with the l2 normalisation backward (eps as in mpl_lookup_bwd_queries).
+ *  - d_sub_keys [2H, n, half] fp32: the gradient with respect to the raw
+ *    sub_keys (fp32 [2H, n, half]) of the routed and balance terms, plus
+ *    *g_diversity times that of key_diversity_loss when g_diversity (a device
+ *    scalar) is given; the diversity loss then goes to diversity_loss [1].
+ *    The diversity Gram pass reuses this call's key packs; its workspace is
+ *    div_workspace (mpl_key_diversity_workspace_bytes).
+ * queries are the raw queries (16-byte aligned when half % 4 == 0), q_hat
+ * their normalisation, or NULL with fp16 scoring at half = 64 or 128: the
+ * operand packs then normalise the raw queries themselves, to the same bits
+ * as mpl_l2_normalize.  Only with the balance term, without query_scale or
+ * balance_temperature_grad, k <= 16 and half <= 128 (MPL_EUNSUPPORTED
+ * otherwise).  Workspace as mpl_lookup_bwd_dense.  No counterpart in the
+ * reference's interface (XLA fuses its own backward): it saves the separate
+ * routed query pass, the fp32 q_hat pass and the split sums.
  */
 int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const float* k_hat,
                                  const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
                                  const float* clean_counts, const void* state, const float* g_balance, int64_t M,
                                  int H, int n, int half, int k, int score_dtype, const float* temperature,
                                  void* workspace, size_t workspace_bytes, float eps, float* d_queries,
-                                 float* dk_hat, void* stream);
+                                 const float* sub_keys, const float* g_diversity, void* div_workspace,
+                                 size_t div_workspace_bytes, float* diversity_loss, float* d_sub_keys,
+                                 void* stream);
 
 #ifdef __cplusplus
 }

@@ -1021,6 +1021,83 @@ __global__ __launch_bounds__(256) void split_sum_kernel(const float* __restrict_
 }
 
 // dlen[m, hc] = T u (query_scale); part[m, hc] = T rho u (d log_t terms).
+// d sub_keys from partial d k_hat slices: dy = sum_i pa[i] + (*gb) sum_i
+// pb[i] (each [rows, dim], slices added in order as split_sum_kernel does),
+// then the l2 normalisation backward dx = r (dy - y (y . dy)), y = x r,
+// r = 1 / sqrt(sum x^2 + eps), in l2norm_bwd_kernel's lanes and order (16
+// lanes per row): without pb the result equals split_sum_kernel followed by
+// l2norm_bwd_kernel bit for bit.  A workgroup takes 8 rows: the slice sums
+// first (one float4 per thread, four slices' loads in flight), staged in
+// LDS, then the row pass on 128 of the threads.  dim % 4 == 0, dim <= 128.
+__device__ __forceinline__ void add4(float4& a, const float4 b) {
+  a.x += b.x;
+  a.y += b.y;
+  a.z += b.z;
+  a.w += b.w;
+}
+
+__device__ __forceinline__ float4 slice_sum4(const float4* __restrict__ p, int n, int64_t slice4, int64_t o) {
+  float4 a = p[o];
+  int i = 1;
+  for (; i + 4 <= n; i += 4) {
+    const float4 b0 = p[i * slice4 + o], b1 = p[(i + 1) * slice4 + o], b2 = p[(i + 2) * slice4 + o],
+                 b3 = p[(i + 3) * slice4 + o];
+    add4(a, b0);
+    add4(a, b1);
+    add4(a, b2);
+    add4(a, b3);
+  }
+  for (; i < n; ++i) add4(a, p[i * slice4 + o]);
+  return a;
+}
+
+__global__ __launch_bounds__(256) void keys_grad_kernel(const float* __restrict__ x, const float* __restrict__ pa,
+                                                        int na, const float* __restrict__ pb, int nb,
+                                                        const float* __restrict__ gb, int64_t rows, int dim,
+                                                        float eps, float* __restrict__ dx) {
+  constexpr int kRows = 8;
+  constexpr int kPitch = 144;  // floats per staged row (dim <= 128; rows 16 banks apart)
+  __shared__ float tdy[kRows * kPitch];
+  const int tid = threadIdx.x;
+  const int64_t r0 = (int64_t)blockIdx.x * kRows;
+  const int d4 = dim >> 2;
+  const int64_t slice4 = rows * d4;
+  const bool two = pb != nullptr && nb > 0;
+  {
+    const int rr = tid / d4, c4 = tid - rr * d4;  // d4 <= 32: the block's 8 rows fit 256 threads
+    if (rr < kRows && r0 + rr < rows) {
+      const int64_t o = (r0 + rr) * d4 + c4;
+      float4 a = slice_sum4((const float4*)pa, na, slice4, o);
+      if (two) {
+        const float g2 = *gb;
+        const float4 b = slice_sum4((const float4*)pb, nb, slice4, o);
+        a = make_float4(fmaf(g2, b.x, a.x), fmaf(g2, b.y, a.y), fmaf(g2, b.z, a.z), fmaf(g2, b.w, a.w));
+      }
+      *(float4*)&tdy[rr * kPitch + 4 * c4] = a;
+    }
+  }
+  __syncthreads();
+  if (tid >= 16 * kRows) return;
+  const int rr = tid >> 4, l = tid & 15;
+  const int64_t row = r0 + rr;
+  const int64_t rc = row < rows ? row : 0;
+  float ss = 0.f, xg = 0.f;
+  for (int j = l; j < dim; j += 16) {
+    const float v = x[rc * dim + j], g = tdy[rr * kPitch + j];
+    ss = fmaf(v, v, ss);
+    xg = fmaf(v, g, xg);
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) {
+    ss += __shfl_xor(ss, o, 16);
+    xg += __shfl_xor(xg, o, 16);
+  }
+  if (row >= rows) return;
+  const float r = 1.0f / sqrtf(ss + eps);
+  const float yg = xg * r;
+  for (int j = l; j < dim; j += 16) dx[row * dim + j] = r * (tdy[rr * kPitch + j] - x[row * dim + j] * r * yg);
+}
+
 __global__ __launch_bounds__(256) void balance_temp_kernel(const float* __restrict__ u, const float* __restrict__ rho,
                                                            int64_t M, int HC, const float* __restrict__ Tp,
                                                            float* __restrict__ dlen, float* __restrict__ part) {
@@ -1102,6 +1179,37 @@ unsigned grid_for(int64_t items, int64_t per_block, unsigned cap = 4096) {
   if (g < 1) g = 1;
   return (unsigned)(g < cap ? g : cap);
 }
+
+struct DivLayout {
+  size_t kt, part, lpart, total;
+  PackDims pd;
+  int splits;
+  int64_t nblk, sbps, groups;
+};
+
+DivLayout div_layout(int H, int n, int half, bool f32) {
+  DivLayout L;
+  const int HC = 2 * H;
+  L.pd = pack_dims(half, f32);
+  L.nblk = cdiv(n, 32);
+  const int64_t kgroups = (int64_t)HC * cdiv(n, kRowsPerGroup);
+  int64_t sp = cdiv(512, kgroups);
+  if (sp > L.nblk) sp = L.nblk;
+  if (sp < 1) sp = 1;
+  L.sbps = cdiv(L.nblk, sp);
+  L.splits = (int)cdiv(L.nblk, L.sbps);
+  L.groups = kgroups * L.splits;
+  size_t o = 0;
+  L.kt = o;
+  o += al256((size_t)HC * L.nblk * L.pd.ND * L.pd.TVPD * kWave * 16);
+  L.part = o;
+  o += al256((size_t)L.splits * HC * n * half * 4);
+  L.lpart = o;
+  o += al256((size_t)L.groups * 4);
+  L.total = o;
+  return L;
+}
+
 
 struct BwdLayout {
   size_t qn, qt, kt, sigma, dks, mx, part, u, tpart, total;
@@ -1261,6 +1369,17 @@ extern "C" size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, 
   return bwd_layout(M, H, n, half, f32).total;
 }
 
+// The fused form's sub-key gradient: d sub_keys [2H, n, half] written from
+// the sub-key pass's slices (and, with g_div, the key diversity pass's,
+// whose loss goes to div_loss), through the l2 normalisation of sub_keys.
+struct KeysGradArgs {
+  const float* sub_keys;
+  const float* g_div;
+  void* div_ws;
+  float* div_loss;
+  float* d_sub_keys;
+};
+
 // q_raw / d_queries (both or neither): the fused form (kModeDQR) that also
 // takes the routed d q_hat and the normalisation backward, writing d queries
 // instead of the balance d q_hat.
@@ -1270,7 +1389,8 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
                                  int balance_temperature_grad, int query_scale, int64_t M, int H, int n, int half,
                                  int k, int score_dtype, const float* temperature, void* workspace,
                                  size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
-                                 const float* q_raw, float eps, float* d_queries, void* stream) {
+                                 const float* q_raw, float eps, float* d_queries, const KeysGradArgs* kg,
+                                 void* stream) {
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_lookup_bwd_dense: bad shape");
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
               "mpl_lookup_bwd_dense: bad score_dtype %d", score_dtype);
@@ -1291,7 +1411,8 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
     MPL_REQUIRE((half & 3) != 0 || ((uintptr_t)q_raw & 15) == 0, MPL_EINVAL,
                 "mpl_lookup_bwd_dense_queries: queries must be 16-byte aligned");
   }
-  MPL_REQUIRE(dk_hat != nullptr && (!btg || dlogt != nullptr), MPL_EINVAL, "mpl_lookup_bwd_dense: null output");
+  MPL_REQUIRE((dk_hat != nullptr || kg != nullptr) && (!btg || dlogt != nullptr), MPL_EINVAL,
+              "mpl_lookup_bwd_dense: null output");
   MPL_REQUIRE(!routed || (sub_idx != nullptr && d_sub != nullptr), MPL_EINVAL,
               "mpl_lookup_bwd_dense: sub_idx and d_sub go together");
   MPL_REQUIRE(M == 0 || q_len != nullptr || !(query_scale != 0 && (routed || scaled)), MPL_EINVAL,
@@ -1406,7 +1527,7 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
   pk.sblk = L.mblk;
   pk.splits = L.splits;
   pk.sblk_per_split = L.sbps;
-  pk.out = L.splits == 1 ? dk_hat : part;
+  pk.out = (L.splits == 1 && kg == nullptr) ? dk_hat : part;
   pk.u = nullptr;
   pk.rho = nullptr;
   pk.bal = bal ? 1 : 0;
@@ -1422,7 +1543,42 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
   balance_grad_kernel<kModeDK, EV, HPV><<<gk, kBalThreads, 0, s>>>(pk)
   MPL_BAL_DISPATCH(f32, L.pd.HP, MPL_GRAD);
 #undef MPL_GRAD
-  if (L.splits > 1) {
+  if (kg != nullptr) {
+    // d sub_keys straight from the slices: the sub-key pass's, and with
+    // g_div the key diversity Gram pass's on the same packs (memory.py:230-240)
+    float* dpart = nullptr;
+    int dsplits = 0;
+    if (kg->g_div != nullptr) {
+      const DivLayout Ld = div_layout(H, n, half, f32);
+      dpart = (float*)((char*)kg->div_ws + Ld.part);
+      float* lpart = (float*)((char*)kg->div_ws + Ld.lpart);
+      const double D = (double)HC * n * (double)(n - 1);
+      BalGradParams pd = {};
+      pd.fix = (const uint4*)packed_keys;
+      pd.str = (const uint4*)packed_keys;
+      pd.strT = kt;
+      pd.coef = (float)(4.0 / D);
+      pd.M = 0;
+      pd.HC = HC;
+      pd.n = n;
+      pd.half = half;
+      pd.fblk = L.nblk;
+      pd.sblk = L.nblk;
+      pd.splits = Ld.splits;
+      pd.sblk_per_split = Ld.sbps;
+      pd.out = dpart;
+      pd.u = lpart;
+      const unsigned gd = (unsigned)Ld.groups;
+#define MPL_DIV(EV, HPV) balance_grad_kernel<kModeDiv, EV, HPV><<<gd, kBalThreads, 0, s>>>(pd)
+      MPL_BAL_DISPATCH(f32, L.pd.HP, MPL_DIV);
+#undef MPL_DIV
+      sum_plain_kernel<<<1, 1024, 0, s>>>(lpart, Ld.groups, 1.0 / D, kg->div_loss);
+      dsplits = Ld.splits;
+    }
+    const int64_t rows = (int64_t)HC * n;
+    keys_grad_kernel<<<(unsigned)cdiv(rows, 8), 256, 0, s>>>(kg->sub_keys, part, L.splits, dpart, dsplits, kg->g_div,
+                                                             rows, half, eps, kg->d_sub_keys);
+  } else if (L.splits > 1) {
     const int64_t cnt = (int64_t)HC * n * half;
     split_sum_kernel<<<grid_for(cnt, 256), 256, 0, s>>>(part, L.splits, cnt, dk_hat);
   }
@@ -1445,7 +1601,7 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   return lookup_bwd_dense_impl(q_hat, q_len, k_hat, packed_keys, sub_idx, d_sub, clean_counts, state, g_balance,
                                balance_temperature_grad, query_scale, M, H, n, half, k, score_dtype, temperature,
                                workspace, workspace_bytes, dq_hat, dk_hat, dlen, dlogt, nullptr, 0.f, nullptr,
-                               stream);
+                               nullptr, stream);
 }
 
 extern "C" int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const float* k_hat,
@@ -1453,46 +1609,30 @@ extern "C" int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* que
                                             const float* clean_counts, const void* state, const float* g_balance,
                                             int64_t M, int H, int n, int half, int k, int score_dtype,
                                             const float* temperature, void* workspace, size_t workspace_bytes,
-                                            float eps, float* d_queries, float* dk_hat, void* stream) {
+                                            float eps, float* d_queries, const float* sub_keys,
+                                            const float* g_diversity, void* div_workspace,
+                                            size_t div_workspace_bytes, float* diversity_loss, float* d_sub_keys,
+                                            void* stream) {
   clear_error();
-  MPL_REQUIRE(d_queries != nullptr, MPL_EINVAL, "mpl_lookup_bwd_dense_queries: null d_queries");
+  MPL_REQUIRE(d_queries != nullptr && sub_keys != nullptr && d_sub_keys != nullptr, MPL_EINVAL,
+              "mpl_lookup_bwd_dense_queries: null d_queries, sub_keys or d_sub_keys");
+  MPL_REQUIRE(half <= 128 && half % 4 == 0, MPL_EUNSUPPORTED,
+              "mpl_lookup_bwd_dense_queries: half must be a multiple of 4 up to 128");
+  if (g_diversity != nullptr) {
+    const size_t need = mpl_key_diversity_workspace_bytes(H, n, half, score_dtype);
+    MPL_REQUIRE(need > 0 && n > 1 && diversity_loss != nullptr && div_workspace != nullptr &&
+                    div_workspace_bytes >= need,
+                MPL_EWORKSPACE, "mpl_lookup_bwd_dense_queries: key diversity needs n > 1, its loss output and a "
+                "workspace of %zu bytes (%zu given)", need, div_workspace_bytes);
+  }
+  const KeysGradArgs kg{sub_keys, g_diversity, div_workspace, diversity_loss, d_sub_keys};
   return lookup_bwd_dense_impl(q_hat, nullptr, k_hat, packed_keys, sub_idx, d_sub, clean_counts, state, g_balance,
                                0, 0, M, H, n, half, k, score_dtype, temperature, workspace, workspace_bytes,
-                               nullptr, dk_hat, nullptr, nullptr, queries, eps, d_queries, stream);
+                               nullptr, nullptr, nullptr, nullptr, queries, eps, d_queries, &kg, stream);
 }
 
 namespace mpl {
 namespace {
-
-struct DivLayout {
-  size_t kt, part, lpart, total;
-  PackDims pd;
-  int splits;
-  int64_t nblk, sbps, groups;
-};
-
-DivLayout div_layout(int H, int n, int half, bool f32) {
-  DivLayout L;
-  const int HC = 2 * H;
-  L.pd = pack_dims(half, f32);
-  L.nblk = cdiv(n, 32);
-  const int64_t kgroups = (int64_t)HC * cdiv(n, kRowsPerGroup);
-  int64_t sp = cdiv(512, kgroups);
-  if (sp > L.nblk) sp = L.nblk;
-  if (sp < 1) sp = 1;
-  L.sbps = cdiv(L.nblk, sp);
-  L.splits = (int)cdiv(L.nblk, L.sbps);
-  L.groups = kgroups * L.splits;
-  size_t o = 0;
-  L.kt = o;
-  o += al256((size_t)HC * L.nblk * L.pd.ND * L.pd.TVPD * kWave * 16);
-  L.part = o;
-  o += al256((size_t)L.splits * HC * n * half * 4);
-  L.lpart = o;
-  o += al256((size_t)L.groups * 4);
-  L.total = o;
-  return L;
-}
 
 }  // namespace
 }  // namespace mpl

@@ -289,7 +289,7 @@ class MemoryPool:
     def forward_backward(self, variables: Dict[str, Any], queries: torch.Tensor, g_out: torch.Tensor,
                          g_balance: Optional[torch.Tensor] = None, *, train: bool = True,
                          noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
-                         rngs: Optional[Dict[str, Any]] = None):
+                         rngs: Optional[Dict[str, Any]] = None, g_diversity: Optional[torch.Tensor] = None):
         """The forward of memory.py:119-227 and its backward for a given
         upstream gradient, without torch autograd: returns
         (out, aux, (d queries, d sub_keys, d log_temperature)).  The values
@@ -298,7 +298,14 @@ class MemoryPool:
         the gradient of aux["balance_loss"] (None: no balance term).  Only
         library kernels and tensor allocations, and no host read, so a whole
         training step built on it can be captured in one HIP graph; the
-        results equal apply() followed by torch.autograd.grad bit for bit."""
+        results equal apply() followed by torch.autograd.grad bit for bit.
+        ``g_diversity`` (a device scalar: the coefficient of
+        key_diversity_loss in the training loss, memory.py:230-240) adds that
+        term's gradient to d sub_keys and puts the loss in
+        aux["key_diversity_loss"]; where the fused dense pass applies, its
+        Gram tiles reuse this call's key packs and both sub-key terms share
+        one normalisation backward (within fp32 rounding of the sum of the
+        separate gradients)."""
         params = variables["params"] if "params" in variables else variables
         res = self.lookup(params, queries, train=train, noise_scale=noise_scale, shuffle_reads=shuffle_reads,
                           rngs=rngs)
@@ -310,8 +317,11 @@ class MemoryPool:
         sub_keys = params["sub_keys"]
         shapes = (tuple(queries.shape), queries.dtype, sub_keys.dtype, params["log_temperature"].dtype)
         values = params["values"] if "values" in params else sub_keys.new_empty(0)
+        extra = {}
         dq, dk, dlt, _ = _lookup_backward(self, res, internal, sub_keys.detach(), values.detach(), shapes, g_out,
-                                          g_balance, bool(shuffle_reads), False)
+                                          g_balance, bool(shuffle_reads), False, g_diversity, extra)
+        if "key_diversity_loss" in extra:
+            dict.__setitem__(aux, "key_diversity_loss", extra["key_diversity_loss"])
         out = res["out"].reshape(*tuple(queries.shape[:-2]), self.d_value)
         return out, aux, (dq, dk, dlt)
 
@@ -626,7 +636,7 @@ class _LookupFunction(torch.autograd.Function):
 
 
 def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_balance, shuffle_reads: bool,
-                     need_dv: bool):
+                     need_dv: bool, g_diversity: Optional[torch.Tensor] = None, extra: Optional[Dict] = None):
     """The backward of memory.py:136-213 on the GPU for one forward result
     ``res`` of MemoryPool.lookup: (d queries, d sub_keys, d log_temperature,
     d values or None).  ``g_balance`` is the gradient of the balance loss
@@ -673,7 +683,7 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
     dense = M > 0 and (code == MPL_F16 or bal)
     # the routed query gradient inside the balance pass (one launch fewer)
     fused_q = (FUSED_QUERY_BWD and dense and bal and not btg and not pool.query_scale and k <= 16
-               and (half % 4 or q.data_ptr() % 16 == 0))
+               and half % 4 == 0 and half <= 128 and q.data_ptr() % 16 == 0)
     dq = torch.empty((M, H, 2, half), dtype=torch.float32, device=dev)
     if fused_q:
         dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
@@ -684,12 +694,22 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
         # (normalised in the pack): no fp32 q_hat pass
         raw_pack = RAW_QUERY_PACK and code == MPL_F16 and half in (64, 128)
         q_hat = None if raw_pack else res["q_hat"]
+        gd = dws = div_loss = None
+        dwsb = 0
+        if g_diversity is not None and n > 1:  # the diversity Gram pass on this call's key packs
+            gd = g_diversity.reshape(1).float().contiguous()
+            dwsb = L.mpl_key_diversity_workspace_bytes(H, n, half, code)
+            dws = torch.empty(max(dwsb, 256), dtype=torch.uint8, device=dev)
+            div_loss = torch.empty(1, dtype=torch.float32, device=dev)
         check(L.mpl_lookup_bwd_dense_queries(ptr(q_hat), ptr(q), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
                                              ptr(d_sub), ptr(internal["_counts"]), ptr(internal["_state"]), ptr(gb),
                                              M, H, n, half, k, code, ptr(T), ptr(ws), wsb, NORM_EPS, ptr(dq),
-                                             ptr(dk_hat), stream), "mpl_lookup_bwd_dense_queries")
-        check(L.mpl_l2_normalize_bwd(ptr(raw_keys), ptr(dk_hat), H * 2 * n, half, NORM_EPS, None, ptr(dk),
-                                     stream), "mpl_l2_normalize_bwd")
+                                             ptr(raw_keys), ptr(gd), ptr(dws), dwsb, ptr(div_loss), ptr(dk),
+                                             stream), "mpl_lookup_bwd_dense_queries")
+        if div_loss is not None:
+            g_diversity = None  # taken in the fused pass
+            if extra is not None:
+                extra["key_diversity_loss"] = div_loss.reshape(())
     elif dense:
         q_hat = res["q_hat"]
         dk_hat = torch.empty((H, 2, n, half), dtype=torch.float32, device=dev)
@@ -723,6 +743,11 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
         check(L.mpl_lookup_bwd_keys(ptr(raw_keys), ptr(res["q_hat"]), ptr(q_len), ptr(res["sub_idx"]), ptr(d_sub),
                                     None, M, H, n, half, k, ptr(T), ptr(ws), wsb, ptr(dk), stream),
               "mpl_lookup_bwd_keys")
+    if g_diversity is not None:  # the key diversity term on its own (memory.py:230-240)
+        dloss, ddk = key_diversity_value_and_grad(sub_keys, g_diversity, pool.score_dtype)
+        dk = dk + ddk
+        if extra is not None:
+            extra["key_diversity_loss"] = dloss
     # log_temperature: straight-through clamp, dT/dlog_t = T (memory.py:143-146)
     dlt = torch.empty(1, dtype=torch.float32, device=dev)
     check(L.mpl_sum(ptr(dlogt_part), M, ptr(dlogt_extra), ptr(dlt), stream), "mpl_sum")

@@ -148,3 +148,35 @@ def test_raw_query_pack_equals_q_hat_pack(gpu_lib, monkeypatch, d_key):
     torch.cuda.synchronize()
     for a, b in zip(out[True], out[False]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("values_dtype,query_scale", [(torch.float16, False), (torch.float32, False),
+                                                      (torch.float16, True)])
+def test_forward_backward_with_key_diversity(gpu_lib, values_dtype, query_scale):
+    """forward_backward(g_diversity=c) against forward_backward() plus
+    key_diversity_value_and_grad(c) added: d sub_keys within 1e-5 of max
+    |d sub_keys| (the fused pass sums the two terms before one
+    normalisation backward), the loss bit for bit, d queries and
+    d log-temperature unchanged."""
+    from model_amd.memory import key_diversity_value_and_grad
+    k, M = 16, 2048
+    n = 512 if values_dtype == torch.float16 else 128
+    pool = MemoryPool(n, H, D_KEY, 64, k, routing_noise=1.0, values_dtype=values_dtype, query_scale=query_scale)
+    params = make_params(pool, 95, key_std=(D_KEY // 2) ** -0.5, value_std=0.02)
+    g = torch.Generator(device="cuda").manual_seed(96)
+    q = torch.randn((M, H, D_KEY), generator=g, device="cuda")
+    g_out = torch.randn((M, 64), generator=g, device="cuda") * 1e-3
+    g_bal = torch.full((), 0.01, device="cuda")
+    g_div = torch.full((), 0.05, device="cuda")
+    print(f"forward_backward + key diversity {values_dtype} query_scale={query_scale}", flush=True)
+    _, aux, (dqa, dka, dla) = pool.forward_backward(params, q, g_out, g_bal, train=True, rngs={"routing": 3},
+                                                    g_diversity=g_div)
+    _, _, (dqb, dkb, dlb) = pool.forward_backward(params, q, g_out, g_bal, train=True, rngs={"routing": 3})
+    loss, ddk = key_diversity_value_and_grad(params["params"]["sub_keys"] if "params" in params
+                                             else params["sub_keys"], g_div, pool.score_dtype)
+    torch.cuda.synchronize()
+    ref = dkb + ddk
+    err = float((dka - ref).abs().max()) / float(ref.abs().max())
+    assert err <= 1e-5, f"d sub_keys: {err:.3g}"
+    assert torch.equal(aux["key_diversity_loss"].reshape(()), loss.reshape(()))
+    assert torch.equal(dqa, dqb) and torch.equal(dla, dlb)
