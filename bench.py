@@ -548,8 +548,8 @@ def train_step_bench(torch, iters):
             out, aux, (dq, gk, dlt) = pool.forward_backward({"params": params}, q, g_out, g_bal, train=True,
                                                             g_diversity=g_div)
             gw = hidden.t() @ dq.reshape(M, H * d_key)
-            rest = R.sum_squares([gw, gk, dlt])  # no memset node in the captured step
-            upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], rest_sq=rest,
+            # the dense gradients' norm in the clip's own pass (no memset node)
+            upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], dense_grads=[gw, gk, dlt],
                 count_slots=True)
 
     ms_graph = time_loop(torch, step_graph, iters, 3)

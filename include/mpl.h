@@ -319,6 +319,19 @@ int mpl_clip_scale(const float* row_sq, int64_t cap, const float* rest_sq, float
                    float* scale_gnorm, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * mpl_clip_scale with the dense gradients' squared norm taken in the same
+ * pass (train.py:395-397: optax.global_norm over every gradient): the sum
+ * of row_sq [cap] plus the squares of the count (< 8) dense buffers x[j]
+ * of n[j] fp32 each, in fp64 in a fixed order, then scale_gnorm as
+ * mpl_clip_scale writes it.  Workspace as mpl_clip_scale.  It replaces
+ * mpl_sum_squares + mpl_clip_scale (two launches fewer).  No counterpart in
+ * the reference's interface.
+ */
+int mpl_clip_scale_dense(const float* row_sq, int64_t cap, const float* const* x, const int64_t* n, int count,
+                         float grad_clip, float* scale_gnorm, void* workspace, size_t workspace_bytes,
+                         void* stream);
+
+/*
  * train.py:395-397 (the dense part of optax.global_norm's square):
  * out[0] = (add ? add[0] : 0) + sum over the count <= 8 fp32 buffers
  * x[j] [n[j]] of x^2.  x and n are host arrays of device pointers and sizes.
@@ -397,6 +410,13 @@ int mpl_lookup_bwd_keys(const float* sub_keys, const float* q_hat, const float* 
                         const int32_t* sub_idx, const float* d_sub, const float* dk_hat_extra,
                         int64_t M, int H, int n, int half, int k, const float* temperature,
                         void* workspace, size_t workspace_bytes, float* d_sub_keys, void* stream);
+
+/*
+ * memory.py:143-146: t[0] = exp(clip(log_t[0], log_min, log_max)) as a
+ * device scalar (a NaN log_t gives NaN), the clamped temperature of the
+ * lookup, in one launch and no host read.
+ */
+int mpl_temperature(const float* log_t, float log_min, float log_max, float* t, void* stream);
 
 /*
  * Backward of mpl_l2_normalize's y = x * rsqrt(sum(x*x) + eps) over rows of

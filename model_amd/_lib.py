@@ -56,6 +56,7 @@ SIGNATURES = {
     "mpl_merge_rows_counts": (_I, [_P, _P, _I64, _I, _P, _I, _I64, _P, _SZ, _P, _P, _P, _P, _I, _P, _P]),
     "mpl_clip_scale_workspace_bytes": (_SZ, []),
     "mpl_clip_scale": (_I, [_P, _I64, _P, _F, _P, _P, _SZ, _P]),
+    "mpl_clip_scale_dense": (_I, [_P, _I64, _P, _P, _I, _F, _P, _P, _SZ, _P]),
     "mpl_sum_squares_workspace_bytes": (_SZ, []),
     "mpl_sum_squares": (_I, [_P, _P, _I, _P, _P, _P, _SZ, _P]),
     "mpl_row_adagrad": (_I, [_P, _I, _P, _P, _P, _P, _I64, _I, _I64, _F, _P, _P]),
@@ -65,6 +66,7 @@ SIGNATURES = {
     "mpl_lookup_bwd_keys_workspace_bytes": (_SZ, [_I64, _I, _I, _I, _I]),
     "mpl_lookup_bwd_keys": (_I, [_P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _P, _P, _SZ, _P, _P]),
     "mpl_sum": (_I, [_P, _I64, _P, _P, _P]),
+    "mpl_temperature": (_I, [_P, _F, _F, _P, _P]),
     "mpl_l2_normalize_bwd": (_I, [_P, _P, _I64, _I, _F, _P, _P, _P]),
     "mpl_key_diversity_workspace_bytes": (_SZ, [_I, _I, _I, _I]),
     "mpl_key_diversity": (_I, [_P, _P, _I, _I, _I, _I, _P, _SZ, _P, _P, _P]),

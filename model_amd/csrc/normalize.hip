@@ -140,6 +140,13 @@ __global__ __launch_bounds__(256) void norm_pack_kernel(const float* __restrict_
 }
 
 
+// memory.py:143-146: T = exp(clip(log_t, ln min, ln max)), one thread (a
+// NaN log_t stays NaN, as jnp.clip passes it).
+__global__ void temperature_kernel(const float* __restrict__ log_t, float lo, float hi, float* __restrict__ t) {
+  const float x = *log_t;
+  t[0] = expf(x != x ? x : fminf(fmaxf(x, lo), hi));
+}
+
 }  // namespace mpl
 
 using namespace mpl;
@@ -153,6 +160,14 @@ extern "C" int mpl_l2_normalize(const float* x, int64_t rows, int dim, float eps
   l2norm_kernel<<<(unsigned)cdiv(rows, 16), 256, 0, (hipStream_t)stream>>>(x, rows, dim, eps, y,
                                                                              (_Float16*)y16, row_len);
   return check_launch("mpl_l2_normalize");
+}
+
+extern "C" int mpl_temperature(const float* log_t, float log_min, float log_max, float* t, void* stream) {
+  clear_error();
+  MPL_REQUIRE(log_t != nullptr && t != nullptr, MPL_EINVAL, "mpl_temperature: null buffer");
+  MPL_REQUIRE(log_min <= log_max, MPL_EINVAL, "mpl_temperature: log_min > log_max");
+  temperature_kernel<<<1, 64, 0, (hipStream_t)stream>>>(log_t, log_min, log_max, t);
+  return check_launch("mpl_temperature");
 }
 
 extern "C" int mpl_l2_normalize_bwd(const float* x, const float* dy, int64_t rows, int dim, float eps,

@@ -682,6 +682,7 @@ struct SqBufs {
   const float* x[kSqMaxBufs];
   int64_t end[kSqMaxBufs];  // exclusive prefix ends of the buffers in the joined array
   int count;
+  unsigned plain;  // bit j: buffer j holds squares already (summed as they are)
 };
 
 __global__ __launch_bounds__(256) void sum_sq_chunks_kernel(SqBufs bufs, double* __restrict__ chunk_sums) {
@@ -696,9 +697,13 @@ __global__ __launch_bounds__(256) void sum_sq_chunks_kernel(SqBufs bufs, double*
     const int64_t lo = b0 > start ? b0 : start;
     const int64_t hi = b1 < bufs.end[j] ? b1 : bufs.end[j];
     const float* __restrict__ x = bufs.x[j];
-    for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
-      const double v = (double)x[i - start];
-      s += v * v;
+    if ((bufs.plain >> j) & 1u) {
+      for (int64_t i = lo + threadIdx.x; i < hi; i += 256) s += (double)x[i - start];
+    } else {
+      for (int64_t i = lo + threadIdx.x; i < hi; i += 256) {
+        const double v = (double)x[i - start];
+        s += v * v;
+      }
     }
     start = bufs.end[j];
   }
@@ -1164,6 +1169,47 @@ extern "C" int mpl_clip_scale(const float* row_sq, int64_t cap, const float* res
   sum_chunks_kernel<<<kSumBlocks, 256, 0, s>>>(row_sq, cap, (double*)workspace);
   clip_finish_kernel<<<1, 256, 0, s>>>((const double*)workspace, rest_sq, grad_clip, scale_gnorm);
   return check_launch("mpl_clip_scale");
+}
+
+extern "C" int mpl_clip_scale_dense(const float* row_sq, int64_t cap, const float* const* x, const int64_t* n,
+                                    int count, float grad_clip, float* scale_gnorm, void* workspace,
+                                    size_t workspace_bytes, void* stream) {
+  clear_error();
+  MPL_REQUIRE(cap >= 0 && scale_gnorm != nullptr && (cap == 0 || row_sq != nullptr), MPL_EINVAL,
+              "mpl_clip_scale_dense: bad arguments");
+  MPL_REQUIRE(count >= 0 && count < kSqMaxBufs && (count == 0 || (x && n)), MPL_EINVAL,
+              "mpl_clip_scale_dense: bad dense buffers (count %d, at most %d)", count, kSqMaxBufs - 1);
+  MPL_REQUIRE(workspace != nullptr && workspace_bytes >= kSumBlocks * sizeof(double), MPL_EWORKSPACE,
+              "mpl_clip_scale_dense: workspace of %zu bytes needed", (size_t)kSumBlocks * sizeof(double));
+  SqBufs b{};
+  int64_t total = 0;
+  int used = 0;
+  if (cap > 0) {
+    total = cap;
+    b.x[0] = row_sq;
+    b.end[0] = total;
+    b.plain = 1u;
+    used = 1;
+  }
+  for (int j = 0; j < count; ++j) {
+    MPL_REQUIRE(n[j] >= 0 && (n[j] == 0 || x[j] != nullptr), MPL_EINVAL,
+                "mpl_clip_scale_dense: buffer %d: bad size or null", j);
+    if (n[j] == 0) continue;
+    total += n[j];
+    b.x[used] = x[j];
+    b.end[used] = total;
+    ++used;
+  }
+  if (used == 0) {
+    b.x[0] = nullptr;
+    b.end[0] = 0;
+    used = 1;
+  }
+  b.count = used;
+  hipStream_t s = (hipStream_t)stream;
+  sum_sq_chunks_kernel<<<kSumBlocks, 256, 0, s>>>(b, (double*)workspace);
+  clip_finish_kernel<<<1, 256, 0, s>>>((const double*)workspace, nullptr, grad_clip, scale_gnorm);
+  return check_launch("mpl_clip_scale_dense");
 }
 
 extern "C" size_t mpl_sum_squares_workspace_bytes() { return kSumBlocks * sizeof(double); }

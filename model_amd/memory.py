@@ -262,8 +262,10 @@ class MemoryPool:
         key = (log_temperature.data_ptr(), log_temperature._version)
         if ((_capturing() and not self._keys.frozen) or key != self._temp_key
                 or log_temperature is not self._temp_src):
-            lt = log_temperature.detach().reshape(1).to(torch.float32)
-            t = torch.exp(lt.clamp(math.log(self.min_temperature), math.log(self.max_temperature)))
+            lt = log_temperature.detach().reshape(1).to(torch.float32).contiguous()
+            t = torch.empty(1, dtype=torch.float32, device=lt.device)
+            check(_lib.lib().mpl_temperature(ptr(lt), math.log(self.min_temperature), math.log(self.max_temperature),
+                                             ptr(t), _lib.stream_ptr(lt.device)), "mpl_temperature")
             if _capturing() and not self._keys.frozen:
                 return t
             self._temp_tensor, self._temp_key, self._temp_src = t, key, log_temperature

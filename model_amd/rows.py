@@ -129,10 +129,29 @@ def fetched_row_grads(aux: Dict, probe_grads, layers: Sequence[int], pool_size: 
     return m.uniq, m.rows
 
 
-def clip_scale(row_sq: torch.Tensor, rest_sq: Optional[torch.Tensor], grad_clip: float) -> torch.Tensor:
-    """train.py:395-397: device tensor [scale, gnorm]."""
+def clip_scale(row_sq: torch.Tensor, rest_sq: Optional[torch.Tensor], grad_clip: float,
+               dense: Optional[Sequence[torch.Tensor]] = None) -> torch.Tensor:
+    """train.py:395-397: device tensor [scale, gnorm].  ``dense`` (at most
+    7 tensors, instead of rest_sq) adds the squares of the dense gradients
+    in the same pass (mpl_clip_scale_dense)."""
     dev = row_sq.device
     out = torch.empty(2, dtype=torch.float32, device=dev)
+    if dense is not None:
+        if rest_sq is not None:
+            raise ValueError("give the dense gradients either as rest_sq or as dense, not both")
+        if len(dense) > 7:
+            raise ValueError("clip_scale takes at most 7 dense gradient tensors")
+        xs = [t.detach().reshape(-1).float().contiguous() for t in dense]
+        L = _lib.lib()
+        wsb = L.mpl_clip_scale_workspace_bytes()
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        ptrs = (C.c_void_p * max(len(xs), 1))(*[x.data_ptr() for x in xs])
+        ns = (C.c_int64 * max(len(xs), 1))(*[x.numel() for x in xs])
+        rs = row_sq.contiguous()
+        check(L.mpl_clip_scale_dense(ptr(rs), rs.shape[0], C.cast(ptrs, C.c_void_p), C.cast(ns, C.c_void_p),
+                                     len(xs), float(grad_clip), ptr(out), ptr(ws), wsb, _lib.stream_ptr(dev)),
+              "mpl_clip_scale_dense")
+        return out
     if rest_sq is not None:
         rest_sq = rest_sq.reshape(1).float().contiguous()
     L = _lib.lib()
@@ -290,19 +309,22 @@ class SparseRowUpdate:
         return {"step": self.step, "pool_m": pm, "pool_v": pv, "values": table}
 
     def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
-                 rest_sq: Optional[torch.Tensor] = None, count_slots: bool = False) -> Dict[str, torch.Tensor]:
+                 rest_sq: Optional[torch.Tensor] = None, count_slots: bool = False,
+                 dense_grads: Optional[Sequence[torch.Tensor]] = None) -> Dict[str, torch.Tensor]:
         """One update from the fetches of ``layers`` (aux["slots"][i],
         aux["weights"][i], probe_grads[layer]).  With count_slots the result
         also holds "slot_counts" [N] fp32, the fetches of every slot summed
         over the layers (the aux slot_counts of memory.py:215 / model.py:136
         that train.py:456 folds into the usage average), from the merge's
-        own sort instead of a separate histogram."""
+        own sort instead of a separate histogram.  The global norm takes the
+        dense gradients as rest_sq (their squared norm, a device scalar) or
+        as dense_grads (the tensors, summed in the clip's own pass)."""
         N = self.host.n_slots if self.host is not None else self.values.shape[0]
         dev = self.values.device if self.values is not None else aux["slots"][0].device
         counts = torch.empty(N, dtype=torch.float32, device=dev) if count_slots else None
         merged = fetched_row_grads_full(aux, probe_grads, layers, N, zero_padding=False,  # optimizers skip padding
                                         slot_counts=counts)
-        sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip)
+        sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip, dense_grads)
         lr = warmup_cosine(self.step, self.lr, self.warmup_steps, self.steps) * self.pool_lr_mult
         scale = sg[0:1]
         if self.host is not None:

@@ -350,3 +350,39 @@ def test_sparse_row_update_counts_slots(gpu_lib):
     ref = sum(np.bincount(s.cpu().numpy().reshape(-1), minlength=N) for s in aux["slots"])
     np.testing.assert_array_equal(oa["slot_counts"].cpu().numpy(), ref.astype(np.float32))
     assert torch.equal(va, vb) and torch.equal(ua.acc, ub.acc)
+
+
+def test_clip_scale_dense_equals_two_pass(gpu_lib):
+    """mpl_clip_scale_dense (the dense gradients' squares in the clip's own
+    fp64 pass) against mpl_sum_squares + mpl_clip_scale and an fp64 numpy
+    norm: gnorm within 1e-6 relative, scale likewise; empty inputs give
+    gnorm 0 and scale 1."""
+    rng = np.random.default_rng(31)
+    row_sq = torch.as_tensor(rng.random(5000).astype(np.float32) * 1e-3, device="cuda")
+    dense = [torch.as_tensor(rng.standard_normal(s).astype(np.float32) * 1e-2, device="cuda")
+             for s in ((256, 1024), (4, 2, 512, 128), (1,))]
+    a = R.clip_scale(row_sq, None, 1.0, dense)
+    b = R.clip_scale(row_sq, R.sum_squares(dense), 1.0)
+    torch.cuda.synchronize()
+    ref = np.sqrt(float(row_sq.double().sum()) + sum(float((t.double() ** 2).sum()) for t in dense))
+    np.testing.assert_allclose(float(a[1]), ref, rtol=1e-6)
+    np.testing.assert_allclose(a.cpu().numpy(), b.cpu().numpy(), rtol=1e-6)
+    z = R.clip_scale(torch.zeros(0, device="cuda"), None, 1.0, [])
+    assert float(z[1]) == 0.0 and float(z[0]) == 1.0
+
+
+def test_sparse_row_update_dense_grads_equals_rest_sq(gpu_lib):
+    """SparseRowUpdate(dense_grads=...) clips like rest_sq=sum_squares(...)."""
+    rng = np.random.default_rng(32)
+    B, T, H, k, N, d = 2, 64, 4, 8, 2048, 32
+    aux = {"slots": [torch.as_tensor(rng.integers(0, N, (B, T, H, k)).astype(np.int32), device="cuda")],
+           "weights": [torch.as_tensor(rng.random((B, T, H, k)).astype(np.float32), device="cuda")]}
+    probes = {0: torch.as_tensor(rng.standard_normal((B, T, d)).astype(np.float32), device="cuda")}
+    dense = [torch.as_tensor(rng.standard_normal((64, 64)).astype(np.float32), device="cuda")]
+    v0 = torch.as_tensor((rng.standard_normal((N, d)) * 0.02).astype(np.float32), device="cuda")
+    va, vb = v0.clone(), v0.clone()
+    oa = R.SparseRowUpdate(va, lr=1e-2, grad_clip=1.0)(aux, probes, [0], dense_grads=dense)
+    ob = R.SparseRowUpdate(vb, lr=1e-2, grad_clip=1.0)(aux, probes, [0], rest_sq=R.sum_squares(dense))
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(float(oa["grad_norm"]), float(ob["grad_norm"]), rtol=1e-6)
+    torch.testing.assert_close(va, vb, rtol=1e-5, atol=1e-7)

@@ -146,3 +146,22 @@ def test_temperature_floor_and_balance_gradient(gpu_lib):
     assert g_bal != 0.0
     g_bal, g_read, _ = _temp_grads({"balance_temperature_grad": False}, math.log(10.0))
     assert g_bal == 0.0 and g_read != 0.0
+
+
+def test_temperature_kernel_matches_torch_clamp_exp(gpu_lib):
+    """mpl_temperature: exp(clip(log_t, ln min, ln max)) bit for bit against
+    torch's clamp + exp, inside, below and above the range; NaN stays NaN."""
+    import math
+    from model_amd import _lib
+    from model_amd._lib import check, ptr
+    lo, hi = math.log(10.0), math.log(100.0)
+    for v in (math.log(20.0), math.log(2.0), math.log(500.0), lo, hi, -30.0, 30.0, float("nan")):
+        lt = torch.tensor([v], dtype=torch.float32, device="cuda")
+        t = torch.empty(1, device="cuda")
+        check(_lib.lib().mpl_temperature(ptr(lt), lo, hi, ptr(t), _lib.stream_ptr(lt.device)), "mpl_temperature")
+        ref = torch.exp(lt.clamp(lo, hi))
+        torch.cuda.synchronize()
+        if math.isnan(v):
+            assert torch.isnan(t).all()
+        else:
+            assert torch.equal(t, ref), (v, float(t), float(ref))
