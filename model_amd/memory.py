@@ -202,6 +202,7 @@ class MemoryPool:
         self._temp_src = None
         self._temp_tensor = None
         self._constants = {}
+        self._side = None  # the second stream of early_clean
 
     def _constant(self, value: float, dev) -> torch.Tensor:
         """A device fp32 scalar [1] holding ``value``, made once per (value,
@@ -291,7 +292,8 @@ class MemoryPool:
     def forward_backward(self, variables: Dict[str, Any], queries: torch.Tensor, g_out: torch.Tensor,
                          g_balance: Optional[torch.Tensor] = None, *, train: bool = True,
                          noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
-                         rngs: Optional[Dict[str, Any]] = None, g_diversity: Optional[torch.Tensor] = None):
+                         rngs: Optional[Dict[str, Any]] = None, g_diversity: Optional[torch.Tensor] = None,
+                         on_forward=None):
         """The forward of memory.py:119-227 and its backward for a given
         upstream gradient, without torch autograd: returns
         (out, aux, (d queries, d sub_keys, d log_temperature)).  The values
@@ -307,11 +309,17 @@ class MemoryPool:
         aux["key_diversity_loss"]; where the fused dense pass applies, its
         Gram tiles reuse this call's key packs and both sub-key terms share
         one normalisation backward (within fp32 rounding of the sum of the
-        separate gradients)."""
+        separate gradients).  ``on_forward(aux)``, when given, is called once
+        the selection and the value read are enqueued (before the balance
+        statistics and the backward), so a caller can start work that needs
+        only aux["slots"] and aux["weights"] (the sparse row merge,
+        SparseRowUpdate.merge) on another stream beside the rest."""
         params = variables["params"] if "params" in variables else variables
         res = self.lookup(params, queries, train=train, noise_scale=noise_scale, shuffle_reads=shuffle_reads,
-                          rngs=rngs)
+                          rngs=rngs, early_clean=g_balance is not None)
         aux = res["aux"]
+        if on_forward is not None:  # the selection and the read are enqueued
+            on_forward(aux)
         internal = {}
         if g_balance is not None:
             aux["balance_loss"]  # computes f and p (memory.py:196-213)
@@ -329,9 +337,14 @@ class MemoryPool:
 
     def lookup(self, params, queries: torch.Tensor, *, train: bool = False,
                noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
-               rngs: Optional[Dict[str, Any]] = None, gumbel: Optional[torch.Tensor] = None) -> Dict[str, Any]:
+               rngs: Optional[Dict[str, Any]] = None, gumbel: Optional[torch.Tensor] = None,
+               early_clean: bool = False) -> Dict[str, Any]:
         """Forward lookup; returns out, aux and the tensors a backward needs.
-        ``gumbel`` [M, H, 2, n] may be given explicitly (parity tests)."""
+        ``gumbel`` [M, H, 2, n] may be given explicitly (parity tests).
+        ``early_clean`` (a training step that will read the balance loss):
+        with routing noise, the clean stage-1 selection behind the balance
+        statistics (memory.py:207) starts at once on a second stream, beside
+        the noise draw and the noisy selection."""
         H, n, k, d = self.heads, self.n_sub_keys, self.top_k, self.d_value
         half = self.d_key // 2
         lead = tuple(queries.shape[:-2])
@@ -351,6 +364,9 @@ class MemoryPool:
         q_len = torch.empty((M, H, 2), dtype=torch.float32, device=dev) if self.query_scale else None
         k_hat, packed = self._keys.get(params["sub_keys"], score_code)
         T = self.temperature(params["log_temperature"])
+        early = None
+        if early_clean and train and self.routing_noise > 0 and gumbel is None and M > 0:
+            early = self._clean_early(q, packed, score_code, T, M)
 
         noise_coef = None  # device scalar routing_noise * noise_scale (memory.py:157)
         if gumbel is None and train and self.routing_noise > 0:
@@ -409,7 +425,7 @@ class MemoryPool:
 
         def stats():
             return self._routing_stats(params, res, k_hat, T, q_len, sub_idx, slots, weights,
-                                       noisy, packed, score_code, M)
+                                       noisy, packed, score_code, M, early)
 
         aux = LazyAux({
             "slots": slots.reshape(*lead, H, k),
@@ -427,7 +443,7 @@ class MemoryPool:
 
     # ------------------------------------------------------------- stats
     def _routing_stats(self, params, res, k_hat, T, q_len, sub_idx, slots, weights, noisy,
-                       packed, score_code, M):
+                       packed, score_code, M, early=None):
         """memory.py:196-215 from the selected ids: the counts on the GPU
         (mpl_route_counts) and the balance loss fused over the MFMA score
         tiles of the scoring precision (mpl_balance_fwd)."""
@@ -436,7 +452,12 @@ class MemoryPool:
         dev = sub_idx.device
         L = _lib.lib()
         stream = _lib.stream_ptr(dev)
-        if noisy:  # memory.py:207: an extra clean selection
+        if noisy and early is not None:  # started on the side stream by lookup()
+            cur = torch.cuda.current_stream(dev)
+            cur.wait_stream(early[1])
+            clean = early[0]
+            clean.record_stream(cur)
+        elif noisy:  # memory.py:207: an extra clean selection
             clean = self._clean_sub_idx(res["q"], packed, score_code, T, M)
         else:
             clean = sub_idx
@@ -461,6 +482,22 @@ class MemoryPool:
         check(_lib.lib().mpl_route_counts(ptr(slots), None, M, H, n, k, None, None, ptr(out), _lib.stream_ptr(dev)),
               "mpl_route_counts(slots)")
         return out
+
+    def _clean_early(self, q, packed, score_code, T, M):
+        """The clean stage-1 lists on the pool's side stream (default
+        priority), after everything the current stream has enqueued: returns
+        (sub_idx, stream); the reader waits for that stream first."""
+        dev = q.device
+        if self._side is None or self._side.device != dev:
+            self._side = torch.cuda.Stream(device=dev)
+        side = self._side
+        cur = torch.cuda.current_stream(dev)
+        side.wait_stream(cur)
+        for t in (q, packed, T):
+            t.record_stream(side)
+        with torch.cuda.stream(side):
+            clean = self._clean_sub_idx(q, packed, score_code, T, M)
+        return clean, side
 
     def _clean_sub_idx(self, q, packed, score_code, T, M):
         """memory.py:207: the stage-1 top-k of the clean scores (no stage 2)."""

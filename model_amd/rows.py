@@ -308,22 +308,38 @@ class SparseRowUpdate:
         table = self.master if self.master is not None else self.values.float()
         return {"step": self.step, "pool_m": pm, "pool_v": pv, "values": table}
 
-    def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
-                 rest_sq: Optional[torch.Tensor] = None, count_slots: bool = False,
-                 dense_grads: Optional[Sequence[torch.Tensor]] = None) -> Dict[str, torch.Tensor]:
-        """One update from the fetches of ``layers`` (aux["slots"][i],
-        aux["weights"][i], probe_grads[layer]).  With count_slots the result
-        also holds "slot_counts" [N] fp32, the fetches of every slot summed
-        over the layers (the aux slot_counts of memory.py:215 / model.py:136
-        that train.py:456 folds into the usage average), from the merge's
-        own sort instead of a separate histogram.  The global norm takes the
-        dense gradients as rest_sq (their squared norm, a device scalar) or
-        as dense_grads (the tensors, summed in the clip's own pass)."""
+    def merge(self, aux: Dict, probe_grads, layers: Sequence[int], count_slots: bool = False) -> Dict:
+        """The first half of an update (train.py:146-172): the fetched rows'
+        gradients merged per slot, on the current stream, as a handle for
+        apply().  It depends only on the forward's slots and weights and the
+        probe gradients, so a training step may run it on a second stream
+        beside the dense backward (the handle's tensors are marked for the
+        stream apply() runs on).  With count_slots the handle also carries
+        the per-slot fetch counts (memory.py:215)."""
         N = self.host.n_slots if self.host is not None else self.values.shape[0]
         dev = self.values.device if self.values is not None else aux["slots"][0].device
+        stream = torch.cuda.current_stream(dev)
+        for layer, sl, w in zip(layers, aux["slots"], aux["weights"]):
+            for t in (sl, w, probe_grads[layer]):  # read here, perhaps made on another stream
+                if t.is_cuda:
+                    t.record_stream(stream)
         counts = torch.empty(N, dtype=torch.float32, device=dev) if count_slots else None
         merged = fetched_row_grads_full(aux, probe_grads, layers, N, zero_padding=False,  # optimizers skip padding
                                         slot_counts=counts)
+        return {"merged": merged, "slot_counts": counts}
+
+    def apply(self, handle: Dict, rest_sq: Optional[torch.Tensor] = None,
+              dense_grads: Optional[Sequence[torch.Tensor]] = None) -> Dict[str, torch.Tensor]:
+        """The second half (train.py:395-429): the global-norm clip over the
+        merged rows and the dense gradients (rest_sq, their squared norm as
+        a device scalar, or dense_grads, the tensors, summed in the clip's
+        own pass), then the row optimizer step.  Call it on a stream that
+        has waited for the merge's."""
+        merged, counts = handle["merged"], handle["slot_counts"]
+        stream = torch.cuda.current_stream(merged.rows.device)
+        for t in (merged.uniq, merged.rows, merged.row_sq, merged.num_unique, counts):
+            if t is not None:
+                t.record_stream(stream)
         sg = clip_scale(merged.row_sq, rest_sq, self.grad_clip, dense_grads)
         lr = warmup_cosine(self.step, self.lr, self.warmup_steps, self.steps) * self.pool_lr_mult
         scale = sg[0:1]
@@ -339,3 +355,17 @@ class SparseRowUpdate:
         if counts is not None:
             out["slot_counts"] = counts
         return out
+
+    def __call__(self, aux: Dict, probe_grads, layers: Sequence[int],
+                 rest_sq: Optional[torch.Tensor] = None, count_slots: bool = False,
+                 dense_grads: Optional[Sequence[torch.Tensor]] = None) -> Dict[str, torch.Tensor]:
+        """One update from the fetches of ``layers`` (aux["slots"][i],
+        aux["weights"][i], probe_grads[layer]): merge() then apply().  With
+        count_slots the result also holds "slot_counts" [N] fp32, the fetches
+        of every slot summed over the layers (the aux slot_counts of
+        memory.py:215 / model.py:136 that train.py:456 folds into the usage
+        average), from the merge's own sort instead of a separate histogram.
+        The global norm takes the dense gradients as rest_sq (their squared
+        norm, a device scalar) or as dense_grads (the tensors, summed in the
+        clip's own pass)."""
+        return self.apply(self.merge(aux, probe_grads, layers, count_slots), rest_sq, dense_grads)

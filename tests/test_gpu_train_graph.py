@@ -187,6 +187,87 @@ def test_training_step_graph_replays_match_eager(gpu_lib):
         print("replay", i, "equal", flush=True)
 
 
+def test_overlapped_training_step_graph_matches_serial_eager(gpu_lib):
+    """The step as the training bench runs it: the sparse row merge started
+    on a second stream from forward_backward's on_forward hook, the clean
+    stage-1 lists on the pool's own second stream, the key diversity term
+    inside the call and the dense gradients in the clip's pass; captured in
+    one graph, every replay equals the same step run eagerly on one stream
+    (SparseRowUpdate's __call__), bit for bit."""
+    pool, keys0, values0, q0, g_out = _setup()
+    g_bal = torch.full((), 0.01, device="cuda")
+    g_div = torch.full((), 0.01, device="cuda")
+    keys = keys0.clone()
+    log_t = torch.tensor(math.log(12.0), device="cuda")
+    values = values0.clone()
+    upd = R.SparseRowUpdate(values, lr=1e-3, pool_lr_mult=3.0, warmup_steps=0, steps=1000, grad_clip=1.0)
+    acc0, master0 = upd.acc.clone(), upd.master.clone()
+    params = {"sub_keys": keys, "values": values, "log_temperature": log_t}
+    merge_stream = torch.cuda.Stream()
+
+    def reset():
+        values.copy_(values0)
+        upd.acc.copy_(acc0)
+        upd.master.copy_(master0)
+        upd.step = 0
+
+    def serial():
+        out, aux, (gq, gk, gt) = pool.forward_backward({"params": params}, q0, g_out, g_bal, train=True,
+                                                       rngs={"routing": 5}, g_diversity=g_div)
+        r = upd({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0], dense_grads=[gk, gt],
+                count_slots=True)
+        return out, gq, gk, gt, r["slot_counts"]
+
+    def overlapped():
+        cur = torch.cuda.current_stream()
+        pending = {}
+
+        def start(aux):
+            merge_stream.wait_stream(cur)
+            with torch.cuda.stream(merge_stream):
+                pending["m"] = upd.merge({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0],
+                                         count_slots=True)
+
+        out, aux, (gq, gk, gt) = pool.forward_backward({"params": params}, q0, g_out, g_bal, train=True,
+                                                       rngs={"routing": 5}, g_diversity=g_div, on_forward=start)
+        cur.wait_stream(merge_stream)
+        r = upd.apply(pending["m"], dense_grads=[gk, gt])
+        return out, gq, gk, gt, r["slot_counts"]
+
+    reset()
+    want = [t.clone() for t in serial()] + [values.clone(), upd.acc.clone(), upd.master.clone()]
+    torch.cuda.synchronize()
+    reset()
+    got_eager = [t.clone() for t in overlapped()] + [values.clone(), upd.acc.clone(), upd.master.clone()]
+    torch.cuda.synchronize()
+    names = ("out", "d_queries", "d_sub_keys", "d_log_temperature", "slot_counts", "values", "acc", "master")
+    for name, a, b in zip(names, got_eager, want):
+        assert torch.equal(a, b), ("eager overlapped", name)
+    print("eager overlapped step equal", flush=True)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            reset()
+            overlapped()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    reset()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs = overlapped()
+    print("captured", flush=True)
+    for i in range(3):
+        reset()
+        graph.replay()
+        torch.cuda.synchronize()
+        got = list(outs) + [values, upd.acc, upd.master]
+        for name, a, b in zip(names, got, want):
+            assert torch.equal(a, b), (i, name)
+        torch.randn(4096, device="cuda").sum().item()  # unrelated eager work between replays
+        print("replay", i, "equal", flush=True)
+
+
 def _graph_node_types(graph):
     """Node types of a captured graph (keep_graph=True), read through the
     HIP runtime's hipGraphGetNodes / hipGraphNodeGetType."""
