@@ -594,6 +594,18 @@ int mpl_rows_linear_pair(const float* x, const float* ln_scale, const float* ln_
                          const float* weight, const float* bias, int activation1, int activation2, int64_t rows,
                          int K, int N1, int N2, float* out1, float* out2, void* stream);
 
+/*
+ * The output layer of a decode step (model.py:125-126): logits [rows, V] =
+ * LayerNorm(x) . emb^T (ln_final, then embed.attend), x [rows, d], emb
+ * [V, d] (16-byte aligned), LayerNorm as in mpl_rows_linear (mean and
+ * biased variance over d, ln_eps inside the square root), products on fp32
+ * MFMA.  rows <= 64 and d a multiple of 4 up to 256 (MPL_EUNSUPPORTED
+ * otherwise).  Deterministic.  No counterpart in the reference's interface:
+ * it replaces a LayerNorm launch and a library GEMM in the decode step.
+ */
+int mpl_vocab_logits(const float* x, const float* ln_scale, const float* ln_bias, float ln_eps, const float* emb,
+                     int64_t rows, int d, int64_t V, float* logits, void* stream);
+
 size_t mpl_lookup_bwd_dense_workspace_bytes(int64_t M, int H, int n, int half, int score_dtype);
 int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_hat, const void* packed_keys,
                          const int32_t* sub_idx, const float* d_sub, const float* clean_counts, const void* state,

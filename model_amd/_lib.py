@@ -77,6 +77,7 @@ SIGNATURES = {
     "mpl_decode_next_token": (_I, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P]),
     "mpl_decode_embed": (_I, [_P, _I64, _P, _I64, _I, _P, _P, _I64, _P, _P]),
     "mpl_rows_linear": (_I, [_P, _P, _P, _P, _F, _P, _I, _P, _I, _P, _I64, _I, _I, _P, _P]),
+    "mpl_vocab_logits": (_I, [_P, _P, _P, _F, _P, _I64, _I, _I64, _P, _P]),
     "mpl_rows_linear_pair": (_I, [_P, _P, _P, _F, _P, _P, _I, _I, _I64, _I, _I, _I, _P, _P, _P]),
     "mpl_balance_state_bytes": (_SZ, [_I64, _I]),
     "mpl_balance_fwd": (_I, [_P, _I, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P, _P, _P]),

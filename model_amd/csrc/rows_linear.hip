@@ -321,6 +321,98 @@ void launch_rows_linear(const LinearArgs& a, bool ln, bool mul, hipStream_t s) {
     rows_linear_kernel<LAYOUT, false, false, 1><<<grid, kThreads, 0, s>>>(a);
 }
 
+// The output layer of a decode step (model.py:125-126): logits [rows, V] =
+// LayerNorm(x) . emb^T (embed.attend of ln_final), rows <= 64, d <= 256 with
+// d % 4 == 0.  A workgroup owns 64 vocabulary rows: their embedding rows
+// and the normalised x rows (LayerNorm as in rows_linear_kernel: mean, then
+// the centred variance, rsqrt(var + eps)) sit in LDS, and each wave forms
+// one 32 x 32 block of the tile with fp32 MFMAs (v_mfma_f32_32x32x2_f32,
+// A = x rows, B = embedding rows: lane l gives element (l % 32, k + l / 32)
+// of each, and holds logits[8 (r/4) + 4 (l/32) + r%4][l % 32] in r).  The
+// LDS pitch (d + 2 floats) puts the two k of a lane pair on adjacent banks.
+constexpr int kVT = 256;       // threads (4 waves: 2 x 2 blocks)
+constexpr int kVR = 64;        // x rows (streams) per tile
+constexpr int kVV = 64;        // vocabulary rows per tile
+constexpr int kVP = 256 + 2;   // LDS pitch in floats (d <= 256)
+
+__global__ __launch_bounds__(kVT) void vocab_logits_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ ln_scale,
+                                                           const float* __restrict__ ln_bias, float eps,
+                                                           const float* __restrict__ emb, int rows, int d,
+                                                           int64_t V, float* __restrict__ out) {
+  __shared__ float sX[kVR * kVP];
+  __shared__ float sE[kVV * kVP];
+  __shared__ float sStat[kVR][2];
+  const int tid = threadIdx.x;
+  const int64_t v0 = (int64_t)blockIdx.x * kVV;
+  const int d4 = d >> 2;
+  constexpr int kPer = kVV * 64 / kVT;  // float4 per thread of a 64-row tile at d = 256
+  // every load of both tiles is issued before the first store (rows past V
+  // or `rows` read as zero)
+  float4 ev[kPer], xv[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int f = tid + kVT * i;
+    const int r = f / d4, c = f - r * d4;
+    const int64_t v = v0 + r;
+    const bool ok = f < kVV * d4;
+    ev[i] = (ok && v < V) ? *(const float4*)(emb + v * d + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    xv[i] = (ok && r < rows) ? *(const float4*)(x + (int64_t)r * d + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int f = tid + kVT * i;
+    if (f >= kVV * d4) break;
+    const int r = f / d4, c = f - r * d4;
+    float2* de = (float2*)&sE[r * kVP + 4 * c];  // 8-byte aligned: kVP and 4 c are even
+    de[0] = make_float2(ev[i].x, ev[i].y);
+    de[1] = make_float2(ev[i].z, ev[i].w);
+    float2* dx = (float2*)&sX[r * kVP + 4 * c];
+    dx[0] = make_float2(xv[i].x, xv[i].y);
+    dx[1] = make_float2(xv[i].z, xv[i].w);
+  }
+  __syncthreads();
+  // LayerNorm statistics of the x rows from LDS, four threads per row
+  {
+    const int row = tid >> 2, part = tid & 3;
+    const float* xr = sX + row * kVP;
+    float s = 0.f;
+    for (int j = part; j < d; j += 4) s += xr[j];
+    s += __shfl_xor(s, 1, 4);
+    s += __shfl_xor(s, 2, 4);
+    const float mean = s / (float)d;
+    float q = 0.f;
+    for (int j = part; j < d; j += 4) {
+      const float c = xr[j] - mean;
+      q += c * c;
+    }
+    q += __shfl_xor(q, 1, 4);
+    q += __shfl_xor(q, 2, 4);
+    if (part == 0) {
+      sStat[row][0] = mean;
+      sStat[row][1] = rsqrtf(q / (float)d + eps);
+    }
+  }
+  __syncthreads();
+  for (int j = tid; j < d; j += kVT) {  // normalise in place, a column per thread (rows past `rows` stay zero)
+    const float gj = ln_scale[j], bj = ln_bias[j];
+    for (int r = 0; r < rows; ++r) sX[r * kVP + j] = (sX[r * kVP + j] - sStat[r][0]) * sStat[r][1] * gj + bj;
+  }
+  __syncthreads();
+  const int wave = tid >> 6, lane = tid & 63, li = lane & 31, lk = lane >> 5;
+  const int tb = wave >> 1, vb = wave & 1;
+  const float* pa = sX + (32 * tb + li) * kVP + lk;
+  const float* pb = sE + (32 * vb + li) * kVP + lk;
+  f32x16 acc = f32x16{};
+  for (int kk = 0; kk < d; kk += 2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[kk], pb[kk], acc, 0, 0, 0);
+  const int64_t v = v0 + 32 * vb + li;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int row = 32 * tb + 8 * (r >> 2) + 4 * lk + (r & 3);
+    if (row < rows && v < V) out[(int64_t)row * V + v] = acc[r];
+  }
+}
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
@@ -357,6 +449,23 @@ extern "C" int mpl_rows_linear(const float* x, const float* x_mul, const float* 
   else
     launch_rows_linear<MPL_W_IN_OUT>(a, ln, mul, s);
   return check_launch("mpl_rows_linear");
+}
+
+extern "C" int mpl_vocab_logits(const float* x, const float* ln_scale, const float* ln_bias, float ln_eps,
+                                const float* emb, int64_t rows, int d, int64_t V, float* logits, void* stream) {
+  clear_error();
+  MPL_REQUIRE(rows >= 0 && d > 0 && V > 0, MPL_EINVAL, "mpl_vocab_logits: bad sizes");
+  MPL_REQUIRE(rows <= kVR && d <= 256 && d % 4 == 0, MPL_EUNSUPPORTED,
+              "mpl_vocab_logits: needs rows <= %d and d a multiple of 4 up to 256 (rows %lld, d %d)", kVR,
+              (long long)rows, d);
+  if (rows == 0) return MPL_OK;
+  MPL_REQUIRE(x && ln_scale && ln_bias && emb && logits && aligned16(emb), MPL_EINVAL,
+              "mpl_vocab_logits: null buffer or unaligned embedding table");
+  const int64_t tiles = (V + kVV - 1) / kVV;
+  MPL_REQUIRE(tiles < ((int64_t)1 << 31), MPL_EUNSUPPORTED, "mpl_vocab_logits: vocabulary too large");
+  vocab_logits_kernel<<<(unsigned)tiles, kVT, 0, (hipStream_t)stream>>>(x, ln_scale, ln_bias, ln_eps, emb,
+                                                                      (int)rows, d, V, logits);
+  return check_launch("mpl_vocab_logits");
 }
 
 extern "C" int mpl_rows_linear_pair(const float* x, const float* ln_scale, const float* ln_bias, float ln_eps,

@@ -203,6 +203,20 @@ def decode_attention(qkv: torch.Tensor, positions: torch.Tensor, layer_cache: Di
     return out
 
 
+def vocab_logits(x: torch.Tensor, ln_scale: torch.Tensor, ln_bias: torch.Tensor, emb: torch.Tensor) -> torch.Tensor:
+    """mpl_vocab_logits: LayerNorm(x) . emb^T (model.py:125-126, ln_final then
+    embed.attend) for at most 64 rows of d <= 256 (d % 4 == 0), one launch."""
+    from . import _lib
+
+    rows, d = x.shape
+    V = emb.shape[0]
+    out = torch.empty((rows, V), dtype=torch.float32, device=x.device)
+    P = lambda t: t.data_ptr()
+    _lib.check(_lib.lib().mpl_vocab_logits(P(x), P(ln_scale.contiguous()), P(ln_bias.contiguous()), LN_EPS, P(emb),
+                                           rows, d, V, P(out), _lib.stream_ptr(x.device)), "mpl_vocab_logits")
+    return out
+
+
 def _ln(x, p):
     return F.layer_norm(x, (x.shape[-1],), p["scale"], p["bias"], LN_EPS)
 
@@ -437,9 +451,12 @@ class MemoryPoolLM:
                     mem, aux = self.pool.apply({"params": p["pool"]}, q, noise_scale=noise_scale, rngs=rngs)
                     x = rows_linear(mem.float().contiguous(), mo["kernel"], mo["bias"], x_mul=gate, residual=x)
                     layer_aux.append(aux)
-            # the vocabulary product is a plain 64 x 256 x 16,384-class GEMM: the library's
-            # tiles run it faster than 16-row tiles would
-            logits = F.linear(_ln(x, p["ln_final"]), emb)[:, None]
+            lf = p["ln_final"]
+            if (B <= 64 and d % 4 == 0 and d <= 256 and emb.dtype == torch.float32 and emb.is_contiguous()
+                    and emb.data_ptr() % 16 == 0 and x.is_contiguous()):
+                logits = vocab_logits(x, lf["scale"], lf["bias"], emb)[:, None]  # one launch
+            else:
+                logits = F.linear(_ln(x, lf), emb)[:, None]
         return logits, _LazyMerged(layer_aux)
 
     def _attention(self, p, h, layer_cache, positions, drop=None):

@@ -118,3 +118,22 @@ def test_rows_linear_pair_equals_two_layers(gpu_lib, rows, K, n1, n2, ln, act1, 
     torch.cuda.synchronize()
     assert o1.shape == (rows, n1) and o2.shape == (rows, n2)
     assert torch.equal(o1, r1) and torch.equal(o2, r2)
+
+
+@pytest.mark.parametrize("rows,d,V", [(64, 256, 16384), (5, 64, 300), (2, 32, 50), (64, 256, 1000), (1, 128, 64)])
+def test_vocab_logits_matches_torch(gpu_lib, rows, d, V):
+    """mpl_vocab_logits against torch's layer_norm + linear in fp64 on the
+    same fp32 inputs: within fp32 rounding (1e-5 of the largest |logit|)."""
+    import torch.nn.functional as F
+    from model_amd.model import LN_EPS, vocab_logits
+    g = torch.Generator(device="cuda").manual_seed(rows * 31 + d + V)
+    x = torch.randn((rows, d), generator=g, device="cuda") * 2.0 + 0.5
+    sc = torch.rand(d, generator=g, device="cuda") + 0.5
+    bi = torch.randn(d, generator=g, device="cuda") * 0.1
+    emb = torch.randn((V, d), generator=g, device="cuda") * 0.05
+    print(f"vocab logits rows={rows} d={d} V={V}", flush=True)
+    out = vocab_logits(x, sc, bi, emb)
+    torch.cuda.synchronize()
+    ref = F.linear(F.layer_norm(x.double(), (d,), sc.double(), bi.double(), LN_EPS), emb.double())
+    err = float((out.double() - ref).abs().max()) / float(ref.abs().max())
+    assert err <= 1e-5, err
