@@ -540,7 +540,8 @@ def train_step_bench(torch, iters):
     # captured in one HIP graph and replayed.
     g_bal = torch.full((), 0.01, device=dev)
     g_div = torch.full((), 0.01, device=dev)
-    side = torch.cuda.Stream()  # default priority
+    side = torch.cuda.Stream()  # default priorities
+    side2 = torch.cuda.Stream()
 
     def step_graph(_i):
         with torch.no_grad():
@@ -554,11 +555,20 @@ def train_step_bench(torch, iters):
                     pending["m"] = upd.merge({"slots": [aux["slots"]], "weights": [aux["weights"]]}, {0: g_out}, [0],
                                              count_slots=True)
 
+            def start_wgrad(dq):  # the projection's weight gradient beside the sub-key passes
+                side2.wait_stream(cur)
+                dq.record_stream(side2)
+                with torch.cuda.stream(side2):
+                    pending["gw"] = hidden.t() @ dq.reshape(M, H * d_key)
+
             # the key diversity term's gradient joins d sub_keys inside the call
             out, aux, (dq, gk, dlt) = pool.forward_backward({"params": params}, q, g_out, g_bal, train=True,
-                                                            g_diversity=g_div, on_forward=start_merge)
-            gw = hidden.t() @ dq.reshape(M, H * d_key)
+                                                            g_diversity=g_div, on_forward=start_merge,
+                                                            on_dq=start_wgrad)
             cur.wait_stream(side)
+            cur.wait_stream(side2)
+            gw = pending["gw"]
+            gw.record_stream(cur)
             # the dense gradients' norm in the clip's own pass (no memset node)
             upd.apply(pending["m"], dense_grads=[gw, gk, dlt])
 
@@ -571,7 +581,8 @@ def train_step_bench(torch, iters):
             "ms_per_step": ms, "tokens_per_s": M / (ms * 1e-3), "timing": "eager, HIP events",
             "graph_ms_per_step": ms_graph, "graph_tokens_per_s": M / (ms_graph * 1e-3),
             "graph_timing": "the same step through MemoryPool.forward_backward (no torch autograd; the sparse row "
-                            "merge on a second stream beside the dense backward), "
+                            "merge and the projection's weight gradient on two more streams beside the dense "
+                            "backward), "
                             f"{iters} steps captured in one HIP graph and replayed between HIP events"}
 
 

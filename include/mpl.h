@@ -635,9 +635,15 @@ int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, const float* k_
  * operand packs then normalise the raw queries themselves, to the same bits
  * as mpl_l2_normalize.  Only with the balance term, without query_scale or
  * balance_temperature_grad, k <= 16 and half <= 128 (MPL_EUNSUPPORTED
- * otherwise).  Workspace as mpl_lookup_bwd_dense.  No counterpart in the
- * reference's interface (XLA fuses its own backward): it saves the separate
- * routed query pass, the fp32 q_hat pass and the split sums.
+ * otherwise).  Workspace as mpl_lookup_bwd_dense.  phase = 0 runs it all;
+ * phase = 1 only the query side (operand packs, scales, the query pass:
+ * d_queries is complete when it returns to the stream) and phase = 2 the
+ * sub-key side from what phase 1 left in the same workspace, so that a
+ * caller can start work that needs d_queries (the projection's weight
+ * gradient) on another stream between the two calls, which take the same
+ * arguments.  No counterpart in the reference's interface (XLA fuses its
+ * own backward): it saves the separate routed query pass, the fp32 q_hat
+ * pass and the split sums.
  */
 int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const float* k_hat,
                                  const void* packed_keys, const int32_t* sub_idx, const float* d_sub,
@@ -645,7 +651,7 @@ int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const
                                  int H, int n, int half, int k, int score_dtype, const float* temperature,
                                  void* workspace, size_t workspace_bytes, float eps, float* d_queries,
                                  const float* sub_keys, const float* g_diversity, void* div_workspace,
-                                 size_t div_workspace_bytes, float* diversity_loss, float* d_sub_keys,
+                                 size_t div_workspace_bytes, float* diversity_loss, float* d_sub_keys, int phase,
                                  void* stream);
 
 #ifdef __cplusplus

@@ -85,7 +85,7 @@ SIGNATURES = {
     "mpl_lookup_bwd_dense": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I64, _I, _I, _I, _I, _I, _P, _P,
                                   _SZ, _P, _P, _P, _P, _P]),
     "mpl_lookup_bwd_dense_queries": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I, _I, _I, _I, _I, _P, _P,
-                                         _SZ, _F, _P, _P, _P, _P, _SZ, _P, _P, _P]),
+                                         _SZ, _F, _P, _P, _P, _P, _SZ, _P, _P, _I, _P]),
 }
 
 _lib = None

@@ -1390,7 +1390,7 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
                                  int k, int score_dtype, const float* temperature, void* workspace,
                                  size_t workspace_bytes, float* dq_hat, float* dk_hat, float* dlen, float* dlogt,
                                  const float* q_raw, float eps, float* d_queries, const KeysGradArgs* kg,
-                                 void* stream) {
+                                 int phase, void* stream) {
   MPL_REQUIRE(M >= 0 && H >= 1 && n >= 1 && k >= 1 && k <= n, MPL_EINVAL, "mpl_lookup_bwd_dense: bad shape");
   MPL_REQUIRE(score_dtype == MPL_F16 || score_dtype == MPL_F32, MPL_EINVAL,
               "mpl_lookup_bwd_dense: bad score_dtype %d", score_dtype);
@@ -1445,6 +1445,9 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
   float* tpart = (float*)(ws + L.tpart);
   const float* rho = scaled ? q_len : nullptr;
 
+  // phase 1: the packs, scales and query pass; phase 2: the sub-key passes,
+  // from what phase 1 left in the same workspace; 0: both
+  const bool run_q = phase != 2, run_k = phase != 1;
   // without q_hat (fused form only) the packs normalise the raw queries
   const bool norm = q_hat == nullptr;
   const float* qsrc = norm ? q_raw : q_hat;
@@ -1454,7 +1457,8 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
 #define MPL_PACK_BOTH(HPV, NRM)                                                                               \
   pack_rows_both_f16_kernel<HPV, NRM><<<(unsigned)(HC * L.mblk), 256, 0, s>>>(qsrc, half, (int64_t)HC * half, M, \
                                                                               L.mblk, eps, qn, qt)
-  if (both && half == 128) {
+  if (!run_q) {
+  } else if (both && half == 128) {
     if (norm) MPL_PACK_BOTH(128, true);
     else MPL_PACK_BOTH(128, false);
   } else if (both) {
@@ -1462,22 +1466,24 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
     else MPL_PACK_BOTH(64, false);
   }
 #undef MPL_PACK_BOTH
-  if (!both) {
+  if (run_q && !both) {
     launch_pack<false>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qn, s);
     launch_pack<true>(L.pd, f32, q_hat, half, (int64_t)HC * half, M, HC, half, nullptr, 0, 0, L.mblk, qt, s);
   }
-  if (bal)
+  if (run_q && bal)
     launch_pack<true>(L.pd, f32, k_hat, (int64_t)n * half, half, n, HC, half, nullptr, 0, 0, L.nblk, kt, s);
   const float inv_mk = (float)(1.0 / ((double)M * k));
   const float coef = (float)((double)n / ((double)HC * M));
   const int vpt = HC * k / 4;
-  if (k % 4 == 0 && 256 % vpt == 0 && 256 % HC == 0 && ((uintptr_t)d_sub & 15) == 0)
+  if (!run_q) {
+  } else if (k % 4 == 0 && 256 % vpt == 0 && 256 % HC == 0 && ((uintptr_t)d_sub & 15) == 0)
     bwd_max_vec_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC,
                                                    k, L.mx_tpg, mx);
   else
     bwd_max_kernel<<<L.mx_groups, 256, 0, s>>>(routed ? d_sub : nullptr, query_scale ? q_len : nullptr, M, HC, k,
                                                L.mx_tpg, mx);
-  bwd_scale_kernel<<<HC, 256, 0, s>>>(bal ? clean_counts : nullptr, mx, L.mx_groups, n, HC, inv_mk,
+  if (run_q)
+    bwd_scale_kernel<<<HC, 256, 0, s>>>(bal ? clean_counts : nullptr, mx, L.mx_groups, n, HC, inv_mk,
                                       bal ? g_balance : nullptr, coef, temperature, btg ? 1 : 0, query_scale ? 1 : 0,
                                       bal ? sigma : nullptr, dks);
 
@@ -1537,12 +1543,13 @@ static int lookup_bwd_dense_impl(const float* q_hat, const float* q_len, const f
   pk.k = k;
   pk.dk_scale = dks;
   const unsigned gk = (unsigned)(HC * cdiv(n, kRowsPerGroup) * L.splits);
-#define MPL_GRAD(EV, HPV)                                                                \
-  if (fused) balance_grad_kernel<kModeDQR, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq);      \
-  else if (bal) balance_grad_kernel<kModeDQ, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq);    \
-  balance_grad_kernel<kModeDK, EV, HPV><<<gk, kBalThreads, 0, s>>>(pk)
+#define MPL_GRAD(EV, HPV)                                                                            \
+  if (run_q && fused) balance_grad_kernel<kModeDQR, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq);         \
+  else if (run_q && bal) balance_grad_kernel<kModeDQ, EV, HPV><<<gq, kBalThreads, 0, s>>>(pq);       \
+  if (run_k) balance_grad_kernel<kModeDK, EV, HPV><<<gk, kBalThreads, 0, s>>>(pk)
   MPL_BAL_DISPATCH(f32, L.pd.HP, MPL_GRAD);
 #undef MPL_GRAD
+  if (!run_k) return check_launch("mpl_lookup_bwd_dense");
   if (kg != nullptr) {
     // d sub_keys straight from the slices: the sub-key pass's, and with
     // g_div the key diversity Gram pass's on the same packs (memory.py:230-240)
@@ -1601,7 +1608,7 @@ extern "C" int mpl_lookup_bwd_dense(const float* q_hat, const float* q_len, cons
   return lookup_bwd_dense_impl(q_hat, q_len, k_hat, packed_keys, sub_idx, d_sub, clean_counts, state, g_balance,
                                balance_temperature_grad, query_scale, M, H, n, half, k, score_dtype, temperature,
                                workspace, workspace_bytes, dq_hat, dk_hat, dlen, dlogt, nullptr, 0.f, nullptr,
-                               nullptr, stream);
+                               nullptr, 0, stream);
 }
 
 extern "C" int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* queries, const float* k_hat,
@@ -1612,8 +1619,9 @@ extern "C" int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* que
                                             float eps, float* d_queries, const float* sub_keys,
                                             const float* g_diversity, void* div_workspace,
                                             size_t div_workspace_bytes, float* diversity_loss, float* d_sub_keys,
-                                            void* stream) {
+                                            int phase, void* stream) {
   clear_error();
+  MPL_REQUIRE(phase >= 0 && phase <= 2, MPL_EINVAL, "mpl_lookup_bwd_dense_queries: phase must be 0, 1 or 2");
   MPL_REQUIRE(d_queries != nullptr && sub_keys != nullptr && d_sub_keys != nullptr, MPL_EINVAL,
               "mpl_lookup_bwd_dense_queries: null d_queries, sub_keys or d_sub_keys");
   MPL_REQUIRE(half <= 128 && half % 4 == 0, MPL_EUNSUPPORTED,
@@ -1628,7 +1636,7 @@ extern "C" int mpl_lookup_bwd_dense_queries(const float* q_hat, const float* que
   const KeysGradArgs kg{sub_keys, g_diversity, div_workspace, diversity_loss, d_sub_keys};
   return lookup_bwd_dense_impl(q_hat, nullptr, k_hat, packed_keys, sub_idx, d_sub, clean_counts, state, g_balance,
                                0, 0, M, H, n, half, k, score_dtype, temperature, workspace, workspace_bytes,
-                               nullptr, nullptr, nullptr, nullptr, queries, eps, d_queries, &kg, stream);
+                               nullptr, nullptr, nullptr, nullptr, queries, eps, d_queries, &kg, phase, stream);
 }
 
 namespace mpl {

@@ -293,7 +293,7 @@ class MemoryPool:
                          g_balance: Optional[torch.Tensor] = None, *, train: bool = True,
                          noise_scale: float | torch.Tensor = 1.0, shuffle_reads: bool = False,
                          rngs: Optional[Dict[str, Any]] = None, g_diversity: Optional[torch.Tensor] = None,
-                         on_forward=None):
+                         on_forward=None, on_dq=None):
         """The forward of memory.py:119-227 and its backward for a given
         upstream gradient, without torch autograd: returns
         (out, aux, (d queries, d sub_keys, d log_temperature)).  The values
@@ -313,7 +313,12 @@ class MemoryPool:
         the selection and the value read are enqueued (before the balance
         statistics and the backward), so a caller can start work that needs
         only aux["slots"] and aux["weights"] (the sparse row merge,
-        SparseRowUpdate.merge) on another stream beside the rest."""
+        SparseRowUpdate.merge) on another stream beside the rest.
+        ``on_dq(d_queries)``, when given, is called once d queries (fp32,
+        shaped like the queries) is enqueued and before the sub-key
+        gradient's passes, so the caller can start what needs only d queries
+        (the projection's weight gradient) on another stream beside them;
+        such work must not write d_queries."""
         params = variables["params"] if "params" in variables else variables
         res = self.lookup(params, queries, train=train, noise_scale=noise_scale, shuffle_reads=shuffle_reads,
                           rngs=rngs, early_clean=g_balance is not None)
@@ -329,7 +334,7 @@ class MemoryPool:
         values = params["values"] if "values" in params else sub_keys.new_empty(0)
         extra = {}
         dq, dk, dlt, _ = _lookup_backward(self, res, internal, sub_keys.detach(), values.detach(), shapes, g_out,
-                                          g_balance, bool(shuffle_reads), False, g_diversity, extra)
+                                          g_balance, bool(shuffle_reads), False, g_diversity, extra, on_dq)
         if "key_diversity_loss" in extra:
             dict.__setitem__(aux, "key_diversity_loss", extra["key_diversity_loss"])
         out = res["out"].reshape(*tuple(queries.shape[:-2]), self.d_value)
@@ -675,7 +680,8 @@ class _LookupFunction(torch.autograd.Function):
 
 
 def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_balance, shuffle_reads: bool,
-                     need_dv: bool, g_diversity: Optional[torch.Tensor] = None, extra: Optional[Dict] = None):
+                     need_dv: bool, g_diversity: Optional[torch.Tensor] = None, extra: Optional[Dict] = None,
+                     on_dq=None):
     """The backward of memory.py:136-213 on the GPU for one forward result
     ``res`` of MemoryPool.lookup: (d queries, d sub_keys, d log_temperature,
     d values or None).  ``g_balance`` is the gradient of the balance loss
@@ -740,11 +746,20 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
             dwsb = L.mpl_key_diversity_workspace_bytes(H, n, half, code)
             dws = torch.empty(max(dwsb, 256), dtype=torch.uint8, device=dev)
             div_loss = torch.empty(1, dtype=torch.float32, device=dev)
-        check(L.mpl_lookup_bwd_dense_queries(ptr(q_hat), ptr(q), ptr(k_hat), ptr(res["packed"]), ptr(res["sub_idx"]),
-                                             ptr(d_sub), ptr(internal["_counts"]), ptr(internal["_state"]), ptr(gb),
-                                             M, H, n, half, k, code, ptr(T), ptr(ws), wsb, NORM_EPS, ptr(dq),
-                                             ptr(raw_keys), ptr(gd), ptr(dws), dwsb, ptr(div_loss), ptr(dk),
-                                             stream), "mpl_lookup_bwd_dense_queries")
+        def dense(phase):
+            check(L.mpl_lookup_bwd_dense_queries(ptr(q_hat), ptr(q), ptr(k_hat), ptr(res["packed"]),
+                                                 ptr(res["sub_idx"]), ptr(d_sub), ptr(internal["_counts"]),
+                                                 ptr(internal["_state"]), ptr(gb), M, H, n, half, k, code, ptr(T),
+                                                 ptr(ws), wsb, NORM_EPS, ptr(dq), ptr(raw_keys), ptr(gd), ptr(dws),
+                                                 dwsb, ptr(div_loss), ptr(dk), phase, stream),
+                  "mpl_lookup_bwd_dense_queries")
+
+        if on_dq is None:
+            dense(0)
+        else:  # the query side, the caller's hook (d queries is enqueued), then the sub-key side
+            dense(1)
+            on_dq(dq.reshape(q_shape))
+            dense(2)
         if div_loss is not None:
             g_diversity = None  # taken in the fused pass
             if extra is not None:
@@ -774,6 +789,8 @@ def _lookup_backward(pool, res, internal, sub_keys, values, shapes, g_out, g_bal
         check(L.mpl_lookup_bwd_queries(ptr(q), ptr(q_len), ptr(k_hat), ptr(res["sub_idx"]), ptr(d_sub),
                                        ptr(res["sub_scores"]), ptr(dq_extra), ptr(dlen_extra), M, H, n, half, k,
                                        ptr(T), ptr(dq), stream), "mpl_lookup_bwd_queries")
+        if on_dq is not None:
+            on_dq(dq.reshape(q_shape))
     # sub-keys (fp32 scoring without the balance term, or no tokens):
     # sort-by-key segmented sum
     if not dense:

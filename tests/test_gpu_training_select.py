@@ -94,8 +94,9 @@ def test_training_backward_c4_with_noise(gpu_lib):
            float(np.abs(ref["d_cos"] * sel["cos"]).sum()))
 
 
-@pytest.mark.parametrize("values_dtype,M", [(torch.float16, 8192), (torch.float16, 300), (torch.float32, 1000)])
-def test_fused_query_backward_equals_separate_pass(gpu_lib, monkeypatch, values_dtype, M):
+@pytest.mark.parametrize("values_dtype,M,k", [(torch.float16, 8192, 16), (torch.float16, 300, 16),
+                                              (torch.float32, 1000, 16), (torch.float16, 777, 8)])
+def test_fused_query_backward_equals_separate_pass(gpu_lib, monkeypatch, values_dtype, M, k):
     """mpl_lookup_bwd_dense_queries (the routed d q_hat inside the balance
     query pass, then the normalisation backward) against the separate
     passes (mpl_lookup_bwd_dense + mpl_lookup_bwd_queries) on the same
@@ -103,7 +104,6 @@ def test_fused_query_backward_equals_separate_pass(gpu_lib, monkeypatch, values_
     rides the fp16 MFMA operand there) and 1e-5 in fp32; the sub-key and
     log-temperature gradients are those of the separate path bit for bit."""
     from model_amd import memory as mem
-    k = 16
     pool = MemoryPool(N_SUB if values_dtype == torch.float16 else 64, H, D_KEY, D, k, routing_noise=1.0,
                       values_dtype=values_dtype)
     params = make_params(pool, 77, key_std=(D_KEY // 2) ** -0.5, value_std=0.02)
@@ -180,3 +180,44 @@ def test_forward_backward_with_key_diversity(gpu_lib, values_dtype, query_scale)
     assert err <= 1e-5, f"d sub_keys: {err:.3g}"
     assert torch.equal(aux["key_diversity_loss"].reshape(()), loss.reshape(()))
     assert torch.equal(dqa, dqb) and torch.equal(dla, dlb)
+
+
+@pytest.mark.parametrize("values_dtype", [torch.float16, torch.float32])
+def test_forward_backward_on_dq_hook(gpu_lib, values_dtype):
+    """forward_backward(on_dq=hook): the dense backward runs as its query
+    phase, the hook, then its sub-key phase (fp16 operands; the fp32 pool
+    takes the separate query pass and calls the hook after it).  The hook
+    gets the finished d queries: a copy it starts on another stream equals
+    the returned d queries, and every gradient and the diversity loss equal
+    those of the call without the hook bit for bit."""
+    k, M = 16, 2048
+    n = 512 if values_dtype == torch.float16 else 128
+    pool = MemoryPool(n, H, D_KEY, 64, k, routing_noise=1.0, values_dtype=values_dtype)
+    params = make_params(pool, 97, key_std=(D_KEY // 2) ** -0.5, value_std=0.02)
+    g = torch.Generator(device="cuda").manual_seed(98)
+    q = torch.randn((M, H, D_KEY), generator=g, device="cuda")
+    g_out = torch.randn((M, 64), generator=g, device="cuda") * 1e-3
+    g_bal = torch.full((), 0.01, device="cuda")
+    g_div = torch.full((), 0.05, device="cuda")
+    print(f"forward_backward on_dq hook {values_dtype}", flush=True)
+    side = torch.cuda.Stream()
+    seen = {}
+
+    def hook(dq):
+        cur = torch.cuda.current_stream()
+        side.wait_stream(cur)
+        dq.record_stream(side)
+        with torch.cuda.stream(side):
+            seen["copy"] = dq.clone()
+        seen["calls"] = seen.get("calls", 0) + 1
+
+    _, aux_a, (dqa, dka, dla) = pool.forward_backward(params, q, g_out, g_bal, train=True, rngs={"routing": 4},
+                                                      g_diversity=g_div, on_dq=hook)
+    torch.cuda.current_stream().wait_stream(side)
+    _, aux_b, (dqb, dkb, dlb) = pool.forward_backward(params, q, g_out, g_bal, train=True, rngs={"routing": 4},
+                                                      g_diversity=g_div)
+    torch.cuda.synchronize()
+    assert seen["calls"] == 1
+    assert torch.equal(seen["copy"], dqa)
+    assert torch.equal(dqa, dqb) and torch.equal(dka, dkb) and torch.equal(dla, dlb)
+    assert torch.equal(aux_a["key_diversity_loss"], aux_b["key_diversity_loss"])
