@@ -597,7 +597,7 @@ int mpl_rows_linear_pair(const float* x, const float* ln_scale, const float* ln_
 /*
  * The output layer of a decode step (model.py:125-126): logits [rows, V] =
  * LayerNorm(x) . emb^T (ln_final, then embed.attend), x [rows, d], emb
- * [V, d] (16-byte aligned), LayerNorm as in mpl_rows_linear (mean and
+ * [V, d] (x, ln_scale, ln_bias and emb 16-byte aligned), LayerNorm as in mpl_rows_linear (mean and
  * biased variance over d, ln_eps inside the square root), products on fp32
  * MFMA.  rows <= 64 and d a multiple of 4 up to 256 (MPL_EUNSUPPORTED
  * otherwise).  Deterministic.  No counterpart in the reference's interface:

@@ -29,6 +29,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "topk.h"
 
 namespace mpl {
 namespace {
@@ -192,11 +193,16 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     float s = 0.0f;
     if (row < nrows) {
       if (hold) {
+        // clamped loads, zeroed after: a select of the load's address would
+        // turn them into flat loads of a private zero
 #pragma unroll
         for (int h = 0; h < kHold; ++h) {
           const int j = part + h * TPR;
-          hv[h] = j < K4 ? xr[j] : zero;
+          hv[h] = xr[j < K4 ? j : K4 - 1];
         }
+#pragma unroll
+        for (int h = 0; h < kHold; ++h)
+          if (part + h * TPR >= K4) hv[h] = zero;
 #pragma unroll
         for (int h = 0; h < kHold; ++h) s += (hv[h].x + hv[h].y) + (hv[h].z + hv[h].w);
       } else {
@@ -323,93 +329,117 @@ void launch_rows_linear(const LinearArgs& a, bool ln, bool mul, hipStream_t s) {
 
 // The output layer of a decode step (model.py:125-126): logits [rows, V] =
 // LayerNorm(x) . emb^T (embed.attend of ln_final), rows <= 64, d <= 256 with
-// d % 4 == 0.  A workgroup owns 64 vocabulary rows: their embedding rows
-// and the normalised x rows (LayerNorm as in rows_linear_kernel: mean, then
-// the centred variance, rsqrt(var + eps)) sit in LDS, and each wave forms
-// one 32 x 32 block of the tile with fp32 MFMAs (v_mfma_f32_32x32x2_f32,
-// A = x rows, B = embedding rows: lane l gives element (l % 32, k + l / 32)
-// of each, and holds logits[8 (r/4) + 4 (l/32) + r%4][l % 32] in r).  The
-// LDS pitch (d + 2 floats) puts the two k of a lane pair on adjacent banks.
+// d % 4 == 0.  A workgroup owns 64 vocabulary rows.  Wave w loads rows
+// w, w + 4, ... of x and of the tile's embedding rows, lane c the float4 at
+// column 4c, all 32 loads before any use; each x row's LayerNorm statistics
+// (mean, then the centred variance, rsqrt(var + eps)) are wave reductions of
+// the registers, and the normalised rows go to LDS beside the embedding rows.
+// Each wave then forms one 32 x 32 block of the tile with fp32 MFMAs
+// (v_mfma_f32_32x32x2_f32: lane l gives element (l % 32, k) of A = x rows and
+// B = embedding rows and holds logits[8 (r/4) + 4 (l/32) + r%4][l % 32] in
+// r).  The K order is permuted so that one 16-byte LDS read feeds four
+// MFMAs: over an 8-column group, MFMA i of the group takes columns i and
+// i + 4 (lanes 0-31 and 32-63), and even and odd MFMAs go to two accumulator
+// chains.  The LDS pitch (d + 4 floats) keeps rows 16-byte aligned, and the
+// 8 lanes of a 16-byte read phase cover all banks.
 constexpr int kVT = 256;       // threads (4 waves: 2 x 2 blocks)
 constexpr int kVR = 64;        // x rows (streams) per tile
 constexpr int kVV = 64;        // vocabulary rows per tile
-constexpr int kVP = 256 + 2;   // LDS pitch in floats (d <= 256)
+constexpr int kVP4 = 65;       // LDS pitch in float4 (d <= 256, plus one)
+
+// v[i] = the sum of v[i] over the wave, in every lane, for N values at
+// once (exchanges on DPP and permlane, no LDS).
+template <int N>
+__device__ __forceinline__ void wave_allsum(float (&v)[N], int lane) {
+#define MPL_XSUM(S)                                                                        \
+  _Pragma("unroll") for (int i = 0; i < N; ++i) v[i] += __uint_as_float(w64::xr<S>(__float_as_uint(v[i]), lane));
+  MPL_XSUM(32) MPL_XSUM(16) MPL_XSUM(8) MPL_XSUM(4) MPL_XSUM(2) MPL_XSUM(1)
+#undef MPL_XSUM
+}
 
 __global__ __launch_bounds__(kVT) void vocab_logits_kernel(const float* __restrict__ x,
                                                            const float* __restrict__ ln_scale,
                                                            const float* __restrict__ ln_bias, float eps,
                                                            const float* __restrict__ emb, int rows, int d,
                                                            int64_t V, float* __restrict__ out) {
-  __shared__ float sX[kVR * kVP];
-  __shared__ float sE[kVV * kVP];
-  __shared__ float sStat[kVR][2];
-  const int tid = threadIdx.x;
+  __shared__ float4 sX[kVR * kVP4];
+  __shared__ float4 sE[kVV * kVP4];
+  constexpr int kPer = kVR / (kVT / 64);  // rows per wave
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int64_t v0 = (int64_t)blockIdx.x * kVV;
   const int d4 = d >> 2;
-  constexpr int kPer = kVV * 64 / kVT;  // float4 per thread of a 64-row tile at d = 256
-  // every load of both tiles is issued before the first store (rows past V
-  // or `rows` read as zero)
+  const bool colok = lane < d4;  // lanes past the row end store zeros
+  const float4 z4 = make_float4(0.f, 0.f, 0.f, 0.f);
+  // every load is issued unconditionally at a clamped (in-bounds) address
+  // and zeroed after, so that all 34 go out back to back
+  const int c4 = 4 * (colok ? lane : d4 - 1);
   float4 ev[kPer], xv[kPer];
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int f = tid + kVT * i;
-    const int r = f / d4, c = f - r * d4;
+    const int r = 4 * i + wave;
     const int64_t v = v0 + r;
-    const bool ok = f < kVV * d4;
-    ev[i] = (ok && v < V) ? *(const float4*)(emb + v * d + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
-    xv[i] = (ok && r < rows) ? *(const float4*)(x + (int64_t)r * d + 4 * c) : make_float4(0.f, 0.f, 0.f, 0.f);
+    ev[i] = *(const float4*)(emb + (v < V ? v : V - 1) * d + c4);
+    xv[i] = *(const float4*)(x + (int64_t)(r < rows ? r : rows - 1) * d + c4);
   }
+  float4 g4 = *(const float4*)(ln_scale + c4);
+  float4 b4 = *(const float4*)(ln_bias + c4);
 #pragma unroll
   for (int i = 0; i < kPer; ++i) {
-    const int f = tid + kVT * i;
-    if (f >= kVV * d4) break;
-    const int r = f / d4, c = f - r * d4;
-    float2* de = (float2*)&sE[r * kVP + 4 * c];  // 8-byte aligned: kVP and 4 c are even
-    de[0] = make_float2(ev[i].x, ev[i].y);
-    de[1] = make_float2(ev[i].z, ev[i].w);
-    float2* dx = (float2*)&sX[r * kVP + 4 * c];
-    dx[0] = make_float2(xv[i].x, xv[i].y);
-    dx[1] = make_float2(xv[i].z, xv[i].w);
+    const int r = 4 * i + wave;
+    if (!colok || v0 + r >= V) ev[i] = z4;
+    if (!colok || r >= rows) xv[i] = z4;
   }
-  __syncthreads();
-  // LayerNorm statistics of the x rows from LDS, four threads per row
-  {
-    const int row = tid >> 2, part = tid & 3;
-    const float* xr = sX + row * kVP;
-    float s = 0.f;
-    for (int j = part; j < d; j += 4) s += xr[j];
-    s += __shfl_xor(s, 1, 4);
-    s += __shfl_xor(s, 2, 4);
-    const float mean = s / (float)d;
-    float q = 0.f;
-    for (int j = part; j < d; j += 4) {
-      const float c = xr[j] - mean;
-      q += c * c;
+  if (!colok) g4 = b4 = z4;
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) sE[(4 * i + wave) * kVP4 + lane] = ev[i];
+  const float inv_d = 1.f / (float)d;
+  float mean[kPer], var[kPer];
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) mean[i] = (xv[i].x + xv[i].y) + (xv[i].z + xv[i].w);
+  wave_allsum<kPer>(mean, lane);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    mean[i] *= inv_d;
+    if (colok) {
+      xv[i].x -= mean[i]; xv[i].y -= mean[i]; xv[i].z -= mean[i]; xv[i].w -= mean[i];
     }
-    q += __shfl_xor(q, 1, 4);
-    q += __shfl_xor(q, 2, 4);
-    if (part == 0) {
-      sStat[row][0] = mean;
-      sStat[row][1] = rsqrtf(q / (float)d + eps);
+    var[i] = (xv[i].x * xv[i].x + xv[i].y * xv[i].y) + (xv[i].z * xv[i].z + xv[i].w * xv[i].w);
+  }
+  wave_allsum<kPer>(var, lane);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int r = 4 * i + wave;
+    const float rs = rsqrtf(var[i] * inv_d + eps);
+    float4 y = z4;  // rows past `rows` and columns past d stay zero
+    if (colok && r < rows) {
+      y.x = xv[i].x * rs * g4.x + b4.x;
+      y.y = xv[i].y * rs * g4.y + b4.y;
+      y.z = xv[i].z * rs * g4.z + b4.z;
+      y.w = xv[i].w * rs * g4.w + b4.w;
     }
+    sX[r * kVP4 + lane] = y;
   }
   __syncthreads();
-  for (int j = tid; j < d; j += kVT) {  // normalise in place, a column per thread (rows past `rows` stay zero)
-    const float gj = ln_scale[j], bj = ln_bias[j];
-    for (int r = 0; r < rows; ++r) sX[r * kVP + j] = (sX[r * kVP + j] - sStat[r][0]) * sStat[r][1] * gj + bj;
-  }
-  __syncthreads();
-  const int wave = tid >> 6, lane = tid & 63, li = lane & 31, lk = lane >> 5;
+  const int li = lane & 31, lk = lane >> 5;
   const int tb = wave >> 1, vb = wave & 1;
-  const float* pa = sX + (32 * tb + li) * kVP + lk;
-  const float* pb = sE + (32 * vb + li) * kVP + lk;
-  f32x16 acc = f32x16{};
-  for (int kk = 0; kk < d; kk += 2) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(pa[kk], pb[kk], acc, 0, 0, 0);
+  const float4* pa = sX + (32 * tb + li) * kVP4 + lk;
+  const float4* pb = sE + (32 * vb + li) * kVP4 + lk;
+  f32x16 acc0 = f32x16{}, acc1 = f32x16{};
+  // all 256 columns, unrolled so that LDS reads run ahead of the MFMAs:
+  // columns past d hold the zeros stored above
+#pragma unroll
+  for (int gi = 0; gi < 32; ++gi) {
+    const float4 av = pa[2 * gi], bv = pb[2 * gi];
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.x, bv.x, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.y, bv.y, acc1, 0, 0, 0);
+    acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.z, bv.z, acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(av.w, bv.w, acc1, 0, 0, 0);
+  }
   const int64_t v = v0 + 32 * vb + li;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int row = 32 * tb + 8 * (r >> 2) + 4 * lk + (r & 3);
-    if (row < rows && v < V) out[(int64_t)row * V + v] = acc[r];
+    if (row < rows && v < V) out[(int64_t)row * V + v] = acc0[r] + acc1[r];
   }
 }
 
@@ -459,8 +489,9 @@ extern "C" int mpl_vocab_logits(const float* x, const float* ln_scale, const flo
               "mpl_vocab_logits: needs rows <= %d and d a multiple of 4 up to 256 (rows %lld, d %d)", kVR,
               (long long)rows, d);
   if (rows == 0) return MPL_OK;
-  MPL_REQUIRE(x && ln_scale && ln_bias && emb && logits && aligned16(emb), MPL_EINVAL,
-              "mpl_vocab_logits: null buffer or unaligned embedding table");
+  MPL_REQUIRE(x && ln_scale && ln_bias && emb && logits, MPL_EINVAL, "mpl_vocab_logits: null buffer");
+  MPL_REQUIRE(aligned16(x) && aligned16(ln_scale) && aligned16(ln_bias) && aligned16(emb), MPL_EINVAL,
+              "mpl_vocab_logits: x, ln_scale, ln_bias and emb must be 16-byte aligned");
   const int64_t tiles = (V + kVV - 1) / kVV;
   MPL_REQUIRE(tiles < ((int64_t)1 << 31), MPL_EUNSUPPORTED, "mpl_vocab_logits: vocabulary too large");
   vocab_logits_kernel<<<(unsigned)tiles, kVT, 0, (hipStream_t)stream>>>(x, ln_scale, ln_bias, ln_eps, emb,
