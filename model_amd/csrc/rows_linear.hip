@@ -90,23 +90,26 @@ __device__ __forceinline__ void fma4(float& acc, const float4& v, const float4& 
 }
 
 // U: K columns per thread whose loads are in flight together (1 when a
-// thread has a single column, K <= 4 * kSlices)
-template <int LAYOUT, bool LN, bool MUL, int U>
+// thread has a single column, K <= 4 * kSlices).  TR: rows per tile, 16, or
+// 4 for narrow products (N = 256 at 64 rows: 256 workgroups instead of 64);
+// the per-element summation order is the same for both.
+template <int LAYOUT, bool LN, bool MUL, int U, int TR = kTR>
 __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
-  __shared__ float red[kWaves][kTR * kTN];
-  __shared__ float s_mean[kTR], s_rstd[kTR];
+  static_assert(TR == 16 || (TR == 4 && !LN), "16-row tiles, or 4-row tiles without the layer norm");
+  __shared__ float red[kWaves][TR * kTN];
+  __shared__ float s_mean[TR], s_rstd[TR];
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-  const int64_t r0 = (int64_t)blockIdx.y * kTR;
+  const int64_t r0 = (int64_t)blockIdx.y * TR;
   const int n0 = blockIdx.x * kTN;
   const int K = a.K, K4 = K / 4;
-  const int nrows = (int)min<int64_t>(kTR, a.rows - r0);  // valid rows of this tile
+  const int nrows = (int)min<int64_t>(TR, a.rows - r0);  // valid rows of this tile
 
   // operands that do not depend on the row statistics are requested first:
   // the epilogue's bias and residual element of this thread (threads below
-  // kTR * kTN) and the weights of its first K columns
+  // TR * kTN) and the weights of its first K columns
   const int erow = tid / kTN, ecol = tid % kTN;
   const int en = n0 + ecol;
-  const bool eval = tid < kTR * kTN && erow < nrows && en < a.N;
+  const bool eval = tid < TR * kTN && erow < nrows && en < a.N;
   const int64_t eat = (r0 + erow) * a.N + en;
   const float ebias = (eval && a.bias) ? a.bias[en] : 0.0f;
   const float eres = (eval && a.residual) ? a.residual[eat] : 0.0f;
@@ -149,8 +152,8 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
   // requested before the row statistics too: the loads do not depend on them
   const float* xt = a.x + r0 * K;
   const float* mt = MUL ? a.x_mul + r0 * K : nullptr;
-  float4 xv[U][kTR];
-  float4 mv[LN && MUL ? U : 1][kTR];  // x_mul rows, applied after the normalisation
+  float4 xv[U][TR];
+  float4 mv[LN && MUL ? U : 1][TR];  // x_mul rows, applied after the normalisation
   float4 g[U], be[U];
   auto load_batch = [&](int jb) {
 #pragma unroll
@@ -159,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
       g[u] = LN ? *(const float4*)(a.ln_scale + k) : zero;
       be[u] = LN ? *(const float4*)(a.ln_bias + k) : zero;
 #pragma unroll
-      for (int i = 0; i < kTR; ++i) {
+      for (int i = 0; i < TR; ++i) {
         // rows past the end read row 0 (in bounds) and are never stored
         const int64_t off = (int64_t)(i < nrows ? i : 0) * K + k;
         float4 v = *(const float4*)(xt + off);
@@ -184,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     // 32 threads per row (consecutive lanes); a thread's part of the row is
     // kept in registers between the two passes when it has at most kHold
     // float4s (K <= 512), and read again otherwise
-    constexpr int TPR = kThreads / kTR;
+    constexpr int TPR = kThreads / TR;
     constexpr int kHold = 4;
     const int row = tid / TPR, part = tid % TPR;
     const float4* xr = (const float4*)(a.x + (r0 + (row < nrows ? row : 0)) * K);
@@ -240,9 +243,9 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     __syncthreads();
   }
 
-  float acc[2 * kTR];  // acc[2 i + c]: row i, column c0 + c
+  float acc[2 * TR];  // acc[2 i + c]: row i, column c0 + c
 #pragma unroll
-  for (int e = 0; e < 2 * kTR; ++e) acc[e] = 0.0f;
+  for (int e = 0; e < 2 * TR; ++e) acc[e] = 0.0f;
 
   for (int jb = j0; jb < K4; jb += U * kSlices) {
     if (jb != j0) load_batch(jb);  // the first batch was requested before the statistics
@@ -257,7 +260,7 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
     for (int u = 0; u < U; ++u) {
       if (jb + u * kSlices >= K4) break;  // a clamped column of the last batch
 #pragma unroll
-      for (int i = 0; i < kTR; ++i) {
+      for (int i = 0; i < TR; ++i) {
         float4 v = xv[u][i];
         if (LN) {
           const float mean = s_mean[i], rstd = s_rstd[i];
@@ -287,12 +290,17 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
   }
 
   // the wave's 8 K-slices (lane bits 3..5): afterwards lane (ks, cp) holds
-  // the sums of acc[4 ks + q], q < 4, i.e. rows 2 ks + q / 2, column 2 cp + q % 2
-  scatter_step<32, 32>(acc, lane);
-  scatter_step<16, 16>(acc, lane);
-  scatter_step<8, 8>(acc, lane);
+  // the sums of acc[e], e = (TR / 4) ks + q, q < TR / 4, i.e. row e / 2,
+  // column 2 cp + e % 2 (every element's sum is ((s0 + s4) + (s2 + s6)) +
+  // ((s1 + s5) + (s3 + s7)) over the slices, whatever TR is)
+  scatter_step<2 * TR, 32>(acc, lane);
+  scatter_step<TR, 16>(acc, lane);
+  scatter_step<TR / 2, 8>(acc, lane);
 #pragma unroll
-  for (int q = 0; q < 4; ++q) red[wave][(2 * ks + q / 2) * kTN + 2 * cp + q % 2] = acc[q];
+  for (int q = 0; q < TR / 4; ++q) {
+    const int e = (TR / 4) * ks + q;
+    red[wave][(e >> 1) * kTN + 2 * cp + (e & 1)] = acc[q];
+  }
   __syncthreads();
   if (eval) {
     const int o = tid;
@@ -311,6 +319,19 @@ __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
 
 template <int LAYOUT>
 void launch_rows_linear(const LinearArgs& a, bool ln, bool mul, hipStream_t s) {
+  // narrow products without the layer norm (N = 256 at 64 rows: the
+  // attention and feed-forward outputs, the memory read's output) take
+  // 4-row tiles, all their K columns in one batch of loads
+  if (!ln && cdiv(a.N, kTN) * cdiv(a.rows, kTR) < 128 && a.K <= 1024) {
+    const dim3 g4((unsigned)cdiv(a.N, kTN), (unsigned)cdiv(a.rows, 4));
+    if (mul)
+      rows_linear_kernel<LAYOUT, false, true, 1, 4><<<g4, kThreads, 0, s>>>(a);
+    else if (a.K / 4 > kSlices)
+      rows_linear_kernel<LAYOUT, false, false, 4, 4><<<g4, kThreads, 0, s>>>(a);
+    else
+      rows_linear_kernel<LAYOUT, false, false, 1, 4><<<g4, kThreads, 0, s>>>(a);
+    return;
+  }
   const dim3 grid((unsigned)cdiv(a.N, kTN), (unsigned)cdiv(a.rows, kTR));
   // two columns in flight only for the plain product with more than one
   // column per thread (the feed-forward output, K = 1,024): with a layer

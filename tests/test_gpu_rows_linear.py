@@ -68,6 +68,26 @@ def test_rows_linear_matches_oracle(gpu_lib, rows, K, N, out_in, ln, mul, act, b
     assert err <= 2e-5, f"relative error {err:.3g}"
 
 
+@pytest.mark.parametrize("K,mul,out_in", [(1024, False, False), (256, False, False), (256, True, False),
+                                          (1024, False, True), (640, False, False)])
+def test_narrow_tiles_equal_wide_tiles(gpu_lib, K, mul, out_in):
+    """A narrow product (N = 256 at 64 rows, no layer norm) runs on 4-row
+    tiles; the same columns inside a wide product (N = 2,048: 16-row tiles)
+    come out bit for bit the same, since each element's K-slice sums are
+    added in the same order on both."""
+    g = torch.Generator(device="cuda").manual_seed(K + 7 * mul + 3 * out_in)
+    x = torch.randn((64, K), generator=g, device="cuda")
+    W = torch.randn((2048, K) if out_in else (K, 2048), generator=g, device="cuda") * K ** -0.5
+    b = torch.randn(2048, generator=g, device="cuda")
+    r = torch.randn((64, 2048), generator=g, device="cuda")
+    m = torch.randn((64, K), generator=g, device="cuda") if mul else None
+    wide = rows_linear(x, W, b, out_in=out_in, x_mul=m, residual=r)
+    Wn = (W[:256] if out_in else W[:, :256]).contiguous()
+    narrow = rows_linear(x, Wn, b[:256].contiguous(), out_in=out_in, x_mul=m, residual=r[:, :256].contiguous())
+    torch.cuda.synchronize()
+    assert torch.equal(wide[:, :256], narrow)
+
+
 def test_rows_linear_is_deterministic_and_accepts_residual_as_output(gpu_lib):
     g = torch.Generator(device="cuda").manual_seed(3)
     x = torch.randn((64, 1024), generator=g, device="cuda")
