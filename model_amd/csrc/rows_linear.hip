@@ -92,7 +92,9 @@ __device__ __forceinline__ void fma4(float& acc, const float4& v, const float4& 
 // U: K columns per thread whose loads are in flight together (1 when a
 // thread has a single column, K <= 4 * kSlices).  TR: rows per tile, 16, or
 // 4 for narrow products (N = 256 at 64 rows: 256 workgroups instead of 64);
-// the per-element summation order is the same for both.
+// the per-element summation order is the same for both.  (8-row tiles for
+// the layer-normalised decode products measured slower: 0.245 against
+// 0.235 ms per generation step.)
 template <int LAYOUT, bool LN, bool MUL, int U, int TR = kTR>
 __global__ __launch_bounds__(kThreads) void rows_linear_kernel(LinearArgs a) {
   static_assert(TR == 16 || (TR == 4 && !LN), "16-row tiles, or 4-row tiles without the layer norm");
