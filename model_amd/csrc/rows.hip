@@ -514,9 +514,14 @@ __device__ __forceinline__ void pad_rows(const uint32_t* __restrict__ num_seg, i
 // segment starts in that range, so that the two crossing segments a range
 // can head, the one it continues and the one it starts, use different
 // rows).  Level 2 (seg_fixup_kernel): the wave of range ra adds the chunk
-// rows in chunk order and writes the segment's row and squared norm.  Rows
-// of segments inside one range were written by seg_reduce_kernel.  The
-// level-2 launch also pads rows [U, cap) with its last workgroups.
+// rows in chunk order and writes the segment's row and squared norm.  A
+// segment of one chunk (at most kFixChunk ranges: every crossing segment of
+// near-uniform routing) skips level 1: level 2 adds its partial rows in
+// range order itself, the same sum with the same bits, since level 2's
+// zero-started sum of one chunk row returns that row (a sum started at +0
+// is never -0).  Rows of segments inside one range were written by
+// seg_reduce_kernel.  The level-2 launch also pads rows [U, cap) with its
+// last workgroups.
 constexpr int kFixChunk = 32;
 
 // PB rows of partial-style storage (stride 2 rows per index) added in
@@ -560,7 +565,8 @@ __global__ __launch_bounds__(kRowThreads) void seg_fix_chunks_kernel(const int32
     const int u = t == 0 ? uf : ul;
     const int64_t s0 = seg_start[u], s1 = seg_start[u + 1];
     const int64_t ra = s0 / kRangeLen, rb = (s1 - 1) / kRangeLen;
-    if (ra == rb || (r - ra) % kFixChunk != 0) continue;  // inside one range, or not a chunk head here
+    // inside one range, one chunk (level 2 adds its partials), or not a chunk head here
+    if (ra == rb || rb - ra < kFixChunk || (r - ra) % kFixChunk != 0) continue;
     const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
     const int64_t count = (rb - r + 1) < kFixChunk ? (rb - r + 1) : kFixChunk;
     RowVec<W> acc[VPL];
@@ -580,7 +586,8 @@ __global__ __launch_bounds__(kRowThreads) void seg_fix_chunks_kernel(const int32
 template <int W, int VPL>
 __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* __restrict__ seg_start,
                                                                  const int32_t* __restrict__ seg_of, int64_t n,
-                                                                 int nv, const float* __restrict__ chunk,
+                                                                 int nv, const float* __restrict__ partial,
+                                                                 const float* __restrict__ chunk,
                                                                  float* __restrict__ rows,
                                                                  float* __restrict__ row_sq, int64_t fix_blocks,
                                                                  const uint32_t* __restrict__ num_seg, int64_t cap,
@@ -605,10 +612,16 @@ __global__ __launch_bounds__(kRowThreads) void seg_fixup_kernel(const int32_t* _
 #pragma unroll
   for (int v = 0; v < VPL; ++v) acc[v].zero();
   constexpr int PB = VPL >= 8 ? 4 : 32 / VPL;
-  const int64_t nchunks = (rb - ra) / kFixChunk + 1;
-  add_rows<W, VPL, PB>(chunk, nv, lane, nchunks,
-                       [&](int64_t j) { const int64_t h = ra + j * kFixChunk; return h * 2 + (j == 0 ? 1 : 0); },
-                       acc);
+  if (rb - ra < kFixChunk) {  // one chunk: its partial rows, in range order (level 1 skipped it)
+    const int slot_a = s0 == ra * kRangeLen ? 0 : 1;
+    add_rows<W, VPL, PB>(partial, nv, lane, rb - ra + 1,
+                         [&](int64_t b) { const int64_t q = ra + b; return q * 2 + (q == ra ? slot_a : 0); }, acc);
+  } else {
+    const int64_t nchunks = (rb - ra) / kFixChunk + 1;
+    add_rows<W, VPL, PB>(chunk, nv, lane, nchunks,
+                         [&](int64_t j) { const int64_t h = ra + j * kFixChunk; return h * 2 + (j == 0 ? 1 : 0); },
+                         acc);
+  }
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = lane + kWave * v;
@@ -967,7 +980,7 @@ static void launch_reduce(const uint32_t* sp, int32_t* seg_of, int32_t* seg_star
   seg_reduce_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(sp, seg_of, weights, g, fpt, nv, P, rows, row_sq, partial,
                                                        nseg, seg_start, num_unique, L.cap);
   seg_fix_chunks_kernel<W, VPL><<<b1, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, chunk);
-  seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, chunk, rows, row_sq, b1,
+  seg_fixup_kernel<W, VPL><<<b1 + 1024, kRowThreads, 0, s>>>(seg_start, seg_of, P, nv, partial, chunk, rows, row_sq, b1,
                                                              nseg, L.cap, pool_size, uniq, zero_padding,
                                                              slot_counts);
 }
