@@ -82,34 +82,6 @@ __global__ __launch_bounds__(kSortThreads) void radix_hist_kernel(const uint32_t
   for (int i = tid; i < BINS; i += kSortThreads) hist[(int64_t)i * ntiles + blockIdx.x] = h[i];
 }
 
-// In-place exclusive scan of a[0, len) by one workgroup; *total (if not
-// null) receives the sum.
-__global__ __launch_bounds__(1024) void scan_exclusive_kernel(uint32_t* __restrict__ a, int64_t len,
-                                                              uint32_t* __restrict__ total) {
-  __shared__ uint32_t part[1024];
-  const int tid = threadIdx.x;
-  const int64_t chunk = cdiv(len, 1024);
-  const int64_t b = tid * chunk;
-  const int64_t e = b + chunk < len ? b + chunk : len;
-  uint32_t s = 0;
-  for (int64_t i = b; i < e; ++i) s += a[i];
-  part[tid] = s;
-  __syncthreads();
-  for (int off = 1; off < 1024; off <<= 1) {
-    const uint32_t v = tid >= off ? part[tid - off] : 0u;
-    __syncthreads();
-    part[tid] += v;
-    __syncthreads();
-  }
-  uint32_t run = tid ? part[tid - 1] : 0u;
-  for (int64_t i = b; i < e; ++i) {
-    const uint32_t v = a[i];
-    a[i] = run;
-    run += v;
-  }
-  if (tid == 1023 && total != nullptr) *total = part[1023];
-}
-
 // Exclusive scan of each digit's row hist[digit][0, ntiles) (one workgroup
 // per digit, chunks of 1024 tiles); the digit's total goes to totals[digit].
 __global__ __launch_bounds__(1024) void digit_scan_kernel(uint32_t* __restrict__ hist, int64_t ntiles,
@@ -250,9 +222,12 @@ __global__ __launch_bounds__(kSortThreads) void seg_count_kernel(const uint32_t*
 // seg_of[i] is the segment of position i.  Segment ids are clamped to
 // cap - 1 (the capacity of uniq / seg_start): only ids outside
 // [0, pool_size) can make more distinct values than that, and they then get
-// wrong results, never out-of-bounds writes.
+// wrong results, never out-of-bounds writes.  Each workgroup takes its
+// tile's first segment id as the sum of the tile counts before it (no scan
+// launch); workgroup 0 sums them all for *total, the number of segments.
 __global__ __launch_bounds__(kSortThreads) void seg_write_kernel(const uint32_t* __restrict__ s, int64_t n,
-                                                                  const uint32_t* __restrict__ tile_base,
+                                                                  const uint32_t* __restrict__ tile_cnt,
+                                                                  int64_t ntiles, uint32_t* __restrict__ total,
                                                                   int32_t* __restrict__ uniq,
                                                                   int32_t* __restrict__ seg_start,
                                                                   int32_t* __restrict__ seg_of, int64_t cap) {
@@ -261,9 +236,22 @@ __global__ __launch_bounds__(kSortThreads) void seg_write_kernel(const uint32_t*
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  if (tid == 0) seen = 0;
   const int64_t base = (int64_t)blockIdx.x * kSortTile;
-  const uint32_t tb = tile_base[blockIdx.x];
+  uint32_t tb;
+  {
+    const int64_t lim = blockIdx.x == 0 ? ntiles : (int64_t)blockIdx.x;
+    uint32_t acc = 0;
+    for (int64_t j = tid; j < lim; j += kSortThreads) acc += tile_cnt[j];
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) wave_cnt[wave] = acc;
+    __syncthreads();
+    uint32_t sum = 0;
+    for (int w = 0; w < kSortThreads / kWave; ++w) sum += wave_cnt[w];
+    tb = blockIdx.x == 0 ? 0u : sum;
+    if (blockIdx.x == 0 && tid == 0 && total != nullptr) *total = sum;
+    if (tid == 0) seen = 0;
+    __syncthreads();  // wave_cnt is reused below
+  }
   for (int r = 0; r < kSortRounds; ++r) {
     const int64_t i = base + r * kSortThreads + tid;
     const bool valid = i < n;
@@ -1055,8 +1043,7 @@ static Segments sort_segments(const uint32_t* slots, int64_t P, const MergeLayou
     cur ^= 1;
   }
   seg_count_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt);
-  scan_exclusive_kernel<<<1, 1024, 0, s>>>(tile_cnt, L.ntiles, nseg);
-  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, uniq, seg_start, seg_of, L.cap);
+  seg_write_kernel<<<nt, kSortThreads, 0, s>>>(kin, P, tile_cnt, L.ntiles, nseg, uniq, seg_start, seg_of, L.cap);
   if (finish) seg_finish_kernel<<<1, 1, 0, s>>>(nseg, P, seg_start, num_unique, L.cap);
   return Segments{vin, seg_start, seg_of, nseg};
 }
