@@ -548,6 +548,21 @@ int mpl_decode_next_token(const float* logits, int64_t rows, int64_t vocab, cons
                           int64_t* out, int64_t out_stride, int64_t out_cap, uint32_t* done, void* stream);
 
 /*
+ * mpl_decode_next_token that also writes the next decode step's input rows:
+ * x_next[b] = emb[next token of b] + pos_emb[p + 1], with p the position it
+ * read, the same bits as mpl_decode_embed at that token and position (a NaN
+ * row for an id outside emb [emb_rows, d] or pos_emb [max_pos, d]; d % 4 ==
+ * 0, the three 16-byte aligned).  A greedy generator whose step graph reads
+ * x_next instead of embedding its tokens saves that launch per step.  No
+ * counterpart in the reference's interface.
+ */
+int mpl_decode_next_token_embed(const float* logits, int64_t rows, int64_t vocab, const int64_t* prompt,
+                                int64_t prompt_stride, const int64_t* prompt_len, int64_t* position, int64_t* token,
+                                int64_t* out, int64_t out_stride, int64_t out_cap, uint32_t* done, const float* emb,
+                                int64_t emb_rows, const float* pos_emb, int64_t max_pos, int d, float* x_next,
+                                void* stream);
+
+/*
  * The input rows of a decode step (model.py:29-127: the token embedding plus
  * the position embedding, for one token per stream): for each of `rows`
  * streams, out[b, :] = emb[token[b], :] + pos_emb[*position, :] (emb

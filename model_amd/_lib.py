@@ -75,6 +75,8 @@ SIGNATURES = {
     "mpl_hash_normal_fill": (_I, [_P, _I, _I64, _I, _U64, _F, _I64, _P]),
     "mpl_decode_attention": (_I, [_P, _I64, _I, _I, _I, _P, _P, _P, _P, _F, _P]),
     "mpl_decode_next_token": (_I, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P]),
+    "mpl_decode_next_token_embed": (_I, [_P, _I64, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _P, _P, _I64, _P,
+                                         _I64, _I, _P, _P]),
     "mpl_decode_embed": (_I, [_P, _I64, _P, _I64, _I, _P, _P, _I64, _P, _P]),
     "mpl_rows_linear": (_I, [_P, _P, _P, _P, _F, _P, _I, _P, _I, _P, _I64, _I, _I, _P, _P]),
     "mpl_vocab_logits": (_I, [_P, _P, _P, _F, _P, _I64, _I, _I64, _P, _P]),

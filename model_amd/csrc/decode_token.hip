@@ -40,7 +40,11 @@ __global__ __launch_bounds__(kTokThreads) void next_token_kernel(const float* __
                                                                  int64_t* __restrict__ position,
                                                                  int64_t* __restrict__ token,
                                                                  int64_t* __restrict__ out, int64_t out_stride,
-                                                                 int64_t out_cap, uint32_t* __restrict__ done) {
+                                                                 int64_t out_cap, uint32_t* __restrict__ done,
+                                                                 const float* __restrict__ emb, int64_t emb_rows,
+                                                                 const float* __restrict__ pos_emb,
+                                                                 int64_t max_pos, int d4,
+                                                                 float* __restrict__ x_next) {
   __shared__ float rv[kTokThreads / kWave];
   __shared__ int ri[kTokThreads / kWave];
   __shared__ int64_t sp[2];
@@ -121,6 +125,20 @@ __global__ __launch_bounds__(kTokThreads) void next_token_kernel(const float* __
       }
     next = bi < V ? bi : 0;  // every element was -inf: index 0, as torch.argmax
   }
+  if (x_next != nullptr) {
+    // the next step's input rows, as decode_embed_kernel forms them for the
+    // token just chosen at position p + 1 (a NaN row for an id outside its
+    // table), so that the next decode step needs no embedding launch
+    const int64_t pn = p + 1;
+    const bool ok = next >= 0 && next < emb_rows && pn >= 0 && pn < max_pos;
+    const float4* e = (const float4*)emb + (ok ? next : 0) * d4;
+    const float4* q = (const float4*)pos_emb + (ok ? pn : 0) * d4;
+    float4* o = (float4*)x_next + b * d4;
+    for (int j = tid; j < d4; j += kTokThreads) {
+      const float4 a = e[j], c = q[j];
+      o[j] = ok ? make_float4(a.x + c.x, a.y + c.y, a.z + c.z, a.w + c.w) : make_float4(NAN, NAN, NAN, NAN);
+    }
+  }
   if (tid == 0) {
     token[b] = next;
     const int64_t g = p + 1 - P;
@@ -176,8 +194,34 @@ extern "C" int mpl_decode_next_token(const float* logits, int64_t rows, int64_t 
   MPL_REQUIRE(logits && prompt && prompt_len && position && token && done && (out || out_cap == 0), MPL_EINVAL,
               "mpl_decode_next_token: null buffer");
   next_token_kernel<<<(unsigned)rows, kTokThreads, 0, (hipStream_t)stream>>>(
-      logits, vocab, prompt, prompt_stride, prompt_len, position, token, out, out_stride, out_cap, done);
+      logits, vocab, prompt, prompt_stride, prompt_len, position, token, out, out_stride, out_cap, done, nullptr, 0,
+      nullptr, 0, 0, nullptr);
   return check_launch("mpl_decode_next_token");
+}
+
+extern "C" int mpl_decode_next_token_embed(const float* logits, int64_t rows, int64_t vocab, const int64_t* prompt,
+                                           int64_t prompt_stride, const int64_t* prompt_len, int64_t* position,
+                                           int64_t* token, int64_t* out, int64_t out_stride, int64_t out_cap,
+                                           uint32_t* done, const float* emb, int64_t emb_rows,
+                                           const float* pos_emb, int64_t max_pos, int d, float* x_next,
+                                           void* stream) {
+  clear_error();
+  MPL_REQUIRE(rows >= 0 && vocab > 0 && prompt_stride >= 0 && out_cap >= 0 && out_stride >= 0 && emb_rows > 0 &&
+                  max_pos > 0 && d > 0 && d % 4 == 0,
+              MPL_EINVAL, "mpl_decode_next_token_embed: bad sizes rows=%lld vocab=%lld d=%d", (long long)rows,
+              (long long)vocab, d);
+  MPL_REQUIRE(rows < ((int64_t)1 << 31) && vocab < ((int64_t)1 << 31), MPL_EINVAL,
+              "mpl_decode_next_token_embed: rows=%lld or vocab=%lld too large", (long long)rows, (long long)vocab);
+  if (rows == 0) return MPL_OK;
+  MPL_REQUIRE(logits && prompt && prompt_len && position && token && done && (out || out_cap == 0) && emb &&
+                  pos_emb && x_next,
+              MPL_EINVAL, "mpl_decode_next_token_embed: null buffer");
+  MPL_REQUIRE(((uintptr_t)emb & 15) == 0 && ((uintptr_t)pos_emb & 15) == 0 && ((uintptr_t)x_next & 15) == 0,
+              MPL_EINVAL, "mpl_decode_next_token_embed: emb, pos_emb and x_next must be 16-byte aligned");
+  next_token_kernel<<<(unsigned)rows, kTokThreads, 0, (hipStream_t)stream>>>(
+      logits, vocab, prompt, prompt_stride, prompt_len, position, token, out, out_stride, out_cap, done, emb,
+      emb_rows, pos_emb, max_pos, d / 4, x_next);
+  return check_launch("mpl_decode_next_token_embed");
 }
 
 extern "C" int mpl_decode_embed(const float* emb, int64_t vocab, const float* pos_emb, int64_t max_pos, int d,

@@ -52,10 +52,11 @@ class Generator:
         self.graph = None
         self.graph_greedy = None
         self.logits_greedy = None
+        self.x_rows = None
         self._captured_state = None
         self.use_graph = graph
 
-    def _step(self):
+    def _step(self, input_rows=None):
         # The step's products have one row per stream.  For such shapes
         # hipBLASLt picks one-workgroup tiles; rocBLAS (torch's "cublas"
         # backend on ROCm) ran the 64-stream step 20% faster.  The choice is
@@ -65,24 +66,41 @@ class Generator:
         torch.backends.cuda.preferred_blas_library("cublas")
         try:
             logits, _ = self.model.apply({"params": self.params}, self.tok[:, None], positions=self.pos,
-                                         cache=self.cache)
+                                         cache=self.cache, input_rows=input_rows)
         finally:
             torch.backends.cuda.preferred_blas_library(prev)
         return logits[:, 0]
 
-    def _next_token(self, logits):
+    def _next_token(self, logits, embed_into=None):
         """generate.py:44-61 for greedy decoding on the device: the next prompt
         token or the argmax of ``logits`` into self.tok, generated tokens into
-        self.out_buf, then the position advanced (mpl_decode_next_token)."""
+        self.out_buf, then the position advanced (mpl_decode_next_token).
+        With ``embed_into`` ([B, d_model] fp32) it also writes the next step's
+        input rows there (mpl_decode_next_token_embed)."""
         from . import _lib
 
         lg = logits.float().contiguous()
         B, V = lg.shape
         P = _lib.ptr
-        _lib.check(_lib.lib().mpl_decode_next_token(
-            P(lg), B, V, P(self.prompt_buf), self.prompt_buf.shape[1], P(self.plen), P(self.pos), P(self.tok),
-            P(self.out_buf), self.out_buf.shape[1], self.out_buf.shape[1], P(self.done),
-            _lib.stream_ptr(self.device)), "mpl_decode_next_token")
+        head = (P(lg), B, V, P(self.prompt_buf), self.prompt_buf.shape[1], P(self.plen), P(self.pos), P(self.tok),
+                P(self.out_buf), self.out_buf.shape[1], self.out_buf.shape[1], P(self.done))
+        if embed_into is None:
+            _lib.check(_lib.lib().mpl_decode_next_token(*head, _lib.stream_ptr(self.device)),
+                       "mpl_decode_next_token")
+        else:
+            emb, pe = self.params["embed"]["embedding"], self.params["pos_embed"]
+            _lib.check(_lib.lib().mpl_decode_next_token_embed(
+                *head, P(emb), emb.shape[0], P(pe), pe.shape[0], emb.shape[1], P(embed_into),
+                _lib.stream_ptr(self.device)), "mpl_decode_next_token_embed")
+
+    def _rows_in_token_step(self) -> bool:
+        """Whether the greedy graph's token step can write the next step's
+        input rows (fp32 contiguous 16-byte-aligned tables of a width that is
+        a multiple of 4, as the GPU decode step's own embedding launch)."""
+        emb, pe = self.params["embed"]["embedding"], self.params["pos_embed"]
+        return (emb.shape[1] % 4 == 0 and emb.shape[1] == pe.shape[1]
+                and all(t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0 and t.is_cuda
+                        for t in (emb, pe)))
 
     def _reset_cache(self):
         for c in self.cache:
@@ -157,11 +175,18 @@ class Generator:
             with torch.cuda.graph(self.graph):
                 self.logits = self._step()
             # the greedy step: the same decode step, then the token choice
-            # (the position it advances is reset by every generate())
+            # (the position it advances is reset by every generate()).  Its
+            # token step also writes the next step's input rows (x_rows), so
+            # the step reads them instead of embedding its tokens;
+            # generate() forms the first ones
+            self.x_rows = None
+            if self._rows_in_token_step():
+                self.x_rows = torch.empty((self.batch_size, self.mcfg.d_model), dtype=torch.float32,
+                                          device=self.device)
             self.graph_greedy = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.graph_greedy):
-                self.logits_greedy = self._step()
-                self._next_token(self.logits_greedy)
+                self.logits_greedy = self._step(input_rows=self.x_rows)
+                self._next_token(self.logits_greedy, embed_into=self.x_rows)
         finally:
             if pool is not None:
                 pool.frozen_under_capture = False
@@ -228,6 +253,10 @@ class Generator:
         self.plen.fill_(P)
         self.pos.fill_(0)
         self.tok.copy_(prompt[:, 0])
+        if self.x_rows is not None:  # the first step's input rows; the token step writes the others
+            from .model import decode_embed
+            self.x_rows.copy_(decode_embed(self.params["embed"]["embedding"], self.params["pos_embed"], self.tok,
+                                           self.pos))
         logits_all, times = [], []
         for _ in range(P + n_new - 1):
             t0 = time.perf_counter()

@@ -407,7 +407,7 @@ class MemoryPoolLM:
         self._qkv_cache[i] = (key, w, b)
         return w, b
 
-    def _decode_step_gpu(self, p, tokens, positions, cache, noise_scale, rngs):
+    def _decode_step_gpu(self, p, tokens, positions, cache, noise_scale, rngs, input_rows=None):
         """One decode step on the GPU (inference: no autograd, no dropout):
         the computation of the general path of apply() for T = 1, with every
         dense layer of a block one mpl_rows_linear launch that also applies
@@ -423,7 +423,9 @@ class MemoryPoolLM:
         layer_aux = []
         with torch.no_grad():
             pe = p["pos_embed"]
-            if (emb.shape[1] % 4 == 0 and tokens.dtype == torch.int64 and positions.dtype == torch.int64
+            if input_rows is not None:
+                x = input_rows
+            elif (emb.shape[1] % 4 == 0 and tokens.dtype == torch.int64 and positions.dtype == torch.int64
                     and all(t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0
                             for t in (emb, pe))):
                 x = decode_embed(emb, pe, tokens[:, 0].contiguous(), positions)  # [B, d], one launch
@@ -491,15 +493,20 @@ class MemoryPoolLM:
     def apply(self, variables: Dict[str, Any], tokens: torch.Tensor, *, train: bool = False, pool_off: bool = False,
               route_through_pool: bool = False, sparse_grad: bool = False,
               probes: Optional[Dict[int, torch.Tensor]] = None, positions: Optional[torch.Tensor] = None,
-              noise_scale: float = 1.0, shuffle_pool: bool = False, cache=None, rngs=None):
+              noise_scale: float = 1.0, shuffle_pool: bool = False, cache=None, rngs=None,
+              input_rows: Optional[torch.Tensor] = None):
         """model.py:27-127: (logits [B, T, vocab], aux).  In decode mode pass
-        ``cache`` (init_cache) and ``positions`` (int64 device tensor [1])."""
+        ``cache`` (init_cache) and ``positions`` (int64 device tensor [1]).
+        ``input_rows`` (GPU decode step only): the step's input rows
+        emb[tokens] + pos_embed[positions], [B, d_model] fp32, already formed
+        (the greedy token step writes them, mpl_decode_next_token_embed); the
+        tokens are then not read."""
         cfg = self.cfg
         p = variables["params"] if "params" in variables else variables
         B, T = tokens.shape
         if (self.decode and tokens.is_cuda and cache is not None and positions is not None and T == 1 and not train
                 and not pool_off and not route_through_pool and probes is None and not shuffle_pool):
-            return self._decode_step_gpu(p, tokens, positions, cache, noise_scale, rngs)
+            return self._decode_step_gpu(p, tokens, positions, cache, noise_scale, rngs, input_rows)
         emb = p["embed"]["embedding"]
         if positions is None:
             x = emb[tokens] + p["pos_embed"][None, :T]

@@ -267,3 +267,47 @@ def test_generation_at_the_268M_slot_shapes(gpu_lib):
         del values
         params = None
         torch.cuda.empty_cache()
+
+
+def test_next_token_embed_writes_next_input_rows(gpu_lib):
+    """mpl_decode_next_token_embed: the same tokens, outputs and position as
+    mpl_decode_next_token, and x_next equal to mpl_decode_embed of the chosen
+    tokens at the advanced position bit for bit (prompt tokens first, then
+    argmax picks); past the position table the rows are NaN."""
+    from model_amd import _lib
+    from model_amd.model import decode_embed
+
+    B, V, Lmax, P, d = 5, 777, 6, 3, 64
+    g = torch.Generator(device="cuda").manual_seed(17)
+    emb = torch.randn((V, d), generator=g, device="cuda")
+    pe = torch.randn((Lmax, d), generator=g, device="cuda")
+    prompt = torch.randint(0, V, (B, Lmax), generator=g, device="cuda")
+    plen = torch.full((1,), P, dtype=torch.int64, device="cuda")
+    st = {}
+    for fused in (False, True):
+        st[fused] = {"pos": torch.zeros(1, dtype=torch.int64, device="cuda"),
+                     "tok": torch.zeros(B, dtype=torch.int64, device="cuda"),
+                     "out": torch.full((B, Lmax), -1, dtype=torch.int64, device="cuda"),
+                     "done": torch.zeros(1, dtype=torch.int32, device="cuda")}
+    x_next = torch.empty((B, d), device="cuda")
+    p_ = _lib.ptr
+    for step in range(Lmax):
+        logits = torch.randn((B, V), generator=g, device="cuda")
+        for fused in (False, True):
+            s = st[fused]
+            head = (p_(logits), B, V, p_(prompt), Lmax, p_(plen), p_(s["pos"]), p_(s["tok"]), p_(s["out"]), Lmax,
+                    Lmax, p_(s["done"]))
+            if fused:
+                pos_before = s["pos"].clone()
+                _lib.check(_lib.lib().mpl_decode_next_token_embed(*head, p_(emb), V, p_(pe), Lmax, d, p_(x_next),
+                                                                  _lib.stream_ptr(logits.device)), "embed")
+            else:
+                _lib.check(_lib.lib().mpl_decode_next_token(*head, _lib.stream_ptr(logits.device)), "next")
+        torch.cuda.synchronize()
+        for key in ("pos", "tok", "out", "done"):
+            assert torch.equal(st[True][key], st[False][key]), (step, key)
+        if step + 1 < Lmax:
+            want = decode_embed(emb, pe, st[True]["tok"], pos_before + 1)
+            assert torch.equal(x_next, want), step
+        else:  # position past the table: NaN rows, nothing read outside it
+            assert torch.isnan(x_next).all()
