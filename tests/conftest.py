@@ -23,3 +23,20 @@ def gpu_lib():
     from model_amd import _lib
 
     return _lib.lib()
+
+
+@pytest.fixture(autouse=True)
+def _release_gpu_memory(request):
+    """After each GPU test, collect reference cycles and return cached blocks,
+    so that a test holding a 100+ GB table (the 268M-slot pool) never leaves
+    it to the next one."""
+    yield
+    if request.node.get_closest_marker("gpu") is None:
+        return
+    import gc
+
+    import torch
+
+    gc.collect()
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
