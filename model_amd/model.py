@@ -455,7 +455,9 @@ class MemoryPoolLM:
                     layer_aux.append(aux)
             lf = p["ln_final"]
             if (B <= 64 and d % 4 == 0 and d <= 256 and emb.dtype == torch.float32 and emb.is_contiguous()
-                    and emb.data_ptr() % 16 == 0 and x.is_contiguous() and x.data_ptr() % 16 == 0):
+                    and x.is_contiguous()
+                    and all(t.dtype == torch.float32 and t.is_contiguous() and t.data_ptr() % 16 == 0
+                            for t in (emb, x, lf["scale"], lf["bias"]))):
                 logits = vocab_logits(x, lf["scale"], lf["bias"], emb)[:, None]  # one launch
             else:
                 logits = F.linear(_ln(x, lf), emb)[:, None]
